@@ -1,0 +1,301 @@
+"""Decode kernels (weights [N, K]) on the GPU against the CPU oracle.
+
+Shapes are the Qwen3-1.7B layer's (hidden 2048, 16 q / 8 kv heads, head_dim
+128, intermediate 6144, vocab 151936) plus edge shapes. Tolerances: the
+reference's GEMV rtol 5e-3 and the bf16 bar (max |d| / max |ref| <= 1e-2)
+everywhere else (examples/qwen3_1_7b-tilelang/fast/test_kernels.py:18-29,66,78);
+integer and index outputs exactly.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import norms as ON
+from oracle import qwen3 as OQ
+from tests._check import assert_close, assert_equal, max_rel
+
+BF = torch.bfloat16
+H, HQ, HKV, D, I, V = 2048, 16, 8, 128, 6144, 151936
+EPS = 1e-6
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def randn(*shape, g, std=1.0, mean=0.0):
+    return (mean + std * torch.randn(*shape, generator=g)).to(BF)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K", [(4096, 2048), (2048, 2048), (2048, 6144), (1056, 2560), (3840, 768), (96, 256)])
+def test_gemv(dev, N, K):
+    from tilefoundry_amd import ops
+
+    g = gen(N + K)
+    x = randn(K, g=g)
+    w = randn(N, K, g=g, std=K ** -0.5)
+    ref = x.float() @ w.float().t()
+    got = ops.gemv(x.to(dev), w.to(dev), out_dtype=torch.float32)
+    assert max_rel(got, ref) < 5e-3
+    gotb = ops.gemv(x.to(dev), w.to(dev))
+    assert_close("gemv bf16", gotb, ref.to(BF))
+
+
+@pytest.mark.gpu
+def test_gemv_exact_on_integers(dev):
+    """Integer-valued bf16 inputs with small sums: every product and partial sum is
+    exact in f32, so the result must equal the integer matmul bit for bit."""
+    from tilefoundry_amd import ops
+
+    g = gen(7)
+    x = torch.randint(-3, 4, (2048,), generator=g).to(BF)
+    w = torch.randint(-3, 4, (512, 2048), generator=g).to(BF)
+    ref = (x.to(torch.int64) @ w.to(torch.int64).t()).to(torch.float32)
+    got = ops.gemv(x.to(dev), w.to(dev), out_dtype=torch.float32)
+    assert_equal("integer gemv", got, ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K", [(4096, 2048), (1056, 2560)])
+def test_rmsnorm_gemv(dev, N, K):
+    from tilefoundry_amd import ops
+
+    g = gen(11)
+    h = randn(K, g=g)
+    gamma = randn(K, g=g, std=0.1, mean=1.0)
+    w = randn(N, K, g=g, std=0.02)
+    ref = OQ.proj(ON.rms_norm_q(h, gamma, EPS), w)
+    got = ops.rmsnorm_gemv(h.to(dev), gamma.to(dev), EPS, w.to(dev))
+    assert_close("rmsnorm_gemv", got, ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K,scaled", [(2048, 2048, False), (2048, 6144, False), (2560, 2560, True)])
+def test_gemv_residual(dev, N, K, scaled):
+    from tilefoundry_amd import ops
+
+    g = gen(13)
+    x = randn(K, g=g)
+    w = randn(N, K, g=g, std=0.02)
+    r = randn(N, g=g)
+    alpha = torch.tensor([1.4 / math.sqrt(62)]).to(BF) if scaled else None
+    p = OQ.proj(x, w)
+    ref = r + (p * alpha if scaled else p)
+    got = ops.gemv_residual(x.to(dev), w.to(dev), r.to(dev),
+                            alpha.to(dev) if scaled else None)
+    assert_close("gemv_residual", got, ref)
+
+
+@pytest.mark.gpu
+def test_rmsnorm_gemv_swiglu(dev):
+    from tilefoundry_amd import ops
+
+    g = gen(17)
+    h = randn(H, g=g)
+    gamma = randn(H, g=g, std=0.1, mean=1.0)
+    wg = randn(I, H, g=g, std=0.02)
+    wu = randn(I, H, g=g, std=0.02)
+    xn = ON.rms_norm_q(h, gamma, EPS)
+    gg, uu = OQ.proj(xn, wg), OQ.proj(xn, wu)
+    ref = torch.nn.functional.silu(gg.float()).to(BF) * uu
+    w_gu = torch.stack([wg, wu], 1).reshape(2 * I, H)
+    got = ops.rmsnorm_gemv_swiglu(h.to(dev), gamma.to(dev), EPS, w_gu.to(dev))
+    assert_close("swiglu", got, ref)
+
+
+@pytest.mark.gpu
+def test_lm_head_argmax(dev):
+    from tilefoundry_amd import ops
+
+    g = gen(19)
+    h = randn(H, g=g)
+    gamma = randn(H, g=g, std=0.1, mean=1.0)
+    w = randn(V, H, g=g, std=0.02)
+    ref = OQ.lm_logits(h, gamma, w.float(), EPS)
+    logits, best = ops.lm_head_argmax(h.to(dev), gamma.to(dev), EPS, w.to(dev))
+    assert max_rel(logits, ref) < 5e-3
+    assert best == int(torch.argmax(logits.cpu())), "argmax of the kernel's own logits"
+    top = torch.topk(ref, 2).values
+    if float(top[0] - top[1]) > 1e-3 * float(ref.abs().max()):
+        assert best == int(torch.argmax(ref))
+
+
+@pytest.mark.gpu
+def test_lm_head_planted_ties(dev):
+    """Identical rows give identical logits: the lowest index must win
+    (torch.argmax; examples/qwen3_1_7b-tilelang/fast/kernels.py:303-319)."""
+    from tilefoundry_amd import ops
+
+    g = gen(23)
+    Vs, K = 4096, 256
+    w = randn(Vs, K, g=g, std=0.02)
+    x = randn(K, g=g)
+    winner = torch.tensor([3.0] * 8 + [1.0] * (K - 8)).to(BF)
+    for idx in (4000, 17, 2500, 18):   # same max planted at four rows, in two blocks
+        w[idx] = winner
+    x[:8] = 1.0
+    logits, best = ops.lm_head_argmax(x.to(dev), None, EPS, w.to(dev))
+    lg = logits.cpu()
+    assert best == int(torch.argmax(lg)) == 17
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("pos,expect_prompt", [(2, True), (4, False), (20, False)])
+def test_sample_step(dev, pos, expect_prompt):
+    """The device-side greedy step: record the pick at pos; feed the next prompt
+    id while the prompt lasts, else the pick; advance pos
+    (examples/qwen3_1_7b-tilelang/fast/test_kernels.py:171-189)."""
+    from tilefoundry_amd import ops
+
+    g = gen(29)
+    Vs, K, PL, NSTEPS = 8192, 256, 5, 64
+    w = randn(Vs, K, g=g, std=0.02)
+    x = randn(K, g=g)
+    st = ops.SampleState(NSTEPS, dev)
+    st.inp.copy_(torch.arange(NSTEPS, dtype=torch.int32) + 100)
+    st.plen.fill_(PL)
+    st.pos.fill_(pos)
+    logits, best = ops.lm_head_argmax(x.to(dev), None, EPS, w.to(dev), sample=st)
+    want_next = pos + 1 + 100 if expect_prompt else best
+    assert int(st.sam[pos]) == best
+    assert int(st.ids[0]) == want_next
+    assert int(st.pos[0]) == pos + 1
+    assert int(st.err[0]) == 0
+
+
+def _qkv_case(g, cap=512):
+    h = randn(H, g=g)
+    gamma_in = randn(H, g=g, std=0.1, mean=1.0)
+    wq = randn(HQ * D, H, g=g, std=0.02)
+    wk = randn(HKV * D, H, g=g, std=0.02)
+    wv = randn(HKV * D, H, g=g, std=0.02)
+    gq = randn(D, g=g, std=0.1, mean=1.0)
+    gk = randn(D, g=g, std=0.1, mean=1.0)
+    cos, sin = OQ.rope_tables(cap, D, 1.0e6)
+    return h, gamma_in, wq, wk, wv, gq, gk, cos, sin
+
+
+def _qkv_ref(h, gamma_in, wq, wk, wv, gq, gk, cos, sin, pos):
+    xn = ON.rms_norm_q(h, gamma_in, EPS)
+    q = OQ.rope(OQ.head_norm(OQ.proj(xn, wq).view(HQ, D), gq, EPS), cos[pos], sin[pos])
+    k = OQ.rope(OQ.head_norm(OQ.proj(xn, wk).view(HKV, D), gk, EPS), cos[pos], sin[pos])
+    v = OQ.proj(xn, wv).view(HKV, D)
+    return q, k, v
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("pos,wr", [(0, 0), (37, 37), (300, 5), (511, 511)])
+def test_decode_qkv(dev, pos, wr):
+    from tilefoundry_amd import ops
+
+    cap = 512
+    args = _qkv_case(gen(31 + pos), cap)
+    h, gamma_in, wq, wk, wv, gq, gk, cos, sin = args
+    qr, kr, vr = _qkv_ref(*args, pos)
+    kc = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
+    vc = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
+    w_qkv = torch.cat([wq, wk, wv], 0).to(dev)
+    q = ops.decode_qkv(h.to(dev), gamma_in.to(dev), EPS, w_qkv, HQ, HKV, D, gq.to(dev), gk.to(dev),
+                       cos.to(dev), sin.to(dev), pos, wr, kc, vc)
+    assert_close("q", q.view(HQ, D), qr)
+    assert_close("k", kc[wr].view(HKV, D), kr)
+    assert_close("v", vc[wr].view(HKV, D), vr)
+    # exactly one cache row written (bit-exact cache indexing)
+    written = (kc.cpu().view(torch.int16) != 0).any(1).nonzero().flatten().tolist()
+    assert written == [wr]
+    written = (vc.cpu().view(torch.int16) != 0).any(1).nonzero().flatten().tolist()
+    assert written == [wr]
+
+
+@pytest.mark.gpu
+def test_decode_qkv_embed_mode(dev):
+    from tilefoundry_amd import ops
+
+    cap = 64
+    g = gen(37)
+    table = randn(1000, H, g=g, std=0.02)
+    _, gamma_in, wq, wk, wv, gq, gk, cos, sin = _qkv_case(g, cap)
+    tok, pos = 777, 3
+    qr, kr, vr = _qkv_ref(table[tok], gamma_in, wq, wk, wv, gq, gk, cos, sin, pos)
+    kc = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
+    vc = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
+    w_qkv = torch.cat([wq, wk, wv], 0).to(dev)
+    hcopy = torch.zeros(H, dtype=BF, device=dev)
+    q = ops.decode_qkv(None, gamma_in.to(dev), EPS, w_qkv, HQ, HKV, D, gq.to(dev), gk.to(dev),
+                       cos.to(dev), sin.to(dev), pos, pos, kc, vc, table=table.to(dev),
+                       token=tok, h_copy=hcopy)
+    assert_equal("gathered row", hcopy, table[tok])
+    assert_close("q", q.view(HQ, D), qr)
+    assert_close("k", kc[pos].view(HKV, D), kr)
+    assert_close("v", vc[pos].view(HKV, D), vr)
+
+
+@pytest.mark.gpu
+def test_rope_position_zero_is_identity(dev):
+    """At position 0 (cos = 1, sin = 0) q is exactly the head-normed projection."""
+    from tilefoundry_amd import ops
+
+    cap = 64
+    args = _qkv_case(gen(41), cap)
+    h, gamma_in, wq, wk, wv, gq, gk, cos, sin = args
+    kc = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
+    vc = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
+    w_qkv = torch.cat([wq, wk, wv], 0).to(dev)
+    q = ops.decode_qkv(h.to(dev), gamma_in.to(dev), EPS, w_qkv, HQ, HKV, D, gq.to(dev), gk.to(dev),
+                       cos.to(dev), sin.to(dev), 0, 0, kc, vc).cpu()
+    # the unrotated head norm of the kernel's own projection must be what comes out
+    qn = OQ.head_norm(OQ.proj(ON.rms_norm_q(h, gamma_in, EPS), wq).view(HQ, D), gq, EPS)
+    assert_close("q at pos 0", q.view(HQ, D), qn)
+
+
+def _attn_case(g, cap, n):
+    q = randn(HQ, D, g=g)
+    kc = torch.zeros(cap, HKV, D, dtype=BF)
+    vc = torch.zeros(cap, HKV, D, dtype=BF)
+    kc[:n] = randn(n, HKV, D, g=g)
+    vc[:n] = randn(n, HKV, D, g=g)
+    return q, kc, vc
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 5, 64, 65, 256, 257, 700, 2048, 4096])
+@pytest.mark.parametrize("split", [64, 256])
+def test_decode_attention(dev, n, split):
+    from tilefoundry_amd import ops
+
+    cap = 4096
+    q, kc, vc = _attn_case(gen(n), cap, n)
+    ref = OQ.attend(q, kc[:n], vc[:n], D ** -0.5)
+    got = ops.decode_attention(q.reshape(-1).to(dev), kc.view(cap, -1).to(dev),
+                               vc.view(cap, -1).to(dev), n - 1, HQ, HKV, split=split)
+    assert_close(f"attention n={n}", got, ref)
+
+
+@pytest.mark.gpu
+def test_attention_single_key_returns_value(dev):
+    from tilefoundry_amd import ops
+
+    cap = 128
+    q, kc, vc = _attn_case(gen(43), cap, 1)
+    got = ops.decode_attention(q.reshape(-1).to(dev), kc.view(cap, -1).to(dev),
+                               vc.view(cap, -1).to(dev), 0, HQ, HKV).cpu()
+    want = vc[0].repeat_interleave(HQ // HKV, 0).reshape(-1)
+    assert_equal("one key", got, want)
+
+
+@pytest.mark.gpu
+def test_attention_partials_and_combine(dev):
+    """Partials-only form + the separate combine equal the merged form."""
+    from tilefoundry_amd import ops
+
+    cap, n = 2560, 700
+    q, kc, vc = _attn_case(gen(47), cap, n)
+    kd, vd, qd = kc.view(cap, -1).to(dev), vc.view(cap, -1).to(dev), q.reshape(-1).to(dev)
+    merged = ops.decode_attention(qd, kd, vd, n - 1, HQ, HKV, split=256)
+    op, mp, lp = ops.attn_partial(qd, kd, vd, n - 1, HQ, HKV, split=256)
+    neutral = torch.tensor(-1.0e30, dtype=torch.float32).item()
+    assert float(lp[3:].abs().max()) == 0.0 and float(mp[3:].max()) == neutral
+    combined = ops.attn_combine(op, mp, lp)
+    assert_equal("combine == merged", combined, merged)

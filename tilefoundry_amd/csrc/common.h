@@ -1,0 +1,132 @@
+// Shared device helpers for the gfx950 kernels: bf16 bit conversions, 128-bit
+// vector access, wave64 reductions and the "last block finishes" handshake.
+//
+// Every kernel in this library stores bf16 as raw uint16_t bits. Conversion
+// from f32 is round-to-nearest-even, the rounding torch's `.to(bfloat16)`
+// performs, so a value computed in f32 lands on the same bf16 the oracle's
+// torch spelling would produce from the same f32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define TFA_DEV __device__ __forceinline__
+
+namespace tfa {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- bf16 bits
+TFA_DEV float bf2f(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+TFA_DEV uint32_t f2bf(float f) {
+  // Round to nearest even; NaN stays a quiet NaN (torch's c10::BFloat16 rule).
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// bf16 round trip: the value f takes after landing in bf16.
+TFA_DEV float round_bf(float f) { return bf2f(f2bf(f)); }
+
+// low / high bf16 of a packed 32-bit word, as f32
+TFA_DEV float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
+TFA_DEV float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+TFA_DEV uint32_t pack_bf(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+
+// 8 bf16 (one 16-byte vector) <-> 8 floats
+TFA_DEV void unpack8(const uint4 v, float* f) {
+  f[0] = lo_bf(v.x); f[1] = hi_bf(v.x);
+  f[2] = lo_bf(v.y); f[3] = hi_bf(v.y);
+  f[4] = lo_bf(v.z); f[5] = hi_bf(v.z);
+  f[6] = lo_bf(v.w); f[7] = hi_bf(v.w);
+}
+
+TFA_DEV uint4 pack8(const float* f) {
+  uint4 v;
+  v.x = pack_bf(f[0], f[1]);
+  v.y = pack_bf(f[2], f[3]);
+  v.z = pack_bf(f[4], f[5]);
+  v.w = pack_bf(f[6], f[7]);
+  return v;
+}
+
+TFA_DEV uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+// Streaming load for data read exactly once (weights, KV cache): non-temporal
+// hint so it does not evict reusable lines from L2 / MALL.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+TFA_DEV uint4 ld16_stream(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+TFA_DEV void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+
+// ---------------------------------------------------------------- reductions
+TFA_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+TFA_DEV float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+
+// Sum over groups of `width` consecutive lanes (width a power of two <= 64).
+template <int WIDTH>
+TFA_DEV float group_sum(float v) {
+#pragma unroll
+  for (int m = WIDTH / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `scratch` holds one
+// float per wave. Every thread gets the total; waves are summed in wave order
+// so the result does not depend on scheduling.
+TFA_DEV float block_sum(float v, float* scratch) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  v = wave_sum(v);
+  if (lane == 0) scratch[wid] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int w = 0; w < nw; ++w) t += scratch[w];
+  __syncthreads();
+  return t;
+}
+
+// 1/sqrt(x) with correctly rounded sqrt and division: the value torch's CPU
+// `rsqrt` returns for the same f32 input.
+TFA_DEV float rsqrt_rn(float x) { return 1.0f / __fsqrt_rn(x); }
+
+TFA_DEV float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+// --------------------------------------------------- last block finishes
+// A group of blocks each publishes a slice of a result, then one of them --
+// whichever arrives last -- runs the step that needs the whole result. The
+// counter resets itself, so the same buffer serves every launch (and every
+// replay of a captured graph) without a memset.
+//
+// Returns true in exactly one block of the group. Every thread of the block
+// must call it (it synchronises the block).
+TFA_DEV bool arrive_last(unsigned int* counter, unsigned int group_size, int* flag_smem) {
+  __threadfence();  // publish this block's slice at device scope
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned int prev = atomicAdd(counter, 1u);
+    int last = (prev == group_size - 1);
+    if (last) atomicExch(counter, 0u);  // no other block of this launch touches it again
+    *flag_smem = last;
+  }
+  __syncthreads();
+  const bool last = *flag_smem != 0;
+  if (last) __threadfence();  // acquire: see every other block's slice
+  return last;
+}
+
+}  // namespace tfa

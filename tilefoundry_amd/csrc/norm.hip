@@ -1,0 +1,191 @@
+// RMSNorm family: plain rows, fused residual-add + norm over rows, and the
+// single-row "reduce split-K partials, add residual, norm" form.
+//
+// Rounding points (each value lands in bf16 exactly where the reference's
+// torch spelling lands it):
+//   MODE 0 (Qwen3 / MiniCPM3, reference examples/qwen3_1_7b-tilelang/fast/kernels.py:58-79):
+//            y = bf16( bf16(x * r) * gamma ),  r = 1/sqrt(mean(x^2) + eps)
+//   MODE 1 (Qwen3.5 prefill, examples/qwen3_8_27b_prefill-tilelang/kernels/elementwise.py:21-68):
+//            y = bf16( (x * r) * (1 + gamma) ) in f32
+// The fused add lands the sum in bf16 first (r' = bf16(x + res)) and normalises
+// that landed value, which is what `Hout = A + ...; Xn = norm(Hout)` does in
+// examples/qwen3_1_7b-tilelang/fast/kernels.py:82-116.
+#include "abi_util.h"
+#include "common.h"
+
+using namespace tfa;
+
+namespace {
+
+template <int MODE>
+TFA_DEV float norm_scale(float x, float r, float g) {
+  if (MODE == 0) return round_bf(round_bf(x * r) * g);
+  return (x * r) * (g + 1.0f);
+}
+
+// One wave per row; each lane owns NC 16-byte vectors of the row, so the whole
+// row sits in registers between the sum of squares and the write.
+template <int NC, bool ADD, int MODE>
+__global__ __launch_bounds__(256) void rms_rows_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
+    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ y,
+    uint16_t* __restrict__ res_out, int rows, int H, float eps) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= rows) return;
+  const int nvec = H >> 3;
+  const size_t base = static_cast<size_t>(row) * H;
+
+  uint4 xv[NC];
+  uint4 rv[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int v = lane + c * kWave;
+    if (v < nvec) {
+      xv[c] = ld16_stream(x + base + 8 * v);
+      if (ADD) rv[c] = ld16_stream(res + base + 8 * v);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int v = lane + c * kWave;
+    if (v < nvec) {
+      float f[8];
+      unpack8(xv[c], f);
+      if (ADD) {
+        float g[8];
+        unpack8(rv[c], g);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f[i] = round_bf(f[i] + g[i]);
+        xv[c] = pack8(f);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrt_rn(ss / static_cast<float>(H) + eps);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int v = lane + c * kWave;
+    if (v < nvec) {
+      float f[8], g[8];
+      unpack8(xv[c], f);
+      unpack8(ld16(gamma + 8 * v), g);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = norm_scale<MODE>(f[i], r, g[i]);
+      st16(y + base + 8 * v, pack8(f));
+      if (ADD) st16(res_out + base + 8 * v, xv[c]);
+    }
+  }
+}
+
+template <int NC>
+int launch_rows(const void* x, const void* res, const void* gamma, void* y, void* res_out,
+                int rows, int H, float eps, int mode, hipStream_t s) {
+  const dim3 block(256);
+  const dim3 grid((rows + 3) / 4);
+  auto X = static_cast<const uint16_t*>(x);
+  auto R = static_cast<const uint16_t*>(res);
+  auto G = static_cast<const uint16_t*>(gamma);
+  auto Y = static_cast<uint16_t*>(y);
+  auto RO = static_cast<uint16_t*>(res_out);
+  if (res) {
+    if (mode == 0) rms_rows_kernel<NC, true, 0><<<grid, block, 0, s>>>(X, R, G, Y, RO, rows, H, eps);
+    else rms_rows_kernel<NC, true, 1><<<grid, block, 0, s>>>(X, R, G, Y, RO, rows, H, eps);
+  } else {
+    if (mode == 0) rms_rows_kernel<NC, false, 0><<<grid, block, 0, s>>>(X, R, G, Y, RO, rows, H, eps);
+    else rms_rows_kernel<NC, false, 1><<<grid, block, 0, s>>>(X, R, G, Y, RO, rows, H, eps);
+  }
+  return launched("rms_norm_rows");
+}
+
+int dispatch_rows(const void* x, const void* res, const void* gamma, void* y, void* res_out,
+                  int64_t rows, int64_t H, float eps, int mode, hipStream_t s) {
+  const int nc = static_cast<int>((H / 8 + kWave - 1) / kWave);
+  switch (nc) {
+#define TFA_NC(n) case n: return launch_rows<n>(x, res, gamma, y, res_out, (int)rows, (int)H, eps, mode, s);
+    TFA_NC(1) TFA_NC(2) TFA_NC(3) TFA_NC(4) TFA_NC(5) TFA_NC(6) TFA_NC(7) TFA_NC(8)
+    TFA_NC(9) TFA_NC(10) TFA_NC(11) TFA_NC(12) TFA_NC(13) TFA_NC(14) TFA_NC(15) TFA_NC(16)
+#undef TFA_NC
+    default: return fail(TFA_ERR_SHAPE, "rms_norm: hidden %lld exceeds 8192", (long long)H);
+  }
+}
+
+int check_rows(const void* x, const void* gamma, const void* y, int64_t rows, int64_t H, int mode,
+               const char* fn) {
+  if (rows < 0 || rows > (1LL << 31) - 1) return fail(TFA_ERR_SHAPE, "%s: rows %lld out of range", fn, (long long)rows);
+  if (H <= 0 || H % 8 != 0 || H > 8192) return fail(TFA_ERR_SHAPE, "%s: hidden %lld must be a positive multiple of 8, at most 8192", fn, (long long)H);
+  if (mode != 0 && mode != 1) return fail(TFA_ERR_ARG, "%s: mode %d is not 0 or 1", fn, mode);
+  if (rows == 0) return TFA_OK;  // nothing to touch; empty tensors may be null
+  if (!x || !gamma || !y) return fail(TFA_ERR_NULL, "%s: null pointer", fn);
+  if (!aligned16(x) || !aligned16(gamma) || !aligned16(y)) return fail(TFA_ERR_ALIGN, "%s: tensors must be 16-byte aligned", fn);
+  return TFA_OK;
+}
+
+// Single row: Hout = A + bf16(sum_s P[s]); Xn = norm(Hout) * gamma (MODE 0).
+// One block; the row is staged in LDS between the sum of squares and the write.
+__global__ __launch_bounds__(256) void resid_rms_partials_kernel(
+    const uint16_t* __restrict__ a, const float* __restrict__ p, int sk,
+    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ hout,
+    uint16_t* __restrict__ xn, int H, float eps) {
+  extern __shared__ float row[];
+  __shared__ float red[16];
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) {
+    float acc = 0.f;
+    for (int s = 0; s < sk; ++s) acc += p[static_cast<size_t>(s) * H + i];
+    const float v = round_bf(bf2f(a[i]) + round_bf(acc));
+    hout[i] = static_cast<uint16_t>(f2bf(v));
+    row[i] = v;
+    ss += v * v;
+  }
+  ss = block_sum(ss, red);
+  const float r = rsqrt_rn(ss / static_cast<float>(H) + eps);
+  for (int i = threadIdx.x; i < H; i += blockDim.x)
+    xn[i] = static_cast<uint16_t>(f2bf(round_bf(round_bf(row[i] * r) * bf2f(gamma[i]))));
+}
+
+}  // namespace
+
+extern "C" {
+
+int tfa_rms_norm(const void* x, const void* gamma, void* y, int64_t rows, int64_t hidden,
+                 float eps, int mode, hipStream_t stream) {
+  int st = check_rows(x, gamma, y, rows, hidden, mode, "tfa_rms_norm");
+  if (st != TFA_OK) return st;
+  if (rows == 0) return TFA_OK;
+  return dispatch_rows(x, nullptr, gamma, y, nullptr, rows, hidden, eps, mode, stream);
+}
+
+int tfa_add_rms_norm(const void* x, const void* residual, const void* gamma, void* y,
+                     void* residual_out, int64_t rows, int64_t hidden, float eps, int mode,
+                     hipStream_t stream) {
+  int st = check_rows(x, gamma, y, rows, hidden, mode, "tfa_add_rms_norm");
+  if (st != TFA_OK || rows == 0) return st;
+  TFA_NONNULL(residual);
+  TFA_NONNULL(residual_out);
+  TFA_ALIGN16(residual);
+  TFA_ALIGN16(residual_out);
+  if (rows == 0) return TFA_OK;
+  return dispatch_rows(x, residual, gamma, y, residual_out, rows, hidden, eps, mode, stream);
+}
+
+int tfa_resid_rms_norm_partials(const void* a, const float* partials, int64_t splits,
+                                const void* gamma, void* h_out, void* xn, int64_t hidden,
+                                float eps, hipStream_t stream) {
+  TFA_NONNULL(a);
+  TFA_NONNULL(partials);
+  TFA_NONNULL(gamma);
+  TFA_NONNULL(h_out);
+  TFA_NONNULL(xn);
+  TFA_REQUIRE(hidden > 0 && hidden <= 8192, TFA_ERR_SHAPE, "tfa_resid_rms_norm_partials: hidden %lld not in [1, 8192]", (long long)hidden);
+  TFA_REQUIRE(splits > 0 && splits <= 4096, TFA_ERR_SHAPE, "tfa_resid_rms_norm_partials: splits %lld not in [1, 4096]", (long long)splits);
+  resid_rms_partials_kernel<<<1, 256, hidden * sizeof(float), stream>>>(
+      static_cast<const uint16_t*>(a), partials, (int)splits, static_cast<const uint16_t*>(gamma),
+      static_cast<uint16_t*>(h_out), static_cast<uint16_t*>(xn), (int)hidden, eps);
+  return launched("resid_rms_norm_partials");
+}
+
+}  // extern "C"

@@ -1,0 +1,300 @@
+// Thin PyTorch-ROCm extension over the C ABI in include/tilefoundry_amd.h.
+//
+// Each binding checks what the C ABI cannot see -- device, dtype, contiguity
+// and that every tensor's size agrees with the dimensions passed down -- then
+// calls the entry point on torch's current HIP stream. A status other than
+// TFA_OK becomes ValueError (bad arguments) or RuntimeError (a refused launch),
+// carrying the entry point's own message.
+#include <c10/hip/HIPStream.h>
+#include <torch/extension.h>
+
+#include <sstream>
+#include <string>
+
+#include "tilefoundry_amd.h"
+
+namespace {
+
+using at::Tensor;
+
+hipStream_t stream_of(const Tensor& t) {
+  return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+void raise_status(int st) {
+  if (st == TFA_OK) return;
+  std::string msg = tfa_last_error();
+  if (msg.empty()) msg = tfa_status_string(st);
+  if (st == TFA_ERR_LAUNCH) throw std::runtime_error(msg);
+  throw pybind11::value_error(msg);
+}
+
+[[noreturn]] void bad(const std::string& m) { throw pybind11::value_error(m); }
+
+void need(const Tensor& t, const char* name, at::ScalarType dt, int64_t numel = -1) {
+  if (!t.defined()) bad(std::string(name) + ": tensor required");
+  if (!t.is_cuda()) bad(std::string(name) + ": must be a GPU tensor");
+  if (t.scalar_type() != dt) {
+    std::ostringstream o;
+    o << name << ": dtype " << t.scalar_type() << ", expected " << dt;
+    bad(o.str());
+  }
+  if (!t.is_contiguous()) bad(std::string(name) + ": must be contiguous");
+  if (numel >= 0 && t.numel() != numel) {
+    std::ostringstream o;
+    o << name << ": has " << t.numel() << " elements, expected " << numel;
+    bad(o.str());
+  }
+}
+
+const auto BF = at::kBFloat16;
+const auto F32 = at::kFloat;
+const auto I32 = at::kInt;
+const auto I64 = at::kLong;
+
+// ------------------------------------------------------------------ norms
+int64_t last_dim(const Tensor& t) { return t.dim() == 0 ? 1 : t.size(-1); }
+
+void rms_norm(const Tensor& x, const Tensor& gamma, const Tensor& y, double eps, int64_t mode) {
+  const int64_t H = last_dim(x);
+  const int64_t rows = H ? x.numel() / H : 0;
+  need(x, "x", BF);
+  need(gamma, "gamma", BF, H);
+  need(y, "y", BF, x.numel());
+  raise_status(tfa_rms_norm(x.data_ptr(), gamma.data_ptr(), y.data_ptr(), rows, H, (float)eps,
+                            (int)mode, stream_of(x)));
+}
+
+void add_rms_norm(const Tensor& x, const Tensor& residual, const Tensor& gamma, const Tensor& y,
+                  const Tensor& residual_out, double eps, int64_t mode) {
+  const int64_t H = last_dim(x);
+  const int64_t rows = H ? x.numel() / H : 0;
+  need(x, "x", BF);
+  need(residual, "residual", BF, x.numel());
+  need(gamma, "gamma", BF, H);
+  need(y, "y", BF, x.numel());
+  need(residual_out, "residual_out", BF, x.numel());
+  raise_status(tfa_add_rms_norm(x.data_ptr(), residual.data_ptr(), gamma.data_ptr(), y.data_ptr(),
+                                residual_out.data_ptr(), rows, H, (float)eps, (int)mode,
+                                stream_of(x)));
+}
+
+void resid_rms_norm_partials(const Tensor& a, const Tensor& partials, const Tensor& gamma,
+                             const Tensor& h_out, const Tensor& xn, double eps) {
+  const int64_t H = a.numel();
+  need(a, "A", BF);
+  need(partials, "P", F32);
+  if (partials.dim() != 2 || partials.size(1) != H) bad("P: expected shape (SK, H)");
+  need(gamma, "G", BF, H);
+  need(h_out, "Hout", BF, H);
+  need(xn, "Xn", BF, H);
+  raise_status(tfa_resid_rms_norm_partials(a.data_ptr(), partials.data_ptr<float>(),
+                                           partials.size(0), gamma.data_ptr(), h_out.data_ptr(),
+                                           xn.data_ptr(), H, (float)eps, stream_of(a)));
+}
+
+// -------------------------------------------------------------- decode
+using OptT = std::optional<Tensor>;
+
+const void* opt_ptr(const OptT& t) { return (t && t->defined()) ? t->data_ptr() : nullptr; }
+template <typename T>
+T* opt_ptr_t(const OptT& t) { return (t && t->defined()) ? static_cast<T*>(t->data_ptr()) : nullptr; }
+
+void need_mat(const Tensor& w, const char* name, int64_t n, int64_t k) {
+  need(w, name, BF);
+  if (w.dim() != 2 || w.size(0) != n || w.size(1) != k) {
+    std::ostringstream o;
+    o << name << ": expected shape (" << n << ", " << k << "), got " << w.sizes();
+    bad(o.str());
+  }
+}
+
+void gemv(const Tensor& x, const Tensor& w, const Tensor& y) {
+  need(x, "x", BF);
+  const int64_t K = x.numel();
+  if (w.dim() != 2) bad("w: expected a 2-D (N, K) weight");
+  const int64_t N = w.size(0);
+  need_mat(w, "w", N, K);
+  const bool f32 = y.scalar_type() == F32;
+  need(y, "y", f32 ? F32 : BF, N);
+  raise_status(tfa_gemv(x.data_ptr(), w.data_ptr(), y.data_ptr(), N, K, f32 ? 1 : 0, stream_of(x)));
+}
+
+void rmsnorm_gemv(const Tensor& h, const Tensor& gamma, double eps, const Tensor& w, const Tensor& y) {
+  need(h, "h", BF);
+  const int64_t K = h.numel();
+  need(gamma, "gamma", BF, K);
+  if (w.dim() != 2) bad("w: expected a 2-D (N, K) weight");
+  const int64_t N = w.size(0);
+  need_mat(w, "w", N, K);
+  need(y, "y", BF, N);
+  raise_status(tfa_rmsnorm_gemv(h.data_ptr(), gamma.data_ptr(), (float)eps, w.data_ptr(),
+                                y.data_ptr(), N, K, stream_of(h)));
+}
+
+void gemv_residual(const Tensor& x, const Tensor& w, const Tensor& residual, const OptT& alpha,
+                   const Tensor& y) {
+  need(x, "x", BF);
+  const int64_t K = x.numel();
+  if (w.dim() != 2) bad("w: expected a 2-D (N, K) weight");
+  const int64_t N = w.size(0);
+  need_mat(w, "w", N, K);
+  need(residual, "residual", BF, N);
+  need(y, "y", BF, N);
+  if (alpha) need(*alpha, "alpha", BF, 1);
+  if (y.data_ptr() == residual.data_ptr()) bad("y must not alias residual");
+  raise_status(tfa_gemv_residual(x.data_ptr(), w.data_ptr(), residual.data_ptr(), opt_ptr(alpha),
+                                 y.data_ptr(), N, K, stream_of(x)));
+}
+
+void rmsnorm_gemv_swiglu(const Tensor& h, const Tensor& gamma, double eps, const Tensor& w_gu,
+                         const Tensor& act) {
+  need(h, "h", BF);
+  const int64_t K = h.numel();
+  need(gamma, "gamma", BF, K);
+  const int64_t I = act.numel();
+  need_mat(w_gu, "w_gu", 2 * I, K);
+  need(act, "act", BF, I);
+  raise_status(tfa_rmsnorm_gemv_swiglu(h.data_ptr(), gamma.data_ptr(), (float)eps, w_gu.data_ptr(),
+                                       act.data_ptr(), I, K, stream_of(h)));
+}
+
+void lm_head_sample(const Tensor& h, const OptT& gamma, double eps, const Tensor& w,
+                    const Tensor& logits, const Tensor& block_val, const Tensor& block_idx,
+                    const Tensor& counter, const OptT& inp, const OptT& prompt_len,
+                    const OptT& ids, const OptT& pos, const OptT& sam, const OptT& err) {
+  need(h, "h", BF);
+  const int64_t K = h.numel();
+  if (gamma) need(*gamma, "gamma", BF, K);
+  if (w.dim() != 2) bad("w: expected a 2-D (V, K) weight");
+  const int64_t V = w.size(0);
+  need_mat(w, "w", V, K);
+  need(logits, "logits", F32, V);
+  const int64_t nb = tfa_lm_head_blocks(V);
+  need(block_val, "block_val", F32, nb);
+  need(block_idx, "block_idx", I32, nb);
+  need(counter, "counter", I32, 1);
+  int64_t nsteps = 0;
+  if (pos) {
+    need(*pos, "pos", I32, 1);
+    if (!inp || !prompt_len || !ids || !sam) bad("sampling needs inp, prompt_len, ids and sam");
+    need(*inp, "inp", I32);
+    nsteps = inp->numel();
+    need(*sam, "sam", I32, nsteps);
+    need(*prompt_len, "prompt_len", I32, 1);
+    need(*ids, "ids", I64, 1);
+  }
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_lm_head_sample(
+      h.data_ptr(), opt_ptr(gamma), (float)eps, w.data_ptr(), V, K, logits.data_ptr<float>(),
+      block_val.data_ptr<float>(), block_idx.data_ptr<int>(),
+      static_cast<unsigned int*>(counter.data_ptr()), opt_ptr_t<const int>(inp),
+      opt_ptr_t<const int>(prompt_len), opt_ptr_t<int64_t>(ids), opt_ptr_t<int>(pos),
+      opt_ptr_t<int>(sam), nsteps, opt_ptr_t<int>(err), stream_of(h)));
+}
+
+void decode_qkv(const OptT& h, const OptT& table, const OptT& ids, const OptT& h_copy,
+                const Tensor& gamma_in, double eps, const Tensor& w_qkv, int64_t hq, int64_t hkv,
+                int64_t head_dim, const Tensor& gamma_q, const Tensor& gamma_k, double eps_head,
+                const Tensor& cos_t, const Tensor& sin_t, const Tensor& pos, const Tensor& wr,
+                const Tensor& k_cache, const Tensor& v_cache, const Tensor& q,
+                const Tensor& scratch, const Tensor& counters, const OptT& err) {
+  const int64_t H = gamma_in.numel();
+  need(gamma_in, "gamma_in", BF, H);
+  int64_t vocab = 0;
+  if (table) {
+    need(*table, "table", BF);
+    if (table->dim() != 2 || table->size(1) != H) bad("table: expected (V, hidden)");
+    vocab = table->size(0);
+    if (!ids || !h_copy) bad("embed mode needs ids and h_copy");
+    need(*ids, "ids", I64, 1);
+    need(*h_copy, "h_copy", BF, H);
+  } else {
+    if (!h) bad("h required when no table is given");
+    need(*h, "h", BF, H);
+  }
+  const int64_t D = head_dim;
+  need_mat(w_qkv, "w_qkv", (hq + 2 * hkv) * D, H);
+  need(gamma_q, "gamma_q", BF, D);
+  need(gamma_k, "gamma_k", BF, D);
+  need(cos_t, "cos", BF);
+  need(sin_t, "sin", BF, cos_t.numel());
+  if (cos_t.dim() != 2 || cos_t.size(1) != D) bad("cos: expected (rows, head_dim)");
+  need(pos, "pos", I32, 1);
+  need(wr, "wr", I32, 1);
+  need(k_cache, "k_cache", BF);
+  need(v_cache, "v_cache", BF, k_cache.numel());
+  if (k_cache.numel() % (hkv * D) != 0) bad("k_cache: size is not a multiple of hkv*head_dim");
+  const int64_t cap = k_cache.numel() / (hkv * D);
+  need(q, "q", BF, hq * D);
+  need(scratch, "scratch", F32, (hq + hkv) * D);
+  need(counters, "counters", I32, hq + hkv);
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_decode_qkv(
+      opt_ptr(h), opt_ptr(table), opt_ptr_t<const int64_t>(ids), vocab, opt_ptr_t<void>(h_copy),
+      gamma_in.data_ptr(), (float)eps, w_qkv.data_ptr(), H, hq, hkv, D, gamma_q.data_ptr(),
+      gamma_k.data_ptr(), (float)eps_head, cos_t.data_ptr(), sin_t.data_ptr(), cos_t.size(0),
+      pos.data_ptr<int>(), wr.data_ptr<int>(), k_cache.data_ptr(), v_cache.data_ptr(), cap,
+      q.data_ptr(), scratch.data_ptr<float>(), static_cast<unsigned int*>(counters.data_ptr()),
+      opt_ptr_t<int>(err), stream_of(gamma_in)));
+}
+
+void decode_attention(const Tensor& q, const Tensor& k_cache, const Tensor& v_cache,
+                      const Tensor& pos, int64_t hq, int64_t hkv, int64_t split, double scale,
+                      const Tensor& op, const Tensor& mp, const Tensor& lp, const OptT& counters,
+                      const OptT& out, const OptT& err) {
+  const int64_t D = 128;
+  need(q, "q", BF, hq * D);
+  need(k_cache, "k_cache", BF);
+  need(v_cache, "v_cache", BF, k_cache.numel());
+  if (k_cache.numel() % (hkv * D) != 0) bad("k_cache: size is not a multiple of hkv*128");
+  const int64_t cap = k_cache.numel() / (hkv * D);
+  if (split <= 0 || cap % split != 0) bad("cache capacity must be a multiple of the split");
+  const int64_t ns = cap / split;
+  need(pos, "pos", I32, 1);
+  need(op, "op", F32, ns * hq * D);
+  need(mp, "mp", F32, ns * hq);
+  need(lp, "lp", F32, ns * hq);
+  if (counters) {
+    need(*counters, "counters", I32, hkv);
+    if (!out) bad("merging needs out");
+    need(*out, "out", BF, hq * D);
+  }
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_decode_attention(
+      q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), pos.data_ptr<int>(), hq, hkv, D, cap,
+      split, (float)scale, op.data_ptr<float>(), mp.data_ptr<float>(), lp.data_ptr<float>(),
+      opt_ptr_t<unsigned int>(counters), opt_ptr_t<void>(out), opt_ptr_t<int>(err), stream_of(q)));
+}
+
+void attn_combine(const Tensor& op, const Tensor& mp, const Tensor& lp, const Tensor& out) {
+  need(mp, "Mp", F32);
+  if (mp.dim() != 2) bad("Mp: expected (NS, HQ)");
+  const int64_t ns = mp.size(0), hq = mp.size(1);
+  need(lp, "Lp", F32, ns * hq);
+  need(op, "Op", F32);
+  if (op.numel() % (ns * hq) != 0) bad("Op: expected (NS, HQ, D)");
+  const int64_t D = op.numel() / (ns * hq);
+  need(out, "O", BF, hq * D);
+  raise_status(tfa_attn_combine(op.data_ptr<float>(), mp.data_ptr<float>(), lp.data_ptr<float>(),
+                                out.data_ptr(), ns, hq, D, stream_of(op)));
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "tilefoundry_amd: thin torch bindings over the gfx950 C ABI";
+  m.def("abi_version", &tfa_abi_version);
+  m.def("rms_norm", &rms_norm);
+  m.def("add_rms_norm", &add_rms_norm);
+  m.def("resid_rms_norm_partials", &resid_rms_norm_partials);
+  m.def("gemv", &gemv);
+  m.def("rmsnorm_gemv", &rmsnorm_gemv);
+  m.def("gemv_residual", &gemv_residual);
+  m.def("rmsnorm_gemv_swiglu", &rmsnorm_gemv_swiglu);
+  m.def("lm_head_blocks", [](int64_t vocab) { return tfa_lm_head_blocks(vocab); });
+  m.def("lm_head_sample", &lm_head_sample);
+  m.def("decode_qkv", &decode_qkv);
+  m.def("decode_attention", &decode_attention);
+  m.def("attn_combine", &attn_combine);
+}

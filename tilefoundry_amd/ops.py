@@ -1,0 +1,190 @@
+"""Per-op functions over the HIP kernels, torch tensors in and out.
+
+Every function writes into caller-owned buffers when ``out=`` (and friends)
+are given and allocates them otherwise -- the convention of the reference's
+``CompiledModule`` (src/tilefoundry/runtime/module.py:75-142) and of
+``examples/minicpm3_4b-cutedsl/kernels/reference_ops.py:24-28`` (``_into``).
+A call that passes every output allocates nothing and may be captured in a
+HIP graph.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import C
+
+BF16 = torch.bfloat16
+
+
+def _out(out, like, shape=None, dtype=None):
+    if out is not None:
+        return out
+    return torch.empty(like.shape if shape is None else shape, device=like.device,
+                       dtype=like.dtype if dtype is None else dtype)
+
+
+def rms_norm(x, gamma, eps: float, out=None, mode: int = 0):
+    """RMSNorm over the last axis. mode 0: ``bf16(bf16(x*r)*gamma)`` (Qwen3,
+    MiniCPM3); mode 1: ``bf16(x*r*(1+gamma))`` (Qwen3.5)."""
+    out = _out(out, x)
+    C.rms_norm(x, gamma, out, float(eps), int(mode))
+    return out
+
+
+def add_rms_norm(x, residual, gamma, eps: float, out=None, residual_out=None, mode: int = 0):
+    """Fused residual add + RMSNorm; returns ``(normed, bf16(x + residual))``.
+
+    ``residual_out`` may be ``residual`` itself (in-place update)."""
+    out = _out(out, x)
+    residual_out = _out(residual_out, x)
+    C.add_rms_norm(x, residual, gamma, out, residual_out, float(eps), int(mode))
+    return out, residual_out
+
+
+def resid_rms_norm(a, partials, gamma, eps: float, h_out=None, xn=None):
+    """``Hout = A + bf16(sum_s P[s])``; ``Xn = rms_norm(Hout)`` for one row."""
+    h_out = _out(h_out, a)
+    xn = _out(xn, a)
+    C.resid_rms_norm_partials(a, partials, gamma, h_out, xn, float(eps))
+    return h_out, xn
+
+
+# --------------------------------------------------------------- decode GEMVs
+# Weights are (out, in) = [N, K] row-major (the checkpoint's layout).
+
+def _dev_i32(v, device):
+    if isinstance(v, torch.Tensor):
+        return v
+    return torch.tensor([int(v)], dtype=torch.int32, device=device)
+
+
+def gemv(x, w, out=None, out_dtype=None):
+    """``x @ w.T`` for one row; f32 or bf16 out
+    (examples/minicpm3_4b-cutedsl/kernels/reference_ops.py:57-58)."""
+    dt = out_dtype or (out.dtype if out is not None else BF16)
+    out = _out(out, x, (w.shape[0],), dt)
+    C.gemv(x, w, out)
+    return out
+
+
+def rmsnorm_gemv(h, gamma, eps: float, w, out=None):
+    """``bf16(rms_norm(h, gamma) @ w.T)``
+    (examples/minicpm3_4b-cutedsl/kernels/reference_ops.py:46-48)."""
+    out = _out(out, h, (w.shape[0],))
+    C.rmsnorm_gemv(h, gamma, float(eps), w, out)
+    return out
+
+
+def gemv_residual(x, w, residual, alpha=None, out=None):
+    """``residual + bf16(x @ w.T)`` (``* alpha`` first when given)
+    (examples/minicpm3_4b-cutedsl/kernels/reference_ops.py:61-63)."""
+    out = _out(out, residual)
+    C.gemv_residual(x, w, residual, alpha, out)
+    return out
+
+
+def rmsnorm_gemv_swiglu(h, gamma, eps: float, w_gu, out=None):
+    """``bf16(silu(g)) * u`` for ``(g, u)`` the interleaved row pairs of
+    ``rms_norm(h) @ w_gu.T`` (examples/minicpm3_4b-cutedsl/kernels/reference_ops.py:66-69)."""
+    out = _out(out, h, (w_gu.shape[0] // 2,))
+    C.rmsnorm_gemv_swiglu(h, gamma, float(eps), w_gu, out)
+    return out
+
+
+class SampleState:
+    """Device-side greedy-loop state: prompt ids, length, next id, position, picks."""
+
+    def __init__(self, nsteps: int, device):
+        z = lambda n, dt=torch.int32: torch.zeros(n, dtype=dt, device=device)  # noqa: E731
+        self.inp = z(nsteps)
+        self.sam = z(nsteps)
+        self.plen = z(1)
+        self.ids = z(1, torch.int64)
+        self.pos = z(1)
+        self.err = z(1)
+
+
+def lm_head_argmax(h, gamma, eps: float, w, logits=None, block_val=None, block_idx=None,
+                   counter=None, sample: SampleState | None = None):
+    """f32 logits of ``rms_norm(h) @ w.T`` (``h`` as is when ``gamma`` is None) and
+    their argmax (lowest index on ties). With ``sample``, also the greedy sample
+    step. Returns ``(logits, best)``; ``best`` is read back (one sync)."""
+    dev = h.device
+    V = w.shape[0]
+    nb = C.lm_head_blocks(V)
+    logits = _out(logits, h, (V,), torch.float32)
+    block_val = _out(block_val, h, (nb,), torch.float32)
+    block_idx = _out(block_idx, h, (nb,), torch.int32)
+    counter = counter if counter is not None else torch.zeros(1, dtype=torch.int32, device=dev)
+    s = sample
+    C.lm_head_sample(h, gamma, float(eps), w, logits, block_val, block_idx, counter,
+                     s.inp if s else None, s.plen if s else None, s.ids if s else None,
+                     s.pos if s else None, s.sam if s else None, s.err if s else None)
+    best = int(block_idx[int(torch.argmax(block_val))]) if sample is None else None
+    if sample is not None:
+        p = int(sample.pos[0]) - 1
+        best = int(sample.sam[p])
+    return logits, best
+
+
+def decode_qkv(h, gamma_in, eps: float, w_qkv, hq: int, hkv: int, head_dim: int, gamma_q,
+               gamma_k, cos, sin, pos, wr, k_cache, v_cache, *, eps_head: float | None = None,
+               table=None, token=None, h_copy=None, q=None, scratch=None, counters=None,
+               err=None):
+    """Input norm + fused q|k|v GEMV + q/k head norm + RoPE at ``pos`` + cache
+    write at slot ``wr``; returns q (bf16 [hq*head_dim]). With ``table`` the input
+    row is ``table[token]`` (copied into ``h_copy``)."""
+    dev = gamma_in.device
+    q = _out(q, gamma_in, (hq * head_dim,))
+    scratch = _out(scratch, gamma_in, ((hq + hkv) * head_dim,), torch.float32)
+    counters = counters if counters is not None else torch.zeros(hq + hkv, dtype=torch.int32, device=dev)
+    ids = None
+    if table is not None:
+        ids = token if isinstance(token, torch.Tensor) else torch.tensor([int(token)], dtype=torch.int64, device=dev)
+    C.decode_qkv(h, table, ids, h_copy, gamma_in, float(eps), w_qkv, hq, hkv, head_dim, gamma_q,
+                 gamma_k, float(eps if eps_head is None else eps_head), cos, sin,
+                 _dev_i32(pos, dev), _dev_i32(wr, dev), k_cache, v_cache, q, scratch, counters, err)
+    return q
+
+
+def _attn_bufs(q, k_cache, hq, hkv, split):
+    cap = k_cache.numel() // (hkv * 128)
+    ns = cap // split
+    op = torch.empty(ns, hq, 128, dtype=torch.float32, device=q.device)
+    mp = torch.empty(ns, hq, dtype=torch.float32, device=q.device)
+    lp = torch.empty(ns, hq, dtype=torch.float32, device=q.device)
+    return op, mp, lp
+
+
+def decode_attention(q, k_cache, v_cache, pos, hq: int, hkv: int, split: int = 64,
+                     scale: float | None = None, out=None, partials=None, counters=None, err=None):
+    """GQA decode attention of q over cache positions 0..pos; bf16 [hq*128]."""
+    dev = q.device
+    scale = 128 ** -0.5 if scale is None else scale
+    op, mp, lp = partials if partials is not None else _attn_bufs(q, k_cache, hq, hkv, split)
+    counters = counters if counters is not None else torch.zeros(hkv, dtype=torch.int32, device=dev)
+    out = _out(out, q, (hq * 128,))
+    C.decode_attention(q, k_cache, v_cache, _dev_i32(pos, dev), hq, hkv, split, float(scale),
+                       op, mp, lp, counters, out, err)
+    return out
+
+
+def attn_partial(q, k_cache, v_cache, pos, hq: int, hkv: int, split: int = 256,
+                 scale: float | None = None, partials=None):
+    """Split partials ``(Op [NS,HQ,128], Mp [NS,HQ], Lp [NS,HQ])``; splits past the
+    context are neutral (examples/qwen3_1_7b-tilelang/fast/kernels.py:418-501)."""
+    dev = q.device
+    scale = 128 ** -0.5 if scale is None else scale
+    op, mp, lp = partials if partials is not None else _attn_bufs(q, k_cache, hq, hkv, split)
+    C.decode_attention(q, k_cache, v_cache, _dev_i32(pos, dev), hq, hkv, split, float(scale),
+                       op, mp, lp, None, None, None)
+    return op, mp, lp
+
+
+def attn_combine(op, mp, lp, out=None):
+    """LSE merge of split partials into bf16 ``[HQ*D]``
+    (examples/qwen3_1_7b-tilelang/fast/kernels.py:504-540)."""
+    ns, hq = mp.shape
+    out = _out(out, op, (op.numel() // ns,), BF16)
+    C.attn_combine(op, mp, lp, out)
+    return out
