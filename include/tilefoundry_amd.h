@@ -102,58 +102,65 @@ int tfa_gemv_residual(const void* x, const void* w, const void* residual, const 
 int tfa_rmsnorm_gemv_swiglu(const void* h, const void* gamma, float eps, const void* w_gu,
                             void* act, int64_t inter, int64_t k, hipStream_t stream);
 
-/* Number of (value, index) block entries tfa_lm_head_sample writes for `vocab`. */
+/* Number of (value, index) block entries tfa_lm_head_argmax writes for `vocab`. */
 int64_t tfa_lm_head_blocks(int64_t vocab);
 
-/* Head + greedy pick: logits = rmsnorm(h) . w^T (f32; gamma == NULL: h as is),
- * per-block (max, lowest index) into block_val / block_idx (tfa_lm_head_blocks entries),
- * then in the last block: best = argmax (lowest index on ties); if pos != NULL the
- * sample step: sam[pos] = best; ids[0] = pos+1 < prompt_len ? inp[pos+1] : best;
- * pos += 1. counter: one zero-initialised uint32, reset by the kernel itself.
- * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:260-321 (lm_head) and
- * :591-637 (sample_step). */
-int tfa_lm_head_sample(const void* h, const void* gamma, float eps, const void* w, int64_t vocab,
+/* Head: logits = rmsnorm(h) . w^T in f32 (gamma == NULL: h as is), plus each
+ * block's best (max, lowest index) into block_val / block_idx
+ * (tfa_lm_head_blocks(vocab) entries). w is [vocab, k] (the tied embedding table
+ * serves as is). Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:260-321
+ * (lm_head). */
+int tfa_lm_head_argmax(const void* h, const void* gamma, float eps, const void* w, int64_t vocab,
                        int64_t k, float* logits, float* block_val, int* block_idx,
-                       unsigned int* counter, const int* inp, const int* prompt_len,
-                       int64_t* ids, int* pos, int* sam, int64_t nsteps, int* err,
                        hipStream_t stream);
 
-/* Fused decode qkv: x = rmsnorm(h) (or rmsnorm(table[ids[0]]) when table != NULL,
- * the gathered row also written to h_copy); [q|k|v] = x . w_qkv^T with w_qkv
- * [(hq+2hkv)*head_dim, hidden]; per head: q/k RMSNorm over head_dim (gamma_q /
- * gamma_k, eps_head), rotate-half RoPE at position pos[0] from cos_t / sin_t
- * [rope_rows, head_dim]; q -> q [hq*head_dim]; k, v -> k_cache / v_cache row wr[0]
- * ([cap, hkv*head_dim]). scratch f32 [(hq+hkv)*head_dim]; counters uint32
- * [hq+hkv], zero-initialised, self-resetting. err (optional int32[1]) gets a
- * nonzero code if a device-resident index is out of range.
+/* Greedy pick + sample step on the device: best = argmax over the block
+ * winners (lowest index on ties); sam[pos] = best; ids[0] = pos+1 < prompt_len ?
+ * inp[pos+1] : best; pos += 1. inp / sam are int32 [nsteps].
+ * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:591-637 (sample_step). */
+int tfa_sample_step(const float* block_val, const int* block_idx, int64_t nblocks, const int* inp,
+                    const int* prompt_len, int64_t* ids, int* pos, int* sam, int64_t nsteps,
+                    int* err, hipStream_t stream);
+
+/* Decode q|k|v projection: x = rmsnorm(h) (or rmsnorm(table[ids[0]]) when
+ * table != NULL, the gathered row also written to h_copy); y = x . w_qkv^T with
+ * w_qkv [(n_qk + n_v), hidden]; rows [0, n_qk) -> qk_out (bf16, raw: the head
+ * norm and RoPE are applied by tfa_decode_attention), rows [n_qk, n_qk + n_v)
+ * -> v_cache row wr[0] ([cap, n_v]). err (optional int32[1]) receives a nonzero
+ * code if a device-resident index is out of range.
  * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:58-79 + :123-145 +
- * :328-411 (rms_norm, gemv(qkv), qk_rope_cache) and :579-588 (embed). */
+ * :579-588 (rms_norm, gemv(qkv), embed) and the value write of :328-411. */
 int tfa_decode_qkv(const void* h, const void* table, const int64_t* ids, int64_t vocab,
                    void* h_copy, const void* gamma_in, float eps, const void* w_qkv,
-                   int64_t hidden, int64_t hq, int64_t hkv, int64_t head_dim,
-                   const void* gamma_q, const void* gamma_k, float eps_head, const void* cos_t,
-                   const void* sin_t, int64_t rope_rows, const int* pos, const int* wr,
-                   void* k_cache, void* v_cache, int64_t cap, void* q, float* scratch,
-                   unsigned int* counters, int* err, hipStream_t stream);
+                   int64_t hidden, int64_t n_qk, int64_t n_v, void* qk_out, const int* wr,
+                   void* v_cache, int64_t cap, int* err, hipStream_t stream);
 
-/* Split-KV GQA decode attention of q [hq*128] over cache positions 0..pos[0]
- * (k_cache / v_cache [cap, hkv*128], position-major), scores scaled by `scale`
- * in f32 after the dot, softmax in f32 per split of `split` positions (64, 128
- * or 256), bf16 weights into P.V. Partials op [cap/split, hq, 128], mp / lp
- * [cap/split, hq]. With counters (uint32 [hkv], zeroed, self-resetting) the last
- * block of each kv head merges the splits into out (bf16 [hq*128]); without,
- * splits past the context are written neutral (m = -1e30, l = 0, o = 0).
+/* Split-KV GQA decode attention (head_dim 128), caches [cap, hkv*128]
+ * position-major, attending slots 0..wr[0]. Scores scaled by `scale` in f32
+ * after the dot; softmax in f32 per split of `split` (64, 128 or 256) slots;
+ * bf16 weights into P.V. Partials op [cap/split, hq, 128], mp / lp
+ * [cap/split, hq]; splits past wr are left untouched unless `neutral`
+ * (then m = -1e30, l = 0, o = 0).
+ * Prepared mode (gamma_q == NULL): q is the final query [hq*128] and the cache
+ * already holds slot wr. Fused mode: q is the raw [q | k] projection
+ * [(hq+hkv)*128]; each query head gets Qwen3RMSNorm (gamma_q, eps_head) and
+ * rotate-half RoPE at pos[0] (cos / sin [rope_rows, 128]); the new key gets the
+ * same with gamma_k and is written to k_cache row wr[0].
  * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:418-501 (attn_partial)
- * and :504-540 (attn_combine). */
-int tfa_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* pos,
-                         int64_t hq, int64_t hkv, int64_t head_dim, int64_t cap, int64_t split,
-                         float scale, float* op, float* mp, float* lp, unsigned int* counters,
-                         void* out, int* err, hipStream_t stream);
+ * and :328-411 (qk_rope_cache). */
+int tfa_decode_attention(const void* q, const void* gamma_q, const void* gamma_k, float eps_head,
+                         const void* cos_t, const void* sin_t, int64_t rope_rows, void* k_cache,
+                         const void* v_cache, const int* pos, const int* wr, int64_t hq,
+                         int64_t hkv, int64_t head_dim, int64_t cap, int64_t split, float scale,
+                         float* op, float* mp, float* lp, int neutral, int* err,
+                         hipStream_t stream);
 
-/* out[h*D + d] = bf16(sum_s op[s,h,d] e^(mp[s,h]-M) / sum_s lp[s,h] e^(mp[s,h]-M)).
+/* out[h*D + d] = bf16(sum_s op[s,h,d] e^(mp[s,h]-M) / sum_s lp[s,h] e^(mp[s,h]-M))
+ * over all `splits`, or (wr != NULL) over the splits holding slots 0..wr[0].
  * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:504-540 (attn_combine). */
 int tfa_attn_combine(const float* op, const float* mp, const float* lp, void* out, int64_t splits,
-                     int64_t hq, int64_t head_dim, hipStream_t stream);
+                     int64_t hq, int64_t head_dim, const int* wr, int64_t split,
+                     hipStream_t stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

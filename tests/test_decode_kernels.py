@@ -114,7 +114,7 @@ def test_lm_head_argmax(dev):
     gamma = randn(H, g=g, std=0.1, mean=1.0)
     w = randn(V, H, g=g, std=0.02)
     ref = OQ.lm_logits(h, gamma, w.float(), EPS)
-    logits, best = ops.lm_head_argmax(h.to(dev), gamma.to(dev), EPS, w.to(dev))
+    logits, best = ops.greedy_pick(h.to(dev), gamma.to(dev), EPS, w.to(dev))
     assert max_rel(logits, ref) < 5e-3
     assert best == int(torch.argmax(logits.cpu())), "argmax of the kernel's own logits"
     top = torch.topk(ref, 2).values
@@ -136,7 +136,7 @@ def test_lm_head_planted_ties(dev):
     for idx in (4000, 17, 2500, 18):   # same max planted at four rows, in two blocks
         w[idx] = winner
     x[:8] = 1.0
-    logits, best = ops.lm_head_argmax(x.to(dev), None, EPS, w.to(dev))
+    logits, best = ops.greedy_pick(x.to(dev), None, EPS, w.to(dev))
     lg = logits.cpu()
     assert best == int(torch.argmax(lg)) == 17
 
@@ -150,19 +150,32 @@ def test_sample_step(dev, pos, expect_prompt):
     from tilefoundry_amd import ops
 
     g = gen(29)
-    Vs, K, PL, NSTEPS = 8192, 256, 5, 64
-    w = randn(Vs, K, g=g, std=0.02)
-    x = randn(K, g=g)
+    NB, NSTEPS, PL = 1187, 64, 5
+    bv = torch.randn(NB, generator=g)
+    bi = torch.randint(0, V, (NB,), generator=g, dtype=torch.int32)
     st = ops.SampleState(NSTEPS, dev)
     st.inp.copy_(torch.arange(NSTEPS, dtype=torch.int32) + 100)
     st.plen.fill_(PL)
     st.pos.fill_(pos)
-    logits, best = ops.lm_head_argmax(x.to(dev), None, EPS, w.to(dev), sample=st)
+    ops.sample_step(bv.to(dev), bi.to(dev), st)
+    best = int(bi[int(bv.argmax())])
     want_next = pos + 1 + 100 if expect_prompt else best
     assert int(st.sam[pos]) == best
     assert int(st.ids[0]) == want_next
     assert int(st.pos[0]) == pos + 1
     assert int(st.err[0]) == 0
+
+
+@pytest.mark.gpu
+def test_sample_step_ties_lowest_index(dev):
+    from tilefoundry_amd import ops
+
+    bv = torch.tensor([1.0, 5.0, 2.0, 5.0, 5.0])
+    bi = torch.tensor([10, 900, 20, 300, 301], dtype=torch.int32)
+    st = ops.SampleState(8, dev)
+    st.plen.fill_(1)
+    ops.sample_step(bv.to(dev), bi.to(dev), st)
+    assert int(st.sam[0]) == 300
 
 
 def _qkv_case(g, cap=512):
@@ -186,25 +199,20 @@ def _qkv_ref(h, gamma_in, wq, wk, wv, gq, gk, cos, sin, pos):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("pos,wr", [(0, 0), (37, 37), (300, 5), (511, 511)])
-def test_decode_qkv(dev, pos, wr):
+@pytest.mark.parametrize("wr", [0, 37, 511])
+def test_decode_qkv(dev, wr):
+    """Raw q|k out, v into exactly one cache row (bit-exact cache indexing)."""
     from tilefoundry_amd import ops
 
     cap = 512
-    args = _qkv_case(gen(31 + pos), cap)
-    h, gamma_in, wq, wk, wv, gq, gk, cos, sin = args
-    qr, kr, vr = _qkv_ref(*args, pos)
-    kc = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
+    h, gamma_in, wq, wk, wv, *_ = _qkv_case(gen(31 + wr), cap)
+    xn = ON.rms_norm_q(h, gamma_in, EPS)
     vc = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
     w_qkv = torch.cat([wq, wk, wv], 0).to(dev)
-    q = ops.decode_qkv(h.to(dev), gamma_in.to(dev), EPS, w_qkv, HQ, HKV, D, gq.to(dev), gk.to(dev),
-                       cos.to(dev), sin.to(dev), pos, wr, kc, vc)
-    assert_close("q", q.view(HQ, D), qr)
-    assert_close("k", kc[wr].view(HKV, D), kr)
-    assert_close("v", vc[wr].view(HKV, D), vr)
-    # exactly one cache row written (bit-exact cache indexing)
-    written = (kc.cpu().view(torch.int16) != 0).any(1).nonzero().flatten().tolist()
-    assert written == [wr]
+    qk = ops.decode_qkv(h.to(dev), gamma_in.to(dev), EPS, w_qkv, (HQ + HKV) * D, wr, vc)
+    assert_close("q raw", qk[: HQ * D], OQ.proj(xn, wq))
+    assert_close("k raw", qk[HQ * D:], OQ.proj(xn, wk))
+    assert_close("v", vc[wr], OQ.proj(xn, wv))
     written = (vc.cpu().view(torch.int16) != 0).any(1).nonzero().flatten().tolist()
     assert written == [wr]
 
@@ -216,38 +224,66 @@ def test_decode_qkv_embed_mode(dev):
     cap = 64
     g = gen(37)
     table = randn(1000, H, g=g, std=0.02)
-    _, gamma_in, wq, wk, wv, gq, gk, cos, sin = _qkv_case(g, cap)
-    tok, pos = 777, 3
-    qr, kr, vr = _qkv_ref(table[tok], gamma_in, wq, wk, wv, gq, gk, cos, sin, pos)
-    kc = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
+    _, gamma_in, wq, wk, wv, *_ = _qkv_case(g, cap)
+    tok = 777
+    xn = ON.rms_norm_q(table[tok], gamma_in, EPS)
     vc = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
-    w_qkv = torch.cat([wq, wk, wv], 0).to(dev)
     hcopy = torch.zeros(H, dtype=BF, device=dev)
-    q = ops.decode_qkv(None, gamma_in.to(dev), EPS, w_qkv, HQ, HKV, D, gq.to(dev), gk.to(dev),
-                       cos.to(dev), sin.to(dev), pos, pos, kc, vc, table=table.to(dev),
-                       token=tok, h_copy=hcopy)
+    w_qkv = torch.cat([wq, wk, wv], 0).to(dev)
+    qk = ops.decode_qkv(None, gamma_in.to(dev), EPS, w_qkv, (HQ + HKV) * D, 3, vc,
+                        table=table.to(dev), token=tok, h_copy=hcopy)
     assert_equal("gathered row", hcopy, table[tok])
-    assert_close("q", q.view(HQ, D), qr)
-    assert_close("k", kc[pos].view(HKV, D), kr)
-    assert_close("v", vc[pos].view(HKV, D), vr)
+    assert_close("q raw", qk[: HQ * D], OQ.proj(xn, wq))
+    assert_close("v", vc[3], OQ.proj(xn, wv))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("pos,wr", [(0, 0), (37, 37), (300, 5), (511, 511)])
+def test_fused_attention_prologue(dev, pos, wr):
+    """q / k head norm + RoPE at pos inside the attention kernel; the new key lands
+    in k_cache[wr] and only there; the output attends slots 0..wr."""
+    from tilefoundry_amd import ops
+
+    cap = 512
+    args = _qkv_case(gen(53 + pos), cap)
+    h, gamma_in, wq, wk, wv, gq, gk, cos, sin = args
+    qr, kr, vr = _qkv_ref(*args, pos)
+    g = gen(59)
+    kc = torch.zeros(cap, HKV, D, dtype=BF)
+    vc = torch.zeros(cap, HKV, D, dtype=BF)
+    kc[:wr] = randn(wr, HKV, D, g=g)
+    vc[:wr] = randn(wr, HKV, D, g=g)
+    vc[wr] = vr
+    xn = ON.rms_norm_q(h, gamma_in, EPS)
+    qk_raw = torch.cat([OQ.proj(xn, wq), OQ.proj(xn, wk)])
+    kd, vd = kc.view(cap, -1).to(dev), vc.view(cap, -1).to(dev)
+    out = ops.decode_attention(qk_raw.to(dev), kd, vd, wr, HQ, HKV, split=64,
+                               rope=(gq.to(dev), gk.to(dev), EPS, cos.to(dev), sin.to(dev), pos))
+    assert_close("k written", kd[wr].view(HKV, D), kr)
+    before = kc.view(cap, -1).clone()
+    before[wr] = kd[wr].cpu()
+    assert_equal("no other cache row touched", kd, before)
+    kk = torch.cat([kc[:wr], kr.unsqueeze(0)])
+    ref = OQ.attend(qr, kk, vc[: wr + 1], D ** -0.5)
+    assert_close("attention output", out, ref)
 
 
 @pytest.mark.gpu
 def test_rope_position_zero_is_identity(dev):
-    """At position 0 (cos = 1, sin = 0) q is exactly the head-normed projection."""
+    """At position 0 (cos = 1, sin = 0) the key written is exactly the head-normed
+    projection: RoPE contributes nothing."""
     from tilefoundry_amd import ops
 
     cap = 64
-    args = _qkv_case(gen(41), cap)
-    h, gamma_in, wq, wk, wv, gq, gk, cos, sin = args
-    kc = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
-    vc = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
-    w_qkv = torch.cat([wq, wk, wv], 0).to(dev)
-    q = ops.decode_qkv(h.to(dev), gamma_in.to(dev), EPS, w_qkv, HQ, HKV, D, gq.to(dev), gk.to(dev),
-                       cos.to(dev), sin.to(dev), 0, 0, kc, vc).cpu()
-    # the unrotated head norm of the kernel's own projection must be what comes out
-    qn = OQ.head_norm(OQ.proj(ON.rms_norm_q(h, gamma_in, EPS), wq).view(HQ, D), gq, EPS)
-    assert_close("q at pos 0", q.view(HQ, D), qn)
+    h, gamma_in, wq, wk, wv, gq, gk, cos, sin = _qkv_case(gen(41), cap)
+    xn = ON.rms_norm_q(h, gamma_in, EPS)
+    k_raw = OQ.proj(xn, wk)
+    qk_raw = torch.cat([OQ.proj(xn, wq), k_raw])
+    kd = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
+    vd = torch.zeros(cap, HKV * D, dtype=BF, device=dev)
+    ops.decode_attention(qk_raw.to(dev), kd, vd, 0, HQ, HKV, split=64,
+                         rope=(gq.to(dev), gk.to(dev), EPS, cos.to(dev), sin.to(dev), 0))
+    assert_equal("k at pos 0", kd[0].view(HKV, D), OQ.head_norm(k_raw.view(HKV, D), gk, EPS))
 
 
 def _attn_case(g, cap, n):
@@ -286,16 +322,17 @@ def test_attention_single_key_returns_value(dev):
 
 
 @pytest.mark.gpu
-def test_attention_partials_and_combine(dev):
-    """Partials-only form + the separate combine equal the merged form."""
+def test_attention_neutral_partials_and_full_combine(dev):
+    """Neutral partials past the context merged over every split equal the merge
+    over the active splits only."""
     from tilefoundry_amd import ops
 
     cap, n = 2560, 700
     q, kc, vc = _attn_case(gen(47), cap, n)
     kd, vd, qd = kc.view(cap, -1).to(dev), vc.view(cap, -1).to(dev), q.reshape(-1).to(dev)
-    merged = ops.decode_attention(qd, kd, vd, n - 1, HQ, HKV, split=256)
-    op, mp, lp = ops.attn_partial(qd, kd, vd, n - 1, HQ, HKV, split=256)
+    op, mp, lp = ops.attn_partial(qd, kd, vd, n - 1, HQ, HKV, split=256, neutral=True)
     neutral = torch.tensor(-1.0e30, dtype=torch.float32).item()
     assert float(lp[3:].abs().max()) == 0.0 and float(mp[3:].max()) == neutral
-    combined = ops.attn_combine(op, mp, lp)
-    assert_equal("combine == merged", combined, merged)
+    full = ops.attn_combine(op, mp, lp)
+    active = ops.attn_combine(op, mp, lp, wr=n - 1, split=256)
+    assert_equal("combine over all == over active", full, active)

@@ -1,0 +1,396 @@
+// Split-KV GQA decode attention (head_dim 128) and the merge of its splits.
+//
+// attn_decode: one block per (split, kv head). The block scores its G query
+// heads against the cached slots of its split that are <= wr (the newest slot),
+// normalises against the split's own max in f32, lands the weights in bf16 and
+// accumulates P.V in f32 -- the order of
+// examples/qwen3_1_7b-tilelang/fast/kernels.py:418-501 (attn_partial). Lanes:
+// slot = lane / 16 picks one of four positions, dc = lane % 16 one 8-wide slice
+// of D, so one load instruction of a wave reads four whole 256-byte key rows.
+// Every K and V load of the split is issued before any arithmetic.
+//
+// Fused mode (q / k head scales given): the block starts from the raw q|k
+// projection and applies the per-head Qwen3RMSNorm and the rotate-half RoPE at
+// `pos` itself (the query of its G heads; the new key too in the one block whose
+// split holds slot wr, which also writes that key into the cache). Each block
+// redoes its two heads' norm from 512 bytes in L2 -- cheaper than any
+// cross-block hand-off. Replaces examples/qwen3_1_7b-tilelang/fast/kernels.py:328-411
+// (qk_rope_cache) in the step.
+//
+// attn_combine: log-sum-exp merge of the splits into bf16 head-major output,
+// examples/qwen3_1_7b-tilelang/fast/kernels.py:504-540.
+#include "abi_util.h"
+#include "common.h"
+
+using namespace tfa;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int D = 128;
+
+struct AttnArgs {
+  const uint16_t* q;      // prepared q [hq*D]; fused mode: raw [q | k] [(hq+hkv)*D]
+  const uint16_t* gq;     // [D] q head scale (fused mode when non-null)
+  const uint16_t* gk;     // [D] k head scale
+  float eps_head;
+  const uint16_t* cos_t;  // [mp_rows, D]
+  const uint16_t* sin_t;
+  int mp_rows;
+  uint16_t* kc;           // [cap, hkv*D]
+  const uint16_t* vc;     // [cap, hkv*D]
+  const int* pos;         // [1] rope position (fused mode)
+  const int* wr;          // [1] newest slot; attend slots 0..wr
+  float* op;              // [ns, hq, D]
+  float* mp;              // [ns, hq]
+  float* lp;              // [ns, hq]
+  int neutral;            // write neutral partials for splits past the context
+  int* err;
+  int hq, hkv, cap, ns;
+  float scale;
+};
+
+TFA_DEV void set_err(int* err, int code) {
+  if (err) atomicExch(err, code);
+}
+
+// Per-head Qwen3RMSNorm + rotate-half RoPE of one 128-wide head by one wave:
+// lane l owns d = l and its rotation partner d = l + 64.
+TFA_DEV void norm_rope_head(const uint16_t* raw, const uint16_t* gam, float eps, float c0, float s0,
+                            float c1, float s1, int lane, float& o0, float& o1) {
+  const float x0 = bf2f(raw[lane]);
+  const float x1 = bf2f(raw[lane + 64]);
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float rs = rsqrt_rn(ss / static_cast<float>(D) + eps);
+  const float n0 = round_bf(round_bf(x0 * rs) * bf2f(gam[lane]));
+  const float n1 = round_bf(round_bf(x1 * rs) * bf2f(gam[lane + 64]));
+  // rotate_half: first half pairs with -x[d + 64], second half with +x[d - 64]
+  o0 = round_bf(__fadd_rn(__fmul_rn(n0, c0), __fmul_rn(-n1, s0)));
+  o1 = round_bf(__fadd_rn(__fmul_rn(n1, c1), __fmul_rn(n0, s1)));
+}
+
+template <int G, int NIT>
+__global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a) {
+  constexpr int SS = 16 * NIT;
+  __shared__ float qs[G][D];
+  __shared__ float knew[D];
+  __shared__ float obuf[kWaves][G][D];
+  __shared__ float red[2][kWaves][G];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  const int slot = lane >> 4;
+  const int dc = lane & 15;
+  const int s = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int t = threadIdx.x;
+  const int KN = a.hkv * D;
+
+  int last = a.wr[0];
+  if (last < 0 || last >= a.cap) {
+    if (s == 0 && kvh == 0 && t == 0) set_err(a.err, 4);
+    last = last < 0 ? -1 : a.cap - 1;
+  }
+  const int n = last + 1;
+  const int start = s * SS;
+  if (start >= n) {
+    if (a.neutral) {
+      for (int e = t; e < G * D; e += kThreads) {
+        const int g = e / D, d = e % D;
+        const int h = kvh * G + g;
+        a.op[(static_cast<size_t>(s) * a.hq + h) * D + d] = 0.f;
+        if (d == 0) {
+          a.mp[s * a.hq + h] = -1.0e30f;
+          a.lp[s * a.hq + h] = 0.f;
+        }
+      }
+    }
+    return;
+  }
+  const bool fused = a.gq != nullptr;
+  const bool has_new = fused && last < start + SS;  // this split holds the newest slot
+
+  // 1. every K / V load of the split, first
+  uint4 kv[NIT], vv[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int pi = start + it * 16 + wid * 4 + slot;
+    const bool valid = pi < n;
+    const size_t off = static_cast<size_t>(pi) * KN + kvh * D + 8 * dc;
+    kv[it] = valid ? ld16_stream(a.kc + off) : make_uint4(0, 0, 0, 0);
+    vv[it] = valid ? ld16_stream(a.vc + off) : make_uint4(0, 0, 0, 0);
+  }
+
+  // 2. the query (and, in one block, the new key) while they are in flight
+  if (fused) {
+    int p = a.pos[0];
+    if (p < 0 || p >= a.mp_rows) {
+      if (s == 0 && kvh == 0 && t == 0) set_err(a.err, 5);
+      p = 0;
+    }
+    const float c0 = bf2f(a.cos_t[static_cast<size_t>(p) * D + lane]);
+    const float s0 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane]);
+    const float c1 = bf2f(a.cos_t[static_cast<size_t>(p) * D + lane + 64]);
+    const float s1 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane + 64]);
+    for (int hh = wid; hh < G + (has_new ? 1 : 0); hh += kWaves) {
+      float o0, o1;
+      if (hh < G) {
+        norm_rope_head(a.q + (kvh * G + hh) * D, a.gq, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
+        qs[hh][lane] = o0;
+        qs[hh][lane + 64] = o1;
+      } else {
+        norm_rope_head(a.q + (a.hq + kvh) * D, a.gk, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
+        knew[lane] = o0;
+        knew[lane + 64] = o1;
+        uint16_t* dst = a.kc + static_cast<size_t>(last) * KN + kvh * D;
+        dst[lane] = static_cast<uint16_t>(f2bf(o0));
+        dst[lane + 64] = static_cast<uint16_t>(f2bf(o1));
+      }
+    }
+  } else {
+    for (int e = t; e < G * D; e += kThreads) qs[e / D][e % D] = bf2f(a.q[(kvh * G) * D + e]);
+  }
+  __syncthreads();
+
+  // 3. scores (scale applied to the finished f32 dot), kept in registers: after
+  //    the 16-lane butterfly every lane of a position's group holds its score
+  float qf[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qf[g][i] = qs[g][8 * dc + i];
+  float sv[G][NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int pi = start + it * 16 + wid * 4 + slot;
+    float kf[8];
+    if (has_new && pi == last) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kf[i] = knew[8 * dc + i];
+    } else {
+      unpack8(kv[it], kf);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) d = fmaf(qf[g][i], kf[i], d);
+      d = group_sum<16>(d);
+      sv[g][it] = pi < n ? d * a.scale : -INFINITY;
+    }
+  }
+
+  // 4. the split's max and sum, f32: in-lane, across the wave's four position
+  //    slots, then across the four waves through LDS
+  float m[G], l[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mx = sv[g][0];
+#pragma unroll
+    for (int it = 1; it < NIT; ++it) mx = fmaxf(mx, sv[g][it]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    if (lane == 0) red[0][wid][g] = mx;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = fmaxf(fmaxf(red[0][0][g], red[0][1][g]), fmaxf(red[0][2][g], red[0][3][g]));
+    float ls = 0.f;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const float e = sv[g][it] == -INFINITY ? 0.f : expf(sv[g][it] - m[g]);
+      ls += e;
+      sv[g][it] = round_bf(e);  // bf16 weights into the value product
+    }
+    ls += __shfl_xor(ls, 16, kWave);
+    ls += __shfl_xor(ls, 32, kWave);
+    if (lane == 0) red[1][wid][g] = ls;
+  }
+
+  // 5. P.V in registers
+  float o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[g][i] = 0.f;
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    float vf[8];
+    unpack8(vv[it], vf);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[g][i] = fmaf(sv[g][it], vf[i], o[g][i]);
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float v = o[g][i];
+      v += __shfl_xor(v, 16, kWave);
+      v += __shfl_xor(v, 32, kWave);
+      o[g][i] = v;
+    }
+  if (slot == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) obuf[wid][g][8 * dc + i] = o[g][i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    l[g] = (red[1][0][g] + red[1][1][g]) + (red[1][2][g] + red[1][3][g]);
+  for (int e = t; e < G * D; e += kThreads) {
+    const int g = e / D, d = e % D;
+    const float v = (obuf[0][g][d] + obuf[1][g][d]) + (obuf[2][g][d] + obuf[3][g][d]);
+    const int h = kvh * G + g;
+    a.op[(static_cast<size_t>(s) * a.hq + h) * D + d] = v;
+    if (d == 0) {
+      a.mp[s * a.hq + h] = m[g];
+      a.lp[s * a.hq + h] = l[g];
+    }
+  }
+}
+
+template <int G>
+int launch_attn_g(const AttnArgs& a, int ss, hipStream_t st) {
+  const dim3 grid(a.ns, a.hkv);
+  switch (ss) {
+    case 64: attn_decode_kernel<G, 4><<<grid, kThreads, 0, st>>>(a); break;
+    case 128: attn_decode_kernel<G, 8><<<grid, kThreads, 0, st>>>(a); break;
+    case 256: attn_decode_kernel<G, 16><<<grid, kThreads, 0, st>>>(a); break;
+    default: return fail(TFA_ERR_SHAPE, "attn_decode: split %d not in {64, 128, 256}", ss);
+  }
+  return launched("attn_decode");
+}
+
+// Merge: out[h*Dh + d] = bf16(sum_s op e^(mp-M) / sum_s lp e^(mp-M)). With wr,
+// only the splits that hold slots <= wr[0] are read. One block per head: the
+// split statistics arrive in one parallel round trip, then eight groups of
+// threads each sum every eighth split of the partial outputs, so the loads of
+// all splits are in flight together; the groups meet in LDS in group order.
+constexpr int kCombThreads = 1024;
+constexpr int kCombGroups = 8;
+constexpr int kCombMaxSplits = 1024;
+constexpr int kCombMaxD = kCombThreads / kCombGroups;
+
+__global__ __launch_bounds__(kCombThreads) void attn_combine_kernel(
+    const float* op, const float* mp, const float* lp, uint16_t* out, int ns, int hq, int Dh,
+    const int* wr, int split) {
+  __shared__ float s_e[kCombMaxSplits];
+  __shared__ float s_l[kCombMaxSplits];
+  __shared__ float s_red[kCombGroups][kCombMaxD];
+  __shared__ float s_mx[kCombThreads / kWave];
+  __shared__ float s_den;
+  const int h = blockIdx.x;
+  const int t = threadIdx.x;
+  int nact = ns;
+  if (wr) {
+    const int w = wr[0];
+    nact = w < 0 ? 0 : w / split + 1;
+    if (nact > ns) nact = ns;
+  }
+  if (nact > kCombMaxSplits) nact = kCombMaxSplits;
+  // 1. statistics, one split per thread
+  float mj = -INFINITY;
+  for (int j = t; j < nact; j += kCombThreads) {
+    mj = fmaxf(mj, mp[j * hq + h]);
+    s_l[j] = lp[j * hq + h];
+  }
+  float mx = wave_max(mj);
+  if ((t & (kWave - 1)) == 0) s_mx[t / kWave] = mx;
+  __syncthreads();
+  mx = -INFINITY;
+  for (int w = 0; w < kCombThreads / kWave; ++w) mx = fmaxf(mx, s_mx[w]);
+  for (int j = t; j < nact; j += kCombThreads) s_e[j] = expf(mp[j * hq + h] - mx);
+  __syncthreads();
+  if (t == 0) {
+    float den = 0.f;
+    for (int j = 0; j < nact; ++j) den = fmaf(s_l[j], s_e[j], den);
+    s_den = den;
+  }
+  // 2. partial outputs: group gi sums splits gi, gi + 8, ...
+  const int gi = t / kCombMaxD;
+  const int d = t % kCombMaxD;
+  if (d < Dh) {
+    float num = 0.f;
+    for (int j = gi; j < nact; j += kCombGroups)
+      num = fmaf(op[(static_cast<size_t>(j) * hq + h) * Dh + d], s_e[j], num);
+    s_red[gi][d] = num;
+  }
+  __syncthreads();
+  if (t < Dh) {
+    float num = 0.f;
+    for (int g = 0; g < kCombGroups; ++g) num += s_red[g][t];
+    out[h * Dh + t] = static_cast<uint16_t>(f2bf(num / s_den));
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int tfa_decode_attention(const void* q, const void* gamma_q, const void* gamma_k, float eps_head,
+                         const void* cos_t, const void* sin_t, int64_t rope_rows, void* k_cache,
+                         const void* v_cache, const int* pos, const int* wr, int64_t hq,
+                         int64_t hkv, int64_t head_dim, int64_t cap, int64_t split, float scale,
+                         float* op, float* mp, float* lp, int neutral, int* err,
+                         hipStream_t stream) {
+  if (!q || !k_cache || !v_cache || !wr || !op || !mp || !lp)
+    return fail(TFA_ERR_NULL, "tfa_decode_attention: null pointer argument");
+  if (head_dim != D) return fail(TFA_ERR_SHAPE, "tfa_decode_attention: head_dim %lld, only 128 supported", (long long)head_dim);
+  if (hkv <= 0 || hq % hkv != 0) return fail(TFA_ERR_SHAPE, "tfa_decode_attention: hq %lld not a multiple of hkv %lld", (long long)hq, (long long)hkv);
+  if (split <= 0 || cap <= 0 || cap % split != 0)
+    return fail(TFA_ERR_SHAPE, "tfa_decode_attention: cap %lld not a positive multiple of split %lld", (long long)cap, (long long)split);
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache))
+    return fail(TFA_ERR_ALIGN, "tfa_decode_attention: q / caches not 16-byte aligned");
+  if (gamma_q && (!gamma_k || !cos_t || !sin_t || !pos || rope_rows <= 0))
+    return fail(TFA_ERR_NULL, "tfa_decode_attention: fused mode needs gamma_k, cos, sin, pos");
+  AttnArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.gq = static_cast<const uint16_t*>(gamma_q);
+  a.gk = static_cast<const uint16_t*>(gamma_k);
+  a.eps_head = eps_head;
+  a.cos_t = static_cast<const uint16_t*>(cos_t);
+  a.sin_t = static_cast<const uint16_t*>(sin_t);
+  a.mp_rows = (int)rope_rows;
+  a.kc = static_cast<uint16_t*>(k_cache);
+  a.vc = static_cast<const uint16_t*>(v_cache);
+  a.pos = pos;
+  a.wr = wr;
+  a.op = op;
+  a.mp = mp;
+  a.lp = lp;
+  a.neutral = neutral;
+  a.err = err;
+  a.hq = (int)hq;
+  a.hkv = (int)hkv;
+  a.cap = (int)cap;
+  a.ns = (int)(cap / split);
+  a.scale = scale;
+  switch (hq / hkv) {
+    case 1: return launch_attn_g<1>(a, (int)split, stream);
+    case 2: return launch_attn_g<2>(a, (int)split, stream);
+    case 4: return launch_attn_g<4>(a, (int)split, stream);
+    case 8: return launch_attn_g<8>(a, (int)split, stream);
+    default: return fail(TFA_ERR_SHAPE, "tfa_decode_attention: group %lld not in {1,2,4,8}", (long long)(hq / hkv));
+  }
+}
+
+int tfa_attn_combine(const float* op, const float* mp, const float* lp, void* out, int64_t splits,
+                     int64_t hq, int64_t head_dim, const int* wr, int64_t split, hipStream_t stream) {
+  if (!op || !mp || !lp || !out) return fail(TFA_ERR_NULL, "tfa_attn_combine: null pointer argument");
+  if (splits <= 0 || hq <= 0 || head_dim <= 0) return fail(TFA_ERR_SHAPE, "tfa_attn_combine: empty shape");
+  if (wr && split <= 0) return fail(TFA_ERR_SHAPE, "tfa_attn_combine: split must be positive with wr");
+  if (head_dim > kCombMaxD) return fail(TFA_ERR_SHAPE, "tfa_attn_combine: head_dim %lld exceeds %d", (long long)head_dim, kCombMaxD);
+  if (splits > kCombMaxSplits) return fail(TFA_ERR_SHAPE, "tfa_attn_combine: %lld splits exceed %d", (long long)splits, kCombMaxSplits);
+  attn_combine_kernel<<<(int)hq, kCombThreads, 0, stream>>>(op, mp, lp, static_cast<uint16_t*>(out),
+                                                   (int)splits, (int)hq, (int)head_dim, wr,
+                                                   (int)split);
+  return launched("attn_combine");
+}
+
+}  // extern "C"

@@ -76,6 +76,53 @@ TFA_DEV float wave_max(float v) {
   return v;
 }
 
+// Multi-row wave reduction: v[0..R) are one lane's partial sums of R rows.
+// Instead of R full butterflies (6R shuffles) the rows are halved at each step
+// -- a lane keeps the half of the rows its mask bit selects and adds the
+// partner's partials for that half -- so R = 8 costs 4+2+1+3 = 10 shuffles and
+// R = 16 costs 17. On return every lane holds the wave total of one row,
+// `row = wave_rows_owner<R>(lane)`; each row's total is replicated on 64/R lanes.
+template <int R>
+TFA_DEV int wave_rows_owner(int lane) {
+  int row = 0;
+  int n = R;
+#pragma unroll
+  for (int m = 32; m >= 1 && n > 1; m >>= 1, n >>= 1)
+    if (lane & m) row += n / 2;
+  return row;
+}
+
+template <int N, int M>
+struct RowHalver {
+  TFA_DEV static void run(float* v, int lane) {
+    const bool upper = (lane & M) != 0;
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) {
+      const float keep = upper ? v[j + N / 2] : v[j];
+      const float send = upper ? v[j] : v[j + N / 2];
+      v[j] = keep + __shfl_xor(send, M, kWave);
+    }
+    RowHalver<N / 2, M / 2>::run(v, lane);
+  }
+};
+template <int M>
+struct RowHalver<1, M> {
+  TFA_DEV static void run(float* v, int lane) {
+#pragma unroll
+    for (int m = M; m >= 1; m >>= 1) v[0] += __shfl_xor(v[0], m, kWave);
+  }
+};
+template <>
+struct RowHalver<1, 0> {
+  TFA_DEV static void run(float*, int) {}
+};
+
+template <int R>
+TFA_DEV float wave_sum_rows(float* v, int lane) {
+  RowHalver<R, 32>::run(v, lane);
+  return v[0];
+}
+
 // Sum over groups of `width` consecutive lanes (width a power of two <= 64).
 template <int WIDTH>
 TFA_DEV float group_sum(float v) {
@@ -112,21 +159,48 @@ TFA_DEV float silu(float x) { return x / (1.0f + __expf(-x)); }
 // counter resets itself, so the same buffer serves every launch (and every
 // replay of a captured graph) without a memset.
 //
+// Coherence without whole-cache maintenance: on gfx950 each XCD has its own
+// L2, and an agent-scope fence (`__threadfence`) writes back and invalidates
+// that entire L2 -- once per block, serialised, it costs milliseconds over a
+// 10k-block grid. So slices are published with agent-scope atomic stores
+// (`global_store ... sc1`, written through to the coherent level) and read
+// back with agent-scope atomic loads (`global_load ... sc1`). Each thread waits
+// for its own publishing stores to complete (`s_waitcnt`) before the block
+// barrier, and only then does one thread bump the counter: every slice a block
+// published is visible at agent scope before its arrival is counted. Data that
+// is only consumed by a later kernel uses ordinary stores (the kernel boundary
+// orders it).
+TFA_DEV void publish(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+TFA_DEV void publish(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+TFA_DEV float fetch(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+TFA_DEV int fetch(const int* p) {
+  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Returns true in exactly one block of the group. Every thread of the block
-// must call it (it synchronises the block).
+// must call it (it synchronises the block). Slices must have been written with
+// publish() and must be read with fetch().
 TFA_DEV bool arrive_last(unsigned int* counter, unsigned int group_size, int* flag_smem) {
-  __threadfence();  // publish this block's slice at device scope
+  __builtin_amdgcn_s_waitcnt(0);    // this thread's published stores are complete
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
   if (threadIdx.x == 0) {
-    unsigned int prev = atomicAdd(counter, 1u);
-    int last = (prev == group_size - 1);
-    if (last) atomicExch(counter, 0u);  // no other block of this launch touches it again
+    const unsigned int prev =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = (prev == group_size - 1);
+    // No other block of this launch touches the counter after the last arrival.
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *flag_smem = last;
   }
   __syncthreads();
-  const bool last = *flag_smem != 0;
-  if (last) __threadfence();  // acquire: see every other block's slice
-  return last;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  return *flag_smem != 0;
 }
 
 }  // namespace tfa

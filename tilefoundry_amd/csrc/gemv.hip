@@ -1,0 +1,461 @@
+// Decode GEMVs for weights stored [N, K] (out, in), plus the greedy pick.
+//
+// gemv_rows: y[n] = sum_k x[k] W[n, k]. A 256-thread block owns R consecutive
+// rows; its four waves split K into contiguous quarters, so each wave reads a
+// contiguous 1 KB run of a row per load instruction (16 bytes a lane) and the
+// block reads R whole rows back to back. The input vector (and the norm scale)
+// is issued first -- it is L2-resident and its round trip should not queue
+// behind the weights -- then every weight load of the block, then the prologue
+// math runs while the weights are in flight. The R partial dots of a wave are
+// reduced by one transposed butterfly and the four waves meet in LDS in wave
+// order, so the result does not depend on scheduling. No block depends on
+// another: there is no in-kernel handshake (on gfx950 each one costs a few
+// coherent memory round trips, more than a kernel boundary).
+//
+// Prologues:  plain x | rmsnorm(h) | rmsnorm(embed[ids[0]])
+// Epilogues:  f32 | bf16 | residual add | scaled residual add | SwiGLU pair |
+//             q|k rows to a bf16 buffer and v rows into the KV cache slot |
+//             logits + the block's best (value, lowest index)
+// The greedy pick over the block winners is a one-block kernel of its own.
+//
+// Reference kernels replaced: examples/qwen3_1_7b-tilelang/fast/kernels.py
+// (rms_norm :58-79, gemv :123-145, gemv_silu :210-257, lm_head :260-321, embed
+// :579-588, sample_step :591-637) and the MiniCPM3 GEMVs
+// examples/minicpm3_4b-cutedsl/kernels/cute_gemv.py:246-495.
+#include <float.h>
+
+#include "abi_util.h"
+#include "common.h"
+
+using namespace tfa;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kLmHeadRows = 16;  // rows per block of the head (one argmax candidate each)
+
+enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_EMBED_NORM = 2 };
+enum {
+  EPI_F32 = 0, EPI_BF16 = 1, EPI_RESID = 2, EPI_RESID_SCALED = 3, EPI_SWIGLU = 4,
+  EPI_ARGMAX = 5, EPI_QKV = 6
+};
+
+struct GemvArgs {
+  // input vector
+  const uint16_t* x;      // [K] bf16: the vector (plain) or the row to normalise
+  const uint16_t* gamma;  // [K] norm scale
+  const uint16_t* table;  // [V, K] embedding table (embed prologue)
+  const int64_t* ids;     // [1] token id (embed prologue)
+  uint16_t* h_copy;       // [K] gathered row, written by block 0 (embed prologue)
+  int64_t vocab;          // rows of `table`
+  float eps;
+  // matrix
+  const uint16_t* w;      // [N, K]
+  int N, K;
+  // outputs
+  float* yf;              // f32 out / logits
+  uint16_t* yb;           // bf16 out (also the q|k rows of the qkv routing)
+  const uint16_t* res;    // [N] residual
+  const uint16_t* alpha;  // [1] bf16 residual scale
+  float* bv;              // [gridDim.x] block maxima (argmax)
+  int* bi;                // [gridDim.x] their indices
+  // qkv routing: rows >= n_qk are value rows, written to vc[wr[0], :]
+  int n_qk;
+  const int* wr;
+  int cap;
+  uint16_t* vc;
+  int* err;
+};
+
+TFA_DEV void set_err(int* err, int code) {
+  if (err) atomicExch(err, code);
+}
+
+// (value, index) order for greedy argmax: larger value wins, equal values go to
+// the lower index (torch.argmax), NaN never wins.
+TFA_DEV bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+template <int NCH, int R, int PRO, int EPI>
+__global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
+  __shared__ float red[kWaves][R];
+  __shared__ float ssq[kWaves];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  const int t = threadIdx.x;
+  const int row0 = blockIdx.x * R;
+  const int K = a.K;
+  const int kq = K / kWaves;   // elements in this wave's quarter
+  const int nch = kq >> 3;     // 16-byte chunks in the quarter
+  const int kbase = wid * kq;
+
+  // 1. the input vector's quarter and its norm scale
+  const uint16_t* src = a.x;
+  if (PRO == PRO_EMBED_NORM) {
+    int64_t id = a.ids[0];
+    if (id < 0 || id >= a.vocab) {
+      if (blockIdx.x == 0 && t == 0) set_err(a.err, 1);
+      id = 0;
+    }
+    src = a.table + id * K;
+  }
+  uint4 xv[NCH], gv[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = lane + j * kWave;
+    xv[j] = c < nch ? ld16(src + kbase + 8 * c) : make_uint4(0, 0, 0, 0);
+    if (PRO != PRO_PLAIN) gv[j] = c < nch ? ld16(a.gamma + kbase + 8 * c) : make_uint4(0, 0, 0, 0);
+  }
+
+  // 2. weights: streamed once, non-temporal
+  uint4 w[R][NCH];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = row0 + r;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + j * kWave;
+      if (row < a.N && c < nch)
+        w[r][j] = ld16_stream(a.w + static_cast<size_t>(row) * K + kbase + 8 * c);
+      else
+        w[r][j] = make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // 3. prologue math while the weights are in flight
+  if (PRO == PRO_EMBED_NORM && blockIdx.x == 0) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + j * kWave;
+      if (c < nch) st16(a.h_copy + kbase + 8 * c, xv[j]);
+    }
+  }
+  float xf[NCH][8];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) unpack8(xv[j], xf[j]);
+  if (PRO != PRO_PLAIN) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += xf[j][i] * xf[j][i];
+    ss = wave_sum(ss);
+    if (lane == 0) ssq[wid] = ss;
+    __syncthreads();
+    const float tot = (ssq[0] + ssq[1]) + (ssq[2] + ssq[3]);
+    const float rs = rsqrt_rn(tot / static_cast<float>(K) + a.eps);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      float g[8];
+      unpack8(gv[j], g);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xf[j][i] = round_bf(round_bf(xf[j][i] * rs) * g[i]);
+    }
+  }
+
+  // 4. dots, then one transposed reduction for all R rows of the wave
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      float f[8];
+      unpack8(w[r][j], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s = fmaf(xf[j][i], f[i], s);
+    }
+    acc[r] = s;
+  }
+  {
+    const float tot = wave_sum_rows<R>(acc, lane);
+    if ((lane & (kWave / R - 1)) == 0) red[wid][wave_rows_owner<R>(lane)] = tot;
+  }
+  __syncthreads();
+  auto total = [&](int r) { return (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]); };
+
+  // 5. epilogues
+  if (EPI == EPI_F32 || EPI == EPI_BF16 || EPI == EPI_RESID || EPI == EPI_RESID_SCALED) {
+    if (t < R && row0 + t < a.N) {
+      const int row = row0 + t;
+      const float v = total(t);
+      if (EPI == EPI_F32) a.yf[row] = v;
+      if (EPI == EPI_BF16) a.yb[row] = static_cast<uint16_t>(f2bf(v));
+      if (EPI == EPI_RESID) a.yb[row] = static_cast<uint16_t>(f2bf(bf2f(a.res[row]) + round_bf(v)));
+      if (EPI == EPI_RESID_SCALED) {
+        const float al = bf2f(a.alpha[0]);
+        a.yb[row] = static_cast<uint16_t>(f2bf(bf2f(a.res[row]) + round_bf(round_bf(v) * al)));
+      }
+    }
+  }
+  if (EPI == EPI_SWIGLU) {
+    // rows (2i, 2i+1) are (gate_i, up_i):  act_i = bf16(bf16(silu(bf16 g)) * bf16 u)
+    if (t < R / 2 && row0 + 2 * t + 1 < a.N) {
+      const float g = round_bf(total(2 * t));
+      const float u = round_bf(total(2 * t + 1));
+      const float act = round_bf(round_bf(g / (1.0f + expf(-g))) * u);
+      a.yb[row0 / 2 + t] = static_cast<uint16_t>(f2bf(act));
+    }
+  }
+  if (EPI == EPI_QKV) {
+    if (t < R && row0 + t < a.N) {
+      const int row = row0 + t;
+      const uint16_t v = static_cast<uint16_t>(f2bf(total(t)));
+      if (row < a.n_qk) {
+        a.yb[row] = v;
+      } else {
+        const int slot = a.wr[0];
+        const int nv = a.N - a.n_qk;  // value row width (hkv * head_dim)
+        if (slot < 0 || slot >= a.cap) set_err(a.err, 3);
+        else a.vc[static_cast<size_t>(slot) * nv + (row - a.n_qk)] = v;
+      }
+    }
+  }
+  if (EPI == EPI_ARGMAX) {
+    if (t < R && row0 + t < a.N) a.yf[row0 + t] = total(t);
+    if (t == 0) {
+      float bvv = -FLT_MAX;
+      int bii = row0;
+      bool any = false;
+      for (int r = 0; r < R && row0 + r < a.N; ++r) {
+        const float v = total(r);
+        if (!any || better(v, row0 + r, bvv, bii)) { bvv = v; bii = row0 + r; any = true; }
+      }
+      a.bv[blockIdx.x] = bvv;
+      a.bi[blockIdx.x] = bii;
+    }
+  }
+}
+
+template <int NCH, int R, int PRO, int EPI>
+int launch_gemv(const GemvArgs& a, hipStream_t s, const char* name) {
+  const int blocks = (a.N + R - 1) / R;
+  gemv_rows_kernel<NCH, R, PRO, EPI><<<blocks, kThreads, 0, s>>>(a);
+  return launched(name);
+}
+
+// Chunks per lane for one wave's quarter of K.
+int chunks_for(int K) { return (K / kWaves / 8 + kWave - 1) / kWave; }
+
+template <int R, int PRO, int EPI>
+int dispatch_k(const GemvArgs& a, hipStream_t s, const char* name) {
+  switch (chunks_for(a.K)) {
+    case 1: return launch_gemv<1, R, PRO, EPI>(a, s, name);
+    case 2: return launch_gemv<2, R, PRO, EPI>(a, s, name);
+    case 3: return launch_gemv<3, R, PRO, EPI>(a, s, name);
+    case 4: return launch_gemv<4, R, PRO, EPI>(a, s, name);
+    default: return fail(TFA_ERR_SHAPE, "%s: K=%d exceeds 8192", name, a.K);
+  }
+}
+
+// Rows per block: enough blocks to cover 256 CUs a few times over, enough rows
+// per block that each lane keeps >= 4 loads in flight.
+template <int PRO, int EPI>
+int dispatch_rows(const GemvArgs& a, hipStream_t s, const char* name) {
+  if (a.N >= 4096 && a.K <= 4096) return dispatch_k<8, PRO, EPI>(a, s, name);
+  return dispatch_k<4, PRO, EPI>(a, s, name);
+}
+
+int check_gemv(const GemvArgs& a, const char* name) {
+  if (a.K <= 0 || a.K % 32 != 0 || a.K > 8192)
+    return fail(TFA_ERR_SHAPE, "%s: K=%d must be a positive multiple of 32, at most 8192", name, a.K);
+  if (a.N <= 0) return fail(TFA_ERR_SHAPE, "%s: N=%d must be positive", name, a.N);
+  if (!a.w) return fail(TFA_ERR_NULL, "%s: null weight", name);
+  if (!aligned16(a.w)) return fail(TFA_ERR_ALIGN, "%s: weight not 16-byte aligned", name);
+  return TFA_OK;
+}
+
+int check_vec(const void* p, const char* what, const char* name) {
+  if (!p) return fail(TFA_ERR_NULL, "%s: null %s", name, what);
+  if (!aligned16(p)) return fail(TFA_ERR_ALIGN, "%s: %s not 16-byte aligned", name, what);
+  return TFA_OK;
+}
+
+#define TFA_TRY(expr) do { int _st = (expr); if (_st != TFA_OK) return _st; } while (0)
+
+// Final greedy pick over the head's block winners, then the sample step:
+// record the pick at pos, feed the next prompt id while the prompt lasts (else
+// the pick), advance pos. One block; ties go to the lowest index.
+__global__ __launch_bounds__(kThreads) void sample_kernel(
+    const float* __restrict__ bv, const int* __restrict__ bi, int nb, const int* inp,
+    const int* plen, int64_t* ids, int* pos, int* sam, int nsteps, int* err) {
+  __shared__ float rv[kThreads];
+  __shared__ int ri[kThreads];
+  const int t = threadIdx.x;
+  float bvv = -FLT_MAX;
+  int bii = 0x7fffffff;
+  for (int b = t; b < nb; b += kThreads)
+    if (better(bv[b], bi[b], bvv, bii)) { bvv = bv[b]; bii = bi[b]; }
+  rv[t] = bvv;
+  ri[t] = bii;
+  __syncthreads();
+  for (int s = kThreads / 2; s > 0; s >>= 1) {
+    if (t < s && better(rv[t + s], ri[t + s], rv[t], ri[t])) {
+      rv[t] = rv[t + s];
+      ri[t] = ri[t + s];
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    const int best = ri[0];
+    const int p = pos[0];
+    if (p < 0 || p >= nsteps) {
+      set_err(err, 2);
+    } else {
+      sam[p] = best;
+      const bool prompt = (p + 1 < plen[0]) && (p + 1 < nsteps);
+      ids[0] = prompt ? static_cast<int64_t>(inp[p + 1]) : static_cast<int64_t>(best);
+      pos[0] = p + 1;
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t tfa_lm_head_blocks(int64_t vocab) { return (vocab + kLmHeadRows - 1) / kLmHeadRows; }
+
+int tfa_gemv(const void* x, const void* w, void* y, int64_t n, int64_t k, int out_f32,
+             hipStream_t stream) {
+  GemvArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = static_cast<const uint16_t*>(w);
+  a.N = (int)n;
+  a.K = (int)k;
+  TFA_TRY(check_gemv(a, "tfa_gemv"));
+  TFA_TRY(check_vec(x, "x", "tfa_gemv"));
+  if (!y) return fail(TFA_ERR_NULL, "tfa_gemv: null y");
+  if (out_f32) {
+    a.yf = static_cast<float*>(y);
+    return dispatch_rows<PRO_PLAIN, EPI_F32>(a, stream, "gemv");
+  }
+  a.yb = static_cast<uint16_t*>(y);
+  return dispatch_rows<PRO_PLAIN, EPI_BF16>(a, stream, "gemv");
+}
+
+int tfa_rmsnorm_gemv(const void* h, const void* gamma, float eps, const void* w, void* y,
+                     int64_t n, int64_t k, hipStream_t stream) {
+  GemvArgs a{};
+  a.x = static_cast<const uint16_t*>(h);
+  a.gamma = static_cast<const uint16_t*>(gamma);
+  a.eps = eps;
+  a.w = static_cast<const uint16_t*>(w);
+  a.N = (int)n;
+  a.K = (int)k;
+  a.yb = static_cast<uint16_t*>(y);
+  TFA_TRY(check_gemv(a, "tfa_rmsnorm_gemv"));
+  TFA_TRY(check_vec(h, "h", "tfa_rmsnorm_gemv"));
+  TFA_TRY(check_vec(gamma, "gamma", "tfa_rmsnorm_gemv"));
+  if (!y) return fail(TFA_ERR_NULL, "tfa_rmsnorm_gemv: null y");
+  return dispatch_rows<PRO_NORM, EPI_BF16>(a, stream, "rmsnorm_gemv");
+}
+
+int tfa_gemv_residual(const void* x, const void* w, const void* residual, const void* alpha,
+                      void* y, int64_t n, int64_t k, hipStream_t stream) {
+  GemvArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = static_cast<const uint16_t*>(w);
+  a.res = static_cast<const uint16_t*>(residual);
+  a.alpha = static_cast<const uint16_t*>(alpha);
+  a.yb = static_cast<uint16_t*>(y);
+  a.N = (int)n;
+  a.K = (int)k;
+  TFA_TRY(check_gemv(a, "tfa_gemv_residual"));
+  TFA_TRY(check_vec(x, "x", "tfa_gemv_residual"));
+  if (!residual || !y) return fail(TFA_ERR_NULL, "tfa_gemv_residual: null residual / y");
+  if (alpha) return dispatch_rows<PRO_PLAIN, EPI_RESID_SCALED>(a, stream, "gemv_residual");
+  return dispatch_rows<PRO_PLAIN, EPI_RESID>(a, stream, "gemv_residual");
+}
+
+int tfa_rmsnorm_gemv_swiglu(const void* h, const void* gamma, float eps, const void* w_gu,
+                            void* act, int64_t inter, int64_t k, hipStream_t stream) {
+  GemvArgs a{};
+  a.x = static_cast<const uint16_t*>(h);
+  a.gamma = static_cast<const uint16_t*>(gamma);
+  a.eps = eps;
+  a.w = static_cast<const uint16_t*>(w_gu);
+  a.N = (int)(2 * inter);
+  a.K = (int)k;
+  a.yb = static_cast<uint16_t*>(act);
+  TFA_TRY(check_gemv(a, "tfa_rmsnorm_gemv_swiglu"));
+  TFA_TRY(check_vec(h, "h", "tfa_rmsnorm_gemv_swiglu"));
+  TFA_TRY(check_vec(gamma, "gamma", "tfa_rmsnorm_gemv_swiglu"));
+  if (!act) return fail(TFA_ERR_NULL, "tfa_rmsnorm_gemv_swiglu: null act");
+  return dispatch_rows<PRO_NORM, EPI_SWIGLU>(a, stream, "rmsnorm_gemv_swiglu");
+}
+
+int tfa_lm_head_argmax(const void* h, const void* gamma, float eps, const void* w, int64_t vocab,
+                       int64_t k, float* logits, float* block_val, int* block_idx,
+                       hipStream_t stream) {
+  GemvArgs a{};
+  a.x = static_cast<const uint16_t*>(h);
+  a.gamma = static_cast<const uint16_t*>(gamma);
+  a.eps = eps;
+  a.w = static_cast<const uint16_t*>(w);
+  a.N = (int)vocab;
+  a.K = (int)k;
+  a.yf = logits;
+  a.bv = block_val;
+  a.bi = block_idx;
+  TFA_TRY(check_gemv(a, "tfa_lm_head_argmax"));
+  TFA_TRY(check_vec(h, "h", "tfa_lm_head_argmax"));
+  if (!logits || !block_val || !block_idx)
+    return fail(TFA_ERR_NULL, "tfa_lm_head_argmax: null logits / block buffers");
+  if (gamma) {
+    TFA_TRY(check_vec(gamma, "gamma", "tfa_lm_head_argmax"));
+    return dispatch_k<kLmHeadRows, PRO_NORM, EPI_ARGMAX>(a, stream, "lm_head_argmax");
+  }
+  return dispatch_k<kLmHeadRows, PRO_PLAIN, EPI_ARGMAX>(a, stream, "lm_head_argmax");
+}
+
+int tfa_sample_step(const float* block_val, const int* block_idx, int64_t nblocks, const int* inp,
+                    const int* prompt_len, int64_t* ids, int* pos, int* sam, int64_t nsteps,
+                    int* err, hipStream_t stream) {
+  if (!block_val || !block_idx || !inp || !prompt_len || !ids || !pos || !sam)
+    return fail(TFA_ERR_NULL, "tfa_sample_step: null pointer argument");
+  if (nblocks <= 0 || nsteps <= 0) return fail(TFA_ERR_SHAPE, "tfa_sample_step: empty block list or step table");
+  sample_kernel<<<1, kThreads, 0, stream>>>(block_val, block_idx, (int)nblocks, inp, prompt_len,
+                                            ids, pos, sam, (int)nsteps, err);
+  return launched("sample_step");
+}
+
+int tfa_decode_qkv(const void* h, const void* table, const int64_t* ids, int64_t vocab,
+                   void* h_copy, const void* gamma_in, float eps, const void* w_qkv,
+                   int64_t hidden, int64_t n_qk, int64_t n_v, void* qk_out, const int* wr,
+                   void* v_cache, int64_t cap, int* err, hipStream_t stream) {
+  GemvArgs a{};
+  a.x = static_cast<const uint16_t*>(h);
+  a.table = static_cast<const uint16_t*>(table);
+  a.ids = ids;
+  a.vocab = vocab;
+  a.h_copy = static_cast<uint16_t*>(h_copy);
+  a.gamma = static_cast<const uint16_t*>(gamma_in);
+  a.eps = eps;
+  a.w = static_cast<const uint16_t*>(w_qkv);
+  a.K = (int)hidden;
+  a.N = (int)(n_qk + n_v);
+  a.n_qk = (int)n_qk;
+  a.yb = static_cast<uint16_t*>(qk_out);
+  a.wr = wr;
+  a.cap = (int)cap;
+  a.vc = static_cast<uint16_t*>(v_cache);
+  a.err = err;
+  TFA_TRY(check_gemv(a, "tfa_decode_qkv"));
+  if (n_qk <= 0 || n_v <= 0) return fail(TFA_ERR_SHAPE, "tfa_decode_qkv: empty q|k or v rows");
+  if (!gamma_in || !qk_out || !wr || !v_cache)
+    return fail(TFA_ERR_NULL, "tfa_decode_qkv: null pointer argument");
+  TFA_TRY(check_vec(gamma_in, "gamma_in", "tfa_decode_qkv"));
+  if (cap <= 0) return fail(TFA_ERR_SHAPE, "tfa_decode_qkv: empty cache");
+  if (table) {
+    if (!ids || !h_copy) return fail(TFA_ERR_NULL, "tfa_decode_qkv: embed mode needs ids and h_copy");
+    TFA_TRY(check_vec(table, "table", "tfa_decode_qkv"));
+    TFA_TRY(check_vec(h_copy, "h_copy", "tfa_decode_qkv"));
+    return dispatch_rows<PRO_EMBED_NORM, EPI_QKV>(a, stream, "decode_qkv");
+  }
+  TFA_TRY(check_vec(h, "h", "tfa_decode_qkv"));
+  return dispatch_rows<PRO_NORM, EPI_QKV>(a, stream, "decode_qkv");
+}
+
+}  // extern "C"

@@ -159,10 +159,8 @@ void rmsnorm_gemv_swiglu(const Tensor& h, const Tensor& gamma, double eps, const
                                        act.data_ptr(), I, K, stream_of(h)));
 }
 
-void lm_head_sample(const Tensor& h, const OptT& gamma, double eps, const Tensor& w,
-                    const Tensor& logits, const Tensor& block_val, const Tensor& block_idx,
-                    const Tensor& counter, const OptT& inp, const OptT& prompt_len,
-                    const OptT& ids, const OptT& pos, const OptT& sam, const OptT& err) {
+void lm_head_argmax(const Tensor& h, const OptT& gamma, double eps, const Tensor& w,
+                    const Tensor& logits, const Tensor& block_val, const Tensor& block_idx) {
   need(h, "h", BF);
   const int64_t K = h.numel();
   if (gamma) need(*gamma, "gamma", BF, K);
@@ -173,32 +171,31 @@ void lm_head_sample(const Tensor& h, const OptT& gamma, double eps, const Tensor
   const int64_t nb = tfa_lm_head_blocks(V);
   need(block_val, "block_val", F32, nb);
   need(block_idx, "block_idx", I32, nb);
-  need(counter, "counter", I32, 1);
-  int64_t nsteps = 0;
-  if (pos) {
-    need(*pos, "pos", I32, 1);
-    if (!inp || !prompt_len || !ids || !sam) bad("sampling needs inp, prompt_len, ids and sam");
-    need(*inp, "inp", I32);
-    nsteps = inp->numel();
-    need(*sam, "sam", I32, nsteps);
-    need(*prompt_len, "prompt_len", I32, 1);
-    need(*ids, "ids", I64, 1);
-  }
+  raise_status(tfa_lm_head_argmax(h.data_ptr(), opt_ptr(gamma), (float)eps, w.data_ptr(), V, K,
+                                  logits.data_ptr<float>(), block_val.data_ptr<float>(),
+                                  block_idx.data_ptr<int>(), stream_of(h)));
+}
+
+void sample_step(const Tensor& block_val, const Tensor& block_idx, const Tensor& inp,
+                 const Tensor& prompt_len, const Tensor& ids, const Tensor& pos, const Tensor& sam,
+                 const OptT& err) {
+  need(block_val, "block_val", F32);
+  need(block_idx, "block_idx", I32, block_val.numel());
+  need(inp, "inp", I32);
+  need(sam, "sam", I32, inp.numel());
+  need(prompt_len, "prompt_len", I32, 1);
+  need(ids, "ids", I64, 1);
+  need(pos, "pos", I32, 1);
   if (err) need(*err, "err", I32, 1);
-  raise_status(tfa_lm_head_sample(
-      h.data_ptr(), opt_ptr(gamma), (float)eps, w.data_ptr(), V, K, logits.data_ptr<float>(),
-      block_val.data_ptr<float>(), block_idx.data_ptr<int>(),
-      static_cast<unsigned int*>(counter.data_ptr()), opt_ptr_t<const int>(inp),
-      opt_ptr_t<const int>(prompt_len), opt_ptr_t<int64_t>(ids), opt_ptr_t<int>(pos),
-      opt_ptr_t<int>(sam), nsteps, opt_ptr_t<int>(err), stream_of(h)));
+  raise_status(tfa_sample_step(block_val.data_ptr<float>(), block_idx.data_ptr<int>(),
+                               block_val.numel(), inp.data_ptr<int>(), prompt_len.data_ptr<int>(),
+                               ids.data_ptr<int64_t>(), pos.data_ptr<int>(), sam.data_ptr<int>(),
+                               inp.numel(), opt_ptr_t<int>(err), stream_of(block_val)));
 }
 
 void decode_qkv(const OptT& h, const OptT& table, const OptT& ids, const OptT& h_copy,
-                const Tensor& gamma_in, double eps, const Tensor& w_qkv, int64_t hq, int64_t hkv,
-                int64_t head_dim, const Tensor& gamma_q, const Tensor& gamma_k, double eps_head,
-                const Tensor& cos_t, const Tensor& sin_t, const Tensor& pos, const Tensor& wr,
-                const Tensor& k_cache, const Tensor& v_cache, const Tensor& q,
-                const Tensor& scratch, const Tensor& counters, const OptT& err) {
+                const Tensor& gamma_in, double eps, const Tensor& w_qkv, int64_t n_qk,
+                const Tensor& qk_out, const Tensor& wr, const Tensor& v_cache, const OptT& err) {
   const int64_t H = gamma_in.numel();
   need(gamma_in, "gamma_in", BF, H);
   int64_t vocab = 0;
@@ -213,61 +210,62 @@ void decode_qkv(const OptT& h, const OptT& table, const OptT& ids, const OptT& h
     if (!h) bad("h required when no table is given");
     need(*h, "h", BF, H);
   }
-  const int64_t D = head_dim;
-  need_mat(w_qkv, "w_qkv", (hq + 2 * hkv) * D, H);
-  need(gamma_q, "gamma_q", BF, D);
-  need(gamma_k, "gamma_k", BF, D);
-  need(cos_t, "cos", BF);
-  need(sin_t, "sin", BF, cos_t.numel());
-  if (cos_t.dim() != 2 || cos_t.size(1) != D) bad("cos: expected (rows, head_dim)");
-  need(pos, "pos", I32, 1);
+  if (w_qkv.dim() != 2) bad("w_qkv: expected (n_qk + n_v, hidden)");
+  const int64_t n_v = w_qkv.size(0) - n_qk;
+  if (n_v <= 0) bad("w_qkv has no value rows");
+  need_mat(w_qkv, "w_qkv", n_qk + n_v, H);
+  need(qk_out, "qk_out", BF, n_qk);
   need(wr, "wr", I32, 1);
-  need(k_cache, "k_cache", BF);
-  need(v_cache, "v_cache", BF, k_cache.numel());
-  if (k_cache.numel() % (hkv * D) != 0) bad("k_cache: size is not a multiple of hkv*head_dim");
-  const int64_t cap = k_cache.numel() / (hkv * D);
-  need(q, "q", BF, hq * D);
-  need(scratch, "scratch", F32, (hq + hkv) * D);
-  need(counters, "counters", I32, hq + hkv);
+  need(v_cache, "v_cache", BF);
+  if (v_cache.numel() % n_v != 0) bad("v_cache: size is not a multiple of the value row");
   if (err) need(*err, "err", I32, 1);
-  raise_status(tfa_decode_qkv(
-      opt_ptr(h), opt_ptr(table), opt_ptr_t<const int64_t>(ids), vocab, opt_ptr_t<void>(h_copy),
-      gamma_in.data_ptr(), (float)eps, w_qkv.data_ptr(), H, hq, hkv, D, gamma_q.data_ptr(),
-      gamma_k.data_ptr(), (float)eps_head, cos_t.data_ptr(), sin_t.data_ptr(), cos_t.size(0),
-      pos.data_ptr<int>(), wr.data_ptr<int>(), k_cache.data_ptr(), v_cache.data_ptr(), cap,
-      q.data_ptr(), scratch.data_ptr<float>(), static_cast<unsigned int*>(counters.data_ptr()),
-      opt_ptr_t<int>(err), stream_of(gamma_in)));
+  raise_status(tfa_decode_qkv(opt_ptr(h), opt_ptr(table), opt_ptr_t<const int64_t>(ids), vocab,
+                              opt_ptr_t<void>(h_copy), gamma_in.data_ptr(), (float)eps,
+                              w_qkv.data_ptr(), H, n_qk, n_v, qk_out.data_ptr(), wr.data_ptr<int>(),
+                              v_cache.data_ptr(), v_cache.numel() / n_v, opt_ptr_t<int>(err),
+                              stream_of(gamma_in)));
 }
 
-void decode_attention(const Tensor& q, const Tensor& k_cache, const Tensor& v_cache,
-                      const Tensor& pos, int64_t hq, int64_t hkv, int64_t split, double scale,
-                      const Tensor& op, const Tensor& mp, const Tensor& lp, const OptT& counters,
-                      const OptT& out, const OptT& err) {
+void decode_attention(const Tensor& q, const OptT& gamma_q, const OptT& gamma_k, double eps_head,
+                      const OptT& cos_t, const OptT& sin_t, const Tensor& k_cache,
+                      const Tensor& v_cache, const OptT& pos, const Tensor& wr, int64_t hq,
+                      int64_t hkv, int64_t split, double scale, const Tensor& op, const Tensor& mp,
+                      const Tensor& lp, bool neutral, const OptT& err) {
   const int64_t D = 128;
-  need(q, "q", BF, hq * D);
+  const bool fused = gamma_q.has_value();
+  need(q, "q", BF, (fused ? hq + hkv : hq) * D);
+  int64_t rope_rows = 0;
+  if (fused) {
+    if (!gamma_k || !cos_t || !sin_t || !pos) bad("fused mode needs gamma_k, cos, sin and pos");
+    need(*gamma_q, "gamma_q", BF, D);
+    need(*gamma_k, "gamma_k", BF, D);
+    need(*cos_t, "cos", BF);
+    need(*sin_t, "sin", BF, cos_t->numel());
+    if (cos_t->dim() != 2 || cos_t->size(1) != D) bad("cos: expected (rows, 128)");
+    rope_rows = cos_t->size(0);
+    need(*pos, "pos", I32, 1);
+  }
   need(k_cache, "k_cache", BF);
   need(v_cache, "v_cache", BF, k_cache.numel());
   if (k_cache.numel() % (hkv * D) != 0) bad("k_cache: size is not a multiple of hkv*128");
   const int64_t cap = k_cache.numel() / (hkv * D);
   if (split <= 0 || cap % split != 0) bad("cache capacity must be a multiple of the split");
   const int64_t ns = cap / split;
-  need(pos, "pos", I32, 1);
+  need(wr, "wr", I32, 1);
   need(op, "op", F32, ns * hq * D);
   need(mp, "mp", F32, ns * hq);
   need(lp, "lp", F32, ns * hq);
-  if (counters) {
-    need(*counters, "counters", I32, hkv);
-    if (!out) bad("merging needs out");
-    need(*out, "out", BF, hq * D);
-  }
   if (err) need(*err, "err", I32, 1);
   raise_status(tfa_decode_attention(
-      q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), pos.data_ptr<int>(), hq, hkv, D, cap,
-      split, (float)scale, op.data_ptr<float>(), mp.data_ptr<float>(), lp.data_ptr<float>(),
-      opt_ptr_t<unsigned int>(counters), opt_ptr_t<void>(out), opt_ptr_t<int>(err), stream_of(q)));
+      q.data_ptr(), opt_ptr(gamma_q), opt_ptr(gamma_k), (float)eps_head, opt_ptr(cos_t),
+      opt_ptr(sin_t), rope_rows, k_cache.data_ptr(), v_cache.data_ptr(), opt_ptr_t<const int>(pos),
+      wr.data_ptr<int>(), hq, hkv, D, cap, split, (float)scale, op.data_ptr<float>(),
+      mp.data_ptr<float>(), lp.data_ptr<float>(), neutral ? 1 : 0, opt_ptr_t<int>(err),
+      stream_of(q)));
 }
 
-void attn_combine(const Tensor& op, const Tensor& mp, const Tensor& lp, const Tensor& out) {
+void attn_combine(const Tensor& op, const Tensor& mp, const Tensor& lp, const Tensor& out,
+                  const OptT& wr, int64_t split) {
   need(mp, "Mp", F32);
   if (mp.dim() != 2) bad("Mp: expected (NS, HQ)");
   const int64_t ns = mp.size(0), hq = mp.size(1);
@@ -276,8 +274,10 @@ void attn_combine(const Tensor& op, const Tensor& mp, const Tensor& lp, const Te
   if (op.numel() % (ns * hq) != 0) bad("Op: expected (NS, HQ, D)");
   const int64_t D = op.numel() / (ns * hq);
   need(out, "O", BF, hq * D);
+  if (wr) need(*wr, "wr", I32, 1);
   raise_status(tfa_attn_combine(op.data_ptr<float>(), mp.data_ptr<float>(), lp.data_ptr<float>(),
-                                out.data_ptr(), ns, hq, D, stream_of(op)));
+                                out.data_ptr(), ns, hq, D, opt_ptr_t<const int>(wr), split,
+                                stream_of(op)));
 }
 
 }  // namespace
@@ -293,7 +293,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gemv_residual", &gemv_residual);
   m.def("rmsnorm_gemv_swiglu", &rmsnorm_gemv_swiglu);
   m.def("lm_head_blocks", [](int64_t vocab) { return tfa_lm_head_blocks(vocab); });
-  m.def("lm_head_sample", &lm_head_sample);
+  m.def("lm_head_argmax", &lm_head_argmax);
+  m.def("sample_step", &sample_step);
   m.def("decode_qkv", &decode_qkv);
   m.def("decode_attention", &decode_attention);
   m.def("attn_combine", &attn_combine);

@@ -104,47 +104,44 @@ class SampleState:
         self.err = z(1)
 
 
-def lm_head_argmax(h, gamma, eps: float, w, logits=None, block_val=None, block_idx=None,
-                   counter=None, sample: SampleState | None = None):
+def lm_head_argmax(h, gamma, eps: float, w, logits=None, block_val=None, block_idx=None):
     """f32 logits of ``rms_norm(h) @ w.T`` (``h`` as is when ``gamma`` is None) and
-    their argmax (lowest index on ties). With ``sample``, also the greedy sample
-    step. Returns ``(logits, best)``; ``best`` is read back (one sync)."""
-    dev = h.device
+    the per-block winners. Returns ``(logits, block_val, block_idx)``
+    (examples/qwen3_1_7b-tilelang/fast/kernels.py:260-321)."""
     V = w.shape[0]
     nb = C.lm_head_blocks(V)
     logits = _out(logits, h, (V,), torch.float32)
     block_val = _out(block_val, h, (nb,), torch.float32)
     block_idx = _out(block_idx, h, (nb,), torch.int32)
-    counter = counter if counter is not None else torch.zeros(1, dtype=torch.int32, device=dev)
-    s = sample
-    C.lm_head_sample(h, gamma, float(eps), w, logits, block_val, block_idx, counter,
-                     s.inp if s else None, s.plen if s else None, s.ids if s else None,
-                     s.pos if s else None, s.sam if s else None, s.err if s else None)
-    best = int(block_idx[int(torch.argmax(block_val))]) if sample is None else None
-    if sample is not None:
-        p = int(sample.pos[0]) - 1
-        best = int(sample.sam[p])
-    return logits, best
+    C.lm_head_argmax(h, gamma, float(eps), w, logits, block_val, block_idx)
+    return logits, block_val, block_idx
 
 
-def decode_qkv(h, gamma_in, eps: float, w_qkv, hq: int, hkv: int, head_dim: int, gamma_q,
-               gamma_k, cos, sin, pos, wr, k_cache, v_cache, *, eps_head: float | None = None,
-               table=None, token=None, h_copy=None, q=None, scratch=None, counters=None,
-               err=None):
-    """Input norm + fused q|k|v GEMV + q/k head norm + RoPE at ``pos`` + cache
-    write at slot ``wr``; returns q (bf16 [hq*head_dim]). With ``table`` the input
-    row is ``table[token]`` (copied into ``h_copy``)."""
+def sample_step(block_val, block_idx, state: SampleState):
+    """The greedy step on the device (examples/qwen3_1_7b-tilelang/fast/kernels.py:591-637)."""
+    C.sample_step(block_val, block_idx, state.inp, state.plen, state.ids, state.pos, state.sam,
+                  state.err)
+
+
+def greedy_pick(h, gamma, eps: float, w):
+    """Logits and their argmax (lowest index on ties), read back to the host."""
+    logits, bv, bi = lm_head_argmax(h, gamma, eps, w)
+    return logits, int(bi[int(torch.argmax(bv))])
+
+
+def decode_qkv(h, gamma_in, eps: float, w_qkv, n_qk: int, wr, v_cache, *, table=None,
+               token=None, h_copy=None, qk_out=None, err=None):
+    """Input norm + fused q|k|v GEMV: raw q|k (bf16 [n_qk]) returned, v written
+    into ``v_cache`` row ``wr``. With ``table`` the input row is ``table[token]``
+    (copied into ``h_copy``)."""
     dev = gamma_in.device
-    q = _out(q, gamma_in, (hq * head_dim,))
-    scratch = _out(scratch, gamma_in, ((hq + hkv) * head_dim,), torch.float32)
-    counters = counters if counters is not None else torch.zeros(hq + hkv, dtype=torch.int32, device=dev)
+    qk_out = _out(qk_out, gamma_in, (n_qk,))
     ids = None
     if table is not None:
         ids = token if isinstance(token, torch.Tensor) else torch.tensor([int(token)], dtype=torch.int64, device=dev)
-    C.decode_qkv(h, table, ids, h_copy, gamma_in, float(eps), w_qkv, hq, hkv, head_dim, gamma_q,
-                 gamma_k, float(eps if eps_head is None else eps_head), cos, sin,
-                 _dev_i32(pos, dev), _dev_i32(wr, dev), k_cache, v_cache, q, scratch, counters, err)
-    return q
+    C.decode_qkv(h, table, ids, h_copy, gamma_in, float(eps), w_qkv, n_qk, qk_out,
+                 _dev_i32(wr, dev), v_cache, err)
+    return qk_out
 
 
 def _attn_bufs(q, k_cache, hq, hkv, split):
@@ -156,35 +153,44 @@ def _attn_bufs(q, k_cache, hq, hkv, split):
     return op, mp, lp
 
 
-def decode_attention(q, k_cache, v_cache, pos, hq: int, hkv: int, split: int = 64,
-                     scale: float | None = None, out=None, partials=None, counters=None, err=None):
-    """GQA decode attention of q over cache positions 0..pos; bf16 [hq*128]."""
+def attn_partial(q, k_cache, v_cache, wr, hq: int, hkv: int, split: int = 256,
+                 scale: float | None = None, partials=None, rope=None, neutral: bool = True,
+                 err=None):
+    """Split partials ``(Op [NS,HQ,128], Mp [NS,HQ], Lp [NS,HQ])`` of decode
+    attention over cache slots 0..wr (examples/qwen3_1_7b-tilelang/fast/kernels.py:418-501).
+
+    ``rope=None``: ``q`` is the final query and the cache already holds slot wr.
+    ``rope=(gamma_q, gamma_k, eps, cos, sin, pos)``: ``q`` is the raw q|k
+    projection; the head norm + RoPE happen here and the new key is written to
+    ``k_cache[wr]``."""
     dev = q.device
     scale = 128 ** -0.5 if scale is None else scale
     op, mp, lp = partials if partials is not None else _attn_bufs(q, k_cache, hq, hkv, split)
-    counters = counters if counters is not None else torch.zeros(hkv, dtype=torch.int32, device=dev)
-    out = _out(out, q, (hq * 128,))
-    C.decode_attention(q, k_cache, v_cache, _dev_i32(pos, dev), hq, hkv, split, float(scale),
-                       op, mp, lp, counters, out, err)
-    return out
-
-
-def attn_partial(q, k_cache, v_cache, pos, hq: int, hkv: int, split: int = 256,
-                 scale: float | None = None, partials=None):
-    """Split partials ``(Op [NS,HQ,128], Mp [NS,HQ], Lp [NS,HQ])``; splits past the
-    context are neutral (examples/qwen3_1_7b-tilelang/fast/kernels.py:418-501)."""
-    dev = q.device
-    scale = 128 ** -0.5 if scale is None else scale
-    op, mp, lp = partials if partials is not None else _attn_bufs(q, k_cache, hq, hkv, split)
-    C.decode_attention(q, k_cache, v_cache, _dev_i32(pos, dev), hq, hkv, split, float(scale),
-                       op, mp, lp, None, None, None)
+    if rope is None:
+        C.decode_attention(q, None, None, 0.0, None, None, k_cache, v_cache, None,
+                           _dev_i32(wr, dev), hq, hkv, split, float(scale), op, mp, lp,
+                           bool(neutral), err)
+    else:
+        gq, gk, eps, cos, sin, pos = rope
+        C.decode_attention(q, gq, gk, float(eps), cos, sin, k_cache, v_cache, _dev_i32(pos, dev),
+                           _dev_i32(wr, dev), hq, hkv, split, float(scale), op, mp, lp,
+                           bool(neutral), err)
     return op, mp, lp
 
 
-def attn_combine(op, mp, lp, out=None):
+def attn_combine(op, mp, lp, out=None, wr=None, split: int = 0):
     """LSE merge of split partials into bf16 ``[HQ*D]``
-    (examples/qwen3_1_7b-tilelang/fast/kernels.py:504-540)."""
+    (examples/qwen3_1_7b-tilelang/fast/kernels.py:504-540); with ``wr`` only the
+    splits holding slots 0..wr are read."""
     ns, hq = mp.shape
     out = _out(out, op, (op.numel() // ns,), BF16)
-    C.attn_combine(op, mp, lp, out)
+    C.attn_combine(op, mp, lp, out, None if wr is None else _dev_i32(wr, op.device), int(split))
     return out
+
+
+def decode_attention(q, k_cache, v_cache, wr, hq: int, hkv: int, split: int = 64,
+                     scale: float | None = None, rope=None, out=None, partials=None, err=None):
+    """Decode attention merged to bf16 ``[hq*128]`` (partials + combine)."""
+    op, mp, lp = attn_partial(q, k_cache, v_cache, wr, hq, hkv, split, scale, partials, rope,
+                              neutral=False, err=err)
+    return attn_combine(op, mp, lp, out, wr=wr, split=split)

@@ -10,16 +10,23 @@ capture walks the prompt and continues past it with no host round trip: the
 last kernel of the step writes the pick, feeds the next prompt id or the pick
 back as the next input, and advances the position.
 
-One step is 5 kernels per layer plus one for the head (141 launches for 28
+One step is 6 kernels per layer plus two for the head (170 launches for 28
 layers; the reference's TileLang step is 228):
 
-    decode_qkv          input norm (embedding gather on layer 0) + q|k|v GEMV +
-                        q/k head norm + RoPE + KV-cache write
-    decode_attention    split-KV GQA attention, splits merged in-kernel
+    decode_qkv          input norm (embedding gather on layer 0) + q|k|v GEMV;
+                        v lands in the cache slot
+    decode_attention    q/k head norm + RoPE + K-cache write, then split-KV GQA
+                        attention partials
+    attn_combine        log-sum-exp merge of the splits
     gemv_residual       o_proj + residual add
     rmsnorm_gemv_swiglu post-attention norm + gate|up GEMV + SwiGLU
     gemv_residual       down_proj + residual add
-    lm_head_sample      final norm + head GEMV + argmax + greedy sample step
+    lm_head_argmax      final norm + head GEMV + per-block winners
+    sample_step         greedy pick, record, next input id, position + 1
+
+No kernel waits on another block of its own launch: on gfx950 a cross-block
+hand-off inside a kernel (coherent stores, an atomic, coherent loads) costs
+more round trips than a kernel boundary inside a graph.
 
 Weights are kept in the checkpoint's ``(out, in)`` layout: ``q|k|v`` stacked
 into one matrix, ``gate`` and ``up`` rows interleaved into another, the head
@@ -199,22 +206,18 @@ class Engine:
 
         self.hid = z(H)
         self.h1 = z(H)
-        self.q = z(HQ * D)
+        self.qk = z((HQ + HKV) * D)
         self.attn = z(HQ * D)
         self.act = z(cfg.inter)
-        self.scratch = z((HQ + HKV) * D, dtype=torch.float32)
-        self.qkv_cnt = z(HQ + HKV, dtype=torch.int32)
         self.op = z(self.ns, HQ, D, dtype=torch.float32)
         self.mp = z(self.ns, HQ, dtype=torch.float32)
         self.lp = z(self.ns, HQ, dtype=torch.float32)
-        self.attn_cnt = z(HKV, dtype=torch.int32)
         self.kc = z(cfg.layers, self.cap, HKV * D)
         self.vc = z(cfg.layers, self.cap, HKV * D)
         self.logits = z(cfg.vocab, dtype=torch.float32)
         nb = C.lm_head_blocks(cfg.vocab)
         self.bv = z(nb, dtype=torch.float32)
         self.bi = z(nb, dtype=torch.int32)
-        self.head_cnt = z(1, dtype=torch.int32)
         self.pos = z(1, dtype=torch.int32)
         self.ids = z(1, dtype=torch.int64)
         self.inp = z(self.nsteps, dtype=torch.int32)
@@ -226,26 +229,26 @@ class Engine:
     def _step(self):
         cfg = self.cfg
         HQ, HKV, D = cfg.heads, cfg.kv_heads, cfg.head_dim
+        n_qk = (HQ + HKV) * D
         for i, w in enumerate(self.layers):
             kc, vc = self.kc[i], self.vc[i]
             if i == 0:
                 C.decode_qkv(None, self.embed, self.ids, self.hid, w["gamma_in"], cfg.eps,
-                             w["w_qkv"], HQ, HKV, D, w["gamma_q"], w["gamma_k"], cfg.eps,
-                             self.cos, self.sin, self.pos, self.pos, kc, vc, self.q,
-                             self.scratch, self.qkv_cnt, self.err)
+                             w["w_qkv"], n_qk, self.qk, self.pos, vc, self.err)
             else:
-                C.decode_qkv(self.hid, None, None, None, w["gamma_in"], cfg.eps, w["w_qkv"],
-                             HQ, HKV, D, w["gamma_q"], w["gamma_k"], cfg.eps, self.cos, self.sin,
-                             self.pos, self.pos, kc, vc, self.q, self.scratch, self.qkv_cnt,
-                             self.err)
-            C.decode_attention(self.q, kc, vc, self.pos, HQ, HKV, self.split, cfg.scale,
-                               self.op, self.mp, self.lp, self.attn_cnt, self.attn, self.err)
+                C.decode_qkv(self.hid, None, None, None, w["gamma_in"], cfg.eps, w["w_qkv"], n_qk,
+                             self.qk, self.pos, vc, self.err)
+            C.decode_attention(self.qk, w["gamma_q"], w["gamma_k"], cfg.eps, self.cos, self.sin,
+                               kc, vc, self.pos, self.pos, HQ, HKV, self.split, cfg.scale,
+                               self.op, self.mp, self.lp, False, self.err)
+            C.attn_combine(self.op, self.mp, self.lp, self.attn, self.pos, self.split)
             C.gemv_residual(self.attn, w["w_o"], self.hid, None, self.h1)
             C.rmsnorm_gemv_swiglu(self.h1, w["gamma_post"], cfg.eps, w["w_gu"], self.act)
             C.gemv_residual(self.act, w["w_down"], self.h1, None, self.hid)
-        C.lm_head_sample(self.hid, self.gamma_final, cfg.eps, self.embed, self.logits, self.bv,
-                         self.bi, self.head_cnt, self.inp, self.plen, self.ids, self.pos,
-                         self.sam, self.err)
+        C.lm_head_argmax(self.hid, self.gamma_final, cfg.eps, self.embed, self.logits, self.bv,
+                         self.bi)
+        C.sample_step(self.bv, self.bi, self.inp, self.plen, self.ids, self.pos, self.sam,
+                      self.err)
 
     def _capture(self):
         side = torch.cuda.Stream(device=self.device)
