@@ -143,6 +143,19 @@ def kernel_lines(eng) -> dict:
     return out
 
 
+def copy_bandwidth(dev) -> dict:
+    """Sustained HBM bandwidth of this device for the decode kernels' access
+    pattern: a 2 GiB read + 2 GiB write copy with 16-byte streaming loads."""
+    from tilefoundry_amd._lib import C
+
+    src = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    ms = _events_time(lambda: C.copy_stream(src, dst), 5)
+    gbs = 2 * src.numel() / (ms * 1e-3) / 1e9
+    del src, dst
+    return {"GB/s": round(gbs, 1), "frac_of_nominal": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def cpu_baseline(seed: int, prompt: list[int], n_steps: int = 48) -> dict:
     """The CPU oracle on this host's cores: the same model (28 layers, vocab
     151936, same synthetic weights), a 4-token prompt walk then n_steps timed
@@ -216,11 +229,13 @@ def main() -> int:
     if args.kernel_only:
         # the dominant kernel's launch loop, then a plain copy of known size (the
         # calibration dispatch for FETCH_SIZE / WRITE_SIZE counter runs)
+        from tilefoundry_amd._lib import C
+
         roof = dominant_kernel(eng)
         src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
         for _ in range(4):
-            dst.copy_(src)
+            C.copy_stream(src, dst)
         torch.cuda.synchronize()
         print(json.dumps({"kernel_only": roof, "copy_bytes": src.numel()}))
         return 0
@@ -234,6 +249,7 @@ def main() -> int:
 
     roof = dominant_kernel(eng)
     kernels = {} if args.no_kernels else kernel_lines(eng)
+    copy_bw = copy_bandwidth(dev)
     weight_bytes = sum(t.numel() * 2 for w in eng.layers for t in w.values()) + eng.embed.numel() * 2
     mean_ctx = PROMPT + args.steps / 2.0
     kv_bytes = cfg.layers * mean_ctx * 2 * cfg.kv_heads * cfg.head_dim * 2
@@ -259,6 +275,7 @@ def main() -> int:
                      "GB/s": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
                      "frac": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         "roofline": roof,
+        "hbm_copy_measured": copy_bw,
         "kernels": kernels,
         "first_tokens": gen.tokens[:8],
     }

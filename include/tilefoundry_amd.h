@@ -162,6 +162,15 @@ int tfa_attn_combine(const float* op, const float* mp, const float* lp, void* ou
                      int64_t hq, int64_t head_dim, const int* wr, int64_t split,
                      hipStream_t stream);
 
+/* ------------------------------------------------------------ measurement */
+
+/* dst[0:bytes) = src[0:bytes) with the decode kernels' own access pattern
+ * (16-byte non-temporal loads, 16-byte stores, 64 KiB per block). Used to
+ * re-measure the sustained HBM bandwidth and as the calibration dispatch for
+ * hardware byte counters. No counterpart in the reference (its READMEs quote
+ * H200 nominal bandwidth). bytes % 16 == 0. */
+int tfa_copy_stream(const void* src, void* dst, int64_t bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

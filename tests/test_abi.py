@@ -1,0 +1,139 @@
+"""The C ABI boundary on a CPU host: the library loads, exports every entry point
+include/tilefoundry_amd.h declares, and every argument check fails with the
+right status before any HIP call is made (no compute here)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "tilefoundry_amd.h"
+LIB = ROOT / "tilefoundry_amd" / "libtilefoundry_amd.so"
+
+OK, NULL, SHAPE, ALIGN, CAPACITY, ARG, LAUNCH = range(7)
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(tfa_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not LIB.exists():
+        pytest.fail("libtilefoundry_amd.so is not built (python -m tilefoundry_amd._build)")
+    L = ctypes.CDLL(str(LIB))
+    L.tfa_last_error.restype = ctypes.c_char_p
+    L.tfa_status_string.restype = ctypes.c_char_p
+    L.tfa_lm_head_blocks.restype = ctypes.c_int64
+    L.tfa_lm_head_blocks.argtypes = [ctypes.c_int64]
+    return L
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared()
+    assert len(names) >= 15
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_status_strings(lib):
+    assert lib.tfa_abi_version() == 1
+    assert lib.tfa_status_string(OK) == b"ok"
+    assert lib.tfa_status_string(SHAPE) == b"unsupported shape"
+    assert lib.tfa_status_string(99) == b"unknown status"
+    assert lib.tfa_lm_head_blocks(151936) == 9496
+
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+F = ctypes.c_float
+I = ctypes.c_int
+BUF = ctypes.create_string_buffer(64)
+A = ctypes.cast(ctypes.addressof(BUF) + (-ctypes.addressof(BUF)) % 16, P)   # 16-byte aligned host pointer
+MIS = P(A.value + 2)                                                         # misaligned
+
+
+def call(lib, name, *args):
+    fn = getattr(lib, name)
+    return fn(*args), lib.tfa_last_error().decode()
+
+
+def test_norm_argument_checks(lib):
+    st, msg = call(lib, "tfa_rms_norm", A, A, A, I64(4), I64(7), F(1e-6), I(0), P(None))
+    assert st == SHAPE and "multiple of 8" in msg
+    st, _ = call(lib, "tfa_rms_norm", A, A, A, I64(4), I64(16384), F(1e-6), I(0), P(None))
+    assert st == SHAPE
+    st, msg = call(lib, "tfa_rms_norm", A, A, A, I64(4), I64(2048), F(1e-6), I(3), P(None))
+    assert st == ARG and "mode" in msg
+    st, _ = call(lib, "tfa_rms_norm", P(None), A, A, I64(4), I64(2048), F(1e-6), I(0), P(None))
+    assert st == NULL
+    st, _ = call(lib, "tfa_rms_norm", MIS, A, A, I64(4), I64(2048), F(1e-6), I(0), P(None))
+    assert st == ALIGN
+    # zero rows: nothing to do, null pointers allowed, no launch
+    st, _ = call(lib, "tfa_rms_norm", P(None), P(None), P(None), I64(0), I64(2048), F(1e-6), I(0), P(None))
+    assert st == OK
+    st, _ = call(lib, "tfa_add_rms_norm", A, P(None), A, A, A, I64(4), I64(2048), F(1e-6), I(0), P(None))
+    assert st == NULL
+    st, _ = call(lib, "tfa_resid_rms_norm_partials", A, A, I64(0), A, A, A, I64(2048), F(1e-6), P(None))
+    assert st == SHAPE
+
+
+def test_gemv_argument_checks(lib):
+    st, msg = call(lib, "tfa_gemv", A, A, A, I64(64), I64(30), I(1), P(None))
+    assert st == SHAPE and "multiple of 32" in msg
+    st, _ = call(lib, "tfa_gemv", A, A, A, I64(0), I64(64), I(1), P(None))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_gemv", A, MIS, A, I64(64), I64(64), I(1), P(None))
+    assert st == ALIGN
+    st, _ = call(lib, "tfa_gemv", A, A, P(None), I64(64), I64(64), I(1), P(None))
+    assert st == NULL
+    st, _ = call(lib, "tfa_gemv_residual", A, A, P(None), P(None), A, I64(64), I64(64), P(None))
+    assert st == NULL
+    st, _ = call(lib, "tfa_rmsnorm_gemv_swiglu", A, P(None), F(1e-6), A, A, I64(64), I64(64), P(None))
+    assert st == NULL
+    st, _ = call(lib, "tfa_lm_head_argmax", A, P(None), F(1e-6), A, I64(100), I64(64), P(None), A, A, P(None))
+    assert st == NULL
+    st, _ = call(lib, "tfa_sample_step", A, A, I64(0), A, A, A, A, A, I64(8), P(None), P(None))
+    assert st == SHAPE
+    st, msg = call(lib, "tfa_decode_qkv", A, P(None), P(None), I64(0), P(None), A, F(1e-6), A,
+                   I64(2048), I64(3072), I64(1024), A, P(None), A, I64(64), P(None), P(None))
+    assert st == NULL
+    st, msg = call(lib, "tfa_decode_qkv", A, A, P(None), I64(1000), P(None), A, F(1e-6), A,
+                   I64(2048), I64(3072), I64(1024), A, A, A, I64(64), P(None), P(None))
+    assert st == NULL and "embed mode" in msg
+
+
+def test_attention_argument_checks(lib):
+    args = lambda hd, cap, split, hq=16, hkv=8: (A, P(None), P(None), F(1e-6), P(None), P(None), I64(0), A, A,
+                                                  P(None), A, I64(hq), I64(hkv), I64(hd), I64(cap),
+                                                  I64(split), F(0.088), A, A, A, I(0), P(None), P(None))
+    st, msg = call(lib, "tfa_decode_attention", *args(64, 512, 64))
+    assert st == SHAPE and "128" in msg
+    st, _ = call(lib, "tfa_decode_attention", *args(128, 500, 64))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_decode_attention", *args(128, 512, 64, hq=12, hkv=8))
+    assert st == SHAPE
+    st, msg = call(lib, "tfa_decode_attention", *args(128, 512, 32))
+    assert st == SHAPE and "split" in msg
+    fused = list(args(128, 512, 64))
+    fused[1] = A  # gamma_q given, the rest of the fused-mode operands missing
+    st, msg = call(lib, "tfa_decode_attention", *fused)
+    assert st == NULL and "fused" in msg
+    st, _ = call(lib, "tfa_attn_combine", A, A, A, A, I64(0), I64(16), I64(128), P(None), I64(0), P(None))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_copy_stream", A, A, I64(17), P(None))
+    assert st == SHAPE
+
+
+def test_torch_extension_rejects_host_tensors():
+    from tilefoundry_amd import ops
+
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    g = torch.ones(64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.rms_norm(x, g, 1e-6)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.gemv(torch.zeros(64, dtype=torch.bfloat16), torch.zeros(8, 64, dtype=torch.bfloat16))

@@ -1,0 +1,225 @@
+"""Pins for the CPU oracle (no GPU): each check is independent of the formula it
+checks -- closed forms, special cases, f64 brute force, exact integer cases and
+planted mistakes -- so that a wrong rounding point, sign, index or operand in the
+oracle fails one of them."""
+import math
+
+import pytest
+import torch
+
+from oracle import norms as ON
+from oracle import qwen3 as OQ
+from tests._check import bf16_ulps
+
+BF = torch.bfloat16
+
+
+def g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---------------------------------------------------------------- norms
+def test_rms_norm_constant_row_closed_form():
+    """A row of one value c normalises to sign(c): y == sign(c) * gamma exactly."""
+    H = 2048
+    gamma = torch.linspace(-3, 3, H).to(BF)
+    for c in (0.5, -3.0, 7.25, -0.125, 100.0):
+        x = torch.full((H,), c).to(BF)
+        y = ON.rms_norm_q(x, gamma, 1e-6)
+        assert torch.equal(y, (math.copysign(1.0, c) * gamma.float()).to(BF))
+
+
+def test_rms_norm_matches_f64_within_one_rounding():
+    x = torch.randn(64, 2048, generator=g(0)).to(BF)
+    gamma = (1 + 0.1 * torch.randn(2048, generator=g(1))).to(BF)
+    x64 = x.double()
+    n64 = x64 * torch.rsqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-6)
+    ref = (n64.to(BF).double() * gamma.double()).to(BF)
+    assert int(bf16_ulps(ON.rms_norm_q(x, gamma, 1e-6), ref).max()) <= 1
+
+
+def test_rms_norm_landing_before_gamma_matters():
+    """Planted mistake: scaling in f32 before the bf16 landing gives a different
+    answer on random rows -- so the oracle's order is actually exercised."""
+    x = torch.randn(64, 2048, generator=g(2)).to(BF)
+    gamma = (1 + 0.1 * torch.randn(2048, generator=g(3))).to(BF)
+    x32 = x.float()
+    wrong = (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + 1e-6) * gamma.float()).to(BF)
+    assert not torch.equal(ON.rms_norm_q(x, gamma, 1e-6), wrong)
+
+
+def test_rms_norm_one_plus_gamma():
+    """Qwen3.5 form: gamma = 0 is the plain normalisation, in one landing."""
+    x = torch.randn(8, 5120, generator=g(4)).to(BF)
+    zero = torch.zeros(5120).to(BF)
+    x64 = x.double()
+    ref = (x64 * torch.rsqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-6)).to(BF)
+    assert int(bf16_ulps(ON.rms_norm_1p(x, zero, 1e-6), ref).max()) <= 1
+
+
+def test_add_rms_norm_residual_is_the_landed_sum():
+    x = torch.randn(4, 256, generator=g(5)).to(BF)
+    r = torch.randn(4, 256, generator=g(6)).to(BF)
+    gamma = torch.ones(256).to(BF)
+    y, ro = ON.add_rms_norm(x, r, gamma, 1e-6)
+    assert torch.equal(ro, (x.double() + r.double()).to(BF))
+    assert torch.equal(y, ON.rms_norm_q(ro, gamma, 1e-6))
+
+
+# ---------------------------------------------------------------- rope
+def test_rope_position_zero_is_identity():
+    cos, sin = OQ.rope_tables(8, 128, 1.0e6)
+    x = torch.randn(16, 128, generator=g(7)).to(BF)
+    assert torch.equal(OQ.rope(x, cos[0], sin[0]), x)
+
+
+def test_rope_is_complex_rotation():
+    """rotate-half on pairs (x_d, x_{d+64}) is multiplication by e^{i theta_d p}."""
+    D, p, theta = 128, 37, 1.0e6
+    x = torch.randn(4, D, generator=g(8)).to(BF)
+    cos, sin = OQ.rope_tables(p + 1, D, theta)
+    got = OQ.rope(x, cos[p], sin[p]).double()
+    z = torch.complex(x[:, :64].double(), x[:, 64:].double())
+    ang = torch.complex(cos[p, :64].double(), sin[p, :64].double())  # the table's own (landed) angles
+    w = z * ang
+    ref = torch.cat([w.real, w.imag], -1)
+    assert float((got - ref).abs().max()) <= float(ref.abs().max()) * 2 ** -8
+
+
+def test_rope_tables_against_closed_form():
+    cos, sin = OQ.rope_tables(100, 128, 1.0e6)
+    d = torch.arange(64, dtype=torch.float64)
+    ang = 99 * (1.0e6 ** (-(2 * d) / 128))
+    assert int(bf16_ulps(cos[99, :64], torch.cos(ang).to(BF)).max()) <= 1
+    assert int(bf16_ulps(sin[99, 64:], torch.sin(ang).to(BF)).max()) <= 1
+
+
+# ---------------------------------------------------------------- attention
+def test_attend_one_key_returns_value():
+    q = torch.randn(16, 128, generator=g(9)).to(BF)
+    k = torch.randn(1, 8, 128, generator=g(10)).to(BF)
+    v = torch.randn(1, 8, 128, generator=g(11)).to(BF)
+    for pb in (False, True):
+        out = OQ.attend(q, k, v, 128 ** -0.5, p_bf16=pb)
+        assert torch.equal(out, v[0].repeat_interleave(2, 0).reshape(-1))
+
+
+def test_attend_identical_keys_give_mean_value():
+    n = 33
+    q = torch.randn(16, 128, generator=g(12)).to(BF)
+    k = torch.randn(1, 8, 128, generator=g(13)).to(BF).expand(n, 8, 128).contiguous()
+    v = torch.randn(n, 8, 128, generator=g(14)).to(BF)
+    ref = v.double().mean(0).repeat_interleave(2, 0).reshape(-1).to(BF)
+    assert int(bf16_ulps(OQ.attend(q, k, v, 128 ** -0.5), ref).max()) <= 1
+
+
+def test_attend_matches_f64_brute_force():
+    n = 7
+    q = torch.randn(4, 128, generator=g(15)).to(BF)
+    k = torch.randn(n, 2, 128, generator=g(16)).to(BF)
+    v = torch.randn(n, 2, 128, generator=g(17)).to(BF)
+    out = OQ.attend(q, k, v, 0.1).double().view(4, 128)
+    for h in range(4):
+        kv = h // 2
+        s = [0.1 * sum(float(q[h, d]) * float(k[j, kv, d]) for d in range(128)) for j in range(n)]
+        m = max(s)
+        e = [math.exp(x - m) for x in s]
+        ref = [sum(e[j] * float(v[j, kv, d]) for j in range(n)) / sum(e) for d in range(128)]
+        ref = torch.tensor(ref, dtype=torch.float64)
+        assert float((out[h] - ref).abs().max()) <= float(ref.abs().max()) * 2 ** -7
+
+
+def test_attend_gqa_mapping_planted_mistake():
+    """Query head h reads kv head h // G (repeat_interleave), not h % HKV."""
+    q = torch.zeros(4, 128).to(BF)
+    k = torch.zeros(3, 2, 128).to(BF)
+    v = torch.zeros(3, 2, 128).to(BF)
+    v[:, 0] = 1.0
+    v[:, 1] = 2.0
+    out = OQ.attend(q, k, v, 1.0).view(4, 128)
+    assert out[:, 0].tolist() == [1.0, 1.0, 2.0, 2.0]
+
+
+def test_attend_p_bf16_close_to_f32():
+    q = torch.randn(16, 128, generator=g(18)).to(BF)
+    k = torch.randn(300, 8, 128, generator=g(19)).to(BF)
+    v = torch.randn(300, 8, 128, generator=g(20)).to(BF)
+    a = OQ.attend(q, k, v, 128 ** -0.5).float()
+    b = OQ.attend(q, k, v, 128 ** -0.5, p_bf16=True).float()
+    assert float((a - b).abs().max()) <= 1e-2 * float(a.abs().max())
+
+
+# ---------------------------------------------------------------- projections / argmax
+def test_proj_exact_on_integers():
+    x = torch.randint(-4, 5, (512,), generator=g(21)).to(BF)
+    w = torch.randint(-4, 5, (64, 512), generator=g(22)).to(BF)
+    ref = (x.long() @ w.long().t())
+    got = OQ.proj(x, w)
+    assert torch.equal(got.float(), ref.float().to(BF).float())
+
+
+def test_greedy_lowest_index_on_ties():
+    logits = torch.tensor([0.5, 3.0, -1.0, 3.0, 3.0])
+    assert OQ.greedy(logits) == 1
+
+
+# ---------------------------------------------------------------- the step
+def _tiny():
+    cfg = OQ.Qwen3Config(hidden=256, heads=4, kv_heads=2, head_dim=128, inter=512, vocab=300, layers=2)
+    return cfg, OQ.random_model(cfg, seed=3)
+
+
+def test_decode_cache_equals_recompute():
+    """Decoding with the appended cache equals re-running every prefix from
+    scratch (the cache holds exactly the per-position keys and values)."""
+    cfg, model = _tiny()
+    ids = [5, 17, 250, 3, 99]
+    cos, sin = OQ.rope_tables(8, cfg.head_dim, cfg.rope_theta)
+    caches = OQ.empty_caches(cfg, cfg.layers)
+    for p, t in enumerate(ids):
+        inc = OQ.step(model, cfg, t, p, caches, cos, sin)
+    fresh = OQ.empty_caches(cfg, cfg.layers)
+    for p, t in enumerate(ids):
+        again = OQ.step(model, cfg, t, p, fresh, cos, sin)
+    assert torch.equal(inc, again)
+    assert all(c[0].shape[0] == len(ids) for c in caches)
+
+
+def test_decode_causal_prefix():
+    """A later token does not change an earlier step's logits."""
+    cfg, model = _tiny()
+    cos, sin = OQ.rope_tables(8, cfg.head_dim, cfg.rope_theta)
+    a, b = OQ.empty_caches(cfg, 2), OQ.empty_caches(cfg, 2)
+    la = [OQ.step(model, cfg, t, p, a, cos, sin) for p, t in enumerate([7, 8, 9])]
+    lb = [OQ.step(model, cfg, t, p, b, cos, sin) for p, t in enumerate([7, 8, 200])]
+    assert torch.equal(la[0], lb[0]) and torch.equal(la[1], lb[1])
+    assert not torch.equal(la[2], lb[2])
+
+
+def test_teacher_forcing_reproduces_free_run():
+    cfg, model = _tiny()
+    free = OQ.decode(model, cfg, [1, 2, 3], 6)
+    forced = OQ.decode(model, cfg, [1, 2, 3], 6, teacher=free)
+    assert free == forced
+
+
+# ---------------------------------------------------------------- synthetic weights
+def test_synthetic_generator_golden_values():
+    """The cross-device generator's first values, pinned (any change to the
+    mixing or the transform changes every weight of every test)."""
+    from tilefoundry_amd.synthetic import normal
+
+    v = normal((6,), seed=0, stream=3, std=1.0, dtype=torch.float32).tolist()
+    want = [0.30610647797584534, -0.6969932913780212, 0.1560002863407135,
+            -0.5078309774398804, 0.13809585571289062, -1.1312625408172607]
+    assert v == pytest.approx(want, rel=0, abs=1e-7)
+
+
+def test_synthetic_generator_statistics():
+    from tilefoundry_amd.synthetic import normal
+
+    x = normal((1 << 20,), seed=1, stream=0, std=0.02, dtype=torch.float32).double()
+    assert abs(float(x.mean())) < 1e-4
+    assert abs(float(x.std()) - 0.02) < 1e-4
+    assert not torch.equal(normal((64,), 1, 0), normal((64,), 1, 1))
+    assert torch.equal(normal((64,), 1, 0), normal((64,), 1, 0))

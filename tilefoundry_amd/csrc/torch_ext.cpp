@@ -280,6 +280,14 @@ void attn_combine(const Tensor& op, const Tensor& mp, const Tensor& lp, const Te
                                 stream_of(op)));
 }
 
+void copy_stream(const Tensor& src, const Tensor& dst) {
+  if (!src.is_cuda() || !dst.is_cuda() || !src.is_contiguous() || !dst.is_contiguous())
+    bad("copy_stream: contiguous GPU tensors required");
+  const int64_t nbytes = src.numel() * src.element_size();
+  if (dst.numel() * dst.element_size() != nbytes) bad("copy_stream: size mismatch");
+  raise_status(tfa_copy_stream(src.data_ptr(), dst.data_ptr(), nbytes, stream_of(src)));
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -298,4 +306,5 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode_qkv", &decode_qkv);
   m.def("decode_attention", &decode_attention);
   m.def("attn_combine", &attn_combine);
+  m.def("copy_stream", &copy_stream);
 }
