@@ -135,32 +135,74 @@ int tfa_decode_qkv(const void* h, const void* table, const int64_t* ids, int64_t
                    int64_t hidden, int64_t n_qk, int64_t n_v, void* qk_out, const int* wr,
                    void* v_cache, int64_t cap, int* err, hipStream_t stream);
 
-/* Split-KV GQA decode attention (head_dim 128), caches [cap, hkv*128]
- * position-major, attending slots 0..wr[0]. Scores scaled by `scale` in f32
- * after the dot; softmax in f32 per split of `split` (64, 128 or 256) slots;
- * bf16 weights into P.V. Partials op [cap/split, hq, 128], mp / lp
- * [cap/split, hq]; splits past wr are left untouched unless `neutral`
- * (then m = -1e30, l = 0, o = 0).
- * Prepared mode (gamma_q == NULL): q is the final query [hq*128] and the cache
- * already holds slot wr. Fused mode: q is the raw [q | k] projection
- * [(hq+hkv)*128]; each query head gets Qwen3RMSNorm (gamma_q, eps_head) and
- * rotate-half RoPE at pos[0] (cos / sin [rope_rows, 128]); the new key gets the
- * same with gamma_k and is written to k_cache row wr[0].
+/* Split-KV GQA decode attention (head_dim 128) for `batch` sequences, each with
+ * its own cache [cap, hkv*128] (position-major; k_cache / v_cache are
+ * [batch, cap, hkv*128]) attending its slots 0..wr[b]. Scores scaled by `scale`
+ * in f32 after the dot; softmax in f32 per split of `split` (64, 128 or 256)
+ * slots; bf16 weights into P.V. Partials op [batch, cap/split, hq, 128],
+ * mp / lp [batch, cap/split, hq]; splits past wr[b] are left untouched unless
+ * `neutral` (then m = -1e30, l = 0, o = 0).
+ * Prepared mode (gamma_q == NULL): q is the final query [batch, hq*128] and the
+ * caches already hold slot wr. Fused mode: q is the raw [q | k] projection
+ * [batch, (hq+hkv)*128] bf16 (the value row is already in v_cache), or -- when
+ * qkv_part != NULL -- the raw [q | k | v] projection is the sum of part_ks f32
+ * split-K partials [part_ks, batch, (hq+2hkv)*128]; each query head gets
+ * Qwen3RMSNorm (gamma_q, eps_head) and rotate-half RoPE at pos[b] (cos / sin
+ * [rope_rows, 128]); the new key gets the same with gamma_k and is written to
+ * k_cache row wr[b] (and, from partials, the new value row to v_cache row wr[b]).
  * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:418-501 (attn_partial)
  * and :328-411 (qk_rope_cache). */
-int tfa_decode_attention(const void* q, const void* gamma_q, const void* gamma_k, float eps_head,
+int tfa_decode_attention(const void* q, const float* qkv_part, int64_t part_ks,
+                         const void* gamma_q, const void* gamma_k, float eps_head,
                          const void* cos_t, const void* sin_t, int64_t rope_rows, void* k_cache,
-                         const void* v_cache, const int* pos, const int* wr, int64_t hq,
+                         void* v_cache, const int* pos, const int* wr, int64_t batch, int64_t hq,
                          int64_t hkv, int64_t head_dim, int64_t cap, int64_t split, float scale,
                          float* op, float* mp, float* lp, int neutral, int* err,
                          hipStream_t stream);
 
-/* out[h*D + d] = bf16(sum_s op[s,h,d] e^(mp[s,h]-M) / sum_s lp[s,h] e^(mp[s,h]-M))
- * over all `splits`, or (wr != NULL) over the splits holding slots 0..wr[0].
+/* out[b, h*D + d] = bf16(sum_s op[b,s,h,d] e^(mp-M) / sum_s lp[b,s,h] e^(mp-M))
+ * over all `splits`, or (wr != NULL) over the splits holding slots 0..wr[b].
  * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:504-540 (attn_combine). */
 int tfa_attn_combine(const float* op, const float* mp, const float* lp, void* out, int64_t splits,
-                     int64_t hq, int64_t head_dim, const int* wr, int64_t split,
+                     int64_t batch, int64_t hq, int64_t head_dim, const int* wr, int64_t split,
                      hipStream_t stream);
+
+/* --------------------------------------------- batched decode (<= 32 rows) */
+
+/* Tiles of 32 weight rows: the per-token block-winner count of the argmax
+ * epilogue for n rows. */
+int64_t tfa_skinny_blocks(int64_t n);
+
+/* Y = X[m, k] . W[n, k]^T for m <= 32 token rows on bf16 MFMA (f32 accumulate).
+ * epilogue 0: f32 split-K partials part[ks, m, n] (sum over ks = Y);
+ * epilogue 1 (ks = 1): SwiGLU over interleaved rows (2i, 2i+1) = (gate_i, up_i):
+ *             act[m, n/2] = bf16(bf16(silu(bf16 g)) * bf16 u);
+ * epilogue 2 (ks = 1): logits[m, n] f32 and, per token, each 32-row block's best
+ *             (max, lowest index) into block_val / block_idx [m, tfa_skinny_blocks(n)].
+ * k % (128 * ks) == 0.
+ * Replaces (batched): examples/qwen3_1_7b-tilelang/fast/kernels.py:123-145 (gemv),
+ * :210-257 (gemv_silu), :260-321 (lm_head). */
+int tfa_skinny_gemm(const void* x, const void* w, int64_t m, int64_t n, int64_t k, int64_t ks,
+                    int epilogue, float* part, void* act, float* logits, float* block_val,
+                    int* block_idx, hipStream_t stream);
+
+/* Per token row: h = table[ids[r]] (table != NULL) or
+ * h = bf16(h_in[r] + bf16(sum_s part[s, r, :])) (ks partials [ks, m, hidden]);
+ * h_out[r] = h (may alias h_in); xn[r] = bf16(bf16(h * rsqrt(mean h^2 + eps)) * gamma).
+ * Replaces (batched): examples/qwen3_1_7b-tilelang/fast/kernels.py:82-116
+ * (resid_rms_norm) and :579-588 (embed). */
+int tfa_rows_norm(const void* table, const int64_t* ids, int64_t vocab, const void* h_in,
+                  const float* part, int64_t ks, void* h_out, const void* gamma, void* xn,
+                  int64_t m, int64_t hidden, float eps, int* err, hipStream_t stream);
+
+/* The greedy step for `batch` sequences: per sequence b, best = argmax over
+ * block_val[b, :] (lowest index on ties); sam[b, pos[b]] = best;
+ * ids[b] = pos[b]+1 < prompt_len[b] ? inp[b, pos[b]+1] : best; pos[b] += 1.
+ * inp / sam are [batch, nsteps].
+ * Replaces (batched): examples/qwen3_1_7b-tilelang/fast/kernels.py:591-637. */
+int tfa_batch_sample_step(const float* block_val, const int* block_idx, int64_t nblocks,
+                          int64_t batch, const int* inp, const int* prompt_len, int64_t* ids,
+                          int* pos, int* sam, int64_t nsteps, int* err, hipStream_t stream);
 
 /* ------------------------------------------------------------ measurement */
 

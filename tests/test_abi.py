@@ -107,9 +107,10 @@ def test_gemv_argument_checks(lib):
 
 
 def test_attention_argument_checks(lib):
-    args = lambda hd, cap, split, hq=16, hkv=8: (A, P(None), P(None), F(1e-6), P(None), P(None), I64(0), A, A,
-                                                  P(None), A, I64(hq), I64(hkv), I64(hd), I64(cap),
-                                                  I64(split), F(0.088), A, A, A, I(0), P(None), P(None))
+    args = lambda hd, cap, split, hq=16, hkv=8: (A, P(None), I64(0), P(None), P(None), F(1e-6), P(None),
+                                                  P(None), I64(0), A, A, P(None), A, I64(1), I64(hq),
+                                                  I64(hkv), I64(hd), I64(cap), I64(split), F(0.088),
+                                                  A, A, A, I(0), P(None), P(None))
     st, msg = call(lib, "tfa_decode_attention", *args(64, 512, 64))
     assert st == SHAPE and "128" in msg
     st, _ = call(lib, "tfa_decode_attention", *args(128, 500, 64))
@@ -119,10 +120,29 @@ def test_attention_argument_checks(lib):
     st, msg = call(lib, "tfa_decode_attention", *args(128, 512, 32))
     assert st == SHAPE and "split" in msg
     fused = list(args(128, 512, 64))
-    fused[1] = A  # gamma_q given, the rest of the fused-mode operands missing
+    fused[3] = A  # gamma_q given, the rest of the fused-mode operands missing
     st, msg = call(lib, "tfa_decode_attention", *fused)
     assert st == NULL and "fused" in msg
-    st, _ = call(lib, "tfa_attn_combine", A, A, A, A, I64(0), I64(16), I64(128), P(None), I64(0), P(None))
+    st, _ = call(lib, "tfa_attn_combine", A, A, A, A, I64(0), I64(1), I64(16), I64(128), P(None), I64(0), P(None))
+    assert st == SHAPE
+    part_only = list(args(128, 512, 64))
+    part_only[0], part_only[1], part_only[2] = P(None), A, I64(1)   # partials without fused mode
+    st, msg = call(lib, "tfa_decode_attention", *part_only)
+    assert st == ARG and "partials" in msg
+
+
+def test_batched_argument_checks(lib):
+    st, msg = call(lib, "tfa_skinny_gemm", A, A, I64(33), I64(64), I64(2048), I64(1), I(0), A, P(None), P(None), P(None), P(None), P(None))
+    assert st == SHAPE and "[1, 32]" in msg
+    st, _ = call(lib, "tfa_skinny_gemm", A, A, I64(32), I64(64), I64(2000), I64(1), I(0), A, P(None), P(None), P(None), P(None), P(None))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_skinny_gemm", A, A, I64(32), I64(64), I64(2048), I64(2), I(1), P(None), A, P(None), P(None), P(None), P(None))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_skinny_gemm", A, A, I64(32), I64(64), I64(2048), I64(1), I(7), A, A, A, A, A, P(None))
+    assert st == ARG
+    st, _ = call(lib, "tfa_rows_norm", P(None), P(None), I64(0), A, P(None), I64(1), A, A, A, I64(4), I64(2048), F(1e-6), P(None), P(None))
+    assert st == NULL
+    st, _ = call(lib, "tfa_batch_sample_step", A, A, I64(10), I64(0), A, A, A, A, A, I64(8), P(None), P(None))
     assert st == SHAPE
     st, _ = call(lib, "tfa_copy_stream", A, A, I64(17), P(None))
     assert st == SHAPE

@@ -1,0 +1,230 @@
+"""Batched decode (up to 32 sequences) against the CPU oracle: the skinny MFMA
+GEMM and its epilogues, the row norms, attention reading split-K partials, and
+the batch engine end to end (each sequence against the oracle's bs=1 decode)."""
+import pytest
+import torch
+
+from oracle import norms as ON
+from oracle import qwen3 as OQ
+from tests._check import assert_close, assert_equal, assert_l2, max_rel
+
+BF = torch.bfloat16
+H, HQ, HKV, D, I = 2048, 16, 8, 128, 6144
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def randn(*shape, g, std=1.0, mean=0.0):
+    return (mean + std * torch.randn(*shape, generator=g)).to(BF)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,ks", [(32, 4096, 2048, 1), (32, 4096, 2048, 2), (5, 2048, 2048, 4),
+                                      (1, 96, 256, 1), (32, 2048, 6144, 4), (17, 1000, 1024, 2)])
+def test_skinny_partials(dev, M, N, K, ks):
+    from tilefoundry_amd import ops
+
+    g = gen(M * N + K)
+    x = randn(M, K, g=g)
+    w = randn(N, K, g=g, std=K ** -0.5)
+    ref = x.float() @ w.float().t()
+    part = ops.skinny_gemm(x.to(dev), w.to(dev), "partial", ks=ks)
+    assert part.shape == (ks, M, N)
+    assert max_rel(part.sum(0), ref) < 5e-3
+
+
+@pytest.mark.gpu
+def test_skinny_exact_on_integers(dev):
+    """Small-integer inputs: every MFMA product and f32 sum is exact."""
+    from tilefoundry_amd import ops
+
+    g = gen(3)
+    x = torch.randint(-3, 4, (32, 2048), generator=g).to(BF)
+    w = torch.randint(-3, 4, (256, 2048), generator=g).to(BF)
+    ref = (x.long() @ w.long().t()).float()
+    part = ops.skinny_gemm(x.to(dev), w.to(dev), "partial", ks=2)
+    assert_equal("integer skinny gemm", part.sum(0).cpu(), ref)
+
+
+@pytest.mark.gpu
+def test_skinny_swiglu(dev):
+    from tilefoundry_amd import ops
+
+    g = gen(5)
+    M = 32
+    xn = randn(M, H, g=g)
+    wg = randn(I, H, g=g, std=0.02)
+    wu = randn(I, H, g=g, std=0.02)
+    gg, uu = OQ.proj(xn, wg), OQ.proj(xn, wu)
+    ref = torch.nn.functional.silu(gg.float()).to(BF) * uu
+    w_gu = torch.stack([wg, wu], 1).reshape(2 * I, H)
+    got = ops.skinny_gemm(xn.to(dev), w_gu.to(dev), "swiglu")
+    assert_close("skinny swiglu", got, ref)
+
+
+@pytest.mark.gpu
+def test_skinny_argmax(dev):
+    from tilefoundry_amd import ops
+
+    g = gen(7)
+    M, V = 32, 151936
+    x = randn(M, H, g=g)
+    w = randn(V, H, g=g, std=0.02)
+    ref = x.float() @ w.float().t()
+    logits, bv, bi = ops.skinny_gemm(x.to(dev), w.to(dev), "argmax")
+    assert max_rel(logits, ref) < 5e-3
+    best = bi.gather(1, bv.argmax(1, keepdim=True)).squeeze(1).cpu()
+    assert torch.equal(best, logits.cpu().argmax(1).to(torch.int32))
+
+
+@pytest.mark.gpu
+def test_skinny_argmax_ties(dev):
+    from tilefoundry_amd import ops
+
+    M, V, K = 3, 4096, 256
+    w = torch.zeros(V, K).to(BF)
+    for idx in (3000, 40, 41, 2000):
+        w[idx, 0] = 1.0
+    x = torch.zeros(M, K).to(BF)
+    x[:, 0] = 1.0
+    logits, bv, bi = ops.skinny_gemm(x.to(dev), w.to(dev), "argmax")
+    best = bi.gather(1, bv.argmax(1, keepdim=True)).squeeze(1).cpu().tolist()
+    assert best == [40, 40, 40]
+
+
+@pytest.mark.gpu
+def test_rows_norm_embed_and_residual(dev):
+    from tilefoundry_amd import ops
+
+    g = gen(9)
+    M = 32
+    table = randn(1000, H, g=g, std=0.02)
+    ids = torch.randint(0, 1000, (M,), generator=g)
+    gamma = randn(H, g=g, std=0.1, mean=1.0)
+    h, xn = ops.rows_norm(gamma.to(dev), 1e-6, table=table.to(dev), ids=ids.to(dev))
+    assert_equal("gathered rows", h, table[ids])
+    assert_close("embed norm", xn, ON.rms_norm_q(table[ids], gamma, 1e-6))
+    hin = randn(M, H, g=g)
+    part = torch.randn(4, M, H, generator=g)
+    h2, xn2 = ops.rows_norm(gamma.to(dev), 1e-6, h_in=hin.to(dev), part=part.to(dev))
+    href = hin + part.sum(0).to(BF)
+    assert_close("residual", h2, href)
+    assert_close("residual norm", xn2, ON.rms_norm_q(href, gamma, 1e-6))
+
+
+@pytest.mark.gpu
+def test_batched_attention_from_partials(dev):
+    """Per sequence: q/k/v from summed f32 partials, head norm + RoPE at its own
+    position, the new K and V rows written at its own slot, attention over its
+    own cache -- each against the oracle."""
+    from tilefoundry_amd._lib import C
+
+    g = gen(11)
+    B, cap, split, ks = 3, 512, 64, 2
+    rows = (HQ + 2 * HKV) * D
+    part = torch.randn(ks, B, rows, generator=g) * 0.5
+    gq = randn(D, g=g, std=0.1, mean=1.0)
+    gk = randn(D, g=g, std=0.1, mean=1.0)
+    cos, sin = OQ.rope_tables(cap, D, 1.0e6)
+    pos = [0, 100, 511]
+    kc = torch.zeros(B, cap, HKV, D).to(BF)
+    vc = torch.zeros(B, cap, HKV, D).to(BF)
+    for b, p in enumerate(pos):
+        kc[b, :p] = randn(p, HKV, D, g=g)
+        vc[b, :p] = randn(p, HKV, D, g=g)
+    kd, vd = kc.view(B, cap, -1).to(dev), vc.view(B, cap, -1).to(dev)
+    ns = cap // split
+    op = torch.empty(B, ns, HQ, D, device=dev)
+    mp = torch.empty(B, ns, HQ, device=dev)
+    lp = torch.empty(B, ns, HQ, device=dev)
+    posd = torch.tensor(pos, dtype=torch.int32, device=dev)
+    C.decode_attention(None, part.to(dev), gq.to(dev), gk.to(dev), 1e-6, cos.to(dev), sin.to(dev),
+                       kd, vd, posd, posd, HQ, HKV, split, D ** -0.5, op, mp, lp, False, None)
+    out = torch.empty(B, HQ * D, dtype=BF, device=dev)
+    C.attn_combine(op, mp, lp, out, posd, split)
+    raw = part.sum(0).to(BF)
+    for b, p in enumerate(pos):
+        q = OQ.rope(OQ.head_norm(raw[b, : HQ * D].view(HQ, D), gq, 1e-6), cos[p], sin[p])
+        k = OQ.rope(OQ.head_norm(raw[b, HQ * D: (HQ + HKV) * D].view(HKV, D), gk, 1e-6), cos[p], sin[p])
+        v = raw[b, (HQ + HKV) * D:].view(HKV, D)
+        assert_close(f"k row b={b}", kd[b, p].view(HKV, D), k)
+        assert_equal(f"v row b={b}", vd[b, p].view(HKV, D), v)
+        kk = torch.cat([kc[b, :p], k.unsqueeze(0)])
+        vv = torch.cat([vc[b, :p], v.unsqueeze(0)])
+        assert_close(f"attention b={b}", out[b], OQ.attend(q, kk, vv, D ** -0.5))
+
+
+def _small(layers=2, vocab=8192, seed=5):
+    from tilefoundry_amd.qwen3 import Qwen3Config, synthetic_weights
+
+    cfg = Qwen3Config(layers=layers, vocab=vocab)
+    return cfg, synthetic_weights(cfg, seed=seed)
+
+
+def _oracle(wts, cfg):
+    from tests.test_qwen3_engine import oracle_cfg, oracle_model
+
+    return oracle_model(wts, cfg), oracle_cfg(cfg)
+
+
+@pytest.mark.gpu
+def test_batch_engine_logits(dev):
+    from tilefoundry_amd.qwen3 import BatchEngine
+
+    cfg, wts = _small()
+    B = 4
+    eng = BatchEngine(cfg, batch=B, device=dev, max_new=32, prompt_room=32, weights=wts)
+    prompts = OQ.prompt_ids(cfg.vocab, 9, seed=21, batch=B)
+    got = eng.logits_for(prompts)
+    om, oc = _oracle(wts, cfg)
+    cos, sin = OQ.rope_tables(9, cfg.head_dim, cfg.rope_theta)
+    for b in range(B):
+        caches = OQ.empty_caches(oc, cfg.layers)
+        for p, t in enumerate(prompts[b]):
+            ref = OQ.step(om, oc, t, p, caches, cos, sin, p_bf16=True)
+        assert_l2(f"logits seq {b}", got[b], ref)
+        for i in range(cfg.layers):
+            kc = eng.kc[i, b, :9].view(9, cfg.kv_heads, cfg.head_dim)
+            check = assert_close if i == 0 else assert_l2
+            check(f"k cache seq {b} layer {i}", kc, caches[i][0])
+
+
+@pytest.mark.gpu
+def test_batch_engine_greedy(dev):
+    """Each sequence's free-running ids equal the oracle's bs=1 decode of that
+    sequence wherever the oracle's own top-2 margin is resolvable."""
+    from tilefoundry_amd.qwen3 import BatchEngine
+
+    cfg, wts = _small()
+    B = 32
+    eng = BatchEngine(cfg, batch=B, device=dev, max_new=32, prompt_room=32, weights=wts)
+    prompts = OQ.prompt_ids(cfg.vocab, 8, seed=22, batch=B)
+    gen = eng.generate(prompts, 16)
+    om, oc = _oracle(wts, cfg)
+    agree = 0
+    for b in (0, 7, 31):
+        rec = []
+        want = OQ.decode(om, oc, prompts[b], 16, record=rec, p_bf16=True)
+        diff = next((i for i, (x, y) in enumerate(zip(gen.tokens[b], want)) if x != y), None)
+        if diff is None:
+            agree += 1
+        else:
+            lg, pick, gap = rec[diff]
+            assert gap < 1e-2 * float(lg.abs().max()), f"seq {b} step {diff}: clear margin {gap:.4g}"
+    assert agree >= 2
+
+
+@pytest.mark.gpu
+def test_batch_engine_matches_single_engine(dev):
+    """The batch engine and the bs=1 engine agree on a sequence's logits."""
+    from tilefoundry_amd.qwen3 import BatchEngine, Engine
+
+    cfg, wts = _small()
+    prompts = OQ.prompt_ids(cfg.vocab, 6, seed=23, batch=2)
+    be = BatchEngine(cfg, batch=2, device=dev, max_new=16, prompt_room=16, weights=wts)
+    se = Engine(cfg, device=dev, max_new=16, prompt_room=16, weights=wts)
+    got = be.logits_for(prompts)
+    for b in range(2):
+        assert_l2(f"seq {b}", got[b], se.logits_for(prompts[b]))

@@ -32,19 +32,23 @@ constexpr int D = 128;
 
 struct AttnArgs {
   const uint16_t* q;      // prepared q [hq*D]; fused mode: raw [q | k] [(hq+hkv)*D]
+  const float* part;      // batched fused mode: q|k|v split-K partials [ks, B, (hq+2hkv)*D]
+  int part_ks;
+  size_t q_bstride;       // elements between sequences in q
+  size_t cache_bstride;   // elements between sequences in k_cache / v_cache
   const uint16_t* gq;     // [D] q head scale (fused mode when non-null)
   const uint16_t* gk;     // [D] k head scale
   float eps_head;
   const uint16_t* cos_t;  // [mp_rows, D]
   const uint16_t* sin_t;
   int mp_rows;
-  uint16_t* kc;           // [cap, hkv*D]
-  const uint16_t* vc;     // [cap, hkv*D]
-  const int* pos;         // [1] rope position (fused mode)
-  const int* wr;          // [1] newest slot; attend slots 0..wr
-  float* op;              // [ns, hq, D]
-  float* mp;              // [ns, hq]
-  float* lp;              // [ns, hq]
+  uint16_t* kc;           // [B, cap, hkv*D]
+  uint16_t* vc;           // [B, cap, hkv*D]
+  const int* pos;         // [B] rope position (fused mode)
+  const int* wr;          // [B] newest slot; attend slots 0..wr
+  float* op;              // [B, ns, hq, D]
+  float* mp;              // [B, ns, hq]
+  float* lp;              // [B, ns, hq]
   int neutral;            // write neutral partials for splits past the context
   int* err;
   int hq, hkv, cap, ns;
@@ -55,12 +59,28 @@ TFA_DEV void set_err(int* err, int code) {
   if (err) atomicExch(err, code);
 }
 
+// Raw projection values of a 128-wide head for lane l: d = l and d = l + 64,
+// landed in bf16 -- from a bf16 vector, or summed over split-K f32 partials.
+TFA_DEV void head_raw(const uint16_t* raw, const float* part, int ks, size_t kstride, int lane,
+                      float& x0, float& x1) {
+  if (part) {
+    float a0 = 0.f, a1 = 0.f;
+    for (int s = 0; s < ks; ++s) {
+      a0 += part[s * kstride + lane];
+      a1 += part[s * kstride + lane + 64];
+    }
+    x0 = round_bf(a0);
+    x1 = round_bf(a1);
+  } else {
+    x0 = bf2f(raw[lane]);
+    x1 = bf2f(raw[lane + 64]);
+  }
+}
+
 // Per-head Qwen3RMSNorm + rotate-half RoPE of one 128-wide head by one wave:
 // lane l owns d = l and its rotation partner d = l + 64.
-TFA_DEV void norm_rope_head(const uint16_t* raw, const uint16_t* gam, float eps, float c0, float s0,
+TFA_DEV void norm_rope_head(float x0, float x1, const uint16_t* gam, float eps, float c0, float s0,
                             float c1, float s1, int lane, float& o0, float& o1) {
-  const float x0 = bf2f(raw[lane]);
-  const float x1 = bf2f(raw[lane + 64]);
   const float ss = wave_sum(x0 * x0 + x1 * x1);
   const float rs = rsqrt_rn(ss / static_cast<float>(D) + eps);
   const float n0 = round_bf(round_bf(x0 * rs) * bf2f(gam[lane]));
@@ -75,6 +95,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
   constexpr int SS = 16 * NIT;
   __shared__ float qs[G][D];
   __shared__ float knew[D];
+  __shared__ float vnew[D];
   __shared__ float obuf[kWaves][G][D];
   __shared__ float red[2][kWaves][G];
 
@@ -84,10 +105,16 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
   const int dc = lane & 15;
   const int s = blockIdx.x;
   const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
   const int t = threadIdx.x;
   const int KN = a.hkv * D;
+  uint16_t* kc = a.kc + b * a.cache_bstride;
+  uint16_t* vc = a.vc + b * a.cache_bstride;
+  float* op = a.op + static_cast<size_t>(b) * a.ns * a.hq * D;
+  float* mp = a.mp + static_cast<size_t>(b) * a.ns * a.hq;
+  float* lp = a.lp + static_cast<size_t>(b) * a.ns * a.hq;
 
-  int last = a.wr[0];
+  int last = a.wr[b];
   if (last < 0 || last >= a.cap) {
     if (s == 0 && kvh == 0 && t == 0) set_err(a.err, 4);
     last = last < 0 ? -1 : a.cap - 1;
@@ -99,10 +126,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
       for (int e = t; e < G * D; e += kThreads) {
         const int g = e / D, d = e % D;
         const int h = kvh * G + g;
-        a.op[(static_cast<size_t>(s) * a.hq + h) * D + d] = 0.f;
+        op[(static_cast<size_t>(s) * a.hq + h) * D + d] = 0.f;
         if (d == 0) {
-          a.mp[s * a.hq + h] = -1.0e30f;
-          a.lp[s * a.hq + h] = 0.f;
+          mp[s * a.hq + h] = -1.0e30f;
+          lp[s * a.hq + h] = 0.f;
         }
       }
     }
@@ -110,6 +137,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
   }
   const bool fused = a.gq != nullptr;
   const bool has_new = fused && last < start + SS;  // this split holds the newest slot
+  const bool new_v = has_new && a.part != nullptr;  // ... and also brings the new value row
 
   // 1. every K / V load of the split, first
   uint4 kv[NIT], vv[NIT];
@@ -118,13 +146,13 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
     const int pi = start + it * 16 + wid * 4 + slot;
     const bool valid = pi < n;
     const size_t off = static_cast<size_t>(pi) * KN + kvh * D + 8 * dc;
-    kv[it] = valid ? ld16_stream(a.kc + off) : make_uint4(0, 0, 0, 0);
-    vv[it] = valid ? ld16_stream(a.vc + off) : make_uint4(0, 0, 0, 0);
+    kv[it] = valid ? ld16_stream(kc + off) : make_uint4(0, 0, 0, 0);
+    vv[it] = valid ? ld16_stream(vc + off) : make_uint4(0, 0, 0, 0);
   }
 
   // 2. the query (and, in one block, the new key) while they are in flight
   if (fused) {
-    int p = a.pos[0];
+    int p = a.pos[b];
     if (p < 0 || p >= a.mp_rows) {
       if (s == 0 && kvh == 0 && t == 0) set_err(a.err, 5);
       p = 0;
@@ -133,23 +161,41 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
     const float s0 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane]);
     const float c1 = bf2f(a.cos_t[static_cast<size_t>(p) * D + lane + 64]);
     const float s1 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane + 64]);
-    for (int hh = wid; hh < G + (has_new ? 1 : 0); hh += kWaves) {
-      float o0, o1;
+    const int rows = (a.hq + 2 * a.hkv) * D;   // q | k | v row width of the partials
+    const uint16_t* qsrc = a.q ? a.q + b * a.q_bstride : nullptr;
+    const float* psrc = a.part ? a.part + static_cast<size_t>(b) * rows : nullptr;
+    const size_t kstride = static_cast<size_t>(rows) * gridDim.z;  // partials are [ks, B, rows]
+    const int nwork = G + (has_new ? 1 : 0) + (new_v ? 1 : 0);
+    for (int hh = wid; hh < nwork; hh += kWaves) {
+      float x0, x1, o0, o1;
       if (hh < G) {
-        norm_rope_head(a.q + (kvh * G + hh) * D, a.gq, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
+        const int off = (kvh * G + hh) * D;
+        head_raw(qsrc ? qsrc + off : nullptr, psrc ? psrc + off : nullptr, a.part_ks, kstride, lane, x0, x1);
+        norm_rope_head(x0, x1, a.gq, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
         qs[hh][lane] = o0;
         qs[hh][lane + 64] = o1;
-      } else {
-        norm_rope_head(a.q + (a.hq + kvh) * D, a.gk, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
+      } else if (hh == G) {
+        const int off = (a.hq + kvh) * D;
+        head_raw(qsrc ? qsrc + off : nullptr, psrc ? psrc + off : nullptr, a.part_ks, kstride, lane, x0, x1);
+        norm_rope_head(x0, x1, a.gk, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
         knew[lane] = o0;
         knew[lane + 64] = o1;
-        uint16_t* dst = a.kc + static_cast<size_t>(last) * KN + kvh * D;
+        uint16_t* dst = kc + static_cast<size_t>(last) * KN + kvh * D;
         dst[lane] = static_cast<uint16_t>(f2bf(o0));
         dst[lane + 64] = static_cast<uint16_t>(f2bf(o1));
+      } else {
+        const int off = (a.hq + a.hkv + kvh) * D;
+        head_raw(nullptr, psrc + off, a.part_ks, kstride, lane, x0, x1);
+        vnew[lane] = x0;
+        vnew[lane + 64] = x1;
+        uint16_t* dst = vc + static_cast<size_t>(last) * KN + kvh * D;
+        dst[lane] = static_cast<uint16_t>(f2bf(x0));
+        dst[lane + 64] = static_cast<uint16_t>(f2bf(x1));
       }
     }
   } else {
-    for (int e = t; e < G * D; e += kThreads) qs[e / D][e % D] = bf2f(a.q[(kvh * G) * D + e]);
+    for (int e = t; e < G * D; e += kThreads)
+      qs[e / D][e % D] = bf2f(a.q[b * a.q_bstride + (kvh * G) * D + e]);
   }
   __syncthreads();
 
@@ -218,7 +264,13 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
     float vf[8];
-    unpack8(vv[it], vf);
+    const int pi = start + it * 16 + wid * 4 + slot;
+    if (new_v && pi == last) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vf[i] = vnew[8 * dc + i];
+    } else {
+      unpack8(vv[it], vf);
+    }
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -247,17 +299,17 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
     const int g = e / D, d = e % D;
     const float v = (obuf[0][g][d] + obuf[1][g][d]) + (obuf[2][g][d] + obuf[3][g][d]);
     const int h = kvh * G + g;
-    a.op[(static_cast<size_t>(s) * a.hq + h) * D + d] = v;
+    op[(static_cast<size_t>(s) * a.hq + h) * D + d] = v;
     if (d == 0) {
-      a.mp[s * a.hq + h] = m[g];
-      a.lp[s * a.hq + h] = l[g];
+      mp[s * a.hq + h] = m[g];
+      lp[s * a.hq + h] = l[g];
     }
   }
 }
 
 template <int G>
-int launch_attn_g(const AttnArgs& a, int ss, hipStream_t st) {
-  const dim3 grid(a.ns, a.hkv);
+int launch_attn_g(const AttnArgs& a, int ss, int batch, hipStream_t st) {
+  const dim3 grid(a.ns, a.hkv, batch);
   switch (ss) {
     case 64: attn_decode_kernel<G, 4><<<grid, kThreads, 0, st>>>(a); break;
     case 128: attn_decode_kernel<G, 8><<<grid, kThreads, 0, st>>>(a); break;
@@ -280,6 +332,11 @@ constexpr int kCombMaxD = kCombThreads / kCombGroups;
 __global__ __launch_bounds__(kCombThreads) void attn_combine_kernel(
     const float* op, const float* mp, const float* lp, uint16_t* out, int ns, int hq, int Dh,
     const int* wr, int split) {
+  const int bb = blockIdx.y;
+  op += static_cast<size_t>(bb) * ns * hq * Dh;
+  mp += static_cast<size_t>(bb) * ns * hq;
+  lp += static_cast<size_t>(bb) * ns * hq;
+  out += static_cast<size_t>(bb) * hq * Dh;
   __shared__ float s_e[kCombMaxSplits];
   __shared__ float s_l[kCombMaxSplits];
   __shared__ float s_red[kCombGroups][kCombMaxD];
@@ -289,7 +346,7 @@ __global__ __launch_bounds__(kCombThreads) void attn_combine_kernel(
   const int t = threadIdx.x;
   int nact = ns;
   if (wr) {
-    const int w = wr[0];
+    const int w = wr[bb];
     nact = w < 0 ? 0 : w / split + 1;
     if (nact > ns) nact = ns;
   }
@@ -333,24 +390,33 @@ __global__ __launch_bounds__(kCombThreads) void attn_combine_kernel(
 
 extern "C" {
 
-int tfa_decode_attention(const void* q, const void* gamma_q, const void* gamma_k, float eps_head,
+int tfa_decode_attention(const void* q, const float* qkv_part, int64_t part_ks,
+                         const void* gamma_q, const void* gamma_k, float eps_head,
                          const void* cos_t, const void* sin_t, int64_t rope_rows, void* k_cache,
-                         const void* v_cache, const int* pos, const int* wr, int64_t hq,
+                         void* v_cache, const int* pos, const int* wr, int64_t batch, int64_t hq,
                          int64_t hkv, int64_t head_dim, int64_t cap, int64_t split, float scale,
                          float* op, float* mp, float* lp, int neutral, int* err,
                          hipStream_t stream) {
-  if (!q || !k_cache || !v_cache || !wr || !op || !mp || !lp)
+  if (!k_cache || !v_cache || !wr || !op || !mp || !lp)
     return fail(TFA_ERR_NULL, "tfa_decode_attention: null pointer argument");
+  if (!q && !qkv_part) return fail(TFA_ERR_NULL, "tfa_decode_attention: q or qkv_part required");
   if (head_dim != D) return fail(TFA_ERR_SHAPE, "tfa_decode_attention: head_dim %lld, only 128 supported", (long long)head_dim);
   if (hkv <= 0 || hq % hkv != 0) return fail(TFA_ERR_SHAPE, "tfa_decode_attention: hq %lld not a multiple of hkv %lld", (long long)hq, (long long)hkv);
   if (split <= 0 || cap <= 0 || cap % split != 0)
     return fail(TFA_ERR_SHAPE, "tfa_decode_attention: cap %lld not a positive multiple of split %lld", (long long)cap, (long long)split);
-  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache))
+  if (batch < 1 || batch > 65535) return fail(TFA_ERR_SHAPE, "tfa_decode_attention: batch %lld out of range", (long long)batch);
+  if ((q && !aligned16(q)) || !aligned16(k_cache) || !aligned16(v_cache))
     return fail(TFA_ERR_ALIGN, "tfa_decode_attention: q / caches not 16-byte aligned");
   if (gamma_q && (!gamma_k || !cos_t || !sin_t || !pos || rope_rows <= 0))
     return fail(TFA_ERR_NULL, "tfa_decode_attention: fused mode needs gamma_k, cos, sin, pos");
+  if (qkv_part && (!gamma_q || part_ks < 1))
+    return fail(TFA_ERR_ARG, "tfa_decode_attention: partials are a fused-mode source (gamma_q, ks >= 1)");
   AttnArgs a{};
-  a.q = static_cast<const uint16_t*>(q);
+  a.q = qkv_part ? nullptr : static_cast<const uint16_t*>(q);
+  a.part = qkv_part;
+  a.part_ks = (int)part_ks;
+  a.q_bstride = static_cast<size_t>(gamma_q ? hq + hkv : hq) * D;
+  a.cache_bstride = static_cast<size_t>(cap) * hkv * D;
   a.gq = static_cast<const uint16_t*>(gamma_q);
   a.gk = static_cast<const uint16_t*>(gamma_k);
   a.eps_head = eps_head;
@@ -358,7 +424,7 @@ int tfa_decode_attention(const void* q, const void* gamma_q, const void* gamma_k
   a.sin_t = static_cast<const uint16_t*>(sin_t);
   a.mp_rows = (int)rope_rows;
   a.kc = static_cast<uint16_t*>(k_cache);
-  a.vc = static_cast<const uint16_t*>(v_cache);
+  a.vc = static_cast<uint16_t*>(v_cache);
   a.pos = pos;
   a.wr = wr;
   a.op = op;
@@ -371,25 +437,28 @@ int tfa_decode_attention(const void* q, const void* gamma_q, const void* gamma_k
   a.cap = (int)cap;
   a.ns = (int)(cap / split);
   a.scale = scale;
+  const int B = (int)batch;
   switch (hq / hkv) {
-    case 1: return launch_attn_g<1>(a, (int)split, stream);
-    case 2: return launch_attn_g<2>(a, (int)split, stream);
-    case 4: return launch_attn_g<4>(a, (int)split, stream);
-    case 8: return launch_attn_g<8>(a, (int)split, stream);
+    case 1: return launch_attn_g<1>(a, (int)split, B, stream);
+    case 2: return launch_attn_g<2>(a, (int)split, B, stream);
+    case 4: return launch_attn_g<4>(a, (int)split, B, stream);
+    case 8: return launch_attn_g<8>(a, (int)split, B, stream);
     default: return fail(TFA_ERR_SHAPE, "tfa_decode_attention: group %lld not in {1,2,4,8}", (long long)(hq / hkv));
   }
 }
 
 int tfa_attn_combine(const float* op, const float* mp, const float* lp, void* out, int64_t splits,
-                     int64_t hq, int64_t head_dim, const int* wr, int64_t split, hipStream_t stream) {
+                     int64_t batch, int64_t hq, int64_t head_dim, const int* wr, int64_t split,
+                     hipStream_t stream) {
   if (!op || !mp || !lp || !out) return fail(TFA_ERR_NULL, "tfa_attn_combine: null pointer argument");
-  if (splits <= 0 || hq <= 0 || head_dim <= 0) return fail(TFA_ERR_SHAPE, "tfa_attn_combine: empty shape");
+  if (splits <= 0 || hq <= 0 || head_dim <= 0 || batch <= 0) return fail(TFA_ERR_SHAPE, "tfa_attn_combine: empty shape");
   if (wr && split <= 0) return fail(TFA_ERR_SHAPE, "tfa_attn_combine: split must be positive with wr");
   if (head_dim > kCombMaxD) return fail(TFA_ERR_SHAPE, "tfa_attn_combine: head_dim %lld exceeds %d", (long long)head_dim, kCombMaxD);
   if (splits > kCombMaxSplits) return fail(TFA_ERR_SHAPE, "tfa_attn_combine: %lld splits exceed %d", (long long)splits, kCombMaxSplits);
-  attn_combine_kernel<<<(int)hq, kCombThreads, 0, stream>>>(op, mp, lp, static_cast<uint16_t*>(out),
-                                                   (int)splits, (int)hq, (int)head_dim, wr,
-                                                   (int)split);
+  const dim3 grid((unsigned)hq, (unsigned)batch);
+  attn_combine_kernel<<<grid, kCombThreads, 0, stream>>>(op, mp, lp, static_cast<uint16_t*>(out),
+                                                         (int)splits, (int)hq, (int)head_dim, wr,
+                                                         (int)split);
   return launched("attn_combine");
 }
 

@@ -1,0 +1,355 @@
+// Batched decode (up to 32 sequences, one token each): every projection is a
+// skinny GEMM Y[M, N] = X[M, K] . W[N, K]^T with M <= 32 on bf16 MFMA.
+//
+// skinny_gemm: a 256-thread block owns 32 weight rows (two 16-wide MFMA column
+// tiles) against all 32 token rows (two 16-high row tiles): four
+// v_mfma_f32_16x16x32_bf16 per k-step. K is split over the block's four waves
+// and, inside a wave, over the four 16-lane groups, so every lane walks a
+// contiguous run of its weight row and of its token row in 16-byte chunks. The
+// MFMA's k-slots only need A and B to agree on which k each lane supplies, so
+// this split is a relabelling of k, not a data movement. Optionally K is also
+// split over `ks` blocks, each writing f32 partials that the consumer reduces
+// (the narrow 2048-row projections then still fill every CU). Weights are
+// streamed once (non-temporal); activations are re-read from L2.
+// Lane layout of v_mfma_f32_16x16x32_bf16 (checked on the device):
+//   A[i = l%16][k = 8*(l/16) + j], B[k = 8*(l/16) + j][n = l%16],
+//   C[i = 4*(l/16) + r][n = l%16], j < 8, r < 4.
+//
+// Epilogues: f32 split-K partials | SwiGLU over interleaved gate/up rows |
+// logits + per-row-block best (value, lowest index) per token.
+//
+// rows_norm: per token row, either gather an embedding row or add the reduced
+// split-K partials to the residual stream, then RMSNorm (mode 0) -- the
+// producer-side norm that feeds the next GEMM.
+//
+// batch_sample: the greedy step for every sequence.
+//
+// Reference kernels replaced (batched form): examples/qwen3_1_7b-tilelang/fast/kernels.py
+// gemv :123-145, gemv_silu :210-257, lm_head :260-321, resid_rms_norm :82-116,
+// embed :579-588, sample_step :591-637.
+#include <float.h>
+
+#include "abi_util.h"
+#include "common.h"
+
+using namespace tfa;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kTileRows = 32;
+constexpr int kMaxTokens = 32;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+enum { SK_PARTIAL = 0, SK_SWIGLU = 1, SK_ARGMAX = 2 };
+
+struct SkinnyArgs {
+  const uint16_t* x;  // [M, K]
+  const uint16_t* w;  // [N, K]
+  int M, N, K, ks;
+  float* part;        // [ks, M, N]
+  uint16_t* act;      // [M, N/2]
+  float* logits;      // [M, N]
+  float* bv;          // [M, gridDim.x]
+  int* bi;            // [M, gridDim.x]
+};
+
+TFA_DEV bf16x8 as_bf8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+TFA_DEV bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+template <int U, int EPI>
+__global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs a) {
+  __shared__ f32x4 cbuf[kWaves][4][kWave];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  const int grp = lane >> 4;
+  const int r16 = lane & 15;
+  const int n0 = blockIdx.x * kTileRows;
+  const int K = a.K;
+  const int kb = K / a.ks;              // this block's K range
+  const int kl = kb / (kWaves * 4);     // this lane's contiguous K run
+  const int k0 = blockIdx.y * kb + wid * (kb / kWaves) + grp * kl;
+  const int nsteps = kl / 8;
+
+  const int row0 = n0 + r16, row1 = n0 + 16 + r16;
+  const int tok0 = r16, tok1 = 16 + r16;
+  const bool w0ok = row0 < a.N, w1ok = row1 < a.N;
+  const bool x0ok = tok0 < a.M, x1ok = tok1 < a.M;
+  const uint16_t* wp0 = a.w + static_cast<size_t>(w0ok ? row0 : 0) * K + k0;
+  const uint16_t* wp1 = a.w + static_cast<size_t>(w1ok ? row1 : 0) * K + k0;
+  const uint16_t* xp0 = a.x + static_cast<size_t>(x0ok ? tok0 : 0) * K + k0;
+  const uint16_t* xp1 = a.x + static_cast<size_t>(x1ok ? tok1 : 0) * K + k0;
+
+  f32x4 c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+
+  for (int s0 = 0; s0 < nsteps; s0 += U) {
+    uint4 wa[U], wb[U], xa[U], xb[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + u;
+      const bool in = s < nsteps;
+      wa[u] = (in && w0ok) ? ld16_stream(wp0 + 8 * s) : zero;
+      wb[u] = (in && w1ok) ? ld16_stream(wp1 + 8 * s) : zero;
+      xa[u] = (in && x0ok) ? ld16(xp0 + 8 * s) : zero;
+      xb[u] = (in && x1ok) ? ld16(xp1 + 8 * s) : zero;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // tile (token half, row half): A = tokens, B = weight rows
+      c[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xa[u]), as_bf8(wa[u]), c[0], 0, 0, 0);
+      c[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xa[u]), as_bf8(wb[u]), c[1], 0, 0, 0);
+      c[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xb[u]), as_bf8(wa[u]), c[2], 0, 0, 0);
+      c[3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xb[u]), as_bf8(wb[u]), c[3], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) cbuf[wid][i][lane] = c[i];
+  __syncthreads();
+  if (wid != 0) return;
+  // wave 0 holds the block's result: tile ti = 2*token_half + row_half; lane
+  // (grp, r16) holds tokens 16*th + 4*grp + r, weight row n0 + 16*rh + r16
+  float v[4][4];
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti) {
+    const f32x4 s = (cbuf[0][ti][lane] + cbuf[1][ti][lane]) + (cbuf[2][ti][lane] + cbuf[3][ti][lane]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[ti][r] = s[r];
+  }
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti) {
+    const int th = ti >> 1, rh = ti & 1;
+    const int n = n0 + 16 * rh + r16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 16 * th + 4 * grp + r;
+      const float val = v[ti][r];
+      if (EPI == SK_PARTIAL) {
+        if (m < a.M && n < a.N) a.part[(static_cast<size_t>(blockIdx.y) * a.M + m) * a.N + n] = val;
+      }
+      if (EPI == SK_SWIGLU) {
+        // rows (2i, 2i+1) = (gate_i, up_i) sit in lanes r16 and r16 ^ 1
+        const float other = __shfl_xor(val, 1, kWave);
+        if ((r16 & 1) == 0 && m < a.M && n + 1 < a.N) {
+          const float g = round_bf(val), u = round_bf(other);
+          const float act = round_bf(round_bf(g / (1.0f + expf(-g))) * u);
+          a.act[static_cast<size_t>(m) * (a.N / 2) + n / 2] = static_cast<uint16_t>(f2bf(act));
+        }
+      }
+      if (EPI == SK_ARGMAX) {
+        if (m < a.M && n < a.N) a.logits[static_cast<size_t>(m) * a.N + n] = val;
+      }
+    }
+  }
+  if (EPI == SK_ARGMAX) {
+    // per token: best over the block's 32 rows (16 lanes x 2 row halves)
+#pragma unroll
+    for (int th = 0; th < 2; ++th) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float bvv = -FLT_MAX;
+        int bii = 0x7fffffff;
+#pragma unroll
+        for (int rh = 0; rh < 2; ++rh) {
+          const int n = n0 + 16 * rh + r16;
+          const float val = v[2 * th + rh][r];
+          if (n < a.N && better(val, n, bvv, bii)) { bvv = val; bii = n; }
+        }
+#pragma unroll
+        for (int msk = 1; msk < 16; msk <<= 1) {
+          const float ov = __shfl_xor(bvv, msk, kWave);
+          const int oi = __shfl_xor(bii, msk, kWave);
+          if (better(ov, oi, bvv, bii)) { bvv = ov; bii = oi; }
+        }
+        const int m = 16 * th + 4 * grp + r;
+        if (r16 == 0 && m < a.M) {
+          a.bv[static_cast<size_t>(m) * gridDim.x + blockIdx.x] = bvv;
+          a.bi[static_cast<size_t>(m) * gridDim.x + blockIdx.x] = bii;
+        }
+      }
+    }
+  }
+}
+
+template <int EPI>
+int launch_skinny(const SkinnyArgs& a, hipStream_t st, const char* name) {
+  const dim3 grid((a.N + kTileRows - 1) / kTileRows, a.ks);
+  const int nsteps = a.K / a.ks / (kWaves * 4) / 8;
+  if (nsteps >= 8) skinny_gemm_kernel<8, EPI><<<grid, kThreads, 0, st>>>(a);
+  else skinny_gemm_kernel<4, EPI><<<grid, kThreads, 0, st>>>(a);
+  return launched(name);
+}
+
+// ---------------------------------------------------------------- rows_norm
+// Per token row m (one block of 256 threads): h = table[ids[m]] (embed mode)
+// or h = bf16(h_in[m] + bf16(sum_s part[s, m, :])) (residual mode); h_out[m] = h;
+// xn[m] = bf16(bf16(h * rsqrt(mean h^2 + eps)) * gamma).
+__global__ __launch_bounds__(kThreads) void rows_norm_kernel(
+    const uint16_t* __restrict__ table, const int64_t* __restrict__ ids, int64_t vocab,
+    const uint16_t* h_in, const float* __restrict__ part, int ks, uint16_t* h_out,
+    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ xn, int M, int H, float eps,
+    int* err) {
+  extern __shared__ float row[];
+  __shared__ float red[kWaves];
+  const int m = blockIdx.x;
+  const int t = threadIdx.x;
+  const uint16_t* src = nullptr;
+  if (table) {
+    int64_t id = ids[m];
+    if (id < 0 || id >= vocab) {
+      if (t == 0 && err) atomicExch(err, 1);
+      id = 0;
+    }
+    src = table + id * H;
+  }
+  float ss = 0.f;
+  for (int i = t; i < H; i += kThreads) {
+    float v;
+    if (table) {
+      v = bf2f(src[i]);
+    } else {
+      float acc = 0.f;
+      for (int s = 0; s < ks; ++s) acc += part[(static_cast<size_t>(s) * M + m) * H + i];
+      v = round_bf(bf2f(h_in[static_cast<size_t>(m) * H + i]) + round_bf(acc));
+    }
+    row[i] = v;
+    h_out[static_cast<size_t>(m) * H + i] = static_cast<uint16_t>(f2bf(v));
+    ss += v * v;
+  }
+  ss = block_sum(ss, red);
+  const float rs = rsqrt_rn(ss / static_cast<float>(H) + eps);
+  for (int i = t; i < H; i += kThreads)
+    xn[static_cast<size_t>(m) * H + i] =
+        static_cast<uint16_t>(f2bf(round_bf(round_bf(row[i] * rs) * bf2f(gamma[i]))));
+}
+
+// -------------------------------------------------------------- batch_sample
+__global__ __launch_bounds__(kThreads) void batch_sample_kernel(
+    const float* __restrict__ bv, const int* __restrict__ bi, int nb, const int* inp,
+    const int* plen, int64_t* ids, int* pos, int* sam, int nsteps, int* err) {
+  __shared__ float rv[kThreads];
+  __shared__ int ri[kThreads];
+  const int b = blockIdx.x;
+  const int t = threadIdx.x;
+  float bvv = -FLT_MAX;
+  int bii = 0x7fffffff;
+  for (int j = t; j < nb; j += kThreads) {
+    const float v = bv[static_cast<size_t>(b) * nb + j];
+    const int i = bi[static_cast<size_t>(b) * nb + j];
+    if (better(v, i, bvv, bii)) { bvv = v; bii = i; }
+  }
+  rv[t] = bvv;
+  ri[t] = bii;
+  __syncthreads();
+  for (int s = kThreads / 2; s > 0; s >>= 1) {
+    if (t < s && better(rv[t + s], ri[t + s], rv[t], ri[t])) {
+      rv[t] = rv[t + s];
+      ri[t] = ri[t + s];
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    const int best = ri[0];
+    const int p = pos[b];
+    if (p < 0 || p >= nsteps) {
+      if (err) atomicExch(err, 2);
+    } else {
+      sam[static_cast<size_t>(b) * nsteps + p] = best;
+      const bool prompt = (p + 1 < plen[b]) && (p + 1 < nsteps);
+      ids[b] = prompt ? static_cast<int64_t>(inp[static_cast<size_t>(b) * nsteps + p + 1])
+                      : static_cast<int64_t>(best);
+      pos[b] = p + 1;
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t tfa_skinny_blocks(int64_t n) { return (n + kTileRows - 1) / kTileRows; }
+
+int tfa_skinny_gemm(const void* x, const void* w, int64_t m, int64_t n, int64_t k, int64_t ks,
+                    int epilogue, float* part, void* act, float* logits, float* block_val,
+                    int* block_idx, hipStream_t stream) {
+  TFA_NONNULL(x);
+  TFA_NONNULL(w);
+  TFA_REQUIRE(m >= 1 && m <= kMaxTokens, TFA_ERR_SHAPE, "tfa_skinny_gemm: m=%lld not in [1, 32]", (long long)m);
+  TFA_REQUIRE(n >= 1, TFA_ERR_SHAPE, "tfa_skinny_gemm: n=%lld must be positive", (long long)n);
+  TFA_REQUIRE(ks >= 1 && k % (128 * ks) == 0, TFA_ERR_SHAPE,
+              "tfa_skinny_gemm: k=%lld must be a multiple of 128*ks (ks=%lld)", (long long)k, (long long)ks);
+  TFA_ALIGN16(x);
+  TFA_ALIGN16(w);
+  SkinnyArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = static_cast<const uint16_t*>(w);
+  a.M = (int)m;
+  a.N = (int)n;
+  a.K = (int)k;
+  a.ks = (int)ks;
+  switch (epilogue) {
+    case 0:
+      TFA_NONNULL(part);
+      a.part = part;
+      return launch_skinny<SK_PARTIAL>(a, stream, "skinny_gemm_partial");
+    case 1:
+      TFA_NONNULL(act);
+      TFA_REQUIRE(ks == 1 && n % 2 == 0, TFA_ERR_SHAPE, "tfa_skinny_gemm: swiglu needs ks=1 and even n");
+      a.act = static_cast<uint16_t*>(act);
+      return launch_skinny<SK_SWIGLU>(a, stream, "skinny_gemm_swiglu");
+    case 2:
+      TFA_NONNULL(logits);
+      TFA_NONNULL(block_val);
+      TFA_NONNULL(block_idx);
+      TFA_REQUIRE(ks == 1, TFA_ERR_SHAPE, "tfa_skinny_gemm: argmax needs ks=1");
+      a.logits = logits;
+      a.bv = block_val;
+      a.bi = block_idx;
+      return launch_skinny<SK_ARGMAX>(a, stream, "skinny_gemm_argmax");
+    default:
+      return fail(TFA_ERR_ARG, "tfa_skinny_gemm: epilogue %d not in {0, 1, 2}", epilogue);
+  }
+}
+
+int tfa_rows_norm(const void* table, const int64_t* ids, int64_t vocab, const void* h_in,
+                  const float* part, int64_t ks, void* h_out, const void* gamma, void* xn,
+                  int64_t m, int64_t hidden, float eps, int* err, hipStream_t stream) {
+  TFA_NONNULL(h_out);
+  TFA_NONNULL(gamma);
+  TFA_NONNULL(xn);
+  TFA_REQUIRE(m >= 0 && hidden > 0 && hidden <= 16384, TFA_ERR_SHAPE, "tfa_rows_norm: bad shape (%lld, %lld)", (long long)m, (long long)hidden);
+  if (table) {
+    TFA_NONNULL(ids);
+    TFA_REQUIRE(vocab > 0, TFA_ERR_SHAPE, "tfa_rows_norm: empty table");
+  } else {
+    TFA_NONNULL(h_in);
+    TFA_NONNULL(part);
+    TFA_REQUIRE(ks >= 1, TFA_ERR_SHAPE, "tfa_rows_norm: ks must be >= 1");
+  }
+  if (m == 0) return TFA_OK;
+  rows_norm_kernel<<<(int)m, kThreads, hidden * sizeof(float), stream>>>(
+      static_cast<const uint16_t*>(table), ids, vocab, static_cast<const uint16_t*>(h_in), part,
+      (int)ks, static_cast<uint16_t*>(h_out), static_cast<const uint16_t*>(gamma),
+      static_cast<uint16_t*>(xn), (int)m, (int)hidden, eps, err);
+  return launched("rows_norm");
+}
+
+int tfa_batch_sample_step(const float* block_val, const int* block_idx, int64_t nblocks,
+                          int64_t batch, const int* inp, const int* prompt_len, int64_t* ids,
+                          int* pos, int* sam, int64_t nsteps, int* err, hipStream_t stream) {
+  if (!block_val || !block_idx || !inp || !prompt_len || !ids || !pos || !sam)
+    return fail(TFA_ERR_NULL, "tfa_batch_sample_step: null pointer argument");
+  TFA_REQUIRE(nblocks > 0 && batch > 0 && nsteps > 0, TFA_ERR_SHAPE, "tfa_batch_sample_step: empty shape");
+  batch_sample_kernel<<<(int)batch, kThreads, 0, stream>>>(block_val, block_idx, (int)nblocks, inp,
+                                                           prompt_len, ids, pos, sam, (int)nsteps, err);
+  return launched("batch_sample_step");
+}
+
+}  // extern "C"

@@ -226,14 +226,27 @@ void decode_qkv(const OptT& h, const OptT& table, const OptT& ids, const OptT& h
                               stream_of(gamma_in)));
 }
 
-void decode_attention(const Tensor& q, const OptT& gamma_q, const OptT& gamma_k, double eps_head,
-                      const OptT& cos_t, const OptT& sin_t, const Tensor& k_cache,
-                      const Tensor& v_cache, const OptT& pos, const Tensor& wr, int64_t hq,
-                      int64_t hkv, int64_t split, double scale, const Tensor& op, const Tensor& mp,
-                      const Tensor& lp, bool neutral, const OptT& err) {
+void decode_attention(const OptT& q, const OptT& qkv_part, const OptT& gamma_q,
+                      const OptT& gamma_k, double eps_head, const OptT& cos_t, const OptT& sin_t,
+                      const Tensor& k_cache, const Tensor& v_cache, const OptT& pos,
+                      const Tensor& wr, int64_t hq, int64_t hkv, int64_t split, double scale,
+                      const Tensor& op, const Tensor& mp, const Tensor& lp, bool neutral,
+                      const OptT& err) {
   const int64_t D = 128;
   const bool fused = gamma_q.has_value();
-  need(q, "q", BF, (fused ? hq + hkv : hq) * D);
+  need(wr, "wr", I32);
+  const int64_t B = wr.numel();
+  int64_t ks = 0;
+  if (qkv_part) {
+    if (!fused) bad("qkv_part needs the fused-mode operands");
+    need(*qkv_part, "qkv_part", F32);
+    const int64_t per = B * (hq + 2 * hkv) * D;
+    if (qkv_part->numel() % per != 0) bad("qkv_part: expected (ks, batch, (hq+2hkv)*128)");
+    ks = qkv_part->numel() / per;
+  } else {
+    if (!q) bad("q required");
+    need(*q, "q", BF, B * (fused ? hq + hkv : hq) * D);
+  }
   int64_t rope_rows = 0;
   if (fused) {
     if (!gamma_k || !cos_t || !sin_t || !pos) bad("fused mode needs gamma_k, cos, sin and pos");
@@ -243,41 +256,120 @@ void decode_attention(const Tensor& q, const OptT& gamma_q, const OptT& gamma_k,
     need(*sin_t, "sin", BF, cos_t->numel());
     if (cos_t->dim() != 2 || cos_t->size(1) != D) bad("cos: expected (rows, 128)");
     rope_rows = cos_t->size(0);
-    need(*pos, "pos", I32, 1);
+    need(*pos, "pos", I32, B);
   }
   need(k_cache, "k_cache", BF);
   need(v_cache, "v_cache", BF, k_cache.numel());
-  if (k_cache.numel() % (hkv * D) != 0) bad("k_cache: size is not a multiple of hkv*128");
-  const int64_t cap = k_cache.numel() / (hkv * D);
+  if (k_cache.numel() % (B * hkv * D) != 0) bad("k_cache: size is not a multiple of batch*hkv*128");
+  const int64_t cap = k_cache.numel() / (B * hkv * D);
   if (split <= 0 || cap % split != 0) bad("cache capacity must be a multiple of the split");
   const int64_t ns = cap / split;
-  need(wr, "wr", I32, 1);
-  need(op, "op", F32, ns * hq * D);
-  need(mp, "mp", F32, ns * hq);
-  need(lp, "lp", F32, ns * hq);
+  need(op, "op", F32, B * ns * hq * D);
+  need(mp, "mp", F32, B * ns * hq);
+  need(lp, "lp", F32, B * ns * hq);
   if (err) need(*err, "err", I32, 1);
   raise_status(tfa_decode_attention(
-      q.data_ptr(), opt_ptr(gamma_q), opt_ptr(gamma_k), (float)eps_head, opt_ptr(cos_t),
-      opt_ptr(sin_t), rope_rows, k_cache.data_ptr(), v_cache.data_ptr(), opt_ptr_t<const int>(pos),
-      wr.data_ptr<int>(), hq, hkv, D, cap, split, (float)scale, op.data_ptr<float>(),
-      mp.data_ptr<float>(), lp.data_ptr<float>(), neutral ? 1 : 0, opt_ptr_t<int>(err),
-      stream_of(q)));
+      opt_ptr(q), opt_ptr_t<const float>(qkv_part), ks, opt_ptr(gamma_q), opt_ptr(gamma_k),
+      (float)eps_head, opt_ptr(cos_t), opt_ptr(sin_t), rope_rows, k_cache.data_ptr(),
+      v_cache.data_ptr(), opt_ptr_t<const int>(pos), wr.data_ptr<int>(), B, hq, hkv, D, cap, split,
+      (float)scale, op.data_ptr<float>(), mp.data_ptr<float>(), lp.data_ptr<float>(),
+      neutral ? 1 : 0, opt_ptr_t<int>(err), stream_of(k_cache)));
 }
 
 void attn_combine(const Tensor& op, const Tensor& mp, const Tensor& lp, const Tensor& out,
                   const OptT& wr, int64_t split) {
   need(mp, "Mp", F32);
-  if (mp.dim() != 2) bad("Mp: expected (NS, HQ)");
-  const int64_t ns = mp.size(0), hq = mp.size(1);
-  need(lp, "Lp", F32, ns * hq);
+  if (mp.dim() != 2 && mp.dim() != 3) bad("Mp: expected ([batch,] NS, HQ)");
+  const int64_t B = mp.dim() == 3 ? mp.size(0) : 1;
+  const int64_t ns = mp.size(-2), hq = mp.size(-1);
+  need(lp, "Lp", F32, B * ns * hq);
   need(op, "Op", F32);
-  if (op.numel() % (ns * hq) != 0) bad("Op: expected (NS, HQ, D)");
-  const int64_t D = op.numel() / (ns * hq);
-  need(out, "O", BF, hq * D);
-  if (wr) need(*wr, "wr", I32, 1);
+  if (op.numel() % (B * ns * hq) != 0) bad("Op: expected ([batch,] NS, HQ, D)");
+  const int64_t D = op.numel() / (B * ns * hq);
+  need(out, "O", BF, B * hq * D);
+  if (wr) need(*wr, "wr", I32, B);
   raise_status(tfa_attn_combine(op.data_ptr<float>(), mp.data_ptr<float>(), lp.data_ptr<float>(),
-                                out.data_ptr(), ns, hq, D, opt_ptr_t<const int>(wr), split,
+                                out.data_ptr(), ns, B, hq, D, opt_ptr_t<const int>(wr), split,
                                 stream_of(op)));
+}
+
+// ---------------------------------------------------------- batched decode
+void skinny_gemm(const Tensor& x, const Tensor& w, int64_t ks, int64_t epilogue, const OptT& part,
+                 const OptT& act, const OptT& logits, const OptT& block_val,
+                 const OptT& block_idx) {
+  need(x, "x", BF);
+  if (x.dim() != 2) bad("x: expected (m, k)");
+  const int64_t M = x.size(0), K = x.size(1);
+  if (w.dim() != 2) bad("w: expected (n, k)");
+  const int64_t N = w.size(0);
+  need_mat(w, "w", N, K);
+  if (epilogue == 0) {
+    if (!part) bad("partial epilogue needs part");
+    need(*part, "part", F32, ks * M * N);
+  } else if (epilogue == 1) {
+    if (!act) bad("swiglu epilogue needs act");
+    need(*act, "act", BF, M * (N / 2));
+  } else if (epilogue == 2) {
+    if (!logits || !block_val || !block_idx) bad("argmax epilogue needs logits, block_val, block_idx");
+    need(*logits, "logits", F32, M * N);
+    const int64_t nb = tfa_skinny_blocks(N);
+    need(*block_val, "block_val", F32, M * nb);
+    need(*block_idx, "block_idx", I32, M * nb);
+  }
+  raise_status(tfa_skinny_gemm(x.data_ptr(), w.data_ptr(), M, N, K, ks, (int)epilogue,
+                               opt_ptr_t<float>(part), opt_ptr_t<void>(act), opt_ptr_t<float>(logits),
+                               opt_ptr_t<float>(block_val), opt_ptr_t<int>(block_idx),
+                               stream_of(x)));
+}
+
+void rows_norm(const OptT& table, const OptT& ids, const OptT& h_in, const OptT& part,
+               const Tensor& h_out, const Tensor& gamma, const Tensor& xn, double eps,
+               const OptT& err) {
+  need(h_out, "h_out", BF);
+  if (h_out.dim() != 2) bad("h_out: expected (m, hidden)");
+  const int64_t M = h_out.size(0), H = h_out.size(1);
+  need(gamma, "gamma", BF, H);
+  need(xn, "xn", BF, M * H);
+  int64_t vocab = 0, ks = 0;
+  if (table) {
+    need(*table, "table", BF);
+    if (table->dim() != 2 || table->size(1) != H) bad("table: expected (V, hidden)");
+    vocab = table->size(0);
+    if (!ids) bad("embed mode needs ids");
+    need(*ids, "ids", I64, M);
+  } else {
+    if (!h_in || !part) bad("residual mode needs h_in and part");
+    need(*h_in, "h_in", BF, M * H);
+    need(*part, "part", F32);
+    if (part->numel() % (M * H) != 0) bad("part: expected (ks, m, hidden)");
+    ks = part->numel() / (M * H);
+  }
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_rows_norm(opt_ptr(table), opt_ptr_t<const int64_t>(ids), vocab, opt_ptr(h_in),
+                             opt_ptr_t<const float>(part), ks, h_out.data_ptr(), gamma.data_ptr(),
+                             xn.data_ptr(), M, H, (float)eps, opt_ptr_t<int>(err), stream_of(h_out)));
+}
+
+void batch_sample_step(const Tensor& block_val, const Tensor& block_idx, const Tensor& inp,
+                       const Tensor& prompt_len, const Tensor& ids, const Tensor& pos,
+                       const Tensor& sam, const OptT& err) {
+  need(pos, "pos", I32);
+  const int64_t B = pos.numel();
+  need(block_val, "block_val", F32);
+  if (block_val.numel() % B != 0) bad("block_val: expected (batch, nblocks)");
+  const int64_t nb = block_val.numel() / B;
+  need(block_idx, "block_idx", I32, B * nb);
+  need(inp, "inp", I32);
+  if (inp.numel() % B != 0) bad("inp: expected (batch, nsteps)");
+  const int64_t nsteps = inp.numel() / B;
+  need(sam, "sam", I32, B * nsteps);
+  need(prompt_len, "prompt_len", I32, B);
+  need(ids, "ids", I64, B);
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_batch_sample_step(block_val.data_ptr<float>(), block_idx.data_ptr<int>(), nb, B,
+                                     inp.data_ptr<int>(), prompt_len.data_ptr<int>(),
+                                     ids.data_ptr<int64_t>(), pos.data_ptr<int>(), sam.data_ptr<int>(),
+                                     nsteps, opt_ptr_t<int>(err), stream_of(pos)));
 }
 
 void copy_stream(const Tensor& src, const Tensor& dst) {
@@ -307,4 +399,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode_attention", &decode_attention);
   m.def("attn_combine", &attn_combine);
   m.def("copy_stream", &copy_stream);
+  m.def("skinny_blocks", [](int64_t n) { return tfa_skinny_blocks(n); });
+  m.def("skinny_gemm", &skinny_gemm);
+  m.def("rows_norm", &rows_norm);
+  m.def("batch_sample_step", &batch_sample_step);
 }

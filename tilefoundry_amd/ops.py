@@ -167,14 +167,14 @@ def attn_partial(q, k_cache, v_cache, wr, hq: int, hkv: int, split: int = 256,
     scale = 128 ** -0.5 if scale is None else scale
     op, mp, lp = partials if partials is not None else _attn_bufs(q, k_cache, hq, hkv, split)
     if rope is None:
-        C.decode_attention(q, None, None, 0.0, None, None, k_cache, v_cache, None,
+        C.decode_attention(q, None, None, None, 0.0, None, None, k_cache, v_cache, None,
                            _dev_i32(wr, dev), hq, hkv, split, float(scale), op, mp, lp,
                            bool(neutral), err)
     else:
         gq, gk, eps, cos, sin, pos = rope
-        C.decode_attention(q, gq, gk, float(eps), cos, sin, k_cache, v_cache, _dev_i32(pos, dev),
-                           _dev_i32(wr, dev), hq, hkv, split, float(scale), op, mp, lp,
-                           bool(neutral), err)
+        C.decode_attention(q, None, gq, gk, float(eps), cos, sin, k_cache, v_cache,
+                           _dev_i32(pos, dev), _dev_i32(wr, dev), hq, hkv, split, float(scale),
+                           op, mp, lp, bool(neutral), err)
     return op, mp, lp
 
 
@@ -194,3 +194,41 @@ def decode_attention(q, k_cache, v_cache, wr, hq: int, hkv: int, split: int = 64
     op, mp, lp = attn_partial(q, k_cache, v_cache, wr, hq, hkv, split, scale, partials, rope,
                               neutral=False, err=err)
     return attn_combine(op, mp, lp, out, wr=wr, split=split)
+
+
+# ------------------------------------------------------- batched (<= 32 rows)
+
+def skinny_gemm(x, w, epilogue: str = "partial", ks: int = 1, part=None, act=None, logits=None,
+                block_val=None, block_idx=None):
+    """``X[m, k] @ W[n, k]^T`` for m <= 32 on bf16 MFMA. ``epilogue``:
+    ``"partial"`` -> f32 ``[ks, m, n]`` (sum over ks is the product);
+    ``"swiglu"`` -> bf16 ``[m, n/2]`` over interleaved gate/up rows;
+    ``"argmax"`` -> ``(logits [m, n] f32, block_val, block_idx)``."""
+    m, n = x.shape[0], w.shape[0]
+    if epilogue == "partial":
+        part = _out(part, x, (ks, m, n), torch.float32)
+        C.skinny_gemm(x, w, ks, 0, part, None, None, None, None)
+        return part
+    if epilogue == "swiglu":
+        act = _out(act, x, (m, n // 2), BF16)
+        C.skinny_gemm(x, w, 1, 1, None, act, None, None, None)
+        return act
+    nb = C.skinny_blocks(n)
+    logits = _out(logits, x, (m, n), torch.float32)
+    block_val = _out(block_val, x, (m, nb), torch.float32)
+    block_idx = _out(block_idx, x, (m, nb), torch.int32)
+    C.skinny_gemm(x, w, 1, 2, None, None, logits, block_val, block_idx)
+    return logits, block_val, block_idx
+
+
+def rows_norm(gamma, eps: float, *, table=None, ids=None, h_in=None, part=None, h_out=None,
+              xn=None, err=None):
+    """Embed-and-norm (``table``, ``ids``) or reduce-partials + residual + norm
+    (``h_in``, ``part [ks, m, H]``) for every token row; returns ``(h, xn)``."""
+    like = h_in if h_in is not None else gamma
+    m = ids.numel() if table is not None else h_in.shape[0]
+    H = gamma.numel()
+    h_out = _out(h_out, like, (m, H), BF16)
+    xn = _out(xn, like, (m, H), BF16)
+    C.rows_norm(table, ids, h_in, part, h_out, gamma, xn, float(eps), err)
+    return h_out, xn

@@ -126,6 +126,35 @@ def rope_tables(n: int, head_dim: int, theta: float, device):
     return ph.cos().to(BF16).to(device), ph.sin().to(BF16).to(device)
 
 
+def pack_weights(cfg: Qwen3Config, wts: dict, dev):
+    """The decode layout of a checkpoint-named weight dict: ``q|k|v`` stacked,
+    ``gate``/``up`` rows interleaved (row 2i = gate_i, 2i+1 = up_i, so one tile
+    holds both halves of every pair), everything else as stored; the embedding
+    table doubles as the tied head. Returns ``(embed, gamma_final, layers)``."""
+
+    def get(name):
+        return wts[name].to(dev, BF16).contiguous()
+
+    embed = get("model.embed_tokens.weight")
+    gamma_final = get("model.norm.weight")
+    layers = []
+    for i in range(cfg.layers):
+        n = hf_names(i)
+        gate, up = get(n["w_gate"]), get(n["w_up"])
+        layers.append({
+            "gamma_in": get(n["gamma_in"]),
+            "w_qkv": torch.cat([get(n["w_q"]), get(n["w_k"]), get(n["w_v"])], 0).contiguous(),
+            "gamma_q": get(n["gamma_q"]),
+            "gamma_k": get(n["gamma_k"]),
+            "w_o": get(n["w_o"]),
+            "gamma_post": get(n["gamma_post"]),
+            "w_gu": torch.stack([gate, up], 1).reshape(2 * cfg.inter, cfg.hidden).contiguous(),
+            "w_down": get(n["w_down"]),
+        })
+        del gate, up
+    return embed, gamma_final, layers
+
+
 @dataclass(frozen=True)
 class Generated:
     """A continuation and the timing of the part that produced it
@@ -171,30 +200,9 @@ class Engine:
 
     # ---------------------------------------------------------------- weights
     def _pack(self, wts):
-        cfg, dev = self.cfg, self.device
-
-        def get(name):
-            return wts[name].to(dev, BF16).contiguous()
-
-        self.embed = get("model.embed_tokens.weight")
-        self.gamma_final = get("model.norm.weight")
-        self.layers = []
-        for i in range(cfg.layers):
-            n = hf_names(i)
-            gate, up = get(n["w_gate"]), get(n["w_up"])
-            self.layers.append({
-                "gamma_in": get(n["gamma_in"]),
-                "w_qkv": torch.cat([get(n["w_q"]), get(n["w_k"]), get(n["w_v"])], 0).contiguous(),
-                "gamma_q": get(n["gamma_q"]),
-                "gamma_k": get(n["gamma_k"]),
-                "w_o": get(n["w_o"]),
-                "gamma_post": get(n["gamma_post"]),
-                # rows (2i, 2i+1) = (gate_i, up_i): one block sees both halves of a pair
-                "w_gu": torch.stack([gate, up], 1).reshape(2 * cfg.inter, cfg.hidden).contiguous(),
-                "w_down": get(n["w_down"]),
-            })
-            del gate, up
-        self.cos, self.sin = rope_tables(self.cap, cfg.head_dim, cfg.rope_theta, dev)
+        self.embed, self.gamma_final, self.layers = pack_weights(self.cfg, wts, self.device)
+        self.cos, self.sin = rope_tables(self.cap, self.cfg.head_dim, self.cfg.rope_theta,
+                                         self.device)
 
     # ---------------------------------------------------------------- buffers
     def _buffers(self):
@@ -238,9 +246,9 @@ class Engine:
             else:
                 C.decode_qkv(self.hid, None, None, None, w["gamma_in"], cfg.eps, w["w_qkv"], n_qk,
                              self.qk, self.pos, vc, self.err)
-            C.decode_attention(self.qk, w["gamma_q"], w["gamma_k"], cfg.eps, self.cos, self.sin,
-                               kc, vc, self.pos, self.pos, HQ, HKV, self.split, cfg.scale,
-                               self.op, self.mp, self.lp, False, self.err)
+            C.decode_attention(self.qk, None, w["gamma_q"], w["gamma_k"], cfg.eps, self.cos,
+                               self.sin, kc, vc, self.pos, self.pos, HQ, HKV, self.split,
+                               cfg.scale, self.op, self.mp, self.lp, False, self.err)
             C.attn_combine(self.op, self.mp, self.lp, self.attn, self.pos, self.split)
             C.gemv_residual(self.attn, w["w_o"], self.hid, None, self.h1)
             C.rmsnorm_gemv_swiglu(self.h1, w["gamma_post"], cfg.eps, w["w_gu"], self.act)
@@ -253,7 +261,7 @@ class Engine:
     def _capture(self):
         side = torch.cuda.Stream(device=self.device)
         side.wait_stream(torch.cuda.current_stream(self.device))
-        self._load([0], 1)
+        self._load(*self._capture_inputs())
         with torch.cuda.stream(side):
             self._step()  # one eager step: every kernel has run once before capture
         torch.cuda.current_stream(self.device).wait_stream(side)
@@ -262,6 +270,9 @@ class Engine:
         with torch.cuda.graph(self.graph):
             self._step()
         self._reset()
+
+    def _capture_inputs(self):
+        return [0], 1
 
     def _run_step(self):
         if self.graph is not None:
@@ -342,6 +353,170 @@ class Engine:
         """The f32 logits after consuming every token of ``prompt_ids``."""
         self._load(list(prompt_ids), len(prompt_ids))
         for _ in range(len(prompt_ids)):
+            self._run_step()
+        torch.cuda.synchronize(self.device)
+        self.check_device_errors()
+        return self.logits.clone()
+
+
+class BatchEngine:
+    """Up to 32 sequences decoded in lockstep, one captured step over all of them.
+
+    Every projection is a skinny bf16-MFMA GEMM over the batch (the weights are
+    streamed once per step for all sequences); each sequence has its own KV
+    cache, position and prompt. One step is 8 launches per layer plus 3:
+
+        rows_norm        embedding gather + input norm (once)
+        skinny_gemm      q|k|v projection -> f32 split-K partials
+        decode_attention sums the partials, q/k head norm + RoPE, writes the new
+                         K and V rows, split-KV attention per sequence
+        attn_combine     merge of the splits
+        skinny_gemm      o_proj -> split-K partials
+        rows_norm        residual add + post-attention norm
+        skinny_gemm      gate|up + SwiGLU
+        skinny_gemm      down_proj -> split-K partials
+        rows_norm        residual add + next input norm (final norm after the last layer)
+        skinny_gemm      head -> logits + per-block winners per sequence
+        batch_sample     greedy step per sequence
+    """
+
+    MAX_BATCH = 32
+
+    def __init__(self, cfg: Qwen3Config = QWEN3_1_7B, *, batch: int = 32, device="cuda:0",
+                 max_new: int = 2048, prompt_room: int = 512, weights: dict | None = None,
+                 seed: int = 0, split: int = 64, ks_qkv: int = 2, ks_o: int = 4, ks_down: int = 4,
+                 capture: bool = True):
+        if not 1 <= batch <= self.MAX_BATCH:
+            raise ValueError(f"batch {batch} not in [1, {self.MAX_BATCH}]")
+        self.cfg = cfg
+        self.batch = batch
+        self.device = torch.device(device)
+        self.split = split
+        self.ks = {"qkv": ks_qkv, "o": ks_o, "down": ks_down}
+        self.nsteps = max_new + prompt_room
+        self.cap = ((self.nsteps + split - 1) // split) * split
+        self.ns = self.cap // split
+        if weights is None:
+            weights = synthetic_weights(cfg, seed, self.device)
+        self.embed, self.gamma_final, self.layers = pack_weights(cfg, weights, self.device)
+        del weights
+        self.cos, self.sin = rope_tables(self.cap, cfg.head_dim, cfg.rope_theta, self.device)
+        self._buffers()
+        self.graph = None
+        if capture:
+            self._capture()
+
+    def _buffers(self):
+        cfg, dev, B = self.cfg, self.device, self.batch
+        H, HQ, HKV, D, I = cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.inter
+
+        def z(*shape, dtype=BF16):
+            return torch.zeros(*shape, device=dev, dtype=dtype)
+
+        f32 = torch.float32
+        self.h = z(B, H)
+        self.h1 = z(B, H)
+        self.xn = z(B, H)
+        self.act = z(B, I)
+        self.attn = z(B, HQ * D)
+        self.qkv_part = z(self.ks["qkv"], B, cfg.qkv_rows, dtype=f32)
+        self.o_part = z(self.ks["o"], B, H, dtype=f32)
+        self.d_part = z(self.ks["down"], B, H, dtype=f32)
+        self.op = z(B, self.ns, HQ, D, dtype=f32)
+        self.mp = z(B, self.ns, HQ, dtype=f32)
+        self.lp = z(B, self.ns, HQ, dtype=f32)
+        self.kc = z(cfg.layers, B, self.cap, HKV * D)
+        self.vc = z(cfg.layers, B, self.cap, HKV * D)
+        self.logits = z(B, cfg.vocab, dtype=f32)
+        nb = C.skinny_blocks(cfg.vocab)
+        self.bv = z(B, nb, dtype=f32)
+        self.bi = z(B, nb, dtype=torch.int32)
+        self.pos = z(B, dtype=torch.int32)
+        self.ids = z(B, dtype=torch.int64)
+        self.inp = z(B, self.nsteps, dtype=torch.int32)
+        self.sam = z(B, self.nsteps, dtype=torch.int32)
+        self.plen = z(B, dtype=torch.int32)
+        self.err = z(1, dtype=torch.int32)
+
+    def _step(self):
+        cfg = self.cfg
+        HQ, HKV = cfg.heads, cfg.kv_heads
+        L = len(self.layers)
+        C.rows_norm(self.embed, self.ids, None, None, self.h, self.layers[0]["gamma_in"], self.xn,
+                    cfg.eps, self.err)
+        for i, w in enumerate(self.layers):
+            C.skinny_gemm(self.xn, w["w_qkv"], self.ks["qkv"], 0, self.qkv_part, None, None, None,
+                          None)
+            C.decode_attention(None, self.qkv_part, w["gamma_q"], w["gamma_k"], cfg.eps, self.cos,
+                               self.sin, self.kc[i], self.vc[i], self.pos, self.pos, HQ, HKV,
+                               self.split, cfg.scale, self.op, self.mp, self.lp, False, self.err)
+            C.attn_combine(self.op, self.mp, self.lp, self.attn, self.pos, self.split)
+            C.skinny_gemm(self.attn, w["w_o"], self.ks["o"], 0, self.o_part, None, None, None, None)
+            C.rows_norm(None, None, self.h, self.o_part, self.h1, w["gamma_post"], self.xn, cfg.eps,
+                        self.err)
+            C.skinny_gemm(self.xn, w["w_gu"], 1, 1, None, self.act, None, None, None)
+            C.skinny_gemm(self.act, w["w_down"], self.ks["down"], 0, self.d_part, None, None, None,
+                          None)
+            nxt = self.layers[i + 1]["gamma_in"] if i + 1 < L else self.gamma_final
+            C.rows_norm(None, None, self.h1, self.d_part, self.h, nxt, self.xn, cfg.eps, self.err)
+        C.skinny_gemm(self.xn, self.embed, 1, 2, None, None, self.logits, self.bv, self.bi)
+        C.batch_sample_step(self.bv, self.bi, self.inp, self.plen, self.ids, self.pos, self.sam,
+                            self.err)
+
+    _capture = Engine._capture
+    _run_step = Engine._run_step
+
+    def _capture_inputs(self):
+        return [[0]] * self.batch, 1
+    check_device_errors = Engine.check_device_errors
+
+    def _reset(self):
+        self.pos.zero_()
+        self.sam.zero_()
+        self.err.zero_()
+
+    def _load(self, rows: list[list[int]], plen: int):
+        if len(rows) != self.batch:
+            raise ValueError(f"{len(rows)} sequences given to an engine of batch {self.batch}")
+        if any(len(r) != len(rows[0]) for r in rows):
+            raise ValueError("sequences of one batch advance in lockstep: give equal lengths")
+        if len(rows[0]) > self.nsteps:
+            raise ValueError(f"{len(rows[0])} input ids exceed this engine's {self.nsteps} steps")
+        if any(not 0 <= t < self.cfg.vocab for r in rows for t in r):
+            raise ValueError(f"token ids out of range [0, {self.cfg.vocab})")
+        self._reset()
+        self.inp.zero_()
+        self.inp[:, : len(rows[0])] = torch.tensor(rows, dtype=torch.int32, device=self.device)
+        self.plen.fill_(plen)
+        self.ids.copy_(torch.tensor([r[0] for r in rows], dtype=torch.int64, device=self.device))
+
+    def generate(self, prompts: list[list[int]], max_new: int) -> Generated:
+        """Walk every prompt, then continue each for ``max_new`` tokens; timing
+        covers the continuation steps only (all sequences together)."""
+        if not prompts or not prompts[0]:
+            raise ValueError("decode needs prompts of at least one token")
+        pl = len(prompts[0])
+        if pl + max_new > self.nsteps:
+            raise ValueError(f"prompt {pl} + {max_new} new exceeds this engine's {self.nsteps} steps")
+        self._load([list(p) for p in prompts], pl)
+        torch.cuda.synchronize(self.device)
+        t0 = perf_counter()
+        for _ in range(pl - 1):
+            self._run_step()
+        torch.cuda.synchronize(self.device)
+        t1 = perf_counter()
+        for _ in range(max_new):
+            self._run_step()
+        torch.cuda.synchronize(self.device)
+        t2 = perf_counter()
+        self.check_device_errors()
+        out = self.sam[:, pl - 1: pl - 1 + max_new].tolist()
+        return Generated(out, t2 - t1, t1 - t0, pl)
+
+    def logits_for(self, prompts: list[list[int]]) -> torch.Tensor:
+        """f32 logits [batch, vocab] after consuming every token of each prompt."""
+        self._load([list(p) for p in prompts], len(prompts[0]))
+        for _ in range(len(prompts[0])):
             self._run_step()
         torch.cuda.synchronize(self.device)
         self.check_device_errors()
