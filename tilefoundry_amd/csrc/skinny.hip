@@ -9,8 +9,11 @@
 // MFMA's k-slots only need A and B to agree on which k each lane supplies, so
 // this split is a relabelling of k, not a data movement. Optionally K is also
 // split over `ks` blocks, each writing f32 partials that the consumer reduces
-// (the narrow 2048-row projections then still fill every CU). Weights are
-// streamed once (non-temporal); activations are re-read from L2.
+// (the narrow 2048-row projections then still fill every CU). A lane's 16-byte
+// steps along its row are consecutive, so the weight loads are ordinary cached
+// loads: the first brings the line in and the next steps hit it (non-temporal
+// loads would refetch the line for every 16 bytes -- each instruction of a wave
+// touches 32 different rows). Activations are re-read from L2.
 // Lane layout of v_mfma_f32_16x16x32_bf16 (checked on the device):
 //   A[i = l%16][k = 8*(l/16) + j], B[k = 8*(l/16) + j][n = l%16],
 //   C[i = 4*(l/16) + r][n = l%16], j < 8, r < 4.
@@ -96,8 +99,8 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs 
     for (int u = 0; u < U; ++u) {
       const int s = s0 + u;
       const bool in = s < nsteps;
-      wa[u] = (in && w0ok) ? ld16_stream(wp0 + 8 * s) : zero;
-      wb[u] = (in && w1ok) ? ld16_stream(wp1 + 8 * s) : zero;
+      wa[u] = (in && w0ok) ? ld16(wp0 + 8 * s) : zero;
+      wb[u] = (in && w1ok) ? ld16(wp1 + 8 * s) : zero;
       xa[u] = (in && x0ok) ? ld16(xp0 + 8 * s) : zero;
       xb[u] = (in && x1ok) ? ld16(xp1 + 8 * s) : zero;
     }
@@ -188,18 +191,20 @@ int launch_skinny(const SkinnyArgs& a, hipStream_t st, const char* name) {
 }
 
 // ---------------------------------------------------------------- rows_norm
-// Per token row m (one block of 256 threads): h = table[ids[m]] (embed mode)
-// or h = bf16(h_in[m] + bf16(sum_s part[s, m, :])) (residual mode); h_out[m] = h;
-// xn[m] = bf16(bf16(h * rsqrt(mean h^2 + eps)) * gamma).
+// Per token row m (one 256-thread block; each thread owns 8-element chunks):
+// h = table[ids[m]] (embed mode) or h = bf16(h_in[m] + bf16(sum_s part[s, m, :]))
+// (residual mode); h_out[m] = h; xn[m] = bf16(bf16(h * rsqrt(mean h^2 + eps)) * gamma).
+// Every load of the row is issued before any arithmetic (one memory round trip).
+constexpr int kRowChunks = 2;   // 8-element chunks per thread: hidden <= 256 * 8 * 2
 __global__ __launch_bounds__(kThreads) void rows_norm_kernel(
     const uint16_t* __restrict__ table, const int64_t* __restrict__ ids, int64_t vocab,
     const uint16_t* h_in, const float* __restrict__ part, int ks, uint16_t* h_out,
     const uint16_t* __restrict__ gamma, uint16_t* __restrict__ xn, int M, int H, float eps,
     int* err) {
-  extern __shared__ float row[];
   __shared__ float red[kWaves];
   const int m = blockIdx.x;
   const int t = threadIdx.x;
+  const int nch = H / 8;
   const uint16_t* src = nullptr;
   if (table) {
     int64_t id = ids[m];
@@ -208,26 +213,43 @@ __global__ __launch_bounds__(kThreads) void rows_norm_kernel(
       id = 0;
     }
     src = table + id * H;
+  } else {
+    src = h_in + static_cast<size_t>(m) * H;
   }
+  float v[kRowChunks][8];
   float ss = 0.f;
-  for (int i = t; i < H; i += kThreads) {
-    float v;
-    if (table) {
-      v = bf2f(src[i]);
-    } else {
-      float acc = 0.f;
-      for (int s = 0; s < ks; ++s) acc += part[(static_cast<size_t>(s) * M + m) * H + i];
-      v = round_bf(bf2f(h_in[static_cast<size_t>(m) * H + i]) + round_bf(acc));
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int ch = t + c * kThreads;
+    if (ch >= nch) continue;
+    unpack8(ld16(src + 8 * ch), v[c]);
+    if (!table) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < ks; ++s) {
+        const float4* p = reinterpret_cast<const float4*>(part + (static_cast<size_t>(s) * M + m) * H + 8 * ch);
+        const float4 a = p[0], b = p[1];
+        acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
+        acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[c][i] = round_bf(v[c][i] + round_bf(acc[i]));
     }
-    row[i] = v;
-    h_out[static_cast<size_t>(m) * H + i] = static_cast<uint16_t>(f2bf(v));
-    ss += v * v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += v[c][i] * v[c][i];
   }
   ss = block_sum(ss, red);
   const float rs = rsqrt_rn(ss / static_cast<float>(H) + eps);
-  for (int i = t; i < H; i += kThreads)
-    xn[static_cast<size_t>(m) * H + i] =
-        static_cast<uint16_t>(f2bf(round_bf(round_bf(row[i] * rs) * bf2f(gamma[i]))));
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int ch = t + c * kThreads;
+    if (ch >= nch) continue;
+    st16(h_out + static_cast<size_t>(m) * H + 8 * ch, pack8(v[c]));
+    float g[8], y[8];
+    unpack8(ld16(gamma + 8 * ch), g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = round_bf(round_bf(v[c][i] * rs) * g[i]);
+    st16(xn + static_cast<size_t>(m) * H + 8 * ch, pack8(y));
+  }
 }
 
 // -------------------------------------------------------------- batch_sample
@@ -324,7 +346,12 @@ int tfa_rows_norm(const void* table, const int64_t* ids, int64_t vocab, const vo
   TFA_NONNULL(h_out);
   TFA_NONNULL(gamma);
   TFA_NONNULL(xn);
-  TFA_REQUIRE(m >= 0 && hidden > 0 && hidden <= 16384, TFA_ERR_SHAPE, "tfa_rows_norm: bad shape (%lld, %lld)", (long long)m, (long long)hidden);
+  TFA_REQUIRE(m >= 0 && hidden > 0 && hidden % 8 == 0 && hidden <= kThreads * 8 * kRowChunks,
+              TFA_ERR_SHAPE, "tfa_rows_norm: hidden %lld must be a multiple of 8, at most %d",
+              (long long)hidden, kThreads * 8 * kRowChunks);
+  TFA_ALIGN16(h_out);
+  TFA_ALIGN16(xn);
+  TFA_ALIGN16(gamma);
   if (table) {
     TFA_NONNULL(ids);
     TFA_REQUIRE(vocab > 0, TFA_ERR_SHAPE, "tfa_rows_norm: empty table");
@@ -334,7 +361,7 @@ int tfa_rows_norm(const void* table, const int64_t* ids, int64_t vocab, const vo
     TFA_REQUIRE(ks >= 1, TFA_ERR_SHAPE, "tfa_rows_norm: ks must be >= 1");
   }
   if (m == 0) return TFA_OK;
-  rows_norm_kernel<<<(int)m, kThreads, hidden * sizeof(float), stream>>>(
+  rows_norm_kernel<<<(int)m, kThreads, 0, stream>>>(
       static_cast<const uint16_t*>(table), ids, vocab, static_cast<const uint16_t*>(h_in), part,
       (int)ks, static_cast<uint16_t*>(h_out), static_cast<const uint16_t*>(gamma),
       static_cast<uint16_t*>(xn), (int)m, (int)hidden, eps, err);
