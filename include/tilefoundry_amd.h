@@ -169,17 +169,18 @@ int tfa_attn_combine(const float* op, const float* mp, const float* lp, void* ou
 
 /* --------------------------------------------- batched decode (<= 32 rows) */
 
-/* Tiles of 32 weight rows: the per-token block-winner count of the argmax
- * epilogue for n rows. */
+/* Groups of 16 weight rows: the per-token winner count of the argmax epilogue
+ * for n rows. */
 int64_t tfa_skinny_blocks(int64_t n);
 
 /* Y = X[m, k] . W[n, k]^T for m <= 32 token rows on bf16 MFMA (f32 accumulate).
  * epilogue 0: f32 split-K partials part[ks, m, n] (sum over ks = Y);
  * epilogue 1 (ks = 1): SwiGLU over interleaved rows (2i, 2i+1) = (gate_i, up_i):
  *             act[m, n/2] = bf16(bf16(silu(bf16 g)) * bf16 u);
- * epilogue 2 (ks = 1): logits[m, n] f32 and, per token, each 32-row block's best
- *             (max, lowest index) into block_val / block_idx [m, tfa_skinny_blocks(n)].
- * k % (128 * ks) == 0.
+ * epilogue 2 (ks = 1): per token, each 16-row group's best (max, lowest index)
+ *             into block_val / block_idx [m, tfa_skinny_blocks(n)], and the f32
+ *             logits[m, n] when `logits` is not NULL.
+ * k % (256 * ks) == 0.
  * Replaces (batched): examples/qwen3_1_7b-tilelang/fast/kernels.py:123-145 (gemv),
  * :210-257 (gemv_silu), :260-321 (lm_head). */
 int tfa_skinny_gemm(const void* x, const void* w, int64_t m, int64_t n, int64_t k, int64_t ks,

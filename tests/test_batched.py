@@ -77,6 +77,14 @@ def test_skinny_argmax(dev):
     assert max_rel(logits, ref) < 5e-3
     best = bi.gather(1, bv.argmax(1, keepdim=True)).squeeze(1).cpu()
     assert torch.equal(best, logits.cpu().argmax(1).to(torch.int32))
+    # every 16-row group's winner is that group's max of the kernel's own logits
+    grp = logits.cpu().view(M, V // 16, 16)
+    assert torch.equal(bv.cpu(), grp.max(2).values)
+    assert torch.equal(bi.cpu(), (grp.argmax(2) + 16 * torch.arange(V // 16)).to(torch.int32))
+    # without the logits store the winners are the same
+    none, bv2, bi2 = ops.skinny_gemm(x.to(dev), w.to(dev), "argmax", with_logits=False)
+    assert none is None
+    assert torch.equal(bv2, bv) and torch.equal(bi2, bi)
 
 
 @pytest.mark.gpu

@@ -3,23 +3,24 @@
 //
 // skinny_gemm: a 256-thread block owns 32 weight rows (two 16-wide MFMA column
 // tiles) against all 32 token rows (two 16-high row tiles): four
-// v_mfma_f32_16x16x32_bf16 per k-step. K is split over the block's four waves
-// and, inside a wave, over the four 16-lane groups, so every lane walks a
-// contiguous run of its weight row and of its token row in 16-byte chunks. The
-// MFMA's k-slots only need A and B to agree on which k each lane supplies, so
-// this split is a relabelling of k, not a data movement. Optionally K is also
-// split over `ks` blocks, each writing f32 partials that the consumer reduces
-// (the narrow 2048-row projections then still fill every CU). A lane's 16-byte
-// steps along its row are consecutive, so the weight loads are ordinary cached
-// loads: the first brings the line in and the next steps hit it (non-temporal
-// loads would refetch the line for every 16 bytes -- each instruction of a wave
-// touches 32 different rows). Activations are re-read from L2.
+// v_mfma_f32_16x16x32_bf16 per 32-wide k-step. K is split over the block's
+// four waves (and optionally over `ks` blocks, each writing f32 partials that
+// the consumer reduces, so the narrow 2048-row projections still fill every
+// CU). The block walks its K range in steps of four 64-element chunks, one per
+// wave (512 contiguous bytes of every row per step): the chunk's 32 weight
+// rows and 32 token rows are loaded coalesced -- eight lanes per 128-byte row
+// run, weights non-temporal -- into a wave-private LDS tile whose 144-byte row
+// pitch makes the MFMA operand reads (16 rows, same column) bank-conflict
+// free; the next chunk's loads are in flight while this chunk's MFMAs run. (A
+// direct register load in MFMA layout would touch 32 rows per instruction, 16
+// bytes each, and the lines are evicted before the next step uses them.)
 // Lane layout of v_mfma_f32_16x16x32_bf16 (checked on the device):
 //   A[i = l%16][k = 8*(l/16) + j], B[k = 8*(l/16) + j][n = l%16],
 //   C[i = 4*(l/16) + r][n = l%16], j < 8, r < 4.
 //
-// Epilogues: f32 split-K partials | SwiGLU over interleaved gate/up rows |
-// logits + per-row-block best (value, lowest index) per token.
+// Epilogues (each wave finishes one of the block's four 16x16 tiles): f32
+// split-K partials | SwiGLU over interleaved gate/up rows | per token the best
+// (value, lowest index) of every 16-row group, optionally with the f32 logits.
 //
 // rows_norm: per token row, either gather an embedding row or add the reduced
 // split-K partials to the residual stream, then RMSNorm (mode 0) -- the
@@ -31,6 +32,7 @@
 // gemv :123-145, gemv_silu :210-257, lm_head :260-321, resid_rms_norm :82-116,
 // embed :579-588, sample_step :591-637.
 #include <float.h>
+#include <stdlib.h>
 
 #include "abi_util.h"
 #include "common.h"
@@ -43,6 +45,7 @@ constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kTileRows = 32;
 constexpr int kMaxTokens = 32;
+constexpr int kGroupRows = 16;   // argmax winners are kept per 16 weight rows
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -55,18 +58,37 @@ struct SkinnyArgs {
   int M, N, K, ks;
   float* part;        // [ks, M, N]
   uint16_t* act;      // [M, N/2]
-  float* logits;      // [M, N]
-  float* bv;          // [M, gridDim.x]
-  int* bi;            // [M, gridDim.x]
+  float* logits;      // [M, N] or null
+  float* bv;          // [M, ngroups]
+  int* bi;            // [M, ngroups]
+  int ngroups;        // 16-row groups of N
 };
 
 TFA_DEV bf16x8 as_bf8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 TFA_DEV bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
-template <int U, int EPI>
+constexpr int kChunk = 64;            // K elements per wave per pipeline step
+constexpr int kLdsRow = kChunk + 8;   // padded LDS row (144 bytes): conflict-free 16-row reads
+
+// Wave-private LDS staging, ordered by the wave's own in-order LDS pipeline: a
+// compiler-level wave barrier keeps each chunk's stores, the other lanes' reads
+// of them and the next chunk's stores in program order.
+TFA_DEV void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+struct SkinnyStage {
+  uint16_t w[kTileRows][kLdsRow];     // the chunk's weight rows
+  uint16_t x[kMaxTokens][kLdsRow];    // the chunk's token rows
+};
+static_assert(sizeof(SkinnyStage) >= 4 * kWave * sizeof(float) * 4, "partials reuse the staging tile");
+
+template <int EPI, int P>
 __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs a) {
-  __shared__ f32x4 cbuf[kWaves][4][kWave];
+  __shared__ SkinnyStage stage[kWaves];   // 18 KB per wave; reused for the block's partial sums
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = threadIdx.x / kWave;
@@ -74,66 +96,97 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs 
   const int r16 = lane & 15;
   const int n0 = blockIdx.x * kTileRows;
   const int K = a.K;
-  const int kb = K / a.ks;              // this block's K range
-  const int kl = kb / (kWaves * 4);     // this lane's contiguous K run
-  const int k0 = blockIdx.y * kb + wid * (kb / kWaves) + grp * kl;
-  const int nsteps = kl / 8;
+  // the block's K range is walked in steps of kWaves chunks, wave w taking chunk
+  // w of each step: the block reads 512 contiguous bytes of each row at a time
+  const int kb = K / a.ks;                  // this block's K range
+  const int nchunks = kb / (kWaves * kChunk);   // chunks per wave
+  const int kw0 = blockIdx.y * kb + wid * kChunk;
+  constexpr int kStride = kWaves * kChunk;  // K elements between a wave's chunks
+  SkinnyStage& st = stage[wid];
 
-  const int row0 = n0 + r16, row1 = n0 + 16 + r16;
-  const int tok0 = r16, tok1 = 16 + r16;
-  const bool w0ok = row0 < a.N, w1ok = row1 < a.N;
-  const bool x0ok = tok0 < a.M, x1ok = tok1 < a.M;
-  const uint16_t* wp0 = a.w + static_cast<size_t>(w0ok ? row0 : 0) * K + k0;
-  const uint16_t* wp1 = a.w + static_cast<size_t>(w1ok ? row1 : 0) * K + k0;
-  const uint16_t* xp0 = a.x + static_cast<size_t>(x0ok ? tok0 : 0) * K + k0;
-  const uint16_t* xp1 = a.x + static_cast<size_t>(x1ok ? tok1 : 0) * K + k0;
+  // coalesced staging: load i covers rows 8i .. 8i+7, eight lanes per 128-byte
+  // row run. Weight rows past N and token rows past M re-read the last valid row
+  // (in bounds, finite); the results they produce are never stored. Loads are
+  // unconditional so the compiler can count them and wait only for the oldest.
+  const int srow = lane >> 3;               // 0..7
+  const int scol = (lane & 7) * 8;          // element offset in the chunk
+  const uint16_t* wp[4];
+  const uint16_t* xp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = min(n0 + 8 * i + srow, a.N - 1), tok = min(8 * i + srow, a.M - 1);
+    wp[i] = a.w + static_cast<size_t>(row) * K + kw0 + scol;
+    xp[i] = a.x + static_cast<size_t>(tok) * K + kw0 + scol;
+  }
+  // ring of P chunks in registers: chunk g*P + p lives in slot p (nchunks % P == 0)
+  uint4 rw[P][4], rx[P][4];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      rw[p][i] = ld16_stream(wp[i] + p * kStride);
+      rx[p][i] = ld16(xp[i] + p * kStride);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // issue the slots in order: slot p is waited for alone
+  }
 
   f32x4 c[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) c[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const uint4 zero = make_uint4(0, 0, 0, 0);
 
-  for (int s0 = 0; s0 < nsteps; s0 += U) {
-    uint4 wa[U], wb[U], xa[U], xb[U];
+  const int ngroups = nchunks / P;
+  for (int g = 0; g < ngroups; ++g) {
+    const bool refill = g + 1 < ngroups;   // wave-uniform
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int s = s0 + u;
-      const bool in = s < nsteps;
-      wa[u] = (in && w0ok) ? ld16(wp0 + 8 * s) : zero;
-      wb[u] = (in && w1ok) ? ld16(wp1 + 8 * s) : zero;
-      xa[u] = (in && x0ok) ? ld16(xp0 + 8 * s) : zero;
-      xb[u] = (in && x1ok) ? ld16(xp1 + 8 * s) : zero;
-    }
+    for (int p = 0; p < P; ++p) {
+      wave_lds_sync();   // the previous chunk's operand reads are issued before these stores
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      // tile (token half, row half): A = tokens, B = weight rows
-      c[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xa[u]), as_bf8(wa[u]), c[0], 0, 0, 0);
-      c[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xa[u]), as_bf8(wb[u]), c[1], 0, 0, 0);
-      c[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xb[u]), as_bf8(wa[u]), c[2], 0, 0, 0);
-      c[3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xb[u]), as_bf8(wb[u]), c[3], 0, 0, 0);
+      for (int i = 0; i < 4; ++i) {
+        *reinterpret_cast<uint4*>(&st.w[8 * i + srow][scol]) = rw[p][i];
+        *reinterpret_cast<uint4*>(&st.x[8 * i + srow][scol]) = rx[p][i];
+      }
+      if (refill) {   // P chunks stay in flight during the MFMAs
+        const int off = ((g + 1) * P + p) * kStride;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          rw[p][i] = ld16_stream(wp[i] + off);
+          rx[p][i] = ld16(xp[i] + off);
+        }
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int kk = 0; kk < kChunk / 32; ++kk) {
+        const int col = kk * 32 + 8 * grp;
+        const uint4 wa = *reinterpret_cast<const uint4*>(&st.w[r16][col]);
+        const uint4 wb = *reinterpret_cast<const uint4*>(&st.w[16 + r16][col]);
+        const uint4 xa = *reinterpret_cast<const uint4*>(&st.x[r16][col]);
+        const uint4 xb = *reinterpret_cast<const uint4*>(&st.x[16 + r16][col]);
+        // tile (token half, row half): A = tokens, B = weight rows
+        c[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xa), as_bf8(wa), c[0], 0, 0, 0);
+        c[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xa), as_bf8(wb), c[1], 0, 0, 0);
+        c[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xb), as_bf8(wa), c[2], 0, 0, 0);
+        c[3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xb), as_bf8(wb), c[3], 0, 0, 0);
+      }
     }
   }
+  __syncthreads();   // every wave is done with its staging tile
+  f32x4 (*cbuf)[kWave] = reinterpret_cast<f32x4 (*)[kWave]>(&stage[wid]);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) cbuf[wid][i][lane] = c[i];
+  for (int i = 0; i < 4; ++i) cbuf[i][lane] = c[i];
   __syncthreads();
-  if (wid != 0) return;
-  // wave 0 holds the block's result: tile ti = 2*token_half + row_half; lane
-  // (grp, r16) holds tokens 16*th + 4*grp + r, weight row n0 + 16*rh + r16
-  float v[4][4];
-#pragma unroll
-  for (int ti = 0; ti < 4; ++ti) {
-    const f32x4 s = (cbuf[0][ti][lane] + cbuf[1][ti][lane]) + (cbuf[2][ti][lane] + cbuf[3][ti][lane]);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) v[ti][r] = s[r];
-  }
-#pragma unroll
-  for (int ti = 0; ti < 4; ++ti) {
-    const int th = ti >> 1, rh = ti & 1;
+  // wave w finishes tile ti = w = 2*token_half + row_half: lane (grp, r16) holds
+  // tokens 16*th + 4*grp + r (r < 4) against weight row n0 + 16*rh + r16
+  {
+    const int ti = wid, th = ti >> 1, rh = ti & 1;
+    const f32x4 s = (reinterpret_cast<const f32x4*>(&stage[0])[ti * kWave + lane] +
+                     reinterpret_cast<const f32x4*>(&stage[1])[ti * kWave + lane]) +
+                    (reinterpret_cast<const f32x4*>(&stage[2])[ti * kWave + lane] +
+                     reinterpret_cast<const f32x4*>(&stage[3])[ti * kWave + lane]);
     const int n = n0 + 16 * rh + r16;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = 16 * th + 4 * grp + r;
-      const float val = v[ti][r];
+      const float val = s[r];
       if (EPI == SK_PARTIAL) {
         if (m < a.M && n < a.N) a.part[(static_cast<size_t>(blockIdx.y) * a.M + m) * a.N + n] = val;
       }
@@ -147,46 +200,43 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs 
         }
       }
       if (EPI == SK_ARGMAX) {
-        if (m < a.M && n < a.N) a.logits[static_cast<size_t>(m) * a.N + n] = val;
-      }
-    }
-  }
-  if (EPI == SK_ARGMAX) {
-    // per token: best over the block's 32 rows (16 lanes x 2 row halves)
-#pragma unroll
-    for (int th = 0; th < 2; ++th) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float bvv = -FLT_MAX;
-        int bii = 0x7fffffff;
-#pragma unroll
-        for (int rh = 0; rh < 2; ++rh) {
-          const int n = n0 + 16 * rh + r16;
-          const float val = v[2 * th + rh][r];
-          if (n < a.N && better(val, n, bvv, bii)) { bvv = val; bii = n; }
-        }
+        if (a.logits && m < a.M && n < a.N) a.logits[static_cast<size_t>(m) * a.N + n] = val;
+        // per token: best of the tile's 16 rows (lowest index on ties)
+        float bvv = n < a.N ? val : -FLT_MAX;
+        int bii = n < a.N ? n : 0x7fffffff;
 #pragma unroll
         for (int msk = 1; msk < 16; msk <<= 1) {
           const float ov = __shfl_xor(bvv, msk, kWave);
           const int oi = __shfl_xor(bii, msk, kWave);
           if (better(ov, oi, bvv, bii)) { bvv = ov; bii = oi; }
         }
-        const int m = 16 * th + 4 * grp + r;
-        if (r16 == 0 && m < a.M) {
-          a.bv[static_cast<size_t>(m) * gridDim.x + blockIdx.x] = bvv;
-          a.bi[static_cast<size_t>(m) * gridDim.x + blockIdx.x] = bii;
+        const int grp16 = n0 / kGroupRows + rh;   // this tile's 16-row group
+        if (r16 == 0 && m < a.M && grp16 < a.ngroups) {
+          a.bv[static_cast<size_t>(m) * a.ngroups + grp16] = bvv;
+          a.bi[static_cast<size_t>(m) * a.ngroups + grp16] = bii;
         }
       }
     }
   }
 }
 
+int skinny_depth(int nchunks) {
+  static const int d = [] {
+    const char* e = getenv("TFA_SKINNY_DEPTH");
+    return e ? atoi(e) : 2;
+  }();
+  return nchunks % d == 0 ? d : (nchunks % 2 == 0 ? 2 : 1);
+}
+
 template <int EPI>
 int launch_skinny(const SkinnyArgs& a, hipStream_t st, const char* name) {
   const dim3 grid((a.N + kTileRows - 1) / kTileRows, a.ks);
-  const int nsteps = a.K / a.ks / (kWaves * 4) / 8;
-  if (nsteps >= 8) skinny_gemm_kernel<8, EPI><<<grid, kThreads, 0, st>>>(a);
-  else skinny_gemm_kernel<4, EPI><<<grid, kThreads, 0, st>>>(a);
+  switch (skinny_depth(a.K / a.ks / kWaves / kChunk)) {
+    case 1: skinny_gemm_kernel<EPI, 1><<<grid, kThreads, 0, st>>>(a); break;
+    case 3: skinny_gemm_kernel<EPI, 3><<<grid, kThreads, 0, st>>>(a); break;
+    case 4: skinny_gemm_kernel<EPI, 4><<<grid, kThreads, 0, st>>>(a); break;
+    default: skinny_gemm_kernel<EPI, 2><<<grid, kThreads, 0, st>>>(a); break;
+  }
   return launched(name);
 }
 
@@ -296,7 +346,7 @@ __global__ __launch_bounds__(kThreads) void batch_sample_kernel(
 
 extern "C" {
 
-int64_t tfa_skinny_blocks(int64_t n) { return (n + kTileRows - 1) / kTileRows; }
+int64_t tfa_skinny_blocks(int64_t n) { return (n + kGroupRows - 1) / kGroupRows; }
 
 int tfa_skinny_gemm(const void* x, const void* w, int64_t m, int64_t n, int64_t k, int64_t ks,
                     int epilogue, float* part, void* act, float* logits, float* block_val,
@@ -305,8 +355,8 @@ int tfa_skinny_gemm(const void* x, const void* w, int64_t m, int64_t n, int64_t 
   TFA_NONNULL(w);
   TFA_REQUIRE(m >= 1 && m <= kMaxTokens, TFA_ERR_SHAPE, "tfa_skinny_gemm: m=%lld not in [1, 32]", (long long)m);
   TFA_REQUIRE(n >= 1, TFA_ERR_SHAPE, "tfa_skinny_gemm: n=%lld must be positive", (long long)n);
-  TFA_REQUIRE(ks >= 1 && k % (128 * ks) == 0, TFA_ERR_SHAPE,
-              "tfa_skinny_gemm: k=%lld must be a multiple of 128*ks (ks=%lld)", (long long)k, (long long)ks);
+  TFA_REQUIRE(ks >= 1 && k % (kWaves * kChunk * ks) == 0, TFA_ERR_SHAPE,
+              "tfa_skinny_gemm: k=%lld must be a multiple of 256*ks (ks=%lld)", (long long)k, (long long)ks);
   TFA_ALIGN16(x);
   TFA_ALIGN16(w);
   SkinnyArgs a{};
@@ -327,11 +377,11 @@ int tfa_skinny_gemm(const void* x, const void* w, int64_t m, int64_t n, int64_t 
       a.act = static_cast<uint16_t*>(act);
       return launch_skinny<SK_SWIGLU>(a, stream, "skinny_gemm_swiglu");
     case 2:
-      TFA_NONNULL(logits);
       TFA_NONNULL(block_val);
       TFA_NONNULL(block_idx);
       TFA_REQUIRE(ks == 1, TFA_ERR_SHAPE, "tfa_skinny_gemm: argmax needs ks=1");
-      a.logits = logits;
+      a.logits = logits;   // optional
+      a.ngroups = (int)tfa_skinny_blocks(n);
       a.bv = block_val;
       a.bi = block_idx;
       return launch_skinny<SK_ARGMAX>(a, stream, "skinny_gemm_argmax");

@@ -310,8 +310,8 @@ void skinny_gemm(const Tensor& x, const Tensor& w, int64_t ks, int64_t epilogue,
     if (!act) bad("swiglu epilogue needs act");
     need(*act, "act", BF, M * (N / 2));
   } else if (epilogue == 2) {
-    if (!logits || !block_val || !block_idx) bad("argmax epilogue needs logits, block_val, block_idx");
-    need(*logits, "logits", F32, M * N);
+    if (!block_val || !block_idx) bad("argmax epilogue needs block_val, block_idx");
+    if (logits) need(*logits, "logits", F32, M * N);
     const int64_t nb = tfa_skinny_blocks(N);
     need(*block_val, "block_val", F32, M * nb);
     need(*block_idx, "block_idx", I32, M * nb);

@@ -199,11 +199,13 @@ def decode_attention(q, k_cache, v_cache, wr, hq: int, hkv: int, split: int = 64
 # ------------------------------------------------------- batched (<= 32 rows)
 
 def skinny_gemm(x, w, epilogue: str = "partial", ks: int = 1, part=None, act=None, logits=None,
-                block_val=None, block_idx=None):
+                block_val=None, block_idx=None, with_logits: bool = True):
     """``X[m, k] @ W[n, k]^T`` for m <= 32 on bf16 MFMA. ``epilogue``:
     ``"partial"`` -> f32 ``[ks, m, n]`` (sum over ks is the product);
     ``"swiglu"`` -> bf16 ``[m, n/2]`` over interleaved gate/up rows;
-    ``"argmax"`` -> ``(logits [m, n] f32, block_val, block_idx)``."""
+    ``"argmax"`` -> ``(logits [m, n] f32 or None, block_val, block_idx)``, the
+    per-token best (value, lowest index) of every 16-row group; the logits are
+    written only ``with_logits``."""
     m, n = x.shape[0], w.shape[0]
     if epilogue == "partial":
         part = _out(part, x, (ks, m, n), torch.float32)
@@ -214,7 +216,8 @@ def skinny_gemm(x, w, epilogue: str = "partial", ks: int = 1, part=None, act=Non
         C.skinny_gemm(x, w, 1, 1, None, act, None, None, None)
         return act
     nb = C.skinny_blocks(n)
-    logits = _out(logits, x, (m, n), torch.float32)
+    if with_logits:
+        logits = _out(logits, x, (m, n), torch.float32)
     block_val = _out(block_val, x, (m, nb), torch.float32)
     block_idx = _out(block_idx, x, (m, nb), torch.int32)
     C.skinny_gemm(x, w, 1, 2, None, None, logits, block_val, block_idx)

@@ -376,7 +376,7 @@ class BatchEngine:
         skinny_gemm      gate|up + SwiGLU
         skinny_gemm      down_proj -> split-K partials
         rows_norm        residual add + next input norm (final norm after the last layer)
-        skinny_gemm      head -> logits + per-block winners per sequence
+        skinny_gemm      head -> per 16-row group winners per sequence
         batch_sample     greedy step per sequence
     """
 
@@ -438,7 +438,7 @@ class BatchEngine:
         self.plen = z(B, dtype=torch.int32)
         self.err = z(1, dtype=torch.int32)
 
-    def _step(self):
+    def _step(self, keep_logits: bool = False):
         cfg = self.cfg
         HQ, HKV = cfg.heads, cfg.kv_heads
         L = len(self.layers)
@@ -459,7 +459,8 @@ class BatchEngine:
                           None)
             nxt = self.layers[i + 1]["gamma_in"] if i + 1 < L else self.gamma_final
             C.rows_norm(None, None, self.h1, self.d_part, self.h, nxt, self.xn, cfg.eps, self.err)
-        C.skinny_gemm(self.xn, self.embed, 1, 2, None, None, self.logits, self.bv, self.bi)
+        C.skinny_gemm(self.xn, self.embed, 1, 2, None, None, self.logits if keep_logits else None,
+                      self.bv, self.bi)
         C.batch_sample_step(self.bv, self.bi, self.inp, self.plen, self.ids, self.pos, self.sam,
                             self.err)
 
@@ -514,10 +515,11 @@ class BatchEngine:
         return Generated(out, t2 - t1, t1 - t0, pl)
 
     def logits_for(self, prompts: list[list[int]]) -> torch.Tensor:
-        """f32 logits [batch, vocab] after consuming every token of each prompt."""
+        """f32 logits [batch, vocab] after consuming every token of each prompt
+        (eager steps: the captured step writes only the per-group winners)."""
         self._load([list(p) for p in prompts], len(prompts[0]))
         for _ in range(len(prompts[0])):
-            self._run_step()
+            self._step(keep_logits=True)
         torch.cuda.synchronize(self.device)
         self.check_device_errors()
         return self.logits.clone()
