@@ -205,6 +205,64 @@ int tfa_batch_sample_step(const float* block_val, const int* block_idx, int64_t 
                           int64_t batch, const int* inp, const int* prompt_len, int64_t* ids,
                           int* pos, int* sam, int64_t nsteps, int* err, hipStream_t stream);
 
+/* ------------------------------------------ MLA decode, absorbed (MiniCPM3) */
+
+/* Per sequence b (batch <= 65535): reduce the split-K partials part
+ * [ks, batch, q_lora + 256 + 32] f32 of x_n . [W_q_a; W_kv_a]^T (each value
+ * landing in bf16); q_n[b] = bf16(bf16(q_a * rsqrt(mean q_a^2 + eps)) * gamma_q_a);
+ * latent_cache[b, pos[b]] = the same norm of kv_c with gamma_kv_a;
+ * rope_cache[b, pos[b]] = rotate-half RoPE of the 32-wide rope slice at pos[b]
+ * (bf16 products and sum). Caches are [batch, cap, 256] / [batch, cap, 32]
+ * bf16; cos/sin [rope_rows, 32] bf16. A pos outside [0, cap) or the table sets
+ * *err = 6 and skips the cache writes. q_lora <= 1024.
+ * Replaces (absorbed form): examples/minicpm3_4b-cutedsl/model.py:220-250 (steps 1-4
+ * of mla_attention), kernels/cute_gemv.py:246-286 (NORM_GEMV) and the kv half
+ * of :291-347 (NORM_GEMV_PAIR). */
+int tfa_mla_prep(const float* part, int64_t ks, int64_t batch, int64_t q_lora, const void* gamma_q_a,
+                 const void* gamma_kv_a, float eps, const void* cos_t, const void* sin_t,
+                 int64_t rope_rows, const int* pos, void* latent_cache, void* rope_cache, int64_t cap,
+                 void* q_n, int* err, hipStream_t stream);
+
+/* The absorbed query: from the split-K partials q_part [ks, batch, heads*96]
+ * f32 of q_n . W_q_b^T (landing in bf16), q_abs[b, h, 0:256] =
+ * bf16(W_UK_h^T q_nope) (f32 accumulate) and q_abs[b, h, 256:288] = RoPE of
+ * q_rope at pos[b]. w_kv_b is [heads*128, 256] (out, in): rows h*128 .. +63
+ * are W_UK_h, rows h*128+64 .. +127 are W_UV_h. batch <= 32, heads <= 48.
+ * Replaces (absorbed form): the q half of kernels/cute_gemv.py:291-347 and the
+ * q rotation of kernels/reference_ops.py:99-107. */
+int tfa_mla_q_absorb(const float* q_part, int64_t ks, int64_t batch, int64_t heads, const void* w_kv_b,
+                     const void* cos_t, const void* sin_t, int64_t rope_rows, const int* pos, void* q_abs,
+                     int* err, hipStream_t stream);
+
+/* Split attention of q_abs [batch, heads, 288] bf16 over slots 0..wr[b] of the
+ * compressed cache on bf16 MFMA: s = scale * (q_abs . [latent | rope]) in f32,
+ * per split (split positions, a multiple of 64, at most 1024) the softmax in
+ * f32 with bf16 weights into the latent sum; op [batch, cap/split, heads, 256]
+ * bf16 = the split's latent sum / its own weight sum, mp / lp [batch,
+ * cap/split, heads] its max and sum. Only splits holding slots <= wr[b] are
+ * written. A wr outside [0, cap) sets *err = 4 (clamped).
+ * Replaces (absorbed form): kernels/cute_attention.py:56-200 (ROPE_ATTEND),
+ * kernels/reference_ops.py:87-130 (rope_attend). */
+int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* rope_cache, const int* wr,
+                      int64_t batch, int64_t heads, int64_t cap, int64_t split, float scale, void* op,
+                      float* mp, float* lp, int* err, hipStream_t stream);
+
+/* Merge of tfa_mla_attention's splits per (head, sequence): weights
+ * w_s = lp e^(mp - max), o_lat = sum_s w_s op_s / sum_s w_s (f32), then
+ * attn[b, h*64 + v] = bf16(W_UV_h o_lat) over the splits holding slots <= wr[b].
+ * Replaces (absorbed form): the 8-warp LSE merge of kernels/cute_attention.py:56-200
+ * and the value half of W_kv_b applied per position in reference_ops.py:111-128. */
+int tfa_mla_combine_up(const void* op, const float* mp, const float* lp, const int* wr, int64_t splits,
+                       int64_t split, int64_t batch, int64_t heads, int64_t cap, const void* w_kv_b,
+                       void* attn, hipStream_t stream);
+
+/* out[i, j] = bf16(residual[i, j] + bf16(bf16(sum_s part[s, i, j]) * alpha)) for
+ * part [ks, m, n] f32 split-K partials (n % 8 == 0): the o_proj epilogue with
+ * MiniCPM3's scale_depth residual.
+ * Replaces: kernels/cute_gemv.py:430-495 (gemv_residual), reference_ops.py:63-65. */
+int tfa_rows_residual(const float* part, int64_t ks, const void* residual, float alpha, void* out,
+                      int64_t m, int64_t n, hipStream_t stream);
+
 /* ------------------------------------------------------------ measurement */
 
 /* dst[0:bytes) = src[0:bytes) with the decode kernels' own access pattern

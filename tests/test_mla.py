@@ -1,0 +1,227 @@
+"""MLA decode (absorbed, MiniCPM3-4B shapes) against the CPU oracle: each kernel
+on its own, the attention core at several context lengths and splits, a
+closed form at the full batch-8 / 8192-position size, and the whole attention
+block against the non-absorbed reference order."""
+import pytest
+import torch
+
+from oracle import minicpm3 as OM
+from oracle.norms import rms_norm_q
+from tests._check import assert_close, assert_equal, assert_l2, assert_ulps, bf16_ulps, rel_l2
+
+BF = torch.bfloat16
+CFG = OM.MLAConfig()
+H, QA, KV, R = CFG.heads, CFG.q_lora, CFG.kv_lora, CFG.rope
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def oracle_weights(seed=3, std=0.05):
+    return OM.random_weights(CFG, seed=seed, std=std)
+
+
+@pytest.mark.gpu
+def test_mla_prep(dev):
+    from tilefoundry_amd._lib import C
+
+    g = gen(1)
+    B, ks, cap = 3, 2, 128
+    part = torch.randn(ks, B, QA + KV + R, generator=g) * 0.5
+    gq = (1 + 0.1 * torch.randn(QA, generator=g)).to(BF)
+    gkv = (1 + 0.1 * torch.randn(KV, generator=g)).to(BF)
+    cos, sin = OM.rope_tables(cap, CFG)
+    pos = [0, 5, 127]
+    lat = torch.zeros(B, cap, KV, dtype=BF, device=dev)
+    rk = torch.zeros(B, cap, R, dtype=BF, device=dev)
+    q_n = torch.empty(B, QA, dtype=BF, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    C.mla_prep(part.to(dev), gq.to(dev), gkv.to(dev), 1e-6, cos.to(dev), sin.to(dev),
+               torch.tensor(pos, dtype=torch.int32, device=dev), lat, rk, q_n, err)
+    assert int(err.item()) == 0
+    red = part.sum(0).to(BF)
+    assert_ulps("q_n", q_n, rms_norm_q(red[:, :QA], gq, 1e-6), max_ulps=2)
+    for b, p in enumerate(pos):
+        assert_ulps(f"latent b={b}", lat[b, p], rms_norm_q(red[b, QA:QA + KV], gkv, 1e-6), max_ulps=2)
+        assert_equal(f"rope key b={b}", rk[b, p], OM.rope32(red[b, QA + KV:], cos[p], sin[p]))
+    # only the slots at pos were written
+    mask = torch.ones(B, cap, dtype=torch.bool)
+    for b, p in enumerate(pos):
+        mask[b, p] = False
+    assert not bool(lat.cpu()[mask].float().abs().sum()) and not bool(rk.cpu()[mask].float().abs().sum())
+
+
+@pytest.mark.gpu
+def test_mla_prep_position_error(dev):
+    from tilefoundry_amd._lib import C
+
+    B, cap = 2, 64
+    lat = torch.zeros(B, cap, KV, dtype=BF, device=dev)
+    rk = torch.zeros(B, cap, R, dtype=BF, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    cos, sin = OM.rope_tables(cap, CFG)
+    C.mla_prep(torch.ones(1, B, QA + KV + R, device=dev), torch.ones(QA, dtype=BF, device=dev),
+               torch.ones(KV, dtype=BF, device=dev), 1e-6, cos.to(dev), sin.to(dev),
+               torch.tensor([3, cap], dtype=torch.int32, device=dev), lat, rk,
+               torch.empty(B, QA, dtype=BF, device=dev), err)
+    assert int(err.item()) == 6
+    assert float(lat[1].float().abs().sum()) == 0.0   # the out-of-range slot wrote nothing
+
+
+@pytest.mark.gpu
+def test_mla_q_absorb(dev):
+    from tilefoundry_amd._lib import C
+
+    g = gen(2)
+    B, ks = 4, 3
+    w = oracle_weights()
+    q_part = torch.randn(ks, B, H * (CFG.nope + R), generator=g) * 0.7
+    cos, sin = OM.rope_tables(512, CFG)
+    pos = [0, 1, 300, 511]
+    q_abs = torch.empty(B, H, KV + R, dtype=BF, device=dev)
+    C.mla_q_absorb(q_part.to(dev), w.w_kv_b.to(dev), cos.to(dev), sin.to(dev),
+                   torch.tensor(pos, dtype=torch.int32, device=dev), q_abs, None)
+    q_up = q_part.sum(0).to(BF).view(B, H, -1)
+    for b, p in enumerate(pos):
+        ref = OM.absorb_query(q_up[b], w, CFG, p, cos, sin)
+        assert_ulps(f"q_lat b={b}", q_abs[b, :, :KV], ref[:, :KV], max_ulps=1, max_frac=0.02)
+        assert_equal(f"q_rope b={b}", q_abs[b, :, KV:], ref[:, KV:])
+
+
+def _attend(dev, q_abs, lat, rk, pos, split, w_kv_b, cap):
+    from tilefoundry_amd._lib import C
+
+    B = q_abs.shape[0]
+    ns = cap // split
+    op = torch.empty(B, ns, H, KV, dtype=BF, device=dev)
+    mp = torch.empty(B, ns, H, device=dev)
+    lp = torch.empty(B, ns, H, device=dev)
+    attn = torch.empty(B, H * CFG.v_dim, dtype=BF, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    posd = torch.tensor(pos, dtype=torch.int32, device=dev)
+    C.mla_attention(q_abs.to(dev), lat.to(dev), rk.to(dev), posd, split, CFG.scale, op, mp, lp, err)
+    C.mla_combine_up(op, mp, lp, posd, split, w_kv_b.to(dev), attn)
+    assert int(err.item()) == 0
+    return attn.cpu()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("split,pos", [(256, [0, 63, 700]), (64, [64, 1, 1023]), (1024, [500, 1023, 2])])
+def test_mla_attention_vs_oracle(dev, split, pos):
+    g = gen(sum(pos) + split)
+    B, cap = 3, 1024
+    w = oracle_weights()
+    lat, rk = OM.random_cache(B, cap, CFG, seed=split)
+    q_abs = torch.randn(B, H, KV + R, generator=g).to(BF)
+    got = _attend(dev, q_abs, lat, rk, pos, split, w.w_kv_b, cap)
+    for b, p in enumerate(pos):
+        ref = OM.attend_absorbed(q_abs[b], lat[b, :p + 1], rk[b, :p + 1], w, CFG, p_bf16=True)
+        assert_close(f"attn b={b} pos={p}", got[b], ref)
+        assert rel_l2(got[b], ref) < 4e-3
+
+
+@pytest.mark.gpu
+def test_mla_attention_stale_slots_ignored(dev):
+    """Slots past the context hold NaN: nothing of them reaches the output."""
+    g = gen(9)
+    B, cap, split = 2, 512, 256
+    w = oracle_weights()
+    lat, rk = OM.random_cache(B, cap, CFG, seed=9)
+    lat[:, 300:] = float("nan")
+    rk[:, 300:] = float("nan")
+    q_abs = torch.randn(B, H, KV + R, generator=g).to(BF)
+    pos = [299, 10]
+    got = _attend(dev, q_abs, lat, rk, pos, split, w.w_kv_b, cap)
+    assert not bool(torch.isnan(got.float()).any())
+    for b, p in enumerate(pos):
+        ref = OM.attend_absorbed(q_abs[b], lat[b, :p + 1], rk[b, :p + 1], w, CFG, p_bf16=True)
+        assert_close(f"attn b={b}", got[b], ref)
+
+
+@pytest.mark.gpu
+def test_mla_attention_full_size_identical_rows(dev):
+    """Batch 8 x 8192 positions, every cached entry equal: each weight is
+    exactly 1 / n whatever the query, so head h returns bf16(W_UV_h c)."""
+    g = gen(10)
+    B, cap, split = 8, 8192, 256
+    w = oracle_weights()
+    c = torch.randn(KV, generator=g).to(BF)
+    r = torch.randn(R, generator=g).to(BF)
+    lat = c.view(1, 1, KV).expand(B, cap, KV).contiguous()
+    rk = r.view(1, 1, R).expand(B, cap, R).contiguous()
+    q_abs = torch.randn(B, H, KV + R, generator=g).to(BF)
+    pos = [8191, 4095, 0, 256, 255, 8000, 1, 7777]
+    got = _attend(dev, q_abs, lat, rk, pos, split, w.w_kv_b, cap).view(B, H, -1)
+    exp = torch.einsum("hvc,c->hv", w.w_uv(CFG).double(), c.double()).to(BF)
+    for b in range(B):
+        assert_ulps(f"b={b}", got[b], exp, max_ulps=1)
+
+
+@pytest.mark.gpu
+def test_mla_attention_full_size_one_sequence(dev):
+    """The config's own size (8 sequences x 8192 positions) with random data;
+    two sequences checked against the oracle in full."""
+    g = gen(11)
+    B, cap, split = 8, 8192, 256
+    w = oracle_weights()
+    lat, rk = OM.random_cache(B, cap, CFG, seed=11)
+    q_abs = torch.randn(B, H, KV + R, generator=g).to(BF)
+    pos = [8191] * B
+    pos[5] = 5000
+    got = _attend(dev, q_abs, lat, rk, pos, split, w.w_kv_b, cap)
+    for b in (0, 5):
+        ref = OM.attend_absorbed(q_abs[b], lat[b, :pos[b] + 1], rk[b, :pos[b] + 1], w, CFG, p_bf16=True)
+        assert_close(f"attn b={b}", got[b], ref)
+
+
+@pytest.mark.gpu
+def test_rows_residual(dev):
+    from tilefoundry_amd._lib import C
+
+    g = gen(12)
+    part = torch.randn(5, 8, 2560, generator=g)
+    res = torch.randn(8, 2560, generator=g).to(BF)
+    out = torch.empty(8, 2560, dtype=BF, device=dev)
+    alpha = float(torch.tensor(0.1778).to(BF))
+    C.rows_residual(part.to(dev), res.to(dev), alpha, out)
+    ref = res + part.sum(0).to(BF) * torch.tensor(alpha).to(BF)
+    assert_equal("rows_residual", out, ref)
+
+
+@pytest.mark.gpu
+def test_mla_block_vs_reference(dev):
+    """The whole attention block (norm, projections, cache append, absorbed
+    attention, o_proj, scaled residual) against the non-absorbed reference
+    order, with each sequence at its own position."""
+    from tilefoundry_amd.minicpm3 import MLABlock, MiniCPM3Config, synthetic_weights
+
+    cfg = MiniCPM3Config()
+    B, cap = 2, 512
+    wts = synthetic_weights(cfg, seed=7)
+    blk = MLABlock(cfg, batch=B, cap=cap, device=dev, weights=wts)
+    ow = OM.MLAWeights(**wts)
+    lat, rk = OM.random_cache(B, cap, CFG, seed=13)
+    blk.latent.copy_(lat.to(dev))
+    blk.rope_k.copy_(rk.to(dev))
+    hidden = torch.randn(B, cfg.hidden, generator=gen(14)).to(BF)
+    pos = [100, 511]
+    out = blk.step(hidden.to(dev), pos).cpu()
+    attn = blk.attn.cpu()
+    cos, sin = OM.rope_tables(cap, CFG)
+    for b, p in enumerate(pos):
+        pr = OM.project(hidden[b], ow, CFG, p, cos, sin)
+        assert_ulps(f"latent b={b}", blk.latent[b, p], pr.latent, max_ulps=2)
+        assert_ulps(f"rope key b={b}", blk.rope_k[b, p], pr.k_rope, max_ulps=1)
+        lat_ctx = torch.cat((lat[b, :p], pr.latent.view(1, -1)))
+        rk_ctx = torch.cat((rk[b, :p], pr.k_rope.view(1, -1)))
+        ref = OM.attend_reference(pr.q_up, lat_ctx, rk_ctx, ow, CFG, p, cos, sin)
+        absd = OM.attend_absorbed(OM.absorb_query(pr.q_up, ow, CFG, p, cos, sin), lat_ctx, rk_ctx, ow, CFG,
+                                  p_bf16=True)
+        assert_l2(f"attn vs reference b={b}", attn[b], ref)
+        assert_close(f"attn vs absorbed oracle b={b}", attn[b], absd)
+        o_ref = OM.o_proj_residual(ref, ow.w_o, hidden[b], cfg.residual_scale)
+        assert_close(f"block out b={b}", out[b], o_ref)
+        # the o_proj branch itself (the residual sum's bf16 landing would hide it)
+        branch = blk.part_o.sum(0)[b].cpu()
+        assert_l2(f"o_proj b={b}", branch, ref.float() @ ow.w_o.float().t())

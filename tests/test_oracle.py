@@ -223,3 +223,90 @@ def test_synthetic_generator_statistics():
     assert abs(float(x.std()) - 0.02) < 1e-4
     assert not torch.equal(normal((64,), 1, 0), normal((64,), 1, 1))
     assert torch.equal(normal((64,), 1, 0), normal((64,), 1, 0))
+
+
+# ---------------------------------------------------------------- MLA (MiniCPM3)
+def _mla_small():
+    from oracle import minicpm3 as OM
+
+    cfg = OM.MLAConfig(hidden=64, heads=4, q_lora=32, kv_lora=32, nope=16, rope=8, v_dim=16)
+    return OM, cfg, OM.random_weights(cfg, seed=4, std=0.25)
+
+
+def test_mla_rope_tables_against_closed_form():
+    from oracle import minicpm3 as OM
+
+    cfg = OM.MLAConfig()
+    cos, sin = OM.rope_tables(5000, cfg)
+    i = torch.arange(16, dtype=torch.float64)
+    inv = 1.0 / (torch.tensor(OM.SHORT_FACTOR, dtype=torch.float64) * 10000.0 ** (2 * i / 32))
+    for p in (0, 1, 77, 4999):
+        assert int(bf16_ulps(cos[p, :16], torch.cos(p * inv).to(BF)).max()) <= 1
+        assert int(bf16_ulps(sin[p, 16:], torch.sin(p * inv).to(BF)).max()) <= 1
+
+
+def test_mla_rope_identity_and_rotation():
+    from oracle import minicpm3 as OM
+
+    cos, sin = OM.rope_tables(64, OM.MLAConfig())
+    x = torch.randn(40, 32, generator=g(30)).to(BF)
+    assert torch.equal(OM.rope32(x, cos[0], sin[0]), x)
+    p = 41
+    got = OM.rope32(x, cos[p], sin[p]).double()
+    z = torch.complex(x[:, :16].double(), x[:, 16:].double()) * torch.complex(cos[p, :16].double(), sin[p, :16].double())
+    ref = torch.cat([z.real, z.imag], -1)
+    assert float((got - ref).abs().max()) <= float(ref.abs().max()) * 2 ** -7
+
+
+def test_mla_absorbed_equals_reference_attention():
+    """The absorption identity: scoring the latent with W_UK^T q_nope and
+    up-projecting the weighted latent with W_UV equals attending the assembled
+    per-head keys / values (to the bf16 bar; they round at different points)."""
+    from tests._check import rel_l2
+
+    OM, cfg, w = _mla_small()
+    n, pos = 37, 36
+    cos, sin = OM.rope_tables(n, cfg)
+    lat, rk = OM.random_cache(1, n, cfg, seed=5)
+    q_up = torch.randn(cfg.heads, cfg.qk_dim, generator=g(31)).to(BF)
+    ref = OM.attend_reference(q_up, lat[0], rk[0], w, cfg, pos, cos, sin)
+    q_abs = OM.absorb_query(q_up, w, cfg, pos, cos, sin)
+    for pb in (False, True):
+        got = OM.attend_absorbed(q_abs, lat[0], rk[0], w, cfg, p_bf16=pb)
+        assert rel_l2(got, ref) < 1e-2
+    # planted mistake: absorbing with the value half of W_kv_b breaks the identity
+    bad = OM.MLAWeights(**{**w.__dict__, "w_kv_b": w.w_kv_b.view(cfg.heads, 2, 16, cfg.kv_lora).flip(1).reshape(-1, cfg.kv_lora)})
+    wrong = OM.attend_absorbed(OM.absorb_query(q_up, bad, cfg, pos, cos, sin), lat[0], rk[0], w, cfg)
+    assert rel_l2(wrong, ref) > 0.1
+
+
+def test_mla_one_position_returns_projected_latent():
+    """One position: the softmax weight is 1, so head h's output is W_UV_h c_0."""
+    OM, cfg, w = _mla_small()
+    cos, sin = OM.rope_tables(4, cfg)
+    lat, rk = OM.random_cache(1, 1, cfg, seed=6)
+    q_up = torch.randn(cfg.heads, cfg.qk_dim, generator=g(32)).to(BF)
+    got = OM.attend_absorbed(OM.absorb_query(q_up, w, cfg, 0, cos, sin), lat[0], rk[0], w, cfg).view(cfg.heads, -1)
+    c0 = lat[0, 0].double()
+    for h in range(cfg.heads):
+        exp = torch.stack([sum(c0[c] * float(w.w_kv_b[h * 32 + 16 + v, c]) for c in range(cfg.kv_lora)) for v in range(16)])
+        assert int(bf16_ulps(got[h], exp.to(BF)).max()) <= 1
+
+
+def test_mla_absorbed_f64_brute_force():
+    import math
+
+    OM, cfg, w = _mla_small()
+    n = 6
+    lat, rk = OM.random_cache(1, n, cfg, seed=7)
+    q_abs = torch.randn(cfg.heads, cfg.kv_lora + cfg.rope, generator=g(33)).to(BF)
+    got = OM.attend_absorbed(q_abs, lat[0], rk[0], w, cfg).double().view(cfg.heads, -1)
+    kc = torch.cat((lat[0], rk[0]), -1)
+    for h in range(cfg.heads):
+        s = [cfg.scale * sum(float(q_abs[h, d]) * float(kc[j, d]) for d in range(kc.shape[1])) for j in range(n)]
+        mx = max(s)
+        e = [math.exp(x - mx) for x in s]
+        o = [sum(e[j] * float(lat[0, j, c]) for j in range(n)) / sum(e) for c in range(cfg.kv_lora)]
+        ref = [sum(o[c] * float(w.w_kv_b[h * 32 + 16 + v, c]) for c in range(cfg.kv_lora)) for v in range(16)]
+        ref = torch.tensor(ref, dtype=torch.float64)
+        assert float((got[h] - ref).abs().max()) <= float(ref.abs().max()) * 2 ** -7

@@ -32,7 +32,6 @@
 // gemv :123-145, gemv_silu :210-257, lm_head :260-321, resid_rms_norm :82-116,
 // embed :579-588, sample_step :591-637.
 #include <float.h>
-#include <stdlib.h>
 
 #include "abi_util.h"
 #include "common.h"
@@ -220,23 +219,17 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs 
   }
 }
 
-int skinny_depth(int nchunks) {
-  static const int d = [] {
-    const char* e = getenv("TFA_SKINNY_DEPTH");
-    return e ? atoi(e) : 2;
-  }();
-  return nchunks % d == 0 ? d : (nchunks % 2 == 0 ? 2 : 1);
-}
+// Register ring depth: two chunks in flight per wave when the wave's chunk count
+// allows it (deeper rings cost occupancy and measured no faster).
+int skinny_depth(int nchunks) { return nchunks % 2 == 0 ? 2 : 1; }
 
 template <int EPI>
 int launch_skinny(const SkinnyArgs& a, hipStream_t st, const char* name) {
   const dim3 grid((a.N + kTileRows - 1) / kTileRows, a.ks);
-  switch (skinny_depth(a.K / a.ks / kWaves / kChunk)) {
-    case 1: skinny_gemm_kernel<EPI, 1><<<grid, kThreads, 0, st>>>(a); break;
-    case 3: skinny_gemm_kernel<EPI, 3><<<grid, kThreads, 0, st>>>(a); break;
-    case 4: skinny_gemm_kernel<EPI, 4><<<grid, kThreads, 0, st>>>(a); break;
-    default: skinny_gemm_kernel<EPI, 2><<<grid, kThreads, 0, st>>>(a); break;
-  }
+  if (skinny_depth(a.K / a.ks / kWaves / kChunk) == 2)
+    skinny_gemm_kernel<EPI, 2><<<grid, kThreads, 0, st>>>(a);
+  else
+    skinny_gemm_kernel<EPI, 1><<<grid, kThreads, 0, st>>>(a);
   return launched(name);
 }
 

@@ -372,6 +372,105 @@ void batch_sample_step(const Tensor& block_val, const Tensor& block_idx, const T
                                      nsteps, opt_ptr_t<int>(err), stream_of(pos)));
 }
 
+// ------------------------------------------------------------------ MLA
+// part [ks, B, q_lora + 288] f32; latent [B, cap, 256], rope [B, cap, 32] bf16.
+void mla_prep(const Tensor& part, const Tensor& gamma_q_a, const Tensor& gamma_kv_a, double eps,
+              const Tensor& cos, const Tensor& sin, const Tensor& pos, const Tensor& latent,
+              const Tensor& rope, const Tensor& q_n, const OptT& err) {
+  need(pos, "pos", I32);
+  const int64_t B = pos.numel();
+  need(latent, "latent", BF);
+  need(rope, "rope", BF);
+  if (latent.dim() != 3 || latent.size(0) != B || latent.size(2) != 256) bad("latent: expected (batch, cap, 256)");
+  const int64_t cap = latent.size(1);
+  need(rope, "rope", BF, B * cap * 32);
+  need(gamma_kv_a, "gamma_kv_a", BF, 256);
+  need(gamma_q_a, "gamma_q_a", BF);
+  const int64_t QA = gamma_q_a.numel();
+  need(q_n, "q_n", BF, B * QA);
+  need(part, "part", F32);
+  if (part.numel() % (B * (QA + 288)) != 0) bad("part: expected (ks, batch, q_lora + 288)");
+  const int64_t ks = part.numel() / (B * (QA + 288));
+  need(cos, "cos", BF);
+  need(sin, "sin", BF, cos.numel());
+  if (cos.numel() % 32 != 0) bad("cos: expected (rows, 32)");
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_mla_prep(part.data_ptr<float>(), ks, B, QA, gamma_q_a.data_ptr(), gamma_kv_a.data_ptr(),
+                            (float)eps, cos.data_ptr(), sin.data_ptr(), cos.numel() / 32, pos.data_ptr<int>(),
+                            latent.data_ptr(), rope.data_ptr(), cap, q_n.data_ptr(), opt_ptr_t<int>(err),
+                            stream_of(pos)));
+}
+
+// q_part [ks, B, H*96] f32, w_kv_b [H*128, 256], q_abs [B, H, 288] bf16.
+void mla_q_absorb(const Tensor& q_part, const Tensor& w_kv_b, const Tensor& cos, const Tensor& sin,
+                  const Tensor& pos, const Tensor& q_abs, const OptT& err) {
+  need(pos, "pos", I32);
+  const int64_t B = pos.numel();
+  need(q_abs, "q_abs", BF);
+  if (q_abs.dim() != 3 || q_abs.size(0) != B || q_abs.size(2) != 288) bad("q_abs: expected (batch, heads, 288)");
+  const int64_t H = q_abs.size(1);
+  need_mat(w_kv_b, "w_kv_b", H * 128, 256);
+  need(q_part, "q_part", F32);
+  if (q_part.numel() % (B * H * 96) != 0) bad("q_part: expected (ks, batch, heads*96)");
+  need(cos, "cos", BF);
+  need(sin, "sin", BF, cos.numel());
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_mla_q_absorb(q_part.data_ptr<float>(), q_part.numel() / (B * H * 96), B, H,
+                                w_kv_b.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.numel() / 32,
+                                pos.data_ptr<int>(), q_abs.data_ptr(), opt_ptr_t<int>(err), stream_of(pos)));
+}
+
+// op [B, ns, H, 256] bf16, mp / lp [B, ns, H] f32.
+void mla_attention(const Tensor& q_abs, const Tensor& latent, const Tensor& rope, const Tensor& wr,
+                   int64_t split, double scale, const Tensor& op, const Tensor& mp, const Tensor& lp,
+                   const OptT& err) {
+  need(wr, "wr", I32);
+  const int64_t B = wr.numel();
+  need(q_abs, "q_abs", BF);
+  if (q_abs.dim() != 3 || q_abs.size(0) != B || q_abs.size(2) != 288) bad("q_abs: expected (batch, heads, 288)");
+  const int64_t H = q_abs.size(1);
+  need(latent, "latent", BF);
+  if (latent.dim() != 3 || latent.size(0) != B || latent.size(2) != 256) bad("latent: expected (batch, cap, 256)");
+  const int64_t cap = latent.size(1);
+  need(rope, "rope", BF, B * cap * 32);
+  if (split <= 0 || cap % split != 0) bad("cache capacity must be a multiple of the split");
+  const int64_t ns = cap / split;
+  need(op, "op", BF, B * ns * H * 256);
+  need(mp, "mp", F32, B * ns * H);
+  need(lp, "lp", F32, B * ns * H);
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_mla_attention(q_abs.data_ptr(), latent.data_ptr(), rope.data_ptr(), wr.data_ptr<int>(), B, H,
+                                 cap, split, (float)scale, op.data_ptr(), mp.data_ptr<float>(),
+                                 lp.data_ptr<float>(), opt_ptr_t<int>(err), stream_of(wr)));
+}
+
+void mla_combine_up(const Tensor& op, const Tensor& mp, const Tensor& lp, const Tensor& wr, int64_t split,
+                    const Tensor& w_kv_b, const Tensor& attn) {
+  need(wr, "wr", I32);
+  const int64_t B = wr.numel();
+  need(op, "op", BF);
+  if (op.dim() != 4 || op.size(0) != B || op.size(3) != 256) bad("op: expected (batch, splits, heads, 256)");
+  const int64_t ns = op.size(1), H = op.size(2);
+  need(mp, "mp", F32, B * ns * H);
+  need(lp, "lp", F32, B * ns * H);
+  need_mat(w_kv_b, "w_kv_b", H * 128, 256);
+  need(attn, "attn", BF, B * H * 64);
+  raise_status(tfa_mla_combine_up(op.data_ptr(), mp.data_ptr<float>(), lp.data_ptr<float>(), wr.data_ptr<int>(),
+                                  ns, split, B, H, ns * split, w_kv_b.data_ptr(), attn.data_ptr(), stream_of(wr)));
+}
+
+// part [ks, m, n] f32; residual / out [m, n] bf16.
+void rows_residual(const Tensor& part, const Tensor& residual, double alpha, const Tensor& out) {
+  need(residual, "residual", BF);
+  if (residual.dim() != 2) bad("residual: expected (m, n)");
+  const int64_t M = residual.size(0), N = residual.size(1);
+  need(out, "out", BF, M * N);
+  need(part, "part", F32);
+  if (part.numel() % (M * N) != 0) bad("part: expected (ks, m, n)");
+  raise_status(tfa_rows_residual(part.data_ptr<float>(), part.numel() / (M * N), residual.data_ptr(),
+                                 (float)alpha, out.data_ptr(), M, N, stream_of(out)));
+}
+
 void copy_stream(const Tensor& src, const Tensor& dst) {
   if (!src.is_cuda() || !dst.is_cuda() || !src.is_contiguous() || !dst.is_contiguous())
     bad("copy_stream: contiguous GPU tensors required");
@@ -403,4 +502,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("skinny_gemm", &skinny_gemm);
   m.def("rows_norm", &rows_norm);
   m.def("batch_sample_step", &batch_sample_step);
+  m.def("mla_prep", &mla_prep);
+  m.def("mla_q_absorb", &mla_q_absorb);
+  m.def("mla_attention", &mla_attention);
+  m.def("mla_combine_up", &mla_combine_up);
+  m.def("rows_residual", &rows_residual);
 }

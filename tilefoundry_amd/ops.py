@@ -235,3 +235,33 @@ def rows_norm(gamma, eps: float, *, table=None, ids=None, h_in=None, part=None, 
     xn = _out(xn, like, (m, H), BF16)
     C.rows_norm(table, ids, h_in, part, h_out, gamma, xn, float(eps), err)
     return h_out, xn
+
+
+# ------------------------------------------------- MLA decode (absorbed)
+
+def mla_attention(q_abs, latent, rope_keys, wr, w_kv_b, split: int = 256, scale: float | None = None,
+                  attn=None, err=None):
+    """Absorbed MLA attention of ``q_abs`` [B, H, 288] over slots ``0..wr[b]`` of
+    the compressed cache (``latent`` [B, cap, 256], ``rope_keys`` [B, cap, 32])
+    followed by the value up-projection: bf16 ``[B, H*64]``."""
+    B, Hh = q_abs.shape[0], q_abs.shape[1]
+    cap = latent.shape[1]
+    ns = cap // split
+    dev = q_abs.device
+    op = torch.empty(B, ns, Hh, 256, dtype=BF16, device=dev)
+    mp = torch.empty(B, ns, Hh, dtype=torch.float32, device=dev)
+    lp = torch.empty_like(mp)
+    wr = _dev_i32(wr, dev)
+    if scale is None:
+        scale = float(torch.tensor(96 ** -0.5).to(BF16))
+    C.mla_attention(q_abs, latent, rope_keys, wr, split, scale, op, mp, lp, err)
+    attn = _out(attn, q_abs, (B, Hh * 64), BF16)
+    C.mla_combine_up(op, mp, lp, wr, split, w_kv_b, attn)
+    return attn
+
+
+def rows_residual(part, residual, alpha: float, out=None):
+    """``bf16(residual + bf16(bf16(sum_s part[s]) * alpha))``."""
+    out = _out(out, residual)
+    C.rows_residual(part, residual, float(alpha), out)
+    return out
