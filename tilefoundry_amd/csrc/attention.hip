@@ -64,13 +64,8 @@ TFA_DEV void set_err(int* err, int code) {
 TFA_DEV void head_raw(const uint16_t* raw, const float* part, int ks, size_t kstride, int lane,
                       float& x0, float& x1) {
   if (part) {
-    float a0 = 0.f, a1 = 0.f;
-    for (int s = 0; s < ks; ++s) {
-      a0 += part[s * kstride + lane];
-      a1 += part[s * kstride + lane + 64];
-    }
-    x0 = round_bf(a0);
-    x1 = round_bf(a1);
+    x0 = round_bf(sum_splits(part + lane, kstride, ks));
+    x1 = round_bf(sum_splits(part + lane + 64, kstride, ks));
   } else {
     x0 = bf2f(raw[lane]);
     x1 = bf2f(raw[lane + 64]);
@@ -411,6 +406,8 @@ int tfa_decode_attention(const void* q, const float* qkv_part, int64_t part_ks,
     return fail(TFA_ERR_NULL, "tfa_decode_attention: fused mode needs gamma_k, cos, sin, pos");
   if (qkv_part && (!gamma_q || part_ks < 1))
     return fail(TFA_ERR_ARG, "tfa_decode_attention: partials are a fused-mode source (gamma_q, ks >= 1)");
+  if (qkv_part && part_ks > kMaxSplitsK)
+    return fail(TFA_ERR_SHAPE, "tfa_decode_attention: part_ks %lld exceeds %d", (long long)part_ks, kMaxSplitsK);
   AttnArgs a{};
   a.q = qkv_part ? nullptr : static_cast<const uint16_t*>(q);
   a.part = qkv_part;

@@ -147,6 +147,47 @@ TFA_DEV float block_sum(float v, float* scratch) {
   return t;
 }
 
+// ------------------------------------------------------------ split-K sums
+// Sum of the first `ks` (<= MAXKS) of p[0], p[stride], p[2 stride], ... in split
+// order, with every load issued before the first add: one memory round trip,
+// not one per split (a runtime-bounded loop waits for each load in turn).
+constexpr int kMaxSplitsK = 8;
+template <int MAXKS = kMaxSplitsK>
+TFA_DEV float sum_splits(const float* p, size_t stride, int ks) {
+  float v[MAXKS];
+#pragma unroll
+  for (int s = 0; s < MAXKS; ++s) v[s] = s < ks ? p[s * stride] : 0.f;
+  float acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < MAXKS; ++s)
+    if (s < ks) acc += v[s];
+  return acc;
+}
+
+// The same for eight consecutive floats (two 16-byte loads per split);
+// p 16-byte aligned, stride a multiple of 4.
+template <int MAXKS = kMaxSplitsK>
+TFA_DEV void sum_splits8(const float* p, size_t stride, int ks, float* acc) {
+  float4 v[MAXKS][2];
+#pragma unroll
+  for (int s = 0; s < MAXKS; ++s) {
+    if (s < ks) {
+      const float4* q = reinterpret_cast<const float4*>(p + s * stride);
+      v[s][0] = q[0];
+      v[s][1] = q[1];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (int s = 0; s < MAXKS; ++s) {
+    if (s < ks) {
+      acc[0] += v[s][0].x; acc[1] += v[s][0].y; acc[2] += v[s][0].z; acc[3] += v[s][0].w;
+      acc[4] += v[s][1].x; acc[5] += v[s][1].y; acc[6] += v[s][1].z; acc[7] += v[s][1].w;
+    }
+  }
+}
+
 // 1/sqrt(x) with correctly rounded sqrt and division: the value torch's CPU
 // `rsqrt` returns for the same f32 input.
 TFA_DEV float rsqrt_rn(float x) { return 1.0f / __fsqrt_rn(x); }

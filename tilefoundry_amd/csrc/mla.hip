@@ -81,9 +81,7 @@ __global__ __launch_bounds__(kThreads) void mla_prep_kernel(
   const size_t kstride = static_cast<size_t>(B) * row;
   const float* pb = part + static_cast<size_t>(b) * row;
   auto reduced = [&](int i) {
-    float acc = 0.f;
-    for (int s = 0; s < ks; ++s) acc += pb[s * kstride + i];
-    return round_bf(acc);   // the projection lands in bf16
+    return round_bf(sum_splits(pb + i, kstride, ks));   // the projection lands in bf16
   };
 
   // q_a -> LoRA norm
@@ -145,8 +143,7 @@ __global__ __launch_bounds__(kThreads) void mla_q_absorb_kernel(
   for (int e = t; e < B * (kNope + kRope); e += kThreads) {
     const int b = e / (kNope + kRope), i = e % (kNope + kRope);
     const float* src = qpart + static_cast<size_t>(b) * qrow + h * (kNope + kRope) + i;
-    float acc = 0.f;
-    for (int s = 0; s < ks; ++s) acc += src[s * kstride];
+    const float acc = sum_splits(src, kstride, ks);
     if (i < kNope) qn[b][i] = round_bf(acc);
     else qr[b][i - kNope] = round_bf(acc);
   }
@@ -296,10 +293,6 @@ __global__ __launch_bounds__(kThreads) void mla_attn_kernel(const MlaAttnArgs a)
       if (tt >= ntiles) break;
       const int buf = tt & 1;
       __syncthreads();   // buf holds tile tt; every wave is done with buf ^ 1
-      if (tt + 1 < ntiles) {   // tile tt + 1 sits in register slot j
-        stage(tt + 1, buf ^ 1, rl[j], rr[j]);
-        if (tt + 1 + D < ntiles) fetch(tt + 1 + D, rl[j], rr[j]);
-      }
 
       // scores of this wave's 16 positions against all heads
       const int prow = 16 * wid + n16;
@@ -380,6 +373,13 @@ __global__ __launch_bounds__(kThreads) void mla_attn_kernel(const MlaAttnArgs a)
           for (int mt = 0; mt < 3; ++mt)
             o_acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(aop[mt]), as_bf8(bop), o_acc[mt][nt], 0, 0, 0);
         }
+      }
+      // tile tt + 1 (register slot j, loaded while this tile was computed) goes
+      // to the other buffer, which every wave finished reading before this
+      // tile's first barrier; the slot is refilled D tiles ahead
+      if (tt + 1 < ntiles) {
+        stage(tt + 1, buf ^ 1, rl[j], rr[j]);
+        if (tt + 1 + D < ntiles) fetch(tt + 1 + D, rl[j], rr[j]);
       }
     }
   }
@@ -478,13 +478,8 @@ __global__ __launch_bounds__(kThreads) void rows_residual_kernel(
   const size_t e0 = (static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x) * 8;
   const size_t total = static_cast<size_t>(M) * N;
   if (e0 >= total) return;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < ks; ++s) {
-    const float4* p = reinterpret_cast<const float4*>(part + static_cast<size_t>(s) * total + e0);
-    const float4 x = p[0], y = p[1];
-    acc[0] += x.x; acc[1] += x.y; acc[2] += x.z; acc[3] += x.w;
-    acc[4] += y.x; acc[5] += y.y; acc[6] += y.z; acc[7] += y.w;
-  }
+  float acc[8];
+  sum_splits8(part + e0, total, ks, acc);
   float r[8];
   unpack8(ld16(res + e0), r);
   float o[8];
@@ -511,7 +506,7 @@ int tfa_mla_prep(const float* part, int64_t ks, int64_t batch, int64_t q_lora, c
   TFA_NONNULL(rope_cache);
   TFA_NONNULL(q_n);
   TFA_REQUIRE(batch >= 1 && batch <= 65535, TFA_ERR_SHAPE, "tfa_mla_prep: batch %lld out of range", (long long)batch);
-  TFA_REQUIRE(ks >= 1, TFA_ERR_SHAPE, "tfa_mla_prep: ks must be >= 1");
+  TFA_REQUIRE(ks >= 1 && ks <= kMaxSplitsK, TFA_ERR_SHAPE, "tfa_mla_prep: ks %lld not in [1, %d]", (long long)ks, kMaxSplitsK);
   TFA_REQUIRE(q_lora >= 1 && q_lora <= 4 * kThreads, TFA_ERR_SHAPE,
               "tfa_mla_prep: q_lora %lld not in [1, %d]", (long long)q_lora, 4 * kThreads);
   TFA_REQUIRE(cap >= 1 && rope_rows >= 1, TFA_ERR_SHAPE, "tfa_mla_prep: empty cache or rope table");
@@ -536,7 +531,8 @@ int tfa_mla_q_absorb(const float* q_part, int64_t ks, int64_t batch, int64_t hea
               (long long)batch, kMaxBatch);
   TFA_REQUIRE(heads >= 1 && heads <= kHeadRows, TFA_ERR_SHAPE, "tfa_mla_q_absorb: heads %lld not in [1, %d]",
               (long long)heads, kHeadRows);
-  TFA_REQUIRE(ks >= 1 && rope_rows >= 1, TFA_ERR_SHAPE, "tfa_mla_q_absorb: ks and rope_rows must be >= 1");
+  TFA_REQUIRE(ks >= 1 && ks <= kMaxSplitsK && rope_rows >= 1, TFA_ERR_SHAPE,
+              "tfa_mla_q_absorb: ks %lld not in [1, %d] or empty rope table", (long long)ks, kMaxSplitsK);
   TFA_ALIGN16(w_kv_b);
   mla_q_absorb_kernel<<<(int)heads, kThreads, 0, stream>>>(
       q_part, (int)ks, (int)batch, (int)heads, static_cast<const uint16_t*>(w_kv_b),
@@ -611,8 +607,8 @@ int tfa_rows_residual(const float* part, int64_t ks, const void* residual, float
   TFA_NONNULL(part);
   TFA_NONNULL(residual);
   TFA_NONNULL(out);
-  TFA_REQUIRE(ks >= 1 && m >= 1 && n >= 8 && n % 8 == 0, TFA_ERR_SHAPE,
-              "tfa_rows_residual: need ks >= 1, m >= 1 and n a positive multiple of 8");
+  TFA_REQUIRE(ks >= 1 && ks <= kMaxSplitsK && m >= 1 && n >= 8 && n % 8 == 0, TFA_ERR_SHAPE,
+              "tfa_rows_residual: need ks in [1, %d], m >= 1 and n a positive multiple of 8", kMaxSplitsK);
   TFA_ALIGN16(part);
   TFA_ALIGN16(residual);
   TFA_ALIGN16(out);

@@ -135,6 +135,7 @@ __global__ __launch_bounds__(256) void resid_rms_partials_kernel(
   float ss = 0.f;
   for (int i = threadIdx.x; i < H; i += blockDim.x) {
     float acc = 0.f;
+#pragma unroll 8
     for (int s = 0; s < sk; ++s) acc += p[static_cast<size_t>(s) * H + i];
     const float v = round_bf(bf2f(a[i]) + round_bf(acc));
     hout[i] = static_cast<uint16_t>(f2bf(v));

@@ -267,13 +267,8 @@ __global__ __launch_bounds__(kThreads) void rows_norm_kernel(
     if (ch >= nch) continue;
     unpack8(ld16(src + 8 * ch), v[c]);
     if (!table) {
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int s = 0; s < ks; ++s) {
-        const float4* p = reinterpret_cast<const float4*>(part + (static_cast<size_t>(s) * M + m) * H + 8 * ch);
-        const float4 a = p[0], b = p[1];
-        acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
-        acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
-      }
+      float acc[8];
+      sum_splits8(part + static_cast<size_t>(m) * H + 8 * ch, static_cast<size_t>(M) * H, ks, acc);
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[c][i] = round_bf(v[c][i] + round_bf(acc[i]));
     }
@@ -401,7 +396,8 @@ int tfa_rows_norm(const void* table, const int64_t* ids, int64_t vocab, const vo
   } else {
     TFA_NONNULL(h_in);
     TFA_NONNULL(part);
-    TFA_REQUIRE(ks >= 1, TFA_ERR_SHAPE, "tfa_rows_norm: ks must be >= 1");
+    TFA_REQUIRE(ks >= 1 && ks <= kMaxSplitsK, TFA_ERR_SHAPE, "tfa_rows_norm: ks %lld not in [1, %d]",
+                (long long)ks, kMaxSplitsK);
   }
   if (m == 0) return TFA_OK;
   rows_norm_kernel<<<(int)m, kThreads, 0, stream>>>(
