@@ -263,6 +263,23 @@ int tfa_mla_combine_up(const void* op, const float* mp, const float* lp, const i
 int tfa_rows_residual(const float* part, int64_t ks, const void* residual, float alpha, void* out,
                       int64_t m, int64_t n, hipStream_t stream);
 
+/* ------------------------------------------------- prefill (Qwen3.5 layer) */
+
+/* Causal GQA attention over a whole prompt with the output gate:
+ * out[n, h*256 + d] = bf16(bf16(o[n, h, d] / l) * bf16(sigmoid(gate[n, h, d]))),
+ * o = sum_{j <= n} bf16(exp(s - m)) v[j, h / (heads/kv_heads)] over the f32
+ * scores s = scale * q[n, h] . k[j, g] (bf16 MFMA, f32 accumulate). Element
+ * (n, h, d) of q / gate sits at q + n*q_rs + h*q_hs + d (k, v likewise per kv
+ * head), so q, gate, k and v can be read in place from the qkv projection's
+ * output. head_dim 256; n a multiple of 128; q/k/v strides multiples of 8,
+ * gate/out strides multiples of 4 (elements).
+ * Replaces: examples/qwen3_8_27b_prefill-tilelang/kernels/attention.py:313-438
+ * (attention_ws / attention_tir), model.py:305-324 (Attention.attention). */
+int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void* k, int64_t k_rs, int64_t k_hs,
+                          const void* v, int64_t v_rs, int64_t v_hs, const void* gate, int64_t g_rs,
+                          int64_t g_hs, void* out, int64_t o_rs, int64_t n, int64_t heads, int64_t kv_heads,
+                          int64_t head_dim, float scale, hipStream_t stream);
+
 /* ------------------------------------------------------------ measurement */
 
 /* dst[0:bytes) = src[0:bytes) with the decode kernels' own access pattern

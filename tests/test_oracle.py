@@ -310,3 +310,87 @@ def test_mla_absorbed_f64_brute_force():
         ref = [sum(o[c] * float(w.w_kv_b[h * 32 + 16 + v, c]) for c in range(cfg.kv_lora)) for v in range(16)]
         ref = torch.tensor(ref, dtype=torch.float64)
         assert float((got[h] - ref).abs().max()) <= float(ref.abs().max()) * 2 ** -7
+
+
+# ---------------------------------------------------------------- prefill attention layer
+def _prefill_small():
+    from oracle import prefill as OP
+
+    cfg = OP.PrefillConfig(hidden=64, heads=4, kv_heads=2, head_dim=16, rot=8)
+    return OP, cfg, OP.random_layer(cfg, seed=5, std=0.2)
+
+
+def test_prefill_rope_tables_against_closed_form():
+    from oracle import prefill as OP
+
+    cos, sin = OP.rope_tables(9000)
+    i = torch.arange(32, dtype=torch.float64)
+    inv = 1.0 / (1.0e7 ** (2 * i / 64))
+    for p in (0, 3, 4095, 8191):
+        assert int(bf16_ulps(cos[p, :32], torch.cos(p * inv).to(BF)).max()) <= 1
+        assert int(bf16_ulps(sin[p, 32:], torch.sin(p * inv).to(BF)).max()) <= 1
+
+
+def test_prefill_causal_prefix_invariance():
+    OP, cfg, w = _prefill_small()
+    cos, sin = OP.rope_tables(16, cfg)
+    hn = torch.randn(12, cfg.hidden, generator=g(40)).to(BF)
+    hn2 = hn.clone()
+    hn2[7:] = torch.randn(5, cfg.hidden, generator=g(41)).to(BF)
+    outs = []
+    for x in (hn, hn2):
+        q, gate, k, v = OP.qkv(x, w["w_q"], w["w_k"], w["w_v"], w["gamma_q"], w["gamma_k"], cos, sin, cfg)
+        outs.append(OP.attention(q, k, v, gate, cfg))
+    assert torch.equal(outs[0][:7], outs[1][:7])
+    assert not torch.equal(outs[0][7:], outs[1][7:])
+
+
+def test_prefill_one_row_returns_gated_value():
+    OP, cfg, w = _prefill_small()
+    q = torch.randn(1, cfg.heads, cfg.head_dim, generator=g(42)).to(BF)
+    gate = torch.randn(1, cfg.heads, cfg.head_dim, generator=g(43)).to(BF)
+    k = torch.randn(1, cfg.kv_heads, cfg.head_dim, generator=g(44)).to(BF)
+    v = torch.randn(1, cfg.kv_heads, cfg.head_dim, generator=g(45)).to(BF)
+    out = OP.attention(q, k, v, gate, cfg).view(cfg.heads, -1)
+    for h in range(cfg.heads):
+        ref = v[0, h // cfg.group].double() / (1.0 + torch.exp(-gate[0, h].double()))
+        assert int(bf16_ulps(out[h], ref.to(BF)).max()) <= 1
+
+
+def test_prefill_identical_keys_give_running_mean():
+    OP, cfg, w = _prefill_small()
+    N = 9
+    q = torch.randn(N, cfg.heads, cfg.head_dim, generator=g(46)).to(BF)
+    k = torch.randn(1, cfg.kv_heads, cfg.head_dim, generator=g(47)).to(BF).expand(N, -1, -1).contiguous()
+    v = torch.randn(N, cfg.kv_heads, cfg.head_dim, generator=g(48)).to(BF)
+    gate = torch.full((N, cfg.heads, cfg.head_dim), 30.0).to(BF)        # sigmoid(30) == 1 in bf16
+    out = OP.attention(q, k, v, gate, cfg).view(N, cfg.heads, -1).double()
+    for i in range(N):
+        for h in range(cfg.heads):
+            ref = v[: i + 1, h // cfg.group].double().mean(0)
+            assert float((out[i, h] - ref).abs().max()) <= 2 ** -6 * float(ref.abs().max()) + 1e-3
+
+
+def test_prefill_attention_f64_brute_force_and_causality():
+    import math
+
+    OP, cfg, w = _prefill_small()
+    N, D = 6, cfg.head_dim
+    q = torch.randn(N, cfg.heads, D, generator=g(49)).to(BF)
+    k = torch.randn(N, cfg.kv_heads, D, generator=g(50)).to(BF)
+    v = torch.randn(N, cfg.kv_heads, D, generator=g(51)).to(BF)
+    gate = torch.randn(N, cfg.heads, D, generator=g(52)).to(BF)
+    out = OP.attention(q, k, v, gate, cfg).view(N, cfg.heads, D).double()
+    for i in range(N):
+        for h in range(cfg.heads):
+            kv = h // cfg.group
+            s = [cfg.scale * sum(float(q[i, h, d]) * float(k[j, kv, d]) for d in range(D)) for j in range(i + 1)]
+            mx = max(s)
+            e = [math.exp(x - mx) for x in s]
+            o = [sum(e[j] * float(v[j, kv, d]) for j in range(i + 1)) / sum(e) for d in range(D)]
+            ref = torch.tensor([o[d] / (1 + math.exp(-float(gate[i, h, d]))) for d in range(D)], dtype=torch.float64)
+            assert float((out[i, h] - ref).abs().max()) <= 2 ** -6 * float(ref.abs().max())
+    # planted mistake: without the causal mask row 0 would see every key
+    s = (q[0, 0].float() @ k[:, 0].float().t()) * cfg.scale
+    full = (torch.softmax(s, -1).to(BF).float() @ v[:, 0].float()).to(BF) * torch.sigmoid(gate[0, 0])
+    assert not torch.equal(full, out[0, 0].to(BF))

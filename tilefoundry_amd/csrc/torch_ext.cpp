@@ -471,6 +471,32 @@ void rows_residual(const Tensor& part, const Tensor& residual, double alpha, con
                                  (float)alpha, out.data_ptr(), M, N, stream_of(out)));
 }
 
+// ------------------------------------------------------------ prefill
+// q / gate: (n, heads, 256) views, k / v: (n, kv_heads, 256) views, each with a
+// unit innermost stride (views into the packed qkv projection output allowed);
+// out (n, heads*256) contiguous.
+void prefill_attention(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& gate,
+                       const Tensor& out, double scale) {
+  auto view3 = [](const Tensor& t, const char* name) {
+    if (!t.defined() || !t.is_cuda()) bad(std::string(name) + ": must be a GPU tensor");
+    if (t.scalar_type() != BF) bad(std::string(name) + ": expected bfloat16");
+    if (t.dim() != 3 || t.stride(2) != 1) bad(std::string(name) + ": expected a (n, heads, d) view with unit inner stride");
+  };
+  view3(q, "q");
+  view3(k, "k");
+  view3(v, "v");
+  view3(gate, "gate");
+  const int64_t N = q.size(0), HQ = q.size(1), Dh = q.size(2), HKV = k.size(1);
+  if (k.size(0) != N || v.size(0) != N || gate.size(0) != N || v.size(1) != HKV || gate.size(1) != HQ ||
+      k.size(2) != Dh || v.size(2) != Dh || gate.size(2) != Dh)
+    bad("prefill_attention: q/gate (n, heads, d) and k/v (n, kv_heads, d) shapes disagree");
+  need(out, "out", BF, N * HQ * Dh);
+  raise_status(tfa_prefill_attention(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+                                     v.data_ptr(), v.stride(0), v.stride(1), gate.data_ptr(), gate.stride(0),
+                                     gate.stride(1), out.data_ptr(), HQ * Dh, N, HQ, HKV, Dh, (float)scale,
+                                     stream_of(out)));
+}
+
 void copy_stream(const Tensor& src, const Tensor& dst) {
   if (!src.is_cuda() || !dst.is_cuda() || !src.is_contiguous() || !dst.is_contiguous())
     bad("copy_stream: contiguous GPU tensors required");
@@ -507,4 +533,5 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("mla_attention", &mla_attention);
   m.def("mla_combine_up", &mla_combine_up);
   m.def("rows_residual", &rows_residual);
+  m.def("prefill_attention", &prefill_attention);
 }
