@@ -19,13 +19,14 @@ constexpr int kWave = 64;
 // ---------------------------------------------------------------- bf16 bits
 TFA_DEV float bf2f(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
-TFA_DEV uint32_t f2bf(float f) {
-  // Round to nearest even; NaN stays a quiet NaN (torch's c10::BFloat16 rule).
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+// f32 -> bf16 on gfx950's v_cvt_pk_bf16_f32: round to nearest even (the rule
+// torch's c10::BFloat16 applies to finite values), two values per instruction.
+typedef float tfa_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 tfa_bf16x2 __attribute__((ext_vector_type(2)));
+TFA_DEV uint32_t pack_bf(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(tfa_f32x2{lo, hi}, tfa_bf16x2));
 }
+TFA_DEV uint32_t f2bf(float f) { return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f))); }
 
 // bf16 round trip: the value f takes after landing in bf16.
 TFA_DEV float round_bf(float f) { return bf2f(f2bf(f)); }
@@ -34,7 +35,6 @@ TFA_DEV float round_bf(float f) { return bf2f(f2bf(f)); }
 TFA_DEV float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
 TFA_DEV float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-TFA_DEV uint32_t pack_bf(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
 
 // 8 bf16 (one 16-byte vector) <-> 8 floats
 TFA_DEV void unpack8(const uint4 v, float* f) {

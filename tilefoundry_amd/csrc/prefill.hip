@@ -2,23 +2,26 @@
 // (Qwen3.5-family full-attention layer, Qwen3.8-27B shapes: 24 query heads
 // over 4 key/value heads), on bf16 MFMA.
 //
-// One 256-thread block per (query head, 128 query rows); each wave owns 32
-// query rows and walks the key tiles (32 keys) up to its diagonal. Per tile:
+// One 512-thread block per (query head, 128 query rows); each pair of waves
+// owns 32 query rows -- one wave per half of the head dims -- and walks the
+// key tiles (32 keys) up to its diagonal. Per tile:
 //
-//   S^T = K . Q^T     v_mfma_f32_32x32x16_bf16, M = 32 keys, N = 32 queries,
-//                     16 k-steps over D; K from LDS (row reads), Q resident
-//                     in registers as the B operand.
+//   S^T = K . Q^T     v_mfma_f32_32x32x16_bf16, M = 32 keys, N = 32 queries;
+//                     each wave of the pair reduces its 128 dims (8 k-steps,
+//                     its half of Q resident as the B operand, K from LDS row
+//                     reads) and the two partials are added through LDS.
 //   online softmax    per query (the MFMA output column): the lane holds 16
 //                     of the tile's keys, its partner lane (l ^ 32) the other
 //                     16 -- one exchange for the row max; exp2 with the
 //                     scale folded in; O rescaled only when a row max grows.
-//   O^T += V^T . P^T  M = 32 value dims (8 tiles over D), K = 16 keys per
-//                     step; P^T is the bf16 score accumulator itself (its key
+//   O^T += V^T . P^T  M = 32 value dims (4 tiles over the wave's half of D),
+//                     K = 16 keys per step; P^T is the bf16 score accumulator (its key
 //                     slots relabelled), V^T comes from ds_read_b64_tr_b16
 //                     transpose reads of the row-major V tile.
 //
 // K and V tiles stream global -> LDS with global_load_lds_dwordx4 (no register
-// staging), double-buffered; 70 KB of LDS per block, two blocks per CU.
+// staging), double-buffered; with the score exchange 103 KB of LDS per block,
+// two waves per SIMD.
 // Epilogue in the reference's order: out = bf16(bf16(o / l) * bf16(sigmoid(gate))).
 //
 // Reference (jingchangshi/TileFoundry): examples/qwen3_8_27b_prefill-tilelang/model.py:305-324
@@ -61,9 +64,11 @@ struct FlashArgs {
 // row): the K operand read (16 rows, one 16-byte chunk per half-wave) is
 // conflict-free. V rows are padded to 576 bytes (+16 banks per row): the
 // transpose reads (4 rows x 64 bytes per half-wave) are conflict-free. Every
-// operand address is then one per-lane base plus an immediate offset.
+// operand address is one per-lane base plus an immediate offset.
 constexpr int kKPitch = D + 8;    // elements
 constexpr int kVPitch = D + 32;
+constexpr int kPairs = 4;         // wave pairs per block, 32 queries each
+constexpr int kHalf = D / 2;      // head dims per wave of a pair
 
 TFA_DEV uint2 ld_tr(const uint16_t* lds_elem) {
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -72,58 +77,67 @@ TFA_DEV uint2 ld_tr(const uint16_t* lds_elem) {
 }
 
 // s_waitcnt immediates (gfx9 encoding): vmcnt(n) with expcnt / lgkmcnt left open.
-constexpr int kWaitVm16 = 16 | (7 << 4) | (15 << 8);
+constexpr int kWaitVm8 = 8 | (7 << 4) | (15 << 8);
 constexpr int kWaitVm0 = 0 | (7 << 4) | (15 << 8);
 
 template <int N>
 using IC = std::integral_constant<int, N>;
 
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// 512 threads: wave pair p owns queries q0 = 128 qt + 32 p; wave `half` of the
+// pair owns head dims [128 half, 128 half + 128) of the scores' reduction and
+// of the output. The pair's partial scores meet in LDS (f32 addition is
+// commutative, so both waves hold bit-identical scores and run the same
+// softmax).
+__global__ __launch_bounds__(2 * kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_prefill_kernel(const FlashArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t ks[2][kBN][kKPitch];
   __shared__ __attribute__((aligned(16))) uint16_t vs[2][kBN][kVPitch];
+  __shared__ float xch[kPairs][2][16][kWave];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = threadIdx.x / kWave;
+  const int pair = wid >> 1;
+  const int half = wid & 1;
   const int n32 = lane & 31;    // MFMA column (query) / row (key, value dim) index
   const int kg = lane >> 5;     // k-group
   const int h = blockIdx.x;
   const int qt = gridDim.y - 1 - blockIdx.y;   // the longest query tiles first
   const int g = h / (a.HQ / a.HKV);
-  const int q0 = qt * kBM + wid * 32;          // this wave's first query row
+  const int q0 = qt * kBM + pair * 32;         // the pair's first query row
   const int ntiles = (qt + 1) * kBM / kBN;     // key tiles the block walks
-  const int my_last = q0 / kBN;                // this wave's diagonal tile
+  const int my_last = q0 / kBN;                // the pair's diagonal tile
 
-  // direct global -> LDS tile loads, one row per instruction (lanes 0..31, 16
-  // bytes each): wave w moves rows 8w .. 8w+7 of K and of V
-  const uint16_t* kglob = a.k + static_cast<size_t>(8 * wid) * a.k_rs + g * a.k_hs + 8 * n32;
-  const uint16_t* vglob = a.v + static_cast<size_t>(8 * wid) * a.v_rs + g * a.v_hs + 8 * n32;
+  // direct global -> LDS tile loads, one 512-byte row per instruction (lanes
+  // 0..31): wave w moves rows 4w .. 4w+3 of K and of V
+  const uint16_t* kglob = a.k + static_cast<size_t>(4 * wid) * a.k_rs + g * a.k_hs + 8 * n32;
+  const uint16_t* vglob = a.v + static_cast<size_t>(4 * wid) * a.v_rs + g * a.v_hs + 8 * n32;
   auto load_tile = [&](int kt, auto bufc) __attribute__((always_inline)) {
     constexpr int buf = decltype(bufc)::value;
     const size_t k0 = static_cast<size_t>(kt) * kBN;
     if (lane < 32) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 4; ++i) {
         __builtin_amdgcn_global_load_lds(kglob + (k0 + i) * a.k_rs,
-                                         (__attribute__((address_space(3))) void*)&ks[buf][8 * wid + i][0], 16, 0, 0);
+                                         (__attribute__((address_space(3))) void*)&ks[buf][4 * wid + i][0], 16, 0, 0);
         __builtin_amdgcn_global_load_lds(vglob + (k0 + i) * a.v_rs,
-                                         (__attribute__((address_space(3))) void*)&vs[buf][8 * wid + i][0], 16, 0, 0);
+                                         (__attribute__((address_space(3))) void*)&vs[buf][4 * wid + i][0], 16, 0, 0);
       }
     }
   };
 
-  // Q resident: lane (query q0 + n32, k-group kg) holds Q[.][16 st + 8 kg .. +7]
-  uint4 qop[D / 16];
+  // this wave's half of Q, resident: lane (query q0 + n32, k-group kg) holds
+  // Q[.][128 half + 16 st + 8 kg .. +7]
+  uint4 qop[kHalf / 16];
   {
-    const uint16_t* qrow = a.q + static_cast<size_t>(q0 + n32) * a.q_rs + h * a.q_hs + 8 * kg;
+    const uint16_t* qrow = a.q + static_cast<size_t>(q0 + n32) * a.q_rs + h * a.q_hs + kHalf * half + 8 * kg;
 #pragma unroll
-    for (int st = 0; st < D / 16; ++st) qop[st] = ld16(qrow + 16 * st);
+    for (int st = 0; st < kHalf / 16; ++st) qop[st] = ld16(qrow + 16 * st);
   }
   load_tile(0, IC<0>{});
 
-  f32x16 o[D / 32];
+  f32x16 o[kHalf / 32];   // O^T rows (value dims) 128 half + 32 mt + ...
 #pragma unroll
-  for (int mt = 0; mt < D / 32; ++mt)
+  for (int mt = 0; mt < kHalf / 32; ++mt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[mt][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
@@ -134,30 +148,62 @@ void flash_prefill_kernel(const FlashArgs a) {
     constexpr int buf = decltype(bufc)::value;
     if (kt + 1 < ntiles) {
       load_tile(kt + 1, IC<buf ^ 1>{});
-      __builtin_amdgcn_s_waitcnt(kWaitVm16);   // this tile's loads are done, the next tile's fly
+      __builtin_amdgcn_s_waitcnt(kWaitVm8);   // this tile's loads are done, the next tile's fly
     } else {
       __builtin_amdgcn_s_waitcnt(kWaitVm0);
     }
     __syncthreads();
 
-    if (kt <= my_last) {   // wave-uniform: tiles past the diagonal hold no visible key
-      // S^T = K . Q^T: element e = 4j + r is key kt*32 + 8j + 4kg + r, query q0 + n32
-      f32x16 s;
+    const bool active = kt <= my_last;   // pair-uniform: later tiles hold no visible key
+    f32x16 s;
+    const uint16_t* vrow = &vs[buf][4 * kg + (L >> 2)][kHalf * half + 16 * half16 + 4 * (L & 3)];
+    uint4 vop0[kHalf / 32], vop1[kHalf / 32];
+    if (active) {
+      // partial S^T = K[:, half] . Q[:, half]^T: element e = 4j + r is key
+      // kt*32 + 8j + 4kg + r, query q0 + n32
+      const uint16_t* krow = &ks[buf][n32][kHalf * half + 8 * kg];
+      uint4 kop[kHalf / 16];
+#pragma unroll
+      for (int st = 0; st < kHalf / 16; ++st) kop[st] = *reinterpret_cast<const uint4*>(krow + 16 * st);
+      // V^T operands of this wave's value dims (A operand, row = value dim
+      // 128 half + 32 mt + n32): key rows 16 ks2 + 4kg + L/4 and +8
+#pragma unroll
+      for (int mt = 0; mt < kHalf / 32; ++mt) {
+        const uint2 v1 = ld_tr(vrow + 32 * mt);
+        const uint2 v2 = ld_tr(vrow + 8 * kVPitch + 32 * mt);
+        vop0[mt] = make_uint4(v1.x, v1.y, v2.x, v2.y);
+      }
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[e] = 0.f;
-      const uint16_t* krow = &ks[buf][n32][8 * kg];
 #pragma unroll
-      for (int st = 0; st < D / 16; ++st) {
-        const uint4 kop = *reinterpret_cast<const uint4*>(krow + 16 * st);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kop), as_bf8(qop[st]), s, 0, 0, 0);
+      for (int st = 0; st < kHalf / 16; ++st)
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kop[st]), as_bf8(qop[st]), s, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xch[pair][half][e][lane] = s[e];
+#pragma unroll
+      for (int mt = 0; mt < kHalf / 32; ++mt) {
+        const uint2 v1 = ld_tr(vrow + 16 * kVPitch + 32 * mt);
+        const uint2 v2 = ld_tr(vrow + 24 * kVPitch + 32 * mt);
+        vop1[mt] = make_uint4(v1.x, v1.y, v2.x, v2.y);
       }
-      const bool diag = kt == my_last;
+    }
+    __syncthreads();   // both halves of every pair's scores are in LDS
+
+    if (active) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {   // scaled (log2 units) and masked in place
-        const int kk = 8 * (e >> 2) + 4 * kg + (e & 3);
-        s[e] = (diag && kk > n32) ? -INFINITY : s[e] * a.scale_log2;
+      for (int e = 0; e < 16; ++e) {   // full score, scaled to log2 units in place
+        s[e] = (s[e] + xch[pair][half ^ 1][e][lane]) * a.scale_log2;
         mx = fmaxf(mx, s[e]);
+      }
+      if (kt == my_last) {   // the diagonal tile: keys past the query are masked
+        mx = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int kk = 8 * (e >> 2) + 4 * kg + (e & 3);
+          s[e] = kk > n32 ? -INFINITY : s[e];
+          mx = fmaxf(mx, s[e]);
+        }
       }
       mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
       const float m_new = fmaxf(m_run, mx);
@@ -165,36 +211,29 @@ void flash_prefill_kernel(const FlashArgs a) {
         const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
         l_run *= alpha;
 #pragma unroll
-        for (int mt = 0; mt < D / 32; ++mt)
+        for (int mt = 0; mt < kHalf / 32; ++mt)
 #pragma unroll
           for (int e = 0; e < 16; ++e) o[mt][e] *= alpha;
       }
       m_run = m_new;
       // O^T += V^T . P^T. P^T is the B operand: k-step ks2 takes keys
-      // 16ks2 + {4kg + r, 8 + 4kg + r} = score elements 8ks2 + r, 8ks2 + 4 + r.
-      // V^T (A operand, row = value dim 32mt + n32) by transpose reads of key
-      // rows 16ks2 + 4kg + L/4 and +8, columns 32mt + 16 half16 + 4 (L % 4)
-      const uint16_t* vrow = &vs[buf][4 * kg + (L >> 2)][16 * half16 + 4 * (L & 3)];
-#pragma unroll
-      for (int ks2 = 0; ks2 < 2; ++ks2) {
+      // 16ks2 + {4kg + r, 8 + 4kg + r} = score elements 8ks2 + r, 8ks2 + 4 + r
+      auto pv = [&](int ks2, const uint4* vop) __attribute__((always_inline)) {
         float p[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float x = s[8 * ks2 + i];
-          p[i] = x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(x - m_new);
+          p[i] = __builtin_amdgcn_exp2f(s[8 * ks2 + i] - m_new);   // masked keys: exp2(-inf) = 0
           l_run += p[i];
         }
         const uint4 pop = pack8(p);   // bf16 weights into the value product
 #pragma unroll
-        for (int mt = 0; mt < D / 32; ++mt) {
-          const uint2 v1 = ld_tr(vrow + (16 * ks2) * kVPitch + 32 * mt);
-          const uint2 v2 = ld_tr(vrow + (16 * ks2 + 8) * kVPitch + 32 * mt);
-          const uint4 vop = make_uint4(v1.x, v1.y, v2.x, v2.y);
-          o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vop), as_bf8(pop), o[mt], 0, 0, 0);
-        }
-      }
+        for (int mt = 0; mt < kHalf / 32; ++mt)
+          o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vop[mt]), as_bf8(pop), o[mt], 0, 0, 0);
+      };
+      pv(0, vop0);
+      pv(1, vop1);
     }
-    __syncthreads();   // every wave is done with buf before it is refilled
+    __syncthreads();   // every wave is done with buf and with xch before they are reused
   };
 
   for (int kt = 0; kt < ntiles; kt += 2) {   // ntiles is a multiple of 4
@@ -202,14 +241,15 @@ void flash_prefill_kernel(const FlashArgs a) {
     step(kt + 1, IC<1>{});
   }
 
-  // epilogue: element e = 4j + r of o[mt] is value dim 32mt + 8j + 4kg + r of query q0 + n32
+  // epilogue: element e = 4j + r of o[mt] is value dim 128 half + 32mt + 8j + 4kg + r
+  // of query q0 + n32
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
   const float inv = 1.0f / l_tot;
   const size_t qn = static_cast<size_t>(q0 + n32);
-  const uint16_t* grow = a.gate + qn * a.g_rs + h * a.g_hs;
-  uint16_t* orow = a.out + qn * a.o_rs + h * D;
+  const uint16_t* grow = a.gate + qn * a.g_rs + h * a.g_hs + kHalf * half;
+  uint16_t* orow = a.out + qn * a.o_rs + h * D + kHalf * half;
 #pragma unroll
-  for (int mt = 0; mt < D / 32; ++mt)
+  for (int mt = 0; mt < kHalf / 32; ++mt)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int d0 = 32 * mt + 8 * j + 4 * kg;
@@ -267,7 +307,7 @@ int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void*
   a.HKV = (int)kv_heads;
   a.scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid((unsigned)heads, (unsigned)(n / kBM));
-  flash_prefill_kernel<<<grid, kThreads, 0, stream>>>(a);
+  flash_prefill_kernel<<<grid, 2 * kThreads, 0, stream>>>(a);
   return launched("flash_prefill");
 }
 
