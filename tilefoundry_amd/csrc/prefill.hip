@@ -13,15 +13,16 @@
 //   online softmax    per query (the MFMA output column): the lane holds 16
 //                     of the tile's keys, its partner lane (l ^ 32) the other
 //                     16 -- one exchange for the row max; exp2 with the
-//                     scale folded in; O rescaled only when a row max grows.
+//                     scale folded in; the running max is only raised (and O
+//                     rescaled) when a row's max passes it by more than 2^8.
 //   O^T += V^T . P^T  M = 32 value dims (4 tiles over the wave's half of D),
 //                     K = 16 keys per step; P^T is the bf16 score accumulator (its key
 //                     slots relabelled), V^T comes from ds_read_b64_tr_b16
 //                     transpose reads of the row-major V tile.
 //
 // K and V tiles stream global -> LDS with global_load_lds_dwordx4 (no register
-// staging), double-buffered; with the score exchange 103 KB of LDS per block,
-// two waves per SIMD.
+// staging), three buffers deep (loads run two tiles ahead); with the score
+// exchange 138 KB of LDS per block, two waves per SIMD.
 // Epilogue in the reference's order: out = bf16(bf16(o / l) * bf16(sigmoid(gate))).
 //
 // Reference (jingchangshi/TileFoundry): examples/qwen3_8_27b_prefill-tilelang/model.py:305-324
@@ -57,6 +58,7 @@ struct FlashArgs {
   uint16_t* out;         // (n, h*256 + d) at out + n*o_rs + h*256 + d
   int q_rs, q_hs, k_rs, k_hs, v_rs, v_hs, g_rs, g_hs, o_rs;
   int N, HQ, HKV;
+  int xcd_heads;         // heads per XCD in the work order (0: plain order)
   float scale_log2;      // head_dim^-1/2 * log2(e)
 };
 
@@ -68,6 +70,7 @@ struct FlashArgs {
 constexpr int kKPitch = D + 8;    // elements
 constexpr int kVPitch = D + 32;
 constexpr int kPairs = 4;         // wave pairs per block, 32 queries each
+constexpr int kStages = 3;        // K / V tile buffers: loads run two tiles ahead
 constexpr int kHalf = D / 2;      // head dims per wave of a pair
 
 TFA_DEV uint2 ld_tr(const uint16_t* lds_elem) {
@@ -90,18 +93,31 @@ using IC = std::integral_constant<int, N>;
 // softmax).
 __global__ __launch_bounds__(2 * kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_prefill_kernel(const FlashArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kBN][kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t vs[2][kBN][kVPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t ks[kStages][kBN][kKPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[kStages][kBN][kVPitch];
   __shared__ float xch[kPairs][2][16][kWave];
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int wid = threadIdx.x / kWave;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);   // wave-uniform, scalar
   const int pair = wid >> 1;
   const int half = wid & 1;
   const int n32 = lane & 31;    // MFMA column (query) / row (key, value dim) index
   const int kg = lane >> 5;     // k-group
-  const int h = blockIdx.x;
-  const int qt = gridDim.y - 1 - blockIdx.y;   // the longest query tiles first
+  // Work order. Consecutive block ids are dispatched round-robin over the 8
+  // XCDs (each with its own L2); XCD x takes a run of consecutive heads --
+  // heads of one key/value group when the counts divide evenly -- so each L2
+  // holds one group's K and V, and within an XCD the longest query tiles go
+  // first.
+  const int nqt = a.N / kBM;
+  int h, qt;
+  if (a.xcd_heads > 0) {
+    const int x = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    h = x * a.xcd_heads + slot % a.xcd_heads;
+    qt = nqt - 1 - slot / a.xcd_heads;
+  } else {
+    h = blockIdx.x % a.HQ;
+    qt = nqt - 1 - blockIdx.x / a.HQ;
+  }
   const int g = h / (a.HQ / a.HKV);
   const int q0 = qt * kBM + pair * 32;         // the pair's first query row
   const int ntiles = (qt + 1) * kBM / kBN;     // key tiles the block walks
@@ -109,17 +125,17 @@ void flash_prefill_kernel(const FlashArgs a) {
 
   // direct global -> LDS tile loads, one 512-byte row per instruction (lanes
   // 0..31): wave w moves rows 4w .. 4w+3 of K and of V
-  const uint16_t* kglob = a.k + static_cast<size_t>(4 * wid) * a.k_rs + g * a.k_hs + 8 * n32;
-  const uint16_t* vglob = a.v + static_cast<size_t>(4 * wid) * a.v_rs + g * a.v_hs + 8 * n32;
-  auto load_tile = [&](int kt, auto bufc) __attribute__((always_inline)) {
-    constexpr int buf = decltype(bufc)::value;
-    const size_t k0 = static_cast<size_t>(kt) * kBN;
+  // (row pointers are wave-uniform: scalar base + the lane's 16-byte offset)
+  auto load_tile = [&](int kt, int buf) __attribute__((always_inline)) {
+    const size_t r0 = static_cast<size_t>(kt) * kBN + 4 * wid;
     if (lane < 32) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        __builtin_amdgcn_global_load_lds(kglob + (k0 + i) * a.k_rs,
+        const uint16_t* krow = a.k + (r0 + i) * a.k_rs + g * a.k_hs;
+        const uint16_t* vrow = a.v + (r0 + i) * a.v_rs + g * a.v_hs;
+        __builtin_amdgcn_global_load_lds(krow + 8 * n32,
                                          (__attribute__((address_space(3))) void*)&ks[buf][4 * wid + i][0], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vglob + (k0 + i) * a.v_rs,
+        __builtin_amdgcn_global_load_lds(vrow + 8 * n32,
                                          (__attribute__((address_space(3))) void*)&vs[buf][4 * wid + i][0], 16, 0, 0);
       }
     }
@@ -133,26 +149,29 @@ void flash_prefill_kernel(const FlashArgs a) {
 #pragma unroll
     for (int st = 0; st < kHalf / 16; ++st) qop[st] = ld16(qrow + 16 * st);
   }
-  load_tile(0, IC<0>{});
+  load_tile(0, 0);
+  if (ntiles > 1) load_tile(1, 1);
 
   f32x16 o[kHalf / 32];   // O^T rows (value dims) 128 half + 32 mt + ...
 #pragma unroll
   for (int mt = 0; mt < kHalf / 32; ++mt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[mt][e] = 0.f;
+  // Running row max (log2 units). It is only raised when some row's tile max
+  // passes it by more than kSlack, so the weights exp2(s - m) stay <= 2^kSlack
+  // (exact in f32, in range for bf16) and O is rescaled rarely; the final
+  // o / l is the same softmax.
+  constexpr float kSlack = 8.0f;
   float m_run = -INFINITY, l_run = 0.f;
 
   const int L = lane & 15;
   const int half16 = (lane >> 4) & 1;
-  auto step = [&](int kt, auto bufc) __attribute__((always_inline)) {
-    constexpr int buf = decltype(bufc)::value;
-    if (kt + 1 < ntiles) {
-      load_tile(kt + 1, IC<buf ^ 1>{});
-      __builtin_amdgcn_s_waitcnt(kWaitVm8);   // this tile's loads are done, the next tile's fly
-    } else {
-      __builtin_amdgcn_s_waitcnt(kWaitVm0);
-    }
-    __syncthreads();
+  int buf = 0;
+  for (int kt = 0; kt < ntiles; ++kt) {
+    if (kt + 1 < ntiles) __builtin_amdgcn_s_waitcnt(kWaitVm8);   // tile kt landed, kt + 1 may fly
+    else __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();   // tile kt visible; every wave is done with iteration kt - 1
+    if (kt + 2 < ntiles) load_tile(kt + 2, buf == 0 ? 2 : buf - 1);   // the buffer of tile kt - 1
 
     const bool active = kt <= my_last;   // pair-uniform: later tiles hold no visible key
     f32x16 s;
@@ -190,10 +209,11 @@ void flash_prefill_kernel(const FlashArgs a) {
     __syncthreads();   // both halves of every pair's scores are in LDS
 
     if (active) {
+      // full (unscaled) score; the scale is applied inside exp2's argument
       float mx = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {   // full score, scaled to log2 units in place
-        s[e] = (s[e] + xch[pair][half ^ 1][e][lane]) * a.scale_log2;
+      for (int e = 0; e < 16; ++e) {
+        s[e] += xch[pair][half ^ 1][e][lane];
         mx = fmaxf(mx, s[e]);
       }
       if (kt == my_last) {   // the diagonal tile: keys past the query are masked
@@ -205,24 +225,24 @@ void flash_prefill_kernel(const FlashArgs a) {
           mx = fmaxf(mx, s[e]);
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-      const float m_new = fmaxf(m_run, mx);
-      if (__builtin_amdgcn_ballot_w64(m_new > m_run) != 0) {   // some row max grew: rescale
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * a.scale_log2;   // log2 units (scale > 0)
+      if (__builtin_amdgcn_ballot_w64(mx > m_run + kSlack) != 0) {   // raise the max: rescale
+        const float m_new = fmaxf(m_run, mx);
         const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
         l_run *= alpha;
 #pragma unroll
         for (int mt = 0; mt < kHalf / 32; ++mt)
 #pragma unroll
           for (int e = 0; e < 16; ++e) o[mt][e] *= alpha;
+        m_run = m_new;
       }
-      m_run = m_new;
       // O^T += V^T . P^T. P^T is the B operand: k-step ks2 takes keys
       // 16ks2 + {4kg + r, 8 + 4kg + r} = score elements 8ks2 + r, 8ks2 + 4 + r
       auto pv = [&](int ks2, const uint4* vop) __attribute__((always_inline)) {
         float p[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          p[i] = __builtin_amdgcn_exp2f(s[8 * ks2 + i] - m_new);   // masked keys: exp2(-inf) = 0
+          p[i] = __builtin_amdgcn_exp2f(fmaf(s[8 * ks2 + i], a.scale_log2, -m_run));   // masked: exp2(-inf) = 0
           l_run += p[i];
         }
         const uint4 pop = pack8(p);   // bf16 weights into the value product
@@ -233,12 +253,7 @@ void flash_prefill_kernel(const FlashArgs a) {
       pv(0, vop0);
       pv(1, vop1);
     }
-    __syncthreads();   // every wave is done with buf and with xch before they are reused
-  };
-
-  for (int kt = 0; kt < ntiles; kt += 2) {   // ntiles is a multiple of 4
-    step(kt, IC<0>{});
-    step(kt + 1, IC<1>{});
+    buf = buf == kStages - 1 ? 0 : buf + 1;
   }
 
   // epilogue: element e = 4j + r of o[mt] is value dim 128 half + 32mt + 8j + 4kg + r
@@ -258,7 +273,9 @@ void flash_prefill_kernel(const FlashArgs a) {
       float y[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float sg = round_bf(1.0f / (1.0f + expf(-gx[r])));
+        // sigmoid from the hardware exp2 / reciprocal (within 2 f32 ulps; the
+        // result lands in bf16)
+        const float sg = round_bf(__builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gx[r] * 1.4426950408889634f)));
         y[r] = round_bf(round_bf(o[mt][4 * j + r] * inv) * sg);
       }
       *reinterpret_cast<uint2*>(orow + d0) = make_uint2(pack_bf(y[0], y[1]), pack_bf(y[2], y[3]));
@@ -306,8 +323,10 @@ int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void*
   a.HQ = (int)heads;
   a.HKV = (int)kv_heads;
   a.scale_log2 = scale * 1.4426950408889634f;
-  const dim3 grid((unsigned)heads, (unsigned)(n / kBM));
-  flash_prefill_kernel<<<grid, 2 * kThreads, 0, stream>>>(a);
+  // XCD-grouped order when every XCD gets whole heads of a single group
+  const int64_t per = heads / 8, group = heads / kv_heads;
+  a.xcd_heads = (heads % 8 == 0 && per >= 1 && (group % per == 0 || per % group == 0)) ? (int)per : 0;
+  flash_prefill_kernel<<<(unsigned)(heads * (n / kBM)), 2 * kThreads, 0, stream>>>(a);
   return launched("flash_prefill");
 }
 
