@@ -280,6 +280,27 @@ int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void*
                           int64_t g_hs, void* out, int64_t o_rs, int64_t n, int64_t heads, int64_t kv_heads,
                           int64_t head_dim, float scale, hipStream_t stream);
 
+/* C[m, n] = bf16(A[m, k] . B[n, k]^T) (residual == NULL) or
+ * C = bf16(residual + bf16(A . B^T)) (residual [m, ldr]); bf16 in, f32 accumulate,
+ * bf16 MFMA. Row strides lda / ldb / ldc in elements. m, n multiples of 256, k of
+ * 64; lda, ldb multiples of 8.
+ * Replaces: examples/qwen3_8_27b_prefill-tilelang/kernels/gemm.py:104-356 (gemm_kernel,
+ * "residual" epilogue :193-198 -- model.py:326-333 Attention.o_proj). */
+int tfa_gemm_nt(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
+                int64_t ldc, const void* residual, int64_t ldr, hipStream_t stream);
+
+/* The qkv projection of the Qwen3.5 attention layer: out[n, (2*heads + 2*kv_heads)*256]
+ * = hn[n, hidden] . w_qkv^T with w_qkv rows laid out [q_0 | gate_0 | ... | q_{H-1} |
+ * gate_{H-1} | k_0..k_{G-1} | v_0..v_{G-1}] (256 rows each); then per token the q
+ * and k slices get bf16(x * rsqrt(mean x^2 + eps) * (1 + gamma)) (f32) and
+ * rotate-half RoPE on dims 0..rot-1 with cos/sin [n, rot] (bf16 products and
+ * sum). head_dim 256, rot 64; n a multiple of 256, hidden of 64.
+ * Replaces: examples/qwen3_8_27b_prefill-tilelang/kernels/gemm.py:226-300 ("qk_norm_rope"
+ * epilogue), model.py:271-303 (Attention.qkv), kernels/pack.py:48-64 (the layout). */
+int tfa_qkv_norm_rope(const void* hn, const void* w_qkv, void* out, int64_t n, int64_t hidden, int64_t heads,
+                      int64_t kv_heads, int64_t head_dim, const void* gamma_q, const void* gamma_k, float eps,
+                      const void* cos_t, const void* sin_t, int64_t rot, hipStream_t stream);
+
 /* ------------------------------------------------------------ measurement */
 
 /* dst[0:bytes) = src[0:bytes) with the decode kernels' own access pattern

@@ -86,3 +86,114 @@ def test_prefill_attention_causal_prefix_4096(dev):
     ref = OP.attention(q[:, :1].contiguous(), k[:, :1].contiguous(), v[:, :1].contiguous(), gate[:, :1].contiguous(),
                        OP.PrefillConfig(heads=1, kv_heads=1))
     assert_close("head 0, whole prompt", a.cpu().view(n, HQ, D)[:, 0], ref.view(n, D))
+
+
+# ------------------------------------------------------------------ projections
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (512, 768, 320), (1024, 5120, 6144)])
+def test_gemm_nt(dev, M, N, K):
+    from tilefoundry_amd._lib import C
+
+    g = torch.Generator().manual_seed(M + N + K)
+    a = torch.randn(M, K, generator=g).to(BF)
+    b = (0.05 * torch.randn(N, K, generator=g)).to(BF)
+    c = torch.empty(M, N, dtype=BF, device=dev)
+    C.gemm_nt(a.to(dev), b.to(dev), c, None)
+    ref = a.float() @ b.float().t()
+    assert_close("gemm", c, ref.to(BF))
+    assert rel_l2(c, ref) < 4e-3
+
+
+@pytest.mark.gpu
+def test_gemm_exact_on_integers(dev):
+    from tilefoundry_amd._lib import C
+
+    g = torch.Generator().manual_seed(3)
+    a = torch.randint(-3, 4, (256, 512), generator=g).to(BF)
+    b = torch.randint(-3, 4, (512, 512), generator=g).to(BF)
+    c = torch.empty(256, 512, dtype=BF, device=dev)
+    C.gemm_nt(a.to(dev), b.to(dev), c, None)
+    assert_equal("integer gemm", c, (a.long() @ b.long().t()).float().to(BF))
+
+
+@pytest.mark.gpu
+def test_o_proj_residual(dev):
+    from tilefoundry_amd._lib import C
+
+    cfg = OP.PrefillConfig()
+    n = 256
+    g = torch.Generator().manual_seed(21)
+    gated = torch.randn(n, cfg.heads * D, generator=g).to(BF)
+    hidden = torch.randn(n, cfg.hidden, generator=g).to(BF)
+    w_o = (0.02 * torch.randn(cfg.hidden, cfg.heads * D, generator=g)).to(BF)
+    out = torch.empty(n, cfg.hidden, dtype=BF, device=dev)
+    C.gemm_nt(gated.to(dev), w_o.to(dev), out, hidden.to(dev))
+    ref = OP.o_proj(gated, hidden, w_o)
+    assert_close("o_proj + residual", out, ref)
+    frac = float((out.cpu() != ref).float().mean())
+    assert frac < 0.02, f"{frac:.3%} of outputs differ from the oracle"
+
+
+def _layer_weights(seed=5):
+    return OP.random_layer(CFG, seed=seed)
+
+
+def _pack_qkv(w):
+    wq = w["w_q"].view(HQ, 2 * D, CFG.hidden)
+    return torch.cat([wq.reshape(-1, CFG.hidden), w["w_k"], w["w_v"]], 0).contiguous()
+
+
+@pytest.mark.gpu
+def test_qkv_norm_rope(dev):
+    from tilefoundry_amd._lib import C
+
+    n = 256
+    w = _layer_weights()
+    g = torch.Generator().manual_seed(22)
+    hn = torch.randn(n, CFG.hidden, generator=g).to(BF)
+    cos, sin = OP.rope_tables(n, CFG)
+    W = (2 * HQ + 2 * HKV) * D
+    out = torch.empty(n, W, dtype=BF, device=dev)
+    C.qkv_norm_rope(hn.to(dev), _pack_qkv(w).to(dev), out, HQ, HKV, w["gamma_q"].to(dev), w["gamma_k"].to(dev),
+                    CFG.eps, cos.to(dev), sin.to(dev))
+    q, gate, k, v = OP.qkv(hn, w["w_q"], w["w_k"], w["w_v"], w["gamma_q"], w["gamma_k"], cos, sin, CFG)
+    o = out.cpu()
+    qg = o[:, : HQ * 2 * D].view(n, HQ, 2 * D)
+    assert_close("q", qg[..., :D], q)
+    assert_close("gate", qg[..., D:], gate)
+    assert_close("k", o[:, HQ * 2 * D: HQ * 2 * D + HKV * D].view(n, HKV, D), k)
+    assert_close("v", o[:, HQ * 2 * D + HKV * D:].view(n, HKV, D), v)
+    frac = float((qg[..., :D] != q).float().mean())
+    assert frac < 0.05, f"{frac:.3%} of q differs from the oracle"
+
+
+@pytest.mark.gpu
+def test_attention_layer_end_to_end(dev):
+    """qkv projection (+ norm / RoPE) -> causal gated attention read in place ->
+    o_proj + residual, against the oracle's layer at 256 tokens."""
+    from tilefoundry_amd._lib import C
+
+    n = 256
+    w = _layer_weights(seed=6)
+    g = torch.Generator().manual_seed(23)
+    hn = torch.randn(n, CFG.hidden, generator=g).to(BF)
+    hidden = torch.randn(n, CFG.hidden, generator=g).to(BF)
+    cos, sin = OP.rope_tables(n, CFG)
+    W = (2 * HQ + 2 * HKV) * D
+    qkv = torch.empty(n, W, dtype=BF, device=dev)
+    C.qkv_norm_rope(hn.to(dev), _pack_qkv(w).to(dev), qkv, HQ, HKV, w["gamma_q"].to(dev), w["gamma_k"].to(dev),
+                    CFG.eps, cos.to(dev), sin.to(dev))
+    qv = qkv[:, : HQ * 2 * D].view(n, HQ, 2 * D)
+    k0 = HQ * 2 * D
+    attn = torch.empty(n, HQ * D, dtype=BF, device=dev)
+    C.prefill_attention(qv[:, :, :D], qkv[:, k0: k0 + HKV * D].view(n, HKV, D),
+                        qkv[:, k0 + HKV * D:].view(n, HKV, D), qv[:, :, D:], attn, CFG.scale)
+    out = torch.empty(n, CFG.hidden, dtype=BF, device=dev)
+    C.gemm_nt(attn, w["w_o"].to(dev), out, hidden.to(dev))
+    q, gate, k, v = OP.qkv(hn, w["w_q"], w["w_k"], w["w_v"], w["gamma_q"], w["gamma_k"], cos, sin, CFG)
+    ref_attn = OP.attention(q, k, v, gate, CFG)
+    assert_close("attention", attn, ref_attn)
+    ref = OP.o_proj(ref_attn, hidden, w["w_o"])
+    assert_close("layer output", out, ref)
+    branch = out.cpu().float() - hidden.float()
+    assert rel_l2(branch, ref.float() - hidden.float()) < 0.1

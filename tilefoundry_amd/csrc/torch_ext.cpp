@@ -497,6 +497,46 @@ void prefill_attention(const Tensor& q, const Tensor& k, const Tensor& v, const 
                                      stream_of(out)));
 }
 
+// a [m, k], b [n, k] (row strides from the tensors), c [m, n]; residual [m, n] optional
+void gemm_nt(const Tensor& a, const Tensor& b, const Tensor& c, const OptT& residual) {
+  auto mat = [](const Tensor& t, const char* name) {
+    if (!t.defined() || !t.is_cuda() || t.scalar_type() != BF || t.dim() != 2 || t.stride(1) != 1)
+      bad(std::string(name) + ": expected a bf16 GPU matrix with unit inner stride");
+  };
+  mat(a, "a");
+  mat(b, "b");
+  mat(c, "c");
+  const int64_t M = a.size(0), K = a.size(1), N = b.size(0);
+  if (b.size(1) != K || c.size(0) != M || c.size(1) != N) bad("gemm_nt: shapes disagree");
+  const void* r = nullptr;
+  int64_t ldr = 0;
+  if (residual) {
+    mat(*residual, "residual");
+    if (residual->size(0) != M || residual->size(1) != N) bad("residual: expected (m, n)");
+    r = residual->data_ptr();
+    ldr = residual->stride(0);
+  }
+  raise_status(tfa_gemm_nt(a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, a.stride(0), b.stride(0),
+                           c.stride(0), r, ldr, stream_of(c)));
+}
+
+void qkv_norm_rope(const Tensor& hn, const Tensor& w_qkv, const Tensor& out, int64_t heads, int64_t kv_heads,
+                   const Tensor& gamma_q, const Tensor& gamma_k, double eps, const Tensor& cos, const Tensor& sin) {
+  need(hn, "hn", BF);
+  if (hn.dim() != 2) bad("hn: expected (n, hidden)");
+  const int64_t N = hn.size(0), H = hn.size(1), W = (2 * heads + 2 * kv_heads) * 256;
+  need_mat(w_qkv, "w_qkv", W, H);
+  need(out, "out", BF, N * W);
+  need(gamma_q, "gamma_q", BF, 256);
+  need(gamma_k, "gamma_k", BF, 256);
+  need(cos, "cos", BF);
+  need(sin, "sin", BF, cos.numel());
+  if (cos.numel() < N * 64) bad("cos / sin: expected at least (n, 64)");
+  raise_status(tfa_qkv_norm_rope(hn.data_ptr(), w_qkv.data_ptr(), out.data_ptr(), N, H, heads, kv_heads, 256,
+                                 gamma_q.data_ptr(), gamma_k.data_ptr(), (float)eps, cos.data_ptr(), sin.data_ptr(),
+                                 64, stream_of(out)));
+}
+
 void copy_stream(const Tensor& src, const Tensor& dst) {
   if (!src.is_cuda() || !dst.is_cuda() || !src.is_contiguous() || !dst.is_contiguous())
     bad("copy_stream: contiguous GPU tensors required");
@@ -534,4 +574,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("mla_combine_up", &mla_combine_up);
   m.def("rows_residual", &rows_residual);
   m.def("prefill_attention", &prefill_attention);
+  m.def("gemm_nt", &gemm_nt);
+  m.def("qkv_norm_rope", &qkv_norm_rope);
 }
