@@ -19,6 +19,10 @@ The JSON line also carries:
                 timed on this host on a bounded sample of the same workload
   kernels       the fused add+RMSNorm workload ([4096, 2048] bf16) and the
                 decode-layer GEMVs, each with achieved GB/s and HBM fraction
+  decode_layer_bs1_ctx4096   one decode layer over a 4096-position cache
+  bs32          the same greedy decode for 32 sequences (tok/s, all sequences)
+  mla_decode_b8_ctx8192      MiniCPM3-shaped absorbed MLA block, batch 8
+  prefill_attention_layer    Qwen3.5 attention layer at 1024 / 4096 / 8192 tokens
 """
 from __future__ import annotations
 
@@ -143,6 +147,181 @@ def kernel_lines(eng) -> dict:
     return out
 
 
+def decode_layer_ctx4096(eng) -> dict:
+    """One Qwen3 decode layer at bs=1 over a 4096-position cache (the single-layer
+    workload): the layer's six launches, timed over the 28 layers' weights; its
+    algorithmic bytes are the layer's weights plus the K and V it reads."""
+    from tilefoundry_amd._lib import C
+
+    cfg = eng.cfg
+    H, HQ, HKV, D = cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim
+    dev = eng.device
+    ctx = 4096
+    split = 64
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(1)
+    kc = torch.randn(ctx, HKV * D, device=dev, generator=g).to(bf)
+    vc = torch.randn(ctx, HKV * D, device=dev, generator=g).to(bf)
+    ns = ctx // split
+    op = torch.empty(ns, HQ, D, device=dev)
+    mp = torch.empty(ns, HQ, device=dev)
+    lp = torch.empty(ns, HQ, device=dev)
+    wr = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
+    from tilefoundry_amd.qwen3 import rope_tables
+    cos, sin = rope_tables(ctx, D, cfg.rope_theta, dev)
+    nqk = (HQ + HKV) * D
+    qk = torch.empty(nqk, device=dev, dtype=bf)
+    attn = torch.empty(HQ * D, device=dev, dtype=bf)
+    h = torch.randn(H, device=dev, generator=g).to(bf)
+    h1 = torch.empty_like(h)
+    act = torch.empty(cfg.inter, device=dev, dtype=bf)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def layer(w):
+        C.decode_qkv(h, None, None, None, w["gamma_in"], cfg.eps, w["w_qkv"], nqk, qk, wr, vc, err)
+        C.decode_attention(qk, None, w["gamma_q"], w["gamma_k"], cfg.eps, cos, sin, kc, vc, wr, wr, HQ, HKV,
+                           split, cfg.scale, op, mp, lp, False, err)
+        C.attn_combine(op, mp, lp, attn, wr, split)
+        C.gemv_residual(attn, w["w_o"], h, None, h1)
+        C.rmsnorm_gemv_swiglu(h1, w["gamma_post"], cfg.eps, w["w_gu"], act)
+        C.gemv_residual(act, w["w_down"], h1, None, h)
+
+    ms = _events_time(lambda: [layer(w) for w in eng.layers], 10) / len(eng.layers)
+    wbytes = sum(t.numel() * 2 for t in eng.layers[0].values())
+    kv = 2 * ctx * HKV * D * 2
+    nbytes = wbytes + kv
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    ms_attn = _events_time(lambda: (
+        C.decode_attention(qk, None, eng.layers[0]["gamma_q"], eng.layers[0]["gamma_k"], cfg.eps, cos, sin, kc,
+                           vc, wr, wr, HQ, HKV, split, cfg.scale, op, mp, lp, False, err),
+        C.attn_combine(op, mp, lp, attn, wr, split)), 50)
+    return {"workload": "one Qwen3-1.7B-shaped decode layer, bs=1, 4096 cached positions attended",
+            "us": round(ms * 1e3, 2), "bytes": int(nbytes), "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "attention_us": round(ms_attn * 1e3, 2),
+            "attention_GB/s": round(kv / (ms_attn * 1e-3) / 1e9, 1)}
+
+
+def batch32(seed: int, steps: int) -> dict:
+    """bs=32 greedy decode: 32 seeded 64-token prompts, `steps` new tokens each,
+    one captured step for all sequences."""
+    from tilefoundry_amd.qwen3 import BatchEngine, QWEN3_1_7B
+
+    cfg = QWEN3_1_7B
+    eng = BatchEngine(cfg, batch=32, device="cuda:0", max_new=steps, prompt_room=PROMPT, seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    prompts = torch.randint(0, cfg.vocab, (32, PROMPT), generator=g).tolist()
+    eng.generate(prompts, min(16, steps))     # warm
+    gen = eng.generate(prompts, steps)
+    weight_bytes = sum(t.numel() * 2 for w in eng.layers for t in w.values()) + eng.embed.numel() * 2
+    mean_ctx = PROMPT + steps / 2.0
+    kv_bytes = 32 * cfg.layers * mean_ctx * 2 * cfg.kv_heads * cfg.head_dim * 2
+    ms = gen.seconds * 1e3 / steps
+    out = {"value": round(gen.tokens_per_second, 1), "unit": "tok/s", "batch": 32, "new_tokens": steps,
+           "prompt_tokens": PROMPT, "ms_per_step": round(ms, 4),
+           "step_hbm": {"bytes_per_step": int(weight_bytes + kv_bytes),
+                        "GB/s": round((weight_bytes + kv_bytes) / (ms * 1e-3) / 1e9, 1)}}
+    del eng
+    torch.cuda.empty_cache()
+    return out
+
+
+def mla_decode() -> dict:
+    """MiniCPM3-4B-shaped MLA attention block, batch 8 x 8192 positions, absorbed:
+    the whole block (one captured step) and its attention core (split attention
+    over the compressed cache + merge / W_UV)."""
+    from tilefoundry_amd._lib import C
+    from tilefoundry_amd.minicpm3 import MLABlock, MiniCPM3Config
+
+    cfg = MiniCPM3Config()
+    B, cap = 8, 8192
+    blk = MLABlock(cfg, batch=B, cap=cap, device="cuda:0")
+    g = torch.Generator(device="cuda:0").manual_seed(2)
+    blk.latent.normal_(generator=g)
+    blk.rope_k.normal_(generator=g)
+    blk.hidden.normal_(generator=g)
+    blk.pos.fill_(cap - 1)
+    blk.capture()
+    ms_blk = _events_time(blk.run, 100)
+
+    def core():
+        C.mla_attention(blk.q_abs, blk.latent, blk.rope_k, blk.pos, blk.split, cfg.scale, blk.op, blk.mp,
+                        blk.lp, blk.err)
+        C.mla_combine_up(blk.op, blk.mp, blk.lp, blk.pos, blk.split, blk.w["w_kv_b"], blk.attn)
+
+    ms_core = _events_time(core, 100)
+    cache = B * cap * (cfg.kv_lora + cfg.rope) * 2
+    weights = sum(t.numel() * 2 for k, t in blk.w.items() if k.startswith("w_"))
+    out = {"workload": "MiniCPM3-4B-shaped MLA decode attention block, batch 8, 8192 positions, absorbed",
+           "block_us": round(ms_blk * 1e3, 2),
+           "block_bytes": int(cache + weights),
+           "block_GB/s": round((cache + weights) / (ms_blk * 1e-3) / 1e9, 1),
+           "attention_core_us": round(ms_core * 1e3, 2),
+           "attention_core_bytes": int(cache),
+           "attention_core_GB/s": round(cache / (ms_core * 1e-3) / 1e9, 1),
+           "attention_core_frac": round(cache / (ms_core * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del blk
+    torch.cuda.empty_cache()
+    return out
+
+
+def prefill_layer(ns=(1024, 4096, 8192)) -> dict:
+    """Qwen3.5 full-attention layer (hidden 5120, 24/4 heads, head_dim 256):
+    qkv projection with the q/k head norm + RoPE, causal gated attention read in
+    place, o_proj + residual; TFLOP/s by the reference's convention (attention
+    2*N^2*heads*head_dim)."""
+    from tilefoundry_amd._lib import C
+
+    dev = "cuda:0"
+    bf = torch.bfloat16
+    HID, HQ, HKV, D = 5120, 24, 4, 256
+    W = (2 * HQ + 2 * HKV) * D
+    g = torch.Generator(device=dev).manual_seed(3)
+    w_qkv = (0.02 * torch.randn(W, HID, device=dev, generator=g)).to(bf)
+    w_o = (0.02 * torch.randn(HID, HQ * D, device=dev, generator=g)).to(bf)
+    gq = (0.1 * torch.randn(D, device=dev, generator=g)).to(bf)
+    gk = (0.1 * torch.randn(D, device=dev, generator=g)).to(bf)
+    out = {}
+    for n in ns:
+        hn = torch.randn(n, HID, device=dev, generator=g).to(bf)
+        hidden = torch.randn(n, HID, device=dev, generator=g).to(bf)
+        inv = 1.0 / (1.0e7 ** (torch.arange(0, 64, 2, device=dev).float() / 64))
+        ph = torch.arange(n, device=dev).float()[:, None] * inv[None]
+        ph = torch.cat((ph, ph), -1)
+        cos, sin = ph.cos().to(bf), ph.sin().to(bf)
+        qkv = torch.empty(n, W, device=dev, dtype=bf)
+        attn = torch.empty(n, HQ * D, device=dev, dtype=bf)
+        res = torch.empty(n, HID, device=dev, dtype=bf)
+        qv = qkv[:, : HQ * 2 * D].view(n, HQ, 2 * D)
+        k0 = HQ * 2 * D
+        kv = qkv[:, k0: k0 + HKV * D].view(n, HKV, D)
+        vv = qkv[:, k0 + HKV * D:].view(n, HKV, D)
+        f_qkv = lambda: C.qkv_norm_rope(hn, w_qkv, qkv, HQ, HKV, gq, gk, 1e-6, cos, sin)
+        f_att = lambda: C.prefill_attention(qv[:, :, :D], kv, vv, qv[:, :, D:], attn, D ** -0.5)
+        f_o = lambda: C.gemm_nt(attn, w_o, res, hidden)
+        f_qkv()
+        reps = 20 if n <= 4096 else 8
+        t_qkv = _events_time(f_qkv, reps)
+        t_att = _events_time(f_att, reps)
+        t_o = _events_time(f_o, reps)
+        t_layer = _events_time(lambda: (f_qkv(), f_att(), f_o()), max(4, reps // 2))
+        fl_att = 12288.0 * n * n
+        fl_qkv = 2.0 * n * W * HID
+        fl_o = 2.0 * n * HID * HQ * D
+        tf = lambda fl, ms: round(fl / (ms * 1e-3) / 1e12, 1)
+        out[str(n)] = {"attention_us": round(t_att * 1e3, 1), "attention_TFLOP/s": tf(fl_att, t_att),
+                       "attention_frac": round(fl_att / (t_att * 1e-3) / 2.5e15, 4),
+                       "qkv_us": round(t_qkv * 1e3, 1), "qkv_TFLOP/s": tf(fl_qkv, t_qkv),
+                       "o_proj_us": round(t_o * 1e3, 1), "o_proj_TFLOP/s": tf(fl_o, t_o),
+                       "layer_us": round(t_layer * 1e3, 1),
+                       "layer_TFLOP/s": tf(fl_att + fl_qkv + fl_o, t_layer)}
+        del hn, hidden, qkv, attn, res
+    torch.cuda.empty_cache()
+    return {"workload": "Qwen3.5 full-attention layer (Qwen3.8-27B shapes), causal GQA 24/4 x 256, "
+                        "qkv (+head norm, RoPE 64 dims) + attention (+gate) + o_proj (+residual)",
+            "peak_TFLOP/s": 2500.0, "by_tokens": out}
+
+
 def copy_bandwidth(dev) -> dict:
     """Sustained HBM bandwidth of this device for the decode kernels' access
     pattern: a 2 GiB read + 2 GiB write copy with 16-byte streaming loads."""
@@ -206,6 +385,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel lines")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the bs=32, MLA and prefill measurements")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only launch the dominant kernel loop (for rocprofv3 counter runs)")
     args = ap.parse_args()
@@ -249,6 +430,7 @@ def main() -> int:
 
     roof = dominant_kernel(eng)
     kernels = {} if args.no_kernels else kernel_lines(eng)
+    layer = None if args.no_kernels else decode_layer_ctx4096(eng)
     copy_bw = copy_bandwidth(dev)
     weight_bytes = sum(t.numel() * 2 for w in eng.layers for t in w.values()) + eng.embed.numel() * 2
     mean_ctx = PROMPT + args.steps / 2.0
@@ -277,11 +459,16 @@ def main() -> int:
         "roofline": roof,
         "hbm_copy_measured": copy_bw,
         "kernels": kernels,
+        "decode_layer_bs1_ctx4096": layer,
         "first_tokens": gen.tokens[:8],
     }
+    del eng
+    torch.cuda.empty_cache()
+    if not args.no_configs:
+        line["bs32"] = batch32(args.seed, args.steps)
+        line["mla_decode_b8_ctx8192"] = mla_decode()
+        line["prefill_attention_layer"] = prefill_layer()
     if not args.no_cpu_baseline:
-        del eng
-        torch.cuda.empty_cache()
         line["cpu_baseline"] = cpu_baseline(args.seed, prompt)
     else:
         line["cpu_baseline"] = None
