@@ -102,6 +102,15 @@ int tfa_gemv_residual(const void* x, const void* w, const void* residual, const 
 int tfa_rmsnorm_gemv_swiglu(const void* h, const void* gamma, float eps, const void* w_gu,
                             void* act, int64_t inter, int64_t k, hipStream_t stream);
 
+/* The same SwiGLU with gate and up as two [inter, K] matrices (no interleaving):
+ * act[i] = bf16(bf16(silu(bf16 g_i)) * bf16 u_i), g = rmsnorm(h) . w_gate^T,
+ * u = rmsnorm(h) . w_up^T. Replaces
+ * examples/minicpm3_4b-cutedsl/kernels/reference_ops.py:66-70 (rmsnorm_gemv_swiglu)
+ * and kernels/cute_gemv.py:352-425 (NORM_GEMV_SWIGLU). */
+int tfa_rmsnorm_gemv_gate_up(const void* h, const void* gamma, float eps, const void* w_gate,
+                             const void* w_up, void* act, int64_t inter, int64_t k,
+                             hipStream_t stream);
+
 /* Number of (value, index) block entries tfa_lm_head_argmax writes for `vocab`. */
 int64_t tfa_lm_head_blocks(int64_t vocab);
 
@@ -114,6 +123,13 @@ int tfa_lm_head_argmax(const void* h, const void* gamma, float eps, const void* 
                        int64_t k, float* logits, float* block_val, int* block_idx,
                        hipStream_t stream);
 
+/* logits[n] = bf16(sum_k bf16(h[k] / divisor) w[n, k]) in bf16 (divisor != 0; a
+ * correctly rounded f32 divide, not a reciprocal multiply). w is [vocab, k].
+ * Replaces examples/minicpm3_4b-cutedsl/kernels/reference_ops.py:78-84
+ * (lm_head_gemv) and kernels/cute_gemv.py:500-531 (LM_HEAD). */
+int tfa_lm_head_gemv(const void* h, const void* w, float divisor, void* logits, int64_t vocab,
+                     int64_t k, hipStream_t stream);
+
 /* Greedy pick + sample step on the device: best = argmax over the block
  * winners (lowest index on ties); sam[pos] = best; ids[0] = pos+1 < prompt_len ?
  * inp[pos+1] : best; pos += 1. inp / sam are int32 [nsteps].
@@ -121,6 +137,20 @@ int tfa_lm_head_argmax(const void* h, const void* gamma, float eps, const void* 
 int tfa_sample_step(const float* block_val, const int* block_idx, int64_t nblocks, const int* inp,
                     const int* prompt_len, int64_t* ids, int* pos, int* sam, int64_t nsteps,
                     int* err, hipStream_t stream);
+
+/* act[r, i] = bf16(bf16(silu(bf16 g)) * bf16 u), g / u the sums over ks (<= 8)
+ * split-K partials part[ks, rows, 2 * inter] (gate in [0, inter), up in
+ * [inter, 2 inter)). Replaces examples/qwen3_1_7b-tilelang/fast/kernels.py:547-572
+ * (silu_mul). */
+int tfa_silu_mul(const float* part, int64_t ks, int64_t inter, int64_t rows, void* act,
+                 hipStream_t stream);
+
+/* out[r, :] = table[ids[r], :] (scaled == 0) or bf16(table[ids[r], :] * scale).
+ * hidden % 8 == 0. An id outside [0, vocab) reads row 0 and sets err = 1.
+ * Replaces examples/qwen3_1_7b-tilelang/fast/kernels.py:579-588 (embed) and
+ * examples/minicpm3_4b-cutedsl/kernels/reference_ops.py:72-76 (embed_scaled). */
+int tfa_embed(const void* table, const int64_t* ids, int64_t vocab, int64_t hidden, int64_t rows,
+              int scaled, float scale, void* out, int* err, hipStream_t stream);
 
 /* Decode q|k|v projection: x = rmsnorm(h) (or rmsnorm(table[ids[0]]) when
  * table != NULL, the gathered row also written to h_copy); y = x . w_qkv^T with
@@ -166,6 +196,19 @@ int tfa_decode_attention(const void* q, const float* qkv_part, int64_t part_ks,
 int tfa_attn_combine(const float* op, const float* mp, const float* lp, void* out, int64_t splits,
                      int64_t batch, int64_t hq, int64_t head_dim, const int* wr, int64_t split,
                      hipStream_t stream);
+
+/* Reduce the q|k|v split-K partials qkv_part [part_ks (<= 8), batch,
+ * (hq + 2 hkv) * 128] f32 (each value landing in bf16); per query head
+ * Qwen3RMSNorm (gamma_q, eps_head) + rotate-half RoPE at pos[b] -> q_out
+ * [batch, hq * 128]; the key head the same with gamma_k -> k_cache row wr[b];
+ * the value head as is -> v_cache row wr[b] (caches [batch, cap, hkv * 128]).
+ * err: 3 = wr out of [0, cap), 5 = pos out of [0, rope_rows).
+ * Replaces examples/qwen3_1_7b-tilelang/fast/kernels.py:328-411 (qk_rope_cache). */
+int tfa_qk_rope_cache(const float* qkv_part, int64_t part_ks, const void* gamma_q,
+                      const void* gamma_k, float eps_head, const void* cos_t, const void* sin_t,
+                      int64_t rope_rows, const int* pos, const int* wr, void* k_cache,
+                      void* v_cache, int64_t cap, void* q_out, int64_t batch, int64_t hq,
+                      int64_t hkv, int64_t head_dim, int* err, hipStream_t stream);
 
 /* --------------------------------------------- batched decode (<= 32 rows) */
 
@@ -255,6 +298,31 @@ int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* r
 int tfa_mla_combine_up(const void* op, const float* mp, const float* lp, const int* wr, int64_t splits,
                        int64_t split, int64_t batch, int64_t heads, int64_t cap, const void* w_kv_b,
                        void* attn, hipStream_t stream);
+
+/* Context splits (256 rows each) tfa_rope_attend uses for a cache of `cap` rows:
+ * the row count of its op / mp / lp workspace. */
+int64_t tfa_rope_attend_splits(int64_t cap);
+
+/* MiniCPM3 decode attention over the assembled per-head cache (non-absorbed):
+ * q_up [heads, nope + rope] and kv_up [heads, nope + v_dim] (this token's
+ * [k_nope | v]) bf16, k_rope [rope] the unrotated shared key slice; cos / sin
+ * [rope_rows, rope]; k_cache [cap, heads, nope + rope], v_cache [cap, heads,
+ * v_dim] of which the first ctx[0] rows are context; scale bf16 [1].
+ * q's rotary slice and k_rope are rotated at pos[0] (bf16 products and sum),
+ * q is multiplied by scale in bf16, scores are f32 dots, the f32 softmax runs
+ * over the context and the token itself, f32 weights into the value sum:
+ * attn [heads * v_dim] bf16; k_new [heads, nope + rope] = [k_nope | rotated
+ * k_rope] and v_new [heads, v_dim] (both optional). op / mp / lp: f32 workspace
+ * [tfa_rope_attend_splits(cap), heads, v_dim] / [.., heads] (unused when cap = 0).
+ * (nope + rope) % 8 == 0, <= 256; v_dim <= 128. err: 4 = ctx out of [0, cap],
+ * 5 = pos out of [0, rope_rows).
+ * Replaces examples/minicpm3_4b-cutedsl/kernels/reference_ops.py:87-130
+ * (rope_attend) and kernels/cute_attention.py:56-200 (ROPE_ATTEND). */
+int tfa_rope_attend(const void* q_up, const void* kv_up, const void* k_rope, const void* cos_t,
+                    const void* sin_t, int64_t rope_rows, const int* pos, const void* k_cache,
+                    const void* v_cache, int64_t cap, const int* ctx, const void* scale,
+                    int64_t heads, int64_t nope, int64_t rope, int64_t v_dim, float* op, float* mp,
+                    float* lp, void* attn, void* k_new, void* v_new, int* err, hipStream_t stream);
 
 /* out[i, j] = bf16(residual[i, j] + bf16(bf16(sum_s part[s, i, j]) * alpha)) for
  * part [ks, m, n] f32 split-K partials (n % 8 == 0): the o_proj epilogue with

@@ -27,6 +27,11 @@ What each function follows (jingchangshi/TileFoundry):
   (model.py:28-38 caches assembled K/V); this is pinned to ``attend_reference``
   by the identity ``q_nope . (W_UK c) = (W_UK^T q_nope) . c`` and
   ``sum_j p_j W_UV c_j = W_UV sum_j p_j c_j``.
+* ``rope_attend`` -- ``reference_ops.rope_attend`` itself (reference_ops.py:87-130)
+  over the assembled cache ``k [cap, heads, 96]``, ``v [cap, heads, 64]`` with
+  ``ctx`` context rows and this token's own key and value: the rotary slices
+  rotated in bf16, ``q * scale`` in bf16, f32 scores against the context and
+  the token, one f32 softmax (a joint max), f32 weighted sum, one landing.
 * ``o_proj_residual`` -- ``gemv_residual``, reference_ops.py:63-65:
   ``residual + bf16(x @ W_o^T) * alpha``, each step landing in bf16.
 
@@ -183,6 +188,64 @@ def attend_reference(q_up, latent_ctx, rope_ctx, wts: MLAWeights, cfg: MLAConfig
     e = torch.exp(s - s.amax(-1, keepdim=True))
     weighted = torch.einsum("hn,nhv->hv", e, v.float())
     return (weighted / e.sum(-1, keepdim=True)).reshape(-1).to(BF16)
+
+
+def rope_attend(q_up, kv_up, k_rope, cos, sin, pos: int, k_cache, v_cache, ctx: int, scale,
+                heads: int, nope: int, rope: int, v_dim: int, drop_new: bool = False):
+    """Returns ``(attn [heads * v_dim], k_new [heads * (nope + rope)], v_new
+    [heads * v_dim])`` bf16. ``k_cache`` [cap, heads, nope + rope] and
+    ``v_cache`` [cap, heads, v_dim] hold ``ctx`` context rows; ``scale`` is the
+    bf16 factor. ``drop_new`` plants a mistake for the pinning tests (the
+    token's own score left out of the softmax)."""
+    qk = nope + rope
+    c, s = cos[pos], sin[pos]
+    q = q_up.view(heads, qk)
+    kv = kv_up.view(heads, nope + v_dim)
+    q_full = torch.cat((q[:, :nope], rope32(q[:, nope:], c, s)), dim=-1)
+    k_rot = rope32(k_rope.view(rope), c, s)
+    k_full = torch.cat((kv[:, :nope], k_rot.view(1, rope).expand(heads, rope)), dim=-1)
+    v_full = kv[:, nope:]
+    qh = (q_full * torch.as_tensor(scale).to(BF16).reshape(())).float()          # bf16 product
+    score_new = (qh * k_full.float()).sum(-1)                                     # [H]
+    if ctx == 0:
+        weighted, total = v_full.float(), torch.ones_like(score_new)
+    else:
+        kc = k_cache[:ctx].float().permute(1, 0, 2)                               # [H, n, qk]
+        vc = v_cache[:ctx].float().permute(1, 0, 2)
+        score_ctx = torch.einsum("hd,hnd->hn", qh, kc)
+        peak = score_ctx.amax(-1) if drop_new else torch.maximum(score_ctx.amax(-1), score_new)
+        p_ctx = torch.exp(score_ctx - peak[:, None])
+        p_new = torch.zeros_like(peak) if drop_new else torch.exp(score_new - peak)
+        total = p_ctx.sum(-1) + p_new
+        weighted = torch.einsum("hn,hnv->hv", p_ctx, vc) + p_new[:, None] * v_full.float()
+    out = (weighted / total[:, None]).reshape(-1).to(BF16)
+    return out, k_full.reshape(-1).contiguous(), v_full.reshape(-1).contiguous()
+
+
+def mla_attention(hidden, wts: MLAWeights, cfg: MLAConfig, pos: int, cos, sin, k_cache, v_cache,
+                  ctx: int, scale):
+    """``mla_attention`` of model.py:205-291 in the ``reference_ops`` spelling
+    (runtime_model.py:146-186): input norm -> ``[q_a | kv_a]`` projection ->
+    LoRA norms -> ``q_b`` / ``kv_b`` -> ``rope_attend`` over the assembled cache
+    -> ``W_o``. Returns ``(out [hidden], k_new, v_new)`` bf16."""
+    x = rms_norm_q(hidden, wts.gamma_in, cfg.eps)
+    q_a = proj(x, wts.w_q_a)
+    comp = proj(x, wts.w_kv_a)
+    q_up = proj(rms_norm_q(q_a, wts.gamma_q_a, cfg.lora_eps), wts.w_q_b)
+    kv_up = proj(rms_norm_q(comp[: cfg.kv_lora], wts.gamma_kv_a, cfg.lora_eps), wts.w_kv_b)
+    attn, k_new, v_new = rope_attend(q_up, kv_up, comp[cfg.kv_lora:], cos, sin, pos, k_cache,
+                                     v_cache, ctx, scale, cfg.heads, cfg.nope, cfg.rope, cfg.v_dim)
+    return proj(attn, wts.w_o), k_new, v_new
+
+
+def assembled_cache(latent_ctx, rope_ctx, wts: MLAWeights, cfg: MLAConfig):
+    """The per-head cache Hugging Face keeps for a compressed one:
+    ``k [n, heads, nope + rope]`` = ``[bf16(c W_UK^T) | k_rope]``, ``v [n, heads,
+    v_dim]`` = ``bf16(c W_UV^T)`` (model.py:28-38)."""
+    n, H = latent_ctx.shape[0], cfg.heads
+    kv = proj(latent_ctx, wts.w_kv_b).view(n, H, cfg.nope + cfg.v_dim)
+    k = torch.cat((kv[:, :, : cfg.nope], rope_ctx.view(n, 1, cfg.rope).expand(n, H, cfg.rope)), -1)
+    return k.contiguous(), kv[:, :, cfg.nope:].contiguous()
 
 
 def absorb_query(q_up, wts: MLAWeights, cfg: MLAConfig, pos: int, cos, sin):

@@ -312,6 +312,119 @@ def test_mla_absorbed_f64_brute_force():
         assert float((got[h] - ref).abs().max()) <= float(ref.abs().max()) * 2 ** -7
 
 
+def _rope_attend_case(n_ctx, seed=40):
+    """A small MLA shape, a latent cache of n_ctx + 1 rows expanded to the
+    assembled per-head cache; the last row is this token's own."""
+    OM, cfg, w = _mla_small()
+    pos = n_ctx
+    cos, sin = OM.rope_tables(n_ctx + 2, cfg)
+    lat, rk_raw = OM.random_cache(1, n_ctx + 1, cfg, seed=seed)
+    # rows 0..n_ctx-1 of the rope cache hold rotated keys; the token brings its raw slice
+    rk = torch.stack([OM.rope32(rk_raw[0, j], cos[j], sin[j]) for j in range(n_ctx + 1)])
+    k_all, v_all = OM.assembled_cache(lat[0], rk, w, cfg)
+    q_up = torch.randn(cfg.heads, cfg.qk_dim, generator=g(seed + 1)).to(BF)
+    kv_up = torch.cat((k_all[n_ctx, :, : cfg.nope], v_all[n_ctx]), -1).contiguous()
+    scale = torch.tensor(cfg.scale).to(BF)
+    args = (q_up.reshape(-1), kv_up.reshape(-1), rk_raw[0, n_ctx], cos, sin, pos,
+            k_all[:n_ctx], v_all[:n_ctx], n_ctx, scale, cfg.heads, cfg.nope, cfg.rope, cfg.v_dim)
+    return OM, cfg, w, args, (q_up, lat[0], rk, cos, sin, pos), k_all[n_ctx], v_all[n_ctx]
+
+
+def test_rope_attend_empty_context_returns_own_value():
+    """ctx = 0: one score, weight 1, the output is the token's value exactly;
+    the returned key is [k_nope | rotated k_rope]. Dropping the token's own
+    score (planted) leaves nothing to attend and fails."""
+    OM, cfg, w, args, _, k_own, v_own = _rope_attend_case(0)
+    attn, k_new, v_new = OM.rope_attend(*args)
+    assert torch.equal(attn, v_own.reshape(-1))
+    assert torch.equal(k_new, k_own.reshape(-1))
+    assert torch.equal(v_new, v_own.reshape(-1))
+    n_ctx = 5
+    OM, cfg, w, args, _, _, _ = _rope_attend_case(n_ctx, seed=41)
+    good = OM.rope_attend(*args)[0]
+    bad = OM.rope_attend(*args, drop_new=True)[0]
+    assert not torch.equal(good, bad)
+
+
+def test_rope_attend_equals_reference_attention_on_expanded_cache():
+    """Two spellings of the same attention: the per-head assembled cache with a
+    separate token term (rope_attend) and one softmax over the latent cache
+    expanded with the token as its last row (attend_reference)."""
+    from tests._check import rel_l2
+
+    for n_ctx in (1, 7, 33):
+        OM, cfg, w, args, (q_up, lat, rk, cos, sin, pos), _, _ = _rope_attend_case(n_ctx, seed=50 + n_ctx)
+        got = OM.rope_attend(*args)[0]
+        ref = OM.attend_reference(q_up, lat, rk, w, cfg, pos, cos, sin)
+        assert rel_l2(got, ref) < 2e-3
+        assert int(bf16_ulps(got, ref).max()) <= 2
+
+
+def test_rope_attend_identical_keys_give_mean_value():
+    """Every context key equal to the token's own: uniform weights, the output is
+    the mean of the context values and the token's value."""
+    OM, cfg, w, args, _, k_own, v_own = _rope_attend_case(6, seed=60)
+    args = list(args)
+    n = 6
+    # context keys: [k_nope | rotated k_rope] of the token itself
+    k_ctx = k_own.unsqueeze(0).expand(n, -1, -1).contiguous()
+    args[6] = k_ctx
+    attn = OM.rope_attend(*args)[0].double().view(cfg.heads, cfg.v_dim)
+    mean = (args[7].double().sum(0) + v_own.double()) / (n + 1)
+    assert float((attn - mean).abs().max()) <= float(mean.abs().max()) * 2 ** -7
+
+
+def test_rope_attend_f64_brute_force():
+    OM, cfg, w, args, _, _, _ = _rope_attend_case(4, seed=70)
+    q_up, kv_up, k_rope, cos, sin, pos, kc, vc, n, scale, H, nope, rope, vd = args
+    got = OM.rope_attend(*args)[0].double().view(H, vd)
+    half = rope // 2
+    for h in range(H):
+        q = [float(x) for x in q_up.view(H, -1)[h]]
+        def rot(x, j):
+            c, s = float(cos[pos, j]), float(sin[pos, j])
+            r = -x[j + half] if j < half else x[j - half]
+            return float(torch.tensor(float(torch.tensor(x[j] * c).to(BF)) + float(torch.tensor(r * s).to(BF))).to(BF))
+        qf = q[:nope] + [rot(q[nope:], j) for j in range(rope)]
+        sc = float(scale)
+        qh = [float(torch.tensor(x * sc).to(BF)) for x in qf]
+        kr = [float(x) for x in k_rope]
+        kv = [float(x) for x in kv_up.view(H, -1)[h]]
+        k_new = kv[:nope] + [rot(kr, j) for j in range(rope)]
+        v_new = kv[nope:]
+        s = [sum(qh[d] * float(kc[j, h, d]) for d in range(nope + rope)) for j in range(n)]
+        s.append(sum(qh[d] * k_new[d] for d in range(nope + rope)))
+        mx = max(s)
+        e = [math.exp(x - mx) for x in s]
+        ref = [(sum(e[j] * float(vc[j, h, v]) for j in range(n)) + e[n] * v_new[v]) / sum(e) for v in range(vd)]
+        ref = torch.tensor(ref, dtype=torch.float64)
+        assert float((got[h] - ref).abs().max()) <= float(ref.abs().max()) * 2 ** -7
+
+
+def test_mla_attention_composition_matches_projected_reference():
+    """The op-by-op spelling (projections, rope_attend over the assembled cache,
+    W_o) equals projecting with ``project`` and attending with
+    ``attend_reference`` on the latent cache the assembled one came from."""
+    from tests._check import rel_l2
+
+    OM, cfg, w = _mla_small()
+    n_ctx = 9
+    pos = n_ctx
+    cos, sin = OM.rope_tables(n_ctx + 1, cfg)
+    hidden = torch.randn(cfg.hidden, generator=g(80)).to(BF)
+    lat, rk = OM.random_cache(1, n_ctx, cfg, seed=81)
+    k_ctx, v_ctx = OM.assembled_cache(lat[0], rk[0], w, cfg)
+    scale = torch.tensor(cfg.scale).to(BF)
+    out, k_new, v_new = OM.mla_attention(hidden, w, cfg, pos, cos, sin, k_ctx, v_ctx, n_ctx, scale)
+    pr = OM.project(hidden, w, cfg, pos, cos, sin)
+    lat_all = torch.cat((lat[0], pr.latent.view(1, -1)), 0)
+    rk_all = torch.cat((rk[0], pr.k_rope.view(1, -1)), 0)
+    ref = OM.proj(OM.attend_reference(pr.q_up, lat_all, rk_all, w, cfg, pos, cos, sin), w.w_o)
+    assert rel_l2(out, ref) < 5e-3
+    k_exp, v_exp = OM.assembled_cache(pr.latent.view(1, -1), pr.k_rope.view(1, -1), w, cfg)
+    assert torch.equal(k_new, k_exp.reshape(-1)) and torch.equal(v_new, v_exp.reshape(-1))
+
+
 # ---------------------------------------------------------------- prefill attention layer
 def _prefill_small():
     from oracle import prefill as OP

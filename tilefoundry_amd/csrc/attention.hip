@@ -319,6 +319,65 @@ int launch_attn_g(const AttnArgs& a, int ss, int batch, hipStream_t st) {
 // split statistics arrive in one parallel round trip, then eight groups of
 // threads each sum every eighth split of the partial outputs, so the loads of
 // all splits are in flight together; the groups meet in LDS in group order.
+// qk_rope_cache: one wave per head of the [q | k | v] projection, summed from
+// its split-K partials [ks, B, (hq + 2 hkv) * 128] and landed in bf16. Query
+// heads get the per-head norm and RoPE at pos[b] and go to q_out; the key head
+// gets the same with gamma_k and the value head nothing, and both are written
+// to cache row wr[b]. The standalone form of the fused mode above, for callers
+// that keep the prepared query (examples/qwen3_1_7b-tilelang/fast/kernels.py:328-411).
+__global__ __launch_bounds__(kThreads) void qk_rope_cache_kernel(
+    const float* __restrict__ part, int ks, const uint16_t* __restrict__ gq,
+    const uint16_t* __restrict__ gk, float eps, const uint16_t* __restrict__ cos_t,
+    const uint16_t* __restrict__ sin_t, int mp_rows, const int* __restrict__ pos,
+    const int* __restrict__ wr, uint16_t* kc, uint16_t* vc, int cap, uint16_t* q_out, int hq,
+    int hkv, int* err) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int hh = blockIdx.x * kWaves + threadIdx.x / kWave;
+  const int b = blockIdx.y;
+  const int tot = hq + 2 * hkv;
+  if (hh >= tot) return;  // whole waves only
+  const int rows = tot * D;
+  const size_t kstride = static_cast<size_t>(rows) * gridDim.y;
+  float x0, x1;
+  head_raw(nullptr, part + static_cast<size_t>(b) * rows + static_cast<size_t>(hh) * D, ks, kstride,
+           lane, x0, x1);
+  const size_t KN = static_cast<size_t>(hkv) * D;
+  const int slot = wr[b];
+  const bool slot_ok = slot >= 0 && slot < cap;
+  if (hh >= hq + hkv) {
+    if (!slot_ok) {
+      if (lane == 0) set_err(err, 3);
+      return;
+    }
+    uint16_t* dst = vc + (static_cast<size_t>(b) * cap + slot) * KN + (hh - hq - hkv) * D;
+    dst[lane] = static_cast<uint16_t>(f2bf(x0));
+    dst[lane + 64] = static_cast<uint16_t>(f2bf(x1));
+    return;
+  }
+  int p = pos[b];
+  if (p < 0 || p >= mp_rows) {
+    if (lane == 0) set_err(err, 5);
+    p = 0;
+  }
+  const size_t pr = static_cast<size_t>(p) * D;
+  const float c0 = bf2f(cos_t[pr + lane]), s0 = bf2f(sin_t[pr + lane]);
+  const float c1 = bf2f(cos_t[pr + lane + 64]), s1 = bf2f(sin_t[pr + lane + 64]);
+  float o0, o1;
+  norm_rope_head(x0, x1, hh < hq ? gq : gk, eps, c0, s0, c1, s1, lane, o0, o1);
+  uint16_t* dst;
+  if (hh < hq) {
+    dst = q_out + (static_cast<size_t>(b) * hq + hh) * D;
+  } else {
+    if (!slot_ok) {
+      if (lane == 0) set_err(err, 3);
+      return;
+    }
+    dst = kc + (static_cast<size_t>(b) * cap + slot) * KN + (hh - hq) * D;
+  }
+  dst[lane] = static_cast<uint16_t>(f2bf(o0));
+  dst[lane + 64] = static_cast<uint16_t>(f2bf(o1));
+}
+
 constexpr int kCombThreads = 1024;
 constexpr int kCombGroups = 8;
 constexpr int kCombMaxSplits = 1024;
@@ -457,6 +516,29 @@ int tfa_attn_combine(const float* op, const float* mp, const float* lp, void* ou
                                                          (int)splits, (int)hq, (int)head_dim, wr,
                                                          (int)split);
   return launched("attn_combine");
+}
+
+int tfa_qk_rope_cache(const float* qkv_part, int64_t part_ks, const void* gamma_q,
+                      const void* gamma_k, float eps_head, const void* cos_t, const void* sin_t,
+                      int64_t rope_rows, const int* pos, const int* wr, void* k_cache,
+                      void* v_cache, int64_t cap, void* q_out, int64_t batch, int64_t hq,
+                      int64_t hkv, int64_t head_dim, int* err, hipStream_t stream) {
+  if (!qkv_part || !gamma_q || !gamma_k || !cos_t || !sin_t || !pos || !wr || !k_cache ||
+      !v_cache || !q_out)
+    return fail(TFA_ERR_NULL, "tfa_qk_rope_cache: null pointer argument");
+  if (head_dim != D) return fail(TFA_ERR_SHAPE, "tfa_qk_rope_cache: head_dim %lld, only 128 supported", (long long)head_dim);
+  if (hq <= 0 || hkv <= 0 || cap <= 0 || rope_rows <= 0)
+    return fail(TFA_ERR_SHAPE, "tfa_qk_rope_cache: empty heads, cache or rope table");
+  if (part_ks < 1 || part_ks > kMaxSplitsK)
+    return fail(TFA_ERR_SHAPE, "tfa_qk_rope_cache: part_ks %lld not in [1, %d]", (long long)part_ks, kMaxSplitsK);
+  if (batch < 1 || batch > 65535) return fail(TFA_ERR_SHAPE, "tfa_qk_rope_cache: batch %lld out of range", (long long)batch);
+  const dim3 grid((unsigned)((hq + 2 * hkv + kWaves - 1) / kWaves), (unsigned)batch);
+  qk_rope_cache_kernel<<<grid, kThreads, 0, stream>>>(
+      qkv_part, (int)part_ks, static_cast<const uint16_t*>(gamma_q),
+      static_cast<const uint16_t*>(gamma_k), eps_head, static_cast<const uint16_t*>(cos_t),
+      static_cast<const uint16_t*>(sin_t), (int)rope_rows, pos, wr, static_cast<uint16_t*>(k_cache),
+      static_cast<uint16_t*>(v_cache), (int)cap, static_cast<uint16_t*>(q_out), (int)hq, (int)hkv, err);
+  return launched("qk_rope_cache");
 }
 
 }  // extern "C"

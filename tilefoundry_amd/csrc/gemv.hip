@@ -52,7 +52,9 @@ struct GemvArgs {
   float eps;
   // matrix
   const uint16_t* w;      // [N, K]
+  const uint16_t* w_odd;  // SwiGLU from separate matrices: odd rows 2i+1 are w_odd[i], even rows w[i]
   int N, K;
+  float in_div;           // plain prologue: x lands as bf16(x / in_div) when nonzero
   // outputs
   float* yf;              // f32 out / logits
   uint16_t* yb;           // bf16 out (also the q|k rows of the qkv routing)
@@ -116,8 +118,12 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = lane + j * kWave;
+      // R is even, so (row & 1) == (r & 1) and the matrix pick is static
+      const uint16_t* wrow = (EPI == EPI_SWIGLU && a.w_odd)
+                                 ? ((r & 1) ? a.w_odd : a.w) + static_cast<size_t>(row >> 1) * K
+                                 : a.w + static_cast<size_t>(row) * K;
       if (row < a.N && c < nch)
-        w[r][j] = ld16_stream(a.w + static_cast<size_t>(row) * K + kbase + 8 * c);
+        w[r][j] = ld16_stream(wrow + kbase + 8 * c);
       else
         w[r][j] = make_uint4(0, 0, 0, 0);
     }
@@ -134,6 +140,12 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
   float xf[NCH][8];
 #pragma unroll
   for (int j = 0; j < NCH; ++j) unpack8(xv[j], xf[j]);
+  if (PRO == PRO_PLAIN && a.in_div != 0.f) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xf[j][i] = round_bf(__fdiv_rn(xf[j][i], a.in_div));
+  }
   if (PRO != PRO_PLAIN) {
     float ss = 0.f;
 #pragma unroll
@@ -311,6 +323,51 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(
   }
 }
 
+// SwiGLU over split-K partials [ks, rows, 2 * inter] of a fused gate|up
+// projection (gate in [0, inter), up in [inter, 2 inter)):
+//   act[r, i] = bf16(bf16(silu(bf16 g)) * bf16 u), g and u summed in split order.
+// examples/qwen3_1_7b-tilelang/fast/kernels.py:547-572 (silu_mul).
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float* __restrict__ part, int ks,
+                                                            int inter, uint16_t* __restrict__ act) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  const int r = blockIdx.y;
+  if (i >= inter) return;
+  const size_t stride = static_cast<size_t>(gridDim.y) * 2 * inter;
+  const float* row = part + static_cast<size_t>(r) * 2 * inter;
+  const float g = round_bf(sum_splits(row + i, stride, ks));
+  const float u = round_bf(sum_splits(row + inter + i, stride, ks));
+  act[static_cast<size_t>(r) * inter + i] =
+      static_cast<uint16_t>(f2bf(round_bf(g / (1.0f + expf(-g))) * u));
+}
+
+// out[r, :] = table[ids[r], :], or bf16(table[ids[r], :] * scale) when `scaled`.
+// 16 bytes a thread. An id outside [0, vocab) reads row 0 and sets err = 1.
+// examples/qwen3_1_7b-tilelang/fast/kernels.py:579-588 (embed) and
+// examples/minicpm3_4b-cutedsl/kernels/reference_ops.py:72-76 (embed_scaled).
+__global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t* __restrict__ table,
+                                                         const int64_t* __restrict__ ids,
+                                                         int64_t vocab, int hidden, int scaled,
+                                                         float scale, uint16_t* __restrict__ out,
+                                                         int* err) {
+  const int c = blockIdx.x * kThreads + threadIdx.x;  // 8-element chunk
+  const int r = blockIdx.y;
+  if (8 * c >= hidden) return;
+  int64_t id = ids[r];
+  if (id < 0 || id >= vocab) {
+    if (c == 0) set_err(err, 1);
+    id = 0;
+  }
+  uint4 v = ld16(table + id * hidden + 8 * c);
+  if (scaled) {
+    float f[8];
+    unpack8(v, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = round_bf(f[i] * scale);
+    v = pack8(f);
+  }
+  st16(out + static_cast<size_t>(r) * hidden + 8 * c, v);
+}
+
 }  // namespace
 
 extern "C" {
@@ -456,6 +513,66 @@ int tfa_decode_qkv(const void* h, const void* table, const int64_t* ids, int64_t
   }
   TFA_TRY(check_vec(h, "h", "tfa_decode_qkv"));
   return dispatch_rows<PRO_NORM, EPI_QKV>(a, stream, "decode_qkv");
+}
+
+int tfa_rmsnorm_gemv_gate_up(const void* h, const void* gamma, float eps, const void* w_gate,
+                             const void* w_up, void* act, int64_t inter, int64_t k,
+                             hipStream_t stream) {
+  GemvArgs a{};
+  a.x = static_cast<const uint16_t*>(h);
+  a.gamma = static_cast<const uint16_t*>(gamma);
+  a.eps = eps;
+  a.w = static_cast<const uint16_t*>(w_gate);
+  a.w_odd = static_cast<const uint16_t*>(w_up);
+  a.N = (int)(2 * inter);
+  a.K = (int)k;
+  a.yb = static_cast<uint16_t*>(act);
+  TFA_TRY(check_gemv(a, "tfa_rmsnorm_gemv_gate_up"));
+  TFA_TRY(check_vec(w_up, "w_up", "tfa_rmsnorm_gemv_gate_up"));
+  TFA_TRY(check_vec(h, "h", "tfa_rmsnorm_gemv_gate_up"));
+  TFA_TRY(check_vec(gamma, "gamma", "tfa_rmsnorm_gemv_gate_up"));
+  if (!act) return fail(TFA_ERR_NULL, "tfa_rmsnorm_gemv_gate_up: null act");
+  return dispatch_rows<PRO_NORM, EPI_SWIGLU>(a, stream, "rmsnorm_gemv_gate_up");
+}
+
+int tfa_lm_head_gemv(const void* h, const void* w, float divisor, void* logits, int64_t vocab,
+                     int64_t k, hipStream_t stream) {
+  GemvArgs a{};
+  a.x = static_cast<const uint16_t*>(h);
+  a.w = static_cast<const uint16_t*>(w);
+  a.in_div = divisor;
+  a.N = (int)vocab;
+  a.K = (int)k;
+  a.yb = static_cast<uint16_t*>(logits);
+  TFA_TRY(check_gemv(a, "tfa_lm_head_gemv"));
+  TFA_TRY(check_vec(h, "h", "tfa_lm_head_gemv"));
+  if (!logits) return fail(TFA_ERR_NULL, "tfa_lm_head_gemv: null logits");
+  if (!(divisor != 0.f)) return fail(TFA_ERR_ARG, "tfa_lm_head_gemv: divisor must be nonzero");
+  return dispatch_rows<PRO_PLAIN, EPI_BF16>(a, stream, "lm_head_gemv");
+}
+
+int tfa_silu_mul(const float* part, int64_t ks, int64_t inter, int64_t rows, void* act,
+                 hipStream_t stream) {
+  if (!part || !act) return fail(TFA_ERR_NULL, "tfa_silu_mul: null pointer argument");
+  if (ks < 1 || ks > kMaxSplitsK) return fail(TFA_ERR_SHAPE, "tfa_silu_mul: ks %lld not in [1, %d]", (long long)ks, kMaxSplitsK);
+  if (inter <= 0 || rows < 1 || rows > 65535) return fail(TFA_ERR_SHAPE, "tfa_silu_mul: bad shape");
+  const dim3 grid((unsigned)((inter + kThreads - 1) / kThreads), (unsigned)rows);
+  silu_mul_kernel<<<grid, kThreads, 0, stream>>>(part, (int)ks, (int)inter,
+                                                  static_cast<uint16_t*>(act));
+  return launched("silu_mul");
+}
+
+int tfa_embed(const void* table, const int64_t* ids, int64_t vocab, int64_t hidden, int64_t rows,
+              int scaled, float scale, void* out, int* err, hipStream_t stream) {
+  if (!table || !ids || !out) return fail(TFA_ERR_NULL, "tfa_embed: null pointer argument");
+  if (hidden <= 0 || hidden % 8 != 0 || vocab <= 0 || rows < 1 || rows > 65535)
+    return fail(TFA_ERR_SHAPE, "tfa_embed: hidden %lld must be a positive multiple of 8", (long long)hidden);
+  if (!aligned16(table) || !aligned16(out)) return fail(TFA_ERR_ALIGN, "tfa_embed: table / out not 16-byte aligned");
+  const dim3 grid((unsigned)((hidden / 8 + kThreads - 1) / kThreads), (unsigned)rows);
+  embed_kernel<<<grid, kThreads, 0, stream>>>(static_cast<const uint16_t*>(table), ids, vocab,
+                                               (int)hidden, scaled, scale,
+                                               static_cast<uint16_t*>(out), err);
+  return launched("embed");
 }
 
 }  // extern "C"

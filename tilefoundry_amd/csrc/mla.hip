@@ -488,6 +488,188 @@ __global__ __launch_bounds__(kThreads) void rows_residual_kernel(
   st16(out + e0, pack8(o));
 }
 
+
+// --------------------------------------------------------------- rope_attend
+// MiniCPM3 decode attention over the assembled per-head cache Hugging Face
+// keeps (k [cap, heads, nope + rope], v [cap, heads, v_dim]): the non-absorbed
+// form, in the order of examples/minicpm3_4b-cutedsl/kernels/reference_ops.py:87-130.
+// The query's rotary slice is rotated at pos (each product and the sum landing
+// in bf16), the whole query is multiplied by the bf16 scale in bf16, scores are
+// f32 dots, the softmax weights stay f32 into the value sum, and the token's own
+// key and value join the context through a log-sum-exp merge.
+//   rope_attend_split  per (split of 256 context rows, head): the split's max,
+//                      sum and unnormalised weighted values; splits past ctx
+//                      exit at once.
+//   rope_attend_merge  per head: the token's key [k_nope | rotated k_rope] and
+//                      value (to k_new / v_new), its score, and the merge of the
+//                      live splits into bf16 attn.
+constexpr int kRaSplit = 256;
+constexpr int kRaMaxQK = 256;
+constexpr int kRaMaxV = 128;
+
+struct RopeAttendArgs {
+  const uint16_t* q_up;    // [heads, qk]: [q_nope | q_rope] (rotary slice unrotated)
+  const uint16_t* kv_up;   // [heads, nope + v_dim]: [k_nope | v]
+  const uint16_t* k_rope;  // [rope] unrotated shared rotary key
+  const uint16_t* cos_t;   // [rope_rows, rope]
+  const uint16_t* sin_t;
+  int rope_rows;
+  const int* pos;          // [1] rotary position
+  const uint16_t* kc;      // [cap, heads, qk]
+  const uint16_t* vc;      // [cap, heads, v_dim]
+  const int* ctx;          // [1] context rows held by the cache
+  const uint16_t* scale;   // [1] bf16
+  int cap, heads, nope, rope, vd;
+  float* op;               // [ns, heads, v_dim]
+  float* mp;               // [ns, heads]
+  float* lp;               // [ns, heads]
+  uint16_t* attn;          // [heads * v_dim]
+  uint16_t* k_new;         // [heads * qk], optional
+  uint16_t* v_new;         // [heads * v_dim], optional
+  int* err;
+};
+
+// Rotate-half of a `rope`-wide slice x at index j, each product and the sum in bf16.
+TFA_DEV float rope_bf(const uint16_t* x, int j, int half, float c, float s) {
+  const float xv = bf2f(x[j]);
+  const float r = j < half ? -bf2f(x[j + half]) : bf2f(x[j - half]);
+  return round_bf(round_bf(xv * c) + round_bf(r * s));
+}
+
+TFA_DEV int ra_pos(const RopeAttendArgs& a) {
+  const int p = a.pos[0];
+  return (p < 0 || p >= a.rope_rows) ? 0 : p;
+}
+
+TFA_DEV int ra_ctx(const RopeAttendArgs& a) {
+  const int n = a.ctx[0];
+  return n < 0 ? 0 : (n > a.cap ? a.cap : n);
+}
+
+// qs[d] = bf16(query[d] * scale) for head h, the rotary slice rotated at p.
+TFA_DEV void ra_query(const RopeAttendArgs& a, int h, int p, float* qs) {
+  const int qk = a.nope + a.rope;
+  const uint16_t* q = a.q_up + static_cast<size_t>(h) * qk;
+  const float sc = bf2f(a.scale[0]);
+  const size_t pr = static_cast<size_t>(p) * a.rope;
+  for (int d = threadIdx.x; d < qk; d += blockDim.x) {
+    float v;
+    if (d < a.nope) {
+      v = bf2f(q[d]);
+    } else {
+      const int j = d - a.nope;
+      v = rope_bf(q + a.nope, j, a.rope / 2, bf2f(a.cos_t[pr + j]), bf2f(a.sin_t[pr + j]));
+    }
+    qs[d] = round_bf(v * sc);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void rope_attend_split_kernel(const RopeAttendArgs a) {
+  __shared__ float qs[kRaMaxQK];
+  __shared__ float ps[kRaSplit];
+  __shared__ float red[2][kWaves];
+  __shared__ float ov[kWaves][kRaMaxV];
+  const int s = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
+  const int lane = t & (kWave - 1), wid = t / kWave;
+  const int n = ra_ctx(a);
+  const int start = s * kRaSplit;
+  if (start >= n) return;  // whole block
+  const int len = min(n - start, kRaSplit);
+  ra_query(a, h, ra_pos(a), qs);
+  __syncthreads();
+
+  // scores: one context row per thread
+  const int qk = a.nope + a.rope;
+  float sco = -INFINITY;
+  if (t < len) {
+    const uint16_t* krow = a.kc + (static_cast<size_t>(start + t) * a.heads + h) * qk;
+    float acc = 0.f;
+    for (int c = 0; c < qk; c += 8) {
+      float f[8];
+      unpack8(ld16(krow + c), f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = fmaf(qs[c + i], f[i], acc);
+    }
+    sco = acc;
+  }
+  float m = wave_max(sco);
+  if (lane == 0) red[0][wid] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  const float e = t < len ? expf(sco - m) : 0.f;
+  ps[t] = e;
+  const float l = wave_sum(e);
+  if (lane == 0) red[1][wid] = l;
+  __syncthreads();
+
+  // weighted values: wave w takes rows 64w .. 64w+63 of the split, lanes the value dims
+  float acc0 = 0.f, acc1 = 0.f;
+  const int j1 = min(len, (wid + 1) * kWave);
+  for (int j = wid * kWave; j < j1; ++j) {
+    const uint16_t* vrow = a.vc + (static_cast<size_t>(start + j) * a.heads + h) * a.vd;
+    const float pj = ps[j];
+    if (lane < a.vd) acc0 = fmaf(pj, bf2f(vrow[lane]), acc0);
+    if (lane + kWave < a.vd) acc1 = fmaf(pj, bf2f(vrow[lane + kWave]), acc1);
+  }
+  ov[wid][lane] = acc0;
+  ov[wid][lane + kWave] = acc1;
+  __syncthreads();
+  for (int d = t; d < a.vd; d += kThreads)
+    a.op[(static_cast<size_t>(s) * a.heads + h) * a.vd + d] = (ov[0][d] + ov[1][d]) + (ov[2][d] + ov[3][d]);
+  if (t == 0) {
+    a.mp[s * a.heads + h] = m;
+    a.lp[s * a.heads + h] = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void rope_attend_merge_kernel(const RopeAttendArgs a) {
+  __shared__ float qs[kRaMaxQK];
+  __shared__ float kn[kRaMaxQK];
+  __shared__ float scr[kWaves];
+  const int h = blockIdx.x, t = threadIdx.x;
+  const int qk = a.nope + a.rope, kvw = a.nope + a.vd;
+  if (h == 0 && t == 0) {
+    const int p = a.pos[0], n = a.ctx[0];
+    if (p < 0 || p >= a.rope_rows) set_err(a.err, 5);
+    if (n < 0 || n > a.cap) set_err(a.err, 4);
+  }
+  const int p = ra_pos(a);
+  const int n = ra_ctx(a);
+  ra_query(a, h, p, qs);
+  const uint16_t* kv = a.kv_up + static_cast<size_t>(h) * kvw;
+  const size_t pr = static_cast<size_t>(p) * a.rope;
+  for (int d = t; d < qk; d += kThreads) {
+    float v;
+    if (d < a.nope) {
+      v = bf2f(kv[d]);
+    } else {
+      const int j = d - a.nope;
+      v = rope_bf(a.k_rope, j, a.rope / 2, bf2f(a.cos_t[pr + j]), bf2f(a.sin_t[pr + j]));
+    }
+    kn[d] = v;
+    if (a.k_new) a.k_new[static_cast<size_t>(h) * qk + d] = static_cast<uint16_t>(f2bf(v));
+  }
+  if (a.v_new)
+    for (int d = t; d < a.vd; d += kThreads) a.v_new[static_cast<size_t>(h) * a.vd + d] = kv[a.nope + d];
+  __syncthreads();
+  float part = 0.f;
+  for (int d = t; d < qk; d += kThreads) part = fmaf(qs[d], kn[d], part);
+  const float snew = block_sum(part, scr);
+
+  const int nact = (n + kRaSplit - 1) / kRaSplit;
+  float peak = snew;
+  for (int j = 0; j < nact; ++j) peak = fmaxf(peak, a.mp[j * a.heads + h]);
+  const float enew = expf(snew - peak);
+  float tot = enew;
+  for (int j = 0; j < nact; ++j) tot = fmaf(a.lp[j * a.heads + h], expf(a.mp[j * a.heads + h] - peak), tot);
+  for (int d = t; d < a.vd; d += kThreads) {
+    float w = enew * bf2f(kv[a.nope + d]);
+    for (int j = 0; j < nact; ++j)
+      w = fmaf(a.op[(static_cast<size_t>(j) * a.heads + h) * a.vd + d], expf(a.mp[j * a.heads + h] - peak), w);
+    a.attn[static_cast<size_t>(h) * a.vd + d] = static_cast<uint16_t>(f2bf(w / tot));
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -616,6 +798,68 @@ int tfa_rows_residual(const float* part, int64_t ks, const void* residual, float
   rows_residual_kernel<<<(unsigned)blocks, kThreads, 0, stream>>>(
       part, (int)ks, static_cast<const uint16_t*>(residual), alpha, static_cast<uint16_t*>(out), (int)m, (int)n);
   return launched("rows_residual");
+}
+
+int64_t tfa_rope_attend_splits(int64_t cap) { return cap <= 0 ? 0 : (cap + kRaSplit - 1) / kRaSplit; }
+
+int tfa_rope_attend(const void* q_up, const void* kv_up, const void* k_rope, const void* cos_t,
+                    const void* sin_t, int64_t rope_rows, const int* pos, const void* k_cache,
+                    const void* v_cache, int64_t cap, const int* ctx, const void* scale,
+                    int64_t heads, int64_t nope, int64_t rope, int64_t v_dim, float* op, float* mp,
+                    float* lp, void* attn, void* k_new, void* v_new, int* err, hipStream_t stream) {
+  TFA_NONNULL(q_up);
+  TFA_NONNULL(kv_up);
+  TFA_NONNULL(k_rope);
+  TFA_NONNULL(cos_t);
+  TFA_NONNULL(sin_t);
+  TFA_NONNULL(pos);
+  TFA_NONNULL(ctx);
+  TFA_NONNULL(scale);
+  TFA_NONNULL(attn);
+  TFA_REQUIRE(heads >= 1 && heads <= 65535 && nope >= 0 && rope >= 2 && rope % 2 == 0 &&
+                  (nope + rope) % 8 == 0 && nope + rope <= kRaMaxQK && v_dim >= 1 && v_dim <= kRaMaxV &&
+                  rope_rows >= 1 && cap >= 0,
+              TFA_ERR_SHAPE,
+              "tfa_rope_attend: need heads >= 1, even rope, (nope + rope) a multiple of 8 up to %d, "
+              "v_dim in [1, %d]", kRaMaxQK, kRaMaxV);
+  RopeAttendArgs a{};
+  a.q_up = static_cast<const uint16_t*>(q_up);
+  a.kv_up = static_cast<const uint16_t*>(kv_up);
+  a.k_rope = static_cast<const uint16_t*>(k_rope);
+  a.cos_t = static_cast<const uint16_t*>(cos_t);
+  a.sin_t = static_cast<const uint16_t*>(sin_t);
+  a.rope_rows = (int)rope_rows;
+  a.pos = pos;
+  a.kc = static_cast<const uint16_t*>(k_cache);
+  a.vc = static_cast<const uint16_t*>(v_cache);
+  a.ctx = ctx;
+  a.scale = static_cast<const uint16_t*>(scale);
+  a.cap = (int)cap;
+  a.heads = (int)heads;
+  a.nope = (int)nope;
+  a.rope = (int)rope;
+  a.vd = (int)v_dim;
+  a.op = op;
+  a.mp = mp;
+  a.lp = lp;
+  a.attn = static_cast<uint16_t*>(attn);
+  a.k_new = static_cast<uint16_t*>(k_new);
+  a.v_new = static_cast<uint16_t*>(v_new);
+  a.err = err;
+  const int64_t ns = tfa_rope_attend_splits(cap);
+  if (ns > 0) {
+    TFA_NONNULL(k_cache);
+    TFA_NONNULL(v_cache);
+    TFA_NONNULL(op);
+    TFA_NONNULL(mp);
+    TFA_NONNULL(lp);
+    TFA_ALIGN16(k_cache);
+    rope_attend_split_kernel<<<dim3((unsigned)ns, (unsigned)heads), kThreads, 0, stream>>>(a);
+    const int st = launched("rope_attend_split");
+    if (st != TFA_OK) return st;
+  }
+  rope_attend_merge_kernel<<<(unsigned)heads, kThreads, 0, stream>>>(a);
+  return launched("rope_attend_merge");
 }
 
 }  // extern "C"

@@ -537,6 +537,121 @@ void qkv_norm_rope(const Tensor& hn, const Tensor& w_qkv, const Tensor& out, int
                                  64, stream_of(out)));
 }
 
+// ------------------------------------------------- per-op decode entries
+void rmsnorm_gemv_gate_up(const Tensor& h, const Tensor& gamma, double eps, const Tensor& w_gate,
+                          const Tensor& w_up, const Tensor& act) {
+  need(h, "x", BF);
+  const int64_t K = h.numel();
+  need(gamma, "gamma", BF, K);
+  const int64_t I = act.numel();
+  need_mat(w_gate, "w_gate", I, K);
+  need_mat(w_up, "w_up", I, K);
+  need(act, "out", BF, I);
+  raise_status(tfa_rmsnorm_gemv_gate_up(h.data_ptr(), gamma.data_ptr(), (float)eps,
+                                        w_gate.data_ptr(), w_up.data_ptr(), act.data_ptr(), I, K,
+                                        stream_of(h)));
+}
+
+void lm_head_gemv(const Tensor& h, const Tensor& w, double divisor, const Tensor& logits) {
+  need(h, "hidden", BF);
+  const int64_t K = h.numel();
+  if (w.dim() != 2) bad("w_head: expected a 2-D (vocab, hidden) weight");
+  const int64_t V = w.size(0);
+  need_mat(w, "w_head", V, K);
+  need(logits, "out", BF, V);
+  raise_status(tfa_lm_head_gemv(h.data_ptr(), w.data_ptr(), (float)divisor, logits.data_ptr(), V, K,
+                                stream_of(h)));
+}
+
+void silu_mul(const Tensor& part, const Tensor& act) {
+  need(part, "P", F32);
+  need(act, "O", BF);
+  if (part.dim() != 2 && part.dim() != 3) bad("P: expected (SK, [rows,] 2I)");
+  const int64_t rows = part.dim() == 3 ? part.size(1) : 1;
+  const int64_t I = part.size(-1) / 2;
+  if (part.size(-1) != 2 * I || act.numel() != rows * I) bad("P / O: expected P (SK, [rows,] 2I) and O (rows, I)");
+  raise_status(tfa_silu_mul(part.data_ptr<float>(), part.size(0), I, rows, act.data_ptr(),
+                            stream_of(part)));
+}
+
+void embed(const Tensor& table, const Tensor& ids, const Tensor& out, const std::optional<double>& scale,
+           const OptT& err) {
+  need(table, "table", BF);
+  if (table.dim() != 2) bad("table: expected (vocab, hidden)");
+  need(ids, "ids", I64);
+  const int64_t rows = ids.numel();
+  need(out, "out", BF, rows * table.size(1));
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_embed(table.data_ptr(), ids.data_ptr<int64_t>(), table.size(0), table.size(1),
+                         rows, scale ? 1 : 0, scale ? (float)*scale : 1.f, out.data_ptr(),
+                         opt_ptr_t<int>(err), stream_of(table)));
+}
+
+void qk_rope_cache(const Tensor& part, const Tensor& gamma_q, const Tensor& gamma_k, double eps,
+                   const Tensor& cos_t, const Tensor& sin_t, const Tensor& pos, const Tensor& wr,
+                   const Tensor& k_cache, const Tensor& v_cache, const Tensor& q_out, int64_t hq,
+                   int64_t hkv, const OptT& err) {
+  const int64_t D = 128;
+  need(pos, "Pos", I32);
+  const int64_t B = pos.numel();
+  need(wr, "Wr", I32, B);
+  need(part, "P", F32);
+  const int64_t per = B * (hq + 2 * hkv) * D;
+  if (part.numel() % per != 0) bad("P: expected (SK, [batch,] (HQ + 2 HKV) * 128)");
+  need(gamma_q, "Gq", BF, D);
+  need(gamma_k, "Gk", BF, D);
+  need(cos_t, "Cos", BF);
+  need(sin_t, "Sin", BF, cos_t.numel());
+  if (cos_t.dim() != 2 || cos_t.size(1) != D) bad("Cos: expected (MP, 128)");
+  need(k_cache, "Kc", BF);
+  need(v_cache, "Vc", BF, k_cache.numel());
+  if (k_cache.numel() % (B * hkv * D) != 0) bad("Kc: size is not a multiple of batch*HKV*128");
+  const int64_t cap = k_cache.numel() / (B * hkv * D);
+  need(q_out, "Q", BF, B * hq * D);
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_qk_rope_cache(part.data_ptr<float>(), part.numel() / per, gamma_q.data_ptr(),
+                                 gamma_k.data_ptr(), (float)eps, cos_t.data_ptr(), sin_t.data_ptr(),
+                                 cos_t.size(0), pos.data_ptr<int>(), wr.data_ptr<int>(),
+                                 k_cache.data_ptr(), v_cache.data_ptr(), cap, q_out.data_ptr(), B, hq,
+                                 hkv, D, opt_ptr_t<int>(err), stream_of(part)));
+}
+
+void rope_attend(const Tensor& q_up, const Tensor& kv_up, const Tensor& k_rope, const Tensor& cos_t,
+                 const Tensor& sin_t, const Tensor& pos, const Tensor& k_cache, const Tensor& v_cache,
+                 const Tensor& ctx, const Tensor& scale, int64_t heads, int64_t nope, int64_t rope,
+                 int64_t v_dim, const Tensor& op, const Tensor& mp, const Tensor& lp, const Tensor& attn,
+                 const OptT& k_new, const OptT& v_new, const OptT& err) {
+  const int64_t qk = nope + rope;
+  need(q_up, "q_up", BF, heads * qk);
+  need(kv_up, "kv_up", BF, heads * (nope + v_dim));
+  need(k_rope, "k_rope", BF, rope);
+  need(cos_t, "cos", BF);
+  need(sin_t, "sin", BF, cos_t.numel());
+  if (cos_t.dim() != 2 || cos_t.size(1) != rope) bad("cos: expected (rows, rope)");
+  need(pos, "pos", I32, 1);
+  need(ctx, "ctx", I32, 1);
+  need(scale, "scale", BF, 1);
+  need(k_cache, "k_cache", BF);
+  if (k_cache.numel() % (heads * qk) != 0) bad("k_cache: expected (capacity, heads, nope + rope)");
+  const int64_t cap = k_cache.numel() / (heads * qk);
+  need(v_cache, "v_cache", BF, cap * heads * v_dim);
+  const int64_t ns = tfa_rope_attend_splits(cap);
+  need(op, "op", F32, ns * heads * v_dim);
+  need(mp, "mp", F32, ns * heads);
+  need(lp, "lp", F32, ns * heads);
+  need(attn, "attn", BF, heads * v_dim);
+  if (k_new) need(*k_new, "k_new", BF, heads * qk);
+  if (v_new) need(*v_new, "v_new", BF, heads * v_dim);
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_rope_attend(
+      q_up.data_ptr(), kv_up.data_ptr(), k_rope.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(),
+      cos_t.size(0), pos.data_ptr<int>(), cap ? k_cache.data_ptr() : nullptr,
+      cap ? v_cache.data_ptr() : nullptr, cap, ctx.data_ptr<int>(), scale.data_ptr(), heads, nope,
+      rope, v_dim, ns ? op.data_ptr<float>() : nullptr, ns ? mp.data_ptr<float>() : nullptr,
+      ns ? lp.data_ptr<float>() : nullptr, attn.data_ptr(), opt_ptr(k_new) ? k_new->data_ptr() : nullptr,
+      opt_ptr(v_new) ? v_new->data_ptr() : nullptr, opt_ptr_t<int>(err), stream_of(q_up)));
+}
+
 void copy_stream(const Tensor& src, const Tensor& dst) {
   if (!src.is_cuda() || !dst.is_cuda() || !src.is_contiguous() || !dst.is_contiguous())
     bad("copy_stream: contiguous GPU tensors required");
@@ -576,4 +691,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("prefill_attention", &prefill_attention);
   m.def("gemm_nt", &gemm_nt);
   m.def("qkv_norm_rope", &qkv_norm_rope);
+  m.def("rmsnorm_gemv_gate_up", &rmsnorm_gemv_gate_up);
+  m.def("lm_head_gemv", &lm_head_gemv);
+  m.def("silu_mul", &silu_mul);
+  m.def("embed", &embed);
+  m.def("qk_rope_cache", &qk_rope_cache);
+  m.def("rope_attend_splits", [](int64_t cap) { return tfa_rope_attend_splits(cap); });
+  m.def("rope_attend", &rope_attend);
 }
