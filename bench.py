@@ -59,6 +59,36 @@ def _events_time(fn, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
+def _graph_time(fn, reps: int, calls: int = 1, copies: int = 16) -> float:
+    """Average milliseconds per launch of fn() -- which makes `calls` launches --
+    replayed from a HIP graph, the way the decode step runs them: fn is warmed up
+    eagerly once on a side stream, captured `copies` times back to back into one
+    graph (so the host's cost of launching a graph is spread over many kernels),
+    and the graph replayed `reps` times between two HIP events on torch's
+    current stream."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(copies):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del graph
+    return e0.elapsed_time(e1) / (reps * calls * copies)
+
+
 def dominant_kernel(eng) -> dict:
     """Post-attention norm + gate|up GEMV + SwiGLU, timed launch by launch
     across the 28 layers' weights (1.4 GB, so the 256 MB last-level cache holds
@@ -72,7 +102,7 @@ def dominant_kernel(eng) -> dict:
         for w in layers:
             C.rmsnorm_gemv_swiglu(eng.h1, w["gamma_post"], cfg.eps, w["w_gu"], eng.act)
 
-    ms = _events_time(one_pass, 20) / len(layers)
+    ms = _graph_time(one_pass, 10, len(layers), copies=4)
     H, I = cfg.hidden, cfg.inter
     algo = 2 * I * H * 2 + 2 * H * 2 + I * 2   # W_gu + h + gamma in, act out
     achieved = algo / (ms * 1e-3) / 1e9
@@ -102,14 +132,11 @@ def kernel_lines(eng) -> dict:
     gamma = (1 + 0.1 * torch.randn(H, device=dev, generator=g)).to(bf)
     y = torch.empty(R, H, device=dev, dtype=bf)
     ro = torch.empty(R, H, device=dev, dtype=bf)
-    it = [0]
-
     def add_norm():
-        x, r = sets[it[0] % 8]
-        it[0] += 1
-        C.add_rms_norm(x, r, gamma, y, ro, 1e-6, 0)
+        for x, r in sets:
+            C.add_rms_norm(x, r, gamma, y, ro, 1e-6, 0)
 
-    ms = _events_time(add_norm, 80)
+    ms = _graph_time(add_norm, 10, len(sets), copies=4)
     algo = 4 * R * H * 2 + H * 2
     gbs = algo / (ms * 1e-3) / 1e9
     out["add_rms_norm_4096x2048"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
@@ -122,7 +149,7 @@ def kernel_lines(eng) -> dict:
     nqk = (HQ + HKV) * D
 
     def per_layer(fn):
-        return _events_time(lambda: [fn(w) for w in L], 10) / len(L)
+        return _graph_time(lambda: [fn(w) for w in L], 10, len(L), copies=4)
 
     rows = {
         "qkv_2048x4096": (lambda w: C.decode_qkv(eng.hid, None, None, None, w["gamma_in"], cfg.eps,
@@ -138,8 +165,8 @@ def kernel_lines(eng) -> dict:
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes}
-    ms = _events_time(lambda: C.lm_head_argmax(eng.hid, eng.gamma_final, cfg.eps, eng.embed,
-                                               eng.logits, eng.bv, eng.bi), 20)
+    ms = _graph_time(lambda: C.lm_head_argmax(eng.hid, eng.gamma_final, cfg.eps, eng.embed,
+                                              eng.logits, eng.bv, eng.bi), 20)
     nbytes = cfg.vocab * H * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
     out["lm_head_151936x2048"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
@@ -186,12 +213,12 @@ def decode_layer_ctx4096(eng) -> dict:
         C.rmsnorm_gemv_swiglu(h1, w["gamma_post"], cfg.eps, w["w_gu"], act)
         C.gemv_residual(act, w["w_down"], h1, None, h)
 
-    ms = _events_time(lambda: [layer(w) for w in eng.layers], 10) / len(eng.layers)
+    ms = _graph_time(lambda: [layer(w) for w in eng.layers], 10, len(eng.layers), copies=2)
     wbytes = sum(t.numel() * 2 for t in eng.layers[0].values())
     kv = 2 * ctx * HKV * D * 2
     nbytes = wbytes + kv
     gbs = nbytes / (ms * 1e-3) / 1e9
-    ms_attn = _events_time(lambda: (
+    ms_attn = _graph_time(lambda: (
         C.decode_attention(qk, None, eng.layers[0]["gamma_q"], eng.layers[0]["gamma_k"], cfg.eps, cos, sin, kc,
                            vc, wr, wr, HQ, HKV, split, cfg.scale, op, mp, lp, False, err),
         C.attn_combine(op, mp, lp, attn, wr, split)), 50)
@@ -249,7 +276,7 @@ def mla_decode() -> dict:
                         blk.lp, blk.err)
         C.mla_combine_up(blk.op, blk.mp, blk.lp, blk.pos, blk.split, blk.w["w_kv_b"], blk.attn)
 
-    ms_core = _events_time(core, 100)
+    ms_core = _graph_time(core, 20)
     cache = B * cap * (cfg.kv_lora + cfg.rope) * 2
     weights = sum(t.numel() * 2 for k, t in blk.w.items() if k.startswith("w_"))
     out = {"workload": "MiniCPM3-4B-shaped MLA decode attention block, batch 8, 8192 positions, absorbed",

@@ -168,7 +168,7 @@ int tfa_decode_qkv(const void* h, const void* table, const int64_t* ids, int64_t
 /* Split-KV GQA decode attention (head_dim 128) for `batch` sequences, each with
  * its own cache [cap, hkv*128] (position-major; k_cache / v_cache are
  * [batch, cap, hkv*128]) attending its slots 0..wr[b]. Scores scaled by `scale`
- * in f32 after the dot; softmax in f32 per split of `split` (64, 128 or 256)
+ * in f32 after the dot; softmax in f32 per split of `split` (32, 64, 128 or 256)
  * slots; bf16 weights into P.V. Partials op [batch, cap/split, hq, 128],
  * mp / lp [batch, cap/split, hq]; splits past wr[b] are left untouched unless
  * `neutral` (then m = -1e30, l = 0, o = 0).

@@ -47,9 +47,19 @@ def _run(cmd: list[str]) -> None:
         )
 
 
+# Per-file code-generation options. The prefill attention keeps its output
+# accumulators (64 KB per wave) and its resident Q operands in one wave's full
+# register budget; with MFMA results allowed in the vector registers the
+# allocator fits both without spilling (with them forced into the accumulation
+# registers it spills).
+FILE_FLAGS = {
+    "prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile_hip(src: Path) -> Path:
     out = OBJ / (src.name + ".o")
-    _run([HIPCC, *HIPFLAGS, "-c", str(src), "-o", str(out)])
+    _run([HIPCC, *HIPFLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(out)])
     return out
 
 

@@ -306,19 +306,112 @@ template <int G>
 int launch_attn_g(const AttnArgs& a, int ss, int batch, hipStream_t st) {
   const dim3 grid(a.ns, a.hkv, batch);
   switch (ss) {
+    case 32: attn_decode_kernel<G, 2><<<grid, kThreads, 0, st>>>(a); break;
     case 64: attn_decode_kernel<G, 4><<<grid, kThreads, 0, st>>>(a); break;
     case 128: attn_decode_kernel<G, 8><<<grid, kThreads, 0, st>>>(a); break;
     case 256: attn_decode_kernel<G, 16><<<grid, kThreads, 0, st>>>(a); break;
-    default: return fail(TFA_ERR_SHAPE, "attn_decode: split %d not in {64, 128, 256}", ss);
+    default: return fail(TFA_ERR_SHAPE, "attn_decode: split %d not in {32, 64, 128, 256}", ss);
   }
   return launched("attn_decode");
 }
 
 // Merge: out[h*Dh + d] = bf16(sum_s op e^(mp-M) / sum_s lp e^(mp-M)). With wr,
-// only the splits that hold slots <= wr[0] are read. One block per head: the
-// split statistics arrive in one parallel round trip, then eight groups of
-// threads each sum every eighth split of the partial outputs, so the loads of
-// all splits are in flight together; the groups meet in LDS in group order.
+// only the splits that hold slots <= wr[0] count. One block per head, one
+// memory round trip: every load -- wr, one split's statistics per thread, and
+// eight splits' partial outputs per thread -- is issued at the start (the
+// partial outputs do not depend on the statistics, and splits past wr are read
+// but never used: their rows are allocated, possibly stale). The block max and
+// the denominator are tree reductions; eight groups of threads sum every eighth
+// split and meet in LDS in group order.
+constexpr int kCombThreads = 1024;
+constexpr int kCombWaves = kCombThreads / kWave;
+constexpr int kCombGroups = 8;
+constexpr int kCombMaxSplits = kCombThreads;
+constexpr int kCombMaxD = kCombThreads / kCombGroups;
+constexpr int kCombUnroll = 8;
+
+__global__ __launch_bounds__(kCombThreads) void attn_combine_kernel(
+    const float* op, const float* mp, const float* lp, uint16_t* out, int ns, int hq, int Dh,
+    const int* wr, int split) {
+  const int bb = blockIdx.y;
+  op += static_cast<size_t>(bb) * ns * hq * Dh;
+  mp += static_cast<size_t>(bb) * ns * hq;
+  lp += static_cast<size_t>(bb) * ns * hq;
+  out += static_cast<size_t>(bb) * hq * Dh;
+  __shared__ float s_e[kCombMaxSplits];
+  __shared__ float s_red[kCombGroups][kCombMaxD];
+  __shared__ float s_w[2][kCombWaves];
+  const int h = blockIdx.x;
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1), wid = t / kWave;
+  const int gi = t / kCombMaxD;
+  const int d = t % kCombMaxD;
+  const int nsc = ns < kCombMaxSplits ? ns : kCombMaxSplits;
+  // 1. every load of the first round, together
+  const int w = wr ? wr[bb] : 0;
+  const bool in = t < nsc;
+  const float mj0 = in ? mp[t * hq + h] : -INFINITY;
+  const float lj0 = in ? lp[t * hq + h] : 0.f;
+  float v[kCombUnroll];
+#pragma unroll
+  for (int u = 0; u < kCombUnroll; ++u) {
+    const int j = gi + u * kCombGroups;
+    v[u] = (d < Dh && j < nsc) ? op[(static_cast<size_t>(j) * hq + h) * Dh + d] : 0.f;
+  }
+  int nact = nsc;
+  if (wr) {
+    nact = w < 0 ? 0 : w / split + 1;
+    if (nact > nsc) nact = nsc;
+  }
+  // 2. statistics: block max, weights, denominator
+  const bool act = t < nact;
+  const float mj = act ? mj0 : -INFINITY;
+  float mx = wave_max(mj);
+  if (lane == 0) s_w[0][wid] = mx;
+  __syncthreads();
+  mx = s_w[0][0];
+#pragma unroll
+  for (int k = 1; k < kCombWaves; ++k) mx = fmaxf(mx, s_w[0][k]);
+  const float e = act ? expf(mj - mx) : 0.f;
+  s_e[t] = e;
+  const float dw = wave_sum(act ? lj0 * e : 0.f);
+  if (lane == 0) s_w[1][wid] = dw;
+  __syncthreads();
+  float den = 0.f;
+#pragma unroll
+  for (int k = 0; k < kCombWaves; ++k) den += s_w[1][k];
+  // 3. partial outputs: group gi sums splits gi, gi + 8, ...
+  if (d < Dh) {
+    float num = 0.f;
+#pragma unroll
+    for (int u = 0; u < kCombUnroll; ++u) {
+      const int j = gi + u * kCombGroups;
+      if (j < nact) num = fmaf(v[u], s_e[j], num);
+    }
+    for (int j0 = gi + kCombGroups * kCombUnroll; j0 < nact; j0 += kCombGroups * kCombUnroll) {
+      float x[kCombUnroll];
+#pragma unroll
+      for (int u = 0; u < kCombUnroll; ++u) {
+        const int j = j0 + u * kCombGroups;
+        x[u] = j < nact ? op[(static_cast<size_t>(j) * hq + h) * Dh + d] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kCombUnroll; ++u) {
+        const int j = j0 + u * kCombGroups;
+        if (j < nact) num = fmaf(x[u], s_e[j], num);
+      }
+    }
+    s_red[gi][d] = num;
+  }
+  __syncthreads();
+  if (t < Dh) {
+    float num = 0.f;
+#pragma unroll
+    for (int g = 0; g < kCombGroups; ++g) num += s_red[g][t];
+    out[h * Dh + t] = static_cast<uint16_t>(f2bf(num / den));
+  }
+}
+
 // qk_rope_cache: one wave per head of the [q | k | v] projection, summed from
 // its split-K partials [ks, B, (hq + 2 hkv) * 128] and landed in bf16. Query
 // heads get the per-head norm and RoPE at pos[b] and go to q_out; the key head
@@ -376,68 +469,6 @@ __global__ __launch_bounds__(kThreads) void qk_rope_cache_kernel(
   }
   dst[lane] = static_cast<uint16_t>(f2bf(o0));
   dst[lane + 64] = static_cast<uint16_t>(f2bf(o1));
-}
-
-constexpr int kCombThreads = 1024;
-constexpr int kCombGroups = 8;
-constexpr int kCombMaxSplits = 1024;
-constexpr int kCombMaxD = kCombThreads / kCombGroups;
-
-__global__ __launch_bounds__(kCombThreads) void attn_combine_kernel(
-    const float* op, const float* mp, const float* lp, uint16_t* out, int ns, int hq, int Dh,
-    const int* wr, int split) {
-  const int bb = blockIdx.y;
-  op += static_cast<size_t>(bb) * ns * hq * Dh;
-  mp += static_cast<size_t>(bb) * ns * hq;
-  lp += static_cast<size_t>(bb) * ns * hq;
-  out += static_cast<size_t>(bb) * hq * Dh;
-  __shared__ float s_e[kCombMaxSplits];
-  __shared__ float s_l[kCombMaxSplits];
-  __shared__ float s_red[kCombGroups][kCombMaxD];
-  __shared__ float s_mx[kCombThreads / kWave];
-  __shared__ float s_den;
-  const int h = blockIdx.x;
-  const int t = threadIdx.x;
-  int nact = ns;
-  if (wr) {
-    const int w = wr[bb];
-    nact = w < 0 ? 0 : w / split + 1;
-    if (nact > ns) nact = ns;
-  }
-  if (nact > kCombMaxSplits) nact = kCombMaxSplits;
-  // 1. statistics, one split per thread
-  float mj = -INFINITY;
-  for (int j = t; j < nact; j += kCombThreads) {
-    mj = fmaxf(mj, mp[j * hq + h]);
-    s_l[j] = lp[j * hq + h];
-  }
-  float mx = wave_max(mj);
-  if ((t & (kWave - 1)) == 0) s_mx[t / kWave] = mx;
-  __syncthreads();
-  mx = -INFINITY;
-  for (int w = 0; w < kCombThreads / kWave; ++w) mx = fmaxf(mx, s_mx[w]);
-  for (int j = t; j < nact; j += kCombThreads) s_e[j] = expf(mp[j * hq + h] - mx);
-  __syncthreads();
-  if (t == 0) {
-    float den = 0.f;
-    for (int j = 0; j < nact; ++j) den = fmaf(s_l[j], s_e[j], den);
-    s_den = den;
-  }
-  // 2. partial outputs: group gi sums splits gi, gi + 8, ...
-  const int gi = t / kCombMaxD;
-  const int d = t % kCombMaxD;
-  if (d < Dh) {
-    float num = 0.f;
-    for (int j = gi; j < nact; j += kCombGroups)
-      num = fmaf(op[(static_cast<size_t>(j) * hq + h) * Dh + d], s_e[j], num);
-    s_red[gi][d] = num;
-  }
-  __syncthreads();
-  if (t < Dh) {
-    float num = 0.f;
-    for (int g = 0; g < kCombGroups; ++g) num += s_red[g][t];
-    out[h * Dh + t] = static_cast<uint16_t>(f2bf(num / s_den));
-  }
 }
 
 }  // namespace

@@ -194,54 +194,94 @@ TFA_DEV float rsqrt_rn(float x) { return 1.0f / __fsqrt_rn(x); }
 
 TFA_DEV float silu(float x) { return x / (1.0f + __expf(-x)); }
 
-// --------------------------------------------------- last block finishes
-// A group of blocks each publishes a slice of a result, then one of them --
-// whichever arrives last -- runs the step that needs the whole result. The
-// counter resets itself, so the same buffer serves every launch (and every
-// replay of a captured graph) without a memset.
-//
-// Coherence without whole-cache maintenance: on gfx950 each XCD has its own
-// L2, and an agent-scope fence (`__threadfence`) writes back and invalidates
-// that entire L2 -- once per block, serialised, it costs milliseconds over a
-// 10k-block grid. So slices are published with agent-scope atomic stores
-// (`global_store ... sc1`, written through to the coherent level) and read
-// back with agent-scope atomic loads (`global_load ... sc1`). Each thread waits
-// for its own publishing stores to complete (`s_waitcnt`) before the block
-// barrier, and only then does one thread bump the counter: every slice a block
-// published is visible at agent scope before its arrival is counted. Data that
-// is only consumed by a later kernel uses ordinary stores (the kernel boundary
-// orders it).
-TFA_DEV void publish(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-TFA_DEV void publish(int* p, int v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-TFA_DEV float fetch(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-TFA_DEV int fetch(const int* p) {
-  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector-memory
+// operations are in flight, expcnt and lgkmcnt left open. vmcnt is six bits,
+// split over bits [3:0] and [15:14] of the immediate.
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+static_assert(waitcnt_vm(0) == 0xF70 && waitcnt_vm(16) == 0x4F70 && waitcnt_vm(63) == 0xCF7F,
+              "vmcnt encoding");
+
+// Direct global -> LDS load of 16 bytes per lane: lane i's bytes land at LDS
+// byte offset lds_off + 16 i (lds_off, held in M0, is wave-uniform; lanes
+// switched off by exec write nothing). Issued as an instruction the compiler
+// does not see into, so its wait-count bookkeeping does not make every LDS read
+// wait for every such load in flight: the caller tracks these loads with its
+// own vmcnt waits (vector-memory loads complete in issue order), and must wait
+// for all of them before its block ends.
+TFA_DEV void lds_dma16(const void* g, uint32_t lds_off) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_off) : "memory");
 }
 
-// Returns true in exactly one block of the group. Every thread of the block
-// must call it (it synchronises the block). Slices must have been written with
-// publish() and must be read with fetch().
-TFA_DEV bool arrive_last(unsigned int* counter, unsigned int group_size, int* flag_smem) {
-  __builtin_amdgcn_s_waitcnt(0);    // this thread's published stores are complete
+// The 32-bit LDS byte offset of a __shared__ object.
+template <typename T>
+TFA_DEV uint32_t lds_offset(T* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void*)p));
+}
+
+// Block barrier that leaves loads in flight: the compiler may not move memory
+// operations across it, and it adds no wait of its own (a __syncthreads() also
+// waits for every outstanding load, which would drain a software pipeline).
+// The caller waits for what the other waves must see before calling it.
+TFA_DEV void block_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned int prev =
-        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = (prev == group_size - 1);
-    // No other block of this launch touches the counter after the last arrival.
-    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *flag_smem = last;
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// ------------------------------------------------------------ greedy pick
+// (value, index) order for greedy argmax: the larger value wins, equal values go
+// to the lower index (torch.argmax), NaN never wins.
+TFA_DEV bool better_pick(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// The best (value, lowest index) pair of nb candidates, reduced by a whole block
+// (blockDim.x a multiple of 64, at most 1024; s_v / s_i hold one entry per
+// wave). Each thread issues eight loads before its first compare. The returned
+// index is valid in thread 0.
+TFA_DEV int block_best(const float* bv, const int* bi, int nb, float* s_v, int* s_i) {
+  const int t = threadIdx.x, nt = blockDim.x;
+  float best_v = -3.402823466e38f;
+  int best_i = 0x7fffffff;
+  for (int b0 = t; b0 < nb; b0 += 8 * nt) {
+    float v[8];
+    int ix[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int b = b0 + u * nt;
+      const bool ok = b < nb;
+      v[u] = ok ? bv[b] : -3.402823466e38f;
+      ix[u] = ok ? bi[b] : 0x7fffffff;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (better_pick(v[u], ix[u], best_v, best_i)) {
+        best_v = v[u];
+        best_i = ix[u];
+      }
+  }
+#pragma unroll
+  for (int m = kWave / 2; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(best_v, m, kWave);
+    const int oi = __shfl_xor(best_i, m, kWave);
+    if (better_pick(ov, oi, best_v, best_i)) {
+      best_v = ov;
+      best_i = oi;
+    }
+  }
+  if ((t & (kWave - 1)) == 0) {
+    s_v[t / kWave] = best_v;
+    s_i[t / kWave] = best_i;
   }
   __syncthreads();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  return *flag_smem != 0;
+  if (t == 0) {
+    for (int w = 1; w < nt / kWave; ++w)
+      if (better_pick(s_v[w], s_i[w], best_v, best_i)) {
+        best_v = s_v[w];
+        best_i = s_i[w];
+      }
+  }
+  return best_i;
 }
 
 }  // namespace tfa

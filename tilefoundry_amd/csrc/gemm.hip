@@ -53,8 +53,8 @@ struct GemmArgs {
 TFA_DEV int swz(int row) { return (row >> 1) & 7; }
 
 // s_waitcnt immediates (gfx9 encoding): vmcnt(n) with expcnt / lgkmcnt left open.
-constexpr int kWaitVm16 = 16 | (7 << 4) | (15 << 8);
-constexpr int kWaitVm0 = 0 | (7 << 4) | (15 << 8);
+constexpr int kWaitVm16 = waitcnt_vm(16);
+constexpr int kWaitVm0 = waitcnt_vm(0);
 
 template <int EPI>
 __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const GemmArgs a) {
@@ -79,8 +79,7 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const GemmArgs a) {
       const int q = (lane & 7) ^ swz(row);
       const uint16_t* src = row < kBM ? a.a + static_cast<size_t>(m0 + row) * a.lda
                                       : a.b + static_cast<size_t>(n0 + row - kBM) * a.ldb;
-      __builtin_amdgcn_global_load_lds(src + k0 + 8 * q, (__attribute__((address_space(3))) void*)&smem[buf][8 * j][0],
-                                       16, 0, 0);
+      lds_dma16(src + k0 + 8 * q, lds_offset(&smem[buf][8 * j][0]));
     }
   };
 
@@ -99,11 +98,11 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const GemmArgs a) {
     const int buf = kt & 1;
     if (kt + 1 < nk) {
       load_stage(kt + 1, buf ^ 1);
-      __builtin_amdgcn_s_waitcnt(kWaitVm16);
+      __builtin_amdgcn_s_waitcnt(kWaitVm16);   // stage kt landed; stage kt + 1 stays in flight
     } else {
       __builtin_amdgcn_s_waitcnt(kWaitVm0);
     }
-    __syncthreads();
+    block_barrier();   // every wave's stage kt landed
     const uint16_t* arow = &smem[buf][wm + n32][0];
     const uint16_t* brow = &smem[buf][kBM + wn + n32][0];
 #pragma unroll
@@ -121,7 +120,7 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const GemmArgs a) {
         for (int j = 0; j < 4; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(aop[i]), as_bf8(bop[j]), acc[i][j], 0, 0, 0);
     }
-    __syncthreads();   // every wave is done with buf before it is refilled
+    block_barrier();   // every wave is done with buf before it is refilled
   }
 
   // acc[i][j][4t + r]: row m0 + wm + 32i + 8t + 4kg + r, column n0 + wn + 32j + n32

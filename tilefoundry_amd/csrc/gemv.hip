@@ -289,28 +289,16 @@ int check_vec(const void* p, const char* what, const char* name) {
 // Final greedy pick over the head's block winners, then the sample step:
 // record the pick at pos, feed the next prompt id while the prompt lasts (else
 // the pick), advance pos. One block; ties go to the lowest index.
-__global__ __launch_bounds__(kThreads) void sample_kernel(
+constexpr int kSampleThreads = 1024;
+
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(
     const float* __restrict__ bv, const int* __restrict__ bi, int nb, const int* inp,
     const int* plen, int64_t* ids, int* pos, int* sam, int nsteps, int* err) {
-  __shared__ float rv[kThreads];
-  __shared__ int ri[kThreads];
+  __shared__ float rv[kSampleThreads / kWave];
+  __shared__ int ri[kSampleThreads / kWave];
   const int t = threadIdx.x;
-  float bvv = -FLT_MAX;
-  int bii = 0x7fffffff;
-  for (int b = t; b < nb; b += kThreads)
-    if (better(bv[b], bi[b], bvv, bii)) { bvv = bv[b]; bii = bi[b]; }
-  rv[t] = bvv;
-  ri[t] = bii;
-  __syncthreads();
-  for (int s = kThreads / 2; s > 0; s >>= 1) {
-    if (t < s && better(rv[t + s], ri[t + s], rv[t], ri[t])) {
-      rv[t] = rv[t + s];
-      ri[t] = ri[t + s];
-    }
-    __syncthreads();
-  }
+  const int best = block_best(bv, bi, nb, rv, ri);
   if (t == 0) {
-    const int best = ri[0];
     const int p = pos[0];
     if (p < 0 || p >= nsteps) {
       set_err(err, 2);
@@ -473,7 +461,7 @@ int tfa_sample_step(const float* block_val, const int* block_idx, int64_t nblock
   if (!block_val || !block_idx || !inp || !prompt_len || !ids || !pos || !sam)
     return fail(TFA_ERR_NULL, "tfa_sample_step: null pointer argument");
   if (nblocks <= 0 || nsteps <= 0) return fail(TFA_ERR_SHAPE, "tfa_sample_step: empty block list or step table");
-  sample_kernel<<<1, kThreads, 0, stream>>>(block_val, block_idx, (int)nblocks, inp, prompt_len,
+  sample_kernel<<<1, kSampleThreads, 0, stream>>>(block_val, block_idx, (int)nblocks, inp, prompt_len,
                                             ids, pos, sam, (int)nsteps, err);
   return launched("sample_step");
 }

@@ -2,27 +2,31 @@
 // (Qwen3.5-family full-attention layer, Qwen3.8-27B shapes: 24 query heads
 // over 4 key/value heads), on bf16 MFMA.
 //
-// One 512-thread block per (query head, 128 query rows); each pair of waves
-// owns 32 query rows -- one wave per half of the head dims -- and walks the
-// key tiles (32 keys) up to its diagonal. Per tile:
+// One 256-thread block per (query head, 128 query rows): each of the four
+// waves (one per SIMD) owns 32 query rows over the whole head dimension and
+// walks the 32-key tiles up to its diagonal. Per tile:
 //
-//   S^T = K . Q^T     v_mfma_f32_32x32x16_bf16, M = 32 keys, N = 32 queries;
-//                     each wave of the pair reduces its 128 dims (8 k-steps,
-//                     its half of Q resident as the B operand, K from LDS row
-//                     reads) and the two partials are added through LDS.
+//   S^T = K . Q^T     v_mfma_f32_32x32x16_bf16, M = 32 keys, N = 32 queries,
+//                     16 k-steps over D; Q^T is resident as the B operand, the
+//                     K operands stream from LDS through a ring of registers
+//                     (each read issued four k-steps ahead of its MFMA).
 //   online softmax    per query (the MFMA output column): the lane holds 16
 //                     of the tile's keys, its partner lane (l ^ 32) the other
-//                     16 -- one exchange for the row max; exp2 with the
-//                     scale folded in; the running max is only raised (and O
+//                     16 -- one exchange for the row max; exp2 with the scale
+//                     folded in; the running max is only raised (and O
 //                     rescaled) when a row's max passes it by more than 2^8.
-//   O^T += V^T . P^T  M = 32 value dims (4 tiles over the wave's half of D),
-//                     K = 16 keys per step; P^T is the bf16 score accumulator (its key
-//                     slots relabelled), V^T comes from ds_read_b64_tr_b16
-//                     transpose reads of the row-major V tile.
+//   O^T += V^T . P^T  M = 32 value dims (8 tiles over D), K = 16 keys per
+//                     step; P^T is the bf16 score accumulator (its key slots
+//                     relabelled), V^T comes from ds_read_b64_tr_b16 transpose
+//                     reads of the row-major V tile, also streamed ahead.
 //
 // K and V tiles stream global -> LDS with global_load_lds_dwordx4 (no register
-// staging), three buffers deep (loads run two tiles ahead); with the score
-// exchange 138 KB of LDS per block, two waves per SIMD.
+// staging) through a three-stage ring, loads running two tiles ahead. Each
+// stage is its own LDS object and the block barrier is a bare s_barrier after
+// an explicit wait for this wave's loads of the current tile, so the loads of
+// the next tile stay in flight across it. 106 KB of LDS per block, one wave per
+// SIMD; the output accumulators (256 dims x 32 queries, f32) and Q stay in
+// registers.
 // Epilogue in the reference's order: out = bf16(bf16(o / l) * bf16(sigmoid(gate))).
 //
 // Reference (jingchangshi/TileFoundry): examples/qwen3_8_27b_prefill-tilelang/model.py:305-324
@@ -39,10 +43,9 @@ using namespace tfa;
 namespace {
 
 constexpr int D = 256;
-constexpr int kBM = 128;    // query rows per block
-constexpr int kBN = 32;     // keys per tile
-constexpr int kThreads = 256;
-constexpr int kChunks = D / 8;   // 16-byte chunks per 512-byte row
+constexpr int kWaves = 4;           // one per SIMD
+constexpr int kBM = 32 * kWaves;    // query rows per block (32 per wave)
+constexpr int kBN = 32;             // keys per tile
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -69,9 +72,14 @@ struct FlashArgs {
 // operand address is one per-lane base plus an immediate offset.
 constexpr int kKPitch = D + 8;    // elements
 constexpr int kVPitch = D + 32;
-constexpr int kPairs = 4;         // wave pairs per block, 32 queries each
 constexpr int kStages = 3;        // K / V tile buffers: loads run two tiles ahead
-constexpr int kHalf = D / 2;      // head dims per wave of a pair
+constexpr int kDT = D / 32;       // 32-dim output tiles
+constexpr int kST = D / 16;       // 16-dim score k-steps
+constexpr int kKPF = 4;           // K operand reads in flight ahead of the score MFMAs
+constexpr int kVPF = 3;           // V^T operand pairs in flight ahead of the output MFMAs
+// sched_group_barrier instruction classes
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
 
 TFA_DEV uint2 ld_tr(const uint16_t* lds_elem) {
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -79,30 +87,38 @@ TFA_DEV uint2 ld_tr(const uint16_t* lds_elem) {
   return __builtin_bit_cast(uint2, v);
 }
 
-// s_waitcnt immediates (gfx9 encoding): vmcnt(n) with expcnt / lgkmcnt left open.
-constexpr int kWaitVm8 = 8 | (7 << 4) | (15 << 8);
-constexpr int kWaitVm0 = 0 | (7 << 4) | (15 << 8);
+constexpr int kWaitVm0 = waitcnt_vm(0);
+constexpr int kWaitVm16 = waitcnt_vm(16);   // one tile's loads of one wave
 
 template <int N>
 using IC = std::integral_constant<int, N>;
 
-// 512 threads: wave pair p owns queries q0 = 128 qt + 32 p; wave `half` of the
-// pair owns head dims [128 half, 128 half + 128) of the scores' reduction and
-// of the output. The pair's partial scores meet in LDS (f32 addition is
-// commutative, so both waves hold bit-identical scores and run the same
-// softmax).
-__global__ __launch_bounds__(2 * kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void flash_prefill_kernel(const FlashArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[kStages][kBN][kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t vs[kStages][kBN][kVPitch];
-  __shared__ float xch[kPairs][2][16][kWave];
+  constexpr int QT = 1;       // 32-row query tiles per wave
+  constexpr int kWM = 32 * QT;
+  // one LDS object per ring stage, indexed only by compile-time stage numbers
+  __shared__ __attribute__((aligned(16))) uint16_t ks0[kBN][kKPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t ks1[kBN][kKPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t ks2[kBN][kKPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t vs0[kBN][kVPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t vs1[kBN][kVPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t vs2[kBN][kVPitch];
+  auto kbuf = [&](auto b) __attribute__((always_inline)) -> uint16_t(*)[kKPitch] {
+    if constexpr (decltype(b)::value == 0) return ks0;
+    else if constexpr (decltype(b)::value == 1) return ks1;
+    else return ks2;
+  };
+  auto vbuf = [&](auto b) __attribute__((always_inline)) -> uint16_t(*)[kVPitch] {
+    if constexpr (decltype(b)::value == 0) return vs0;
+    else if constexpr (decltype(b)::value == 1) return vs1;
+    else return vs2;
+  };
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);   // wave-uniform, scalar
-  const int pair = wid >> 1;
-  const int half = wid & 1;
-  const int n32 = lane & 31;    // MFMA column (query) / row (key, value dim) index
-  const int kg = lane >> 5;     // k-group
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int n32 = lane & 31;
+  const int kg = lane >> 5;
   // Work order. Consecutive block ids are dispatched round-robin over the 8
   // XCDs (each with its own L2); XCD x takes a run of consecutive heads --
   // heads of one key/value group when the counts divide evenly -- so each L2
@@ -119,167 +135,210 @@ void flash_prefill_kernel(const FlashArgs a) {
     qt = nqt - 1 - blockIdx.x / a.HQ;
   }
   const int g = h / (a.HQ / a.HKV);
-  const int q0 = qt * kBM + pair * 32;         // the pair's first query row
-  const int ntiles = (qt + 1) * kBM / kBN;     // key tiles the block walks
-  const int my_last = q0 / kBN;                // the pair's diagonal tile
+  const int q0 = qt * kBM + wid * kWM;          // the wave's first query row
+  const int ntiles = (qt + 1) * kBM / kBN;      // key tiles the block walks
+  const int my_last = (q0 + kWM - 1) / kBN;     // the wave's last tile with a visible key
 
   // direct global -> LDS tile loads, one 512-byte row per instruction (lanes
-  // 0..31): wave w moves rows 4w .. 4w+3 of K and of V
-  // (row pointers are wave-uniform: scalar base + the lane's 16-byte offset)
-  auto load_tile = [&](int kt, int buf) __attribute__((always_inline)) {
-    const size_t r0 = static_cast<size_t>(kt) * kBN + 4 * wid;
+  // 0..31): wave w moves rows 8w .. 8w+7 of K and of V. Every step issues
+  // exactly one tile's loads (past the last tile it reloads the last tile into
+  // the free stage, where nothing reads it), so the number of loads in flight
+  // behind tile kt is always one tile's and every wait count is a constant.
+  auto load_tile = [&](int kt, auto b) __attribute__((always_inline)) {
+    kt = kt < ntiles ? kt : ntiles - 1;
+    const size_t r0 = static_cast<size_t>(kt) * kBN + 8 * wid;
+    uint16_t(*kb)[kKPitch] = kbuf(b);
+    uint16_t(*vb)[kVPitch] = vbuf(b);
     if (lane < 32) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 8; ++i) {
         const uint16_t* krow = a.k + (r0 + i) * a.k_rs + g * a.k_hs;
         const uint16_t* vrow = a.v + (r0 + i) * a.v_rs + g * a.v_hs;
-        __builtin_amdgcn_global_load_lds(krow + 8 * n32,
-                                         (__attribute__((address_space(3))) void*)&ks[buf][4 * wid + i][0], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vrow + 8 * n32,
-                                         (__attribute__((address_space(3))) void*)&vs[buf][4 * wid + i][0], 16, 0, 0);
+        lds_dma16(krow + 8 * n32, lds_offset(&kb[8 * wid + i][0]));
+        lds_dma16(vrow + 8 * n32, lds_offset(&vb[8 * wid + i][0]));
       }
     }
   };
 
-  // this wave's half of Q, resident: lane (query q0 + n32, k-group kg) holds
-  // Q[.][128 half + 16 st + 8 kg .. +7]
-  uint4 qop[kHalf / 16];
-  {
-    const uint16_t* qrow = a.q + static_cast<size_t>(q0 + n32) * a.q_rs + h * a.q_hs + kHalf * half + 8 * kg;
+  // Q^T operands, resident: q-tile t, lane (query q0 + 32t + n32, k-group kg)
+  // holds Q[.][16 st + 8 kg .. +7]
+  uint4 qop[QT][kST];
 #pragma unroll
-    for (int st = 0; st < kHalf / 16; ++st) qop[st] = ld16(qrow + 16 * st);
+  for (int t = 0; t < QT; ++t) {
+    const uint16_t* qrow = a.q + static_cast<size_t>(q0 + 32 * t + n32) * a.q_rs + h * a.q_hs + 8 * kg;
+#pragma unroll
+    for (int st = 0; st < kST; ++st) qop[t][st] = ld16(qrow + 16 * st);
   }
-  load_tile(0, 0);
-  if (ntiles > 1) load_tile(1, 1);
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);   // Q is in; from here on only tile loads are in flight
+  load_tile(0, IC<0>{});
+  load_tile(1, IC<1>{});
 
-  f32x16 o[kHalf / 32];   // O^T rows (value dims) 128 half + 32 mt + ...
+  f32x16 o[kDT][QT];   // O^T: value dims 32 dt + ..., queries q0 + 32 t + n32
 #pragma unroll
-  for (int mt = 0; mt < kHalf / 32; ++mt)
+  for (int dt = 0; dt < kDT; ++dt)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) o[mt][e] = 0.f;
+    for (int t = 0; t < QT; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[dt][t][e] = 0.f;
   // Running row max (log2 units). It is only raised when some row's tile max
   // passes it by more than kSlack, so the weights exp2(s - m) stay <= 2^kSlack
   // (exact in f32, in range for bf16) and O is rescaled rarely; the final
   // o / l is the same softmax.
   constexpr float kSlack = 8.0f;
-  float m_run = -INFINITY, l_run = 0.f;
+  float m_run[QT], l_run[QT];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    m_run[t] = -INFINITY;
+    l_run[t] = 0.f;
+  }
 
   const int L = lane & 15;
   const int half16 = (lane >> 4) & 1;
-  int buf = 0;
-  for (int kt = 0; kt < ntiles; ++kt) {
-    if (kt + 1 < ntiles) __builtin_amdgcn_s_waitcnt(kWaitVm8);   // tile kt landed, kt + 1 may fly
-    else __builtin_amdgcn_s_waitcnt(kWaitVm0);
-    __syncthreads();   // tile kt visible; every wave is done with iteration kt - 1
-    if (kt + 2 < ntiles) load_tile(kt + 2, buf == 0 ? 2 : buf - 1);   // the buffer of tile kt - 1
+  // One key tile in ring stage `b`. The block barrier is a bare s_barrier
+  // between compiler fences: each wave first waits for its own loads of tile
+  // kt (the loads of kt + 1 stay in flight), and its reads of the stage being
+  // refilled were consumed by MFMAs of the previous step before it arrives.
+  auto step = [&](int kt, auto b) __attribute__((always_inline)) {
+    constexpr int B = decltype(b)::value;
+    __builtin_amdgcn_s_waitcnt(kWaitVm16);   // tile kt landed; the next tile's loads may fly
+    block_barrier();
+    load_tile(kt + 2, IC<(B + 2) % kStages>{});   // into the stage of tile kt - 1
+    uint16_t(*kb)[kKPitch] = kbuf(b);
+    uint16_t(*vb)[kVPitch] = vbuf(b);
 
-    const bool active = kt <= my_last;   // pair-uniform: later tiles hold no visible key
-    f32x16 s;
-    const uint16_t* vrow = &vs[buf][4 * kg + (L >> 2)][kHalf * half + 16 * half16 + 4 * (L & 3)];
-    uint4 vop0[kHalf / 32], vop1[kHalf / 32];
-    if (active) {
-      // partial S^T = K[:, half] . Q[:, half]^T: element e = 4j + r is key
-      // kt*32 + 8j + 4kg + r, query q0 + n32
-      const uint16_t* krow = &ks[buf][n32][kHalf * half + 8 * kg];
-      uint4 kop[kHalf / 16];
+    if (kt <= my_last) {   // wave-uniform: later tiles hold no key this wave sees
+      // S^T = K . Q^T: element e = 4j + r is key 32 kt + 8j + 4kg + r,
+      // query q0 + 32 t + n32
+      f32x16 s[QT];
 #pragma unroll
-      for (int st = 0; st < kHalf / 16; ++st) kop[st] = *reinterpret_cast<const uint4*>(krow + 16 * st);
-      // V^T operands of this wave's value dims (A operand, row = value dim
-      // 128 half + 32 mt + n32): key rows 16 ks2 + 4kg + L/4 and +8
+      for (int t = 0; t < QT; ++t)
 #pragma unroll
-      for (int mt = 0; mt < kHalf / 32; ++mt) {
-        const uint2 v1 = ld_tr(vrow + 32 * mt);
-        const uint2 v2 = ld_tr(vrow + 8 * kVPitch + 32 * mt);
-        vop0[mt] = make_uint4(v1.x, v1.y, v2.x, v2.y);
+        for (int e = 0; e < 16; ++e) s[t][e] = 0.f;
+      // K operands stream through a ring of kKPF registers: the read for
+      // k-step st + kKPF is issued behind the MFMA of k-step st
+      const uint16_t* krow = &kb[n32][8 * kg];
+      uint4 kq[kKPF];
+#pragma unroll
+      for (int i = 0; i < kKPF; ++i) kq[i] = *reinterpret_cast<const uint4*>(krow + 16 * i);
+#pragma unroll
+      for (int st = 0; st < kST; ++st) {
+        const uint4 kop = kq[st % kKPF];
+        if (st + kKPF < kST) kq[st % kKPF] = *reinterpret_cast<const uint4*>(krow + 16 * (st + kKPF));
+#pragma unroll
+        for (int t = 0; t < QT; ++t)
+          s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kop), as_bf8(qop[t][st]), s[t], 0, 0, 0);
       }
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kKPF, 0);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s[e] = 0.f;
-#pragma unroll
-      for (int st = 0; st < kHalf / 16; ++st)
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kop[st]), as_bf8(qop[st]), s, 0, 0, 0);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) xch[pair][half][e][lane] = s[e];
-#pragma unroll
-      for (int mt = 0; mt < kHalf / 32; ++mt) {
-        const uint2 v1 = ld_tr(vrow + 16 * kVPitch + 32 * mt);
-        const uint2 v2 = ld_tr(vrow + 24 * kVPitch + 32 * mt);
-        vop1[mt] = make_uint4(v1.x, v1.y, v2.x, v2.y);
+      for (int st = 0; st < kST; ++st) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, QT, 0);
+        if (st + kKPF < kST) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
       }
-    }
-    __syncthreads();   // both halves of every pair's scores are in LDS
-
-    if (active) {
-      // full (unscaled) score; the scale is applied inside exp2's argument
-      float mx = -INFINITY;
+      // online softmax per query tile (the scale is folded into exp2's argument)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        s[e] += xch[pair][half ^ 1][e][lane];
-        mx = fmaxf(mx, s[e]);
-      }
-      if (kt == my_last) {   // the diagonal tile: keys past the query are masked
-        mx = -INFINITY;
+      for (int t = 0; t < QT; ++t) {
+        const int qrow0 = q0 + 32 * t;
+        if (kt * kBN + kBN - 1 > qrow0) {   // tile reaches past this query tile's first row
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int kk = 8 * (e >> 2) + 4 * kg + (e & 3);
-          s[e] = kk > n32 ? -INFINITY : s[e];
-          mx = fmaxf(mx, s[e]);
+          for (int e = 0; e < 16; ++e) {
+            const int kk = kt * kBN + 8 * (e >> 2) + 4 * kg + (e & 3);
+            s[t][e] = kk > qrow0 + n32 ? -INFINITY : s[t][e];
+          }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * a.scale_log2;
+        if (__builtin_amdgcn_ballot_w64(mx > m_run[t] + kSlack) != 0) {
+          const float m_new = fmaxf(m_run[t], mx);
+          const float alpha = m_run[t] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[t] - m_new);
+          l_run[t] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) o[dt][t][e] *= alpha;
+          m_run[t] = m_new;
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * a.scale_log2;   // log2 units (scale > 0)
-      if (__builtin_amdgcn_ballot_w64(mx > m_run + kSlack) != 0) {   // raise the max: rescale
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-        l_run *= alpha;
+      // O^T += V^T . P^T: k-step ks2 takes keys 16 ks2 + {4kg + r, 8 + 4kg + r}
+      // = score elements 8 ks2 + r, 8 ks2 + 4 + r; each V^T operand serves
+      // every query tile
+      const uint16_t* vrow = &vb[4 * kg + (L >> 2)][16 * half16 + 4 * (L & 3)];
+      uint4 pop[2][QT];
 #pragma unroll
-        for (int mt = 0; mt < kHalf / 32; ++mt)
+      for (int ks2 = 0; ks2 < 2; ++ks2)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) o[mt][e] *= alpha;
-        m_run = m_new;
-      }
-      // O^T += V^T . P^T. P^T is the B operand: k-step ks2 takes keys
-      // 16ks2 + {4kg + r, 8 + 4kg + r} = score elements 8ks2 + r, 8ks2 + 4 + r
-      auto pv = [&](int ks2, const uint4* vop) __attribute__((always_inline)) {
-        float p[8];
+        for (int t = 0; t < QT; ++t) {
+          float p[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          p[i] = __builtin_amdgcn_exp2f(fmaf(s[8 * ks2 + i], a.scale_log2, -m_run));   // masked: exp2(-inf) = 0
-          l_run += p[i];
+          for (int i = 0; i < 8; ++i) {
+            p[i] = __builtin_amdgcn_exp2f(fmaf(s[t][8 * ks2 + i], a.scale_log2, -m_run[t]));
+            l_run[t] += p[i];
+          }
+          pop[ks2][t] = pack8(p);
         }
-        const uint4 pop = pack8(p);   // bf16 weights into the value product
-#pragma unroll
-        for (int mt = 0; mt < kHalf / 32; ++mt)
-          o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vop[mt]), as_bf8(pop), o[mt], 0, 0, 0);
+      // V^T operands, pair i = (ks2, dt) = (i / kDT, i % kDT), stream through a
+      // ring of kVPF register pairs like the K operands
+      constexpr int kNPV = 2 * kDT;
+      auto vld = [&](int i, uint2* dst) __attribute__((always_inline)) {
+        const int ks2 = i / kDT, dt = i % kDT;
+        dst[0] = ld_tr(vrow + 16 * ks2 * kVPitch + 32 * dt);
+        dst[1] = ld_tr(vrow + (16 * ks2 + 8) * kVPitch + 32 * dt);
       };
-      pv(0, vop0);
-      pv(1, vop1);
-    }
-    buf = buf == kStages - 1 ? 0 : buf + 1;
-  }
-
-  // epilogue: element e = 4j + r of o[mt] is value dim 128 half + 32mt + 8j + 4kg + r
-  // of query q0 + n32
-  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
-  const float inv = 1.0f / l_tot;
-  const size_t qn = static_cast<size_t>(q0 + n32);
-  const uint16_t* grow = a.gate + qn * a.g_rs + h * a.g_hs + kHalf * half;
-  uint16_t* orow = a.out + qn * a.o_rs + h * D + kHalf * half;
+      uint2 vq[kVPF][2];
 #pragma unroll
-  for (int mt = 0; mt < kHalf / 32; ++mt)
+      for (int i = 0; i < kVPF; ++i) vld(i, vq[i]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d0 = 32 * mt + 8 * j + 4 * kg;
-      const uint2 gv = *reinterpret_cast<const uint2*>(grow + d0);
-      const float gx[4] = {lo_bf(gv.x), hi_bf(gv.x), lo_bf(gv.y), hi_bf(gv.y)};
-      float y[4];
+      for (int i = 0; i < kNPV; ++i) {
+        const uint4 vop = make_uint4(vq[i % kVPF][0].x, vq[i % kVPF][0].y, vq[i % kVPF][1].x, vq[i % kVPF][1].y);
+        if (i + kVPF < kNPV) vld(i + kVPF, vq[i % kVPF]);
+        const int ks2 = i / kDT, dt = i % kDT;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        // sigmoid from the hardware exp2 / reciprocal (within 2 f32 ulps; the
-        // result lands in bf16)
-        const float sg = round_bf(__builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gx[r] * 1.4426950408889634f)));
-        y[r] = round_bf(round_bf(o[mt][4 * j + r] * inv) * sg);
+        for (int t = 0; t < QT; ++t)
+          o[dt][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vop), as_bf8(pop[ks2][t]), o[dt][t], 0, 0, 0);
       }
-      *reinterpret_cast<uint2*>(orow + d0) = make_uint2(pack_bf(y[0], y[1]), pack_bf(y[2], y[3]));
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kVPF, 0);
+#pragma unroll
+      for (int i = 0; i < kNPV; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, QT, 0);
+        if (i + kVPF < kNPV) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      }
     }
+  };
+  static_assert(kStages == 3, "the key loop is unrolled over three ring stages");
+  for (int kt = 0; kt < ntiles; kt += kStages) {
+    step(kt, IC<0>{});
+    if (kt + 1 < ntiles) step(kt + 1, IC<1>{});
+    if (kt + 2 < ntiles) step(kt + 2, IC<2>{});
+  }
+  // no load may still be writing this block's LDS when the block ends
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+
+  // epilogue: element e = 4j + r of o[dt][t] is value dim 32 dt + 8j + 4kg + r
+  // of query q0 + 32 t + n32
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const float l_tot = l_run[t] + __shfl_xor(l_run[t], 32, kWave);
+    const float inv = 1.0f / l_tot;
+    const size_t qn = static_cast<size_t>(q0 + 32 * t + n32);
+    const uint16_t* grow = a.gate + qn * a.g_rs + h * a.g_hs;
+    uint16_t* orow = a.out + qn * a.o_rs + h * D;
+#pragma unroll
+    for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = 32 * dt + 8 * j + 4 * kg;
+        const uint2 gv = *reinterpret_cast<const uint2*>(grow + d0);
+        const float gx[4] = {lo_bf(gv.x), hi_bf(gv.x), lo_bf(gv.y), hi_bf(gv.y)};
+        float y[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float sg = round_bf(__builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gx[r] * 1.4426950408889634f)));
+          y[r] = round_bf(round_bf(o[dt][t][4 * j + r] * inv) * sg);
+        }
+        *reinterpret_cast<uint2*>(orow + d0) = make_uint2(pack_bf(y[0], y[1]), pack_bf(y[2], y[3]));
+      }
+  }
 }
 
 }  // namespace
@@ -326,7 +385,7 @@ int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void*
   // XCD-grouped order when every XCD gets whole heads of a single group
   const int64_t per = heads / 8, group = heads / kv_heads;
   a.xcd_heads = (heads % 8 == 0 && per >= 1 && (group % per == 0 || per % group == 0)) ? (int)per : 0;
-  flash_prefill_kernel<<<(unsigned)(heads * (n / kBM)), 2 * kThreads, 0, stream>>>(a);
+  flash_prefill_kernel<<<(unsigned)(heads * (n / kBM)), kWaves * kWave, 0, stream>>>(a);
   return launched("flash_prefill");
 }
 

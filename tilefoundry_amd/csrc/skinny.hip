@@ -291,32 +291,17 @@ __global__ __launch_bounds__(kThreads) void rows_norm_kernel(
 }
 
 // -------------------------------------------------------------- batch_sample
-__global__ __launch_bounds__(kThreads) void batch_sample_kernel(
+constexpr int kSampleThreads = 1024;
+
+__global__ __launch_bounds__(kSampleThreads) void batch_sample_kernel(
     const float* __restrict__ bv, const int* __restrict__ bi, int nb, const int* inp,
     const int* plen, int64_t* ids, int* pos, int* sam, int nsteps, int* err) {
-  __shared__ float rv[kThreads];
-  __shared__ int ri[kThreads];
+  __shared__ float rv[kSampleThreads / kWave];
+  __shared__ int ri[kSampleThreads / kWave];
   const int b = blockIdx.x;
   const int t = threadIdx.x;
-  float bvv = -FLT_MAX;
-  int bii = 0x7fffffff;
-  for (int j = t; j < nb; j += kThreads) {
-    const float v = bv[static_cast<size_t>(b) * nb + j];
-    const int i = bi[static_cast<size_t>(b) * nb + j];
-    if (better(v, i, bvv, bii)) { bvv = v; bii = i; }
-  }
-  rv[t] = bvv;
-  ri[t] = bii;
-  __syncthreads();
-  for (int s = kThreads / 2; s > 0; s >>= 1) {
-    if (t < s && better(rv[t + s], ri[t + s], rv[t], ri[t])) {
-      rv[t] = rv[t + s];
-      ri[t] = ri[t + s];
-    }
-    __syncthreads();
-  }
+  const int best = block_best(bv + static_cast<size_t>(b) * nb, bi + static_cast<size_t>(b) * nb, nb, rv, ri);
   if (t == 0) {
-    const int best = ri[0];
     const int p = pos[b];
     if (p < 0 || p >= nsteps) {
       if (err) atomicExch(err, 2);
@@ -413,7 +398,7 @@ int tfa_batch_sample_step(const float* block_val, const int* block_idx, int64_t 
   if (!block_val || !block_idx || !inp || !prompt_len || !ids || !pos || !sam)
     return fail(TFA_ERR_NULL, "tfa_batch_sample_step: null pointer argument");
   TFA_REQUIRE(nblocks > 0 && batch > 0 && nsteps > 0, TFA_ERR_SHAPE, "tfa_batch_sample_step: empty shape");
-  batch_sample_kernel<<<(int)batch, kThreads, 0, stream>>>(block_val, block_idx, (int)nblocks, inp,
+  batch_sample_kernel<<<(int)batch, kSampleThreads, 0, stream>>>(block_val, block_idx, (int)nblocks, inp,
                                                            prompt_len, ids, pos, sam, (int)nsteps, err);
   return launched("batch_sample_step");
 }

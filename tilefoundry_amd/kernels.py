@@ -209,11 +209,11 @@ def attn_partial(HQ: int, HKV: int, D: int, CAP: int, SS: int, scale: float, thr
     """One split's ``(max, sum, weighted values)`` over its ``SS`` slots of the
     context ``0..Pos`` (kernels.py:418-501): f32 scores scaled after the dot,
     f32 softmax against the split's max, bf16 weights into ``P.V``; splits past
-    the context write the neutral partial ``(0, -1e30, 0)``. ``SS`` is 64, 128 or
+    the context write the neutral partial ``(0, -1e30, 0)``. ``SS`` is 32, 64, 128 or
     256 and divides ``CAP``."""
     _positive(HQ=HQ, HKV=HKV, D=D, CAP=CAP, SS=SS, threads=threads)
-    if SS not in (64, 128, 256) or CAP % SS:
-        raise ValueError(f"SS={SS} must be 64, 128 or 256 and divide CAP={CAP}")
+    if SS not in (32, 64, 128, 256) or CAP % SS:
+        raise ValueError(f"SS={SS} must be 32, 64, 128 or 256 and divide CAP={CAP}")
     if D != 128:
         raise ValueError(f"D={D}: the gfx950 decode kernels take head_dim 128")
 
