@@ -47,13 +47,18 @@ def _run(cmd: list[str]) -> None:
         )
 
 
-# Per-file code-generation options. The prefill attention keeps its output
-# accumulators (64 KB per wave) and its resident Q operands in one wave's full
-# register budget; with MFMA results allowed in the vector registers the
-# allocator fits both without spilling (with them forced into the accumulation
-# registers it spills).
+# Per-file code-generation options.
+# * MFMA results in the vector registers (-amdgpu-mfma-vgpr-form): the prefill
+#   attention keeps its output accumulators and resident Q operands in one
+#   wave's register budget without the accumulation-register copies the
+#   default form inserts; the MLA attention likewise drops ~200 register moves
+#   per key tile.
+# * IEEE mode off with NaNs assumed absent (MLA attention): fmaxf then needs no
+#   input quieting, and the DPP max reductions fold into v_max_f32_dpp.
+VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 FILE_FLAGS = {
-    "prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "prefill.hip": VGPR_MFMA,
+    "mla.hip": VGPR_MFMA + ["-mno-amdgpu-ieee", "-fno-honor-nans"],
 }
 
 

@@ -192,7 +192,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
     for (int e = t; e < G * D; e += kThreads)
       qs[e / D][e % D] = bf2f(a.q[b * a.q_bstride + (kvh * G) * D + e]);
   }
-  __syncthreads();
+  lds_barrier();
 
   // 3. scores (scale applied to the finished f32 dot), kept in registers: after
   //    the 16-lane butterfly every lane of a position's group holds its score
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
     if (lane == 0) red[0][wid][g] = mx;
   }
-  __syncthreads();
+  lds_barrier();
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m[g] = fmaxf(fmaxf(red[0][0][g], red[0][1][g]), fmaxf(red[0][2][g], red[0][3][g]));
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
 #pragma unroll
       for (int i = 0; i < 8; ++i) obuf[wid][g][8 * dc + i] = o[g][i];
   }
-  __syncthreads();
+  lds_barrier();
 #pragma unroll
   for (int g = 0; g < G; ++g)
     l[g] = (red[1][0][g] + red[1][1][g]) + (red[1][2][g] + red[1][3][g]);
@@ -368,7 +368,7 @@ __global__ __launch_bounds__(kCombThreads) void attn_combine_kernel(
   const float mj = act ? mj0 : -INFINITY;
   float mx = wave_max(mj);
   if (lane == 0) s_w[0][wid] = mx;
-  __syncthreads();
+  lds_barrier();
   mx = s_w[0][0];
 #pragma unroll
   for (int k = 1; k < kCombWaves; ++k) mx = fmaxf(mx, s_w[0][k]);
@@ -376,7 +376,7 @@ __global__ __launch_bounds__(kCombThreads) void attn_combine_kernel(
   s_e[t] = e;
   const float dw = wave_sum(act ? lj0 * e : 0.f);
   if (lane == 0) s_w[1][wid] = dw;
-  __syncthreads();
+  lds_barrier();
   float den = 0.f;
 #pragma unroll
   for (int k = 0; k < kCombWaves; ++k) den += s_w[1][k];
@@ -403,7 +403,7 @@ __global__ __launch_bounds__(kCombThreads) void attn_combine_kernel(
     }
     s_red[gi][d] = num;
   }
-  __syncthreads();
+  lds_barrier();
   if (t < Dh) {
     float num = 0.f;
 #pragma unroll

@@ -76,6 +76,21 @@ TFA_DEV float wave_max(float v) {
   return v;
 }
 
+// Max over each 16-lane row of the wave (every lane gets its row's max) by DPP
+// lane permutations -- quad swaps, then the half-row and row mirrors -- with
+// no LDS traffic.
+template <int CTRL>
+TFA_DEV float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+TFA_DEV float row16_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));    // quad_perm [1, 0, 3, 2]
+  v = fmaxf(v, dpp_f32<0x4E>(v));    // quad_perm [2, 3, 0, 1]
+  v = fmaxf(v, dpp_f32<0x141>(v));   // row_half_mirror
+  v = fmaxf(v, dpp_f32<0x140>(v));   // row_mirror
+  return v;
+}
+
 // Multi-row wave reduction: v[0..R) are one lane's partial sums of R rows.
 // Instead of R full butterflies (6R shuffles) the rows are halved at each step
 // -- a lane keeps the half of the rows its mask bit selects and adds the
@@ -226,6 +241,18 @@ TFA_DEV void block_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_barrier();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// s_waitcnt immediate waiting for every LDS (and scalar-memory) operation of
+// the wave, vmcnt and expcnt left open.
+constexpr int kWaitLgkm0 = 15 | (7 << 4) | (0 << 8) | (3 << 14);
+
+// Block barrier for an LDS hand-off: this wave's LDS operations complete, then
+// every wave meets. Loads into registers stay in flight -- the compiler waits
+// for each one where it is used -- where a __syncthreads() would drain them all.
+TFA_DEV void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  block_barrier();
 }
 
 // ------------------------------------------------------------ greedy pick

@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
       for (int i = 0; i < 8; ++i) ss += xf[j][i] * xf[j][i];
     ss = wave_sum(ss);
     if (lane == 0) ssq[wid] = ss;
-    __syncthreads();
+    lds_barrier();
     const float tot = (ssq[0] + ssq[1]) + (ssq[2] + ssq[3]);
     const float rs = rsqrt_rn(tot / static_cast<float>(K) + a.eps);
 #pragma unroll
@@ -184,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
     const float tot = wave_sum_rows<R>(acc, lane);
     if ((lane & (kWave / R - 1)) == 0) red[wid][wave_rows_owner<R>(lane)] = tot;
   }
-  __syncthreads();
+  lds_barrier();
   auto total = [&](int r) { return (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]); };
 
   // 5. epilogues

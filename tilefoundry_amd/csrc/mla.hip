@@ -47,6 +47,7 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxBatch = 32;
 constexpr int kMaxSplits = 1024;
+constexpr float kSlack = 8.0f;   // running-max headroom, log2 units
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(kThreads) void mla_q_absorb_kernel(
     if (i < kNope) qn[b][i] = round_bf(acc);
     else qr[b][i - kNope] = round_bf(acc);
   }
-  __syncthreads();
+  lds_barrier();
   for (int b = 0; b < B; ++b) {
     float acc = 0.f;
 #pragma unroll
@@ -181,6 +182,7 @@ struct MlaAttnArgs {
   int* err;
   int H, cap, ns, tiles;   // a split is `tiles` steps of 64 positions
   float scale;
+  float scale_log2;   // scale * log2(e)
 };
 
 // LDS tiles keep a position per row. Latent rows are 512 bytes of 32 16-byte
@@ -262,9 +264,22 @@ __global__ __launch_bounds__(kThreads) void mla_attn_kernel(const MlaAttnArgs a)
   fetch(0, rl[0], rr[0]);
   // the query of all heads, resident in LDS (padding rows repeat the last head;
   // their results are never stored)
-  for (int e = t; e < kHeadRows * (kQK / 8); e += kThreads) {
-    const int h = e / (kQK / 8), c = e % (kQK / 8);
-    q_s[h][c] = ld16(a.q + (static_cast<size_t>(b) * a.H + min(h, a.H - 1)) * kQK + 8 * c);
+  {
+    // every load first (one round trip), then the stores
+    constexpr int kQChunks = kHeadRows * (kQK / 8);
+    constexpr int kQPer = (kQChunks + kThreads - 1) / kThreads;
+    uint4 qv[kQPer];
+#pragma unroll
+    for (int i = 0; i < kQPer; ++i) {
+      const int e = min(t + i * kThreads, kQChunks - 1);
+      const int h = e / (kQK / 8), c = e % (kQK / 8);
+      qv[i] = ld16(a.q + (static_cast<size_t>(b) * a.H + min(h, a.H - 1)) * kQK + 8 * c);
+    }
+#pragma unroll
+    for (int i = 0; i < kQPer; ++i) {
+      const int e = t + i * kThreads;
+      if (e < kQChunks) q_s[e / (kQK / 8)][e % (kQK / 8)] = qv[i];
+    }
   }
   stage(0, 0, rl[0], rr[0]);
 #pragma unroll
@@ -292,7 +307,7 @@ __global__ __launch_bounds__(kThreads) void mla_attn_kernel(const MlaAttnArgs a)
       const int tt = tt0 + j;
       if (tt >= ntiles) break;
       const int buf = tt & 1;
-      __syncthreads();   // buf holds tile tt; every wave is done with buf ^ 1
+      lds_barrier();   // buf holds tile tt; every wave is done with buf ^ 1
 
       // scores of this wave's 16 positions against all heads
       const int prow = 16 * wid + n16;
@@ -308,45 +323,60 @@ __global__ __launch_bounds__(kThreads) void mla_attn_kernel(const MlaAttnArgs a)
           sacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(q_s[16 * mt + n16][4 * ks + g]), as_bf8(bop),
                                                              sacc[mt], 0, 0, 0);
       }
+      // scores in log2 units (the scale folded in), their max over the wave's
+      // 16 positions by DPP within each 16-lane row
       const bool valid = pos0 + tt * kTile + prow < n;
       float sv[3][4], mx[3][4];
 #pragma unroll
       for (int mt = 0; mt < 3; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          sv[mt][r] = valid ? sacc[mt][r] * a.scale : -INFINITY;
-          mx[mt][r] = sv[mt][r];
+          sv[mt][r] = valid ? sacc[mt][r] * a.scale_log2 : -INFINITY;
+          mx[mt][r] = row16_max(sv[mt][r]);
         }
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1)
-#pragma unroll
-        for (int mt = 0; mt < 3; ++mt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) mx[mt][r] = fmaxf(mx[mt][r], __shfl_xor(mx[mt][r], m, kWave));
       if (n16 == 0) {
 #pragma unroll
         for (int mt = 0; mt < 3; ++mt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) red[wid][16 * mt + 4 * g + r] = mx[mt][r];
       }
-      __syncthreads();
-      // online softmax: every wave forms the same tile max per head
+      lds_barrier();
+      // online softmax: every wave forms the same tile max per head. The
+      // running max (log2 units) is only raised -- and O rescaled -- when some
+      // head's tile max passes it by more than kSlack, so the weights
+      // exp2(s - m) stay <= 2^kSlack; every wave takes the same decision.
+      float mtile[3][4];
+      bool raise = false;
 #pragma unroll
       for (int mt = 0; mt < 3; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int h = 16 * mt + 4 * g + r;
-          const float mtile = fmaxf(fmaxf(red[0][h], red[1][h]), fmaxf(red[2][h], red[3][h]));
-          const float m_new = fmaxf(m_run[mt][r], mtile);
-          const float alpha = m_run[mt][r] == -INFINITY ? 0.f : expf(m_run[mt][r] - m_new);
-          const float e = sv[mt][r] == -INFINITY ? 0.f : expf(sv[mt][r] - m_new);
-          l_run[mt][r] = l_run[mt][r] * alpha + e;
-          m_run[mt][r] = m_new;
-          p_s[h][prow] = static_cast<uint16_t>(f2bf(e));   // bf16 weights into the value product
-#pragma unroll
-          for (int nt = 0; nt < 4; ++nt) o_acc[mt][nt][r] *= alpha;
+          mtile[mt][r] = fmaxf(fmaxf(red[0][h], red[1][h]), fmaxf(red[2][h], red[3][h]));
+          raise |= mtile[mt][r] > m_run[mt][r] + kSlack;
         }
-      __syncthreads();
+      if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+#pragma unroll
+        for (int mt = 0; mt < 3; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float m_new = fmaxf(m_run[mt][r], mtile[mt][r]);
+            const float alpha = m_run[mt][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[mt][r] - m_new);
+            l_run[mt][r] *= alpha;
+            m_run[mt][r] = m_new;
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) o_acc[mt][nt][r] *= alpha;
+          }
+      }
+#pragma unroll
+      for (int mt = 0; mt < 3; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float e = __builtin_amdgcn_exp2f(sv[mt][r] - m_run[mt][r]);   // masked: exp2(-inf) = 0
+          l_run[mt][r] += e;
+          p_s[16 * mt + 4 * g + r][prow] = static_cast<uint16_t>(f2bf(e));   // bf16 weights into the value product
+        }
+      lds_barrier();
 
       // O[:, this wave's 64 latent columns] += P . C
 #pragma unroll
@@ -397,7 +427,7 @@ __global__ __launch_bounds__(kThreads) void mla_attn_kernel(const MlaAttnArgs a)
 #pragma unroll
       for (int r = 0; r < 4; ++r) red[wid][16 * mt + 4 * g + r] = l_run[mt][r];
   }
-  __syncthreads();
+  lds_barrier();
   const size_t orow = (static_cast<size_t>(b) * a.ns + s) * a.H;
 #pragma unroll
   for (int mt = 0; mt < 3; ++mt)
@@ -411,7 +441,7 @@ __global__ __launch_bounds__(kThreads) void mla_attn_kernel(const MlaAttnArgs a)
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) dst[16 * nt] = static_cast<uint16_t>(f2bf(o_acc[mt][nt][r] * inv));
       if (wid == 0 && n16 == 0) {
-        a.mp[orow + h] = m_run[mt][r];
+        a.mp[orow + h] = m_run[mt][r] * 0.6931471805599453f;   // natural-log units
         a.lp[orow + h] = lt;
       }
     }
@@ -438,21 +468,21 @@ __global__ __launch_bounds__(kThreads) void mla_combine_up_kernel(
   for (int s = t; s < nsa; s += kThreads) mx = fmaxf(mx, mp[srow + static_cast<size_t>(s) * H]);
   mx = wave_max(mx);
   if ((t & (kWave - 1)) == 0) scratch[t / kWave] = mx;
-  __syncthreads();
+  lds_barrier();
   const float M = fmaxf(fmaxf(scratch[0], scratch[1]), fmaxf(scratch[2], scratch[3]));
-  __syncthreads();
+  lds_barrier();
   for (int s = t; s < nsa; s += kThreads) {
     const size_t i = srow + static_cast<size_t>(s) * H;
     wgt[s] = lp[i] * expf(mp[i] - M);
   }
-  __syncthreads();
+  lds_barrier();
   float L = 0.f, acc = 0.f;
   for (int s = 0; s < nsa; ++s) {
     L += wgt[s];
     acc = fmaf(wgt[s], bf2f(op[(srow + static_cast<size_t>(s) * H) * kLat + t]), acc);
   }
   olat[t] = acc / L;
-  __syncthreads();
+  lds_barrier();
   // value row v = t / 4, latent quarter q = t % 4
   const int v = t >> 2, q = t & 3;
   const uint16_t* wrow = w_kv_b + (static_cast<size_t>(h) * kKvB + kNope + v) * kLat + 64 * q;
@@ -576,7 +606,7 @@ __global__ __launch_bounds__(kThreads) void rope_attend_split_kernel(const RopeA
   if (start >= n) return;  // whole block
   const int len = min(n - start, kRaSplit);
   ra_query(a, h, ra_pos(a), qs);
-  __syncthreads();
+  lds_barrier();
 
   // scores: one context row per thread
   const int qk = a.nope + a.rope;
@@ -594,13 +624,13 @@ __global__ __launch_bounds__(kThreads) void rope_attend_split_kernel(const RopeA
   }
   float m = wave_max(sco);
   if (lane == 0) red[0][wid] = m;
-  __syncthreads();
+  lds_barrier();
   m = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
   const float e = t < len ? expf(sco - m) : 0.f;
   ps[t] = e;
   const float l = wave_sum(e);
   if (lane == 0) red[1][wid] = l;
-  __syncthreads();
+  lds_barrier();
 
   // weighted values: wave w takes rows 64w .. 64w+63 of the split, lanes the value dims
   float acc0 = 0.f, acc1 = 0.f;
@@ -613,7 +643,7 @@ __global__ __launch_bounds__(kThreads) void rope_attend_split_kernel(const RopeA
   }
   ov[wid][lane] = acc0;
   ov[wid][lane + kWave] = acc1;
-  __syncthreads();
+  lds_barrier();
   for (int d = t; d < a.vd; d += kThreads)
     a.op[(static_cast<size_t>(s) * a.heads + h) * a.vd + d] = (ov[0][d] + ov[1][d]) + (ov[2][d] + ov[3][d]);
   if (t == 0) {
@@ -651,7 +681,7 @@ __global__ __launch_bounds__(kThreads) void rope_attend_merge_kernel(const RopeA
   }
   if (a.v_new)
     for (int d = t; d < a.vd; d += kThreads) a.v_new[static_cast<size_t>(h) * a.vd + d] = kv[a.nope + d];
-  __syncthreads();
+  lds_barrier();
   float part = 0.f;
   for (int d = t; d < qk; d += kThreads) part = fmaf(qs[d], kn[d], part);
   const float snew = block_sum(part, scr);
@@ -758,6 +788,7 @@ int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* r
   a.ns = (int)(cap / split);
   a.tiles = (int)(split / kTile);
   a.scale = scale;
+  a.scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid(a.ns, (unsigned)batch);
   mla_attn_kernel<2><<<grid, kThreads, 0, stream>>>(a);
   return launched("mla_attn");
