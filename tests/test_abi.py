@@ -117,7 +117,7 @@ def test_attention_argument_checks(lib):
     assert st == SHAPE
     st, _ = call(lib, "tfa_decode_attention", *args(128, 512, 64, hq=12, hkv=8))
     assert st == SHAPE
-    st, msg = call(lib, "tfa_decode_attention", *args(128, 512, 32))
+    st, msg = call(lib, "tfa_decode_attention", *args(128, 512, 16))
     assert st == SHAPE and "split" in msg
     fused = list(args(128, 512, 64))
     fused[3] = A  # gamma_q given, the rest of the fused-mode operands missing
@@ -129,6 +129,19 @@ def test_attention_argument_checks(lib):
     part_only[0], part_only[1], part_only[2] = P(None), A, I64(1)   # partials without fused mode
     st, msg = call(lib, "tfa_decode_attention", *part_only)
     assert st == ARG and "partials" in msg
+
+
+def test_mla_attention_argument_checks(lib):
+    args = lambda heads, cap, split: (A, A, A, A, I64(8), I64(heads), I64(cap), I64(split), F(0.1), A, A, A,
+                                      P(None), P(None))
+    st, msg = call(lib, "tfa_mla_attention", *args(40, 8192, 64))
+    assert st == SHAPE and "multiple of 128" in msg
+    st, _ = call(lib, "tfa_mla_attention", *args(40, 8192, 2048))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_mla_attention", *args(49, 8192, 256))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_mla_attention", *args(40, 8000, 256))
+    assert st == SHAPE
 
 
 def test_batched_argument_checks(lib):

@@ -107,7 +107,7 @@ def _attend(dev, q_abs, lat, rk, pos, split, w_kv_b, cap):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("split,pos", [(256, [0, 63, 700]), (64, [64, 1, 1023]), (1024, [500, 1023, 2])])
+@pytest.mark.parametrize("split,pos", [(256, [0, 63, 700]), (128, [128, 1, 1023]), (1024, [500, 1023, 2])])
 def test_mla_attention_vs_oracle(dev, split, pos):
     g = gen(sum(pos) + split)
     B, cap = 3, 1024

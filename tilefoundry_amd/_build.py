@@ -51,14 +51,13 @@ def _run(cmd: list[str]) -> None:
 # * MFMA results in the vector registers (-amdgpu-mfma-vgpr-form): the prefill
 #   attention keeps its output accumulators and resident Q operands in one
 #   wave's register budget without the accumulation-register copies the
-#   default form inserts; the MLA attention likewise drops ~200 register moves
-#   per key tile.
+#   default form inserts.
 # * IEEE mode off with NaNs assumed absent (MLA attention): fmaxf then needs no
 #   input quieting, and the DPP max reductions fold into v_max_f32_dpp.
 VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 FILE_FLAGS = {
     "prefill.hip": VGPR_MFMA,
-    "mla.hip": VGPR_MFMA + ["-mno-amdgpu-ieee", "-fno-honor-nans"],
+    "mla.hip": ["-mno-amdgpu-ieee", "-fno-honor-nans"],
 }
 
 

@@ -13,8 +13,9 @@
 //                 rope cache slot pos.
 //   mla_q_absorb  per head: reduce the q_b partials, q_lat = bf16(W_UK^T q_nope)
 //                 (f32 accumulate), q_rope -> RoPE; writes q_abs [B, H, 288].
-//   mla_attn      per (split of 64*tiles positions, sequence), bf16 MFMA:
-//                 S = q_abs . [c | k_rope]^T, online softmax in f32, O += P . c;
+//   mla_attn      per (split of 128*tiles positions, sequence), bf16 MFMA:
+//                 S = q_abs . [c | k_rope]^T, online softmax in f32, O += P . c,
+//                 each wave over its own positions and heads, merged at the end;
 //                 writes the split's latent output (normalised by its own sum,
 //                 bf16) with its max and sum.
 //   mla_combine_up per (head, sequence): log-sum-exp merge of the splits into
@@ -42,7 +43,6 @@ constexpr int kNope = 64;      // qk_nope_head_dim
 constexpr int kV = 64;         // v_head_dim
 constexpr int kKvB = kNope + kV;   // rows of W_kv_b per head
 constexpr int kHeadRows = 48;  // heads padded to three 16-row MFMA tiles
-constexpr int kTile = 64;      // positions per pipeline step
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxBatch = 32;
@@ -180,15 +180,36 @@ struct MlaAttnArgs {
   float* mp;             // [B, ns, H] split max
   float* lp;             // [B, ns, H] split sum
   int* err;
-  int H, cap, ns, tiles;   // a split is `tiles` steps of 64 positions
+  int H, cap, ns, tiles;   // a split is `tiles` steps of kStep positions
   float scale;
   float scale_log2;   // scale * log2(e)
 };
 
-// LDS tiles keep a position per row. Latent rows are 512 bytes of 32 16-byte
-// chunks, stored XOR-swizzled by the row: the score operand reads (16 rows, one
-// chunk) and the transpose reads of the value product (8 rows x 32 bytes per
-// half-wave) then both hit 16 distinct bank groups.
+// Work split: a step is 128 positions in two LDS stages, filled by DMA. Wave
+// (quarter u, head tile mt) -- 12 waves, three per SIMD -- owns positions
+// 32u .. 32u + 31 of every step and heads 16mt .. 16mt + 15, with its own
+// online-softmax state; the four quarters of a head tile are merged at the
+// end. One barrier per step publishes the step's rows and frees the other
+// stage for the next step's DMA.
+constexpr int kAttnWaves = 12;
+constexpr int kAttnThreads = kAttnWaves * kWave;
+constexpr int kQuarters = 4;
+constexpr int kWaveRows = 32;
+constexpr int kStep = kQuarters * kWaveRows;
+constexpr int kLatChunks = kLat / 8;     // 16-byte chunks per latent row
+constexpr int kLatStage = kStep * kLat * 2;     // bytes
+constexpr int kRopeStage = kStep * kRope * 2;
+constexpr int kStageBytes = kLatStage + kRopeStage;
+constexpr int kStepDma = kStageBytes / (16 * kWave);   // 64 latent (2 rows) + 8 rope (16 rows)
+constexpr int kStepVm = kStepDma / kAttnWaves;          // per wave
+static_assert(kStepDma == 72 && kStepVm * kAttnWaves == kStepDma, "step DMA split evenly over the waves");
+constexpr int kWaitVmStep = waitcnt_vm(kStepVm);
+constexpr int kWaitVm0 = waitcnt_vm(0);
+
+// Latent rows are 512 bytes of 32 16-byte chunks, stored XOR-swizzled by the
+// row: the score operand reads (16 rows, one chunk) and the transpose reads of
+// the value product (8 rows x 32 bytes per half-wave) then both hit 16
+// distinct bank groups. The maps are involutions: slot <-> chunk.
 TFA_DEV int lat_slot(int row, int chunk) { return chunk ^ (((row & 7) << 1) | ((row >> 3) & 1)); }
 TFA_DEV int rope_slot(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
 
@@ -197,254 +218,247 @@ TFA_DEV int rope_slot(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
 // base + L / 4 at column col0 + 4 (L % 4) therefore receives
 // C[base + j][col0 + i], j = 0..3 -- four consecutive positions of one latent
 // column, the MFMA's K-major operand.
-TFA_DEV uint2 ld_tr(const uint16_t* lds_elem) {
+TFA_DEV uint2 ld_tr(const char* lds_byte) {
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4*)(lds_elem));
+      (__attribute__((address_space(3))) s16x4*)(lds_byte));
   return __builtin_bit_cast(uint2, v);
 }
 
-template <int D>   // tiles prefetched in registers
-__global__ __launch_bounds__(kThreads) void mla_attn_kernel(const MlaAttnArgs a) {
-  __shared__ uint4 lat_s[2][kTile][kLat / 8];
-  __shared__ uint4 rope_s[2][kTile][kRope / 8];
-  __shared__ __attribute__((aligned(16))) uint16_t p_s[kHeadRows][kTile + 4];
-  __shared__ uint4 q_s[kHeadRows][kQK / 8 + 1];   // 592-byte rows: 16-row operand reads conflict-free
-  __shared__ float red[kWaves][kHeadRows];
+// max / sum over the four 16-lane rows (lanes l, l ^ 16, l ^ 32, l ^ 48)
+TFA_DEV float rows4_max(float v) {
+  auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
+  auto y = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(y[0]), __uint_as_float(y[1]));
+}
+TFA_DEV float rows4_sum(float v) {
+  auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+  auto y = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(y[0]) + __uint_as_float(y[1]);
+}
+
+// Scores are computed transposed, S^T = [c | k_rope] . q^T (positions as MFMA
+// rows, heads as columns): the accumulator of lane (head n16, row group g)
+// then holds positions 4g + r of 16, which is exactly the K-slice lane
+// (n16, g) supplies as the B operand of the value product O^T += C^T . P^T,
+// so the weights never leave registers. K index 8g + i of that product is
+// position 4g + i (i < 4) or 16 + 4g + i - 4 of the wave's 32.
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3, 3)))
+void mla_attn_kernel(const MlaAttnArgs a) {
+  __shared__ uint4 smem[2 * kStageBytes / 16];   // two stages; the split merge reuses them
+  __shared__ float st_m[kAttnWaves][16];
+  __shared__ float st_l[kAttnWaves][16];
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int wid = threadIdx.x / kWave;
-  const int t = threadIdx.x;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int u = wid / 3;    // position quarter
+  const int mt = wid % 3;   // head tile
   const int n16 = lane & 15;
   const int g = lane >> 4;
   const int s = blockIdx.x;
   const int b = blockIdx.y;
 
-  int last = a.wr[b];
+  int last = __builtin_amdgcn_readfirstlane(a.wr[b]);
   if (last < 0 || last >= a.cap) {
-    if (s == 0 && t == 0) set_err(a.err, 4);
+    if (s == 0 && threadIdx.x == 0) set_err(a.err, 4);
     last = last < 0 ? -1 : a.cap - 1;
   }
   const int n = last + 1;
-  const int split = kTile * a.tiles;
-  const int pos0 = s * split;
+  const int pos0 = s * kStep * a.tiles;
   if (pos0 >= n) return;
-  const int ntiles = min(a.tiles, (n - pos0 + kTile - 1) / kTile);
-  const uint16_t* lat = a.lat + (static_cast<size_t>(b) * a.cap + pos0) * kLat;
-  const uint16_t* rk = a.rk + (static_cast<size_t>(b) * a.cap + pos0) * kRope;
+  const int nsteps = min(a.tiles, (n - pos0 + kStep - 1) / kStep);
+  const uint16_t* lat = a.lat + static_cast<size_t>(b) * a.cap * kLat;
+  const uint16_t* rk = a.rk + static_cast<size_t>(b) * a.cap * kRope;
+  const char* lds = reinterpret_cast<const char*>(smem);
+  const uint32_t lds0 = lds_offset(smem);
 
-  // staging: thread t moves latent chunks (row 8i + t/32, chunk t%32), i < 8,
-  // and rope chunk (row t/4, chunk t%4). Rows past the context are stored as
-  // zero (stale slots may hold anything; their weight is zero).
-  const int srow = t >> 5, schunk = t & 31;
-  const int rrow = t >> 2, rchunk = t & 3;
-  uint4 rl[D][8], rr[D];
-  auto fetch = [&](int tile, uint4* dl, uint4& dr) __attribute__((always_inline)) {
-    const uint16_t* lt = lat + static_cast<size_t>(tile) * kTile * kLat;
+  // Step t's rows into stage st, DMAs 6 wid .. 6 wid + 5 of the step: latent
+  // DMA j lands rows 2j, 2j + 1 (lane L at row 2j + L/32, slot L%32, so it
+  // fetches chunk lat_slot(row, slot)); rope DMA j - 64 lands 16 rows. Rows
+  // past the context load the last live row instead (finite data; their
+  // weight is zero), also for a step past the end.
+  auto issue = [&](int t, int st) __attribute__((always_inline)) {
+    const int p0 = pos0 + kStep * t;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dl[i] = ld16_stream(lt + (8 * i + srow) * kLat + schunk * 8);
-    dr = ld16_stream(rk + (static_cast<size_t>(tile) * kTile + rrow) * kRope + rchunk * 8);
-  };
-  auto keep = [](uint4 v, bool ok) __attribute__((always_inline)) {   // a value select, not an address select
-    v.x = ok ? v.x : 0u;
-    v.y = ok ? v.y : 0u;
-    v.z = ok ? v.z : 0u;
-    v.w = ok ? v.w : 0u;
-    return v;
-  };
-  auto stage = [&](int tile, int buf, const uint4* dl, const uint4& dr) __attribute__((always_inline)) {
-    const int base = pos0 + tile * kTile;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = 8 * i + srow;
-      lat_s[buf][row][lat_slot(row, schunk)] = keep(dl[i], base + row < n);
+    for (int i = 0; i < kStepVm; ++i) {
+      const int j = kStepVm * wid + i;
+      if (j < kStep / 2) {
+        const int row = 2 * j + (lane >> 5);
+        const int p = min(p0 + row, n - 1);
+        lds_dma16(lat + static_cast<size_t>(p) * kLat + 8 * lat_slot(row, lane & 31),
+                  lds0 + st * kStageBytes + j * 16 * kWave);
+      } else {
+        const int row = 16 * (j - kStep / 2) + (lane >> 2);
+        const int p = min(p0 + row, n - 1);
+        lds_dma16(rk + static_cast<size_t>(p) * kRope + 8 * rope_slot(row, lane & 3),
+                  lds0 + st * kStageBytes + kLatStage + (j - kStep / 2) * 16 * kWave);
+      }
     }
-    rope_s[buf][rrow][rope_slot(rrow, rchunk)] = keep(dr, base + rrow < n);
   };
 
-  fetch(0, rl[0], rr[0]);
-  // the query of all heads, resident in LDS (padding rows repeat the last head;
-  // their results are never stored)
+  // q^T operands, resident: lane (n16, g) holds q[head 16mt + n16][32ks + 8g ..
+  // +7] (padding heads repeat the last head; their results are never stored).
+  // Loaded before any DMA: the compiler's own wait for them, at their first
+  // use in step 0, is then the only wait it places.
+  uint4 qop[9];
   {
-    // every load first (one round trip), then the stores
-    constexpr int kQChunks = kHeadRows * (kQK / 8);
-    constexpr int kQPer = (kQChunks + kThreads - 1) / kThreads;
-    uint4 qv[kQPer];
+    const uint16_t* qrow = a.q + (static_cast<size_t>(b) * a.H + min(16 * mt + n16, a.H - 1)) * kQK + 8 * g;
 #pragma unroll
-    for (int i = 0; i < kQPer; ++i) {
-      const int e = min(t + i * kThreads, kQChunks - 1);
-      const int h = e / (kQK / 8), c = e % (kQK / 8);
-      qv[i] = ld16(a.q + (static_cast<size_t>(b) * a.H + min(h, a.H - 1)) * kQK + 8 * c);
-    }
-#pragma unroll
-    for (int i = 0; i < kQPer; ++i) {
-      const int e = t + i * kThreads;
-      if (e < kQChunks) q_s[e / (kQK / 8)][e % (kQK / 8)] = qv[i];
-    }
+    for (int ks = 0; ks < 9; ++ks) qop[ks] = ld16(qrow + 32 * ks);
   }
-  stage(0, 0, rl[0], rr[0]);
-#pragma unroll
-  for (int d = 0; d < D; ++d)
-    if (1 + d < ntiles) fetch(1 + d, rl[d], rr[d]);
+  issue(0, 0);
+  issue(1, 1);   // clamped rows when there is no step 1
 
-  // running state of the lane's head rows h = 16mt + 4g + r
-  float m_run[3][4], l_run[3][4];
-  f32x4 o_acc[3][4];   // [mt][nt]: rows 16mt + 4g + r, latent column 64 wid + 16 nt + n16
+  // Lane byte offsets into a stage (the lat_slot swizzle worked out so that
+  // the rest of each address is an immediate). Score operand (ks, pt): row
+  // 32u + 16pt + n16, chunk 4ks + g, at so[ks % 4] + 256 (ks / 4) + 8192 pt.
+  const int fs = ((n16 & 7) << 1) | (n16 >> 3);
+  uint32_t so[4];
 #pragma unroll
-  for (int mt = 0; mt < 3; ++mt)
+  for (int j = 0; j < 4; ++j)
+    so[j] = (kWaveRows * u + n16) * 2 * kLat + 16 * (g ^ (fs & 3)) + 64 * (j ^ (fs >> 2));
+  const uint32_t ro = kLatStage + (kWaveRows * u + n16) * 2 * kRope + 16 * (g ^ ((n16 >> 2) & 3));   // + 1024 pt
+  // value operand ct: rows r1 = 32u + 4g + n16/4 and r1 + 16, columns
+  // 16ct + 4 (n16 % 4), at to[ct % 8] + 256 (ct / 8) (+ 8192 for r1 + 16)
+  const int r1 = 4 * g + (n16 >> 2);
+  const int f1 = ((r1 & 7) << 1) | ((r1 >> 3) & 1);
+  uint32_t to[8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      m_run[mt][r] = -INFINITY;
-      l_run[mt][r] = 0.f;
+  for (int j = 0; j < 8; ++j)
+    to[j] = (kWaveRows * u + r1) * 2 * kLat + 16 * (((n16 & 3) >> 1) ^ (f1 & 1)) + 8 * (n16 & 1) +
+            32 * (j ^ (f1 >> 1));
+
+  // running state of head 16mt + n16 (the same in the lane's four row groups;
+  // l_run sums only the lane's own positions)
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 o[16];   // O^T[latent column 16ct + 4g + r][head 16mt + n16]
+#pragma unroll
+  for (int ct = 0; ct < 16; ++ct) o[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  bool started = false;
+  const bool live_tile = 16 * mt < a.H;
+
+  auto step = [&](int t, const char* stage) __attribute__((always_inline)) {
+    const int pb = pos0 + kStep * t + kWaveRows * u;
+    if (!live_tile || pb >= n) return;   // no live position or head in this wave's block
+    f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int ks = 0; ks < 9; ++ks)
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt) {
+        const uint4 aop = ks < 8 ? *reinterpret_cast<const uint4*>(stage + so[ks & 3] + 256 * (ks >> 2) + 8192 * pt)
+                                 : *reinterpret_cast<const uint4*>(stage + ro + 1024 * pt);
+        sacc[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(aop), as_bf8(qop[ks]), sacc[pt], 0, 0, 0);
+      }
+    // scores in log2 units (the scale folded in); masked positions are -inf
+    float sv[2][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sv[pt][r] = pb + 16 * pt + 4 * g + r < n ? sacc[pt][r] * a.scale_log2 : -INFINITY;
+        tmax = fmaxf(tmax, sv[pt][r]);
+      }
+    // online softmax: the running max (log2 units) is only raised -- and O
+    // rescaled -- when some head's block max passes it by more than kSlack,
+    // so the weights exp2(s - m) stay <= 2^kSlack. Position pb is live, so
+    // every head's block max is finite.
+    tmax = rows4_max(tmax);
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run + kSlack) != 0) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // 0 while m_run is -inf
+      l_run *= alpha;
+      m_run = m_new;
+      if (started) {
+#pragma unroll
+        for (int ct = 0; ct < 16; ++ct) o[ct] *= alpha;
+      }
+      started = true;
     }
+    float e[2][4];
 #pragma unroll
-  for (int mt = 0; mt < 3; ++mt)
+    for (int pt = 0; pt < 2; ++pt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) o_acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  for (int tt0 = 0; tt0 < ntiles; tt0 += D) {
-#pragma unroll
-    for (int j = 0; j < D; ++j) {
-      const int tt = tt0 + j;
-      if (tt >= ntiles) break;
-      const int buf = tt & 1;
-      lds_barrier();   // buf holds tile tt; every wave is done with buf ^ 1
-
-      // scores of this wave's 16 positions against all heads
-      const int prow = 16 * wid + n16;
-      f32x4 sacc[3];
-#pragma unroll
-      for (int mt = 0; mt < 3; ++mt) sacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 9; ++ks) {
-        const uint4 bop = ks < 8 ? lat_s[buf][prow][lat_slot(prow, 4 * ks + g)]
-                                 : rope_s[buf][prow][rope_slot(prow, g)];
-#pragma unroll
-        for (int mt = 0; mt < 3; ++mt)
-          sacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(q_s[16 * mt + n16][4 * ks + g]), as_bf8(bop),
-                                                             sacc[mt], 0, 0, 0);
+      for (int r = 0; r < 4; ++r) {
+        e[pt][r] = __builtin_amdgcn_exp2f(sv[pt][r] - m_run);   // masked: exp2(-inf) = 0
+        l_run += e[pt][r];
       }
-      // scores in log2 units (the scale folded in), their max over the wave's
-      // 16 positions by DPP within each 16-lane row
-      const bool valid = pos0 + tt * kTile + prow < n;
-      float sv[3][4], mx[3][4];
+    // P^T operand: bf16 weights of positions 4g + {0..3, 16..19}
+    const uint4 pop = make_uint4(pack_bf(e[0][0], e[0][1]), pack_bf(e[0][2], e[0][3]), pack_bf(e[1][0], e[1][1]),
+                                 pack_bf(e[1][2], e[1][3]));
+    // O^T += C^T . P^T over the wave's 32 positions
 #pragma unroll
-      for (int mt = 0; mt < 3; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          sv[mt][r] = valid ? sacc[mt][r] * a.scale_log2 : -INFINITY;
-          mx[mt][r] = row16_max(sv[mt][r]);
-        }
-      if (n16 == 0) {
-#pragma unroll
-        for (int mt = 0; mt < 3; ++mt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) red[wid][16 * mt + 4 * g + r] = mx[mt][r];
-      }
-      lds_barrier();
-      // online softmax: every wave forms the same tile max per head. The
-      // running max (log2 units) is only raised -- and O rescaled -- when some
-      // head's tile max passes it by more than kSlack, so the weights
-      // exp2(s - m) stay <= 2^kSlack; every wave takes the same decision.
-      float mtile[3][4];
-      bool raise = false;
-#pragma unroll
-      for (int mt = 0; mt < 3; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int h = 16 * mt + 4 * g + r;
-          mtile[mt][r] = fmaxf(fmaxf(red[0][h], red[1][h]), fmaxf(red[2][h], red[3][h]));
-          raise |= mtile[mt][r] > m_run[mt][r] + kSlack;
-        }
-      if (__builtin_amdgcn_ballot_w64(raise) != 0) {
-#pragma unroll
-        for (int mt = 0; mt < 3; ++mt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float m_new = fmaxf(m_run[mt][r], mtile[mt][r]);
-            const float alpha = m_run[mt][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[mt][r] - m_new);
-            l_run[mt][r] *= alpha;
-            m_run[mt][r] = m_new;
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt) o_acc[mt][nt][r] *= alpha;
-          }
-      }
-#pragma unroll
-      for (int mt = 0; mt < 3; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float e = __builtin_amdgcn_exp2f(sv[mt][r] - m_run[mt][r]);   // masked: exp2(-inf) = 0
-          l_run[mt][r] += e;
-          p_s[16 * mt + 4 * g + r][prow] = static_cast<uint16_t>(f2bf(e));   // bf16 weights into the value product
-        }
-      lds_barrier();
-
-      // O[:, this wave's 64 latent columns] += P . C
-#pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
-        uint4 aop[3];
-#pragma unroll
-        for (int mt = 0; mt < 3; ++mt) {
-          const uint16_t* pr = &p_s[16 * mt + n16][32 * k2 + 4 * g];
-          const uint2 lo = *reinterpret_cast<const uint2*>(pr);
-          const uint2 hi = *reinterpret_cast<const uint2*>(pr + 16);
-          aop[mt] = make_uint4(lo.x, lo.y, hi.x, hi.y);   // positions 32k2 + 4g + {0..3, 16..19}
-        }
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const int col = 64 * wid + 16 * nt + 4 * (n16 & 3);
-          const int r1 = 32 * k2 + 4 * g + (n16 >> 2);
-          const int r2 = r1 + 16;
-          const uint16_t* e1 = reinterpret_cast<const uint16_t*>(&lat_s[buf][r1][lat_slot(r1, col >> 3)]) + (col & 7);
-          const uint16_t* e2 = reinterpret_cast<const uint16_t*>(&lat_s[buf][r2][lat_slot(r2, col >> 3)]) + (col & 7);
-          const uint2 v1 = ld_tr(e1);
-          const uint2 v2 = ld_tr(e2);
-          const uint4 bop = make_uint4(v1.x, v1.y, v2.x, v2.y);
-#pragma unroll
-          for (int mt = 0; mt < 3; ++mt)
-            o_acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(aop[mt]), as_bf8(bop), o_acc[mt][nt], 0, 0, 0);
-        }
-      }
-      // tile tt + 1 (register slot j, loaded while this tile was computed) goes
-      // to the other buffer, which every wave finished reading before this
-      // tile's first barrier; the slot is refilled D tiles ahead
-      if (tt + 1 < ntiles) {
-        stage(tt + 1, buf ^ 1, rl[j], rr[j]);
-        if (tt + 1 + D < ntiles) fetch(tt + 1 + D, rl[j], rr[j]);
-      }
+    for (int ct = 0; ct < 16; ++ct) {
+      const uint2 v1 = ld_tr(stage + to[ct & 7] + 256 * (ct >> 3));
+      const uint2 v2 = ld_tr(stage + to[ct & 7] + 256 * (ct >> 3) + 16 * 2 * kLat);
+      o[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(make_uint4(v1.x, v1.y, v2.x, v2.y)), as_bf8(pop), o[ct],
+                                                       0, 0, 0);
     }
+  };
+
+  // step 0 (step 1 is in flight behind it); from step 1 on, the next step's
+  // DMA goes out once every wave is past the barrier, i.e. done with the
+  // stage it refills
+  __builtin_amdgcn_s_waitcnt(kWaitVmStep);
+  block_barrier();
+  step(0, lds);
+  for (int t = 1; t < nsteps; ++t) {
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    block_barrier();
+    if (t + 1 < nsteps) issue(t + 1, (t + 1) & 1);
+    step(t, lds + (t & 1) * kStageBytes);
   }
 
-  // split sums: over the lane's 16 position columns, then over the waves
+  // merge the four quarters of each head tile: per-head max and sum, then
+  // each quarter's share of the latent columns (64) summed in f32
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);   // an unused step-1 DMA may still be out
+  lds_barrier();   // every wave is done with the stages
+  {
+    const float lw = rows4_sum(l_run);
+    if (g == 0) {
+      st_m[wid][n16] = m_run;
+      st_l[wid][n16] = lw;
+    }
+  }
+  lds_barrier();
+  float mmax = -INFINITY;
 #pragma unroll
-  for (int m = 1; m < 16; m <<= 1)
+  for (int v = 0; v < kQuarters; ++v) mmax = fmaxf(mmax, st_m[3 * v + mt][n16]);   // quarter 0 saw pos0
+  float lsum = 0.f;
 #pragma unroll
-    for (int mt = 0; mt < 3; ++mt)
+  for (int v = 0; v < kQuarters; ++v)
+    lsum += st_l[3 * v + mt][n16] * __builtin_amdgcn_exp2f(st_m[3 * v + mt][n16] - mmax);
+  const float fself = __builtin_amdgcn_exp2f(m_run - mmax) / lsum;
+  // columns 64v .. 64v + 63 of head tile mt belong to quarter v; the other
+  // quarters' parts go through LDS: xb[mt][owner][sender slot][ct % 4][lane]
+  f32x4* xb = reinterpret_cast<f32x4*>(smem);
+  static_assert(3 * kQuarters * 3 * 4 * kWave * 16 <= 2 * kStageBytes, "merge fits the stages");
 #pragma unroll
-      for (int r = 0; r < 4; ++r) l_run[mt][r] += __shfl_xor(l_run[mt][r], m, kWave);
-  if (n16 == 0) {
-#pragma unroll
-    for (int mt = 0; mt < 3; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) red[wid][16 * mt + 4 * g + r] = l_run[mt][r];
+  for (int ct = 0; ct < 16; ++ct) {
+    const int owner = ct >> 2;
+    if (owner != u) {
+      const int slot = u < owner ? u : u - 1;
+      xb[(((mt * kQuarters + owner) * 3 + slot) * 4 + (ct & 3)) * kWave + lane] = o[ct] * fself;
+    }
   }
   lds_barrier();
   const size_t orow = (static_cast<size_t>(b) * a.ns + s) * a.H;
+  const int h = 16 * mt + n16;
 #pragma unroll
-  for (int mt = 0; mt < 3; ++mt)
+  for (int ct = 0; ct < 16; ++ct) {
+    if ((ct >> 2) != u) continue;
+    f32x4 acc = o[ct] * fself;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int h = 16 * mt + 4 * g + r;
-      if (h >= a.H) continue;
-      const float lt = (red[0][h] + red[1][h]) + (red[2][h] + red[3][h]);
-      const float inv = 1.0f / lt;
-      uint16_t* dst = a.op + (orow + h) * kLat + 64 * wid + n16;
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) dst[16 * nt] = static_cast<uint16_t>(f2bf(o_acc[mt][nt][r] * inv));
-      if (wid == 0 && n16 == 0) {
-        a.mp[orow + h] = m_run[mt][r] * 0.6931471805599453f;   // natural-log units
-        a.lp[orow + h] = lt;
-      }
-    }
+    for (int slot = 0; slot < 3; ++slot) acc += xb[(((mt * kQuarters + u) * 3 + slot) * 4 + (ct & 3)) * kWave + lane];
+    if (h < a.H)
+      *reinterpret_cast<uint2*>(a.op + (orow + h) * kLat + 16 * ct + 4 * g) =
+          make_uint2(pack_bf(acc[0], acc[1]), pack_bf(acc[2], acc[3]));
+  }
+  if (u == 0 && g == 0 && h < a.H) {
+    a.mp[orow + h] = mmax * 0.6931471805599453f;   // natural-log units
+    a.lp[orow + h] = lsum;
+  }
 }
 
 // ------------------------------------------------------------ mla_combine_up
@@ -766,8 +780,8 @@ int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* r
   TFA_REQUIRE(batch >= 1 && batch <= 65535, TFA_ERR_SHAPE, "tfa_mla_attention: batch %lld out of range", (long long)batch);
   TFA_REQUIRE(heads >= 1 && heads <= kHeadRows, TFA_ERR_SHAPE, "tfa_mla_attention: heads %lld not in [1, %d]",
               (long long)heads, kHeadRows);
-  TFA_REQUIRE(split >= kTile && split % kTile == 0 && split <= 16 * kTile, TFA_ERR_SHAPE,
-              "tfa_mla_attention: split %lld must be a multiple of %d, at most %d", (long long)split, kTile, 16 * kTile);
+  TFA_REQUIRE(split >= kStep && split % kStep == 0 && split <= 8 * kStep, TFA_ERR_SHAPE,
+              "tfa_mla_attention: split %lld must be a multiple of %d, at most %d", (long long)split, kStep, 8 * kStep);
   TFA_REQUIRE(cap >= 1 && cap % split == 0 && cap / split <= kMaxSplits, TFA_ERR_SHAPE,
               "tfa_mla_attention: cap %lld must be a multiple of split %lld with at most %d splits",
               (long long)cap, (long long)split, kMaxSplits);
@@ -786,11 +800,11 @@ int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* r
   a.H = (int)heads;
   a.cap = (int)cap;
   a.ns = (int)(cap / split);
-  a.tiles = (int)(split / kTile);
+  a.tiles = (int)(split / kStep);
   a.scale = scale;
   a.scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid(a.ns, (unsigned)batch);
-  mla_attn_kernel<2><<<grid, kThreads, 0, stream>>>(a);
+  mla_attn_kernel<<<grid, kAttnThreads, 0, stream>>>(a);
   return launched("mla_attn");
 }
 
