@@ -364,12 +364,13 @@ class BatchEngine:
 
     Every projection is a skinny bf16-MFMA GEMM over the batch (the weights are
     streamed once per step for all sequences); each sequence has its own KV
-    cache, position and prompt. One step is 8 launches per layer plus 3:
+    cache, position and prompt. One step is 9 launches per layer plus 3:
 
         rows_norm        embedding gather + input norm (once)
         skinny_gemm      q|k|v projection -> f32 split-K partials
-        decode_attention sums the partials, q/k head norm + RoPE, writes the new
-                         K and V rows, split-KV attention per sequence
+        qk_rope_cache    sums the partials, q/k head norm + RoPE, writes the new
+                         K and V rows and the prepared query
+        decode_attention split-KV attention per sequence over the cache
         attn_combine     merge of the splits
         skinny_gemm      o_proj -> split-K partials
         rows_norm        residual add + post-attention norm
@@ -384,7 +385,7 @@ class BatchEngine:
 
     def __init__(self, cfg: Qwen3Config = QWEN3_1_7B, *, batch: int = 32, device="cuda:0",
                  max_new: int = 2048, prompt_room: int = 512, weights: dict | None = None,
-                 seed: int = 0, split: int = 64, ks_qkv: int = 2, ks_o: int = 4, ks_down: int = 4,
+                 seed: int = 0, split: int = 128, ks_qkv: int = 2, ks_o: int = 4, ks_down: int = 4,
                  capture: bool = True):
         if not 1 <= batch <= self.MAX_BATCH:
             raise ValueError(f"batch {batch} not in [1, {self.MAX_BATCH}]")
@@ -419,6 +420,7 @@ class BatchEngine:
         self.xn = z(B, H)
         self.act = z(B, I)
         self.attn = z(B, HQ * D)
+        self.q = z(B, HQ * D)
         self.qkv_part = z(self.ks["qkv"], B, cfg.qkv_rows, dtype=f32)
         self.o_part = z(self.ks["o"], B, H, dtype=f32)
         self.d_part = z(self.ks["down"], B, H, dtype=f32)
@@ -447,9 +449,12 @@ class BatchEngine:
         for i, w in enumerate(self.layers):
             C.skinny_gemm(self.xn, w["w_qkv"], self.ks["qkv"], 0, self.qkv_part, None, None, None,
                           None)
-            C.decode_attention(None, self.qkv_part, w["gamma_q"], w["gamma_k"], cfg.eps, self.cos,
-                               self.sin, self.kc[i], self.vc[i], self.pos, self.pos, HQ, HKV,
-                               self.split, cfg.scale, self.op, self.mp, self.lp, False, self.err)
+            # the query prepared once per sequence, not once per split block
+            C.qk_rope_cache(self.qkv_part, w["gamma_q"], w["gamma_k"], cfg.eps, self.cos, self.sin,
+                            self.pos, self.pos, self.kc[i], self.vc[i], self.q, HQ, HKV, self.err)
+            C.decode_attention(self.q, None, None, None, 0.0, None, None, self.kc[i], self.vc[i], None,
+                               self.pos, HQ, HKV, self.split, cfg.scale, self.op, self.mp, self.lp,
+                               False, self.err)
             C.attn_combine(self.op, self.mp, self.lp, self.attn, self.pos, self.split)
             C.skinny_gemm(self.attn, w["w_o"], self.ks["o"], 0, self.o_part, None, None, None, None)
             C.rows_norm(None, None, self.h, self.o_part, self.h1, w["gamma_post"], self.xn, cfg.eps,
