@@ -22,7 +22,8 @@ def randn(*shape, g, std=1.0, mean=0.0):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K,ks", [(32, 4096, 2048, 1), (32, 4096, 2048, 2), (5, 2048, 2048, 4),
-                                      (1, 96, 256, 1), (32, 2048, 6144, 4), (17, 1000, 1024, 2)])
+                                      (1, 96, 256, 1), (32, 2048, 6144, 4), (17, 1000, 1024, 2),
+                                      (32, 12288, 2048, 1), (7, 12250, 512, 1)])
 def test_skinny_partials(dev, M, N, K, ks):
     from tilefoundry_amd import ops
 
@@ -85,6 +86,21 @@ def test_skinny_argmax(dev):
     none, bv2, bi2 = ops.skinny_gemm(x.to(dev), w.to(dev), "argmax", with_logits=False)
     assert none is None
     assert torch.equal(bv2, bv) and torch.equal(bi2, bi)
+
+
+@pytest.mark.gpu
+def test_skinny_argmax_48_row_blocks(dev):
+    """A row count whose 48-row blocks fill 256 CUs in one round (ragged tail)."""
+    from tilefoundry_amd import ops
+
+    g = gen(9)
+    M, V = 5, 12250
+    x = randn(M, H, g=g)
+    w = randn(V, H, g=g, std=0.02)
+    logits, bv, bi = ops.skinny_gemm(x.to(dev), w.to(dev), "argmax")
+    assert max_rel(logits, x.float() @ w.float().t()) < 5e-3
+    best = bi.gather(1, bv.argmax(1, keepdim=True)).squeeze(1).cpu()
+    assert torch.equal(best, logits.cpu().argmax(1).to(torch.int32))
 
 
 @pytest.mark.gpu

@@ -42,7 +42,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-constexpr int kTileRows = 32;
 constexpr int kMaxTokens = 32;
 constexpr int kGroupRows = 16;   // argmax winners are kept per 16 weight rows
 
@@ -79,21 +78,27 @@ TFA_DEV void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+template <int TR>
 struct SkinnyStage {
-  uint16_t w[kTileRows][kLdsRow];     // the chunk's weight rows
+  uint16_t w[TR][kLdsRow];            // the chunk's weight rows
   uint16_t x[kMaxTokens][kLdsRow];    // the chunk's token rows
 };
-static_assert(sizeof(SkinnyStage) >= 4 * kWave * sizeof(float) * 4, "partials reuse the staging tile");
 
-template <int EPI, int P>
+// TR weight rows per block (32 or 48: TR / 16 MFMA column tiles) against the
+// 32 token rows (two row tiles).
+template <int EPI, int P, int TR>
 __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs a) {
-  __shared__ SkinnyStage stage[kWaves];   // 18 KB per wave; reused for the block's partial sums
+  constexpr int RT = TR / 16;       // weight-row tiles
+  constexpr int NT = 2 * RT;        // output tiles (token half, row tile)
+  constexpr int WL = TR / 8;        // weight-row loads per lane per chunk
+  static_assert(sizeof(SkinnyStage<TR>) >= NT * kWave * sizeof(float) * 4, "partials reuse the staging tile");
+  __shared__ SkinnyStage<TR> stage[kWaves];   // reused for the block's partial sums
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = threadIdx.x / kWave;
   const int grp = lane >> 4;
   const int r16 = lane & 15;
-  const int n0 = blockIdx.x * kTileRows;
+  const int n0 = blockIdx.x * TR;
   const int K = a.K;
   // the block's K range is walked in steps of kWaves chunks, wave w taking chunk
   // w of each step: the block reads 512 contiguous bytes of each row at a time
@@ -101,7 +106,7 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs 
   const int nchunks = kb / (kWaves * kChunk);   // chunks per wave
   const int kw0 = blockIdx.y * kb + wid * kChunk;
   constexpr int kStride = kWaves * kChunk;  // K elements between a wave's chunks
-  SkinnyStage& st = stage[wid];
+  SkinnyStage<TR>& st = stage[wid];
 
   // coalesced staging: load i covers rows 8i .. 8i+7, eight lanes per 128-byte
   // row run. Weight rows past N and token rows past M re-read the last valid row
@@ -109,29 +114,32 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs 
   // unconditional so the compiler can count them and wait only for the oldest.
   const int srow = lane >> 3;               // 0..7
   const int scol = (lane & 7) * 8;          // element offset in the chunk
-  const uint16_t* wp[4];
+  const uint16_t* wp[WL];
   const uint16_t* xp[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = min(n0 + 8 * i + srow, a.N - 1), tok = min(8 * i + srow, a.M - 1);
+  for (int i = 0; i < WL; ++i) {
+    const int row = min(n0 + 8 * i + srow, a.N - 1);
     wp[i] = a.w + static_cast<size_t>(row) * K + kw0 + scol;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int tok = min(8 * i + srow, a.M - 1);
     xp[i] = a.x + static_cast<size_t>(tok) * K + kw0 + scol;
   }
   // ring of P chunks in registers: chunk g*P + p lives in slot p (nchunks % P == 0)
-  uint4 rw[P][4], rx[P][4];
+  uint4 rw[P][WL], rx[P][4];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      rw[p][i] = ld16_stream(wp[i] + p * kStride);
-      rx[p][i] = ld16(xp[i] + p * kStride);
-    }
+    for (int i = 0; i < WL; ++i) rw[p][i] = ld16_stream(wp[i] + p * kStride);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rx[p][i] = ld16(xp[i] + p * kStride);
     __builtin_amdgcn_sched_barrier(0);   // issue the slots in order: slot p is waited for alone
   }
 
-  f32x4 c[4];
+  f32x4 c[NT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) c[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < NT; ++i) c[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int ngroups = nchunks / P;
   for (int g = 0; g < ngroups; ++g) {
@@ -140,43 +148,43 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs 
     for (int p = 0; p < P; ++p) {
       wave_lds_sync();   // the previous chunk's operand reads are issued before these stores
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        *reinterpret_cast<uint4*>(&st.w[8 * i + srow][scol]) = rw[p][i];
-        *reinterpret_cast<uint4*>(&st.x[8 * i + srow][scol]) = rx[p][i];
-      }
+      for (int i = 0; i < WL; ++i) *reinterpret_cast<uint4*>(&st.w[8 * i + srow][scol]) = rw[p][i];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&st.x[8 * i + srow][scol]) = rx[p][i];
       if (refill) {   // P chunks stay in flight during the MFMAs
         const int off = ((g + 1) * P + p) * kStride;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          rw[p][i] = ld16_stream(wp[i] + off);
-          rx[p][i] = ld16(xp[i] + off);
-        }
+        for (int i = 0; i < WL; ++i) rw[p][i] = ld16_stream(wp[i] + off);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rx[p][i] = ld16(xp[i] + off);
       }
       wave_lds_sync();
 #pragma unroll
       for (int kk = 0; kk < kChunk / 32; ++kk) {
         const int col = kk * 32 + 8 * grp;
-        const uint4 wa = *reinterpret_cast<const uint4*>(&st.w[r16][col]);
-        const uint4 wb = *reinterpret_cast<const uint4*>(&st.w[16 + r16][col]);
+        uint4 wt[RT];
+#pragma unroll
+        for (int rh = 0; rh < RT; ++rh) wt[rh] = *reinterpret_cast<const uint4*>(&st.w[16 * rh + r16][col]);
         const uint4 xa = *reinterpret_cast<const uint4*>(&st.x[r16][col]);
         const uint4 xb = *reinterpret_cast<const uint4*>(&st.x[16 + r16][col]);
-        // tile (token half, row half): A = tokens, B = weight rows
-        c[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xa), as_bf8(wa), c[0], 0, 0, 0);
-        c[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xa), as_bf8(wb), c[1], 0, 0, 0);
-        c[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xb), as_bf8(wa), c[2], 0, 0, 0);
-        c[3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xb), as_bf8(wb), c[3], 0, 0, 0);
+        // tile (token half th, row tile rh) = th * RT + rh: A = tokens, B = weight rows
+#pragma unroll
+        for (int rh = 0; rh < RT; ++rh) {
+          c[rh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xa), as_bf8(wt[rh]), c[rh], 0, 0, 0);
+          c[RT + rh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(xb), as_bf8(wt[rh]), c[RT + rh], 0, 0, 0);
+        }
       }
     }
   }
   __syncthreads();   // every wave is done with its staging tile
   f32x4 (*cbuf)[kWave] = reinterpret_cast<f32x4 (*)[kWave]>(&stage[wid]);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) cbuf[i][lane] = c[i];
+  for (int i = 0; i < NT; ++i) cbuf[i][lane] = c[i];
   __syncthreads();
-  // wave w finishes tile ti = w = 2*token_half + row_half: lane (grp, r16) holds
-  // tokens 16*th + 4*grp + r (r < 4) against weight row n0 + 16*rh + r16
-  {
-    const int ti = wid, th = ti >> 1, rh = ti & 1;
+  // wave w finishes tiles ti = w, w + 4, ...: lane (grp, r16) holds tokens
+  // 16*th + 4*grp + r (r < 4) against weight row n0 + 16*rh + r16
+  for (int ti = wid; ti < NT; ti += kWaves) {
+    const int th = ti / RT, rh = ti % RT;
     const f32x4 s = (reinterpret_cast<const f32x4*>(&stage[0])[ti * kWave + lane] +
                      reinterpret_cast<const f32x4*>(&stage[1])[ti * kWave + lane]) +
                     (reinterpret_cast<const f32x4*>(&stage[2])[ti * kWave + lane] +
@@ -223,13 +231,40 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs 
 // allows it (deeper rings cost occupancy and measured no faster).
 int skinny_depth(int nchunks) { return nchunks % 2 == 0 ? 2 : 1; }
 
+// Block height: 32 weight rows, or 48 when that fills the device in fewer
+// rounds of one block per CU (e.g. 12288 rows: 384 blocks of 32 take two
+// rounds on 256 CUs, 256 blocks of 48 take one of 1.5x the work).
+int skinny_cus() {
+  static int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    return n;
+  }();
+  return cus;
+}
+
+template <int EPI, int TR>
+void launch_tr(const SkinnyArgs& a, hipStream_t st) {
+  const dim3 grid((a.N + TR - 1) / TR, a.ks);
+  if (skinny_depth(a.K / a.ks / kWaves / kChunk) == 2)
+    skinny_gemm_kernel<EPI, 2, TR><<<grid, kThreads, 0, st>>>(a);
+  else
+    skinny_gemm_kernel<EPI, 1, TR><<<grid, kThreads, 0, st>>>(a);
+}
+
 template <int EPI>
 int launch_skinny(const SkinnyArgs& a, hipStream_t st, const char* name) {
-  const dim3 grid((a.N + kTileRows - 1) / kTileRows, a.ks);
-  if (skinny_depth(a.K / a.ks / kWaves / kChunk) == 2)
-    skinny_gemm_kernel<EPI, 2><<<grid, kThreads, 0, st>>>(a);
+  const int64_t cus = skinny_cus();
+  auto cost = [&](int64_t tr) {   // rounds of resident blocks x rows per block
+    const int64_t blocks = (a.N + tr - 1) / tr * a.ks;
+    return (blocks + cus - 1) / cus * tr;
+  };
+  if (cost(48) < cost(32))
+    launch_tr<EPI, 48>(a, st);
   else
-    skinny_gemm_kernel<EPI, 1><<<grid, kThreads, 0, st>>>(a);
+    launch_tr<EPI, 32>(a, st);
   return launched(name);
 }
 
