@@ -416,6 +416,9 @@ def main() -> int:
                     help="skip the bs=32, MLA and prefill measurements")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only launch the dominant kernel loop (for rocprofv3 counter runs)")
+    ap.add_argument("--only", choices=("bs32", "mla", "prefill"),
+                    help="run one of the secondary configurations alone and print its line "
+                         "(for rocprofv3 kernel traces of that workload)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode path runs on a single MI355X; "
@@ -424,6 +427,12 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+
+    if args.only:
+        run = {"bs32": lambda: batch32(args.seed, args.steps), "mla": mla_decode,
+               "prefill": prefill_layer}[args.only]
+        print(json.dumps({args.only: run()}))
+        return 0
 
     from tilefoundry_amd.qwen3 import Engine, QWEN3_1_7B
 

@@ -3,6 +3,7 @@
     python -m tilefoundry_amd.rocprof_summary stats <dir>   # *kernel_stats.csv -> stats_summary.json
     python -m tilefoundry_amd.rocprof_summary pmc <dir>     # *counter_collection.csv -> pmc_summary.json
     python -m tilefoundry_amd.rocprof_summary traffic <fetch_dir> <write_dir> <kernel substring>
+    python -m tilefoundry_amd.rocprof_summary table <dir> [rows]  # stats_summary.json -> markdown
 
 ``stats`` keeps per-kernel call counts and durations and deletes the raw kernel
 trace (it can exceed what a run may copy back). ``pmc`` averages each counter
@@ -66,12 +67,25 @@ def traffic(fetch_dir: str, write_dir: str, needle: str, copy_bytes: int = 64 <<
             "traffic_bytes_per_launch": int(round(f_k * kib * ff + w_k * kib * wf))}
 
 
+def table(d: str, rows: int = 16) -> str:
+    """The busiest kernels of a ``stats`` summary as a markdown table."""
+    data = json.load(open(os.path.join(d, "stats_summary.json")))
+    lines = ["| kernel | calls | avg us | min us | max us | % time |", "|---|---:|---:|---:|---:|---:|"]
+    for r in data[:rows]:
+        name = r["name"].replace("|", "\\|")
+        lines.append(f"| `{name[:110]}` | {r['calls']} | {r['avg_us']:.2f} | {r['min_us']:.2f} | "
+                     f"{r['max_us']:.2f} | {r['pct']:.2f} |")
+    return "\n".join(lines)
+
+
 if __name__ == "__main__":
     mode = sys.argv[1]
     if mode == "stats":
         stats(sys.argv[2])
     elif mode == "pmc":
         pmc(sys.argv[2])
+    elif mode == "table":
+        print(table(sys.argv[2], int(sys.argv[3]) if len(sys.argv) > 3 else 16))
     elif mode == "traffic":
         print(json.dumps(traffic(sys.argv[2], sys.argv[3], sys.argv[4]), indent=1))
     else:
