@@ -2,9 +2,9 @@
 // (Qwen3.5-family full-attention layer, Qwen3.8-27B shapes: 24 query heads
 // over 4 key/value heads), on bf16 MFMA.
 //
-// One 256-thread block per (query head, 128 query rows): each of the four
-// waves (one per SIMD) owns 32 query rows over the whole head dimension and
-// walks the 32-key tiles up to its diagonal. Per tile:
+// One 256-thread block per (query head, 128 query rows), two blocks per CU:
+// each of the four waves (one per SIMD per block) owns 32 query rows over the
+// whole head dimension and walks the 32-key tiles up to its diagonal. Per tile:
 //
 //   S^T = K . Q^T     v_mfma_f32_32x32x16_bf16, M = 32 keys, N = 32 queries,
 //                     16 k-steps over D; Q^T is resident as the B operand, the
@@ -21,12 +21,14 @@
 //                     reads of the row-major V tile, also streamed ahead.
 //
 // K and V tiles stream global -> LDS with global_load_lds_dwordx4 (no register
-// staging) through a three-stage ring, loads running two tiles ahead. Each
-// stage is its own LDS object and the block barrier is a bare s_barrier after
-// an explicit wait for this wave's loads of the current tile, so the loads of
-// the next tile stay in flight across it. 106 KB of LDS per block, one wave per
-// SIMD; the output accumulators (256 dims x 32 queries, f32) and Q stay in
-// registers.
+// staging) through two stages: the next tile's loads go out right after the
+// tile barrier and land while this tile is computed. Each stage is its own LDS
+// object and the block barrier is a bare s_barrier after an explicit wait for
+// this wave's loads. 70 KB of LDS and at most 256 registers per wave, so two
+// blocks share a CU (two waves per SIMD): one block's softmax and barrier
+// waits run under the other's MFMAs (three stages at one block per CU measured
+// 16 % slower). The output accumulators (256 dims x 32 queries, f32) and Q stay
+// in registers.
 // Epilogue in the reference's order: out = bf16(bf16(o / l) * bf16(sigmoid(gate))).
 //
 // Reference (jingchangshi/TileFoundry): examples/qwen3_8_27b_prefill-tilelang/model.py:305-324
@@ -72,7 +74,7 @@ struct FlashArgs {
 // operand address is one per-lane base plus an immediate offset.
 constexpr int kKPitch = D + 8;    // elements
 constexpr int kVPitch = D + 32;
-constexpr int kStages = 3;        // K / V tile buffers: loads run two tiles ahead
+constexpr int kStages = 2;        // K / V tile buffers: loads run one tile ahead
 constexpr int kDT = D / 32;       // 32-dim output tiles
 constexpr int kST = D / 16;       // 16-dim score k-steps
 constexpr int kKPF = 4;           // K operand reads in flight ahead of the score MFMAs
@@ -88,31 +90,26 @@ TFA_DEV uint2 ld_tr(const uint16_t* lds_elem) {
 }
 
 constexpr int kWaitVm0 = waitcnt_vm(0);
-constexpr int kWaitVm16 = waitcnt_vm(16);   // one tile's loads of one wave
 
 template <int N>
 using IC = std::integral_constant<int, N>;
 
-__global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_prefill_kernel(const FlashArgs a) {
   constexpr int QT = 1;       // 32-row query tiles per wave
   constexpr int kWM = 32 * QT;
   // one LDS object per ring stage, indexed only by compile-time stage numbers
   __shared__ __attribute__((aligned(16))) uint16_t ks0[kBN][kKPitch];
   __shared__ __attribute__((aligned(16))) uint16_t ks1[kBN][kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t ks2[kBN][kKPitch];
   __shared__ __attribute__((aligned(16))) uint16_t vs0[kBN][kVPitch];
   __shared__ __attribute__((aligned(16))) uint16_t vs1[kBN][kVPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t vs2[kBN][kVPitch];
   auto kbuf = [&](auto b) __attribute__((always_inline)) -> uint16_t(*)[kKPitch] {
     if constexpr (decltype(b)::value == 0) return ks0;
-    else if constexpr (decltype(b)::value == 1) return ks1;
-    else return ks2;
+    else return ks1;
   };
   auto vbuf = [&](auto b) __attribute__((always_inline)) -> uint16_t(*)[kVPitch] {
     if constexpr (decltype(b)::value == 0) return vs0;
-    else if constexpr (decltype(b)::value == 1) return vs1;
-    else return vs2;
+    else return vs1;
   };
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -171,7 +168,6 @@ void flash_prefill_kernel(const FlashArgs a) {
   }
   __builtin_amdgcn_s_waitcnt(kWaitVm0);   // Q is in; from here on only tile loads are in flight
   load_tile(0, IC<0>{});
-  load_tile(1, IC<1>{});
 
   f32x16 o[kDT][QT];   // O^T: value dims 32 dt + ..., queries q0 + 32 t + n32
 #pragma unroll
@@ -196,13 +192,14 @@ void flash_prefill_kernel(const FlashArgs a) {
   const int half16 = (lane >> 4) & 1;
   // One key tile in ring stage `b`. The block barrier is a bare s_barrier
   // between compiler fences: each wave first waits for its own loads of tile
-  // kt (the loads of kt + 1 stay in flight), and its reads of the stage being
-  // refilled were consumed by MFMAs of the previous step before it arrives.
+  // kt (the only ones in flight), and its reads of the stage being refilled --
+  // tile kt - 1's -- were consumed by MFMAs of the previous step before it
+  // arrives.
   auto step = [&](int kt, auto b) __attribute__((always_inline)) {
     constexpr int B = decltype(b)::value;
-    __builtin_amdgcn_s_waitcnt(kWaitVm16);   // tile kt landed; the next tile's loads may fly
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
     block_barrier();
-    load_tile(kt + 2, IC<(B + 2) % kStages>{});   // into the stage of tile kt - 1
+    load_tile(kt + 1, IC<(B + 1) % kStages>{});   // into the stage of tile kt - 1   // into the stage of tile kt - 1
     uint16_t(*kb)[kKPitch] = kbuf(b);
     uint16_t(*vb)[kVPitch] = vbuf(b);
 
@@ -305,11 +302,10 @@ void flash_prefill_kernel(const FlashArgs a) {
       }
     }
   };
-  static_assert(kStages == 3, "the key loop is unrolled over three ring stages");
+  static_assert(kStages == 2, "the key loop is unrolled over two ring stages");
   for (int kt = 0; kt < ntiles; kt += kStages) {
     step(kt, IC<0>{});
     if (kt + 1 < ntiles) step(kt + 1, IC<1>{});
-    if (kt + 2 < ntiles) step(kt + 2, IC<2>{});
   }
   // no load may still be writing this block's LDS when the block ends
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
