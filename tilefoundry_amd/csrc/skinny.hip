@@ -86,13 +86,13 @@ struct SkinnyStage {
 
 // TR weight rows per block (32 or 48: TR / 16 MFMA column tiles) against the
 // 32 token rows (two row tiles).
-template <int EPI, int P, int TR>
-__global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs a) {
+template <int EPI, int P, int TR, int W>
+__global__ __launch_bounds__(W * kWave) void skinny_gemm_kernel(const SkinnyArgs a) {
   constexpr int RT = TR / 16;       // weight-row tiles
   constexpr int NT = 2 * RT;        // output tiles (token half, row tile)
   constexpr int WL = TR / 8;        // weight-row loads per lane per chunk
   static_assert(sizeof(SkinnyStage<TR>) >= NT * kWave * sizeof(float) * 4, "partials reuse the staging tile");
-  __shared__ SkinnyStage<TR> stage[kWaves];   // reused for the block's partial sums
+  __shared__ SkinnyStage<TR> stage[W];   // reused for the block's partial sums
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = threadIdx.x / kWave;
@@ -100,12 +100,12 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs 
   const int r16 = lane & 15;
   const int n0 = blockIdx.x * TR;
   const int K = a.K;
-  // the block's K range is walked in steps of kWaves chunks, wave w taking chunk
-  // w of each step: the block reads 512 contiguous bytes of each row at a time
+  // the block's K range is walked in steps of W chunks, wave w taking chunk w
+  // of each step: the block reads 128 W contiguous bytes of each row at a time
   const int kb = K / a.ks;                  // this block's K range
-  const int nchunks = kb / (kWaves * kChunk);   // chunks per wave
+  const int nchunks = kb / (W * kChunk);   // chunks per wave
   const int kw0 = blockIdx.y * kb + wid * kChunk;
-  constexpr int kStride = kWaves * kChunk;  // K elements between a wave's chunks
+  constexpr int kStride = W * kChunk;  // K elements between a wave's chunks
   SkinnyStage<TR>& st = stage[wid];
 
   // coalesced staging: load i covers rows 8i .. 8i+7, eight lanes per 128-byte
@@ -183,12 +183,12 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(const SkinnyArgs 
   __syncthreads();
   // wave w finishes tiles ti = w, w + 4, ...: lane (grp, r16) holds tokens
   // 16*th + 4*grp + r (r < 4) against weight row n0 + 16*rh + r16
-  for (int ti = wid; ti < NT; ti += kWaves) {
+  for (int ti = wid; ti < NT; ti += W) {
     const int th = ti / RT, rh = ti % RT;
-    const f32x4 s = (reinterpret_cast<const f32x4*>(&stage[0])[ti * kWave + lane] +
-                     reinterpret_cast<const f32x4*>(&stage[1])[ti * kWave + lane]) +
-                    (reinterpret_cast<const f32x4*>(&stage[2])[ti * kWave + lane] +
-                     reinterpret_cast<const f32x4*>(&stage[3])[ti * kWave + lane]);
+    // pairwise over the waves' K ranges: ((0 + 1) + (2 + 3)) [+ ((4 + 5) + (6 + 7))]
+    auto part = [&](int w) { return reinterpret_cast<const f32x4*>(&stage[w])[ti * kWave + lane]; };
+    f32x4 s = (part(0) + part(1)) + (part(2) + part(3));
+    if (W == 8) s += (part(4) + part(5)) + (part(6) + part(7));
     const int n = n0 + 16 * rh + r16;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -245,13 +245,23 @@ int skinny_cus() {
   return cus;
 }
 
+template <int EPI, int TR, int W>
+void launch_trw(const SkinnyArgs& a, hipStream_t st) {
+  const dim3 grid((a.N + TR - 1) / TR, a.ks);
+  if (skinny_depth(a.K / a.ks / W / kChunk) == 2)
+    skinny_gemm_kernel<EPI, 2, TR, W><<<grid, W * kWave, 0, st>>>(a);
+  else
+    skinny_gemm_kernel<EPI, 1, TR, W><<<grid, W * kWave, 0, st>>>(a);
+}
+
+// Eight waves per block (two per SIMD) when the block's K range splits into
+// 512-element steps: twice the loads in flight per CU of the four-wave form.
 template <int EPI, int TR>
 void launch_tr(const SkinnyArgs& a, hipStream_t st) {
-  const dim3 grid((a.N + TR - 1) / TR, a.ks);
-  if (skinny_depth(a.K / a.ks / kWaves / kChunk) == 2)
-    skinny_gemm_kernel<EPI, 2, TR><<<grid, kThreads, 0, st>>>(a);
+  if ((a.K / a.ks) % (8 * kChunk) == 0)
+    launch_trw<EPI, TR, 8>(a, st);
   else
-    skinny_gemm_kernel<EPI, 1, TR><<<grid, kThreads, 0, st>>>(a);
+    launch_trw<EPI, TR, 4>(a, st);
 }
 
 template <int EPI>
