@@ -122,6 +122,42 @@ def test_mla_attention_vs_oracle(dev, split, pos):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("heads", [1, 8, 17, 48])
+def test_mla_attention_split_outputs_other_head_counts(dev, heads):
+    """The split outputs (op normalised by the split's own sum, natural-log max,
+    sum) merged over the live splits equal the oracle's latent sum, for head
+    counts that leave whole or partial 16-head tiles empty and contexts that end
+    inside a 128-position step."""
+    from dataclasses import replace
+
+    from tilefoundry_amd._lib import C
+
+    cfg = replace(CFG, heads=heads)
+    B, cap, split = 2, 512, 128
+    pos = [129, 511]
+    lat, rk = OM.random_cache(B, cap, cfg, seed=heads)
+    g = gen(heads)
+    q_abs = torch.randn(B, heads, KV + R, generator=g).to(BF)
+    ns = cap // split
+    op = torch.empty(B, ns, heads, KV, dtype=BF, device=dev)
+    mp = torch.empty(B, ns, heads, device=dev)
+    lp = torch.empty(B, ns, heads, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    C.mla_attention(q_abs.to(dev), lat.to(dev), rk.to(dev), torch.tensor(pos, dtype=torch.int32, device=dev),
+                    split, cfg.scale, op, mp, lp, err)
+    assert int(err.item()) == 0
+    w = OM.random_weights(cfg, seed=1)
+    for b, p in enumerate(pos):
+        live = p // split + 1
+        o, m, l = op[b, :live].float().cpu(), mp[b, :live].cpu(), lp[b, :live].cpu()
+        wgt = l * torch.exp(m - m.amax(0, keepdim=True))                   # [live, heads]
+        got = (o * wgt[..., None]).sum(0) / wgt.sum(0)[:, None]
+        _, ref = OM.attend_absorbed(q_abs[b], lat[b, :p + 1], rk[b, :p + 1], w, cfg, p_bf16=True,
+                                    return_latent=True)
+        assert_close(f"o_lat heads={heads} b={b} pos={p}", got, ref)
+
+
+@pytest.mark.gpu
 def test_mla_attention_stale_slots_ignored(dev):
     """Slots past the context hold NaN: nothing of them reaches the output."""
     g = gen(9)
