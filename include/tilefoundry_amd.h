@@ -349,9 +349,12 @@ int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void*
                           int64_t head_dim, float scale, hipStream_t stream);
 
 /* C[m, n] = bf16(A[m, k] . B[n, k]^T) (residual == NULL) or
- * C = bf16(residual + bf16(A . B^T)) (residual [m, ldr]); bf16 in, f32 accumulate,
- * bf16 MFMA. Row strides lda / ldb / ldc in elements. m, n multiples of 256, k of
- * 64; lda, ldb multiples of 8.
+ * C = bf16(residual + bf16(A . B^T)) (residual [m, ldr]); bf16 in, f32 accumulate.
+ * The product runs on hipBLASLt (one plan per device and shape, made on the
+ * first call, no workspace), the residual as a separate pass; shapes without a
+ * library plan -- and all shapes when TFA_GEMM_NATIVE=1 -- use the built-in bf16
+ * MFMA kernel. Row strides lda / ldb / ldc in elements. m, n multiples of 256,
+ * k of 64; lda, ldb multiples of 8 (and ldc, ldr with a residual).
  * Replaces: examples/qwen3_8_27b_prefill-tilelang/kernels/gemm.py:104-356 (gemm_kernel,
  * "residual" epilogue :193-198 -- model.py:326-333 Attention.o_proj). */
 int tfa_gemm_nt(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,

@@ -134,6 +134,44 @@ def test_o_proj_residual(dev):
     assert frac < 0.02, f"{frac:.3%} of outputs differ from the oracle"
 
 
+_NATIVE_GEMM = """
+import sys, torch
+from tilefoundry_amd._lib import C
+a, b, res = (torch.load(sys.argv[1], weights_only=True)[k].to("cuda:0") for k in ("a", "b", "res"))
+plain = torch.empty(a.shape[0], b.shape[0], dtype=torch.bfloat16, device="cuda:0")
+resid = torch.empty_like(plain)
+C.gemm_nt(a, b, plain, None)
+C.gemm_nt(a, b, resid, res)
+torch.save({"plain": plain.cpu(), "resid": resid.cpu()}, sys.argv[2])
+"""
+
+
+@pytest.mark.gpu
+def test_gemm_native_kernel(dev, tmp_path):
+    """The hand-written MFMA GEMM (the path for shapes the library has no plan
+    for, forced by TFA_GEMM_NATIVE=1 in a child process) against the oracle, plain
+    and with the o_proj residual."""
+    import os
+    import subprocess
+    import sys
+
+    g = torch.Generator().manual_seed(31)
+    M, N, K = 512, 768, 320
+    a = torch.randn(M, K, generator=g).to(BF)
+    b = (0.05 * torch.randn(N, K, generator=g)).to(BF)
+    res = torch.randn(M, N, generator=g).to(BF)
+    torch.save({"a": a, "b": b, "res": res}, tmp_path / "in.pt")
+    env = dict(os.environ, TFA_GEMM_NATIVE="1")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    subprocess.run([sys.executable, "-c", _NATIVE_GEMM, str(tmp_path / "in.pt"), str(tmp_path / "out.pt")],
+                   env=env, cwd=root, check=True, timeout=120)
+    out = torch.load(tmp_path / "out.pt", weights_only=True)
+    ref = a.float() @ b.float().t()
+    assert_close("native gemm", out["plain"], ref.to(BF))
+    assert rel_l2(out["plain"], ref) < 4e-3
+    assert_close("native gemm + residual", out["resid"], OP.o_proj(a, res, b))
+
+
 def _layer_weights(seed=5):
     return OP.random_layer(CFG, seed=seed)
 

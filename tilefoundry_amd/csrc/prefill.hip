@@ -45,8 +45,6 @@ using namespace tfa;
 namespace {
 
 constexpr int D = 256;
-constexpr int kWaves = 4;           // one per SIMD
-constexpr int kBM = 32 * kWaves;    // query rows per block (32 per wave)
 constexpr int kBN = 32;             // keys per tile
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -74,7 +72,6 @@ struct FlashArgs {
 // operand address is one per-lane base plus an immediate offset.
 constexpr int kKPitch = D + 8;    // elements
 constexpr int kVPitch = D + 32;
-constexpr int kStages = 2;        // K / V tile buffers: loads run one tile ahead
 constexpr int kDT = D / 32;       // 32-dim output tiles
 constexpr int kST = D / 16;       // 16-dim score k-steps
 constexpr int kKPF = 4;           // K operand reads in flight ahead of the score MFMAs
@@ -94,22 +91,35 @@ constexpr int kWaitVm0 = waitcnt_vm(0);
 template <int N>
 using IC = std::integral_constant<int, N>;
 
-__global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// W waves of 32 query rows per block. W = 8 (256 rows, 3 stages, one block per
+// CU) halves the K/V bytes moved into LDS per FLOP against W = 4 (128 rows, 2
+// stages, two blocks per CU); both keep two waves per SIMD.
+template <int W>
+__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_prefill_kernel(const FlashArgs a) {
   constexpr int QT = 1;       // 32-row query tiles per wave
   constexpr int kWM = 32 * QT;
+  constexpr int kBM = kWM * W;                 // query rows per block
+  constexpr int kStages = W == 8 ? 3 : 2;      // loads run kStages - 1 tiles ahead
+  constexpr int kRowsPerWave = kBN / W;        // K and V rows each wave moves per tile
+  constexpr int kTileVm = 2 * kRowsPerWave;    // DMA instructions per wave per tile
+  constexpr int kWaitStep = waitcnt_vm(kStages == 3 ? kTileVm : 0);
   // one LDS object per ring stage, indexed only by compile-time stage numbers
   __shared__ __attribute__((aligned(16))) uint16_t ks0[kBN][kKPitch];
   __shared__ __attribute__((aligned(16))) uint16_t ks1[kBN][kKPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t ks2[kStages == 3 ? kBN : 1][kKPitch];
   __shared__ __attribute__((aligned(16))) uint16_t vs0[kBN][kVPitch];
   __shared__ __attribute__((aligned(16))) uint16_t vs1[kBN][kVPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t vs2[kStages == 3 ? kBN : 1][kVPitch];
   auto kbuf = [&](auto b) __attribute__((always_inline)) -> uint16_t(*)[kKPitch] {
     if constexpr (decltype(b)::value == 0) return ks0;
-    else return ks1;
+    else if constexpr (decltype(b)::value == 1) return ks1;
+    else return ks2;
   };
   auto vbuf = [&](auto b) __attribute__((always_inline)) -> uint16_t(*)[kVPitch] {
     if constexpr (decltype(b)::value == 0) return vs0;
-    else return vs1;
+    else if constexpr (decltype(b)::value == 1) return vs1;
+    else return vs2;
   };
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -137,22 +147,22 @@ void flash_prefill_kernel(const FlashArgs a) {
   const int my_last = (q0 + kWM - 1) / kBN;     // the wave's last tile with a visible key
 
   // direct global -> LDS tile loads, one 512-byte row per instruction (lanes
-  // 0..31): wave w moves rows 8w .. 8w+7 of K and of V. Every step issues
-  // exactly one tile's loads (past the last tile it reloads the last tile into
-  // the free stage, where nothing reads it), so the number of loads in flight
-  // behind tile kt is always one tile's and every wait count is a constant.
+  // 0..31): wave w moves rows R w .. R w + R - 1 of K and of V (R = 32 / W).
+  // Every step issues exactly one tile's loads (past the last tile it reloads
+  // the last tile into a free stage, where nothing reads it), so the number of
+  // loads in flight behind tile kt is constant and so is every wait count.
   auto load_tile = [&](int kt, auto b) __attribute__((always_inline)) {
     kt = kt < ntiles ? kt : ntiles - 1;
-    const size_t r0 = static_cast<size_t>(kt) * kBN + 8 * wid;
+    const size_t r0 = static_cast<size_t>(kt) * kBN + kRowsPerWave * wid;
     uint16_t(*kb)[kKPitch] = kbuf(b);
     uint16_t(*vb)[kVPitch] = vbuf(b);
     if (lane < 32) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kRowsPerWave; ++i) {
         const uint16_t* krow = a.k + (r0 + i) * a.k_rs + g * a.k_hs;
         const uint16_t* vrow = a.v + (r0 + i) * a.v_rs + g * a.v_hs;
-        lds_dma16(krow + 8 * n32, lds_offset(&kb[8 * wid + i][0]));
-        lds_dma16(vrow + 8 * n32, lds_offset(&vb[8 * wid + i][0]));
+        lds_dma16(krow + 8 * n32, lds_offset(&kb[kRowsPerWave * wid + i][0]));
+        lds_dma16(vrow + 8 * n32, lds_offset(&vb[kRowsPerWave * wid + i][0]));
       }
     }
   };
@@ -168,6 +178,7 @@ void flash_prefill_kernel(const FlashArgs a) {
   }
   __builtin_amdgcn_s_waitcnt(kWaitVm0);   // Q is in; from here on only tile loads are in flight
   load_tile(0, IC<0>{});
+  if constexpr (kStages == 3) load_tile(1, IC<1>{});
 
   f32x16 o[kDT][QT];   // O^T: value dims 32 dt + ..., queries q0 + 32 t + n32
 #pragma unroll
@@ -197,9 +208,9 @@ void flash_prefill_kernel(const FlashArgs a) {
   // arrives.
   auto step = [&](int kt, auto b) __attribute__((always_inline)) {
     constexpr int B = decltype(b)::value;
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __builtin_amdgcn_s_waitcnt(kWaitStep);   // tile kt landed; with three stages tile kt + 1 may fly
     block_barrier();
-    load_tile(kt + 1, IC<(B + 1) % kStages>{});   // into the stage of tile kt - 1   // into the stage of tile kt - 1
+    load_tile(kt + kStages - 1, IC<(B + kStages - 1) % kStages>{});   // into the stage of tile kt - 1
     uint16_t(*kb)[kKPitch] = kbuf(b);
     uint16_t(*vb)[kVPitch] = vbuf(b);
 
@@ -302,10 +313,11 @@ void flash_prefill_kernel(const FlashArgs a) {
       }
     }
   };
-  static_assert(kStages == 2, "the key loop is unrolled over two ring stages");
   for (int kt = 0; kt < ntiles; kt += kStages) {
     step(kt, IC<0>{});
     if (kt + 1 < ntiles) step(kt + 1, IC<1>{});
+    if constexpr (kStages == 3)
+      if (kt + 2 < ntiles) step(kt + 2, IC<2>{});
   }
   // no load may still be writing this block's LDS when the block ends
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
@@ -351,8 +363,8 @@ int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void*
   TFA_NONNULL(gate);
   TFA_NONNULL(out);
   TFA_REQUIRE(head_dim == D, TFA_ERR_SHAPE, "tfa_prefill_attention: head_dim %lld, only 256 supported", (long long)head_dim);
-  TFA_REQUIRE(n >= kBM && n % kBM == 0 && n <= (1 << 20), TFA_ERR_SHAPE,
-              "tfa_prefill_attention: n %lld must be a positive multiple of %d", (long long)n, kBM);
+  TFA_REQUIRE(n >= 128 && n % 128 == 0 && n <= (1 << 20), TFA_ERR_SHAPE,
+              "tfa_prefill_attention: n %lld must be a positive multiple of %d", (long long)n, 128);
   TFA_REQUIRE(kv_heads >= 1 && heads >= kv_heads && heads % kv_heads == 0 && heads <= 65535, TFA_ERR_SHAPE,
               "tfa_prefill_attention: heads %lld not a multiple of kv_heads %lld", (long long)heads, (long long)kv_heads);
   TFA_REQUIRE(q_rs % 8 == 0 && q_hs % 8 == 0 && k_rs % 8 == 0 && k_hs % 8 == 0 && v_rs % 8 == 0 &&
@@ -381,7 +393,11 @@ int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void*
   // XCD-grouped order when every XCD gets whole heads of a single group
   const int64_t per = heads / 8, group = heads / kv_heads;
   a.xcd_heads = (heads % 8 == 0 && per >= 1 && (group % per == 0 || per % group == 0)) ? (int)per : 0;
-  flash_prefill_kernel<<<(unsigned)(heads * (n / kBM)), kWaves * kWave, 0, stream>>>(a);
+  // 256-row blocks when they still give every CU a block, else 128-row blocks
+  if (n % 256 == 0 && heads * (n / 256) >= 256)
+    flash_prefill_kernel<8><<<(unsigned)(heads * (n / 256)), 8 * kWave, 0, stream>>>(a);
+  else
+    flash_prefill_kernel<4><<<(unsigned)(heads * (n / 128)), 4 * kWave, 0, stream>>>(a);
   return launched("flash_prefill");
 }
 
