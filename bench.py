@@ -23,6 +23,9 @@ The JSON line also carries:
   bs32          the same greedy decode for 32 sequences (tok/s, all sequences)
   mla_decode_b8_ctx8192      MiniCPM3-shaped absorbed MLA block, batch 8
   prefill_attention_layer    Qwen3.5 attention layer at 1024 / 4096 / 8192 tokens
+  prompt_prefill_bs1         time to consume a 64- and a 512-token prompt, walked
+                             (one decode step per token) and prefilled (every layer
+                             over all prompt rows at once); bs32.prompt likewise
 """
 from __future__ import annotations
 
@@ -30,6 +33,7 @@ import argparse
 import json
 import os
 import platform
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -240,6 +244,8 @@ def batch32(seed: int, steps: int) -> dict:
     prompts = torch.randint(0, cfg.vocab, (32, PROMPT), generator=g).tolist()
     eng.generate(prompts, min(16, steps))     # warm
     gen = eng.generate(prompts, steps)
+    walk = _first_token_ms(eng, prompts, False, reps=3)
+    pre = _first_token_ms(eng, prompts, True, reps=3)
     weight_bytes = sum(t.numel() * 2 for w in eng.layers for t in w.values()) + eng.embed.numel() * 2
     mean_ctx = PROMPT + steps / 2.0
     kv_bytes = 32 * cfg.layers * mean_ctx * 2 * cfg.kv_heads * cfg.head_dim * 2
@@ -247,10 +253,51 @@ def batch32(seed: int, steps: int) -> dict:
     out = {"value": round(gen.tokens_per_second, 1), "unit": "tok/s", "batch": 32, "new_tokens": steps,
            "prompt_tokens": PROMPT, "ms_per_step": round(ms, 4),
            "step_hbm": {"bytes_per_step": int(weight_bytes + kv_bytes),
-                        "GB/s": round((weight_bytes + kv_bytes) / (ms * 1e-3) / 1e9, 1)}}
+                        "GB/s": round((weight_bytes + kv_bytes) / (ms * 1e-3) / 1e9, 1)},
+           "prompt": {"walk": walk, "prefill": pre,
+                      "speedup": round(walk["prompt_ms"] / pre["prompt_ms"], 1)}}
     del eng
     torch.cuda.empty_cache()
     return out
+
+
+def _first_token_ms(eng, prompts, prefill: bool, reps: int = 5) -> dict:
+    """Median over `reps` of the time spent consuming the prompt before the first
+    kept pick (`prefill_seconds`) and of that plus the first decode step."""
+    eng.prompt_prefill = prefill
+    pre, ttft = [], []
+    for _ in range(reps + 1):
+        gen = eng.generate(prompts, 1)
+        pre.append(gen.prefill_seconds * 1e3)
+        ttft.append((gen.prefill_seconds + gen.seconds) * 1e3)
+    eng.prompt_prefill = False
+    return {"prompt_ms": round(statistics.median(pre[1:]), 3),
+            "first_token_ms": round(statistics.median(ttft[1:]), 3), "first_pick": gen.tokens[0]}
+
+
+def prompt_prefill(eng, seed: int, lengths=(64, 512)) -> dict:
+    """bs=1 prompt consumption on the decode model: the reference's walk (one
+    captured decode step per prompt token) against the prompt prefill (every
+    layer over all prompt rows at once: f32 GEMMs, row norms, one causal
+    attention launch per layer), same engine, same prompt."""
+    cfg = eng.cfg
+    out = {}
+    for n in lengths:
+        g = torch.Generator().manual_seed(seed + n)
+        prompt = torch.randint(0, cfg.vocab, (n,), generator=g).tolist()
+        walk = _first_token_ms(eng, prompt, False)
+        pre = _first_token_ms(eng, prompt, True)
+        out[str(n)] = {"walk": walk, "prefill": pre,
+                       "speedup": round(walk["prompt_ms"] / pre["prompt_ms"], 1),
+                       "same_first_pick": walk["first_pick"] == pre["first_pick"]}
+    return out
+
+
+def prompt_only(seed: int) -> dict:
+    from tilefoundry_amd.qwen3 import Engine, QWEN3_1_7B
+
+    eng = Engine(QWEN3_1_7B, device="cuda:0", max_new=16, prompt_room=512, seed=seed)
+    return prompt_prefill(eng, seed)
 
 
 def mla_decode() -> dict:
@@ -416,7 +463,7 @@ def main() -> int:
                     help="skip the bs=32, MLA and prefill measurements")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only launch the dominant kernel loop (for rocprofv3 counter runs)")
-    ap.add_argument("--only", choices=("bs32", "mla", "prefill"),
+    ap.add_argument("--only", choices=("bs32", "mla", "prefill", "prompt"),
                     help="run one of the secondary configurations alone and print its line "
                          "(for rocprofv3 kernel traces of that workload)")
     args = ap.parse_args()
@@ -430,7 +477,7 @@ def main() -> int:
 
     if args.only:
         run = {"bs32": lambda: batch32(args.seed, args.steps), "mla": mla_decode,
-               "prefill": prefill_layer}[args.only]
+               "prefill": prefill_layer, "prompt": lambda: prompt_only(args.seed)}[args.only]
         print(json.dumps({args.only: run()}))
         return 0
 
@@ -497,6 +544,7 @@ def main() -> int:
         "kernels": kernels,
         "decode_layer_bs1_ctx4096": layer,
         "first_tokens": gen.tokens[:8],
+        "prompt_prefill_bs1": None if args.no_kernels else prompt_prefill(eng, args.seed),
     }
     del eng
     torch.cuda.empty_cache()

@@ -353,8 +353,8 @@ int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void*
  * The product runs on hipBLASLt (one plan per device and shape, made on the
  * first call, no workspace), the residual as a separate pass; shapes without a
  * library plan -- and all shapes when TFA_GEMM_NATIVE=1 -- use the built-in bf16
- * MFMA kernel. Row strides lda / ldb / ldc in elements. m, n multiples of 256,
- * k of 64; lda, ldb multiples of 8 (and ldc, ldr with a residual).
+ * MFMA kernel. Row strides lda / ldb / ldc in elements. m >= 1, n a multiple of
+ * 256, k of 64; lda, ldb multiples of 8 (and ldc, ldr with a residual).
  * Replaces: examples/qwen3_8_27b_prefill-tilelang/kernels/gemm.py:104-356 (gemm_kernel,
  * "residual" epilogue :193-198 -- model.py:326-333 Attention.o_proj). */
 int tfa_gemm_nt(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
@@ -371,6 +371,59 @@ int tfa_gemm_nt(const void* a, const void* b, void* c, int64_t m, int64_t n, int
 int tfa_qkv_norm_rope(const void* hn, const void* w_qkv, void* out, int64_t n, int64_t hidden, int64_t heads,
                       int64_t kv_heads, int64_t head_dim, const void* gamma_q, const void* gamma_k, float eps,
                       const void* cos_t, const void* sin_t, int64_t rot, hipStream_t stream);
+
+/* ------------------------------------- prompt prefill (Qwen3-shaped decode model) */
+
+/* C[m, n] = A[m, k] . B[n, k]^T in f32 (bf16 in, f32 accumulate, no rounding):
+ * the prompt rows' projections, landed in bf16 by their consumers exactly as
+ * the decode step lands its split-K partials (tfa_rows_norm, tfa_silu_mul and
+ * tfa_prefill_qk_rope with ks = 1). hipBLASLt with the fallback of tfa_gemm_nt;
+ * m >= 1, n a multiple of 256, k of 64, lda / ldb multiples of 8.
+ * Replaces: the per-token projection GEMVs of the prompt walk,
+ * examples/qwen3_1_7b-tilelang/fast/engine.py:261-263 over fast/kernels.py:123-145
+ * (gemv) -- the same products for every prompt row in one call. */
+int tfa_gemm_nt_f32(const void* a, const void* b, float* c, int64_t m, int64_t n, int64_t k, int64_t lda,
+                    int64_t ldb, int64_t ldc, hipStream_t stream);
+
+/* SwiGLU of the prompt rows' fused gate|up product: gu f32 [rows, ld] with
+ * column 2i = gate_i, 2i+1 = up_i (the interleaved decode weight layout);
+ * act[r, i] = bf16(bf16(silu(bf16 g)) * bf16 u) -- the decode step's epilogue.
+ * inter a multiple of 4; ld >= 2*inter, a multiple of 4; gu 16-byte aligned.
+ * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:547-572 (silu_mul) and the
+ * SwiGLU prologue of :210-257 (gemv_silu), for every prompt row at once. */
+int tfa_swiglu_pairs(const float* gu, int64_t ld, int64_t rows, int64_t inter, void* act, hipStream_t stream);
+
+/* Per-head norm + RoPE + cache write for the prompt rows of a batch: qkv f32
+ * [batch * n, ldq] holds sequence b's row r at b * n + r (position pos0 + r),
+ * columns [q (hq*128) | k (hkv*128) | v (hkv*128)]. Each head lands in bf16;
+ * query heads get Qwen3RMSNorm(gamma_q) + rotate-half RoPE at the position and
+ * go to q_out[(b*n + r), hq*128]; key heads the same with gamma_k into
+ * k_cache[b, pos0 + r], value heads into v_cache[b, pos0 + r] (caches
+ * [batch, cap, hkv*128]). The arithmetic of tfa_qk_rope_cache, so a prefilled
+ * cache row is what the decode step would have written from the same
+ * projection values. head_dim 128; pos0 + n <= cap and <= rope_rows.
+ * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:328-411 (qk_rope_cache) run
+ * once per prompt token by the walk (fast/engine.py:261-263). */
+int tfa_prefill_qk_rope(const float* qkv, int64_t ldq, const void* gamma_q, const void* gamma_k, float eps_head,
+                        const void* cos_t, const void* sin_t, int64_t rope_rows, int64_t batch, int64_t n,
+                        int64_t pos0, void* k_cache, void* v_cache, int64_t cap, void* q_out, int64_t hq,
+                        int64_t hkv, int64_t head_dim, hipStream_t stream);
+
+/* Causal GQA attention of every row of a batch of prompts, no gate:
+ * out[b, r, h*D + d] = bf16(o / l), o = sum_{j <= r} bf16(exp(s - m)) v[b, j, g],
+ * s = scale * q[b, r, h] . k[b, j, g] (f32), g = h / (heads / kv_heads).
+ * Element (b, r, h, d) of q sits at q + b*q_bs + r*q_rs + h*q_hs + d; k and v
+ * likewise per kv head (the decode cache [batch, cap, kv_heads*D] is read in
+ * place: k_rs = kv_heads*D, k_hs = D, k_bs = cap*kv_heads*D); out rows at
+ * out + b*o_bs + r*o_rs. head_dim 128 or 256; any n >= 1; q/k/v strides
+ * multiples of 8, out strides multiples of 4 (elements).
+ * Replaces: the per-token attention of the prompt walk,
+ * examples/qwen3_1_7b-tilelang/fast/kernels.py:418-540 (attn_partial + merge) at each
+ * position 0..n-1 (fast/engine.py:261-263); ref_src/model.py:171-215 (self_attention). */
+int tfa_causal_attention(const void* q, int64_t q_rs, int64_t q_hs, int64_t q_bs, const void* k, int64_t k_rs,
+                         int64_t k_hs, int64_t k_bs, const void* v, int64_t v_rs, int64_t v_hs, int64_t v_bs,
+                         void* out, int64_t o_rs, int64_t o_bs, int64_t batch, int64_t n, int64_t heads,
+                         int64_t kv_heads, int64_t head_dim, float scale, hipStream_t stream);
 
 /* ------------------------------------------------------------ measurement */
 

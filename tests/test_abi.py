@@ -161,6 +161,46 @@ def test_batched_argument_checks(lib):
     assert st == SHAPE
 
 
+def test_prompt_prefill_argument_checks(lib):
+    # f32 GEMM: n not a multiple of 256, k not of 64, a null operand
+    st, msg = call(lib, "tfa_gemm_nt_f32", A, A, A, I64(37), I64(300), I64(2048), I64(2048), I64(2048), I64(300), P(None))
+    assert st == SHAPE and "256" in msg
+    st, _ = call(lib, "tfa_gemm_nt_f32", A, A, A, I64(37), I64(512), I64(100), I64(100), I64(100), I64(512), P(None))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_gemm_nt_f32", P(None), A, A, I64(37), I64(512), I64(2048), I64(2048), I64(2048), I64(512), P(None))
+    assert st == NULL
+    # SwiGLU pairs: odd inter, ld too small, misaligned gu
+    st, _ = call(lib, "tfa_swiglu_pairs", A, I64(12288), I64(4), I64(6146), A, P(None))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_swiglu_pairs", A, I64(100), I64(4), I64(6144), A, P(None))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_swiglu_pairs", MIS, I64(12288), I64(4), I64(6144), A, P(None))
+    assert st == ALIGN
+    # q/k norm + RoPE rows: positions past the cache or the rope table, head_dim
+    qk = lambda n, pos0, cap, rope, hd=128: (A, I64(4096), A, A, F(1e-6), A, A, I64(rope), I64(2), I64(n),
+                                             I64(pos0), A, A, I64(cap), A, I64(16), I64(8), I64(hd), P(None))
+    st, msg = call(lib, "tfa_prefill_qk_rope", *qk(100, 10, 100, 512))
+    assert st == CAPACITY and "capacity" in msg
+    st, msg = call(lib, "tfa_prefill_qk_rope", *qk(100, 0, 512, 64))
+    assert st == CAPACITY and "rope" in msg
+    st, _ = call(lib, "tfa_prefill_qk_rope", *qk(100, 0, 512, 512, hd=64))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_prefill_qk_rope", *qk(0, 0, 512, 512))
+    assert st == SHAPE
+    # causal attention: head_dim, empty n, heads not a multiple, misaligned stride
+    ca = lambda n, hd=128, hq=16, hkv=8, q_rs=2048: (A, I64(q_rs), I64(128), I64(0), A, I64(1024), I64(128), I64(0),
+                                                     A, I64(1024), I64(128), I64(0), A, I64(2048), I64(0), I64(1),
+                                                     I64(n), I64(hq), I64(hkv), I64(hd), F(0.088), P(None))
+    st, msg = call(lib, "tfa_causal_attention", *ca(64, hd=64))
+    assert st == SHAPE and "128, 256" in msg
+    st, _ = call(lib, "tfa_causal_attention", *ca(0))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_causal_attention", *ca(64, hq=12))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_causal_attention", *ca(64, q_rs=2044))
+    assert st == ALIGN
+
+
 def test_torch_extension_rejects_host_tensors():
     from tilefoundry_amd import ops
 

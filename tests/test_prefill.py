@@ -142,15 +142,19 @@ plain = torch.empty(a.shape[0], b.shape[0], dtype=torch.bfloat16, device="cuda:0
 resid = torch.empty_like(plain)
 C.gemm_nt(a, b, plain, None)
 C.gemm_nt(a, b, resid, res)
-torch.save({"plain": plain.cpu(), "resid": resid.cpu()}, sys.argv[2])
+f32 = torch.full((a.shape[0], b.shape[0]), float("nan"), device="cuda:0")
+C.gemm_nt_f32(a, b, f32)
+ragged = torch.full((37, b.shape[0]), float("nan"), device="cuda:0")
+C.gemm_nt_f32(a[:37], b, ragged)
+torch.save({"plain": plain.cpu(), "resid": resid.cpu(), "f32": f32.cpu(), "ragged": ragged.cpu()}, sys.argv[2])
 """
 
 
 @pytest.mark.gpu
 def test_gemm_native_kernel(dev, tmp_path):
     """The hand-written MFMA GEMM (the path for shapes the library has no plan
-    for, forced by TFA_GEMM_NATIVE=1 in a child process) against the oracle, plain
-    and with the o_proj residual."""
+    for, forced by TFA_GEMM_NATIVE=1 in a child process) against the oracle, plain,
+    with the o_proj residual, and with the f32 store (full and 37-row ragged)."""
     import os
     import subprocess
     import sys
@@ -170,6 +174,10 @@ def test_gemm_native_kernel(dev, tmp_path):
     assert_close("native gemm", out["plain"], ref.to(BF))
     assert rel_l2(out["plain"], ref) < 4e-3
     assert_close("native gemm + residual", out["resid"], OP.o_proj(a, res, b))
+    ref64 = a.double() @ b.double().t()
+    bound = K * 2.0 ** -23 * (a.double().abs() @ b.double().abs().t()) + 1e-6
+    assert bool(((out["f32"].double() - ref64).abs() <= bound).all()), "native f32 store"
+    assert bool(((out["ragged"].double() - ref64[:37]).abs() <= bound[:37]).all()), "native f32 ragged rows"
 
 
 def _layer_weights(seed=5):

@@ -49,12 +49,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 TFA_DEV bf16x8 as_bf8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-enum { EPI_STORE = 0, EPI_RESID = 1 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_F32 = 2 };
 
 struct GemmArgs {
   const uint16_t* a;      // [M, lda]
   const uint16_t* b;      // [N, ldb]
   uint16_t* c;            // [M, ldc]
+  float* cf;              // [M, ldc] (f32 store)
   int M, N, K, lda, ldb, ldc;
   const uint16_t* res;    // residual [M, ldr]
   int ldr;
@@ -93,7 +94,7 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const GemmArgs a) {
       const int j = 16 * wid + i;                 // wave-uniform
       const int row = 8 * j + (lane >> 3);        // stage row
       const int q = (lane & 7) ^ swz(row);
-      const uint16_t* src = row < kBM ? a.a + static_cast<size_t>(m0 + row) * a.lda
+      const uint16_t* src = row < kBM ? a.a + static_cast<size_t>(min(m0 + row, a.M - 1)) * a.lda
                                       : a.b + static_cast<size_t>(n0 + row - kBM) * a.ldb;
       lds_dma16(src + k0 + 8 * q, lds_offset(&smem[buf][8 * j][0]));
     }
@@ -148,9 +149,14 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const GemmArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const size_t row = m0 + wm + 32 * i + 8 * t + 4 * kg + r;
+          if (row >= static_cast<size_t>(a.M)) continue;   // rows past M read row M - 1
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int col = n0 + wn + 32 * j + n32;
+            if (EPI == EPI_F32) {
+              a.cf[row * a.ldc + col] = acc[i][j][4 * t + r];
+              continue;
+            }
             float v = round_bf(acc[i][j][4 * t + r]);
             if (EPI == EPI_RESID) v = round_bf(bf2f(a.res[row * a.ldr + col]) + v);
             a.c[row * a.ldc + col] = static_cast<uint16_t>(f2bf(v));
@@ -206,7 +212,7 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(
 
 template <int EPI>
 int launch(const GemmArgs& g, hipStream_t st, const char* name) {
-  const dim3 grid((unsigned)(g.N / kBN), (unsigned)(g.M / kBM));
+  const dim3 grid((unsigned)(g.N / kBN), (unsigned)((g.M + kBM - 1) / kBM));
   gemm_nt_kernel<EPI><<<grid, kThreads, 0, st>>>(g);
   return launched(name);
 }
@@ -214,9 +220,9 @@ int launch(const GemmArgs& g, hipStream_t st, const char* name) {
 int check_gemm(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
                int64_t ldc, const char* fn) {
   if (!a || !b || !c) return fail(TFA_ERR_NULL, "%s: null pointer argument", fn);
-  if (m < kBM || m % kBM || n < kBN || n % kBN || k < kBK || k % kBK || m > (1 << 24) || n > (1 << 24))
-    return fail(TFA_ERR_SHAPE, "%s: m %lld and n %lld must be multiples of 256, k %lld of 64", fn, (long long)m,
-                (long long)n, (long long)k);
+  if (m < 1 || n < kBN || n % kBN || k < kBK || k % kBK || m > (1 << 24) || n > (1 << 24))
+    return fail(TFA_ERR_SHAPE, "%s: m %lld must be positive, n %lld a multiple of 256, k %lld of 64", fn,
+                (long long)m, (long long)n, (long long)k);
   if (lda < k || ldb < k || ldc < n || lda % 8 || ldb % 8)
     return fail(TFA_ERR_SHAPE, "%s: leading dimensions too small or not multiples of 8", fn);
   if (!aligned16(a) || !aligned16(b)) return fail(TFA_ERR_ALIGN, "%s: a / b not 16-byte aligned", fn);
@@ -263,7 +269,7 @@ struct LtPlan {
 
 std::mutex g_lt_mu;
 std::map<int, hipblasLtHandle_t> g_lt_handles;
-std::map<std::tuple<int, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t>, LtPlan> g_lt_plans;
+std::map<std::tuple<int, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, bool>, LtPlan> g_lt_plans;
 
 bool force_native() {
   static const bool f = [] {
@@ -273,9 +279,9 @@ bool force_native() {
   return f;
 }
 
-// The plan for this device and shape (created once; ok == false when the
-// library has none, and the caller uses the native kernel).
-const LtPlan* lt_plan(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc,
+// The plan for this device, shape and output type (created once; ok == false
+// when the library has none, and the caller uses the native kernel).
+const LtPlan* lt_plan(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, bool out_f32,
                       hipblasLtHandle_t* handle) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
@@ -287,7 +293,7 @@ const LtPlan* lt_plan(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
     hit = g_lt_handles.emplace(dev, h).first;
   }
   *handle = hit->second;
-  const auto key = std::make_tuple(dev, m, n, k, lda, ldb, ldc);
+  const auto key = std::make_tuple(dev, m, n, k, lda, ldb, ldc, out_f32);
   auto it = g_lt_plans.find(key);
   if (it != g_lt_plans.end()) return &it->second;
   LtPlan p;
@@ -302,7 +308,7 @@ const LtPlan* lt_plan(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
          hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) == HIPBLAS_STATUS_SUCCESS &&
          hipblasLtMatrixLayoutCreate(&p.lw, HIP_R_16BF, k, n, ldb) == HIPBLAS_STATUS_SUCCESS &&
          hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, k, m, lda) == HIPBLAS_STATUS_SUCCESS &&
-         hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_16BF, n, m, ldc) == HIPBLAS_STATUS_SUCCESS &&
+         hipblasLtMatrixLayoutCreate(&p.lc, out_f32 ? HIP_R_32F : HIP_R_16BF, n, m, ldc) == HIPBLAS_STATUS_SUCCESS &&
          hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
          hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws)) ==
              HIPBLAS_STATUS_SUCCESS &&
@@ -320,14 +326,15 @@ const LtPlan* lt_plan(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
   return &g_lt_plans.emplace(key, p).first->second;
 }
 
-// C = bf16(A . B^T) through the library; false when there is no plan (the
-// caller then launches the native kernel), or with *status set on a failed call.
+// C = bf16(A . B^T) (or the f32 A . B^T) through the library; false when there
+// is no plan (the caller then launches the native kernel), or with *status set
+// on a failed call.
 bool lt_gemm(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
-             int64_t ldc, hipStream_t st, int* status) {
+             int64_t ldc, hipStream_t st, int* status, bool out_f32 = false) {
   *status = TFA_OK;
   if (force_native()) return false;
   hipblasLtHandle_t h = nullptr;
-  const LtPlan* p = lt_plan(m, n, k, lda, ldb, ldc, &h);
+  const LtPlan* p = lt_plan(m, n, k, lda, ldb, ldc, out_f32, &h);
   if (!p || !p->ok) return false;
   const float alpha = 1.f, beta = 0.f;
   const hipblasStatus_t r = hipblasLtMatmul(h, p->desc, &alpha, b, p->lw, a, p->la, &beta, c, p->lc, c, p->lc,
@@ -363,6 +370,16 @@ int tfa_gemm_nt(const void* a, const void* b, void* c, int64_t m, int64_t n, int
     return launch<EPI_RESID>(g, stream, "gemm_nt_residual");
   }
   return launch<EPI_STORE>(g, stream, "gemm_nt");
+}
+
+int tfa_gemm_nt_f32(const void* a, const void* b, float* c, int64_t m, int64_t n, int64_t k, int64_t lda,
+                    int64_t ldb, int64_t ldc, hipStream_t stream) {
+  int st = check_gemm(a, b, c, m, n, k, lda, ldb, ldc, "tfa_gemm_nt_f32");
+  if (st != TFA_OK) return st;
+  if (lt_gemm(a, b, c, m, n, k, lda, ldb, ldc, stream, &st, true)) return st;
+  GemmArgs g = make(a, b, nullptr, m, n, k, lda, ldb, ldc);
+  g.cf = c;
+  return launch<EPI_F32>(g, stream, "gemm_nt_f32");
 }
 
 int tfa_qkv_norm_rope(const void* hn, const void* w_qkv, void* out, int64_t n, int64_t hidden, int64_t heads,

@@ -328,6 +328,31 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float* __restr
       static_cast<uint16_t>(f2bf(round_bf(g / (1.0f + expf(-g))) * u));
 }
 
+// SwiGLU over an f32 gate|up product with interleaved columns (column 2i =
+// gate_i, 2i + 1 = up_i: the decode layout of the fused weight), four pairs a
+// thread: act[r, i] = bf16(bf16(silu(bf16 g)) * bf16 u), the arithmetic of the
+// decode step's fused epilogue. examples/qwen3_1_7b-tilelang/fast/kernels.py:210-257
+// (gemv_silu's prologue) and :547-572 (silu_mul).
+__global__ __launch_bounds__(kThreads) void swiglu_pairs_kernel(const float* __restrict__ gu, int64_t ld,
+                                                                int64_t rows, int inter,
+                                                                uint16_t* __restrict__ act) {
+  const int per_row = inter / 4;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (e >= rows * per_row) return;
+  const int64_t r = e / per_row;
+  const int i0 = static_cast<int>(e % per_row) * 4;
+  const float4* src = reinterpret_cast<const float4*>(gu + r * ld + 2 * i0);
+  const float4 a = src[0], b = src[1];
+  const float g[4] = {a.x, a.z, b.x, b.z}, u[4] = {a.y, a.w, b.y, b.w};
+  float y[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float gb = round_bf(g[j]), ub = round_bf(u[j]);
+    y[j] = round_bf(round_bf(gb / (1.0f + expf(-gb))) * ub);
+  }
+  *reinterpret_cast<uint2*>(act + r * inter + i0) = make_uint2(pack_bf(y[0], y[1]), pack_bf(y[2], y[3]));
+}
+
 // out[r, :] = table[ids[r], :], or bf16(table[ids[r], :] * scale) when `scaled`.
 // 16 bytes a thread. An id outside [0, vocab) reads row 0 and sets err = 1.
 // examples/qwen3_1_7b-tilelang/fast/kernels.py:579-588 (embed) and
@@ -548,6 +573,20 @@ int tfa_silu_mul(const float* part, int64_t ks, int64_t inter, int64_t rows, voi
   silu_mul_kernel<<<grid, kThreads, 0, stream>>>(part, (int)ks, (int)inter,
                                                   static_cast<uint16_t*>(act));
   return launched("silu_mul");
+}
+
+int tfa_swiglu_pairs(const float* gu, int64_t ld, int64_t rows, int64_t inter, void* act, hipStream_t stream) {
+  if (!gu || !act) return fail(TFA_ERR_NULL, "tfa_swiglu_pairs: null pointer argument");
+  if (inter < 4 || inter % 4 || rows < 1 || ld < 2 * inter || ld % 4)
+    return fail(TFA_ERR_SHAPE, "tfa_swiglu_pairs: inter %lld must be a positive multiple of 4, ld >= 2 inter "
+                "and a multiple of 4", (long long)inter);
+  if (!aligned16(gu) || (reinterpret_cast<uintptr_t>(act) & 7))
+    return fail(TFA_ERR_ALIGN, "tfa_swiglu_pairs: gu must be 16-byte, act 8-byte aligned");
+  const int64_t threads = rows * (inter / 4);
+  if ((threads + kThreads - 1) / kThreads > INT32_MAX) return fail(TFA_ERR_SHAPE, "tfa_swiglu_pairs: too many rows");
+  swiglu_pairs_kernel<<<(unsigned)((threads + kThreads - 1) / kThreads), kThreads, 0, stream>>>(
+      gu, ld, rows, (int)inter, static_cast<uint16_t*>(act));
+  return launched("swiglu_pairs");
 }
 
 int tfa_embed(const void* table, const int64_t* ids, int64_t vocab, int64_t hidden, int64_t rows,

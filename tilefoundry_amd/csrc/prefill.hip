@@ -1,13 +1,20 @@
-// Causal GQA prefill attention, head_dim 256, with the output gate
-// (Qwen3.5-family full-attention layer, Qwen3.8-27B shapes: 24 query heads
-// over 4 key/value heads), on bf16 MFMA.
+// Causal GQA prefill attention on bf16 MFMA, in two forms:
 //
-// One 256-thread block per (query head, 128 query rows), two blocks per CU:
-// each of the four waves (one per SIMD per block) owns 32 query rows over the
-// whole head dimension and walks the 32-key tiles up to its diagonal. Per tile:
+//   tfa_prefill_attention  head_dim 256 with the output gate (Qwen3.5-family
+//                          full-attention layer, Qwen3.8-27B shapes: 24 query
+//                          heads over 4 key/value heads), one sequence, n a
+//                          multiple of 128;
+//   tfa_causal_attention   head_dim 128 or 256, no gate, a batch of sequences
+//                          of any length n (the prompt prefill of a decode
+//                          model: Qwen3-1.7B shapes, 16 query heads over 8,
+//                          K and V read straight from the decode cache).
+//
+// One block per (query head, 128 or 256 query rows, sequence): each wave (two
+// per SIMD) owns 32 query rows over the whole head dimension and walks the
+// 32-key tiles up to its diagonal. Per tile:
 //
 //   S^T = K . Q^T     v_mfma_f32_32x32x16_bf16, M = 32 keys, N = 32 queries,
-//                     16 k-steps over D; Q^T is resident as the B operand, the
+//                     D/16 k-steps; Q^T is resident as the B operand, the
 //                     K operands stream from LDS through a ring of registers
 //                     (each read issued four k-steps ahead of its MFMA).
 //   online softmax    per query (the MFMA output column): the lane holds 16
@@ -15,24 +22,29 @@
 //                     16 -- one exchange for the row max; exp2 with the scale
 //                     folded in; the running max is only raised (and O
 //                     rescaled) when a row's max passes it by more than 2^8.
-//   O^T += V^T . P^T  M = 32 value dims (8 tiles over D), K = 16 keys per
+//   O^T += V^T . P^T  M = 32 value dims (D/32 tiles), K = 16 keys per
 //                     step; P^T is the bf16 score accumulator (its key slots
 //                     relabelled), V^T comes from ds_read_b64_tr_b16 transpose
 //                     reads of the row-major V tile, also streamed ahead.
 //
 // K and V tiles stream global -> LDS with global_load_lds_dwordx4 (no register
-// staging) through two stages: the next tile's loads go out right after the
-// tile barrier and land while this tile is computed. Each stage is its own LDS
-// object and the block barrier is a bare s_barrier after an explicit wait for
-// this wave's loads. 70 KB of LDS and at most 256 registers per wave, so two
-// blocks share a CU (two waves per SIMD): one block's softmax and barrier
-// waits run under the other's MFMAs (three stages at one block per CU measured
-// 16 % slower). The output accumulators (256 dims x 32 queries, f32) and Q stay
-// in registers.
-// Epilogue in the reference's order: out = bf16(bf16(o / l) * bf16(sigmoid(gate))).
+// staging) through two or three stages: the next tile's loads go out right
+// after the tile barrier and land while this tile is computed. Each stage is
+// its own LDS object and the block barrier is a bare s_barrier after an
+// explicit wait for this wave's loads. At D = 256: 70 KB of LDS and at most
+// 256 registers per wave for 128-row blocks, so two blocks share a CU (two
+// waves per SIMD): one block's softmax and barrier waits run under the
+// other's MFMAs. The output accumulators (D dims x 32 queries, f32) and Q stay
+// in registers. Rows past n (a ragged last tile) read row n - 1 and are not
+// stored.
+// Epilogue in the reference's order: out = bf16(bf16(o / l) * bf16(sigmoid(gate)))
+// with the gate, out = bf16(o / l) without.
 //
 // Reference (jingchangshi/TileFoundry): examples/qwen3_8_27b_prefill-tilelang/model.py:305-324
-// (Attention.attention), kernels/attention.py:1-19,313-438 (attention_ws / attention_tir).
+// (Attention.attention), kernels/attention.py:1-19,313-438 (attention_ws / attention_tir);
+// the ungated form computes the attention of examples/qwen3_1_7b-tilelang/ref_src/model.py:171-215
+// for every prompt row at once (the reference walks the prompt one decode step at a time,
+// fast/engine.py:261-263).
 #include <float.h>
 
 #include <type_traits>
@@ -44,7 +56,6 @@ using namespace tfa;
 
 namespace {
 
-constexpr int D = 256;
 constexpr int kBN = 32;             // keys per tile
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -54,26 +65,24 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 TFA_DEV bf16x8 as_bf8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 struct FlashArgs {
-  const uint16_t* q;     // element (n, h, d) at q + n*q_rs + h*q_hs + d
-  const uint16_t* k;     // (n, g, d) at k + n*k_rs + g*k_hs + d
+  const uint16_t* q;     // element (b, n, h, d) at q + b*q_bs + n*q_rs + h*q_hs + d
+  const uint16_t* k;     // (b, n, g, d) at k + b*k_bs + n*k_rs + g*k_hs + d
   const uint16_t* v;
-  const uint16_t* gate;  // like q
-  uint16_t* out;         // (n, h*256 + d) at out + n*o_rs + h*256 + d
+  const uint16_t* gate;  // like q (gated form only)
+  uint16_t* out;         // (b, n, h*D + d) at out + b*o_bs + n*o_rs + h*D + d
+  int64_t q_bs, k_bs, v_bs, g_bs, o_bs;
   int q_rs, q_hs, k_rs, k_hs, v_rs, v_hs, g_rs, g_hs, o_rs;
-  int N, HQ, HKV;
+  int N, HQ, HKV;        // N query rows (= keys) per sequence; any N >= 1
   int xcd_heads;         // heads per XCD in the work order (0: plain order)
   float scale_log2;      // head_dim^-1/2 * log2(e)
 };
 
-// LDS tiles hold one key per row. K rows are padded to 528 bytes (+4 banks per
+// LDS tiles hold one key per row. K rows are padded by 16 bytes (+4 banks per
 // row): the K operand read (16 rows, one 16-byte chunk per half-wave) is
-// conflict-free. V rows are padded to 576 bytes (+16 banks per row): the
-// transpose reads (4 rows x 64 bytes per half-wave) are conflict-free. Every
-// operand address is one per-lane base plus an immediate offset.
-constexpr int kKPitch = D + 8;    // elements
-constexpr int kVPitch = D + 32;
-constexpr int kDT = D / 32;       // 32-dim output tiles
-constexpr int kST = D / 16;       // 16-dim score k-steps
+// conflict-free. V rows are padded by 64 bytes (+16 banks per row): the
+// transpose reads (4 rows x 64 bytes per half-wave) are conflict-free. Both
+// hold for 256- and 512-byte rows. Every operand address is one per-lane base
+// plus an immediate offset.
 constexpr int kKPF = 4;           // K operand reads in flight ahead of the score MFMAs
 constexpr int kVPF = 3;           // V^T operand pairs in flight ahead of the output MFMAs
 // sched_group_barrier instruction classes
@@ -93,8 +102,9 @@ using IC = std::integral_constant<int, N>;
 
 // W waves of 32 query rows per block. W = 8 (256 rows, 3 stages, one block per
 // CU) halves the K/V bytes moved into LDS per FLOP against W = 4 (128 rows, 2
-// stages, two blocks per CU); both keep two waves per SIMD.
-template <int W>
+// stages, two blocks per CU); both keep two waves per SIMD. D is the head
+// dimension (128 or 256); GATE applies the sigmoid output gate.
+template <int W, int D, bool GATE>
 __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_prefill_kernel(const FlashArgs a) {
   constexpr int QT = 1;       // 32-row query tiles per wave
@@ -104,6 +114,11 @@ void flash_prefill_kernel(const FlashArgs a) {
   constexpr int kRowsPerWave = kBN / W;        // K and V rows each wave moves per tile
   constexpr int kTileVm = 2 * kRowsPerWave;    // DMA instructions per wave per tile
   constexpr int kWaitStep = waitcnt_vm(kStages == 3 ? kTileVm : 0);
+  constexpr int kKPitch = D + 8;               // elements
+  constexpr int kVPitch = D + 32;
+  constexpr int kDT = D / 32;                  // 32-dim output tiles
+  constexpr int kST = D / 16;                  // 16-dim score k-steps
+  constexpr int kRowLanes = D / 8;             // lanes moving one K or V row (16 bytes each)
   // one LDS object per ring stage, indexed only by compile-time stage numbers
   __shared__ __attribute__((aligned(16))) uint16_t ks0[kBN][kKPitch];
   __shared__ __attribute__((aligned(16))) uint16_t ks1[kBN][kKPitch];
@@ -126,12 +141,13 @@ void flash_prefill_kernel(const FlashArgs a) {
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int n32 = lane & 31;
   const int kg = lane >> 5;
+  const int N = a.N;
   // Work order. Consecutive block ids are dispatched round-robin over the 8
   // XCDs (each with its own L2); XCD x takes a run of consecutive heads --
   // heads of one key/value group when the counts divide evenly -- so each L2
   // holds one group's K and V, and within an XCD the longest query tiles go
-  // first.
-  const int nqt = a.N / kBM;
+  // first. blockIdx.y is the sequence.
+  const int nqt = (N + kBM - 1) / kBM;
   int h, qt;
   if (a.xcd_heads > 0) {
     const int x = blockIdx.x & 7, slot = blockIdx.x >> 3;
@@ -141,38 +157,45 @@ void flash_prefill_kernel(const FlashArgs a) {
     h = blockIdx.x % a.HQ;
     qt = nqt - 1 - blockIdx.x / a.HQ;
   }
+  const int b = blockIdx.y;
   const int g = h / (a.HQ / a.HKV);
+  const uint16_t* kseq = a.k + b * a.k_bs + g * a.k_hs;
+  const uint16_t* vseq = a.v + b * a.v_bs + g * a.v_hs;
   const int q0 = qt * kBM + wid * kWM;          // the wave's first query row
-  const int ntiles = (qt + 1) * kBM / kBN;      // key tiles the block walks
-  const int my_last = (q0 + kWM - 1) / kBN;     // the wave's last tile with a visible key
+  // key tiles the block walks: up to its last row, and no tile wholly past N
+  const int kend = min((qt + 1) * kBM, N);
+  const int ntiles = (kend + kBN - 1) / kBN;
+  const int my_last = min((q0 + kWM - 1) / kBN, ntiles - 1);   // the wave's last tile with a visible key
 
-  // direct global -> LDS tile loads, one 512-byte row per instruction (lanes
-  // 0..31): wave w moves rows R w .. R w + R - 1 of K and of V (R = 32 / W).
-  // Every step issues exactly one tile's loads (past the last tile it reloads
-  // the last tile into a free stage, where nothing reads it), so the number of
-  // loads in flight behind tile kt is constant and so is every wait count.
-  auto load_tile = [&](int kt, auto b) __attribute__((always_inline)) {
+  // direct global -> LDS tile loads, one K or V row per instruction (lanes
+  // 0 .. D/8-1): wave w moves rows R w .. R w + R - 1 of K and of V (R = 32 / W).
+  // Rows past N repeat row N - 1 (only rows past N see them, and those rows
+  // are not stored). Every step issues exactly one tile's loads (past the last
+  // tile it reloads the last tile into a free stage, where nothing reads it),
+  // so the number of loads in flight behind tile kt is constant and so is
+  // every wait count.
+  auto load_tile = [&](int kt, auto bs) __attribute__((always_inline)) {
     kt = kt < ntiles ? kt : ntiles - 1;
-    const size_t r0 = static_cast<size_t>(kt) * kBN + kRowsPerWave * wid;
-    uint16_t(*kb)[kKPitch] = kbuf(b);
-    uint16_t(*vb)[kVPitch] = vbuf(b);
-    if (lane < 32) {
+    const int r0 = kt * kBN + kRowsPerWave * wid;
+    uint16_t(*kb)[kKPitch] = kbuf(bs);
+    uint16_t(*vb)[kVPitch] = vbuf(bs);
+    if (lane < kRowLanes) {
 #pragma unroll
       for (int i = 0; i < kRowsPerWave; ++i) {
-        const uint16_t* krow = a.k + (r0 + i) * a.k_rs + g * a.k_hs;
-        const uint16_t* vrow = a.v + (r0 + i) * a.v_rs + g * a.v_hs;
-        lds_dma16(krow + 8 * n32, lds_offset(&kb[kRowsPerWave * wid + i][0]));
-        lds_dma16(vrow + 8 * n32, lds_offset(&vb[kRowsPerWave * wid + i][0]));
+        const size_t r = static_cast<size_t>(min(r0 + i, N - 1));
+        lds_dma16(kseq + r * a.k_rs + 8 * lane, lds_offset(&kb[kRowsPerWave * wid + i][0]));
+        lds_dma16(vseq + r * a.v_rs + 8 * lane, lds_offset(&vb[kRowsPerWave * wid + i][0]));
       }
     }
   };
 
   // Q^T operands, resident: q-tile t, lane (query q0 + 32t + n32, k-group kg)
-  // holds Q[.][16 st + 8 kg .. +7]
+  // holds Q[.][16 st + 8 kg .. +7]; rows past N read row N - 1
   uint4 qop[QT][kST];
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
-    const uint16_t* qrow = a.q + static_cast<size_t>(q0 + 32 * t + n32) * a.q_rs + h * a.q_hs + 8 * kg;
+    const size_t qn = static_cast<size_t>(min(q0 + 32 * t + n32, N - 1));
+    const uint16_t* qrow = a.q + b * a.q_bs + qn * a.q_rs + h * a.q_hs + 8 * kg;
 #pragma unroll
     for (int st = 0; st < kST; ++st) qop[t][st] = ld16(qrow + 16 * st);
   }
@@ -201,18 +224,18 @@ void flash_prefill_kernel(const FlashArgs a) {
 
   const int L = lane & 15;
   const int half16 = (lane >> 4) & 1;
-  // One key tile in ring stage `b`. The block barrier is a bare s_barrier
+  // One key tile in ring stage `bs`. The block barrier is a bare s_barrier
   // between compiler fences: each wave first waits for its own loads of tile
   // kt (the only ones in flight), and its reads of the stage being refilled --
   // tile kt - 1's -- were consumed by MFMAs of the previous step before it
   // arrives.
-  auto step = [&](int kt, auto b) __attribute__((always_inline)) {
-    constexpr int B = decltype(b)::value;
+  auto step = [&](int kt, auto bs) __attribute__((always_inline)) {
+    constexpr int B = decltype(bs)::value;
     __builtin_amdgcn_s_waitcnt(kWaitStep);   // tile kt landed; with three stages tile kt + 1 may fly
     block_barrier();
     load_tile(kt + kStages - 1, IC<(B + kStages - 1) % kStages>{});   // into the stage of tile kt - 1
-    uint16_t(*kb)[kKPitch] = kbuf(b);
-    uint16_t(*vb)[kVPitch] = vbuf(b);
+    uint16_t(*kb)[kKPitch] = kbuf(bs);
+    uint16_t(*vb)[kVPitch] = vbuf(bs);
 
     if (kt <= my_last) {   // wave-uniform: later tiles hold no key this wave sees
       // S^T = K . Q^T: element e = 4j + r is key 32 kt + 8j + 4kg + r,
@@ -328,25 +351,49 @@ void flash_prefill_kernel(const FlashArgs a) {
   for (int t = 0; t < QT; ++t) {
     const float l_tot = l_run[t] + __shfl_xor(l_run[t], 32, kWave);
     const float inv = 1.0f / l_tot;
-    const size_t qn = static_cast<size_t>(q0 + 32 * t + n32);
-    const uint16_t* grow = a.gate + qn * a.g_rs + h * a.g_hs;
-    uint16_t* orow = a.out + qn * a.o_rs + h * D;
+    const int qn = q0 + 32 * t + n32;
+    if (qn >= N) continue;
+    uint16_t* orow = a.out + b * a.o_bs + static_cast<size_t>(qn) * a.o_rs + h * D;
+    const uint16_t* grow = GATE ? a.gate + b * a.g_bs + static_cast<size_t>(qn) * a.g_rs + h * a.g_hs : nullptr;
 #pragma unroll
     for (int dt = 0; dt < kDT; ++dt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int d0 = 32 * dt + 8 * j + 4 * kg;
-        const uint2 gv = *reinterpret_cast<const uint2*>(grow + d0);
-        const float gx[4] = {lo_bf(gv.x), hi_bf(gv.x), lo_bf(gv.y), hi_bf(gv.y)};
         float y[4];
+        if constexpr (GATE) {
+          // out = bf16(bf16(o / l) * bf16(sigmoid(gate)))
+          const uint2 gv = *reinterpret_cast<const uint2*>(grow + d0);
+          const float gx[4] = {lo_bf(gv.x), hi_bf(gv.x), lo_bf(gv.y), hi_bf(gv.y)};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float sg = round_bf(__builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gx[r] * 1.4426950408889634f)));
-          y[r] = round_bf(round_bf(o[dt][t][4 * j + r] * inv) * sg);
+          for (int r = 0; r < 4; ++r) {
+            const float sg = round_bf(__builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gx[r] * 1.4426950408889634f)));
+            y[r] = round_bf(round_bf(o[dt][t][4 * j + r] * inv) * sg);
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[r] = round_bf(o[dt][t][4 * j + r] * inv);
         }
         *reinterpret_cast<uint2*>(orow + d0) = make_uint2(pack_bf(y[0], y[1]), pack_bf(y[2], y[3]));
       }
   }
+}
+
+// XCD-grouped order when every XCD gets whole heads of a single group
+int xcd_heads(int64_t heads, int64_t kv_heads) {
+  const int64_t per = heads / 8, group = heads / kv_heads;
+  return (heads % 8 == 0 && per >= 1 && (group % per == 0 || per % group == 0)) ? (int)per : 0;
+}
+
+// 256-row blocks when they still give every CU a block, else 128-row blocks.
+template <int D, bool GATE>
+int launch_flash(const FlashArgs& a, int64_t batch, hipStream_t stream, const char* name) {
+  const int64_t t256 = (a.N + 255) / 256, t128 = (a.N + 127) / 128;
+  if (a.HQ * t256 * batch >= 256)
+    flash_prefill_kernel<8, D, GATE><<<dim3((unsigned)(a.HQ * t256), (unsigned)batch), 8 * kWave, 0, stream>>>(a);
+  else
+    flash_prefill_kernel<4, D, GATE><<<dim3((unsigned)(a.HQ * t128), (unsigned)batch), 4 * kWave, 0, stream>>>(a);
+  return launched(name);
 }
 
 }  // namespace
@@ -362,7 +409,7 @@ int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void*
   TFA_NONNULL(v);
   TFA_NONNULL(gate);
   TFA_NONNULL(out);
-  TFA_REQUIRE(head_dim == D, TFA_ERR_SHAPE, "tfa_prefill_attention: head_dim %lld, only 256 supported", (long long)head_dim);
+  TFA_REQUIRE(head_dim == 256, TFA_ERR_SHAPE, "tfa_prefill_attention: head_dim %lld, only 256 supported", (long long)head_dim);
   TFA_REQUIRE(n >= 128 && n % 128 == 0 && n <= (1 << 20), TFA_ERR_SHAPE,
               "tfa_prefill_attention: n %lld must be a positive multiple of %d", (long long)n, 128);
   TFA_REQUIRE(kv_heads >= 1 && heads >= kv_heads && heads % kv_heads == 0 && heads <= 65535, TFA_ERR_SHAPE,
@@ -390,15 +437,54 @@ int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void*
   a.HQ = (int)heads;
   a.HKV = (int)kv_heads;
   a.scale_log2 = scale * 1.4426950408889634f;
-  // XCD-grouped order when every XCD gets whole heads of a single group
-  const int64_t per = heads / 8, group = heads / kv_heads;
-  a.xcd_heads = (heads % 8 == 0 && per >= 1 && (group % per == 0 || per % group == 0)) ? (int)per : 0;
-  // 256-row blocks when they still give every CU a block, else 128-row blocks
-  if (n % 256 == 0 && heads * (n / 256) >= 256)
-    flash_prefill_kernel<8><<<(unsigned)(heads * (n / 256)), 8 * kWave, 0, stream>>>(a);
-  else
-    flash_prefill_kernel<4><<<(unsigned)(heads * (n / 128)), 4 * kWave, 0, stream>>>(a);
-  return launched("flash_prefill");
+  a.xcd_heads = xcd_heads(heads, kv_heads);
+  return launch_flash<256, true>(a, 1, stream, "flash_prefill");
+}
+
+int tfa_causal_attention(const void* q, int64_t q_rs, int64_t q_hs, int64_t q_bs, const void* k, int64_t k_rs,
+                         int64_t k_hs, int64_t k_bs, const void* v, int64_t v_rs, int64_t v_hs, int64_t v_bs,
+                         void* out, int64_t o_rs, int64_t o_bs, int64_t batch, int64_t n, int64_t heads,
+                         int64_t kv_heads, int64_t head_dim, float scale, hipStream_t stream) {
+  TFA_NONNULL(q);
+  TFA_NONNULL(k);
+  TFA_NONNULL(v);
+  TFA_NONNULL(out);
+  TFA_REQUIRE(head_dim == 128 || head_dim == 256, TFA_ERR_SHAPE,
+              "tfa_causal_attention: head_dim %lld not in {128, 256}", (long long)head_dim);
+  TFA_REQUIRE(n >= 1 && n <= (1 << 20), TFA_ERR_SHAPE, "tfa_causal_attention: n %lld not in [1, 2^20]", (long long)n);
+  TFA_REQUIRE(batch >= 1 && batch <= 65535, TFA_ERR_SHAPE, "tfa_causal_attention: batch %lld out of range",
+              (long long)batch);
+  TFA_REQUIRE(kv_heads >= 1 && heads >= kv_heads && heads % kv_heads == 0 && heads <= 65535, TFA_ERR_SHAPE,
+              "tfa_causal_attention: heads %lld not a multiple of kv_heads %lld", (long long)heads, (long long)kv_heads);
+  const int64_t lim = int64_t(1) << 31;
+  TFA_REQUIRE(q_rs >= 0 && q_rs < lim && k_rs >= 0 && k_rs < lim && v_rs >= 0 && v_rs < lim && o_rs >= 0 &&
+                  o_rs < lim && q_hs >= 0 && q_hs < lim && k_hs >= 0 && k_hs < lim && v_hs >= 0 && v_hs < lim &&
+                  q_bs >= 0 && k_bs >= 0 && v_bs >= 0 && o_bs >= 0,
+              TFA_ERR_SHAPE, "tfa_causal_attention: strides must be non-negative, row / head strides below 2^31");
+  TFA_REQUIRE(q_rs % 8 == 0 && q_hs % 8 == 0 && q_bs % 8 == 0 && k_rs % 8 == 0 && k_hs % 8 == 0 && k_bs % 8 == 0 &&
+                  v_rs % 8 == 0 && v_hs % 8 == 0 && v_bs % 8 == 0 && o_rs % 4 == 0 && o_bs % 4 == 0,
+              TFA_ERR_ALIGN, "tfa_causal_attention: strides must keep 16-byte (q, k, v) and 8-byte (out) alignment");
+  TFA_ALIGN16(q);
+  TFA_ALIGN16(k);
+  TFA_ALIGN16(v);
+  TFA_REQUIRE((reinterpret_cast<uintptr_t>(out) & 7) == 0, TFA_ERR_ALIGN, "tfa_causal_attention: out must be 8-byte aligned");
+  FlashArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.out = static_cast<uint16_t*>(out);
+  a.q_bs = q_bs; a.k_bs = k_bs; a.v_bs = v_bs; a.o_bs = o_bs;
+  a.q_rs = (int)q_rs; a.q_hs = (int)q_hs;
+  a.k_rs = (int)k_rs; a.k_hs = (int)k_hs;
+  a.v_rs = (int)v_rs; a.v_hs = (int)v_hs;
+  a.o_rs = (int)o_rs;
+  a.N = (int)n;
+  a.HQ = (int)heads;
+  a.HKV = (int)kv_heads;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.xcd_heads = xcd_heads(heads, kv_heads);
+  if (head_dim == 128) return launch_flash<128, false>(a, batch, stream, "causal_attention");
+  return launch_flash<256, false>(a, batch, stream, "causal_attention");
 }
 
 }  // extern "C"

@@ -537,6 +537,81 @@ void qkv_norm_rope(const Tensor& hn, const Tensor& w_qkv, const Tensor& out, int
                                  64, stream_of(out)));
 }
 
+// ------------------------------------------- prompt prefill (decode model)
+// a [m, k], b [n, k] bf16 (row strides from the tensors); c [m, n] f32
+void gemm_nt_f32(const Tensor& a, const Tensor& b, const Tensor& c) {
+  auto mat = [](const Tensor& t, const char* name, at::ScalarType dt) {
+    if (!t.defined() || !t.is_cuda() || t.scalar_type() != dt || t.dim() != 2 || t.stride(1) != 1)
+      bad(std::string(name) + ": expected a GPU matrix of the right dtype with unit inner stride");
+  };
+  mat(a, "a", BF);
+  mat(b, "b", BF);
+  mat(c, "c", F32);
+  const int64_t M = a.size(0), K = a.size(1), N = b.size(0);
+  if (b.size(1) != K || c.size(0) != M || c.size(1) != N) bad("gemm_nt_f32: shapes disagree");
+  raise_status(tfa_gemm_nt_f32(a.data_ptr(), b.data_ptr(), c.data_ptr<float>(), M, N, K, a.stride(0), b.stride(0),
+                               c.stride(0), stream_of(c)));
+}
+
+// gu f32 (rows, 2 * inter) with interleaved gate / up columns; act bf16 (rows, inter)
+void swiglu_pairs(const Tensor& gu, const Tensor& act) {
+  if (!gu.defined() || !gu.is_cuda() || gu.scalar_type() != F32 || gu.dim() != 2 || gu.stride(1) != 1)
+    bad("gu: expected an f32 (rows, 2 * inter) GPU matrix with unit inner stride");
+  const int64_t R = gu.size(0), I = gu.size(1) / 2;
+  need(act, "act", BF, R * I);
+  if (gu.size(1) != 2 * I) bad("gu: odd column count");
+  raise_status(tfa_swiglu_pairs(gu.data_ptr<float>(), gu.stride(0), R, I, act.data_ptr(), stream_of(gu)));
+}
+
+// qkv f32 (batch * n, ldq); caches (batch, cap, hkv * 128) or (cap, hkv * 128);
+// q_out bf16 (batch * n, hq * 128).
+void prefill_qk_rope(const Tensor& qkv, const Tensor& gamma_q, const Tensor& gamma_k, double eps, const Tensor& cos,
+                     const Tensor& sin, int64_t batch, int64_t n, int64_t pos0, const Tensor& k_cache,
+                     const Tensor& v_cache, const Tensor& q_out, int64_t hq, int64_t hkv) {
+  need(qkv, "qkv", F32);
+  if (qkv.dim() != 2 || qkv.size(0) != batch * n) bad("qkv: expected (batch * n, columns)");
+  need(gamma_q, "gamma_q", BF, 128);
+  need(gamma_k, "gamma_k", BF, 128);
+  need(cos, "cos", BF);
+  need(sin, "sin", BF, cos.numel());
+  if (cos.dim() != 2 || cos.size(1) != 128) bad("cos / sin: expected (rows, 128)");
+  need(k_cache, "k_cache", BF);
+  need(v_cache, "v_cache", BF, k_cache.numel());
+  const int64_t KN = hkv * 128;
+  if (batch < 1 || KN < 1 || k_cache.size(-1) != KN || k_cache.numel() % (batch * KN) != 0)
+    bad("k_cache / v_cache: expected (batch, cap, kv_heads * 128)");
+  need(q_out, "q_out", BF, batch * n * hq * 128);
+  raise_status(tfa_prefill_qk_rope(qkv.data_ptr<float>(), qkv.size(1), gamma_q.data_ptr(), gamma_k.data_ptr(),
+                                   (float)eps, cos.data_ptr(), sin.data_ptr(), cos.size(0), batch, n, pos0,
+                                   k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() / (batch * KN),
+                                   q_out.data_ptr(), hq, hkv, 128, stream_of(qkv)));
+}
+
+// q (batch, n, heads, d), k / v (batch, >= n, kv_heads, d) views with unit inner
+// stride (the decode cache viewed in place); out (batch, n, heads * d) with a
+// unit inner stride.
+void causal_attention(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& out, double scale) {
+  auto view4 = [](const Tensor& t, const char* name) {
+    if (!t.defined() || !t.is_cuda()) bad(std::string(name) + ": must be a GPU tensor");
+    if (t.scalar_type() != BF) bad(std::string(name) + ": expected bfloat16");
+    if (t.dim() != 4 || t.stride(3) != 1) bad(std::string(name) + ": expected a (batch, n, heads, d) view with unit inner stride");
+  };
+  view4(q, "q");
+  view4(k, "k");
+  view4(v, "v");
+  const int64_t B = q.size(0), N = q.size(1), HQ = q.size(2), Dh = q.size(3), HKV = k.size(2);
+  if (k.size(0) != B || v.size(0) != B || k.size(1) < N || v.size(1) < N || v.size(2) != HKV || k.size(3) != Dh ||
+      v.size(3) != Dh)
+    bad("causal_attention: q (batch, n, heads, d) and k/v (batch, >= n, kv_heads, d) shapes disagree");
+  if (!out.defined() || !out.is_cuda() || out.scalar_type() != BF || out.dim() != 3 || out.size(0) != B ||
+      out.size(1) != N || out.size(2) != HQ * Dh || out.stride(2) != 1)
+    bad("out: expected a bf16 (batch, n, heads * d) GPU tensor with unit inner stride");
+  raise_status(tfa_causal_attention(q.data_ptr(), q.stride(1), q.stride(2), q.stride(0), k.data_ptr(), k.stride(1),
+                                    k.stride(2), k.stride(0), v.data_ptr(), v.stride(1), v.stride(2), v.stride(0),
+                                    out.data_ptr(), out.stride(1), out.stride(0), B, N, HQ, HKV, Dh, (float)scale,
+                                    stream_of(out)));
+}
+
 // ------------------------------------------------- per-op decode entries
 void rmsnorm_gemv_gate_up(const Tensor& h, const Tensor& gamma, double eps, const Tensor& w_gate,
                           const Tensor& w_up, const Tensor& act) {
@@ -691,6 +766,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("prefill_attention", &prefill_attention);
   m.def("gemm_nt", &gemm_nt);
   m.def("qkv_norm_rope", &qkv_norm_rope);
+  m.def("gemm_nt_f32", &gemm_nt_f32);
+  m.def("swiglu_pairs", &swiglu_pairs);
+  m.def("prefill_qk_rope", &prefill_qk_rope);
+  m.def("causal_attention", &causal_attention);
   m.def("rmsnorm_gemv_gate_up", &rmsnorm_gemv_gate_up);
   m.def("lm_head_gemv", &lm_head_gemv);
   m.def("silu_mul", &silu_mul);

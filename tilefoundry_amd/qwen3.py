@@ -155,6 +155,61 @@ def pack_weights(cfg: Qwen3Config, wts: dict, dev):
     return embed, gamma_final, layers
 
 
+def prefill_caches(cfg: Qwen3Config, embed, layers, kc, vc, cos, sin, ids: torch.Tensor, err):
+    """Every layer over whole prompts at once, writing their K/V cache rows.
+
+    ``ids`` int64 ``[B, n]`` on the device: sequence b's tokens at positions
+    0..n-1; ``kc`` / ``vc`` per layer ``[B, cap, kv_heads*head_dim]`` (or
+    ``[cap, .]`` for B = 1). Afterwards cache rows 0..n-1 hold what n decode
+    steps over the same tokens would have written, computed with the same
+    rounding points: every projection is an f32 GEMM over all B*n rows
+    (``gemm_nt_f32``) whose consumer lands it in bf16 as the decode step lands
+    its split-K partials -- ``prefill_qk_rope`` (per-head norm + RoPE + cache
+    write), ``rows_norm`` (residual add + norm), ``swiglu_pairs`` -- and the
+    attention of every row is one causal launch over the cache
+    (``causal_attention``). Only the summation order of the products differs
+    from the walk. 11 launches per layer, none per token; the last layer stops
+    after its attention (nothing downstream of it reaches a cache).
+
+    This replaces the reference's token-by-token prompt walk
+    (examples/qwen3_1_7b-tilelang/fast/engine.py:261-263); it computes
+    ref_src/model.py:235-265 (decoder_layer) for every prompt row.
+    """
+    H, HQ, HKV, D, I = cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.inter
+    B, n = ids.shape
+    R = B * n
+    dev = ids.device
+    f32 = torch.float32
+
+    def e(*shape, dtype=BF16):
+        return torch.empty(*shape, device=dev, dtype=dtype)
+
+    h, h1, xn = e(R, H), e(R, H), e(R, H)
+    qkv = e(R, cfg.qkv_rows, dtype=f32)
+    q = e(R, HQ * D)
+    attn = e(R, HQ * D)
+    o = e(R, H, dtype=f32)
+    gu = e(R, 2 * I, dtype=f32)
+    act = e(R, I)
+    d = e(R, H, dtype=f32)
+    C.rows_norm(embed, ids.reshape(-1), None, None, h, layers[0]["gamma_in"], xn, cfg.eps, err)
+    for i, w in enumerate(layers):
+        k4 = kc[i].view(B, -1, HKV, D)
+        v4 = vc[i].view(B, -1, HKV, D)
+        C.gemm_nt_f32(xn, w["w_qkv"], qkv)
+        C.prefill_qk_rope(qkv, w["gamma_q"], w["gamma_k"], cfg.eps, cos, sin, B, n, 0,
+                          k4.view(B, -1, HKV * D), v4.view(B, -1, HKV * D), q, HQ, HKV)
+        if i + 1 == len(layers):
+            break
+        C.causal_attention(q.view(B, n, HQ, D), k4, v4, attn.view(B, n, HQ * D), cfg.scale)
+        C.gemm_nt_f32(attn, w["w_o"], o)
+        C.rows_norm(None, None, h, o, h1, w["gamma_post"], xn, cfg.eps, err)
+        C.gemm_nt_f32(xn, w["w_gu"], gu)
+        C.swiglu_pairs(gu, act)
+        C.gemm_nt_f32(act, w["w_down"], d)
+        C.rows_norm(None, None, h1, d, h, layers[i + 1]["gamma_in"], xn, cfg.eps, err)
+
+
 @dataclass(frozen=True)
 class Generated:
     """A continuation and the timing of the part that produced it
@@ -182,10 +237,11 @@ class Engine:
 
     def __init__(self, cfg: Qwen3Config = QWEN3_1_7B, *, device="cuda:0", max_new: int = 2048,
                  prompt_room: int = 512, weights: dict | None = None, seed: int = 0,
-                 split: int = 64, capture: bool = True):
+                 split: int = 64, capture: bool = True, prompt_prefill: bool = False):
         self.cfg = cfg
         self.device = torch.device(device)
         self.split = split
+        self.prompt_prefill = prompt_prefill
         self.nsteps = max_new + prompt_room
         self.cap = ((self.nsteps + split - 1) // split) * split
         self.ns = self.cap // split
@@ -303,13 +359,31 @@ class Engine:
         if code:
             raise DeviceIndexError(f"a decode kernel found an index out of range (code {code})")
 
+    def _walk_or_prefill(self, rows: list[list[int]]):
+        """Consume all but the last prompt token of every sequence: one decode
+        step per token (the reference's walk), or with ``prompt_prefill`` one
+        pass of every layer over all of them (``prefill_caches``), after which
+        the position and the next input are set as the walk would leave them."""
+        n = len(rows[0]) - 1
+        if not self.prompt_prefill or n < 1:
+            for _ in range(n):
+                self._run_step()
+            return
+        ids = torch.tensor([r[:n] for r in rows], dtype=torch.int64, device=self.device)
+        prefill_caches(self.cfg, self.embed, self.layers, self.kc, self.vc, self.cos, self.sin, ids,
+                       self.err)
+        self.pos.fill_(n)
+        self.ids.copy_(torch.tensor([r[n] for r in rows], dtype=torch.int64, device=self.device))
+
     # ------------------------------------------------------------ generation
     def generate(self, prompt_ids: list[int], max_new: int) -> Generated:
-        """Walk ``prompt_ids``, then continue for ``max_new`` tokens.
+        """Walk ``prompt_ids`` (or prefill them, with ``prompt_prefill``), then
+        continue for ``max_new`` tokens.
 
         Timing covers exactly the steps that produce the continuation: the step at
         ``pos = len(prompt) - 1`` is the first whose pick is kept
-        (examples/qwen3_1_7b-tilelang/fast/engine.py:239-271).
+        (examples/qwen3_1_7b-tilelang/fast/engine.py:239-271); ``prefill_seconds``
+        is the walk (or the prefill) before it.
         """
         pl = len(prompt_ids)
         if pl < 1:
@@ -319,8 +393,7 @@ class Engine:
         self._load(list(prompt_ids), pl)
         torch.cuda.synchronize(self.device)
         t0 = perf_counter()
-        for _ in range(pl - 1):
-            self._run_step()
+        self._walk_or_prefill([list(prompt_ids)])
         torch.cuda.synchronize(self.device)
         t1 = perf_counter()
         for _ in range(max_new):
@@ -386,13 +459,14 @@ class BatchEngine:
     def __init__(self, cfg: Qwen3Config = QWEN3_1_7B, *, batch: int = 32, device="cuda:0",
                  max_new: int = 2048, prompt_room: int = 512, weights: dict | None = None,
                  seed: int = 0, split: int = 128, ks_qkv: int = 2, ks_o: int = 4, ks_down: int = 4,
-                 capture: bool = True):
+                 capture: bool = True, prompt_prefill: bool = False):
         if not 1 <= batch <= self.MAX_BATCH:
             raise ValueError(f"batch {batch} not in [1, {self.MAX_BATCH}]")
         self.cfg = cfg
         self.batch = batch
         self.device = torch.device(device)
         self.split = split
+        self.prompt_prefill = prompt_prefill
         self.ks = {"qkv": ks_qkv, "o": ks_o, "down": ks_down}
         self.nsteps = max_new + prompt_room
         self.cap = ((self.nsteps + split - 1) // split) * split
@@ -471,6 +545,7 @@ class BatchEngine:
 
     _capture = Engine._capture
     _run_step = Engine._run_step
+    _walk_or_prefill = Engine._walk_or_prefill
 
     def _capture_inputs(self):
         return [[0]] * self.batch, 1
@@ -497,8 +572,8 @@ class BatchEngine:
         self.ids.copy_(torch.tensor([r[0] for r in rows], dtype=torch.int64, device=self.device))
 
     def generate(self, prompts: list[list[int]], max_new: int) -> Generated:
-        """Walk every prompt, then continue each for ``max_new`` tokens; timing
-        covers the continuation steps only (all sequences together)."""
+        """Walk (or prefill) every prompt, then continue each for ``max_new``
+        tokens; timing covers the continuation steps only (all sequences together)."""
         if not prompts or not prompts[0]:
             raise ValueError("decode needs prompts of at least one token")
         pl = len(prompts[0])
@@ -507,8 +582,7 @@ class BatchEngine:
         self._load([list(p) for p in prompts], pl)
         torch.cuda.synchronize(self.device)
         t0 = perf_counter()
-        for _ in range(pl - 1):
-            self._run_step()
+        self._walk_or_prefill([list(p) for p in prompts])
         torch.cuda.synchronize(self.device)
         t1 = perf_counter()
         for _ in range(max_new):
