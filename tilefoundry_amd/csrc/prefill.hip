@@ -386,6 +386,9 @@ int xcd_heads(int64_t heads, int64_t kv_heads) {
 }
 
 // 256-row blocks when they still give every CU a block, else 128-row blocks.
+// (64- and 32-row blocks were measured slower on short prompts: a block walks
+// its key tiles one after another with one tile of look-ahead, so thinner
+// blocks only add more serial walks of the same latency.)
 template <int D, bool GATE>
 int launch_flash(const FlashArgs& a, int64_t batch, hipStream_t stream, const char* name) {
   const int64_t t256 = (a.N + 255) / 256, t128 = (a.N + 127) / 128;

@@ -3,7 +3,7 @@
     python -m tilefoundry_amd.rocprof_summary stats <dir>   # *kernel_stats.csv -> stats_summary.json
     python -m tilefoundry_amd.rocprof_summary pmc <dir>     # *counter_collection.csv -> pmc_summary.json
     python -m tilefoundry_amd.rocprof_summary traffic <fetch_dir> <write_dir> <kernel substring>
-    python -m tilefoundry_amd.rocprof_summary table <dir> [rows]  # stats_summary.json -> markdown
+    python -m tilefoundry_amd.rocprof_summary table <dir> [rows] [regex]  # stats_summary.json -> markdown
 
 ``stats`` keeps per-kernel call counts and durations and deletes the raw kernel
 trace (it can exceed what a run may copy back). ``pmc`` averages each counter
@@ -13,10 +13,13 @@ same counter reads for ``copy_stream`` -- a copy of known size issued through
 the same 16-byte load / store path -- and prints the JSON bench.py reads from
 profiles/roofline_traffic.json.
 """
+from __future__ import annotations
+
 import csv
 import glob
 import json
 import os
+import re
 import sys
 from collections import defaultdict
 
@@ -67,9 +70,12 @@ def traffic(fetch_dir: str, write_dir: str, needle: str, copy_bytes: int = 64 <<
             "traffic_bytes_per_launch": int(round(f_k * kib * ff + w_k * kib * wf))}
 
 
-def table(d: str, rows: int = 16) -> str:
-    """The busiest kernels of a ``stats`` summary as a markdown table."""
+def table(d: str, rows: int = 16, match: str | None = None) -> str:
+    """The busiest kernels of a ``stats`` summary (those whose name matches the
+    regular expression ``match``, when given) as a markdown table."""
     data = json.load(open(os.path.join(d, "stats_summary.json")))
+    if match:
+        data = [r for r in data if re.search(match, r["name"])]
     lines = ["| kernel | calls | avg us | min us | max us | % time |", "|---|---:|---:|---:|---:|---:|"]
     for r in data[:rows]:
         name = r["name"].replace("|", "\\|")
@@ -85,7 +91,8 @@ if __name__ == "__main__":
     elif mode == "pmc":
         pmc(sys.argv[2])
     elif mode == "table":
-        print(table(sys.argv[2], int(sys.argv[3]) if len(sys.argv) > 3 else 16))
+        print(table(sys.argv[2], int(sys.argv[3]) if len(sys.argv) > 3 else 16,
+                    sys.argv[4] if len(sys.argv) > 4 else None))
     elif mode == "traffic":
         print(json.dumps(traffic(sys.argv[2], sys.argv[3], sys.argv[4]), indent=1))
     else:
