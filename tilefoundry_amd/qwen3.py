@@ -30,7 +30,9 @@ more round trips than a kernel boundary inside a graph.
 
 Weights are kept in the checkpoint's ``(out, in)`` layout: ``q|k|v`` stacked
 into one matrix, ``gate`` and ``up`` rows interleaved into another, the head
-tied to the embedding table (one 622 MB tensor serves both).
+tied to the embedding table (one 622 MB tensor serves both) unless the
+checkpoint ships its own ``lm_head.weight``. ``Engine.from_checkpoint(dir)``
+reads a published checkpoint directory (``checkpoint.load_qwen3``).
 """
 from __future__ import annotations
 
@@ -130,7 +132,8 @@ def pack_weights(cfg: Qwen3Config, wts: dict, dev):
     """The decode layout of a checkpoint-named weight dict: ``q|k|v`` stacked,
     ``gate``/``up`` rows interleaved (row 2i = gate_i, 2i+1 = up_i, so one tile
     holds both halves of every pair), everything else as stored; the embedding
-    table doubles as the tied head. Returns ``(embed, gamma_final, layers)``."""
+    table doubles as the head unless the dict holds an untied ``lm_head.weight``.
+    Returns ``(embed, gamma_final, layers, head)``."""
 
     def get(name):
         return wts[name].to(dev, BF16).contiguous()
@@ -152,7 +155,8 @@ def pack_weights(cfg: Qwen3Config, wts: dict, dev):
             "w_down": get(n["w_down"]),
         })
         del gate, up
-    return embed, gamma_final, layers
+    head = get("lm_head.weight") if "lm_head.weight" in wts else embed
+    return embed, gamma_final, layers, head
 
 
 def prefill_caches(cfg: Qwen3Config, embed, layers, kc, vc, cos, sin, ids: torch.Tensor, err):
@@ -254,9 +258,21 @@ class Engine:
         if capture:
             self._capture()
 
+    @classmethod
+    def from_checkpoint(cls, ckpt, ref_dir=None, *, device="cuda:0", **kw):
+        """The reference's ``Engine(ckpt, ref_dir, device=..., max_new=...,
+        prompt_room=...)`` (examples/qwen3_1_7b-tilelang/fast/engine.py:69-107): the
+        model is the checkpoint directory's ``config.json`` and its safetensors
+        weights. ``ref_dir`` (the reference's model-source directory) is accepted
+        for the same call shape and not read: the model here is the config's."""
+        from .checkpoint import load_qwen3
+
+        cfg, wts = load_qwen3(ckpt, device)
+        return cls(cfg, device=device, weights=wts, **kw)
+
     # ---------------------------------------------------------------- weights
     def _pack(self, wts):
-        self.embed, self.gamma_final, self.layers = pack_weights(self.cfg, wts, self.device)
+        self.embed, self.gamma_final, self.layers, self.head = pack_weights(self.cfg, wts, self.device)
         self.cos, self.sin = rope_tables(self.cap, self.cfg.head_dim, self.cfg.rope_theta,
                                          self.device)
 
@@ -309,7 +325,7 @@ class Engine:
             C.gemv_residual(self.attn, w["w_o"], self.hid, None, self.h1)
             C.rmsnorm_gemv_swiglu(self.h1, w["gamma_post"], cfg.eps, w["w_gu"], self.act)
             C.gemv_residual(self.act, w["w_down"], self.h1, None, self.hid)
-        C.lm_head_argmax(self.hid, self.gamma_final, cfg.eps, self.embed, self.logits, self.bv,
+        C.lm_head_argmax(self.hid, self.gamma_final, cfg.eps, self.head, self.logits, self.bv,
                          self.bi)
         C.sample_step(self.bv, self.bi, self.inp, self.plen, self.ids, self.pos, self.sam,
                       self.err)
@@ -473,7 +489,7 @@ class BatchEngine:
         self.ns = self.cap // split
         if weights is None:
             weights = synthetic_weights(cfg, seed, self.device)
-        self.embed, self.gamma_final, self.layers = pack_weights(cfg, weights, self.device)
+        self.embed, self.gamma_final, self.layers, self.head = pack_weights(cfg, weights, self.device)
         del weights
         self.cos, self.sin = rope_tables(self.cap, cfg.head_dim, cfg.rope_theta, self.device)
         self._buffers()
@@ -538,13 +554,14 @@ class BatchEngine:
                           None)
             nxt = self.layers[i + 1]["gamma_in"] if i + 1 < L else self.gamma_final
             C.rows_norm(None, None, self.h1, self.d_part, self.h, nxt, self.xn, cfg.eps, self.err)
-        C.skinny_gemm(self.xn, self.embed, 1, 2, None, None, self.logits if keep_logits else None,
+        C.skinny_gemm(self.xn, self.head, 1, 2, None, None, self.logits if keep_logits else None,
                       self.bv, self.bi)
         C.batch_sample_step(self.bv, self.bi, self.inp, self.plen, self.ids, self.pos, self.sam,
                             self.err)
 
     _capture = Engine._capture
     _run_step = Engine._run_step
+    from_checkpoint = classmethod(Engine.from_checkpoint.__func__)
     _walk_or_prefill = Engine._walk_or_prefill
 
     def _capture_inputs(self):
