@@ -22,6 +22,7 @@ The JSON line also carries:
   decode_layer_bs1_ctx4096   one decode layer over a 4096-position cache
   bs32          the same greedy decode for 32 sequences (tok/s, all sequences)
   mla_decode_b8_ctx8192      MiniCPM3-shaped absorbed MLA block, batch 8
+  minicpm3_decode_bs1        the whole MiniCPM3-4B-shaped model, greedy, bs=1
   prefill_attention_layer    Qwen3.5 attention layer at 1024 / 4096 / 8192 tokens
   prompt_prefill_bs1         time to consume a 64- and a 512-token prompt, walked
                              (one decode step per token) and prefilled (every layer
@@ -300,6 +301,30 @@ def prompt_only(seed: int) -> dict:
     return prompt_prefill(eng, seed)
 
 
+def minicpm3_decode(seed: int, lengths=(32, 128, 512)) -> dict:
+    """MiniCPM3-4B-shaped greedy decode at bs=1 (62 layers, vocab 73448 tied,
+    random-init weights): an 8-token seeded prompt, then 32 / 128 / 512 new
+    tokens, one captured step per token; tok/s beside the reference's H200
+    figures for the same lengths."""
+    from tilefoundry_amd.minicpm3 import MINICPM3_4B, MiniCPM3Engine
+
+    ref = {32: 281.5, 128: 281.3, 512: 223.7}
+    eng = MiniCPM3Engine(MINICPM3_4B, device="cuda:0", max_new=max(lengths), prompt_room=16, seed=seed)
+    g = torch.Generator().manual_seed(seed + 3)
+    prompt = torch.randint(0, MINICPM3_4B.vocab, (8,), generator=g).tolist()
+    eng.generate([prompt], 8)   # warm
+    out = {"workload": "MiniCPM3-4B-shaped greedy decode, bs=1, 8-token prompt", "by_new_tokens": {}}
+    for n in lengths:
+        gen = eng.generate([prompt], n)
+        tps = gen.tokens_per_second
+        out["by_new_tokens"][str(n)] = {"tok/s": round(tps, 1), "ms_per_step": round(gen.seconds * 1e3 / n, 4),
+                                        "vs_reference_h200": round(tps / ref[n], 3)}
+    out["first_tokens"] = gen.tokens[0][:8]
+    del eng
+    torch.cuda.empty_cache()
+    return out
+
+
 def mla_decode() -> dict:
     """MiniCPM3-4B-shaped MLA attention block, batch 8 x 8192 positions, absorbed:
     the whole block (one captured step) and its attention core (split attention
@@ -463,7 +488,7 @@ def main() -> int:
                     help="skip the bs=32, MLA and prefill measurements")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only launch the dominant kernel loop (for rocprofv3 counter runs)")
-    ap.add_argument("--only", choices=("bs32", "mla", "prefill", "prompt"),
+    ap.add_argument("--only", choices=("bs32", "mla", "prefill", "prompt", "minicpm3"),
                     help="run one of the secondary configurations alone and print its line "
                          "(for rocprofv3 kernel traces of that workload)")
     args = ap.parse_args()
@@ -477,7 +502,8 @@ def main() -> int:
 
     if args.only:
         run = {"bs32": lambda: batch32(args.seed, args.steps), "mla": mla_decode,
-               "prefill": prefill_layer, "prompt": lambda: prompt_only(args.seed)}[args.only]
+               "prefill": prefill_layer, "prompt": lambda: prompt_only(args.seed),
+               "minicpm3": lambda: minicpm3_decode(args.seed)}[args.only]
         print(json.dumps({args.only: run()}))
         return 0
 
@@ -551,6 +577,7 @@ def main() -> int:
     if not args.no_configs:
         line["bs32"] = batch32(args.seed, args.steps)
         line["mla_decode_b8_ctx8192"] = mla_decode()
+        line["minicpm3_decode_bs1"] = minicpm3_decode(args.seed)
         line["prefill_attention_layer"] = prefill_layer()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.seed, prompt)

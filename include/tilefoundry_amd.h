@@ -54,6 +54,14 @@ const char* tfa_last_error(void);
 int tfa_rms_norm(const void* x, const void* gamma, void* y, int64_t rows, int64_t hidden,
                  float eps, int mode, hipStream_t stream);
 
+/* y[r,:] = bf16(bf16(bf16(x*rsqrt(mean x^2 + eps)) * gamma) / divisor), the divide
+ * correctly rounded: MiniCPM3's final norm followed by the head's division by
+ * logits_scaling (a divide, since 1/10 is not a bf16 number). divisor != 0.
+ * Replaces: examples/minicpm3_4b-cutedsl/model.py:367-392 (MiniCPM3_4B.final_rms_norm and
+ * the divide of lm_head), kernels/reference_ops.py:78-84 (lm_head_gemv's divide). */
+int tfa_rms_norm_div(const void* x, const void* gamma, void* y, int64_t rows, int64_t hidden, float eps,
+                     float divisor, hipStream_t stream);
+
 /* Fused residual add + RMSNorm over rows x hidden:
  *   residual_out = bf16(x + residual);  y = rmsnorm(residual_out) (mode as above).
  * residual_out may alias residual and y may alias x.
@@ -222,10 +230,14 @@ int64_t tfa_skinny_blocks(int64_t n);
  *             act[m, n/2] = bf16(bf16(silu(bf16 g)) * bf16 u);
  * epilogue 2 (ks = 1): per token, each 16-row group's best (max, lowest index)
  *             into block_val / block_idx [m, tfa_skinny_blocks(n)], and the f32
- *             logits[m, n] when `logits` is not NULL.
+ *             logits[m, n] when `logits` is not NULL;
+ * epilogue 3 (ks = 1): as 2 with every logit landed in bf16 first (the winner
+ *             among equal bf16 logits is the lowest index), for heads whose
+ *             reference returns bf16 logits.
  * k % (256 * ks) == 0.
  * Replaces (batched): examples/qwen3_1_7b-tilelang/fast/kernels.py:123-145 (gemv),
- * :210-257 (gemv_silu), :260-321 (lm_head). */
+ * :210-257 (gemv_silu), :260-321 (lm_head); epilogue 3 the greedy pick over
+ * examples/minicpm3_4b-cutedsl/kernels/reference_ops.py:78-84 (lm_head_gemv, bf16). */
 int tfa_skinny_gemm(const void* x, const void* w, int64_t m, int64_t n, int64_t k, int64_t ks,
                     int epilogue, float* part, void* act, float* logits, float* block_val,
                     int* block_idx, hipStream_t stream);
@@ -238,6 +250,16 @@ int tfa_skinny_gemm(const void* x, const void* w, int64_t m, int64_t n, int64_t 
 int tfa_rows_norm(const void* table, const int64_t* ids, int64_t vocab, const void* h_in,
                   const float* part, int64_t ks, void* h_out, const void* gamma, void* xn,
                   int64_t m, int64_t hidden, float eps, int* err, hipStream_t stream);
+
+/* MiniCPM3's scaled residual followed by the next norm, per token row:
+ * h = bf16(h_in[r] + bf16(bf16(sum_s part[s, r, :]) * alpha)), h_out[r] = h (may
+ * alias h_in), xn[r] = bf16(bf16(h * rsqrt(mean h^2 + eps)) * gamma); alpha is
+ * scale_depth / sqrt(layers). The rows_residual of one block fused with the norm
+ * that opens the next.
+ * Replaces: examples/minicpm3_4b-cutedsl/kernels/reference_ops.py:63-65 (gemv_residual,
+ * scaled) followed by :42-48 (rmsnorm), model.py:320-344 (decoder_layer's residuals). */
+int tfa_rows_norm_scaled(const float* part, int64_t ks, const void* h_in, float alpha, void* h_out,
+                         const void* gamma, void* xn, int64_t m, int64_t hidden, float eps, hipStream_t stream);
 
 /* The greedy step for `batch` sequences: per sequence b, best = argmax over
  * block_val[b, :] (lowest index on ties); sam[b, pos[b]] = best;

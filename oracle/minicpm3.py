@@ -1,4 +1,5 @@
-"""MiniCPM3-4B-shaped MLA decode attention, restated on the CPU -- test infrastructure only.
+"""MiniCPM3-4B decode restated on the CPU: the MLA attention and, at the end of this
+file, the whole model (embedding, layers, head) -- test infrastructure only.
 
 What each function follows (jingchangshi/TileFoundry):
 
@@ -283,3 +284,127 @@ def random_cache(batch: int, n: int, cfg: MLAConfig, seed: int = 1):
     g = torch.Generator().manual_seed(seed)
     return (torch.randn(batch, n, cfg.kv_lora, generator=g).to(BF16),
             torch.randn(batch, n, cfg.rope, generator=g).to(BF16))
+
+
+# ---------------------------------------------------------------- the whole model
+# MiniCPM3_4B's root and decoder layer (examples/minicpm3_4b-cutedsl/model.py:320-420),
+# decoded one token at a time over the compressed cache:
+#   embed           bf16(table[id] * scale_emb)                         (:356-365)
+#   decoder_layer   h1 = h + bf16(attn(h) * a); h' = h1 + bf16(mlp(h1) * a),
+#                   a = bf16(scale_depth / sqrt(layers))                (:320-344)
+#   mlp             down(bf16(silu(gate(xn))) * up(xn)), xn = norm(h1) (reference_ops.py:66-70)
+#   final_rms_norm  + lm_head: bf16(bf16(norm(h)) / logits_scaling) @ W_embed^T,
+#                   landed in bf16 (:367-392); greedy = lowest-index argmax.
+# Pinned (tests/test_oracle.py) against Hugging Face's MiniCPM3ForCausalLM (the
+# reference's own third-party arithmetic boundary, transformers installed here)
+# built from the same tiny random weights, within the bf16 bar, and by the
+# zero-branch closed form (all projections zero: every layer is the identity
+# and the logits are the head of the scaled embedding's norm).
+
+
+@dataclass(frozen=True)
+class ModelConfig(MLAConfig):
+    """MLAConfig plus the fields of the whole model (examples/minicpm3_4b-cutedsl/config.json)."""
+
+    inter: int = 6400
+    vocab: int = 73448
+    layers: int = 62
+    scale_emb: float = 12.0
+    dim_model_base: int = 256
+    scale_depth: float = 1.4
+
+    @property
+    def logits_scaling(self) -> float:
+        return self.hidden / self.dim_model_base
+
+    @property
+    def residual_scale(self) -> float:
+        """``scale_depth / sqrt(layers)`` as the bf16 scalar the reference passes."""
+        import math
+
+        return float(torch.tensor(self.scale_depth / math.sqrt(self.layers)).to(BF16))
+
+
+@dataclass
+class LayerWeights(MLAWeights):
+    gamma_post: torch.Tensor = None   # [hidden]
+    w_gate: torch.Tensor = None       # [inter, hidden]
+    w_up: torch.Tensor = None         # [inter, hidden]
+    w_down: torch.Tensor = None       # [hidden, inter]
+
+
+@dataclass
+class ModelWeights:
+    embed: torch.Tensor               # [vocab, hidden], tied with the head
+    gamma_final: torch.Tensor
+    layers: list
+
+
+def random_model(cfg: ModelConfig, seed: int = 0, std: float = 0.02) -> ModelWeights:
+    g = torch.Generator().manual_seed(seed)
+
+    def w(*shape):
+        return (std * torch.randn(*shape, generator=g)).to(BF16)
+
+    def gam(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=g)).to(BF16)
+
+    layers = []
+    for _ in range(cfg.layers):
+        a = random_weights(cfg, seed=int(torch.randint(0, 2 ** 31 - 1, (1,), generator=g)), std=std)
+        layers.append(LayerWeights(**a.__dict__, gamma_post=gam(cfg.hidden), w_gate=w(cfg.inter, cfg.hidden),
+                                   w_up=w(cfg.inter, cfg.hidden), w_down=w(cfg.hidden, cfg.inter)))
+    return ModelWeights(embed=w(cfg.vocab, cfg.hidden), gamma_final=gam(cfg.hidden), layers=layers)
+
+
+def mlp(h1, lw: LayerWeights, cfg: ModelConfig):
+    xn = rms_norm_q(h1, lw.gamma_post, cfg.eps)
+    act = torch.nn.functional.silu(proj(xn, lw.w_gate).float()).to(BF16) * proj(xn, lw.w_up)
+    return proj(act, lw.w_down)
+
+
+def decode_step(model: ModelWeights, cfg: ModelConfig, token: int, pos: int, caches, cos, sin,
+                p_bf16: bool = True):
+    """One decode step of the whole model over the compressed caches
+    (``caches[i] = [latent [n, kv_lora], rope_k [n, rope]]``, appended in place).
+    Returns the logits (f32 holding the bf16 values the reference returns)."""
+    a = torch.tensor(cfg.residual_scale).to(BF16)
+    h = model.embed[token] * torch.tensor(cfg.scale_emb).to(BF16)
+    for lw, cache in zip(model.layers, caches):
+        pr = project(h, lw, cfg, pos, cos, sin)
+        cache[0] = torch.cat((cache[0], pr.latent.view(1, -1)), 0)
+        cache[1] = torch.cat((cache[1], pr.k_rope.view(1, -1)), 0)
+        q_abs = absorb_query(pr.q_up, lw, cfg, pos, cos, sin)
+        attn = attend_absorbed(q_abs, cache[0], cache[1], lw, cfg, p_bf16=p_bf16)
+        h1 = o_proj_residual(attn, lw.w_o, h, cfg.residual_scale)
+        h = h1 + mlp(h1, lw, cfg) * a
+    xs = rms_norm_q(h, model.gamma_final, cfg.eps) / torch.tensor(cfg.logits_scaling).to(BF16)
+    return proj(xs, model.embed).float()
+
+
+def empty_caches(cfg: ModelConfig, n_layers: int):
+    return [[torch.zeros(0, cfg.kv_lora, dtype=BF16), torch.zeros(0, cfg.rope, dtype=BF16)]
+            for _ in range(n_layers)]
+
+
+def greedy(logits: torch.Tensor) -> int:
+    return int(torch.argmax(logits))
+
+
+def decode(model: ModelWeights, cfg: ModelConfig, prompt: list, max_new: int, record=None,
+           p_bf16: bool = True) -> list:
+    """Greedy continuation; ``record`` receives ``(logits, pick, top-2 gap)`` per generated step."""
+    cos, sin = rope_tables(len(prompt) + max_new, cfg)
+    caches = empty_caches(cfg, len(model.layers))
+    for p, t in enumerate(prompt):
+        logits = decode_step(model, cfg, t, p, caches, cos, sin, p_bf16)
+    out = []
+    for i in range(max_new):
+        pick = greedy(logits)
+        out.append(pick)
+        if record is not None:
+            top = torch.topk(logits, 2).values
+            record.append((logits.clone(), pick, float(top[0] - top[1])))
+        if i + 1 < max_new:
+            logits = decode_step(model, cfg, pick, len(prompt) + i, caches, cos, sin, p_bf16)
+    return out

@@ -153,6 +153,12 @@ def test_batched_argument_checks(lib):
     assert st == SHAPE
     st, _ = call(lib, "tfa_skinny_gemm", A, A, I64(32), I64(64), I64(2048), I64(1), I(7), A, A, A, A, A, P(None))
     assert st == ARG
+    st, msg = call(lib, "tfa_skinny_gemm", A, A, I64(4), I64(64), I64(2048), I64(2), I(3), P(None), P(None), P(None), A, A, P(None))
+    assert st == SHAPE and "ks=1" in msg
+    st, _ = call(lib, "tfa_rms_norm_div", A, A, A, I64(4), I64(2560), F(1e-5), F(0.0), P(None))
+    assert st == ARG
+    st, _ = call(lib, "tfa_rms_norm_div", A, A, A, I64(4), I64(2561), F(1e-5), F(10.0), P(None))
+    assert st == SHAPE
     st, _ = call(lib, "tfa_rows_norm", P(None), P(None), I64(0), A, P(None), I64(1), A, A, A, I64(4), I64(2048), F(1e-6), P(None), P(None))
     assert st == NULL
     st, _ = call(lib, "tfa_batch_sample_step", A, A, I64(10), I64(0), A, A, A, A, A, I64(8), P(None), P(None))

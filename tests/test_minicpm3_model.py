@@ -1,0 +1,130 @@
+"""The whole MiniCPM3 decode model (``minicpm3.MiniCPM3Engine``) against the
+oracle's token-by-token decode (oracle/minicpm3.py ``decode_step``, itself
+pinned to Hugging Face's MiniCPM3ForCausalLM in test_oracle.py).
+
+Small stacks keep the published layer shapes (hidden 2560, 40 heads, q_lora 768,
+kv_lora 256, SwiGLU 6400) with fewer layers and a smaller vocabulary, so the
+CPU oracle finishes in seconds; the full 62-layer model runs as a smoke test
+(finite, reproducible, the sampler's contract).
+"""
+from dataclasses import replace
+
+import pytest
+import torch
+
+from oracle import minicpm3 as OM
+from tests._check import assert_close
+
+BF16 = torch.bfloat16
+
+
+def _small(layers=2, vocab=4096):
+    from tilefoundry_amd.minicpm3 import MINICPM3_4B, synthetic_model_weights
+
+    cfg = replace(MINICPM3_4B, layers=layers, vocab=vocab)
+    return cfg, synthetic_model_weights(cfg, seed=11)
+
+
+def _oracle(cfg, wts):
+    from tilefoundry_amd.minicpm3 import hf_layer_names
+
+    ocfg = OM.ModelConfig(hidden=cfg.hidden, heads=cfg.heads, q_lora=cfg.q_lora, kv_lora=cfg.kv_lora,
+                          nope=cfg.nope, rope=cfg.rope, v_dim=cfg.v_dim, eps=cfg.eps, lora_eps=cfg.lora_eps,
+                          rope_theta=cfg.rope_theta, inter=cfg.inter, vocab=cfg.vocab, layers=cfg.layers,
+                          scale_emb=cfg.scale_emb, dim_model_base=cfg.dim_model_base,
+                          scale_depth=cfg.scale_depth)
+    layers = [OM.LayerWeights(**{k: wts[v].cpu() for k, v in hf_layer_names(i).items()})
+              for i in range(cfg.layers)]
+    model = OM.ModelWeights(embed=wts["model.embed_tokens.weight"].cpu(),
+                            gamma_final=wts["model.norm.weight"].cpu(), layers=layers)
+    return ocfg, model
+
+
+@pytest.mark.gpu
+def test_minicpm3_engine_logits_and_caches(dev):
+    """After a 9-token prompt the bf16 logits and each layer's compressed cache
+    rows agree with the oracle's decode (layer 0's cache at the per-op bar)."""
+    from tilefoundry_amd.minicpm3 import MiniCPM3Engine
+
+    cfg, wts = _small()
+    eng = MiniCPM3Engine(cfg, device=dev, max_new=16, prompt_room=16, weights=wts)
+    prompt = [5, 77, 1023, 4000, 12, 9, 300, 2047, 64]
+    eng.generate([prompt], 1)
+    ocfg, model = _oracle(cfg, wts)
+    cos, sin = OM.rope_tables(len(prompt), ocfg)
+    caches = OM.empty_caches(ocfg, cfg.layers)
+    for p, t in enumerate(prompt):
+        ref = OM.decode_step(model, ocfg, t, p, caches, cos, sin)
+    assert_close("logits", eng.logits[0], ref)
+    n = len(prompt)
+    assert_close("latent cache layer 0", eng.latent[0, 0, :n], caches[0][0])
+    assert_close("rope-key cache layer 0", eng.rope_k[0, 0, :n], caches[0][1])
+    assert_close("latent cache layer 1", eng.latent[1, 0, :n], caches[1][0], rtol=2e-2)
+
+
+@pytest.mark.gpu
+def test_minicpm3_engine_greedy_against_oracle(dev):
+    """Greedy ids equal the oracle's wherever its top-2 margin is resolvable at bf16."""
+    from tilefoundry_amd.minicpm3 import MiniCPM3Engine
+
+    cfg, wts = _small()
+    eng = MiniCPM3Engine(cfg, device=dev, max_new=32, prompt_room=16, weights=wts)
+    prompt = [1, 2200, 17, 3999, 508, 60]
+    gen = eng.generate([prompt], 20)
+    ocfg, model = _oracle(cfg, wts)
+    rec = []
+    want = OM.decode(model, ocfg, prompt, 20, record=rec)
+    got = gen.tokens[0]
+    diff = next((i for i, (a, b) in enumerate(zip(got, want)) if a != b), None)
+    if diff is not None:
+        logits, pick, gap = rec[diff]
+        assert gap < 1e-2 * float(logits.abs().max()), f"step {diff}: {got[diff]} != {want[diff]} at margin {gap:.4g}"
+        assert diff >= 6
+
+
+@pytest.mark.gpu
+def test_minicpm3_engine_batch_rows_are_independent(dev):
+    """Three sequences in one batch decode exactly what each decodes alone."""
+    from tilefoundry_amd.minicpm3 import MiniCPM3Engine
+
+    cfg, wts = _small()
+    prompts = [[3, 4, 5, 6], [4000, 1, 2, 3], [77, 77, 77, 77]]
+    batch = MiniCPM3Engine(cfg, batch=3, device=dev, max_new=16, prompt_room=8, weights=wts)
+    got = batch.generate(prompts, 12).tokens
+    one = MiniCPM3Engine(cfg, batch=1, device=dev, max_new=16, prompt_room=8, weights=wts)
+    for b, p in enumerate(prompts):
+        assert one.generate([p], 12).tokens[0] == got[b], f"sequence {b}"
+
+
+@pytest.mark.gpu
+def test_minicpm3_sampler(dev):
+    """The top-p sampler: reproducible under a seeded generator, and with a
+    vanishing top_p it keeps only the most likely token -- the greedy ids."""
+    from tilefoundry_amd.minicpm3 import MiniCPM3Engine, sample_top_p
+
+    cfg, wts = _small()
+    eng = MiniCPM3Engine(cfg, device=dev, max_new=24, prompt_room=8, weights=wts)
+    prompt = [[10, 20, 30, 40]]
+    greedy = eng.generate(prompt, 16).tokens
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    a = eng.generate(prompt, 16, sampler=sample_top_p(0.8, 0.8, g)).tokens
+    g.manual_seed(1)
+    b = eng.generate(prompt, 16, sampler=sample_top_p(0.8, 0.8, g)).tokens
+    assert a == b
+    assert eng.generate(prompt, 16, sampler=sample_top_p(0.8, 1e-9, g)).tokens == greedy
+    assert all(0 <= t < cfg.vocab for t in a[0])
+
+
+@pytest.mark.gpu
+def test_minicpm3_full_model_smoke(dev):
+    """62 layers, vocab 73448, random weights: a greedy continuation is
+    reproducible, every id in range, and the bf16 logits finite."""
+    from tilefoundry_amd.minicpm3 import MiniCPM3Engine
+
+    eng = MiniCPM3Engine(device=dev, max_new=16, prompt_room=16, seed=1)
+    prompt = [[1, 100, 2000, 30000, 73000]]
+    a = eng.generate(prompt, 12).tokens
+    b = eng.generate(prompt, 12).tokens
+    assert a == b and all(0 <= t < 73448 for t in a[0])
+    assert bool(torch.isfinite(eng.logits).all())

@@ -507,3 +507,74 @@ def test_prefill_attention_f64_brute_force_and_causality():
     s = (q[0, 0].float() @ k[:, 0].float().t()) * cfg.scale
     full = (torch.softmax(s, -1).to(BF).float() @ v[:, 0].float()).to(BF) * torch.sigmoid(gate[0, 0])
     assert not torch.equal(full, out[0, 0].to(BF))
+
+
+# ------------------------------------------------ MiniCPM3 whole-model oracle
+def _minicpm3_against_hf(mutate=None):
+    """Max relative L2 of the oracle's per-position logits against Hugging Face's
+    MiniCPM3ForCausalLM (bf16, eager) built from the same random weights: the
+    reference's third-party arithmetic boundary, installed here. ``mutate`` plants
+    a mistake in the oracle's config."""
+    import dataclasses
+
+    from transformers import MiniCPM3Config
+    from transformers.models.minicpm3 import modeling_minicpm3 as HF
+
+    from oracle import minicpm3 as OM
+
+    # scale_depth 0.3 over 2 layers makes the residual scale 0.21, far from 1,
+    # so a dropped scale shows
+    cfg = OM.ModelConfig(hidden=256, heads=4, q_lora=96, kv_lora=64, inter=512, vocab=512, layers=2,
+                         dim_model_base=64, scale_depth=0.3)
+    m = OM.random_model(cfg, 3, std=0.05)
+    hc = MiniCPM3Config(
+        hidden_size=cfg.hidden, num_hidden_layers=cfg.layers, intermediate_size=cfg.inter,
+        num_attention_heads=cfg.heads, num_key_value_heads=cfg.heads, qk_nope_head_dim=cfg.nope,
+        qk_rope_head_dim=cfg.rope, q_lora_rank=cfg.q_lora, kv_lora_rank=cfg.kv_lora, v_head_dim=cfg.v_dim,
+        vocab_size=cfg.vocab, rms_norm_eps=cfg.eps, scale_emb=cfg.scale_emb, dim_model_base=cfg.dim_model_base,
+        scale_depth=cfg.scale_depth, max_position_embeddings=4096, tie_word_embeddings=True,
+        rope_scaling={"type": "longrope", "factor": 1.0, "long_factor": list(OM.SHORT_FACTOR),
+                      "short_factor": list(OM.SHORT_FACTOR), "original_max_position_embeddings": 4096,
+                      "rope_theta": cfg.rope_theta})
+    hf = HF.MiniCPM3ForCausalLM(hc).eval().to(torch.bfloat16)
+    names = {"gamma_in": "input_layernorm", "w_q_a": "self_attn.q_a_proj", "gamma_q_a": "self_attn.q_a_layernorm",
+             "w_q_b": "self_attn.q_b_proj", "w_kv_a": "self_attn.kv_a_proj_with_mqa",
+             "gamma_kv_a": "self_attn.kv_a_layernorm", "w_kv_b": "self_attn.kv_b_proj", "w_o": "self_attn.o_proj",
+             "gamma_post": "post_attention_layernorm", "w_gate": "mlp.gate_proj", "w_up": "mlp.up_proj",
+             "w_down": "mlp.down_proj"}
+    sd = {"model.embed_tokens.weight": m.embed, "model.norm.weight": m.gamma_final, "lm_head.weight": m.embed}
+    for i, lw in enumerate(m.layers):
+        for k, n in names.items():
+            sd[f"model.layers.{i}.{n}.weight"] = getattr(lw, k)
+    missing, unexpected = hf.load_state_dict(sd, strict=False)
+    assert not missing and not unexpected, (missing, unexpected)
+    prompt = [3, 17, 42, 99, 7, 250]
+    with torch.no_grad():
+        ref = hf(torch.tensor([prompt])).logits[0].float()
+    ocfg = mutate(cfg) if mutate else cfg
+    cos, sin = OM.rope_tables(len(prompt), ocfg)
+    caches = OM.empty_caches(ocfg, ocfg.layers)
+    worst = 0.0
+    for p, t in enumerate(prompt):
+        lg = OM.decode_step(m, ocfg, t, p, caches, cos, sin)
+        worst = max(worst, float((lg - ref[p]).norm() / ref[p].norm()))
+    return worst
+
+
+def test_minicpm3_model_oracle_against_hugging_face():
+    assert _minicpm3_against_hf() < 1e-2
+
+
+def test_minicpm3_model_oracle_planted_mistakes():
+    import dataclasses
+
+    from oracle import minicpm3 as OM
+
+    class NoResidualScale(OM.ModelConfig):
+        @property
+        def residual_scale(self):
+            return 1.0
+
+    assert _minicpm3_against_hf(lambda c: NoResidualScale(**dataclasses.asdict(c))) > 0.1
+    assert _minicpm3_against_hf(lambda c: dataclasses.replace(c, scale_emb=1.0)) > 0.1
+    assert _minicpm3_against_hf(lambda c: dataclasses.replace(c, dim_model_base=c.hidden * c.hidden // c.dim_model_base)) > 0.1

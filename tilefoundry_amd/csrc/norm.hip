@@ -7,6 +7,9 @@
 //            y = bf16( bf16(x * r) * gamma ),  r = 1/sqrt(mean(x^2) + eps)
 //   MODE 1 (Qwen3.5 prefill, examples/qwen3_8_27b_prefill-tilelang/kernels/elementwise.py:21-68):
 //            y = bf16( (x * r) * (1 + gamma) ) in f32
+//   MODE 2 (MiniCPM3 final norm + the head's divide, examples/minicpm3_4b-cutedsl/model.py
+//           final_rms_norm and lm_head):
+//            y = bf16( bf16( bf16(x * r) * gamma ) / d ), a correctly rounded divide
 // The fused add lands the sum in bf16 first (r' = bf16(x + res)) and normalises
 // that landed value, which is what `Hout = A + ...; Xn = norm(Hout)` does in
 // examples/qwen3_1_7b-tilelang/fast/kernels.py:82-116.
@@ -18,8 +21,9 @@ using namespace tfa;
 namespace {
 
 template <int MODE>
-TFA_DEV float norm_scale(float x, float r, float g) {
+TFA_DEV float norm_scale(float x, float r, float g, float d) {
   if (MODE == 0) return round_bf(round_bf(x * r) * g);
+  if (MODE == 2) return round_bf(__fdiv_rn(round_bf(round_bf(x * r) * g), d));
   return (x * r) * (g + 1.0f);
 }
 
@@ -29,7 +33,7 @@ template <int NC, bool ADD, int MODE>
 __global__ __launch_bounds__(256) void rms_rows_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
     const uint16_t* __restrict__ gamma, uint16_t* __restrict__ y,
-    uint16_t* __restrict__ res_out, int rows, int H, float eps) {
+    uint16_t* __restrict__ res_out, int rows, int H, float eps, float div) {
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
   if (row >= rows) return;
@@ -74,7 +78,7 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(
       unpack8(xv[c], f);
       unpack8(ld16(gamma + 8 * v), g);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) f[i] = norm_scale<MODE>(f[i], r, g[i]);
+      for (int i = 0; i < 8; ++i) f[i] = norm_scale<MODE>(f[i], r, g[i], div);
       st16(y + base + 8 * v, pack8(f));
       if (ADD) st16(res_out + base + 8 * v, xv[c]);
     }
@@ -83,7 +87,7 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(
 
 template <int NC>
 int launch_rows(const void* x, const void* res, const void* gamma, void* y, void* res_out,
-                int rows, int H, float eps, int mode, hipStream_t s) {
+                int rows, int H, float eps, int mode, float div, hipStream_t s) {
   const dim3 block(256);
   const dim3 grid((rows + 3) / 4);
   auto X = static_cast<const uint16_t*>(x);
@@ -92,20 +96,21 @@ int launch_rows(const void* x, const void* res, const void* gamma, void* y, void
   auto Y = static_cast<uint16_t*>(y);
   auto RO = static_cast<uint16_t*>(res_out);
   if (res) {
-    if (mode == 0) rms_rows_kernel<NC, true, 0><<<grid, block, 0, s>>>(X, R, G, Y, RO, rows, H, eps);
-    else rms_rows_kernel<NC, true, 1><<<grid, block, 0, s>>>(X, R, G, Y, RO, rows, H, eps);
+    if (mode == 0) rms_rows_kernel<NC, true, 0><<<grid, block, 0, s>>>(X, R, G, Y, RO, rows, H, eps, div);
+    else rms_rows_kernel<NC, true, 1><<<grid, block, 0, s>>>(X, R, G, Y, RO, rows, H, eps, div);
   } else {
-    if (mode == 0) rms_rows_kernel<NC, false, 0><<<grid, block, 0, s>>>(X, R, G, Y, RO, rows, H, eps);
-    else rms_rows_kernel<NC, false, 1><<<grid, block, 0, s>>>(X, R, G, Y, RO, rows, H, eps);
+    if (mode == 0) rms_rows_kernel<NC, false, 0><<<grid, block, 0, s>>>(X, R, G, Y, RO, rows, H, eps, div);
+    else if (mode == 1) rms_rows_kernel<NC, false, 1><<<grid, block, 0, s>>>(X, R, G, Y, RO, rows, H, eps, div);
+    else rms_rows_kernel<NC, false, 2><<<grid, block, 0, s>>>(X, R, G, Y, RO, rows, H, eps, div);
   }
   return launched("rms_norm_rows");
 }
 
 int dispatch_rows(const void* x, const void* res, const void* gamma, void* y, void* res_out,
-                  int64_t rows, int64_t H, float eps, int mode, hipStream_t s) {
+                  int64_t rows, int64_t H, float eps, int mode, hipStream_t s, float div = 1.f) {
   const int nc = static_cast<int>((H / 8 + kWave - 1) / kWave);
   switch (nc) {
-#define TFA_NC(n) case n: return launch_rows<n>(x, res, gamma, y, res_out, (int)rows, (int)H, eps, mode, s);
+#define TFA_NC(n) case n: return launch_rows<n>(x, res, gamma, y, res_out, (int)rows, (int)H, eps, mode, div, s);
     TFA_NC(1) TFA_NC(2) TFA_NC(3) TFA_NC(4) TFA_NC(5) TFA_NC(6) TFA_NC(7) TFA_NC(8)
     TFA_NC(9) TFA_NC(10) TFA_NC(11) TFA_NC(12) TFA_NC(13) TFA_NC(14) TFA_NC(15) TFA_NC(16)
 #undef TFA_NC
@@ -158,6 +163,15 @@ int tfa_rms_norm(const void* x, const void* gamma, void* y, int64_t rows, int64_
   if (st != TFA_OK) return st;
   if (rows == 0) return TFA_OK;
   return dispatch_rows(x, nullptr, gamma, y, nullptr, rows, hidden, eps, mode, stream);
+}
+
+int tfa_rms_norm_div(const void* x, const void* gamma, void* y, int64_t rows, int64_t hidden, float eps,
+                     float divisor, hipStream_t stream) {
+  int st = check_rows(x, gamma, y, rows, hidden, 0, "tfa_rms_norm_div");
+  if (st != TFA_OK) return st;
+  TFA_REQUIRE(divisor != 0.f && divisor == divisor, TFA_ERR_ARG, "tfa_rms_norm_div: divisor must be nonzero");
+  if (rows == 0) return TFA_OK;
+  return dispatch_rows(x, nullptr, gamma, y, nullptr, rows, hidden, eps, 2, stream, divisor);
 }
 
 int tfa_add_rms_norm(const void* x, const void* residual, const void* gamma, void* y,

@@ -48,7 +48,7 @@ constexpr int kGroupRows = 16;   // argmax winners are kept per 16 weight rows
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-enum { SK_PARTIAL = 0, SK_SWIGLU = 1, SK_ARGMAX = 2 };
+enum { SK_PARTIAL = 0, SK_SWIGLU = 1, SK_ARGMAX = 2, SK_ARGMAX_BF16 = 3 };
 
 struct SkinnyArgs {
   const uint16_t* x;  // [M, K]
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(W * kWave) void skinny_gemm_kernel(const SkinnyArgs
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = 16 * th + 4 * grp + r;
-      const float val = s[r];
+      float val = s[r];
       if (EPI == SK_PARTIAL) {
         if (m < a.M && n < a.N) a.part[(static_cast<size_t>(blockIdx.y) * a.M + m) * a.N + n] = val;
       }
@@ -206,7 +206,8 @@ __global__ __launch_bounds__(W * kWave) void skinny_gemm_kernel(const SkinnyArgs
           a.act[static_cast<size_t>(m) * (a.N / 2) + n / 2] = static_cast<uint16_t>(f2bf(act));
         }
       }
-      if (EPI == SK_ARGMAX) {
+      if (EPI == SK_ARGMAX || EPI == SK_ARGMAX_BF16) {
+        if (EPI == SK_ARGMAX_BF16) val = round_bf(val);   // bf16 logits: ties as the landed values have them
         if (a.logits && m < a.M && n < a.N) a.logits[static_cast<size_t>(m) * a.N + n] = val;
         // per token: best of the tile's 16 rows (lowest index on ties)
         float bvv = n < a.N ? val : -FLT_MAX;
@@ -281,14 +282,17 @@ int launch_skinny(const SkinnyArgs& a, hipStream_t st, const char* name) {
 // ---------------------------------------------------------------- rows_norm
 // Per token row m (one 256-thread block; each thread owns 8-element chunks):
 // h = table[ids[m]] (embed mode) or h = bf16(h_in[m] + bf16(sum_s part[s, m, :]))
-// (residual mode); h_out[m] = h; xn[m] = bf16(bf16(h * rsqrt(mean h^2 + eps)) * gamma).
+// (residual mode), or with SCALED h = bf16(h_in[m] + bf16(bf16(sum_s part) * alpha))
+// (MiniCPM3's scale_depth residual); h_out[m] = h;
+// xn[m] = bf16(bf16(h * rsqrt(mean h^2 + eps)) * gamma).
 // Every load of the row is issued before any arithmetic (one memory round trip).
 constexpr int kRowChunks = 2;   // 8-element chunks per thread: hidden <= 256 * 8 * 2
+template <bool SCALED>
 __global__ __launch_bounds__(kThreads) void rows_norm_kernel(
     const uint16_t* __restrict__ table, const int64_t* __restrict__ ids, int64_t vocab,
     const uint16_t* h_in, const float* __restrict__ part, int ks, uint16_t* h_out,
     const uint16_t* __restrict__ gamma, uint16_t* __restrict__ xn, int M, int H, float eps,
-    int* err) {
+    int* err, float alpha) {
   __shared__ float red[kWaves];
   const int m = blockIdx.x;
   const int t = threadIdx.x;
@@ -315,7 +319,9 @@ __global__ __launch_bounds__(kThreads) void rows_norm_kernel(
       float acc[8];
       sum_splits8(part + static_cast<size_t>(m) * H + 8 * ch, static_cast<size_t>(M) * H, ks, acc);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[c][i] = round_bf(v[c][i] + round_bf(acc[i]));
+      for (int i = 0; i < 8; ++i)
+        v[c][i] = SCALED ? round_bf(v[c][i] + round_bf(round_bf(acc[i]) * alpha))
+                         : round_bf(v[c][i] + round_bf(acc[i]));
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss += v[c][i] * v[c][i];
@@ -395,6 +401,7 @@ int tfa_skinny_gemm(const void* x, const void* w, int64_t m, int64_t n, int64_t 
       a.act = static_cast<uint16_t*>(act);
       return launch_skinny<SK_SWIGLU>(a, stream, "skinny_gemm_swiglu");
     case 2:
+    case 3:
       TFA_NONNULL(block_val);
       TFA_NONNULL(block_idx);
       TFA_REQUIRE(ks == 1, TFA_ERR_SHAPE, "tfa_skinny_gemm: argmax needs ks=1");
@@ -402,9 +409,10 @@ int tfa_skinny_gemm(const void* x, const void* w, int64_t m, int64_t n, int64_t 
       a.ngroups = (int)tfa_skinny_blocks(n);
       a.bv = block_val;
       a.bi = block_idx;
+      if (epilogue == 3) return launch_skinny<SK_ARGMAX_BF16>(a, stream, "skinny_gemm_argmax_bf16");
       return launch_skinny<SK_ARGMAX>(a, stream, "skinny_gemm_argmax");
     default:
-      return fail(TFA_ERR_ARG, "tfa_skinny_gemm: epilogue %d not in {0, 1, 2}", epilogue);
+      return fail(TFA_ERR_ARG, "tfa_skinny_gemm: epilogue %d not in {0, 1, 2, 3}", epilogue);
   }
 }
 
@@ -430,11 +438,34 @@ int tfa_rows_norm(const void* table, const int64_t* ids, int64_t vocab, const vo
                 (long long)ks, kMaxSplitsK);
   }
   if (m == 0) return TFA_OK;
-  rows_norm_kernel<<<(int)m, kThreads, 0, stream>>>(
+  rows_norm_kernel<false><<<(int)m, kThreads, 0, stream>>>(
       static_cast<const uint16_t*>(table), ids, vocab, static_cast<const uint16_t*>(h_in), part,
       (int)ks, static_cast<uint16_t*>(h_out), static_cast<const uint16_t*>(gamma),
-      static_cast<uint16_t*>(xn), (int)m, (int)hidden, eps, err);
+      static_cast<uint16_t*>(xn), (int)m, (int)hidden, eps, err, 0.f);
   return launched("rows_norm");
+}
+
+int tfa_rows_norm_scaled(const float* part, int64_t ks, const void* h_in, float alpha, void* h_out,
+                         const void* gamma, void* xn, int64_t m, int64_t hidden, float eps, hipStream_t stream) {
+  TFA_NONNULL(part);
+  TFA_NONNULL(h_in);
+  TFA_NONNULL(h_out);
+  TFA_NONNULL(gamma);
+  TFA_NONNULL(xn);
+  TFA_REQUIRE(m >= 0 && hidden > 0 && hidden % 8 == 0 && hidden <= kThreads * 8 * kRowChunks,
+              TFA_ERR_SHAPE, "tfa_rows_norm_scaled: hidden %lld must be a multiple of 8, at most %d",
+              (long long)hidden, kThreads * 8 * kRowChunks);
+  TFA_REQUIRE(ks >= 1 && ks <= kMaxSplitsK, TFA_ERR_SHAPE, "tfa_rows_norm_scaled: ks %lld not in [1, %d]",
+              (long long)ks, kMaxSplitsK);
+  TFA_ALIGN16(h_in);
+  TFA_ALIGN16(h_out);
+  TFA_ALIGN16(xn);
+  TFA_ALIGN16(gamma);
+  if (m == 0) return TFA_OK;
+  rows_norm_kernel<true><<<(int)m, kThreads, 0, stream>>>(
+      nullptr, nullptr, 0, static_cast<const uint16_t*>(h_in), part, (int)ks, static_cast<uint16_t*>(h_out),
+      static_cast<const uint16_t*>(gamma), static_cast<uint16_t*>(xn), (int)m, (int)hidden, eps, nullptr, alpha);
+  return launched("rows_norm_scaled");
 }
 
 int tfa_batch_sample_step(const float* block_val, const int* block_idx, int64_t nblocks,

@@ -65,6 +65,16 @@ void rms_norm(const Tensor& x, const Tensor& gamma, const Tensor& y, double eps,
                             (int)mode, stream_of(x)));
 }
 
+void rms_norm_div(const Tensor& x, const Tensor& gamma, const Tensor& y, double eps, double divisor) {
+  const int64_t H = last_dim(x);
+  const int64_t rows = H ? x.numel() / H : 0;
+  need(x, "x", BF);
+  need(gamma, "gamma", BF, H);
+  need(y, "y", BF, x.numel());
+  raise_status(tfa_rms_norm_div(x.data_ptr(), gamma.data_ptr(), y.data_ptr(), rows, H, (float)eps,
+                                (float)divisor, stream_of(x)));
+}
+
 void add_rms_norm(const Tensor& x, const Tensor& residual, const Tensor& gamma, const Tensor& y,
                   const Tensor& residual_out, double eps, int64_t mode) {
   const int64_t H = last_dim(x);
@@ -309,7 +319,7 @@ void skinny_gemm(const Tensor& x, const Tensor& w, int64_t ks, int64_t epilogue,
   } else if (epilogue == 1) {
     if (!act) bad("swiglu epilogue needs act");
     need(*act, "act", BF, M * (N / 2));
-  } else if (epilogue == 2) {
+  } else if (epilogue == 2 || epilogue == 3) {
     if (!block_val || !block_idx) bad("argmax epilogue needs block_val, block_idx");
     if (logits) need(*logits, "logits", F32, M * N);
     const int64_t nb = tfa_skinny_blocks(N);
@@ -457,6 +467,22 @@ void mla_combine_up(const Tensor& op, const Tensor& mp, const Tensor& lp, const 
   need(attn, "attn", BF, B * H * 64);
   raise_status(tfa_mla_combine_up(op.data_ptr(), mp.data_ptr<float>(), lp.data_ptr<float>(), wr.data_ptr<int>(),
                                   ns, split, B, H, ns * split, w_kv_b.data_ptr(), attn.data_ptr(), stream_of(wr)));
+}
+
+// part [ks, m, hidden] f32; h_in / h_out / xn [m, hidden] bf16
+void rows_norm_scaled(const Tensor& part, const Tensor& h_in, double alpha, const Tensor& h_out, const Tensor& gamma,
+                      const Tensor& xn, double eps) {
+  need(h_in, "h_in", BF);
+  if (h_in.dim() != 2) bad("h_in: expected (m, hidden)");
+  const int64_t M = h_in.size(0), H = h_in.size(1);
+  need(h_out, "h_out", BF, M * H);
+  need(xn, "xn", BF, M * H);
+  need(gamma, "gamma", BF, H);
+  need(part, "part", F32);
+  if (M * H == 0 || part.numel() % (M * H) != 0) bad("part: expected (ks, m, hidden)");
+  raise_status(tfa_rows_norm_scaled(part.data_ptr<float>(), part.numel() / (M * H), h_in.data_ptr(), (float)alpha,
+                                    h_out.data_ptr(), gamma.data_ptr(), xn.data_ptr(), M, H, (float)eps,
+                                    stream_of(xn)));
 }
 
 // part [ks, m, n] f32; residual / out [m, n] bf16.
@@ -741,6 +767,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "tilefoundry_amd: thin torch bindings over the gfx950 C ABI";
   m.def("abi_version", &tfa_abi_version);
   m.def("rms_norm", &rms_norm);
+  m.def("rms_norm_div", &rms_norm_div);
   m.def("add_rms_norm", &add_rms_norm);
   m.def("resid_rms_norm_partials", &resid_rms_norm_partials);
   m.def("gemv", &gemv);
@@ -763,6 +790,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("mla_attention", &mla_attention);
   m.def("mla_combine_up", &mla_combine_up);
   m.def("rows_residual", &rows_residual);
+  m.def("rows_norm_scaled", &rows_norm_scaled);
   m.def("prefill_attention", &prefill_attention);
   m.def("gemm_nt", &gemm_nt);
   m.def("qkv_norm_rope", &qkv_norm_rope);

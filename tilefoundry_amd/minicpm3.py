@@ -47,7 +47,7 @@ SHORT_FACTOR = (
 
 @dataclass(frozen=True)
 class MiniCPM3Config:
-    """examples/minicpm3_4b-cutedsl/config.json (attention-block fields)."""
+    """examples/minicpm3_4b-cutedsl/config.json."""
 
     hidden: int = 2560
     heads: int = 40
@@ -62,6 +62,16 @@ class MiniCPM3Config:
     rope_theta: float = 10000.0
     scale_depth: float = 1.4
     short_factor: tuple = field(default=SHORT_FACTOR)
+    inter: int = 6400
+    vocab: int = 73448
+    scale_emb: float = 12.0
+    dim_model_base: int = 256
+    original_max_pos: int = 32768   # rope_scaling.original_max_position_embeddings
+
+    @property
+    def logits_scaling(self) -> float:
+        """hidden / dim_model_base: MiniCPM3ForCausalLM divides the final hidden state by it."""
+        return self.hidden / self.dim_model_base
 
     @property
     def qk_dim(self) -> int:
@@ -218,3 +228,287 @@ class MLABlock:
         if e:
             raise RuntimeError(f"mla block: device error code {e}")
         return self.out
+
+
+# ------------------------------------------------------------ the whole model
+MLP_NAMES = {   # key -> Hugging Face name within layer i
+    "gamma_post": "post_attention_layernorm.weight",
+    "w_gate": "mlp.gate_proj.weight",
+    "w_up": "mlp.up_proj.weight",
+    "w_down": "mlp.down_proj.weight",
+}
+
+
+def hf_layer_names(i: int) -> dict[str, str]:
+    """Key -> published checkpoint name of every weight of layer i."""
+    return {k: f"model.layers.{i}.{v}" for k, v in {**NAMES, **MLP_NAMES}.items()}
+
+
+def synthetic_model_weights(cfg: MiniCPM3Config = MINICPM3_4B, seed: int = 0, device="cpu",
+                            std: float = 0.02) -> dict[str, torch.Tensor]:
+    """Random-init weights of the whole model under the published names and
+    ``(out, in)`` shapes (the embedding doubles as the tied head)."""
+    H, I = cfg.hidden, cfg.inter
+    out = {"model.embed_tokens.weight": synthetic.normal((cfg.vocab, H), seed, 9000, std, device=device),
+           "model.norm.weight": synthetic.normal((H,), seed, 9001, 0.1, 1.0, device=device)}
+    for i in range(cfg.layers):
+        names = hf_layer_names(i)
+        for k, v in synthetic_weights(cfg, seed, device, layer=i, std=std).items():
+            out[names[k]] = v
+        base = 20000 + 8 * i
+        out[names["gamma_post"]] = synthetic.normal((H,), seed, base, 0.1, 1.0, device=device)
+        out[names["w_gate"]] = synthetic.normal((I, H), seed, base + 1, std, device=device)
+        out[names["w_up"]] = synthetic.normal((I, H), seed, base + 2, std, device=device)
+        out[names["w_down"]] = synthetic.normal((H, I), seed, base + 3, std, device=device)
+    return out
+
+
+def sample_top_p(temperature: float = 0.8, top_p: float = 0.8, generator: torch.Generator | None = None):
+    """The sampler of examples/minicpm3_4b-cutedsl/run.py:29-47 (``_sampler``, the
+    published ``generation_config.json``: T = 0.8, top-p 0.8): softmax of
+    ``logits / T``, probabilities ranked, a token kept while the mass before it is
+    below ``top_p``, one multinomial draw over the kept mass. Runs on the device
+    the logits are on; ``generator`` makes the draws reproducible."""
+
+    def sample(logits: torch.Tensor) -> int:
+        row = logits.reshape(-1).float() / temperature
+        probs = torch.softmax(row, dim=-1)
+        order = torch.argsort(probs, descending=True)
+        ranked = probs[order]
+        keep = torch.cumsum(ranked, dim=-1) - ranked < top_p
+        ranked = torch.where(keep, ranked, torch.zeros_like(ranked))
+        return int(order[torch.multinomial(ranked, 1, generator=generator)].item())
+
+    return sample
+
+
+class MiniCPM3Engine:
+    """The whole MiniCPM3 decode model for up to 32 sequences in lockstep, one
+    captured step over all of them (examples/minicpm3_4b-cutedsl/model.py:320-420,
+    runtime twin runtime_model.py; run.py drives it token by token).
+
+    One step, 11 launches per layer plus 5:
+
+        embed            bf16(table[id] * scale_emb), then the first input norm
+        -- per layer: the MLA attention block of ``MLABlock`` ----------------
+        skinny_gemm [q_a | kv_a], mla_prep, skinny_gemm q_b, mla_q_absorb,
+        mla_attention, mla_combine_up, skinny_gemm o_proj,
+        rows_norm_scaled h1 = h + bf16(bf16(o) * a), a = scale_depth / sqrt(layers),
+                         and the post-attention norm of h1
+        -- the MLP -------------------------------------------------------------
+        skinny_gemm      gate|up + SwiGLU (interleaved rows)
+        skinny_gemm      down -> split-K partials
+        rows_norm_scaled h = h1 + bf16(bf16(down) * a) and the next layer's input
+                         norm (rows_residual after the last layer)
+        -- the head -------------------------------------------------------------
+        rms_norm_div     bf16(bf16(norm(h)) / logits_scaling)             (once)
+        skinny_gemm      head, bf16 logits, per-group winners (lowest index on ties)
+        batch_sample     greedy pick, next input id, position + 1
+
+    The compressed cache holds 576 bytes per position per layer (latent 256 +
+    rotated rope key 32, bf16). ``generate`` takes ``sampler=`` (for example
+    ``sample_top_p()``) to sample instead of taking the greedy pick: the step then
+    also keeps the bf16 logits, and the sampled id replaces the greedy one after
+    each replay (one host round trip per step, as the reference's sampler has).
+    """
+
+    MAX_BATCH = 32
+
+    def __init__(self, cfg: MiniCPM3Config = MINICPM3_4B, *, batch: int = 1, device="cuda:0",
+                 max_new: int = 512, prompt_room: int = 512, weights: dict | None = None, seed: int = 0,
+                 split: int | None = None, ks_a: int = 5, ks_qb: int = 3, ks_o: int = 5, ks_down: int = 5,
+                 capture: bool = True):
+        if cfg.kv_lora != 256 or cfg.rope != 32 or cfg.nope != 64 or cfg.v_dim != 64:
+            raise ValueError("the MLA kernels are built for kv_lora 256, rope 32, nope 64, value 64")
+        if not 1 <= batch <= self.MAX_BATCH:
+            raise ValueError(f"batch {batch} not in [1, {self.MAX_BATCH}]")
+        # positions per attention split: 128 at small batch (more blocks for one
+        # sequence), 256 once the batch alone fills the device
+        split = split if split is not None else (128 if batch <= 4 else 256)
+        self.cfg, self.batch, self.split = cfg, batch, split
+        self.device = torch.device(device)
+        self.ks = {"a": ks_a, "qb": ks_qb, "o": ks_o, "down": ks_down}
+        self.nsteps = max_new + prompt_room
+        self.cap = ((self.nsteps + split - 1) // split) * split
+        if self.cap > cfg.original_max_pos:
+            raise ValueError(f"cache of {self.cap} positions: past original_max_position_embeddings "
+                             f"({cfg.original_max_pos}) longrope switches to its long factors, not built here")
+        if weights is None:
+            weights = synthetic_model_weights(cfg, seed, self.device)
+        self._pack(weights)
+        del weights
+        self.cos, self.sin = rope_tables(self.cap, cfg, self.device)
+        self.alpha = cfg.residual_scale
+        self._buffers()
+        self.sampler = None
+        self.graph = None
+        if capture:
+            self._capture()
+
+    def _pack(self, wts):
+        cfg, dev = self.cfg, self.device
+
+        def get(name):
+            return wts[name].to(dev, BF16).contiguous()
+
+        self.embed = get("model.embed_tokens.weight")
+        self.gamma_final = get("model.norm.weight")
+        self.head = get("lm_head.weight") if "lm_head.weight" in wts else self.embed
+        self.layers = []
+        for i in range(cfg.layers):
+            n = hf_layer_names(i)
+            gate, up = get(n["w_gate"]), get(n["w_up"])
+            self.layers.append({
+                "gamma_in": get(n["gamma_in"]),
+                "w_a": torch.cat((get(n["w_q_a"]), get(n["w_kv_a"])), 0).contiguous(),
+                "gamma_q_a": get(n["gamma_q_a"]),
+                "w_q_b": get(n["w_q_b"]),
+                "gamma_kv_a": get(n["gamma_kv_a"]),
+                "w_kv_b": get(n["w_kv_b"]),
+                "w_o": get(n["w_o"]),
+                "gamma_post": get(n["gamma_post"]),
+                "w_gu": torch.stack([gate, up], 1).reshape(2 * cfg.inter, cfg.hidden).contiguous(),
+                "w_down": get(n["w_down"]),
+            })
+            del gate, up
+
+    def _buffers(self):
+        cfg, B, dev, ks = self.cfg, self.batch, self.device, self.ks
+        f32 = torch.float32
+
+        def z(*shape, dtype=BF16):
+            return torch.zeros(*shape, device=dev, dtype=dtype)
+
+        H, NH = cfg.hidden, cfg.heads
+        self.ns = self.cap // self.split
+        self.h = z(B, H)
+        self.h1 = z(B, H)
+        self.xn = z(B, H)
+        self.part_a = z(ks["a"], B, cfg.q_lora + cfg.kv_lora + cfg.rope, dtype=f32)
+        self.q_n = z(B, cfg.q_lora)
+        self.part_qb = z(ks["qb"], B, NH * cfg.qk_dim, dtype=f32)
+        self.q_abs = z(B, NH, cfg.kv_lora + cfg.rope)
+        self.latent = z(cfg.layers, B, self.cap, cfg.kv_lora)
+        self.rope_k = z(cfg.layers, B, self.cap, cfg.rope)
+        self.op = z(B, self.ns, NH, cfg.kv_lora)
+        self.mp = z(B, self.ns, NH, dtype=f32)
+        self.lp = z(B, self.ns, NH, dtype=f32)
+        self.attn = z(B, NH * cfg.v_dim)
+        self.part_o = z(ks["o"], B, H, dtype=f32)
+        self.act = z(B, cfg.inter)
+        self.part_d = z(ks["down"], B, H, dtype=f32)
+        self.logits = z(B, cfg.vocab, dtype=f32)
+        nb = C.skinny_blocks(cfg.vocab)
+        self.bv = z(B, nb, dtype=f32)
+        self.bi = z(B, nb, dtype=torch.int32)
+        self.pos = z(B, dtype=torch.int32)
+        self.ids = z(B, dtype=torch.int64)
+        self.inp = z(B, self.nsteps, dtype=torch.int32)
+        self.sam = z(B, self.nsteps, dtype=torch.int32)
+        self.plen = z(B, dtype=torch.int32)
+        self.err = z(1, dtype=torch.int32)
+
+    def _step(self, keep_logits: bool = True):
+        cfg, ks = self.cfg, self.ks
+        L = len(self.layers)
+        C.embed(self.embed, self.ids, self.h, cfg.scale_emb, self.err)
+        C.rms_norm(self.h, self.layers[0]["gamma_in"], self.xn, cfg.eps, 0)
+        for i, w in enumerate(self.layers):
+            lat, rk = self.latent[i], self.rope_k[i]
+            C.skinny_gemm(self.xn, w["w_a"], ks["a"], 0, self.part_a, None, None, None, None)
+            C.mla_prep(self.part_a, w["gamma_q_a"], w["gamma_kv_a"], cfg.lora_eps, self.cos, self.sin,
+                       self.pos, lat, rk, self.q_n, self.err)
+            C.skinny_gemm(self.q_n, w["w_q_b"], ks["qb"], 0, self.part_qb, None, None, None, None)
+            C.mla_q_absorb(self.part_qb, w["w_kv_b"], self.cos, self.sin, self.pos, self.q_abs, self.err)
+            C.mla_attention(self.q_abs, lat, rk, self.pos, self.split, cfg.scale, self.op, self.mp,
+                            self.lp, self.err)
+            C.mla_combine_up(self.op, self.mp, self.lp, self.pos, self.split, w["w_kv_b"], self.attn)
+            C.skinny_gemm(self.attn, w["w_o"], ks["o"], 0, self.part_o, None, None, None, None)
+            C.rows_norm_scaled(self.part_o, self.h, self.alpha, self.h1, w["gamma_post"], self.xn, cfg.eps)
+            C.skinny_gemm(self.xn, w["w_gu"], 1, 1, None, self.act, None, None, None)
+            C.skinny_gemm(self.act, w["w_down"], ks["down"], 0, self.part_d, None, None, None, None)
+            if i + 1 < L:   # the residual fused with the next layer's input norm
+                C.rows_norm_scaled(self.part_d, self.h1, self.alpha, self.h, self.layers[i + 1]["gamma_in"],
+                                   self.xn, cfg.eps)
+            else:
+                C.rows_residual(self.part_d, self.h1, self.alpha, self.h)
+        C.rms_norm_div(self.h, self.gamma_final, self.xn, cfg.eps, cfg.logits_scaling)
+        C.skinny_gemm(self.xn, self.head, 1, 3, None, None, self.logits if keep_logits else None,
+                      self.bv, self.bi)
+        C.batch_sample_step(self.bv, self.bi, self.inp, self.plen, self.ids, self.pos, self.sam,
+                            self.err)
+
+    def _capture(self):
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        self._load([[0]] * self.batch, 1)
+        with torch.cuda.stream(side):
+            self._step()  # every kernel has run once before capture
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+        self._load([[0]] * self.batch, 1)
+
+    def _run_step(self):
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self._step()
+
+    def _load(self, rows: list[list[int]], plen: int):
+        if len(rows) != self.batch:
+            raise ValueError(f"{len(rows)} sequences given to an engine of batch {self.batch}")
+        if any(len(r) != len(rows[0]) for r in rows):
+            raise ValueError("sequences of one batch advance in lockstep: give equal lengths")
+        if len(rows[0]) > self.nsteps:
+            raise ValueError(f"{len(rows[0])} input ids exceed this engine's {self.nsteps} steps")
+        if any(not 0 <= t < self.cfg.vocab for r in rows for t in r):
+            raise ValueError(f"token ids out of range [0, {self.cfg.vocab})")
+        self.pos.zero_()
+        self.sam.zero_()
+        self.err.zero_()
+        self.inp.zero_()
+        self.inp[:, : len(rows[0])] = torch.tensor(rows, dtype=torch.int32, device=self.device)
+        self.plen.fill_(plen)
+        self.ids.copy_(torch.tensor([r[0] for r in rows], dtype=torch.int64, device=self.device))
+
+    def check_device_errors(self):
+        code = int(self.err.item())
+        if code:
+            raise RuntimeError(f"a decode kernel found an index out of range (code {code})")
+
+    def generate(self, prompts: list[list[int]], max_new: int, sampler=None):
+        """Walk every prompt, then continue each for ``max_new`` tokens, greedy
+        (lowest-index argmax over the bf16 logits) or drawn by ``sampler(logits)``.
+        Returns ``qwen3.Generated``; timing covers the continuation steps only."""
+        from time import perf_counter
+
+        from .qwen3 import Generated
+
+        if not prompts or not prompts[0]:
+            raise ValueError("decode needs prompts of at least one token")
+        pl = len(prompts[0])
+        if pl + max_new > self.nsteps:
+            raise ValueError(f"prompt {pl} + {max_new} new exceeds this engine's {self.nsteps} steps")
+        self._load([list(p) for p in prompts], pl)
+        torch.cuda.synchronize(self.device)
+        t0 = perf_counter()
+        for _ in range(pl - 1):
+            self._run_step()
+        torch.cuda.synchronize(self.device)
+        t1 = perf_counter()
+        for s in range(max_new):
+            self._run_step()
+            if sampler is not None:
+                p = pl - 1 + s
+                picks = [sampler(self.logits[b]) for b in range(self.batch)]
+                t = torch.tensor(picks, dtype=torch.int64, device=self.device)
+                self.ids.copy_(t)
+                self.sam[:, p] = t.to(torch.int32)
+        torch.cuda.synchronize(self.device)
+        t2 = perf_counter()
+        self.check_device_errors()
+        out = self.sam[:, pl - 1: pl - 1 + max_new].tolist()
+        return Generated(out, t2 - t1, t1 - t0, pl)
