@@ -85,41 +85,68 @@ __global__ __launch_bounds__(kThreads) void mla_prep_kernel(
     return round_bf(sum_splits(pb + i, kstride, ks));   // the projection lands in bf16
   };
 
-  // q_a -> LoRA norm
+  // Every load this thread needs goes out before any arithmetic (one memory
+  // round trip): the position, both norm scales, the split-K partials, and
+  // the rope table row (behind the position's scalar load only).
+  const int p_raw = pos[b];
+  float gqv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = t + kThreads * j;
+    gqv[j] = i < qa ? bf2f(gq[i]) : 0.f;
+  }
+  const float gk = bf2f(gkv[t]);
+  // q_a -> LoRA norm; kv_c -> LoRA norm (the latent); the rope slice
   float qv[4];
-  float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int i = t + kThreads * j;
     qv[j] = i < qa ? reduced(i) : 0.f;
-    ss += qv[j] * qv[j];
   }
-  // kv_c -> LoRA norm (the latent); the rope slice
   const float cv = reduced(qa + t);
   if (t < kRope) kr[t] = reduced(qa + kLat + t);
-  const float rq = rsqrt_rn(block_sum(ss, scratch[0]) / static_cast<float>(qa) + eps);
-  const float rk = rsqrt_rn(block_sum(cv * cv, scratch[1]) / static_cast<float>(kLat) + eps);
+  const bool p_ok = p_raw >= 0 && p_raw < cap && p_raw < rope_rows;
+  float c = 0.f, s = 0.f;
+  if (t < kRope && p_ok) {
+    c = bf2f(cos_t[static_cast<size_t>(p_raw) * kRope + t]);
+    s = bf2f(sin_t[static_cast<size_t>(p_raw) * kRope + t]);
+  }
+  // both sums of squares in one block reduction (waves summed in order)
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ss += qv[j] * qv[j];
+  ss = wave_sum(ss);
+  const float sk = wave_sum(cv * cv);
+  const int lane = t & (kWave - 1), wid = t / kWave;
+  if (lane == 0) {
+    scratch[0][wid] = ss;
+    scratch[1][wid] = sk;
+  }
+  __syncthreads();   // also publishes kr
+  float tq = 0.f, tk = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    tq += scratch[0][w];
+    tk += scratch[1][w];
+  }
+  const float rq = rsqrt_rn(tq / static_cast<float>(qa) + eps);
+  const float rk = rsqrt_rn(tk / static_cast<float>(kLat) + eps);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int i = t + kThreads * j;
     if (i < qa)
-      q_n[static_cast<size_t>(b) * qa + i] =
-          static_cast<uint16_t>(f2bf(round_bf(qv[j] * rq) * bf2f(gq[i])));
+      q_n[static_cast<size_t>(b) * qa + i] = static_cast<uint16_t>(f2bf(round_bf(qv[j] * rq) * gqv[j]));
   }
-  const int p = pos[b];
-  if (p < 0 || p >= cap || p >= rope_rows) {
+  if (!p_ok) {
     if (t == 0) set_err(err, 6);
     return;
   }
-  lat_cache[(static_cast<size_t>(b) * cap + p) * kLat + t] =
-      static_cast<uint16_t>(f2bf(round_bf(cv * rk) * bf2f(gkv[t])));
-  if (t < kRope) {   // kr was written before the block sums' barriers
+  const int p = p_raw;
+  lat_cache[(static_cast<size_t>(b) * cap + p) * kLat + t] = static_cast<uint16_t>(f2bf(round_bf(cv * rk) * gk));
+  if (t < kRope) {
     const float x = kr[t];
     const float partner = t < kRope / 2 ? -kr[t + kRope / 2] : kr[t - kRope / 2];
-    const float c = bf2f(cos_t[static_cast<size_t>(p) * kRope + t]);
-    const float s = bf2f(sin_t[static_cast<size_t>(p) * kRope + t]);
-    rope_cache[(static_cast<size_t>(b) * cap + p) * kRope + t] =
-        static_cast<uint16_t>(f2bf(rope_bf(x, partner, c, s)));
+    rope_cache[(static_cast<size_t>(b) * cap + p) * kRope + t] = static_cast<uint16_t>(f2bf(rope_bf(x, partner, c, s)));
   }
 }
 

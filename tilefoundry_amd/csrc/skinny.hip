@@ -308,6 +308,14 @@ __global__ __launch_bounds__(kThreads) void rows_norm_kernel(
   } else {
     src = h_in + static_cast<size_t>(m) * H;
   }
+  // gamma goes out with the row's own loads: it is not needed until after the
+  // reduction, and loading it there would add a second memory round trip
+  uint4 gq[kRowChunks];
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int ch = t + c * kThreads;
+    if (ch < nch) gq[c] = ld16(gamma + 8 * ch);
+  }
   float v[kRowChunks][8];
   float ss = 0.f;
 #pragma unroll
@@ -334,7 +342,7 @@ __global__ __launch_bounds__(kThreads) void rows_norm_kernel(
     if (ch >= nch) continue;
     st16(h_out + static_cast<size_t>(m) * H + 8 * ch, pack8(v[c]));
     float g[8], y[8];
-    unpack8(ld16(gamma + 8 * ch), g);
+    unpack8(gq[c], g);
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = round_bf(round_bf(v[c][i] * rs) * g[i]);
     st16(xn + static_cast<size_t>(m) * H + 8 * ch, pack8(y));
