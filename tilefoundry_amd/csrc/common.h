@@ -62,6 +62,12 @@ TFA_DEV uint4 ld16_stream(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 TFA_DEV void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+// Streaming store for outputs no kernel of this launch reads back and the next
+// does not read straight from L2 (many-row passes): non-temporal hint.
+TFA_DEV void st16_stream(void* p, uint4 v) {
+  const u32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+}
 
 // ---------------------------------------------------------------- reductions
 TFA_DEV float wave_sum(float v) {
