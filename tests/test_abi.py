@@ -216,3 +216,19 @@ def test_torch_extension_rejects_host_tensors():
         ops.rms_norm(x, g, 1e-6)
     with pytest.raises(ValueError, match="GPU tensor"):
         ops.gemv(torch.zeros(64, dtype=torch.bfloat16), torch.zeros(8, 64, dtype=torch.bfloat16))
+
+
+def test_integration_stub_argtypes_match_the_header():
+    """Every ctypes binding shown in INTEGRATION.md passes as many arguments as
+    the header declares for that entry point."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    decls = {m.group(1): m.group(2) for m in re.finditer(r"\b(tfa_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S)}
+    stub = (ROOT / "INTEGRATION.md").read_text()
+    bound = re.findall(r"L\.(tfa_\w+)\.argtypes\s*=\s*\[([^\]]*)\]", stub, flags=re.S)
+    assert len(bound) >= 8
+    for name, args in bound:
+        assert name in decls, f"{name} is bound in INTEGRATION.md but not declared"
+        params = decls[name].strip()
+        n_decl = 0 if params in ("", "void") else params.count(",") + 1
+        n_stub = len([a for a in args.split(",") if a.strip()])
+        assert n_stub == n_decl, f"{name}: {n_stub} argtypes, {n_decl} declared parameters"
