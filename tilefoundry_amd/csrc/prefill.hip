@@ -77,14 +77,12 @@ struct FlashArgs {
   float scale_log2;      // head_dim^-1/2 * log2(e)
 };
 
-// LDS tiles hold one key per row. K rows are padded by 16 bytes (+4 banks per
-// row): the K operand read (16 rows, one 16-byte chunk per half-wave) is
-// conflict-free. V rows are padded by 64 bytes (+16 banks per row): the
-// transpose reads (4 rows x 64 bytes per half-wave) are conflict-free. Both
-// hold for 256- and 512-byte rows. Every operand address is one per-lane base
-// plus an immediate offset.
-constexpr int kKPF = 4;           // K operand reads in flight ahead of the score MFMAs
-constexpr int kVPF = 3;           // V^T operand pairs in flight ahead of the output MFMAs
+// LDS tiles hold one key per row, unpadded, so one DMA instruction fills 1 KB
+// (2 rows at head_dim 256, 4 at 128). Each row's 16-byte chunks are XOR-
+// swizzled instead: K row r by (r & 15), so the K operand read (16 rows, one
+// chunk each per 16 lanes) hits 16 distinct bank quads; V row r by 4 (r & 3),
+// so the transpose reads (4 rows x 64 bytes per 32 lanes) cover the 64 banks
+// once. Every operand address is one per-lane base plus an immediate offset.
 // sched_group_barrier instruction classes
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
@@ -112,20 +110,30 @@ void flash_prefill_kernel(const FlashArgs a) {
   constexpr int kBM = kWM * W;                 // query rows per block
   constexpr int kStages = W == 8 ? 3 : 2;      // loads run kStages - 1 tiles ahead
   constexpr int kRowsPerWave = kBN / W;        // K and V rows each wave moves per tile
-  constexpr int kTileVm = 2 * kRowsPerWave;    // DMA instructions per wave per tile
+  constexpr int kKPitch = D;                   // elements: rows are unpadded, chunks swizzled
+  constexpr int kVPitch = D;
+  constexpr int kRowBytes = 2 * D;
+  constexpr int kCPR = D / 8;                  // 16-byte chunks per row
+  constexpr int kRPI = kWave / kCPR;           // rows one 1 KB DMA instruction fills
+  constexpr int kInstr = kRowsPerWave / kRPI;  // DMA instructions per wave per tile, for K and for V
+  static_assert(kRowsPerWave % kRPI == 0, "a wave's rows fill whole DMA instructions");
+  constexpr int kTileVm = 2 * kInstr;          // DMA instructions per wave per tile
   constexpr int kWaitStep = waitcnt_vm(kStages == 3 ? kTileVm : 0);
-  constexpr int kKPitch = D + 8;               // elements
-  constexpr int kVPitch = D + 32;
   constexpr int kDT = D / 32;                  // 32-dim output tiles
   constexpr int kST = D / 16;                  // 16-dim score k-steps
-  constexpr int kRowLanes = D / 8;             // lanes moving one K or V row (16 bytes each)
+  // K operand reads and V^T operand pairs in flight ahead of their MFMAs:
+  // 4 and 3, or 3 and 2 where the 128-row, head_dim-256 block would otherwise
+  // spill (its four DMA instructions per tile leave no room for more)
+  constexpr bool kTight = W == 4 && D == 256;
+  constexpr int kKPF = kTight ? 3 : 4;
+  constexpr int kVPF = kTight ? 2 : 3;
   // one LDS object per ring stage, indexed only by compile-time stage numbers
-  __shared__ __attribute__((aligned(16))) uint16_t ks0[kBN][kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t ks1[kBN][kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t ks2[kStages == 3 ? kBN : 1][kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t vs0[kBN][kVPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t vs1[kBN][kVPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t vs2[kStages == 3 ? kBN : 1][kVPitch];
+  __shared__ __attribute__((aligned(1024))) uint16_t ks0[kBN][kKPitch];
+  __shared__ __attribute__((aligned(1024))) uint16_t ks1[kBN][kKPitch];
+  __shared__ __attribute__((aligned(1024))) uint16_t ks2[kStages == 3 ? kBN : 1][kKPitch];
+  __shared__ __attribute__((aligned(1024))) uint16_t vs0[kBN][kVPitch];
+  __shared__ __attribute__((aligned(1024))) uint16_t vs1[kBN][kVPitch];
+  __shared__ __attribute__((aligned(1024))) uint16_t vs2[kStages == 3 ? kBN : 1][kVPitch];
   auto kbuf = [&](auto b) __attribute__((always_inline)) -> uint16_t(*)[kKPitch] {
     if constexpr (decltype(b)::value == 0) return ks0;
     else if constexpr (decltype(b)::value == 1) return ks1;
@@ -167,25 +175,29 @@ void flash_prefill_kernel(const FlashArgs a) {
   const int ntiles = (kend + kBN - 1) / kBN;
   const int my_last = min((q0 + kWM - 1) / kBN, ntiles - 1);   // the wave's last tile with a visible key
 
-  // direct global -> LDS tile loads, one K or V row per instruction (lanes
-  // 0 .. D/8-1): wave w moves rows R w .. R w + R - 1 of K and of V (R = 32 / W).
-  // Rows past N repeat row N - 1 (only rows past N see them, and those rows
-  // are not stored). Every step issues exactly one tile's loads (past the last
-  // tile it reloads the last tile into a free stage, where nothing reads it),
-  // so the number of loads in flight behind tile kt is constant and so is
-  // every wait count.
+  // Direct global -> LDS tile loads, 1 KB per instruction: the 64 lanes fill
+  // kRPI whole rows (lane l: row l / kCPR, physical chunk l % kCPR). Rows are
+  // unpadded; a row's 16-byte chunks are XOR-swizzled so that the operand
+  // reads below hit distinct banks -- K row r keeps logical chunk c at
+  // physical chunk c ^ (r & 15), V row r at c ^ 4 (r & 3) -- so each lane
+  // fetches the logical chunk its physical slot holds. Wave w moves rows
+  // R w .. R w + R - 1 of K and of V (R = 32 / W). Rows past N repeat row
+  // N - 1 (only rows past N see them, and those rows are not stored). Every
+  // step issues exactly one tile's loads (past the last tile it reloads the
+  // last tile into a free stage, where nothing reads it), so the number of
+  // loads in flight behind tile kt is constant and so is every wait count.
+  const int dma_row = lane / kCPR, dma_chunk = lane % kCPR;
   auto load_tile = [&](int kt, auto bs) __attribute__((always_inline)) {
     kt = kt < ntiles ? kt : ntiles - 1;
-    const int r0 = kt * kBN + kRowsPerWave * wid;
     uint16_t(*kb)[kKPitch] = kbuf(bs);
     uint16_t(*vb)[kVPitch] = vbuf(bs);
-    if (lane < kRowLanes) {
 #pragma unroll
-      for (int i = 0; i < kRowsPerWave; ++i) {
-        const size_t r = static_cast<size_t>(min(r0 + i, N - 1));
-        lds_dma16(kseq + r * a.k_rs + 8 * lane, lds_offset(&kb[kRowsPerWave * wid + i][0]));
-        lds_dma16(vseq + r * a.v_rs + 8 * lane, lds_offset(&vb[kRowsPerWave * wid + i][0]));
-      }
+    for (int i = 0; i < kInstr; ++i) {
+      const int t0 = kRowsPerWave * wid + kRPI * i;     // first tile row of this instruction
+      const int trow = t0 + dma_row;
+      const size_t r = static_cast<size_t>(min(kt * kBN + trow, N - 1));
+      lds_dma16(kseq + r * a.k_rs + 8 * (dma_chunk ^ (trow & 15)), lds_offset(&kb[t0][0]));
+      lds_dma16(vseq + r * a.v_rs + 8 * (dma_chunk ^ (4 * (trow & 3))), lds_offset(&vb[t0][0]));
     }
   };
 
@@ -224,6 +236,17 @@ void flash_prefill_kernel(const FlashArgs a) {
 
   const int L = lane & 15;
   const int half16 = (lane >> 4) & 1;
+  // Swizzled operand addresses: one per-lane base plus an immediate. K: lane
+  // (key n32, k-group kg) reads logical chunk 2 st + kg of row n32, physical
+  // (2 st + kg) ^ s with s = n32 & 15, i.e. byte 32 (st ^ (s >> 1)) + 16 (kg ^ (s & 1))
+  // -- 256 (st >> 3) an immediate. V: the
+  // transpose read of rows 4 kg + L / 4 (+ 8, + 16 ks2) at chunk
+  // 2 half16 + (L & 3) / 2 + 4 dt, physical ... + 4 (dt ^ q) with q = (L / 4) & 3
+  // -- the swizzle bits (5-7 for K, 6-7 for V) are zero in the rest of the
+  // lane's base, so each address is that base XOR a compile-time constant.
+  const int k_base = n32 * kRowBytes + 16 * (kg ^ (n32 & 1)) + 32 * ((n32 & 15) >> 1);
+  const int v_base = (4 * kg + (L >> 2)) * kRowBytes + 16 * (2 * half16 + ((L & 3) >> 1)) + 8 * (L & 1) +
+                     64 * ((L >> 2) & 3);
   // One key tile in ring stage `bs`. The block barrier is a bare s_barrier
   // between compiler fences: each wave first waits for its own loads of tile
   // kt (the only ones in flight), and its reads of the stage being refilled --
@@ -247,14 +270,21 @@ void flash_prefill_kernel(const FlashArgs a) {
         for (int e = 0; e < 16; ++e) s[t][e] = 0.f;
       // K operands stream through a ring of kKPF registers: the read for
       // k-step st + kKPF is issued behind the MFMA of k-step st
-      const uint16_t* krow = &kb[n32][8 * kg];
+      const char* kbytes = reinterpret_cast<const char*>(&kb[0][0]);
+      // opaque per tile: the XORs below are recomputed, not hoisted into a
+      // register per k-step (which would not fit beside the accumulators)
+      int kx = k_base;
+      asm volatile("" : "+v"(kx));
+      auto kld = [&](int st) __attribute__((always_inline)) {
+        return *reinterpret_cast<const uint4*>(kbytes + (kx ^ (32 * (st & 7))) + 256 * (st >> 3));
+      };
       uint4 kq[kKPF];
 #pragma unroll
-      for (int i = 0; i < kKPF; ++i) kq[i] = *reinterpret_cast<const uint4*>(krow + 16 * i);
+      for (int i = 0; i < kKPF; ++i) kq[i] = kld(i);
 #pragma unroll
       for (int st = 0; st < kST; ++st) {
         const uint4 kop = kq[st % kKPF];
-        if (st + kKPF < kST) kq[st % kKPF] = *reinterpret_cast<const uint4*>(krow + 16 * (st + kKPF));
+        if (st + kKPF < kST) kq[st % kKPF] = kld(st + kKPF);
 #pragma unroll
         for (int t = 0; t < QT; ++t)
           s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kop), as_bf8(qop[t][st]), s[t], 0, 0, 0);
@@ -294,7 +324,9 @@ void flash_prefill_kernel(const FlashArgs a) {
       // O^T += V^T . P^T: k-step ks2 takes keys 16 ks2 + {4kg + r, 8 + 4kg + r}
       // = score elements 8 ks2 + r, 8 ks2 + 4 + r; each V^T operand serves
       // every query tile
-      const uint16_t* vrow = &vb[4 * kg + (L >> 2)][16 * half16 + 4 * (L & 3)];
+      const char* vbytes = reinterpret_cast<const char*>(&vb[0][0]);
+      int vx = v_base;
+      asm volatile("" : "+v"(vx));
       uint4 pop[2][QT];
 #pragma unroll
       for (int ks2 = 0; ks2 < 2; ++ks2)
@@ -313,8 +345,9 @@ void flash_prefill_kernel(const FlashArgs a) {
       constexpr int kNPV = 2 * kDT;
       auto vld = [&](int i, uint2* dst) __attribute__((always_inline)) {
         const int ks2 = i / kDT, dt = i % kDT;
-        dst[0] = ld_tr(vrow + 16 * ks2 * kVPitch + 32 * dt);
-        dst[1] = ld_tr(vrow + (16 * ks2 + 8) * kVPitch + 32 * dt);
+        const char* p = vbytes + (vx ^ (64 * (dt & 3))) + 256 * (dt >> 2) + 16 * ks2 * kRowBytes;
+        dst[0] = ld_tr(reinterpret_cast<const uint16_t*>(p));
+        dst[1] = ld_tr(reinterpret_cast<const uint16_t*>(p + 8 * kRowBytes));
       };
       uint2 vq[kVPF][2];
 #pragma unroll
