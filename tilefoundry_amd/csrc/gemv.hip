@@ -262,12 +262,12 @@ int dispatch_k(const GemvArgs& a, hipStream_t s, const char* name) {
 }
 
 // Rows per block: enough blocks to cover 256 CUs a few times over. Measured on
-// the decode step's shapes: 8 rows only from 8192 rows up (gate|up), 2 rows up
-// to 2048 rows (o_proj 3.75 -> 3.64 us, down 6.16 -> 6.02 us), 4 otherwise
-// (q|k|v 4096 x 2048: 5.73 -> 5.61 us against 8 rows).
+// the decode step's shapes: 2 rows up to 2048 rows (o_proj 3.75 -> 3.64 us,
+// down 6.16 -> 6.02 us), 4 up to 16383 (q|k|v 4096 x 2048: 5.73 -> 5.61 us
+// against 8 rows; gate|up 12288 x 2048 the same at 4 or 8), 8 beyond.
 template <int PRO, int EPI>
 int dispatch_rows(const GemvArgs& a, hipStream_t s, const char* name) {
-  if (a.N >= 8192 && a.K <= 4096) return dispatch_k<8, PRO, EPI>(a, s, name);
+  if (a.N >= 16384 && a.K <= 4096) return dispatch_k<8, PRO, EPI>(a, s, name);
   if (a.N <= 2048) return dispatch_k<2, PRO, EPI>(a, s, name);
   return dispatch_k<4, PRO, EPI>(a, s, name);
 }
