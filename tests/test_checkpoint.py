@@ -169,3 +169,110 @@ def test_engine_untied_head_against_oracle(dev, tmp_path):
     for p, t in enumerate(prompt):
         ref = OQ.step(om, oc, t, p, caches, cos, sin, p_bf16=True)
     assert_close("untied-head logits", got, ref)
+
+
+# ------------------------------------------------------------------ MiniCPM3
+def _minicpm3_hf_config(cfg, tied=True):
+    return {"architectures": ["MiniCPM3ForCausalLM"], "hidden_act": "silu", "hidden_size": cfg.hidden,
+            "num_hidden_layers": cfg.layers, "intermediate_size": cfg.inter, "num_attention_heads": cfg.heads,
+            "num_key_value_heads": cfg.heads, "qk_nope_head_dim": cfg.nope, "qk_rope_head_dim": cfg.rope,
+            "q_lora_rank": cfg.q_lora, "kv_lora_rank": cfg.kv_lora, "rms_norm_eps": cfg.eps,
+            "rope_scaling": {"type": "longrope", "long_factor": list(cfg.short_factor),
+                             "short_factor": list(cfg.short_factor),
+                             "original_max_position_embeddings": cfg.original_max_pos},
+            "vocab_size": cfg.vocab, "scale_emb": cfg.scale_emb, "dim_model_base": cfg.dim_model_base,
+            "scale_depth": cfg.scale_depth, "tie_word_embeddings": tied, "max_position_embeddings": 32768}
+
+
+def _write_minicpm3(path, cfg, wts, shards=1, bin_file=False):
+    from safetensors.torch import save_file
+
+    path.mkdir(parents=True, exist_ok=True)
+    (path / "config.json").write_text(json.dumps(_minicpm3_hf_config(cfg)))
+    cpu = {k: v.detach().to("cpu").contiguous() for k, v in wts.items()}
+    if bin_file:
+        torch.save(cpu, str(path / "pytorch_model.bin"))
+        return path
+    names = sorted(cpu)
+    if shards == 1:
+        save_file(cpu, str(path / "model.safetensors"))
+        return path
+    wm = {}
+    for s in range(shards):
+        part = names[s::shards]
+        fname = f"model-{s + 1:05d}-of-{shards:05d}.safetensors"
+        save_file({k: cpu[k] for k in part}, str(path / fname))
+        wm.update(dict.fromkeys(part, fname))
+    (path / "model.safetensors.index.json").write_text(json.dumps({"metadata": {}, "weight_map": wm}))
+    return path
+
+
+def test_minicpm3_published_config():
+    from pathlib import Path
+
+    from tilefoundry_amd.checkpoint import minicpm3_config
+    from tilefoundry_amd.minicpm3 import MINICPM3_4B
+
+    cfg = minicpm3_config(Path(__file__).parent / "golden" / "minicpm3_4b_config")
+    assert cfg == MINICPM3_4B
+    assert cfg.logits_scaling == 10.0
+
+
+@pytest.mark.parametrize("form", ["single", "sharded", "bin"])
+def test_minicpm3_round_trip(tmp_path, form):
+    from dataclasses import replace
+
+    from tilefoundry_amd.checkpoint import load_minicpm3
+    from tilefoundry_amd.minicpm3 import MINICPM3_4B, synthetic_model_weights
+
+    cfg = replace(MINICPM3_4B, hidden=256, heads=4, q_lora=96, kv_lora=64, inter=512, vocab=512, layers=2,
+                  dim_model_base=64)
+    wts = synthetic_model_weights(cfg, seed=3)
+    _write_minicpm3(tmp_path, cfg, wts, shards=3 if form == "sharded" else 1, bin_file=form == "bin")
+    got_cfg, got = load_minicpm3(tmp_path)
+    assert got_cfg == cfg
+    assert sorted(got) == sorted(wts)
+    for k, v in wts.items():
+        assert torch.equal(got[k], v), k
+
+
+def test_minicpm3_checkpoint_errors(tmp_path):
+    from dataclasses import replace
+
+    from tilefoundry_amd.checkpoint import load_minicpm3
+    from tilefoundry_amd.minicpm3 import MINICPM3_4B, synthetic_model_weights
+
+    with pytest.raises(FileNotFoundError):
+        (tmp_path / "empty").mkdir()
+        load_minicpm3(tmp_path / "empty")
+    cfg = replace(MINICPM3_4B, hidden=256, heads=4, q_lora=96, kv_lora=64, inter=512, vocab=512, layers=1,
+                  dim_model_base=64)
+    wts = synthetic_model_weights(cfg, seed=4)
+    p = _write_minicpm3(tmp_path / "yarn", cfg, wts)
+    c = json.loads((p / "config.json").read_text())
+    c["rope_scaling"]["type"] = "yarn"
+    (p / "config.json").write_text(json.dumps(c))
+    with pytest.raises(ValueError, match="longrope"):
+        load_minicpm3(p)
+    short = {k: v for k, v in wts.items() if "kv_b_proj" not in k}
+    with pytest.raises(KeyError, match="kv_b_proj"):
+        load_minicpm3(_write_minicpm3(tmp_path / "short", cfg, short))
+
+
+@pytest.mark.gpu
+def test_minicpm3_engine_from_checkpoint(dev, tmp_path):
+    """A 2-layer MiniCPM3-4B-shaped checkpoint (published layer shapes, vocab 4096)
+    decodes the same ids through ``MiniCPM3Engine.from_checkpoint`` as the engine
+    built from the same weights in memory."""
+    from dataclasses import replace
+
+    from tilefoundry_amd.minicpm3 import MINICPM3_4B, MiniCPM3Engine, synthetic_model_weights
+
+    cfg = replace(MINICPM3_4B, layers=2, vocab=4096)
+    wts = synthetic_model_weights(cfg, seed=5)
+    _write_minicpm3(tmp_path, cfg, wts, shards=2)
+    prompt = [[7, 70, 700, 3000]]
+    want = MiniCPM3Engine(cfg, device=dev, max_new=16, prompt_room=8, weights=wts).generate(prompt, 10).tokens
+    eng = MiniCPM3Engine.from_checkpoint(tmp_path, device=dev, max_new=16, prompt_room=8)
+    assert eng.cfg == cfg
+    assert eng.generate(prompt, 10).tokens == want

@@ -147,3 +147,100 @@ def load_qwen3(path: str | Path, device="cpu", cfg=None) -> tuple:
             raise ValueError(f"checkpoint weight {name}: shape {tuple(t.shape)}, the config says {shape}")
         out[name] = t
     return cfg, out
+
+
+# ------------------------------------------------------------------ MiniCPM3
+def minicpm3_config(path: str | Path):
+    """``config.json`` of a MiniCPM3 checkpoint (the fields of
+    examples/minicpm3_4b-cutedsl/config.json) -> ``minicpm3.MiniCPM3Config``. A
+    rope scaling other than longrope, or longrope whose short and long factors
+    differ while the cache could pass ``original_max_position_embeddings``, is
+    for the engine to refuse; here the fields are only read."""
+    from dataclasses import replace
+
+    from .minicpm3 import MINICPM3_4B
+
+    with open(Path(path) / "config.json", encoding="utf-8") as fh:
+        c = json.load(fh)
+    if c.get("hidden_act", "silu") != "silu":
+        raise ValueError(f"config.json: hidden_act {c['hidden_act']!r}, only silu is supported")
+    rs = c.get("rope_scaling") or {}
+    if rs and rs.get("type", rs.get("rope_type")) != "longrope":
+        raise ValueError(f"config.json: rope_scaling type {rs.get('type')!r}, only longrope is supported")
+    heads = int(c["num_attention_heads"])
+    if int(c.get("num_key_value_heads", heads)) != heads:
+        raise ValueError("config.json: MLA needs num_key_value_heads == num_attention_heads")
+    short = tuple(float(x) for x in rs.get("short_factor", MINICPM3_4B.short_factor))
+    hidden = int(c["hidden_size"])
+    return replace(
+        MINICPM3_4B, hidden=hidden, heads=heads, q_lora=int(c["q_lora_rank"]), kv_lora=int(c["kv_lora_rank"]),
+        nope=int(c["qk_nope_head_dim"]), rope=int(c["qk_rope_head_dim"]),
+        v_dim=int(c.get("v_head_dim", c["qk_nope_head_dim"])), layers=int(c["num_hidden_layers"]),
+        eps=float(c.get("rms_norm_eps", 1e-5)), rope_theta=float(c.get("rope_theta", 10000.0)),
+        scale_depth=float(c.get("scale_depth", 1.4)), short_factor=short, inter=int(c["intermediate_size"]),
+        vocab=int(c["vocab_size"]), scale_emb=float(c.get("scale_emb", 1.0)),
+        dim_model_base=int(c.get("dim_model_base", hidden)),
+        original_max_pos=int(rs.get("original_max_position_embeddings", c.get("max_position_embeddings", 32768))))
+
+
+class _TorchBinCheckpoint:
+    """A single ``pytorch_model.bin`` read with ``torch.load(weights_only=True)``:
+    tensors only, nothing in the file is executed."""
+
+    def __init__(self, path: Path, device):
+        self.device = torch.device(device)
+        self._sd = torch.load(str(path), map_location="cpu", weights_only=True)
+
+    def keys(self) -> list[str]:
+        return sorted(self._sd)
+
+    def __contains__(self, name: str) -> bool:
+        return name in self._sd
+
+    def read(self, name: str, dtype=BF16) -> torch.Tensor:
+        if name not in self._sd:
+            raise KeyError(f"weight {name!r} is not in the checkpoint")
+        return self._sd[name].to(device=self.device, dtype=dtype).contiguous()
+
+
+def load_minicpm3(path: str | Path, device="cpu", cfg=None) -> tuple:
+    """Every tensor ``minicpm3.MiniCPM3Engine`` uses, from a MiniCPM3 checkpoint at
+    ``path`` -- safetensors (sharded or single) or the published single
+    ``pytorch_model.bin`` (read without unpickling code) -- onto ``device`` as
+    bf16 under the published names, shapes checked against the config.
+    Returns ``(cfg, weights)``; an ``lm_head.weight`` is kept only when
+    ``tie_word_embeddings`` is false (MiniCPM3 ties it)."""
+    from .minicpm3 import hf_layer_names
+
+    p = Path(path)
+    if (p / INDEX).is_file() or (p / SINGLE).is_file():
+        ck = SafetensorsCheckpoint(p, device)
+    elif (p / "pytorch_model.bin").is_file():
+        ck = _TorchBinCheckpoint(p / "pytorch_model.bin", device)
+    else:
+        raise FileNotFoundError(f"{p} holds neither safetensors shards nor pytorch_model.bin")
+    tied = True
+    if cfg is None:
+        cfg = minicpm3_config(p)
+        with open(p / "config.json", encoding="utf-8") as fh:
+            tied = bool(json.load(fh).get("tie_word_embeddings", True))
+    H, NH, QA, KV, R = cfg.hidden, cfg.heads, cfg.q_lora, cfg.kv_lora, cfg.rope
+    shapes = {
+        "gamma_in": (H,), "w_q_a": (QA, H), "gamma_q_a": (QA,), "w_q_b": (NH * (cfg.nope + R), QA),
+        "w_kv_a": (KV + R, H), "gamma_kv_a": (KV,), "w_kv_b": (NH * (cfg.nope + cfg.v_dim), KV),
+        "w_o": (H, NH * cfg.v_dim), "gamma_post": (H,), "w_gate": (cfg.inter, H), "w_up": (cfg.inter, H),
+        "w_down": (H, cfg.inter),
+    }
+    want = {"model.embed_tokens.weight": (cfg.vocab, H), "model.norm.weight": (H,)}
+    for i in range(cfg.layers):
+        for key, name in hf_layer_names(i).items():
+            want[name] = shapes[key]
+    if not tied:
+        want["lm_head.weight"] = (cfg.vocab, H)
+    out = {}
+    for name, shape in want.items():
+        t = ck.read(name)
+        if tuple(t.shape) != shape:
+            raise ValueError(f"checkpoint weight {name}: shape {tuple(t.shape)}, the config says {shape}")
+        out[name] = t
+    return cfg, out

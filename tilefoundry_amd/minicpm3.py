@@ -345,6 +345,16 @@ class MiniCPM3Engine:
         if capture:
             self._capture()
 
+    @classmethod
+    def from_checkpoint(cls, ckpt, *, device="cuda:0", **kw):
+        """The engine over a MiniCPM3 checkpoint directory (``config.json`` and
+        safetensors shards or ``pytorch_model.bin``, ``checkpoint.load_minicpm3``):
+        the model run.py decodes from ``--ckpt`` (examples/minicpm3_4b-cutedsl/run.py:53-116)."""
+        from .checkpoint import load_minicpm3
+
+        cfg, wts = load_minicpm3(ckpt, device)
+        return cls(cfg, device=device, weights=wts, **kw)
+
     def _pack(self, wts):
         cfg, dev = self.cfg, self.device
 
