@@ -95,6 +95,13 @@ int tfa_gemv(const void* x, const void* w, void* y, int64_t n, int64_t k, int ou
 int tfa_rmsnorm_gemv(const void* h, const void* gamma, float eps, const void* w, void* y,
                      int64_t n, int64_t k, hipStream_t stream);
 
+/* The same product left in f32 (y[n] = rmsnorm(h) . w[n], no landing): one
+ * sequence's [q_a | kv_a] projection as the single split-K partial the MLA
+ * prep lands in bf16. Replaces: examples/minicpm3_4b-cutedsl/kernels/cute_gemv.py:246-286
+ * (NORM_GEMV over the fused q_a / kv_a weights, runtime_model.py's first launch of a layer). */
+int tfa_rmsnorm_gemv_f32(const void* h, const void* gamma, float eps, const void* w, float* y,
+                         int64_t n, int64_t k, hipStream_t stream);
+
 /* y[n] = bf16(residual[n] + bf16(x.w[n])), or with alpha (bf16 [1]):
  * y[n] = bf16(residual[n] + bf16(bf16(x.w[n]) * alpha)).  y may not alias residual.
  * Replaces: the residual adds of examples/qwen3_1_7b-tilelang/ref_src/model.py:263-265

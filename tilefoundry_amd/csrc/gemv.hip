@@ -425,6 +425,23 @@ int tfa_rmsnorm_gemv(const void* h, const void* gamma, float eps, const void* w,
   return dispatch_rows<PRO_NORM, EPI_BF16>(a, stream, "rmsnorm_gemv");
 }
 
+int tfa_rmsnorm_gemv_f32(const void* h, const void* gamma, float eps, const void* w, float* y,
+                         int64_t n, int64_t k, hipStream_t stream) {
+  GemvArgs a{};
+  a.x = static_cast<const uint16_t*>(h);
+  a.gamma = static_cast<const uint16_t*>(gamma);
+  a.eps = eps;
+  a.w = static_cast<const uint16_t*>(w);
+  a.N = (int)n;
+  a.K = (int)k;
+  a.yf = y;
+  TFA_TRY(check_gemv(a, "tfa_rmsnorm_gemv_f32"));
+  TFA_TRY(check_vec(h, "h", "tfa_rmsnorm_gemv_f32"));
+  TFA_TRY(check_vec(gamma, "gamma", "tfa_rmsnorm_gemv_f32"));
+  if (!y) return fail(TFA_ERR_NULL, "tfa_rmsnorm_gemv_f32: null y");
+  return dispatch_rows<PRO_NORM, EPI_F32>(a, stream, "rmsnorm_gemv_f32");
+}
+
 int tfa_gemv_residual(const void* x, const void* w, const void* residual, const void* alpha,
                       void* y, int64_t n, int64_t k, hipStream_t stream) {
   GemvArgs a{};

@@ -142,6 +142,18 @@ void rmsnorm_gemv(const Tensor& h, const Tensor& gamma, double eps, const Tensor
                                 y.data_ptr(), N, K, stream_of(h)));
 }
 
+void rmsnorm_gemv_f32(const Tensor& h, const Tensor& gamma, double eps, const Tensor& w, const Tensor& y) {
+  need(h, "h", BF);
+  const int64_t K = h.numel();
+  need(gamma, "gamma", BF, K);
+  if (w.dim() != 2) bad("w: expected a 2-D (N, K) weight");
+  const int64_t N = w.size(0);
+  need_mat(w, "w", N, K);
+  need(y, "y", F32, N);
+  raise_status(tfa_rmsnorm_gemv_f32(h.data_ptr(), gamma.data_ptr(), (float)eps, w.data_ptr(),
+                                    y.data_ptr<float>(), N, K, stream_of(h)));
+}
+
 void gemv_residual(const Tensor& x, const Tensor& w, const Tensor& residual, const OptT& alpha,
                    const Tensor& y) {
   need(x, "x", BF);
@@ -772,6 +784,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("resid_rms_norm_partials", &resid_rms_norm_partials);
   m.def("gemv", &gemv);
   m.def("rmsnorm_gemv", &rmsnorm_gemv);
+  m.def("rmsnorm_gemv_f32", &rmsnorm_gemv_f32);
   m.def("gemv_residual", &gemv_residual);
   m.def("rmsnorm_gemv_swiglu", &rmsnorm_gemv_swiglu);
   m.def("lm_head_blocks", [](int64_t vocab) { return tfa_lm_head_blocks(vocab); });

@@ -287,7 +287,8 @@ class MiniCPM3Engine:
     captured step over all of them (examples/minicpm3_4b-cutedsl/model.py:320-420,
     runtime twin runtime_model.py; run.py drives it token by token).
 
-    One step, 11 launches per layer plus 5:
+    One step (batch > 1), 11 launches per layer plus 5 -- at one sequence the
+    projections run on the bs=1 GEMVs instead, 9 launches per layer (``_step_one``):
 
         embed            bf16(table[id] * scale_emb), then the first input norm
         -- per layer: the MLA attention block of ``MLABlock`` ----------------
@@ -339,6 +340,7 @@ class MiniCPM3Engine:
         del weights
         self.cos, self.sin = rope_tables(self.cap, cfg, self.device)
         self.alpha = cfg.residual_scale
+        self.alpha_t = torch.tensor([self.alpha], dtype=BF16, device=self.device)
         self._buffers()
         self.sampler = None
         self.graph = None
@@ -419,6 +421,9 @@ class MiniCPM3Engine:
         self.err = z(1, dtype=torch.int32)
 
     def _step(self, keep_logits: bool = True):
+        if self.batch == 1:
+            self._step_one(keep_logits)
+            return
         cfg, ks = self.cfg, self.ks
         L = len(self.layers)
         C.embed(self.embed, self.ids, self.h, cfg.scale_emb, self.err)
@@ -442,6 +447,36 @@ class MiniCPM3Engine:
                                    self.xn, cfg.eps)
             else:
                 C.rows_residual(self.part_d, self.h1, self.alpha, self.h)
+        C.rms_norm_div(self.h, self.gamma_final, self.xn, cfg.eps, cfg.logits_scaling)
+        C.skinny_gemm(self.xn, self.head, 1, 3, None, None, self.logits if keep_logits else None,
+                      self.bv, self.bi)
+        C.batch_sample_step(self.bv, self.bi, self.inp, self.plen, self.ids, self.pos, self.sam,
+                            self.err)
+
+    def _step_one(self, keep_logits: bool = True):
+        """One sequence: the projections on the bs=1 GEMVs, each with its norm or
+        scaled residual fused (9 launches per layer):
+        rmsnorm_gemv_f32 [q_a | kv_a] (the single split-K partial mla_prep lands),
+        mla_prep, gemv q_b (f32), mla_q_absorb, mla_attention, mla_combine_up,
+        gemv_residual o_proj + scaled residual, rmsnorm_gemv_swiglu (post norm +
+        gate|up + SwiGLU), gemv_residual down + scaled residual."""
+        cfg = self.cfg
+        h, h1 = self.h[0], self.h1[0]
+        part_a, part_qb = self.part_a[:1], self.part_qb[:1]
+        C.embed(self.embed, self.ids, self.h, cfg.scale_emb, self.err)
+        for i, w in enumerate(self.layers):
+            lat, rk = self.latent[i], self.rope_k[i]
+            C.rmsnorm_gemv_f32(h, w["gamma_in"], cfg.eps, w["w_a"], part_a.view(-1))
+            C.mla_prep(part_a, w["gamma_q_a"], w["gamma_kv_a"], cfg.lora_eps, self.cos, self.sin,
+                       self.pos, lat, rk, self.q_n, self.err)
+            C.gemv(self.q_n[0], w["w_q_b"], part_qb.view(-1))
+            C.mla_q_absorb(part_qb, w["w_kv_b"], self.cos, self.sin, self.pos, self.q_abs, self.err)
+            C.mla_attention(self.q_abs, lat, rk, self.pos, self.split, cfg.scale, self.op, self.mp,
+                            self.lp, self.err)
+            C.mla_combine_up(self.op, self.mp, self.lp, self.pos, self.split, w["w_kv_b"], self.attn)
+            C.gemv_residual(self.attn[0], w["w_o"], h, self.alpha_t, h1)
+            C.rmsnorm_gemv_swiglu(h1, w["gamma_post"], cfg.eps, w["w_gu"], self.act[0])
+            C.gemv_residual(self.act[0], w["w_down"], h1, self.alpha_t, h)
         C.rms_norm_div(self.h, self.gamma_final, self.xn, cfg.eps, cfg.logits_scaling)
         C.skinny_gemm(self.xn, self.head, 1, 3, None, None, self.logits if keep_logits else None,
                       self.bv, self.bi)
