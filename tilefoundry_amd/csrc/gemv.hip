@@ -262,13 +262,14 @@ int dispatch_k(const GemvArgs& a, hipStream_t s, const char* name) {
 }
 
 // Rows per block: enough blocks to cover 256 CUs a few times over. Measured on
-// the decode step's shapes: 2 rows up to 2048 rows (o_proj 3.75 -> 3.64 us,
-// down 6.16 -> 6.02 us), 4 up to 16383 (q|k|v 4096 x 2048: 5.73 -> 5.61 us
-// against 8 rows; gate|up 12288 x 2048 the same at 4 or 8), 8 beyond.
+// the decode steps' shapes: 2 rows up to 2560 rows (Qwen3 o_proj 3.75 -> 3.64 us,
+// down 6.16 -> 6.02 us; MiniCPM3's 2560-row o_proj and down likewise), 4 up to
+// 16383 (q|k|v 4096 x 2048: 5.73 -> 5.61 us against 8 rows; gate|up 12288 x
+// 2048 the same at 4 or 8), 8 beyond.
 template <int PRO, int EPI>
 int dispatch_rows(const GemvArgs& a, hipStream_t s, const char* name) {
   if (a.N >= 16384 && a.K <= 4096) return dispatch_k<8, PRO, EPI>(a, s, name);
-  if (a.N <= 2048) return dispatch_k<2, PRO, EPI>(a, s, name);
+  if (a.N <= 2560) return dispatch_k<2, PRO, EPI>(a, s, name);
   return dispatch_k<4, PRO, EPI>(a, s, name);
 }
 
