@@ -102,6 +102,22 @@ int tfa_rmsnorm_gemv(const void* h, const void* gamma, float eps, const void* w,
 int tfa_rmsnorm_gemv_f32(const void* h, const void* gamma, float eps, const void* w, float* y,
                          int64_t n, int64_t k, hipStream_t stream);
 
+/* One sequence's MLA prep fused into the q_b GEMV: part = [q_a (q_lora) |
+ * kv_c (256) | k_rope (32)] f32, the single split-K partial that
+ * tfa_rmsnorm_gemv_f32 leaves; every block lands q_a in bf16, takes its LoRA
+ * norm with gamma_q_a (summed in tfa_mla_prep's order, so q_n is bit-equal)
+ * and writes q_part[n] = q_n . w_q_b[n] (f32, w_q_b [n, q_lora]); block 0 also
+ * writes latent_cache[pos[0]] and rope_cache[pos[0]] exactly as tfa_mla_prep
+ * does (caches [cap, 256] / [cap, 32] bf16; a pos outside [0, cap) or the
+ * rope table sets *err = 6 and skips them). q_lora a multiple of 32, <= 1024.
+ * Replaces: examples/minicpm3_4b-cutedsl/model.py:220-250 (steps 1-4 of
+ * mla_attention at one sequence) and kernels/cute_gemv.py:246-286 (NORM_GEMV
+ * of q_b over the normalised q_a). */
+int tfa_mla_prep_q_gemv(const float* part, int64_t q_lora, const void* gamma_q_a, const void* gamma_kv_a,
+                        float eps, const void* cos_t, const void* sin_t, int64_t rope_rows, const int* pos,
+                        void* latent_cache, void* rope_cache, int64_t cap, const void* w_q_b, float* q_part,
+                        int64_t n, int* err, hipStream_t stream);
+
 /* y[n] = bf16(residual[n] + bf16(x.w[n])), or with alpha (bf16 [1]):
  * y[n] = bf16(residual[n] + bf16(bf16(x.w[n]) * alpha)).  y may not alias residual.
  * Replaces: the residual adds of examples/qwen3_1_7b-tilelang/ref_src/model.py:263-265

@@ -207,6 +207,22 @@ def test_prompt_prefill_argument_checks(lib):
     assert st == ALIGN
 
 
+def test_mla_prep_q_gemv_argument_checks(lib):
+    # q_lora past 1024 or not a multiple of 32, an empty cache, a null cache, a misaligned partial
+    args = lambda qa, cap=64, part=A, lat=A: (part, I64(qa), A, A, F(1e-6), A, A, I64(64), A, lat, A,
+                                              I64(cap), A, A, I64(3840), P(None))
+    st, msg = call(lib, "tfa_mla_prep_q_gemv", *args(1056))
+    assert st == SHAPE and "1024" in msg
+    st, _ = call(lib, "tfa_mla_prep_q_gemv", *args(100))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_mla_prep_q_gemv", *args(768, cap=0))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_mla_prep_q_gemv", *args(768, lat=P(None)))
+    assert st == NULL
+    st, _ = call(lib, "tfa_mla_prep_q_gemv", *args(768, part=MIS))
+    assert st == ALIGN
+
+
 def test_torch_extension_rejects_host_tensors():
     from tilefoundry_amd import ops
 

@@ -70,6 +70,63 @@ def test_mla_prep_position_error(dev):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("qa,n,p", [(QA, H * 96, 77), (QA, 999, 0), (1024, 16400, 127), (96, 40, 5)])
+def test_mla_prep_q_gemv_equals_prep_then_gemv(dev, qa, n, p):
+    """The one-sequence fusion of the prep into the q_b GEMV: q_part, the
+    latent and the rope key are bit-equal to mla_prep followed by the f32 GEMV
+    over its q_n, and q_part agrees with the oracle's norm and product."""
+    from tilefoundry_amd._lib import C
+
+    g = gen(7)
+    cap = 128
+    part = (torch.randn(qa + KV + R, generator=g) * 0.5).to(dev)
+    gq = (1 + 0.1 * torch.randn(qa, generator=g)).to(BF).to(dev)
+    gkv = (1 + 0.1 * torch.randn(KV, generator=g)).to(BF).to(dev)
+    w = (torch.randn(n, qa, generator=g) * 0.05).to(BF).to(dev)
+    cos, sin = (t.to(dev) for t in OM.rope_tables(cap, CFG))
+    pos = torch.tensor([p], dtype=torch.int32, device=dev)
+    outs = []
+    for fused in (False, True):
+        lat = torch.zeros(1, cap, KV, dtype=BF, device=dev)
+        rk = torch.zeros(1, cap, R, dtype=BF, device=dev)
+        q_part = torch.empty(n, dtype=torch.float32, device=dev)
+        err = torch.zeros(1, dtype=torch.int32, device=dev)
+        if fused:
+            C.mla_prep_q_gemv(part, gq, gkv, 1e-6, cos, sin, pos, lat, rk, w, q_part, err)
+        else:
+            q_n = torch.empty(1, qa, dtype=BF, device=dev)
+            C.mla_prep(part.view(1, 1, -1), gq, gkv, 1e-6, cos, sin, pos, lat, rk, q_n, err)
+            C.gemv(q_n[0], w, q_part)
+        assert int(err.item()) == 0
+        outs.append((q_part, lat, rk))
+    for name, a, b in zip(("q_part", "latent cache", "rope cache"), *outs):
+        assert_equal(name, b, a)
+    q_n = rms_norm_q(part[:qa].cpu().to(BF)[None], gq.cpu(), 1e-6)
+    assert_close("q_part vs oracle", outs[1][0], q_n.float()[0] @ w.cpu().float().T)
+
+
+@pytest.mark.gpu
+def test_mla_prep_q_gemv_position_error(dev):
+    """A position outside the cache sets err = 6 and writes no cache slot; the
+    product is still written."""
+    from tilefoundry_amd._lib import C
+
+    cap = 64
+    lat = torch.zeros(1, cap, KV, dtype=BF, device=dev)
+    rk = torch.zeros(1, cap, R, dtype=BF, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    q_part = torch.full((96,), float("nan"), device=dev)
+    cos, sin = OM.rope_tables(cap, CFG)
+    C.mla_prep_q_gemv(torch.ones(QA + KV + R, device=dev), torch.ones(QA, dtype=BF, device=dev),
+                      torch.ones(KV, dtype=BF, device=dev), 1e-6, cos.to(dev), sin.to(dev),
+                      torch.tensor([cap], dtype=torch.int32, device=dev), lat, rk,
+                      torch.ones(96, QA, dtype=BF, device=dev), q_part, err)
+    assert int(err.item()) == 6
+    assert float(lat.float().abs().sum()) == 0.0 and float(rk.float().abs().sum()) == 0.0
+    assert bool(torch.isfinite(q_part).all())
+
+
+@pytest.mark.gpu
 def test_mla_q_absorb(dev):
     from tilefoundry_amd._lib import C
 

@@ -35,7 +35,9 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kLmHeadRows = 16;  // rows per block of the head (one argmax candidate each)
 
-enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_EMBED_NORM = 2 };
+enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_EMBED_NORM = 2, PRO_LORA = 3 };
+constexpr int kLoraLat = 256;   // MLA latent width (kv_lora_rank)
+constexpr int kLoraRope = 32;   // MLA rope slice
 enum {
   EPI_F32 = 0, EPI_BF16 = 1, EPI_RESID = 2, EPI_RESID_SCALED = 3, EPI_SWIGLU = 4,
   EPI_ARGMAX = 5, EPI_QKV = 6
@@ -68,6 +70,16 @@ struct GemvArgs {
   int cap;
   uint16_t* vc;
   int* err;
+  // LoRA prologue (MLA at one sequence): xf = [q_a (K) | kv_c (256) | k_rope (32)]
+  // f32, one split; block 0 also lands the latent and rope key at pos[0].
+  const float* xf;
+  const uint16_t* gkv;    // [256] latent norm scale
+  const uint16_t* cos_t;  // [rope_rows, 32]
+  const uint16_t* sin_t;
+  int rope_rows;
+  const int* pos;
+  uint16_t* lat_cache;    // [cap, 256]
+  uint16_t* rope_cache;   // [cap, 32]
 };
 
 TFA_DEV void set_err(int* err, int code) {
@@ -103,11 +115,41 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
     src = a.table + id * K;
   }
   uint4 xv[NCH], gv[NCH];
+  // LoRA prologue: q_a[t + 256 j] (the order its norm sums in), this lane's f32
+  // chunks, and for block 0 the latent column t, the rope slice and the position
+  float qs[4], xl[NCH][8];
+  float cv = 0.f, gk = 0.f, krv = 0.f;
+  int p_raw = 0;
+  const bool side = PRO == PRO_LORA && blockIdx.x == 0;
+  if (PRO == PRO_LORA) {
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    const int c = lane + j * kWave;
-    xv[j] = c < nch ? ld16(src + kbase + 8 * c) : make_uint4(0, 0, 0, 0);
-    if (PRO != PRO_PLAIN) gv[j] = c < nch ? ld16(a.gamma + kbase + 8 * c) : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < 4; ++j) {
+      const int i = t + kThreads * j;
+      qs[j] = i < K ? a.xf[i] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + j * kWave;
+      const uint4 zero = make_uint4(0, 0, 0, 0);
+      const float4 lo = __builtin_bit_cast(float4, c < nch ? ld16(a.xf + kbase + 8 * c) : zero);
+      const float4 hi = __builtin_bit_cast(float4, c < nch ? ld16(a.xf + kbase + 8 * c + 4) : zero);
+      xl[j][0] = lo.x; xl[j][1] = lo.y; xl[j][2] = lo.z; xl[j][3] = lo.w;
+      xl[j][4] = hi.x; xl[j][5] = hi.y; xl[j][6] = hi.z; xl[j][7] = hi.w;
+      gv[j] = c < nch ? ld16(a.gamma + kbase + 8 * c) : make_uint4(0, 0, 0, 0);
+    }
+    if (side) {
+      p_raw = a.pos[0];
+      gk = bf2f(a.gkv[t]);
+      cv = a.xf[K + t];
+      if (t < kLoraRope) krv = a.xf[K + kLoraLat + t];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = lane + j * kWave;
+      xv[j] = c < nch ? ld16(src + kbase + 8 * c) : make_uint4(0, 0, 0, 0);
+      if (PRO != PRO_PLAIN) gv[j] = c < nch ? ld16(a.gamma + kbase + 8 * c) : make_uint4(0, 0, 0, 0);
+    }
   }
 
   // 2. weights: streamed once, non-temporal
@@ -138,15 +180,76 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
     }
   }
   float xf[NCH][8];
+  if (PRO != PRO_LORA) {
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) unpack8(xv[j], xf[j]);
+    for (int j = 0; j < NCH; ++j) unpack8(xv[j], xf[j]);
+  }
   if (PRO == PRO_PLAIN && a.in_div != 0.f) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j)
 #pragma unroll
       for (int i = 0; i < 8; ++i) xf[j][i] = round_bf(__fdiv_rn(xf[j][i], a.in_div));
   }
-  if (PRO != PRO_PLAIN) {
+  if (PRO == PRO_LORA) {
+    // Each projection value lands in bf16 (a one-split sum, 0 + v); the q_a norm
+    // sums thread t's values j = 0..3, then the wave, then waves 0..3 in order, and
+    // block 0 reduces the latent's squares alongside.
+    __shared__ float kss[kWaves];
+    __shared__ float kr[kLoraRope];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float q = round_bf(0.f + qs[j]);
+      ss += q * q;
+    }
+    ss = wave_sum(ss);
+    float sk = 0.f, c = 0.f, s = 0.f;
+    bool p_ok = false;
+    if (side) {
+      cv = round_bf(0.f + cv);
+      sk = wave_sum(cv * cv);
+      if (t < kLoraRope) kr[t] = round_bf(0.f + krv);
+      p_ok = p_raw >= 0 && p_raw < a.cap && p_raw < a.rope_rows;
+      if (t < kLoraRope && p_ok) {
+        c = bf2f(a.cos_t[static_cast<size_t>(p_raw) * kLoraRope + t]);
+        s = bf2f(a.sin_t[static_cast<size_t>(p_raw) * kLoraRope + t]);
+      }
+    }
+    if (lane == 0) {
+      ssq[wid] = ss;
+      kss[wid] = sk;
+    }
+    lds_barrier();   // also publishes kr
+    float tq = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tq += ssq[w];
+    const float rq = rsqrt_rn(tq / static_cast<float>(K) + a.eps);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      float g[8];
+      unpack8(gv[j], g);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xf[j][i] = round_bf(round_bf(round_bf(0.f + xl[j][i]) * rq) * g[i]);
+    }
+    if (side) {
+      float tk = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) tk += kss[w];
+      const float rk = rsqrt_rn(tk / static_cast<float>(kLoraLat) + a.eps);
+      if (!p_ok) {
+        if (t == 0) set_err(a.err, 6);
+      } else {
+        a.lat_cache[static_cast<size_t>(p_raw) * kLoraLat + t] = static_cast<uint16_t>(f2bf(round_bf(cv * rk) * gk));
+        if (t < kLoraRope) {
+          const float x = kr[t];
+          const float partner = t < kLoraRope / 2 ? -kr[t + kLoraRope / 2] : kr[t - kLoraRope / 2];
+          a.rope_cache[static_cast<size_t>(p_raw) * kLoraRope + t] =
+              static_cast<uint16_t>(f2bf(round_bf(round_bf(x * c) + round_bf(partner * s))));
+        }
+      }
+    }
+  }
+  if (PRO == PRO_NORM || PRO == PRO_EMBED_NORM) {
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < NCH; ++j)
@@ -441,6 +544,41 @@ int tfa_rmsnorm_gemv_f32(const void* h, const void* gamma, float eps, const void
   TFA_TRY(check_vec(gamma, "gamma", "tfa_rmsnorm_gemv_f32"));
   if (!y) return fail(TFA_ERR_NULL, "tfa_rmsnorm_gemv_f32: null y");
   return dispatch_rows<PRO_NORM, EPI_F32>(a, stream, "rmsnorm_gemv_f32");
+}
+
+int tfa_mla_prep_q_gemv(const float* part, int64_t q_lora, const void* gamma_q_a, const void* gamma_kv_a,
+                        float eps, const void* cos_t, const void* sin_t, int64_t rope_rows, const int* pos,
+                        void* latent_cache, void* rope_cache, int64_t cap, const void* w_q_b, float* q_part,
+                        int64_t n, int* err, hipStream_t stream) {
+  static const char* name = "tfa_mla_prep_q_gemv";
+  GemvArgs a{};
+  a.w = static_cast<const uint16_t*>(w_q_b);
+  a.N = (int)n;
+  a.K = (int)q_lora;
+  TFA_TRY(check_gemv(a, name));
+  if (q_lora > 4 * kThreads) return fail(TFA_ERR_SHAPE, "%s: q_lora %lld exceeds %d", name, (long long)q_lora, 4 * kThreads);
+  TFA_TRY(check_vec(part, "part", name));
+  TFA_TRY(check_vec(gamma_q_a, "gamma_q_a", name));
+  if (!gamma_kv_a || !cos_t || !sin_t || !pos || !latent_cache || !rope_cache || !q_part)
+    return fail(TFA_ERR_NULL, "%s: null argument", name);
+  if (cap < 1 || rope_rows < 1) return fail(TFA_ERR_SHAPE, "%s: empty cache or rope table", name);
+  a.xf = part;
+  a.gamma = static_cast<const uint16_t*>(gamma_q_a);
+  a.gkv = static_cast<const uint16_t*>(gamma_kv_a);
+  a.eps = eps;
+  a.cos_t = static_cast<const uint16_t*>(cos_t);
+  a.sin_t = static_cast<const uint16_t*>(sin_t);
+  a.rope_rows = (int)rope_rows;
+  a.pos = pos;
+  a.lat_cache = static_cast<uint16_t*>(latent_cache);
+  a.rope_cache = static_cast<uint16_t*>(rope_cache);
+  a.cap = (int)cap;
+  a.yf = q_part;
+  a.err = err;
+  // q_lora <= 1024 is one 16-byte chunk per lane; rows per block as dispatch_rows
+  if (a.N <= 2560) return launch_gemv<1, 2, PRO_LORA, EPI_F32>(a, stream, "mla_prep_q_gemv");
+  if (a.N < 16384) return launch_gemv<1, 4, PRO_LORA, EPI_F32>(a, stream, "mla_prep_q_gemv");
+  return launch_gemv<1, 8, PRO_LORA, EPI_F32>(a, stream, "mla_prep_q_gemv");
 }
 
 int tfa_gemv_residual(const void* x, const void* w, const void* residual, const void* alpha,

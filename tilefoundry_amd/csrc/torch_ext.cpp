@@ -154,6 +154,35 @@ void rmsnorm_gemv_f32(const Tensor& h, const Tensor& gamma, double eps, const Te
                                     y.data_ptr<float>(), N, K, stream_of(h)));
 }
 
+// One sequence: part [q_lora + 288] f32, latent (1, cap, 256), rope (1, cap, 32),
+// w_q_b [N, q_lora], q_part [N] f32.
+void mla_prep_q_gemv(const Tensor& part, const Tensor& gamma_q_a, const Tensor& gamma_kv_a, double eps,
+                     const Tensor& cos, const Tensor& sin, const Tensor& pos, const Tensor& latent,
+                     const Tensor& rope, const Tensor& w_q_b, const Tensor& q_part, const OptT& err) {
+  need(pos, "pos", I32, 1);
+  need(latent, "latent", BF);
+  if (latent.dim() != 3 || latent.size(0) != 1 || latent.size(2) != 256) bad("latent: expected (1, cap, 256)");
+  const int64_t cap = latent.size(1);
+  need(rope, "rope", BF, cap * 32);
+  need(gamma_kv_a, "gamma_kv_a", BF, 256);
+  need(gamma_q_a, "gamma_q_a", BF);
+  const int64_t QA = gamma_q_a.numel();
+  need(part, "part", F32, QA + 288);
+  if (w_q_b.dim() != 2) bad("w_q_b: expected a 2-D (N, q_lora) weight");
+  const int64_t N = w_q_b.size(0);
+  need_mat(w_q_b, "w_q_b", N, QA);
+  need(q_part, "q_part", F32, N);
+  need(cos, "cos", BF);
+  need(sin, "sin", BF, cos.numel());
+  if (cos.numel() % 32 != 0) bad("cos: expected (rows, 32)");
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_mla_prep_q_gemv(part.data_ptr<float>(), QA, gamma_q_a.data_ptr(), gamma_kv_a.data_ptr(),
+                                   (float)eps, cos.data_ptr(), sin.data_ptr(), cos.numel() / 32,
+                                   pos.data_ptr<int>(), latent.data_ptr(), rope.data_ptr(), cap,
+                                   w_q_b.data_ptr(), q_part.data_ptr<float>(), N, opt_ptr_t<int>(err),
+                                   stream_of(pos)));
+}
+
 void gemv_residual(const Tensor& x, const Tensor& w, const Tensor& residual, const OptT& alpha,
                    const Tensor& y) {
   need(x, "x", BF);
@@ -799,6 +828,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("rows_norm", &rows_norm);
   m.def("batch_sample_step", &batch_sample_step);
   m.def("mla_prep", &mla_prep);
+  m.def("mla_prep_q_gemv", &mla_prep_q_gemv);
   m.def("mla_q_absorb", &mla_q_absorb);
   m.def("mla_attention", &mla_attention);
   m.def("mla_combine_up", &mla_combine_up);

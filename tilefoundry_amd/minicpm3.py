@@ -288,7 +288,7 @@ class MiniCPM3Engine:
     runtime twin runtime_model.py; run.py drives it token by token).
 
     One step (batch > 1), 11 launches per layer plus 5 -- at one sequence the
-    projections run on the bs=1 GEMVs instead, 9 launches per layer (``_step_one``):
+    projections run on the bs=1 GEMVs instead, 8 launches per layer (``_step_one``):
 
         embed            bf16(table[id] * scale_emb), then the first input norm
         -- per layer: the MLA attention block of ``MLABlock`` ----------------
@@ -455,9 +455,10 @@ class MiniCPM3Engine:
 
     def _step_one(self, keep_logits: bool = True):
         """One sequence: the projections on the bs=1 GEMVs, each with its norm or
-        scaled residual fused (9 launches per layer):
-        rmsnorm_gemv_f32 [q_a | kv_a] (the single split-K partial mla_prep lands),
-        mla_prep, gemv q_b (f32), mla_q_absorb, mla_attention, mla_combine_up,
+        scaled residual fused (8 launches per layer):
+        rmsnorm_gemv_f32 [q_a | kv_a] (one f32 split-K partial), mla_prep_q_gemv
+        (q_a lands, LoRA norm, q_b GEMV in f32; block 0 lands the latent and the
+        rope key in the caches), mla_q_absorb, mla_attention, mla_combine_up,
         gemv_residual o_proj + scaled residual, rmsnorm_gemv_swiglu (post norm +
         gate|up + SwiGLU), gemv_residual down + scaled residual."""
         cfg = self.cfg
@@ -467,9 +468,8 @@ class MiniCPM3Engine:
         for i, w in enumerate(self.layers):
             lat, rk = self.latent[i], self.rope_k[i]
             C.rmsnorm_gemv_f32(h, w["gamma_in"], cfg.eps, w["w_a"], part_a.view(-1))
-            C.mla_prep(part_a, w["gamma_q_a"], w["gamma_kv_a"], cfg.lora_eps, self.cos, self.sin,
-                       self.pos, lat, rk, self.q_n, self.err)
-            C.gemv(self.q_n[0], w["w_q_b"], part_qb.view(-1))
+            C.mla_prep_q_gemv(part_a.view(-1), w["gamma_q_a"], w["gamma_kv_a"], cfg.lora_eps, self.cos,
+                              self.sin, self.pos, lat, rk, w["w_q_b"], part_qb.view(-1), self.err)
             C.mla_q_absorb(part_qb, w["w_kv_b"], self.cos, self.sin, self.pos, self.q_abs, self.err)
             C.mla_attention(self.q_abs, lat, rk, self.pos, self.split, cfg.scale, self.op, self.mp,
                             self.lp, self.err)
