@@ -4,10 +4,15 @@
 
 A step is one greedy decode step of the whole model (28 layers, vocab 151936,
 tied head) for every sequence of the batch, replayed from one captured HIP
-graph; the workload is a 64-token seeded-uniform prompt followed by K new
+graph; the workload is a 64-token seeded-uniform prompt followed by 2048 new
 tokens per sequence (random-init bf16 weights ~N(0, 0.02), synthetic data).
-W untimed warmup steps run first (a full generate() of W tokens). The timed
-region is bracketed by torch.cuda.synchronize() on both sides.
+The timed region is always the workload's 2048 decode steps, whatever --steps
+asks (the mean KV length, and so the bytes per step, depend on it); the line
+reports the count actually timed as `steps` and the request as
+`steps_requested`. W untimed warmup steps run first (a generate() of W
+tokens). The timed region is bracketed by torch.cuda.synchronize() on both
+sides. Each secondary measurement runs inside its own try/except: a failure
+there becomes an "error" field of that object, not a lost line.
 
 The JSON line also carries:
   roofline      the dominant kernel (post-attention norm + gate|up GEMV +
@@ -46,7 +51,46 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
 REFERENCE_TOKS = 612.5          # reference's published bs=1 decode tok/s (one H200)
-PROMPT = 64
+PROMPT = 64                     # prompt tokens per sequence
+NEW_TOKENS = 2048               # new tokens per sequence, bs=1 and bs=32
+PROMPT_LENGTHS = (64, 512)      # prompt-prefill leg, bs=1
+MINICPM3_LENGTHS = (32, 128, 512)
+MINICPM3_PROMPT = 8
+
+
+def sizing(args) -> dict:
+    """Every engine the run builds, as ``(max_new, prompt_room)``, and every
+    ``(prompt_len, new_tokens)`` request the run makes of it. An engine holds
+    ``max_new + prompt_room`` steps; a request needs ``prompt_len + new``."""
+    warm = max(1, args.warmup)
+    return {
+        "headline": {"engine": (max(NEW_TOKENS, warm), PROMPT),
+                     "requests": [(PROMPT, warm), (PROMPT, NEW_TOKENS)]},
+        "prompt_prefill_bs1": {"engine": (16, max(PROMPT_LENGTHS)),
+                               "requests": [(n, 1) for n in PROMPT_LENGTHS]},
+        "bs32": {"engine": (NEW_TOKENS, PROMPT),
+                 "requests": [(PROMPT, 16), (PROMPT, NEW_TOKENS), (PROMPT, 1)]},
+        "minicpm3_decode_bs1": {"engine": (max(MINICPM3_LENGTHS), 16),
+                                "requests": [(MINICPM3_PROMPT, 8)]
+                                + [(MINICPM3_PROMPT, n) for n in MINICPM3_LENGTHS]},
+    }
+
+
+def _leg(fn, *a, **kw):
+    """Run one secondary measurement; an exception becomes its "error" field.
+    A line on stderr names each measurement as it ends."""
+    t0 = time.perf_counter()
+    try:
+        out = fn(*a, **kw)
+        print(f"[bench] {fn.__name__} done in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+        return out
+    except Exception as exc:  # noqa: BLE001 -- reported in the line, not swallowed
+        import traceback
+
+        traceback.print_exc()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        return {"error": f"{type(exc).__name__}: {exc}"}
 
 
 def _events_time(fn, reps: int) -> float:
@@ -129,16 +173,20 @@ def kernel_lines(eng) -> dict:
     out = {}
     dev = eng.device
     bf = torch.bfloat16
-    # fused residual add + RMSNorm, x / residual bf16 [4096, 2048]; 8 rotating sets
+    # fused residual add + RMSNorm, x / residual bf16 [4096, 2048]: 12 rotating
+    # input sets and 4 output sets (537 MB read + 134 MB written per rotation,
+    # twice the 256 MB last-level cache)
     R, H = 4096, 2048
     g = torch.Generator(device=dev).manual_seed(0)
     sets = [(torch.randn(R, H, device=dev, generator=g).to(bf),
-             torch.randn(R, H, device=dev, generator=g).to(bf)) for _ in range(8)]
+             torch.randn(R, H, device=dev, generator=g).to(bf)) for _ in range(12)]
     gamma = (1 + 0.1 * torch.randn(H, device=dev, generator=g)).to(bf)
-    y = torch.empty(R, H, device=dev, dtype=bf)
-    ro = torch.empty(R, H, device=dev, dtype=bf)
+    outs = [(torch.empty(R, H, device=dev, dtype=bf), torch.empty(R, H, device=dev, dtype=bf))
+            for _ in range(4)]
+
     def add_norm():
-        for x, r in sets:
+        for i, (x, r) in enumerate(sets):
+            y, ro = outs[i % len(outs)]
             C.add_rms_norm(x, r, gamma, y, ro, 1e-6, 0)
 
     ms = _graph_time(add_norm, 10, len(sets), copies=4)
@@ -146,7 +194,7 @@ def kernel_lines(eng) -> dict:
     gbs = algo / (ms * 1e-3) / 1e9
     out["add_rms_norm_4096x2048"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                                      "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": algo}
-    del sets, y, ro
+    del sets, outs
     # decode-layer GEMVs over the 28 layers' weights
     cfg = eng.cfg
     L = eng.layers
@@ -181,7 +229,9 @@ def kernel_lines(eng) -> dict:
 
 def decode_layer_ctx4096(eng) -> dict:
     """One Qwen3 decode layer at bs=1 over a 4096-position cache (the single-layer
-    workload): the layer's six launches, timed over the 28 layers' weights; its
+    workload): the layer's six launches, timed over the 28 layers' weights, each
+    layer with a K/V cache of its own (28 x 16.8 MB, so no layer's cache is
+    still in the 256 MB last-level cache when its turn comes again); its
     algorithmic bytes are the layer's weights plus the K and V it reads."""
     from tilefoundry_amd._lib import C
 
@@ -189,11 +239,12 @@ def decode_layer_ctx4096(eng) -> dict:
     H, HQ, HKV, D = cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim
     dev = eng.device
     ctx = 4096
-    split = 64
+    split = eng.split
     bf = torch.bfloat16
     g = torch.Generator(device=dev).manual_seed(1)
-    kc = torch.randn(ctx, HKV * D, device=dev, generator=g).to(bf)
-    vc = torch.randn(ctx, HKV * D, device=dev, generator=g).to(bf)
+    L = len(eng.layers)
+    kcs = [torch.randn(ctx, HKV * D, device=dev, generator=g).to(bf) for _ in range(L)]
+    vcs = [torch.randn(ctx, HKV * D, device=dev, generator=g).to(bf) for _ in range(L)]
     ns = ctx // split
     op = torch.empty(ns, HQ, D, device=dev)
     mp = torch.empty(ns, HQ, device=dev)
@@ -209,38 +260,44 @@ def decode_layer_ctx4096(eng) -> dict:
     act = torch.empty(cfg.inter, device=dev, dtype=bf)
     err = torch.zeros(1, dtype=torch.int32, device=dev)
 
-    def layer(w):
-        C.decode_qkv(h, None, None, None, w["gamma_in"], cfg.eps, w["w_qkv"], nqk, qk, wr, vc, err)
+    def attention(w, kc, vc):
         C.decode_attention(qk, None, w["gamma_q"], w["gamma_k"], cfg.eps, cos, sin, kc, vc, wr, wr, HQ, HKV,
                            split, cfg.scale, op, mp, lp, False, err)
         C.attn_combine(op, mp, lp, attn, wr, split)
+
+    def layer(w, kc, vc):
+        C.decode_qkv(h, None, None, None, w["gamma_in"], cfg.eps, w["w_qkv"], nqk, qk, wr, vc, err)
+        attention(w, kc, vc)
         C.gemv_residual(attn, w["w_o"], h, None, h1)
         C.rmsnorm_gemv_swiglu(h1, w["gamma_post"], cfg.eps, w["w_gu"], act)
         C.gemv_residual(act, w["w_down"], h1, None, h)
 
-    ms = _graph_time(lambda: [layer(w) for w in eng.layers], 10, len(eng.layers), copies=2)
+    ms = _graph_time(lambda: [layer(w, kc, vc) for w, kc, vc in zip(eng.layers, kcs, vcs)], 10, L, copies=2)
     wbytes = sum(t.numel() * 2 for t in eng.layers[0].values())
     kv = 2 * ctx * HKV * D * 2
     nbytes = wbytes + kv
     gbs = nbytes / (ms * 1e-3) / 1e9
-    ms_attn = _graph_time(lambda: (
-        C.decode_attention(qk, None, eng.layers[0]["gamma_q"], eng.layers[0]["gamma_k"], cfg.eps, cos, sin, kc,
-                           vc, wr, wr, HQ, HKV, split, cfg.scale, op, mp, lp, False, err),
-        C.attn_combine(op, mp, lp, attn, wr, split)), 50)
+    ms_attn = _graph_time(lambda: [attention(w, kc, vc) for w, kc, vc in zip(eng.layers, kcs, vcs)], 20, L,
+                          copies=2)
+    del kcs, vcs
     return {"workload": "one Qwen3-1.7B-shaped decode layer, bs=1, 4096 cached positions attended",
             "us": round(ms * 1e3, 2), "bytes": int(nbytes), "GB/s": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "attention_us": round(ms_attn * 1e3, 2),
-            "attention_GB/s": round(kv / (ms_attn * 1e-3) / 1e9, 1)}
+            "attention_GB/s": round(kv / (ms_attn * 1e-3) / 1e9, 1),
+            "attention_frac": round(kv / (ms_attn * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "working_set": f"{L} layers' weights and {L} K/V caches of {kv} B, rotated"}
 
 
-def batch32(seed: int, steps: int) -> dict:
+def batch32(seed: int, steps: int = NEW_TOKENS, args=None) -> dict:
     """bs=32 greedy decode: 32 seeded 64-token prompts, `steps` new tokens each,
     one captured step for all sequences."""
     from tilefoundry_amd.qwen3 import BatchEngine, QWEN3_1_7B
 
     cfg = QWEN3_1_7B
-    eng = BatchEngine(cfg, batch=32, device="cuda:0", max_new=steps, prompt_room=PROMPT, seed=seed)
+    max_new, room = sizing(args)["bs32"]["engine"] if args is not None else (steps, PROMPT)
+    eng = BatchEngine(cfg, batch=32, device="cuda:0", max_new=max(max_new, steps), prompt_room=room,
+                      seed=seed)
     g = torch.Generator().manual_seed(seed + 1)
     prompts = torch.randint(0, cfg.vocab, (32, PROMPT), generator=g).tolist()
     eng.generate(prompts, min(16, steps))     # warm
@@ -276,7 +333,7 @@ def _first_token_ms(eng, prompts, prefill: bool, reps: int = 5) -> dict:
             "first_token_ms": round(statistics.median(ttft[1:]), 3), "first_pick": gen.tokens[0]}
 
 
-def prompt_prefill(eng, seed: int, lengths=(64, 512)) -> dict:
+def prompt_prefill(eng, seed: int, lengths=PROMPT_LENGTHS) -> dict:
     """bs=1 prompt consumption on the decode model: the reference's walk (one
     captured decode step per prompt token) against the prompt prefill (every
     layer over all prompt rows at once: f32 GEMMs, row norms, one causal
@@ -294,14 +351,19 @@ def prompt_prefill(eng, seed: int, lengths=(64, 512)) -> dict:
     return out
 
 
-def prompt_only(seed: int) -> dict:
+def prompt_only(seed: int, args=None) -> dict:
+    """The prompt-prefill leg on an engine of its own, sized for the longest prompt."""
     from tilefoundry_amd.qwen3 import Engine, QWEN3_1_7B
 
-    eng = Engine(QWEN3_1_7B, device="cuda:0", max_new=16, prompt_room=512, seed=seed)
-    return prompt_prefill(eng, seed)
+    max_new, room = sizing(args)["prompt_prefill_bs1"]["engine"] if args is not None else (16, 512)
+    eng = Engine(QWEN3_1_7B, device="cuda:0", max_new=max_new, prompt_room=room, seed=seed)
+    out = prompt_prefill(eng, seed)
+    del eng
+    torch.cuda.empty_cache()
+    return out
 
 
-def minicpm3_decode(seed: int, lengths=(32, 128, 512)) -> dict:
+def minicpm3_decode(seed: int, lengths=MINICPM3_LENGTHS, args=None) -> dict:
     """MiniCPM3-4B-shaped greedy decode at bs=1 (62 layers, vocab 73448 tied,
     random-init weights): an 8-token seeded prompt, then 32 / 128 / 512 new
     tokens, one captured step per token; tok/s beside the reference's H200
@@ -309,9 +371,10 @@ def minicpm3_decode(seed: int, lengths=(32, 128, 512)) -> dict:
     from tilefoundry_amd.minicpm3 import MINICPM3_4B, MiniCPM3Engine
 
     ref = {32: 281.5, 128: 281.3, 512: 223.7}
-    eng = MiniCPM3Engine(MINICPM3_4B, device="cuda:0", max_new=max(lengths), prompt_room=16, seed=seed)
+    max_new, room = sizing(args)["minicpm3_decode_bs1"]["engine"] if args is not None else (max(lengths), 16)
+    eng = MiniCPM3Engine(MINICPM3_4B, device="cuda:0", max_new=max_new, prompt_room=room, seed=seed)
     g = torch.Generator().manual_seed(seed + 3)
-    prompt = torch.randint(0, MINICPM3_4B.vocab, (8,), generator=g).tolist()
+    prompt = torch.randint(0, MINICPM3_4B.vocab, (MINICPM3_PROMPT,), generator=g).tolist()
     eng.generate([prompt], 8)   # warm
     out = {"workload": "MiniCPM3-4B-shaped greedy decode, bs=1, 8-token prompt", "by_new_tokens": {}}
     for n in lengths:
@@ -325,32 +388,37 @@ def minicpm3_decode(seed: int, lengths=(32, 128, 512)) -> dict:
     return out
 
 
-def mla_decode() -> dict:
+def mla_decode(nblocks: int = 8) -> dict:
     """MiniCPM3-4B-shaped MLA attention block, batch 8 x 8192 positions, absorbed:
     the whole block (one captured step) and its attention core (split attention
-    over the compressed cache + merge / W_UV)."""
+    over the compressed cache + merge / W_UV). ``nblocks`` independent blocks
+    (own weights, own caches: 8 x 64.8 MB) are stepped in turn, so the 256 MB
+    last-level cache holds none of a block's cache when its turn comes again."""
     from tilefoundry_amd._lib import C
     from tilefoundry_amd.minicpm3 import MLABlock, MiniCPM3Config
 
     cfg = MiniCPM3Config()
     B, cap = 8, 8192
-    blk = MLABlock(cfg, batch=B, cap=cap, device="cuda:0")
     g = torch.Generator(device="cuda:0").manual_seed(2)
-    blk.latent.normal_(generator=g)
-    blk.rope_k.normal_(generator=g)
-    blk.hidden.normal_(generator=g)
-    blk.pos.fill_(cap - 1)
-    blk.capture()
-    ms_blk = _events_time(blk.run, 100)
+    blks = []
+    for i in range(nblocks):
+        blk = MLABlock(cfg, batch=B, cap=cap, device="cuda:0", seed=i)
+        blk.latent.normal_(generator=g)
+        blk.rope_k.normal_(generator=g)
+        blk.hidden.normal_(generator=g)
+        blk.pos.fill_(cap - 1)
+        blk.capture()
+        blks.append(blk)
+    ms_blk = _events_time(lambda: [b.run() for b in blks], 20) / nblocks
 
     def core():
-        C.mla_attention(blk.q_abs, blk.latent, blk.rope_k, blk.pos, blk.split, cfg.scale, blk.op, blk.mp,
-                        blk.lp, blk.err)
-        C.mla_combine_up(blk.op, blk.mp, blk.lp, blk.pos, blk.split, blk.w["w_kv_b"], blk.attn)
+        for b in blks:
+            C.mla_attention(b.q_abs, b.latent, b.rope_k, b.pos, b.split, cfg.scale, b.op, b.mp, b.lp, b.err)
+            C.mla_combine_up(b.op, b.mp, b.lp, b.pos, b.split, b.w["w_kv_b"], b.attn)
 
-    ms_core = _graph_time(core, 20)
+    ms_core = _graph_time(core, 10, nblocks, copies=2)
     cache = B * cap * (cfg.kv_lora + cfg.rope) * 2
-    weights = sum(t.numel() * 2 for k, t in blk.w.items() if k.startswith("w_"))
+    weights = sum(t.numel() * 2 for k, t in blks[0].w.items() if k.startswith("w_"))
     out = {"workload": "MiniCPM3-4B-shaped MLA decode attention block, batch 8, 8192 positions, absorbed",
            "block_us": round(ms_blk * 1e3, 2),
            "block_bytes": int(cache + weights),
@@ -358,8 +426,9 @@ def mla_decode() -> dict:
            "attention_core_us": round(ms_core * 1e3, 2),
            "attention_core_bytes": int(cache),
            "attention_core_GB/s": round(cache / (ms_core * 1e-3) / 1e9, 1),
-           "attention_core_frac": round(cache / (ms_core * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-    del blk
+           "attention_core_frac": round(cache / (ms_core * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "working_set": f"{nblocks} blocks (own weights and caches) stepped in turn"}
+    del blks
     torch.cuda.empty_cache()
     return out
 
@@ -434,52 +503,177 @@ def copy_bandwidth(dev) -> dict:
     return {"GB/s": round(gbs, 1), "frac_of_nominal": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def cpu_baseline(seed: int, prompt: list[int], n_steps: int = 48) -> dict:
-    """The CPU oracle on this host's cores: the same model (28 layers, vocab
-    151936, same synthetic weights), a 4-token prompt walk then n_steps timed
-    greedy steps. Weights are drawn on the GPU (identical values, see
-    tilefoundry_amd.synthetic) and copied to host memory."""
-    from oracle import qwen3 as OQ
-    from tilefoundry_amd.qwen3 import QWEN3_1_7B, hf_names, synthetic_weights
-
-    cfg = QWEN3_1_7B
-    torch.set_num_threads(os.cpu_count() or 1)
-    wts = {k: v.cpu() for k, v in synthetic_weights(cfg, seed, "cuda:0").items()}
-    layers = [OQ.LayerWeights(**{k: wts[v] for k, v in hf_names(i).items()})
-              for i in range(cfg.layers)]
-    model = OQ.ModelWeights(embed=wts["model.embed_tokens.weight"],
-                            gamma_final=wts["model.norm.weight"], layers=layers)
-    ocfg = OQ.Qwen3Config()
-    p = prompt[:4]
-    cos, sin = OQ.rope_tables(len(p) + n_steps + 1, ocfg.head_dim, ocfg.rope_theta)
-    caches = OQ.empty_caches(ocfg, ocfg.layers)
-    for i, t in enumerate(p):                       # untimed: also converts weights to f32
-        logits = OQ.step(model, ocfg, t, i, caches, cos, sin, p_bf16=True)
-    t0 = time.perf_counter()
-    tok = OQ.greedy(logits)
-    for s in range(n_steps):
-        logits = OQ.step(model, ocfg, tok, len(p) + s, caches, cos, sin, p_bf16=True)
-        tok = OQ.greedy(logits)
-    dt = time.perf_counter() - t0
+def _cpu_name() -> str:
     cpu = platform.processor() or platform.machine()
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
             if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(n_steps / dt, 3), "unit": "tok/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": (f"oracle (torch CPU, f32 matmuls) of the same 28-layer model: {n_steps} greedy "
-                       f"decode steps at bs=1 after a 4-token prompt walk; {dt:.1f} s; "
-                       f"os.cpu_count()={os.cpu_count()}; cpu='{cpu}'")}
+    return cpu
+
+
+def _protocol(fn, warm: int = 2, runs: int = 7) -> dict:
+    """``warm`` untimed calls, then ``runs`` timed ones: median / min / max seconds."""
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return {"median_s": statistics.median(ts), "min_s": min(ts), "max_s": max(ts), "runs": runs,
+            "warmups": warm}
+
+
+def _rate(prot: dict, work: float, unit: str, scale: float = 1.0) -> dict:
+    """Throughput ``work / time`` at the median and at the extremes (min time = max rate)."""
+    r = lambda t: round(work / t / scale, 3)
+    return {"value": r(prot["median_s"]), "unit": unit, "min": r(prot["max_s"]), "max": r(prot["min_s"]),
+            "median_ms": round(prot["median_s"] * 1e3, 3), "runs": prot["runs"], "warmups": prot["warmups"]}
+
+
+def cpu_baseline(seed: int, prompt: list[int]) -> dict:
+    """The CPU oracle (the torch restatement the tests check against) on this
+    host's cores, for every configuration, with the reference's protocol: 2
+    untimed runs, then 7 timed, median (``value``) with min / max. Weights are
+    drawn on the GPU (identical values on any device, see
+    tilefoundry_amd.synthetic) and copied to host memory. The top-level fields
+    are the headline workload's (bs=1 greedy decode of the 28-layer model);
+    ``by_config`` holds the rest. Each sample is bounded; ``sample`` says what
+    it was."""
+    from oracle import minicpm3 as OM
+    from oracle import norms as ON
+    from oracle import prefill as OP
+    from oracle import qwen3 as OQ
+    from tilefoundry_amd.qwen3 import QWEN3_1_7B, hf_names, synthetic_weights
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    bf = torch.bfloat16
+    cfg = QWEN3_1_7B
+    ocfg = OQ.Qwen3Config()
+    by = {}
+    t_all = time.perf_counter()
+
+    # config 1: fused add + RMSNorm over [4096, 2048]
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(4096, 2048, generator=g).to(bf)
+    r = torch.randn(4096, 2048, generator=g).to(bf)
+    gam = (1 + 0.1 * torch.randn(2048, generator=g)).to(bf)
+    p = _protocol(lambda: ON.add_rms_norm(x, r, gam, 1e-6))
+    by["add_rms_norm_4096x2048"] = {**_rate(p, 4 * 4096 * 2048 * 2 + 2048 * 2, "GB/s", 1e9),
+                                    "sample": "the whole [4096, 2048] call"}
+    del x, r
+
+    # the 28-layer model's weights (configs 2 and 5)
+    wts = {k: v.cpu() for k, v in synthetic_weights(cfg, seed, "cuda:0").items()}
+    layers = [OQ.LayerWeights(**{k: wts[v] for k, v in hf_names(i).items()}) for i in range(cfg.layers)]
+    model = OQ.ModelWeights(embed=wts["model.embed_tokens.weight"],
+                            gamma_final=wts["model.norm.weight"], layers=layers)
+    del wts
+
+    # config 2: one decode layer attending 4096 positions (4095 cached + its own)
+    ctx = 4096
+    cos, sin = OQ.rope_tables(ctx, ocfg.head_dim, ocfg.rope_theta)
+    kc = torch.randn(ctx - 1, ocfg.kv_heads, ocfg.head_dim, generator=g).to(bf)
+    vc = torch.randn(ctx - 1, ocfg.kv_heads, ocfg.head_dim, generator=g).to(bf)
+    h = torch.randn(ocfg.hidden, generator=g).to(bf)
+    lw = layers[0]
+    p = _protocol(lambda: OQ.decoder_layer(h, lw, ocfg, cos[ctx - 1], sin[ctx - 1], kc, vc))
+    layer_bytes = sum(getattr(lw, f).numel() * 2 for f in
+                      ("gamma_in", "w_q", "w_k", "w_v", "gamma_q", "gamma_k", "w_o", "gamma_post",
+                       "w_gate", "w_up", "w_down")) + 2 * ctx * ocfg.kv_heads * ocfg.head_dim * 2
+    by["decode_layer_bs1_ctx4096"] = {**_rate(p, layer_bytes, "GB/s", 1e9),
+                                      "sample": "one layer step over a 4096-position cache"}
+    del kc, vc
+
+    # config 5 at bs=1: one greedy step of the 28-layer model per run, after a 4-token walk
+    caches = OQ.empty_caches(ocfg, ocfg.layers)
+    cos, sin = OQ.rope_tables(64, ocfg.head_dim, ocfg.rope_theta)
+    walk = prompt[:4]
+    for i, t in enumerate(walk):                  # untimed: also converts weights to f32
+        logits = OQ.step(model, ocfg, t, i, caches, cos, sin, p_bf16=True)
+    state = {"tok": OQ.greedy(logits), "pos": len(walk)}
+
+    def one_step():
+        lg = OQ.step(model, ocfg, state["tok"], state["pos"], caches, cos, sin, p_bf16=True)
+        state["tok"], state["pos"] = OQ.greedy(lg), state["pos"] + 1
+
+    p = _protocol(one_step)
+    head = {**_rate(p, 1.0, "tok/s"),
+            "sample": ("oracle (torch CPU, f32 matmuls) of the same 28-layer model: 9 greedy decode "
+                       "steps at bs=1 (2 untimed + 7 timed, one step per run) after a 4-token prompt "
+                       "walk, contexts 5..13")}
+
+    # config 5 at bs=32: one batched greedy step of 32 sequences per run
+    B = 32
+    pr = OQ.prompt_ids(cfg.vocab, 4, seed=seed + 1, batch=B)
+    caches_b = [OQ.empty_caches(ocfg, ocfg.layers) for _ in range(B)]
+    for i in range(4):
+        logits = OQ.step_batch(model, ocfg, [row[i] for row in pr], [i] * B, caches_b, cos, sin, p_bf16=True)
+    st = {"tok": logits.argmax(-1).tolist(), "pos": 4}
+
+    def batch_step():
+        lg = OQ.step_batch(model, ocfg, st["tok"], [st["pos"]] * B, caches_b, cos, sin, p_bf16=True)
+        st["tok"], st["pos"] = lg.argmax(-1).tolist(), st["pos"] + 1
+
+    p = _protocol(batch_step)
+    by["decode_bs32"] = {**_rate(p, float(B), "tok/s"),
+                         "sample": "9 batched greedy steps of 32 sequences (one step per run) after a "
+                                   "4-token prompt walk"}
+    del model, layers, caches, caches_b
+
+    # config 3: MLA attention block, batch 8, 8192 positions (absorbed form)
+    mcfg = OM.MLAConfig()
+    mw = OM.random_weights(mcfg, seed)
+    lat, rk = OM.random_cache(8, 8192, mcfg, seed=seed + 2)
+    hid = torch.randn(8, mcfg.hidden, generator=g).to(bf)
+    mcos, msin = OM.rope_tables(8192, mcfg)
+
+    def mla_block():
+        for b in range(8):
+            pj = OM.project(hid[b], mw, mcfg, 8191, mcos, msin)
+            qa = OM.absorb_query(pj.q_up, mw, mcfg, 8191, mcos, msin)
+            attn = OM.attend_absorbed(qa, lat[b], rk[b], mw, mcfg)
+            OM.o_proj_residual(attn, mw.w_o, hid[b], 1.0)
+
+    p = _protocol(mla_block)
+    cache_bytes = 8 * 8192 * (mcfg.kv_lora + mcfg.rope) * 2
+    by["mla_decode_b8_ctx8192"] = {**_rate(p, cache_bytes, "GB/s (cache bytes)", 1e9),
+                                   "sample": "the whole block for 8 sequences x 8192 positions"}
+    del lat, rk
+
+    # config 4: the prefill attention layer at 1024 tokens
+    pc = OP.PrefillConfig()
+    lwp = OP.random_layer(pc, seed)
+    n = 1024
+    hn = torch.randn(n, pc.hidden, generator=g).to(bf)
+    pcos, psin = OP.rope_tables(n, pc)
+
+    def prefill_layer_cpu():
+        q, gate, k, v = OP.qkv(hn, lwp["w_q"], lwp["w_k"], lwp["w_v"], lwp["gamma_q"], lwp["gamma_k"],
+                               pcos, psin, pc)
+        a = OP.attention(q, k, v, gate, pc)
+        OP.o_proj(a, hn, lwp["w_o"])
+
+    p = _protocol(prefill_layer_cpu)
+    fl = 12288.0 * n * n + 146_800_640.0 * n + 62_914_560.0 * n
+    by["prefill_layer_1024"] = {**_rate(p, fl, "TFLOP/s", 1e12),
+                                "sample": "qkv (+head norm, RoPE) + causal attention (+gate) + o_proj "
+                                          "(+residual) at 1024 tokens"}
+    return {**head, "cores": torch.get_num_threads(), "kind": "port", "by_config": by,
+            "host": {"os.cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+                     "cpu": _cpu_name()},
+            "seconds_total": round(time.perf_counter() - t_all, 1)}
 
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2048, help="timed decode steps (new tokens)")
+    ap.add_argument("--steps", type=int, default=NEW_TOKENS,
+                    help="requested timed decode steps; the headline always times the workload's "
+                         f"{NEW_TOKENS} new tokens and reports that count")
     ap.add_argument("--warmup", type=int, default=64, help="untimed decode steps first")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -488,10 +682,28 @@ def main() -> int:
                     help="skip the bs=32, MLA and prefill measurements")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only launch the dominant kernel loop (for rocprofv3 counter runs)")
-    ap.add_argument("--only", choices=("bs32", "mla", "prefill", "prompt", "minicpm3"),
+    ap.add_argument("--only", choices=("bs32", "mla", "prefill", "prompt", "minicpm3", "cpu"),
                     help="run one of the secondary configurations alone and print its line "
                          "(for rocprofv3 kernel traces of that workload)")
-    args = ap.parse_args()
+    return run(ap.parse_args())
+
+
+def parse(argv: list[str]):
+    """The parsed arguments of ``argv`` (used by the tests of the run's sizing)."""
+    saved = sys.argv
+    try:
+        sys.argv = ["bench.py", *argv]
+        ap = argparse.ArgumentParser()
+        ap.add_argument("--gpus", type=int, default=1)
+        ap.add_argument("--steps", type=int, default=NEW_TOKENS)
+        ap.add_argument("--warmup", type=int, default=64)
+        ap.add_argument("--seed", type=int, default=0)
+        return ap.parse_known_args()[0]
+    finally:
+        sys.argv = saved
+
+
+def run(args) -> int:
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode path runs on a single MI355X; "
               "run with --gpus 1 (multi-GPU sharding is described, not run).", file=sys.stderr)
@@ -500,21 +712,22 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
 
+    cfg_prompt = torch.randint(0, 151936, (PROMPT,), generator=torch.Generator().manual_seed(args.seed)).tolist()
     if args.only:
-        run = {"bs32": lambda: batch32(args.seed, args.steps), "mla": mla_decode,
-               "prefill": prefill_layer, "prompt": lambda: prompt_only(args.seed),
-               "minicpm3": lambda: minicpm3_decode(args.seed)}[args.only]
-        print(json.dumps({args.only: run()}))
+        fn = {"bs32": lambda: batch32(args.seed, NEW_TOKENS, args), "mla": mla_decode,
+              "prefill": prefill_layer, "prompt": lambda: prompt_only(args.seed, args),
+              "minicpm3": lambda: minicpm3_decode(args.seed, args=args),
+              "cpu": lambda: cpu_baseline(args.seed, cfg_prompt)}[args.only]
+        print(json.dumps({args.only: fn()}))
         return 0
 
     from tilefoundry_amd.qwen3 import Engine, QWEN3_1_7B
 
     cfg = QWEN3_1_7B
     dev = torch.device("cuda:0")
-    eng = Engine(cfg, device=dev, max_new=max(args.steps, args.warmup), prompt_room=PROMPT,
-                 seed=args.seed)
-    g = torch.Generator().manual_seed(args.seed)
-    prompt = torch.randint(0, cfg.vocab, (PROMPT,), generator=g).tolist()
+    max_new, room = sizing(args)["headline"]["engine"]
+    eng = Engine(cfg, device=dev, max_new=max_new, prompt_room=room, seed=args.seed)
+    prompt = cfg_prompt
 
     if args.kernel_only:
         # the dominant kernel's launch loop, then a plain copy of known size (the
@@ -530,19 +743,19 @@ def main() -> int:
         print(json.dumps({"kernel_only": roof, "copy_bytes": src.numel()}))
         return 0
 
-    if args.warmup > 0:
-        eng.generate(prompt, args.warmup)
+    eng.generate(prompt, max(1, args.warmup))
     torch.cuda.synchronize()
-    gen = eng.generate(prompt, args.steps)      # synchronize() on both sides inside
+    gen = eng.generate(prompt, NEW_TOKENS)      # synchronize() on both sides inside
     toks = gen.tokens_per_second
-    ms_per_step = gen.seconds * 1e3 / args.steps
+    ms_per_step = gen.seconds * 1e3 / NEW_TOKENS
+    print(f"[bench] headline {toks:.1f} tok/s over {NEW_TOKENS} steps", file=sys.stderr, flush=True)
 
     roof = dominant_kernel(eng)
-    kernels = {} if args.no_kernels else kernel_lines(eng)
-    layer = None if args.no_kernels else decode_layer_ctx4096(eng)
-    copy_bw = copy_bandwidth(dev)
+    kernels = {} if args.no_kernels else _leg(kernel_lines, eng)
+    layer = None if args.no_kernels else _leg(decode_layer_ctx4096, eng)
+    copy_bw = _leg(copy_bandwidth, dev)
     weight_bytes = sum(t.numel() * 2 for w in eng.layers for t in w.values()) + eng.embed.numel() * 2
-    mean_ctx = PROMPT + args.steps / 2.0
+    mean_ctx = PROMPT + NEW_TOKENS / 2.0
     kv_bytes = cfg.layers * mean_ctx * 2 * cfg.kv_heads * cfg.head_dim * 2
     step_bytes = weight_bytes + kv_bytes
     line = {
@@ -550,7 +763,8 @@ def main() -> int:
         "value": round(toks, 2),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": NEW_TOKENS,
+        "steps_requested": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
@@ -559,8 +773,9 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded-uniform prompt ids, random-init weights ~N(0,0.02))",
         "config": {"workload": "Qwen3-1.7B-shaped greedy decode: 28 layers, hidden 2048, 16/8 heads, "
-                               "head_dim 128, SwiGLU 6144, vocab 151936 tied; 64-token prompt",
-                   "batch": 1, "prompt_tokens": PROMPT, "new_tokens": args.steps,
+                               "head_dim 128, SwiGLU 6144, vocab 151936 tied; 64-token prompt, "
+                               f"{NEW_TOKENS} new tokens",
+                   "batch": 1, "prompt_tokens": PROMPT, "new_tokens": NEW_TOKENS,
                    "parallelism": "single GPU"},
         "step_hbm": {"bytes_per_step": int(step_bytes),
                      "GB/s": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
@@ -570,17 +785,18 @@ def main() -> int:
         "kernels": kernels,
         "decode_layer_bs1_ctx4096": layer,
         "first_tokens": gen.tokens[:8],
-        "prompt_prefill_bs1": None if args.no_kernels else prompt_prefill(eng, args.seed),
     }
     del eng
     torch.cuda.empty_cache()
+    if not args.no_kernels:
+        line["prompt_prefill_bs1"] = _leg(prompt_only, args.seed, args)
     if not args.no_configs:
-        line["bs32"] = batch32(args.seed, args.steps)
-        line["mla_decode_b8_ctx8192"] = mla_decode()
-        line["minicpm3_decode_bs1"] = minicpm3_decode(args.seed)
-        line["prefill_attention_layer"] = prefill_layer()
+        line["bs32"] = _leg(batch32, args.seed, NEW_TOKENS, args)
+        line["mla_decode_b8_ctx8192"] = _leg(mla_decode)
+        line["minicpm3_decode_bs1"] = _leg(minicpm3_decode, args.seed, args=args)
+        line["prefill_attention_layer"] = _leg(prefill_layer)
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(args.seed, prompt)
+        line["cpu_baseline"] = _leg(cpu_baseline, args.seed, prompt)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line))

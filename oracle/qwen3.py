@@ -219,6 +219,36 @@ def step(model: ModelWeights, cfg: Qwen3Config, token: int, pos: int, caches, co
     return lm_logits(h, model.gamma_final, model.head32(), cfg.eps)
 
 
+def step_batch(model: ModelWeights, cfg: Qwen3Config, tokens: list[int], positions: list[int],
+               caches_b, cos, sin, p_bf16: bool = False):
+    """One decode step of ``B`` sequences at once: the same arithmetic as
+    :func:`step` for each row (the norms, projections, RoPE and SwiGLU act row by
+    row; attention runs per sequence over its own cache), with the projections
+    as one ``[B, in]`` matmul. ``caches_b[b]`` is sequence b's per-layer
+    ``[k, v]`` list, appended in place. Returns f32 logits ``[B, V]``.
+
+    Pinned against :func:`step` run per sequence (tests/test_oracle.py)."""
+    HQ, HKV, D = cfg.heads, cfg.kv_heads, cfg.head_dim
+    B = len(tokens)
+    h = model.embed[torch.tensor(tokens, dtype=torch.int64)].clone()
+    c = cos[torch.tensor(positions, dtype=torch.int64)].unsqueeze(1)
+    s = sin[torch.tensor(positions, dtype=torch.int64)].unsqueeze(1)
+    for li, lw in enumerate(model.layers):
+        xn = rms_norm_q(h, lw.gamma_in, cfg.eps)
+        q = rope(head_norm(_proj(xn, lw, "w_q").view(B, HQ, D), lw.gamma_q, cfg.eps), c, s)
+        k = rope(head_norm(_proj(xn, lw, "w_k").view(B, HKV, D), lw.gamma_k, cfg.eps), c, s)
+        v = _proj(xn, lw, "w_v").view(B, HKV, D)
+        outs = []
+        for b in range(B):
+            cache = caches_b[b][li]
+            cache[0] = torch.cat([cache[0], k[b].unsqueeze(0)], dim=0)
+            cache[1] = torch.cat([cache[1], v[b].unsqueeze(0)], dim=0)
+            outs.append(attend(q[b], cache[0], cache[1], cfg.scale, p_bf16))
+        h1 = h + _proj(torch.stack(outs, 0), lw, "w_o")
+        h = h1 + mlp(h1, lw, cfg)
+    return lm_logits(h, model.gamma_final, model.head32(), cfg.eps)
+
+
 def empty_caches(cfg: Qwen3Config, n_layers: int):
     z = torch.zeros(0, cfg.kv_heads, cfg.head_dim, dtype=BF16)
     return [[z, z] for _ in range(n_layers)]
@@ -288,5 +318,5 @@ def prompt_ids(vocab: int, n: int = 64, seed: int = 0, batch: int = 1) -> list[l
 __all__ = [
     "Qwen3Config", "rope_tables", "proj", "head_norm", "rope", "attend", "LayerWeights",
     "self_attention", "mlp", "decoder_layer", "lm_logits", "greedy", "ModelWeights", "step",
-    "empty_caches", "decode", "random_model", "prompt_ids",
+    "step_batch", "empty_caches", "decode", "random_model", "prompt_ids",
 ]

@@ -203,6 +203,27 @@ def test_teacher_forcing_reproduces_free_run():
     assert free == forced
 
 
+def test_step_batch_equals_per_sequence_steps():
+    """The batched step (the CPU baseline's bs=32 sample) is the single-sequence
+    step row by row: three sequences at different positions, stepped together,
+    give each one's own logits and cache rows (the [B, in] matmul may sum in
+    another order, so within one bf16 landing)."""
+    cfg, model = _tiny()
+    cos, sin = OQ.rope_tables(8, cfg.head_dim, cfg.rope_theta)
+    seqs = [[5, 17, 250], [3, 99, 1], [42, 7, 8]]
+    caches_b = [OQ.empty_caches(cfg, cfg.layers) for _ in seqs]
+    singles = [OQ.empty_caches(cfg, cfg.layers) for _ in seqs]
+    for p in range(3):
+        batch = OQ.step_batch(model, cfg, [s[p] for s in seqs], [p] * 3, caches_b, cos, sin)
+        for b, s in enumerate(seqs):
+            one = OQ.step(model, cfg, s[p], p, singles[b], cos, sin)
+            assert float((batch[b] - one).norm() / one.norm()) < 2e-3
+    for b in range(3):
+        for li in range(cfg.layers):
+            for j in range(2):
+                assert int(bf16_ulps(caches_b[b][li][j], singles[b][li][j]).max()) <= 1
+
+
 # ---------------------------------------------------------------- synthetic weights
 def test_synthetic_generator_golden_values():
     """The cross-device generator's first values, pinned (any change to the
@@ -578,3 +599,203 @@ def test_minicpm3_model_oracle_planted_mistakes():
     assert _minicpm3_against_hf(lambda c: NoResidualScale(**dataclasses.asdict(c))) > 0.1
     assert _minicpm3_against_hf(lambda c: dataclasses.replace(c, scale_emb=1.0)) > 0.1
     assert _minicpm3_against_hf(lambda c: dataclasses.replace(c, dim_model_base=c.hidden * c.hidden // c.dim_model_base)) > 0.1
+
+
+# ------------------------------------------------ Qwen3 oracle against Hugging Face
+# The reference builds its decode oracle from the Hugging Face layer
+# (tests/core/models/decode_oracle.py:213-233; smoke_qwen3_1_7b.py:78-125):
+# Qwen3ForCausalLM, installed here, is the third-party arithmetic boundary. It is
+# built from a tiny config and loaded with the oracle's own random weights.
+_QWEN3_HF_NAMES = {"gamma_in": "input_layernorm", "w_q": "self_attn.q_proj", "w_k": "self_attn.k_proj",
+                   "w_v": "self_attn.v_proj", "gamma_q": "self_attn.q_norm", "gamma_k": "self_attn.k_norm",
+                   "w_o": "self_attn.o_proj", "gamma_post": "post_attention_layernorm",
+                   "w_gate": "mlp.gate_proj", "w_up": "mlp.up_proj", "w_down": "mlp.down_proj"}
+_QWEN3_PROMPT = [3, 17, 42, 99, 7, 250, 31, 400, 5, 77, 128, 9]
+
+
+def _qwen3_hf(std: float, gspread: float):
+    """(oracle config, oracle weights, HF model) from the same tiny random weights.
+    ``gspread`` is the spread of the q/k head-norm scales around 1: a wide one makes
+    the order of norm and rotation matter (planted-mistake tests)."""
+    from transformers import Qwen3Config
+    from transformers.models.qwen3 import modeling_qwen3 as HF
+
+    cfg = OQ.Qwen3Config(hidden=256, heads=4, kv_heads=2, head_dim=64, inter=512, vocab=512, layers=2)
+    m = OQ.random_model(cfg, seed=11, std=std)
+    gen = g(12)
+    for lw in m.layers:
+        lw.gamma_q = (1 + gspread * torch.randn(cfg.head_dim, generator=gen)).to(BF)
+        lw.gamma_k = (1 + gspread * torch.randn(cfg.head_dim, generator=gen)).to(BF)
+    hc = Qwen3Config(vocab_size=cfg.vocab, hidden_size=cfg.hidden, intermediate_size=cfg.inter,
+                     num_hidden_layers=cfg.layers, num_attention_heads=cfg.heads,
+                     num_key_value_heads=cfg.kv_heads, head_dim=cfg.head_dim, rms_norm_eps=cfg.eps,
+                     rope_theta=cfg.rope_theta, max_position_embeddings=4096, tie_word_embeddings=True,
+                     attention_bias=False)
+    hc._attn_implementation = "eager"
+    hf = HF.Qwen3ForCausalLM(hc).eval().to(BF)
+    # .to(bf16) also lands the rotary inverse frequencies; a bf16 checkpoint load
+    # keeps them in f32 (they are recomputed, not stored)
+    inv, _ = hf.model.rotary_emb.compute_default_rope_parameters(hc)
+    hf.model.rotary_emb.inv_freq = inv.float()
+    sd = {"model.embed_tokens.weight": m.embed, "model.norm.weight": m.gamma_final, "lm_head.weight": m.embed}
+    for i, lw in enumerate(m.layers):
+        for k, n in _QWEN3_HF_NAMES.items():
+            sd[f"model.layers.{i}.{n}.weight"] = getattr(lw, k)
+    missing, unexpected = hf.load_state_dict(sd, strict=False)
+    assert not missing and not unexpected, (missing, unexpected)
+    return cfg, m, hf
+
+
+def _qwen3_vs_hf(cfg, m, hf, prompt=_QWEN3_PROMPT):
+    """Worst relative L2 over the prompt's positions of (logits, layer-0 output):
+    the oracle's cached step by step against HF's one causal forward."""
+    with torch.no_grad():
+        out = hf(torch.tensor([prompt]), output_hidden_states=True)
+    ref_logits, ref_h0 = out.logits[0].float(), out.hidden_states[1][0].float()
+    cos, sin = OQ.rope_tables(len(prompt), cfg.head_dim, cfg.rope_theta)
+    caches = OQ.empty_caches(cfg, cfg.layers)
+    worst_l, worst_h = 0.0, 0.0
+    for p, t in enumerate(prompt):
+        h = m.embed[t].clone()
+        for li, (lw, cache) in enumerate(zip(m.layers, caches)):
+            h, k, v = OQ.decoder_layer(h, lw, cfg, cos[p], sin[p], cache[0], cache[1], p_bf16=True)
+            cache[0] = torch.cat([cache[0], k.unsqueeze(0)], 0)
+            cache[1] = torch.cat([cache[1], v.unsqueeze(0)], 0)
+            if li == 0:
+                worst_h = max(worst_h, float((h.float() - ref_h0[p]).norm() / ref_h0[p].norm()))
+        lg = OQ.lm_logits(h, m.gamma_final, m.head32(), cfg.eps)
+        worst_l = max(worst_l, float((lg - ref_logits[p]).norm() / ref_logits[p].norm()))
+    return worst_l, worst_h
+
+
+def test_qwen3_oracle_against_hugging_face():
+    """Per-position logits and the first decoder layer's output agree with HF's
+    Qwen3ForCausalLM within the bf16 bar. HF lands the RoPE products, the scores
+    and the logits in bf16 where the oracle keeps f32 (the reference kernel's
+    order), which is what remains."""
+    lg, h0 = _qwen3_vs_hf(*_qwen3_hf(std=0.02, gspread=0.1))
+    assert lg < 1e-2 and h0 < 1e-2, (lg, h0)
+    # sharp attention (larger weights, widely spread head-norm scales)
+    lg, h0 = _qwen3_vs_hf(*_qwen3_hf(std=0.05, gspread=0.5))
+    assert lg < 2e-2 and h0 < 1.5e-2, (lg, h0)
+
+
+def _sa_planted(kind):
+    """``self_attention`` with one planted mistake."""
+    def sa(h, lw, c, cos_row, sin_row, k_cache, v_cache, p_bf16=False):
+        HQ, HKV, D = c.heads, c.kv_heads, c.head_dim
+        xn = ON.rms_norm_q(h, lw.gamma_in, c.eps)
+        q = OQ._proj(xn, lw, "w_q").view(HQ, D)
+        k = OQ._proj(xn, lw, "w_k").view(HKV, D)
+        v = OQ._proj(xn, lw, "w_v").view(HKV, D)
+        if kind == "rope_before_norm":
+            q = OQ.head_norm(OQ.rope(q, cos_row, sin_row), lw.gamma_q, c.eps)
+            k = OQ.head_norm(OQ.rope(k, cos_row, sin_row), lw.gamma_k, c.eps)
+        elif kind == "no_head_norm":
+            q, k = OQ.rope(q, cos_row, sin_row), OQ.rope(k, cos_row, sin_row)
+        elif kind == "k_gamma_for_q":
+            q = OQ.rope(OQ.head_norm(q, lw.gamma_k, c.eps), cos_row, sin_row)
+            k = OQ.rope(OQ.head_norm(k, lw.gamma_k, c.eps), cos_row, sin_row)
+        kk = torch.cat([k_cache, k.unsqueeze(0)], 0)
+        vv = torch.cat([v_cache, v.unsqueeze(0)], 0)
+        return OQ._proj(OQ.attend(q, kk, vv, c.scale, p_bf16), lw, "w_o"), k, v
+    return sa
+
+
+def _mlp_swapped(h1, lw, c):
+    xn = ON.rms_norm_q(h1, lw.gamma_post, c.eps)
+    act = torch.nn.functional.silu(OQ._proj(xn, lw, "w_up").float()).to(BF) * OQ._proj(xn, lw, "w_gate")
+    return OQ._proj(act, lw, "w_down")
+
+
+@pytest.mark.parametrize("plant", ["gate_up_swapped", "rope_before_norm", "no_head_norm", "k_gamma_for_q",
+                                   "no_residual"])
+def test_qwen3_oracle_planted_mistakes_fail_the_hf_pin(plant, monkeypatch):
+    """Each planted mistake moves the logits far past the tolerance of the pin above."""
+    built = _qwen3_hf(std=0.05, gspread=0.5)
+    if plant == "gate_up_swapped":
+        monkeypatch.setattr(OQ, "mlp", _mlp_swapped)
+    elif plant == "no_residual":
+        orig = OQ.self_attention
+        monkeypatch.setattr(OQ, "decoder_layer", lambda h, lw, c, cr, sr, kc, vc, p_bf16=False: (
+            lambda a: (a[0] + OQ.mlp(a[0], lw, c), a[1], a[2]))(orig(h, lw, c, cr, sr, kc, vc, p_bf16)))
+    else:
+        monkeypatch.setattr(OQ, "self_attention", _sa_planted(plant))
+    lg, _ = _qwen3_vs_hf(*built)
+    assert lg > 0.1, (plant, lg)
+
+
+# ------------------------------------ Qwen3.5 attention-layer oracle against Hugging Face
+def _qwen35_vs_hf(std=0.05, gspread=0.5, n=24):
+    """Relative L2 of the prefill oracle's attention block (``qkv`` -> ``attention``
+    -> ``o_proj``) against Hugging Face's Qwen3_5Attention (eager, bf16) with the
+    same weights, plus the rope tables' largest difference from HF's rotary
+    module. The residual is left out of the comparison (``o_proj`` over a zero
+    hidden state) so that a small block output is not hidden under it."""
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as HF
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
+
+    from oracle import prefill as OP
+
+    pc = OP.PrefillConfig(hidden=256, heads=6, kv_heads=2, head_dim=64, rot=16)
+    lw = OP.random_layer(pc, seed=5, std=std)
+    gen = g(6)
+    lw["gamma_q"] = (gspread * torch.randn(pc.head_dim, generator=gen)).to(BF)
+    lw["gamma_k"] = (gspread * torch.randn(pc.head_dim, generator=gen)).to(BF)
+    hc = Qwen3_5TextConfig(hidden_size=pc.hidden, num_attention_heads=pc.heads, num_key_value_heads=pc.kv_heads,
+                           head_dim=pc.head_dim, rms_norm_eps=pc.eps, num_hidden_layers=1,
+                           layer_types=["full_attention"], vocab_size=64, intermediate_size=128,
+                           rope_parameters={"rope_type": "default", "rope_theta": pc.rope_theta,
+                                            "partial_rotary_factor": pc.rot / pc.head_dim},
+                           max_position_embeddings=4096, attention_bias=False)
+    hc._attn_implementation = "eager"
+    att = HF.Qwen3_5Attention(hc, 0).eval().to(BF)
+    att.load_state_dict({"q_proj.weight": lw["w_q"], "k_proj.weight": lw["w_k"], "v_proj.weight": lw["w_v"],
+                         "o_proj.weight": lw["w_o"], "q_norm.weight": lw["gamma_q"],
+                         "k_norm.weight": lw["gamma_k"]})
+    rot = HF.Qwen3_5TextRotaryEmbedding(hc)
+    hn = torch.randn(1, n, pc.hidden, generator=gen).to(BF)
+    with torch.no_grad():
+        cos_h, sin_h = rot(hn, torch.arange(n)[None])
+        mask = torch.full((n, n), float("-inf")).triu(1)[None, None].to(BF)
+        ref = att(hn, (cos_h, sin_h), mask)[0][0].float()
+    cos, sin = OP.rope_tables(n, pc)
+    table_diff = max(float((cos.float() - cos_h[0].float()).abs().max()),
+                     float((sin.float() - sin_h[0].float()).abs().max()))
+    q, gate, k, v = OP.qkv(hn[0], lw["w_q"], lw["w_k"], lw["w_v"], lw["gamma_q"], lw["gamma_k"], cos, sin, pc)
+    out = OP.o_proj(OP.attention(q, k, v, gate, pc), torch.zeros(n, pc.hidden), lw["w_o"]).float()
+    return float((out - ref).norm() / ref.norm()), table_diff
+
+
+def test_prefill_oracle_against_hugging_face():
+    """``qkv`` (per-head [q | gate] split, (1+gamma) head norms, 16 of 64 dims
+    rotated), ``attention`` (causal, sigmoid output gate) and ``o_proj`` agree
+    with HF's Qwen3_5Attention; the rope tables are HF's exactly."""
+    err, table_diff = _qwen35_vs_hf()
+    assert err < 1e-2 and table_diff == 0.0, (err, table_diff)
+    err, _ = _qwen35_vs_hf(std=0.02, gspread=0.1)
+    assert err < 1e-2, err
+
+
+@pytest.mark.parametrize("plant", ["plain_gamma", "gate_dropped", "no_rope", "full_rotation"])
+def test_prefill_oracle_planted_mistakes_fail_the_hf_pin(plant, monkeypatch):
+    from oracle import prefill as OP
+
+    if plant == "plain_gamma":        # gamma instead of (1 + gamma)
+        monkeypatch.setattr(OP, "rms_norm_1p", lambda x, gm, eps: (
+            x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + eps) * gm.float()).to(BF))
+    elif plant == "gate_dropped":     # sigmoid(gate) -> 1
+        orig = OP.attention
+        monkeypatch.setattr(OP, "attention", lambda q, k, v, gate, cfg=None, heads=None: orig(
+            q, k, v, torch.full_like(gate, 30.0), cfg))
+    elif plant == "no_rope":
+        orig_r = OP.rope_partial
+        monkeypatch.setattr(OP, "rope_partial", lambda x, c, s, rot: orig_r(x, torch.ones_like(c),
+                                                                            torch.zeros_like(s), rot))
+    elif plant == "full_rotation":    # rotate all 64 dims with the 16-dim tables tiled
+        orig_r = OP.rope_partial
+        monkeypatch.setattr(OP, "rope_partial", lambda x, c, s, rot: orig_r(
+            x, c.repeat(*([1] * (c.dim() - 1)), x.shape[-1] // rot), s.repeat(*([1] * (s.dim() - 1)),
+                                                                             x.shape[-1] // rot), x.shape[-1]))
+    err, _ = _qwen35_vs_hf()
+    assert err > 5e-2, (plant, err)
