@@ -107,6 +107,23 @@ def attention(q, k, v, gate, cfg: PrefillConfig = PrefillConfig(), heads=None):
     return torch.stack(outs, 1).reshape(N, -1)
 
 
+def attention_rows(q, k, v, gate, rows, heads, cfg: PrefillConfig = PrefillConfig()):
+    """:func:`attention` for the listed query rows and heads only: row i (its
+    position) attends keys 0..i, in the same operation order. Returns
+    ``[len(rows), len(heads), D]`` bf16. For full-length prompts where the
+    whole N x N computation would take minutes on the CPU; pinned against
+    :func:`attention` on a small prompt (tests/test_oracle.py)."""
+    out = torch.empty(len(rows), len(heads), q.shape[-1], dtype=BF16)
+    for r, i in enumerate(rows):
+        for c, h in enumerate(heads):
+            kv = h // cfg.group
+            s = (q[i, h].float().unsqueeze(0) @ k[: i + 1, kv].float().t()) * cfg.scale
+            p = torch.softmax(s, dim=-1).to(BF16)
+            o = (p.float() @ v[: i + 1, kv].float()).to(BF16)
+            out[r, c] = o[0] * torch.sigmoid(gate[i, h])
+    return out
+
+
 def o_proj(gated, hidden, w_o):
     return hidden.to(BF16) + proj(gated, w_o)
 

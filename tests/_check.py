@@ -72,3 +72,46 @@ def assert_equal(name: str, got, ref):
         g, r = g.view(torch.int16), r.view(torch.int16)
     bad = (g != r)
     assert not bool(bad.any()), f"{name}: {int(bad.sum())} of {g.numel()} elements differ"
+
+
+def forced_agreement(name: str, picks, gold, gpu_logits, top_ids, top_vals, gaps, floor: int):
+    """Teacher-forced greedy agreement with the oracle, position by position.
+
+    ``picks[i]`` is the GPU's pick at position i when fed the oracle's ids;
+    ``gold[i]`` the oracle's; ``gpu_logits[i]`` the GPU's logits there;
+    ``top_ids[i]`` / ``top_vals[i]`` the oracle's largest logits and
+    ``gaps[i]`` its top-1 / top-2 gap. At each position ``delta`` is the
+    largest |GPU - oracle| over those candidates: a pick can only flip where
+    the gap is at most ``2 * delta``. Every differing pick must be such a near
+    tie and one of the oracle's candidates; the count of equal picks is printed
+    and must reach ``floor``. Returns ``(agree, deltas)``."""
+    n = len(gold)
+    agree, ties, bad, deltas = 0, 0, [], []
+    for i in range(n):
+        ids = torch.as_tensor(top_ids[i], dtype=torch.int64)
+        got = gpu_logits[i].reshape(-1)[ids.to(gpu_logits[i].device)].double().cpu()
+        delta = float((got - torch.as_tensor(top_vals[i], dtype=torch.float64)).abs().max())
+        deltas.append(delta)
+        tie = gaps[i] <= 2.0 * delta
+        ties += int(tie)
+        if picks[i] == gold[i]:
+            agree += 1
+        elif not tie or picks[i] not in top_ids[i]:
+            bad.append((i, picks[i], gold[i], gaps[i], delta))
+    print(f"\n[agreement] {name}: {agree}/{n} picks equal the oracle's; {ties} positions are near ties "
+          f"under the measured logit error (max |delta| {max(deltas):.4g}, median "
+          f"{sorted(deltas)[n // 2]:.4g})", flush=True)
+    assert not bad, f"{name}: picks differ at clear margins (pos, got, want, gap, delta): {bad[:5]}"
+    assert agree >= floor, f"{name}: {agree}/{n} picks agree, below the floor {floor}"
+    return agree, deltas
+
+
+def oracle_candidates(logits_list, k: int = 16):
+    """(top_ids, top_vals, gaps) of a list of oracle logits."""
+    ids, vals, gaps = [], [], []
+    for lg in logits_list:
+        t = torch.topk(lg.float(), k)
+        ids.append(t.indices.tolist())
+        vals.append([float(v) for v in t.values])
+        gaps.append(float(t.values[0] - t.values[1]))
+    return ids, vals, gaps

@@ -6,7 +6,7 @@ import torch
 
 from oracle import norms as ON
 from oracle import qwen3 as OQ
-from tests._check import assert_close, assert_equal, assert_l2, max_rel
+from tests._check import forced_agreement, oracle_candidates, assert_close, assert_equal, assert_l2, max_rel
 
 BF = torch.bfloat16
 H, HQ, HKV, D, I = 2048, 16, 8, 128, 6144
@@ -217,27 +217,33 @@ def test_batch_engine_logits(dev):
 
 @pytest.mark.gpu
 def test_batch_engine_greedy(dev):
-    """Each sequence's free-running ids equal the oracle's bs=1 decode of that
-    sequence wherever the oracle's own top-2 margin is resolvable."""
+    """32 sequences teacher-forced along their oracle greedy ids (three of them
+    checked against the oracle's bs=1 decode): every pick equals the oracle's
+    except at near ties under the measured logit error; the free run of each
+    leaves the oracle only at such a tie."""
     from tilefoundry_amd.qwen3 import BatchEngine
 
     cfg, wts = _small()
-    B = 32
+    B, n = 32, 16
     eng = BatchEngine(cfg, batch=B, device=dev, max_new=32, prompt_room=32, weights=wts)
     prompts = OQ.prompt_ids(cfg.vocab, 8, seed=22, batch=B)
-    gen = eng.generate(prompts, 16)
     om, oc = _oracle(wts, cfg)
-    agree = 0
-    for b in (0, 7, 31):
+    checked = (0, 7, 31)
+    wants, recs = {}, {}
+    for b in checked:
         rec = []
-        want = OQ.decode(om, oc, prompts[b], 16, record=rec, p_bf16=True)
-        diff = next((i for i, (x, y) in enumerate(zip(gen.tokens[b], want)) if x != y), None)
-        if diff is None:
-            agree += 1
-        else:
-            lg, pick, gap = rec[diff]
-            assert gap < 1e-2 * float(lg.abs().max()), f"seq {b} step {diff}: clear margin {gap:.4g}"
-    assert agree >= 2
+        wants[b] = OQ.decode(om, oc, prompts[b], n, record=rec, p_bf16=True)
+        recs[b] = rec
+    teachers = [wants[b][:-1] if b in wants else prompts[b][:1] * (n - 1) for b in range(B)]
+    picks, logits = eng.forced(prompts, teachers, record_logits=True)
+    gen = eng.generate(prompts, n)
+    for b in checked:
+        ids, vals, gaps = oracle_candidates([r[0] for r in recs[b]])
+        _, deltas = forced_agreement(f"2-layer bs=32, sequence {b}", picks[b], wants[b], [lg[b] for lg in logits],
+                                     ids, vals, gaps, floor=n - 2)
+        diff = next((i for i, (x, y) in enumerate(zip(gen.tokens[b], wants[b])) if x != y), None)
+        if diff is not None:
+            assert gaps[diff] <= 2 * deltas[diff], f"seq {b}: free run leaves the oracle at a clear margin"
 
 
 @pytest.mark.gpu
@@ -252,3 +258,38 @@ def test_batch_engine_matches_single_engine(dev):
     got = be.logits_for(prompts)
     for b in range(2):
         assert_l2(f"seq {b}", got[b], se.logits_for(prompts[b]))
+
+
+@pytest.mark.gpu
+def test_full_model_batch32_golden(dev):
+    """The full Qwen3-1.7B-shaped model (28 layers, vocab 151936) at bs=32:
+    teacher-forced along the oracle's 32 greedy ids of 4 of the 32 sequences
+    (tests/golden/qwen3_batch_golden.json, the oracle stepping them together),
+    every pick equals the oracle's except at near ties under the measured logit
+    error; the agreement count is printed per sequence. This model's logits are
+    flat: 22-25 of each sequence's 32 positions have a top-2 gap under 0.26, twice
+    the largest logit spread between the oracle's own two valid orders."""
+    import json
+    from pathlib import Path
+
+    from tilefoundry_amd.qwen3 import BatchEngine, QWEN3_1_7B
+
+    gold = json.loads((Path(__file__).parent / "golden" / "qwen3_batch_golden.json").read_text())
+    B, keep = gold["batch"], gold["kept"]
+    prompts = OQ.prompt_ids(QWEN3_1_7B.vocab, len(gold["prompts"][0]), seed=gold["prompt_seed"], batch=B)
+    assert prompts[:keep] == gold["prompts"]
+    n = len(gold["tokens"][0])
+    eng = BatchEngine(QWEN3_1_7B, batch=B, device=dev, max_new=n, prompt_room=len(prompts[0]), seed=gold["seed"])
+    filler = OQ.prompt_ids(QWEN3_1_7B.vocab, n - 1, seed=99, batch=B)
+    teachers = [gold["tokens"][b][:-1] if b < keep else filler[b] for b in range(B)]
+    picks, logits = eng.forced(prompts, teachers, record_logits=True)
+    total = 0
+    for b in range(keep):
+        agree, _ = forced_agreement(f"28-layer bs=32, sequence {b}, 32 teacher-forced positions", picks[b],
+                                    gold["tokens"][b], [lg[b] for lg in logits], gold["top_ids"][b],
+                                    gold["top_vals"][b], gold["gaps"][b], floor=n - 8)
+        total += agree
+    print(f"[agreement] 28-layer bs=32: {total}/{keep * n} over the {keep} checked sequences", flush=True)
+    # the bs=1 model's own two valid orders agree on 91 % of picks (233 / 256);
+    # over 128 positions hold the batch to 87.5 %
+    assert total >= 112, f"{total}/{keep * n}"

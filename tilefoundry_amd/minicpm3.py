@@ -524,6 +524,25 @@ class MiniCPM3Engine:
         if code:
             raise RuntimeError(f"a decode kernel found an index out of range (code {code})")
 
+    def forced(self, prompts: list[list[int]], teachers: list[list[int]], record_logits: bool = False):
+        """Teacher-forced greedy picks: position ``len(prompt) - 1 + i`` of sequence b
+        is fed ``teachers[b][i - 1]``. Returns the picks ``[batch][len(teacher) + 1]``
+        (and, when asked, the logits ``[batch, vocab]`` of each of those positions)."""
+        if len(teachers) != self.batch or any(len(t) != len(teachers[0]) for t in teachers):
+            raise ValueError(f"give {self.batch} teacher sequences of equal length")
+        rows = [list(p) + list(t) for p, t in zip(prompts, teachers)]
+        self._load(rows, len(rows[0]))
+        pl = len(prompts[0])
+        logits = []
+        for p in range(len(rows[0])):
+            self._run_step()
+            if record_logits and p >= pl - 1:
+                logits.append(self.logits.clone())
+        torch.cuda.synchronize(self.device)
+        self.check_device_errors()
+        picks = self.sam[:, pl - 1: len(rows[0])].tolist()
+        return (picks, logits) if record_logits else picks
+
     def generate(self, prompts: list[list[int]], max_new: int, sampler=None):
         """Walk every prompt, then continue each for ``max_new`` tokens, greedy
         (lowest-index argmax over the bf16 logits) or drawn by ``sampler(logits)``.

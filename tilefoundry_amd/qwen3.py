@@ -423,15 +423,17 @@ class Engine:
     def forced(self, prompt_ids: list[int], teacher: list[int], record_logits: bool = False):
         """Teacher-forced picks: position ``len(prompt) - 1 + i`` is fed ``teacher[i-1]``.
 
-        Returns the model's pick at each of ``len(teacher) + 1`` positions (and
-        the f32 logits of each, when asked)."""
+        The prompt is walked, or prefilled with ``prompt_prefill``, as in
+        ``generate``. Returns the model's pick at each of ``len(teacher) + 1``
+        positions (and the f32 logits of each, when asked)."""
         ids = list(prompt_ids) + list(teacher)
         self._load(ids, len(ids))
         pl = len(prompt_ids)
+        self._walk_or_prefill([list(prompt_ids)])
         logits = []
-        for p in range(len(ids)):
+        for _ in range(pl - 1, len(ids)):
             self._run_step()
-            if record_logits and p >= pl - 1:
+            if record_logits:
                 logits.append(self.logits.clone())
         torch.cuda.synchronize(self.device)
         self.check_device_errors()
@@ -609,6 +611,31 @@ class BatchEngine:
         self.check_device_errors()
         out = self.sam[:, pl - 1: pl - 1 + max_new].tolist()
         return Generated(out, t2 - t1, t1 - t0, pl)
+
+    def forced(self, prompts: list[list[int]], teachers: list[list[int]], record_logits: bool = False):
+        """Teacher-forced picks of every sequence: position ``len(prompt) - 1 + i``
+        of sequence b is fed ``teachers[b][i - 1]``; the prompts are walked, or
+        prefilled with ``prompt_prefill``. Returns the picks ``[batch]
+        [len(teacher) + 1]`` (and, when asked, the f32 logits ``[batch, vocab]`` of
+        each of those positions: those steps run eagerly, since the captured step
+        writes only the per-group winners)."""
+        if len(teachers) != self.batch or any(len(t) != len(teachers[0]) for t in teachers):
+            raise ValueError(f"give {self.batch} teacher sequences of equal length")
+        rows = [list(p) + list(t) for p, t in zip(prompts, teachers)]
+        self._load(rows, len(rows[0]))
+        pl = len(prompts[0])
+        self._walk_or_prefill([list(p) for p in prompts])
+        logits = []
+        for _ in range(pl - 1, len(rows[0])):
+            if record_logits:
+                self._step(keep_logits=True)
+                logits.append(self.logits.clone())
+            else:
+                self._run_step()
+        torch.cuda.synchronize(self.device)
+        self.check_device_errors()
+        picks = self.sam[:, pl - 1: len(rows[0])].tolist()
+        return (picks, logits) if record_logits else picks
 
     def logits_for(self, prompts: list[list[int]]) -> torch.Tensor:
         """f32 logits [batch, vocab] after consuming every token of each prompt
