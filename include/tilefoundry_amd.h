@@ -369,6 +369,28 @@ int tfa_rope_attend(const void* q_up, const void* kv_up, const void* k_rope, con
                     int64_t heads, int64_t nope, int64_t rope, int64_t v_dim, float* op, float* mp,
                     float* lp, void* attn, void* k_new, void* v_new, int* err, hipStream_t stream);
 
+/* tfa_rope_attend with no workspace argument: the same kernels, arguments and
+ * results, with the split partials (op, then mp and lp) kept in a file-scope
+ * device array of tfa_rope_attend_noalloc_max_floats() = 1,048,576 floats
+ * (4 MiB) that each GPU the library runs on holds until the process ends.
+ * Nothing is allocated, by the library or the caller.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).
+ * Limit: tfa_rope_attend_splits(cap) * heads * (v_dim + 2) <= 1,048,576, else
+ * TFA_ERR_CAPACITY (MiniCPM3's 40 heads x 64 value dims: cap <= 101,632).
+ * The first call on a device resolves the array's address there
+ * (hipGetSymbolAddress); make that call outside graph capture. Every call on
+ * one GPU shares that GPU's array, so calls that overlap on one GPU (on two
+ * streams, or from two threads) race; nothing in the array needs clearing,
+ * since each call writes every partial it reads. */
+int64_t tfa_rope_attend_noalloc_max_floats(void);
+int tfa_rope_attend_noalloc(const void* q_up, const void* kv_up, const void* k_rope, const void* cos_t,
+                            const void* sin_t, int64_t rope_rows, const int* pos, const void* k_cache,
+                            const void* v_cache, int64_t cap, const int* ctx, const void* scale,
+                            int64_t heads, int64_t nope, int64_t rope, int64_t v_dim, void* attn,
+                            void* k_new, void* v_new, int* err, hipStream_t stream);
+
 /* out[i, j] = bf16(residual[i, j] + bf16(bf16(sum_s part[s, i, j]) * alpha)) for
  * part [ks, m, n] f32 split-K partials (n % 8 == 0): the o_proj epilogue with
  * MiniCPM3's scale_depth residual.

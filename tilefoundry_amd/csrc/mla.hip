@@ -29,6 +29,8 @@
 // kernels/cute_gemv.py:430-495 and reference_ops.py:63-65 (gemv_residual).
 #include <float.h>
 
+#include <mutex>
+
 #include "abi_util.h"
 #include "common.h"
 
@@ -74,7 +76,7 @@ __global__ __launch_bounds__(kThreads) void mla_prep_kernel(
     const uint16_t* __restrict__ sin_t, int rope_rows, const int* __restrict__ pos,
     uint16_t* __restrict__ lat_cache, uint16_t* __restrict__ rope_cache, int cap,
     uint16_t* __restrict__ q_n, int* err) {
-  __shared__ float scratch[2][kWaves];
+  __shared__ float sumsq[2][kWaves];
   __shared__ float kr[kRope];
   const int b = blockIdx.x;
   const int t = threadIdx.x;
@@ -119,15 +121,15 @@ __global__ __launch_bounds__(kThreads) void mla_prep_kernel(
   const float sk = wave_sum(cv * cv);
   const int lane = t & (kWave - 1), wid = t / kWave;
   if (lane == 0) {
-    scratch[0][wid] = ss;
-    scratch[1][wid] = sk;
+    sumsq[0][wid] = ss;
+    sumsq[1][wid] = sk;
   }
   __syncthreads();   // also publishes kr
   float tq = 0.f, tk = 0.f;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
-    tq += scratch[0][w];
-    tk += scratch[1][w];
+    tq += sumsq[0][w];
+    tk += sumsq[1][w];
   }
   const float rq = rsqrt_rn(tq / static_cast<float>(qa) + eps);
   const float rk = rsqrt_rn(tk / static_cast<float>(kLat) + eps);
@@ -497,7 +499,7 @@ __global__ __launch_bounds__(kThreads) void mla_combine_up_kernel(
     uint16_t* __restrict__ attn) {
   __shared__ float wgt[kMaxSplits];
   __shared__ float olat[kLat];
-  __shared__ float scratch[kWaves];
+  __shared__ float wave_max_s[kWaves];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int t = threadIdx.x;
@@ -508,9 +510,9 @@ __global__ __launch_bounds__(kThreads) void mla_combine_up_kernel(
   float mx = -INFINITY;
   for (int s = t; s < nsa; s += kThreads) mx = fmaxf(mx, mp[srow + static_cast<size_t>(s) * H]);
   mx = wave_max(mx);
-  if ((t & (kWave - 1)) == 0) scratch[t / kWave] = mx;
+  if ((t & (kWave - 1)) == 0) wave_max_s[t / kWave] = mx;
   lds_barrier();
-  const float M = fmaxf(fmaxf(scratch[0], scratch[1]), fmaxf(scratch[2], scratch[3]));
+  const float M = fmaxf(fmaxf(wave_max_s[0], wave_max_s[1]), fmaxf(wave_max_s[2], wave_max_s[3]));
   lds_barrier();
   for (int s = t; s < nsa; s += kThreads) {
     const size_t i = srow + static_cast<size_t>(s) * H;
@@ -743,6 +745,43 @@ __global__ __launch_bounds__(kThreads) void rope_attend_merge_kernel(const RopeA
 
 }  // namespace
 
+// ------------------------------------------------- no-allocation rope_attend
+// tfa_rope_attend_noalloc keeps the split partials (op [ns, heads, v_dim], then
+// mp and lp [ns, heads]) in this array instead of a caller's workspace. Each GPU
+// the library runs on holds its own copy until the process ends. In host code
+// the name is only a stand-in: the device address comes from
+// hipGetSymbolAddress, once per device, and only that address reaches a kernel.
+constexpr int64_t kRaScratchFloats = int64_t(1) << 20;   // 4 MiB
+static __device__ __align__(256) float scratch[kRaScratchFloats];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_base[kMaxScratchDevices] = {};
+
+// The current device's address of `scratch`, resolved on its first use there.
+int scratch_base(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(TFA_ERR_LAUNCH, "tfa_rope_attend_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(TFA_ERR_ARG, "tfa_rope_attend_noalloc: device %d beyond the %d the library tracks", dev,
+                kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_base[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(TFA_ERR_LAUNCH, "tfa_rope_attend_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_base[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_base[dev];
+  return TFA_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int tfa_mla_prep(const float* part, int64_t ks, int64_t batch, int64_t q_lora, const void* gamma_q_a,
@@ -932,6 +971,34 @@ int tfa_rope_attend(const void* q_up, const void* kv_up, const void* k_rope, con
   }
   rope_attend_merge_kernel<<<(unsigned)heads, kThreads, 0, stream>>>(a);
   return launched("rope_attend_merge");
+}
+
+int64_t tfa_rope_attend_noalloc_max_floats(void) { return kRaScratchFloats; }
+
+int tfa_rope_attend_noalloc(const void* q_up, const void* kv_up, const void* k_rope, const void* cos_t,
+                            const void* sin_t, int64_t rope_rows, const int* pos, const void* k_cache,
+                            const void* v_cache, int64_t cap, const int* ctx, const void* scale,
+                            int64_t heads, int64_t nope, int64_t rope, int64_t v_dim, void* attn,
+                            void* k_new, void* v_new, int* err, hipStream_t stream) {
+  float *op = nullptr, *mp = nullptr, *lp = nullptr;
+  const int64_t ns = tfa_rope_attend_splits(cap);
+  if (ns > 0) {
+    TFA_REQUIRE(heads >= 1 && heads <= 65535 && v_dim >= 1 && v_dim <= kRaMaxV, TFA_ERR_SHAPE,
+                "tfa_rope_attend_noalloc: need heads in [1, 65535] and v_dim in [1, %d]", kRaMaxV);
+    const int64_t need = ns * heads * (v_dim + 2);
+    TFA_REQUIRE(need <= kRaScratchFloats, TFA_ERR_CAPACITY,
+                "tfa_rope_attend_noalloc: %lld splits x %lld heads x (v_dim %lld + 2) = %lld floats exceed the "
+                "%lld-float scratch array; use tfa_rope_attend with a workspace",
+                (long long)ns, (long long)heads, (long long)v_dim, (long long)need, (long long)kRaScratchFloats);
+    float* base = nullptr;
+    const int st = scratch_base(&base);
+    if (st != TFA_OK) return st;
+    op = base;
+    mp = base + ns * heads * v_dim;
+    lp = mp + ns * heads;
+  }
+  return tfa_rope_attend(q_up, kv_up, k_rope, cos_t, sin_t, rope_rows, pos, k_cache, v_cache, cap, ctx, scale,
+                         heads, nope, rope, v_dim, op, mp, lp, attn, k_new, v_new, err, stream);
 }
 
 }  // extern "C"
