@@ -467,7 +467,8 @@ def prefill_layer(ns=(1024, 4096, 8192)) -> dict:
         f_qkv = lambda: C.qkv_norm_rope(hn, w_qkv, qkv, HQ, HKV, gq, gk, 1e-6, cos, sin)
         f_att = lambda: C.prefill_attention(qv[:, :, :D], kv, vv, qv[:, :, D:], attn, D ** -0.5)
         f_o = lambda: C.gemm_nt(attn, w_o, res, hidden)
-        f_qkv()
+        for _ in range(3):          # clocks up and caches warm before any timing
+            f_qkv(), f_att(), f_o()
         reps = 20 if n <= 4096 else 8
         t_qkv = _events_time(f_qkv, reps)
         t_att = _events_time(f_att, reps)

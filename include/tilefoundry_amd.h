@@ -416,12 +416,10 @@ int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void*
                           int64_t head_dim, float scale, hipStream_t stream);
 
 /* C[m, n] = bf16(A[m, k] . B[n, k]^T) (residual == NULL) or
- * C = bf16(residual + bf16(A . B^T)) (residual [m, ldr]); bf16 in, f32 accumulate.
- * The product runs on hipBLASLt (one plan per device and shape, made on the
- * first call, no workspace), the residual as a separate pass; shapes without a
- * library plan -- and all shapes when TFA_GEMM_NATIVE=1 -- use the built-in bf16
- * MFMA kernel. Row strides lda / ldb / ldc in elements. m >= 1, n a multiple of
- * 256, k of 64; lda, ldb multiples of 8 (and ldc, ldr with a residual).
+ * C = bf16(residual + bf16(A . B^T)) (residual [m, ldr]); bf16 in, f32 accumulate
+ * on bf16 MFMA, the residual added in the kernel's epilogue. Row strides lda /
+ * ldb / ldc in elements. m >= 1, n a multiple of 128, k of 64; lda, ldb
+ * multiples of 8, ldc, ldr of 4; a, b 16-byte and c, residual 8-byte aligned.
  * Replaces: examples/qwen3_8_27b_prefill-tilelang/kernels/gemm.py:104-356 (gemm_kernel,
  * "residual" epilogue :193-198 -- model.py:326-333 Attention.o_proj). */
 int tfa_gemm_nt(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
@@ -432,7 +430,8 @@ int tfa_gemm_nt(const void* a, const void* b, void* c, int64_t m, int64_t n, int
  * gate_{H-1} | k_0..k_{G-1} | v_0..v_{G-1}] (256 rows each); then per token the q
  * and k slices get bf16(x * rsqrt(mean x^2 + eps) * (1 + gamma)) (f32) and
  * rotate-half RoPE on dims 0..rot-1 with cos/sin [n, rot] (bf16 products and
- * sum). head_dim 256, rot 64; n a multiple of 256, hidden of 64.
+ * sum), all in the GEMM's epilogue. head_dim 256, rot 64; n >= 1, hidden a
+ * multiple of 64.
  * Replaces: examples/qwen3_8_27b_prefill-tilelang/kernels/gemm.py:226-300 ("qk_norm_rope"
  * epilogue), model.py:271-303 (Attention.qkv), kernels/pack.py:48-64 (the layout). */
 int tfa_qkv_norm_rope(const void* hn, const void* w_qkv, void* out, int64_t n, int64_t hidden, int64_t heads,
@@ -444,24 +443,39 @@ int tfa_qkv_norm_rope(const void* hn, const void* w_qkv, void* out, int64_t n, i
 /* C[m, n] = A[m, k] . B[n, k]^T in f32 (bf16 in, f32 accumulate, no rounding):
  * the prompt rows' projections, landed in bf16 by their consumers exactly as
  * the decode step lands its split-K partials (tfa_rows_norm, tfa_silu_mul and
- * tfa_prefill_qk_rope with ks = 1). hipBLASLt with the fallback of tfa_gemm_nt;
- * m >= 1, n a multiple of 256, k of 64, lda / ldb multiples of 8.
+ * tfa_prefill_qk_rope with ks = 1). The MFMA kernel of tfa_gemm_nt with an f32
+ * store; m >= 1, n a multiple of 128, k of 64, lda / ldb multiples of 8.
  * Replaces: the per-token projection GEMVs of the prompt walk,
  * examples/qwen3_1_7b-tilelang/fast/engine.py:261-263 over fast/kernels.py:123-145
  * (gemv) -- the same products for every prompt row in one call. */
 int tfa_gemm_nt_f32(const void* a, const void* b, float* c, int64_t m, int64_t n, int64_t k, int64_t lda,
                     int64_t ldb, int64_t ldc, hipStream_t stream);
 
-/* SwiGLU of the prompt rows' fused gate|up product: gu f32 [rows, ld] with
- * column 2i = gate_i, 2i+1 = up_i (the interleaved decode weight layout);
+/* The same product with K split into ks equal ranges (ks in [1, 8], dividing k / 64):
+ * range z lands, unrounded, in c + z * m * ldc, so c holds ks partials [ks, m, ldc]
+ * whose consumers sum them in split order (tfa_rows_norm, tfa_swiglu_pairs and
+ * tfa_prefill_qk_rope take ks). For few token rows, where the unsplit grid leaves
+ * most CUs idle. Replaces the same products as tfa_gemm_nt_f32. */
+int tfa_gemm_nt_f32_split(const void* a, const void* b, float* c, int64_t m, int64_t n, int64_t k, int64_t lda,
+                          int64_t ldb, int64_t ldc, int64_t ks, hipStream_t stream);
+
+/* The split count tfa_gemm_nt_f32_split is fastest with for this shape on the
+ * current device (1 when the unsplit grid fills the CUs). */
+int64_t tfa_gemm_f32_splits(int64_t m, int64_t n, int64_t k);
+
+/* SwiGLU of the prompt rows' fused gate|up product: gu f32 [ks, rows, ld] split-K
+ * partials (ks in [1, 8], summed in split order) with column 2i = gate_i, 2i+1 =
+ * up_i (the interleaved decode weight layout);
  * act[r, i] = bf16(bf16(silu(bf16 g)) * bf16 u) -- the decode step's epilogue.
  * inter a multiple of 4; ld >= 2*inter, a multiple of 4; gu 16-byte aligned.
  * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:547-572 (silu_mul) and the
  * SwiGLU prologue of :210-257 (gemv_silu), for every prompt row at once. */
-int tfa_swiglu_pairs(const float* gu, int64_t ld, int64_t rows, int64_t inter, void* act, hipStream_t stream);
+int tfa_swiglu_pairs(const float* gu, int64_t ks, int64_t ld, int64_t rows, int64_t inter, void* act,
+                     hipStream_t stream);
 
 /* Per-head norm + RoPE + cache write for the prompt rows of a batch: qkv f32
- * [batch * n, ldq] holds sequence b's row r at b * n + r (position pos0 + r),
+ * [ks, batch * n, ldq] split-K partials (ks in [1, 8], summed in split order)
+ * hold sequence b's row r at b * n + r (position pos0 + r),
  * columns [q (hq*128) | k (hkv*128) | v (hkv*128)]. Each head lands in bf16;
  * query heads get Qwen3RMSNorm(gamma_q) + rotate-half RoPE at the position and
  * go to q_out[(b*n + r), hq*128]; key heads the same with gamma_k into
@@ -471,9 +485,9 @@ int tfa_swiglu_pairs(const float* gu, int64_t ld, int64_t rows, int64_t inter, v
  * projection values. head_dim 128; pos0 + n <= cap and <= rope_rows.
  * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:328-411 (qk_rope_cache) run
  * once per prompt token by the walk (fast/engine.py:261-263). */
-int tfa_prefill_qk_rope(const float* qkv, int64_t ldq, const void* gamma_q, const void* gamma_k, float eps_head,
-                        const void* cos_t, const void* sin_t, int64_t rope_rows, int64_t batch, int64_t n,
-                        int64_t pos0, void* k_cache, void* v_cache, int64_t cap, void* q_out, int64_t hq,
+int tfa_prefill_qk_rope(const float* qkv, int64_t ks, int64_t ldq, const void* gamma_q, const void* gamma_k,
+                        float eps_head, const void* cos_t, const void* sin_t, int64_t rope_rows, int64_t batch,
+                        int64_t n, int64_t pos0, void* k_cache, void* v_cache, int64_t cap, void* q_out, int64_t hq,
                         int64_t hkv, int64_t head_dim, hipStream_t stream);
 
 /* Causal GQA attention of every row of a batch of prompts, no gate:

@@ -168,23 +168,35 @@ def test_batched_argument_checks(lib):
 
 
 def test_prompt_prefill_argument_checks(lib):
-    # f32 GEMM: n not a multiple of 256, k not of 64, a null operand
+    # f32 GEMM: n not a multiple of 128, k not of 64, a null operand
     st, msg = call(lib, "tfa_gemm_nt_f32", A, A, A, I64(37), I64(300), I64(2048), I64(2048), I64(2048), I64(300), P(None))
-    assert st == SHAPE and "256" in msg
+    assert st == SHAPE and "128" in msg
     st, _ = call(lib, "tfa_gemm_nt_f32", A, A, A, I64(37), I64(512), I64(100), I64(100), I64(100), I64(512), P(None))
     assert st == SHAPE
     st, _ = call(lib, "tfa_gemm_nt_f32", P(None), A, A, I64(37), I64(512), I64(2048), I64(2048), I64(2048), I64(512), P(None))
     assert st == NULL
-    # SwiGLU pairs: odd inter, ld too small, misaligned gu
-    st, _ = call(lib, "tfa_swiglu_pairs", A, I64(12288), I64(4), I64(6146), A, P(None))
+    # split f32 GEMM: splits that do not divide the k-tiles, too many splits
+    st, msg = call(lib, "tfa_gemm_nt_f32_split", A, A, A, I64(37), I64(512), I64(2048), I64(2048), I64(2048),
+                   I64(512), I64(3), P(None))
+    assert st == SHAPE and "splits" in msg
+    st, _ = call(lib, "tfa_gemm_nt_f32_split", A, A, A, I64(37), I64(512), I64(2048), I64(2048), I64(2048),
+                 I64(512), I64(16), P(None))
     assert st == SHAPE
-    st, _ = call(lib, "tfa_swiglu_pairs", A, I64(100), I64(4), I64(6144), A, P(None))
+    # SwiGLU pairs: odd inter, ld too small, misaligned gu, bad split count
+    st, _ = call(lib, "tfa_swiglu_pairs", A, I64(1), I64(12288), I64(4), I64(6146), A, P(None))
     assert st == SHAPE
-    st, _ = call(lib, "tfa_swiglu_pairs", MIS, I64(12288), I64(4), I64(6144), A, P(None))
+    st, _ = call(lib, "tfa_swiglu_pairs", A, I64(1), I64(100), I64(4), I64(6144), A, P(None))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_swiglu_pairs", MIS, I64(1), I64(12288), I64(4), I64(6144), A, P(None))
     assert st == ALIGN
-    # q/k norm + RoPE rows: positions past the cache or the rope table, head_dim
-    qk = lambda n, pos0, cap, rope, hd=128: (A, I64(4096), A, A, F(1e-6), A, A, I64(rope), I64(2), I64(n),
-                                             I64(pos0), A, A, I64(cap), A, I64(16), I64(8), I64(hd), P(None))
+    st, _ = call(lib, "tfa_swiglu_pairs", A, I64(9), I64(12288), I64(4), I64(6144), A, P(None))
+    assert st == SHAPE
+    # q/k norm + RoPE rows: positions past the cache or the rope table, head_dim, split count
+    qk = lambda n, pos0, cap, rope, hd=128, ks=1: (A, I64(ks), I64(4096), A, A, F(1e-6), A, A, I64(rope), I64(2),
+                                                   I64(n), I64(pos0), A, A, I64(cap), A, I64(16), I64(8), I64(hd),
+                                                   P(None))
+    st, msg = call(lib, "tfa_prefill_qk_rope", *qk(100, 0, 512, 512, ks=0))
+    assert st == SHAPE and "ks" in msg
     st, msg = call(lib, "tfa_prefill_qk_rope", *qk(100, 10, 100, 512))
     assert st == CAPACITY and "capacity" in msg
     st, msg = call(lib, "tfa_prefill_qk_rope", *qk(100, 0, 512, 64))

@@ -92,6 +92,7 @@ def test_prefill_attention_causal_prefix_4096(dev):
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (512, 768, 320), (1024, 5120, 6144)])
 def test_gemm_nt(dev, M, N, K):
+    """bf16 store against the f32 product (the 128 x 128 tile: small grids)."""
     from tilefoundry_amd._lib import C
 
     g = torch.Generator().manual_seed(M + N + K)
@@ -134,50 +135,27 @@ def test_o_proj_residual(dev):
     assert frac < 0.02, f"{frac:.3%} of outputs differ from the oracle"
 
 
-_NATIVE_GEMM = """
-import sys, torch
-from tilefoundry_amd._lib import C
-a, b, res = (torch.load(sys.argv[1], weights_only=True)[k].to("cuda:0") for k in ("a", "b", "res"))
-plain = torch.empty(a.shape[0], b.shape[0], dtype=torch.bfloat16, device="cuda:0")
-resid = torch.empty_like(plain)
-C.gemm_nt(a, b, plain, None)
-C.gemm_nt(a, b, resid, res)
-f32 = torch.full((a.shape[0], b.shape[0]), float("nan"), device="cuda:0")
-C.gemm_nt_f32(a, b, f32)
-ragged = torch.full((37, b.shape[0]), float("nan"), device="cuda:0")
-C.gemm_nt_f32(a[:37], b, ragged)
-torch.save({"plain": plain.cpu(), "resid": resid.cpu(), "f32": f32.cpu(), "ragged": ragged.cpu()}, sys.argv[2])
-"""
-
-
 @pytest.mark.gpu
-def test_gemm_native_kernel(dev, tmp_path):
-    """The hand-written MFMA GEMM (the path for shapes the library has no plan
-    for, forced by TFA_GEMM_NATIVE=1 in a child process) against the oracle, plain,
-    with the o_proj residual, and with the f32 store (full and 37-row ragged)."""
-    import os
-    import subprocess
-    import sys
+@pytest.mark.parametrize("M,N,K", [(512, 768, 320), (37, 2048, 2048), (1024, 12288, 2048), (4096, 4096, 2048)])
+def test_gemm_tiles_f32_and_ragged(dev, M, N, K):
+    """Each tile shape the launch picks (128 x 128 for small grids, 256 x 256 for
+    full rounds) with the f32 store -- including a 37-row ragged edge and a
+    gate|up-sized product at 1024 rows -- within an f64 error bound, and the bf16
+    store of the same product equal to the f32 sums landed in bf16."""
+    from tilefoundry_amd._lib import C
 
-    g = torch.Generator().manual_seed(31)
-    M, N, K = 512, 768, 320
+    g = torch.Generator().manual_seed(M + N + K)
     a = torch.randn(M, K, generator=g).to(BF)
     b = (0.05 * torch.randn(N, K, generator=g)).to(BF)
-    res = torch.randn(M, N, generator=g).to(BF)
-    torch.save({"a": a, "b": b, "res": res}, tmp_path / "in.pt")
-    env = dict(os.environ, TFA_GEMM_NATIVE="1")
-    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    subprocess.run([sys.executable, "-c", _NATIVE_GEMM, str(tmp_path / "in.pt"), str(tmp_path / "out.pt")],
-                   env=env, cwd=root, check=True, timeout=120)
-    out = torch.load(tmp_path / "out.pt", weights_only=True)
-    ref = a.float() @ b.float().t()
-    assert_close("native gemm", out["plain"], ref.to(BF))
-    assert rel_l2(out["plain"], ref) < 4e-3
-    assert_close("native gemm + residual", out["resid"], OP.o_proj(a, res, b))
+    ad, bd = a.to(dev), b.to(dev)
+    f32 = torch.full((M, N), float("nan"), device=dev)
+    C.gemm_nt_f32(ad, bd, f32)
+    plain = torch.empty(M, N, dtype=BF, device=dev)
+    C.gemm_nt(ad, bd, plain, None)
     ref64 = a.double() @ b.double().t()
     bound = K * 2.0 ** -23 * (a.double().abs() @ b.double().abs().t()) + 1e-6
-    assert bool(((out["f32"].double() - ref64).abs() <= bound).all()), "native f32 store"
-    assert bool(((out["ragged"].double() - ref64[:37]).abs() <= bound[:37]).all()), "native f32 ragged rows"
+    assert bool(((f32.cpu().double() - ref64).abs() <= bound).all()), "f32 store outside the f64 bound"
+    assert_equal("bf16 store == landed f32 sums", plain, f32.to(BF))
 
 
 def _layer_weights(seed=5):
@@ -243,3 +221,27 @@ def test_attention_layer_end_to_end(dev):
     assert_close("layer output", out, ref)
     branch = out.cpu().float() - hidden.float()
     assert rel_l2(branch, ref.float() - hidden.float()) < 0.1
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,ks", [(63, 4096, 2048, 8), (63, 2048, 6144, 8), (511, 12288, 2048, 2), (37, 768, 320, 5)])
+def test_gemm_f32_split_partials(dev, M, N, K, ks):
+    """K split into ks ranges: the partial slices sum (in split order) to the
+    product within the f64 bound, each slice is the product over its own K
+    range, and the library's own split choice for few rows is > 1 where the
+    k-tiles divide."""
+    from tilefoundry_amd._lib import C
+
+    g = torch.Generator().manual_seed(M * ks + N)
+    a = torch.randn(M, K, generator=g).to(BF)
+    b = (0.05 * torch.randn(N, K, generator=g)).to(BF)
+    part = torch.full((ks, M, N), float("nan"), device=dev)
+    C.gemm_nt_f32(a.to(dev), b.to(dev), part)
+    got = part.cpu().double()
+    kr = K // ks
+    for z in range(ks):
+        ref = a[:, z * kr:(z + 1) * kr].double() @ b[:, z * kr:(z + 1) * kr].double().t()
+        bound = kr * 2.0 ** -23 * (a[:, z * kr:(z + 1) * kr].double().abs() @ b[:, z * kr:(z + 1) * kr].double().abs().t())
+        assert bool(((got[z] - ref).abs() <= bound + 1e-6).all()), f"slice {z}"
+    if M < 128 and (K // 64) % 8 == 0:   # few rows, and the k-tiles allow splits
+        assert C.gemm_f32_splits(M, N, K) > 1

@@ -101,7 +101,7 @@ def build(verbose: bool = True) -> None:
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         objs = list(pool.map(_compile_hip, sources))
     _run([HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", *map(str, objs), "-o", str(LIB),
-          f"-L{ROCM / 'lib'}", "-lhipblaslt", f"-Wl,-rpath,{ROCM / 'lib'}"])
+          f"-L{ROCM / 'lib'}", f"-Wl,-rpath,{ROCM / 'lib'}"])
     _build_ext()
     if verbose:
         print(f"built {LIB.name} ({len(objs)} objects) and {EXT.name}", file=sys.stderr)

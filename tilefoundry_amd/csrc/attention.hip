@@ -471,14 +471,15 @@ __global__ __launch_bounds__(kThreads) void qk_rope_cache_kernel(
   dst[lane + 64] = static_cast<uint16_t>(f2bf(o1));
 }
 
-// prefill_qk_rope: the prompt rows of a q|k|v projection, f32 [rows, ldq]
-// with rows = batch * n (sequence b's row r at b * n + r, position pos0 + r).
+// prefill_qk_rope: the prompt rows of a q|k|v projection, the sum of ks f32
+// split-K partials [ks, rows, ldq] with rows = batch * n (sequence b's row r
+// at b * n + r, position pos0 + r).
 // One wave per (row, head), the decode step's per-head arithmetic: land in
 // bf16, query heads get the per-head norm and RoPE and go to q_out[row],
 // the key head the same with gamma_k into cache row pos0 + r of sequence b,
 // the value head straight into the value cache.
 __global__ __launch_bounds__(kThreads) void prefill_qk_rope_kernel(
-    const float* __restrict__ part, int64_t ldq, const uint16_t* __restrict__ gq,
+    const float* __restrict__ part, int ks, int64_t ldq, const uint16_t* __restrict__ gq,
     const uint16_t* __restrict__ gk, float eps, const uint16_t* __restrict__ cos_t,
     const uint16_t* __restrict__ sin_t, int n, int pos0, uint16_t* kc, uint16_t* vc, int64_t cap,
     uint16_t* q_out, int hq, int hkv, int64_t rows) {
@@ -491,7 +492,8 @@ __global__ __launch_bounds__(kThreads) void prefill_qk_rope_kernel(
   const int64_t b = m / n;
   const int p = pos0 + static_cast<int>(m % n);
   float x0, x1;
-  head_raw(nullptr, part + m * ldq + static_cast<int64_t>(hh) * D, 1, 0, lane, x0, x1);
+  head_raw(nullptr, part + m * ldq + static_cast<int64_t>(hh) * D, ks, static_cast<size_t>(rows * ldq), lane, x0,
+           x1);
   const int64_t KN = static_cast<int64_t>(hkv) * D;
   const int64_t crow = (b * cap + p) * KN;
   if (hh >= hq + hkv) {
@@ -611,12 +613,14 @@ int tfa_qk_rope_cache(const float* qkv_part, int64_t part_ks, const void* gamma_
   return launched("qk_rope_cache");
 }
 
-int tfa_prefill_qk_rope(const float* qkv, int64_t ldq, const void* gamma_q, const void* gamma_k, float eps_head,
-                        const void* cos_t, const void* sin_t, int64_t rope_rows, int64_t batch, int64_t n,
-                        int64_t pos0, void* k_cache, void* v_cache, int64_t cap, void* q_out, int64_t hq,
+int tfa_prefill_qk_rope(const float* qkv, int64_t ks, int64_t ldq, const void* gamma_q, const void* gamma_k,
+                        float eps_head, const void* cos_t, const void* sin_t, int64_t rope_rows, int64_t batch,
+                        int64_t n, int64_t pos0, void* k_cache, void* v_cache, int64_t cap, void* q_out, int64_t hq,
                         int64_t hkv, int64_t head_dim, hipStream_t stream) {
   if (!qkv || !gamma_q || !gamma_k || !cos_t || !sin_t || !k_cache || !v_cache || !q_out)
     return fail(TFA_ERR_NULL, "tfa_prefill_qk_rope: null pointer argument");
+  if (ks < 1 || ks > kMaxSplitsK)
+    return fail(TFA_ERR_SHAPE, "tfa_prefill_qk_rope: ks %lld not in [1, %d]", (long long)ks, kMaxSplitsK);
   if (head_dim != D) return fail(TFA_ERR_SHAPE, "tfa_prefill_qk_rope: head_dim %lld, only 128 supported", (long long)head_dim);
   if (hq <= 0 || hkv <= 0 || hq % hkv != 0)
     return fail(TFA_ERR_SHAPE, "tfa_prefill_qk_rope: hq %lld not a multiple of hkv %lld", (long long)hq, (long long)hkv);
@@ -636,7 +640,7 @@ int tfa_prefill_qk_rope(const float* qkv, int64_t ldq, const void* gamma_q, cons
   if ((waves + kWaves - 1) / kWaves > INT32_MAX)
     return fail(TFA_ERR_SHAPE, "tfa_prefill_qk_rope: %lld rows too many", (long long)rows);
   prefill_qk_rope_kernel<<<(unsigned)((waves + kWaves - 1) / kWaves), kThreads, 0, stream>>>(
-      qkv, ldq, static_cast<const uint16_t*>(gamma_q), static_cast<const uint16_t*>(gamma_k), eps_head,
+      qkv, (int)ks, ldq, static_cast<const uint16_t*>(gamma_q), static_cast<const uint16_t*>(gamma_k), eps_head,
       static_cast<const uint16_t*>(cos_t), static_cast<const uint16_t*>(sin_t), (int)n, (int)pos0,
       static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), cap, static_cast<uint16_t*>(q_out),
       (int)hq, (int)hkv, rows);

@@ -440,7 +440,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float* __restr
 // thread: act[r, i] = bf16(bf16(silu(bf16 g)) * bf16 u), the arithmetic of the
 // decode step's fused epilogue. examples/qwen3_1_7b-tilelang/fast/kernels.py:210-257
 // (gemv_silu's prologue) and :547-572 (silu_mul).
-__global__ __launch_bounds__(kThreads) void swiglu_pairs_kernel(const float* __restrict__ gu, int64_t ld,
+__global__ __launch_bounds__(kThreads) void swiglu_pairs_kernel(const float* __restrict__ gu, int ks, int64_t ld,
                                                                 int64_t rows, int inter,
                                                                 uint16_t* __restrict__ act) {
   const int per_row = inter / 4;
@@ -448,9 +448,9 @@ __global__ __launch_bounds__(kThreads) void swiglu_pairs_kernel(const float* __r
   if (e >= rows * per_row) return;
   const int64_t r = e / per_row;
   const int i0 = static_cast<int>(e % per_row) * 4;
-  const float4* src = reinterpret_cast<const float4*>(gu + r * ld + 2 * i0);
-  const float4 a = src[0], b = src[1];
-  const float g[4] = {a.x, a.z, b.x, b.z}, u[4] = {a.y, a.w, b.y, b.w};
+  float s[8];
+  sum_splits8(gu + r * ld + 2 * i0, static_cast<size_t>(rows * ld), ks, s);   // split-K partials in split order
+  const float g[4] = {s[0], s[2], s[4], s[6]}, u[4] = {s[1], s[3], s[5], s[7]};
   float y[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -734,8 +734,10 @@ int tfa_silu_mul(const float* part, int64_t ks, int64_t inter, int64_t rows, voi
   return launched("silu_mul");
 }
 
-int tfa_swiglu_pairs(const float* gu, int64_t ld, int64_t rows, int64_t inter, void* act, hipStream_t stream) {
+int tfa_swiglu_pairs(const float* gu, int64_t ks, int64_t ld, int64_t rows, int64_t inter, void* act,
+                     hipStream_t stream) {
   if (!gu || !act) return fail(TFA_ERR_NULL, "tfa_swiglu_pairs: null pointer argument");
+  if (ks < 1 || ks > kMaxSplitsK) return fail(TFA_ERR_SHAPE, "tfa_swiglu_pairs: ks %lld not in [1, %d]", (long long)ks, kMaxSplitsK);
   if (inter < 4 || inter % 4 || rows < 1 || ld < 2 * inter || ld % 4)
     return fail(TFA_ERR_SHAPE, "tfa_swiglu_pairs: inter %lld must be a positive multiple of 4, ld >= 2 inter "
                 "and a multiple of 4", (long long)inter);
@@ -744,7 +746,7 @@ int tfa_swiglu_pairs(const float* gu, int64_t ld, int64_t rows, int64_t inter, v
   const int64_t threads = rows * (inter / 4);
   if ((threads + kThreads - 1) / kThreads > INT32_MAX) return fail(TFA_ERR_SHAPE, "tfa_swiglu_pairs: too many rows");
   swiglu_pairs_kernel<<<(unsigned)((threads + kThreads - 1) / kThreads), kThreads, 0, stream>>>(
-      gu, ld, rows, (int)inter, static_cast<uint16_t*>(act));
+      gu, (int)ks, ld, rows, (int)inter, static_cast<uint16_t*>(act));
   return launched("swiglu_pairs");
 }
 

@@ -605,7 +605,8 @@ void qkv_norm_rope(const Tensor& hn, const Tensor& w_qkv, const Tensor& out, int
 }
 
 // ------------------------------------------- prompt prefill (decode model)
-// a [m, k], b [n, k] bf16 (row strides from the tensors); c [m, n] f32
+// a [m, k], b [n, k] bf16 (row strides from the tensors); c [m, n] f32, or
+// [ks, m, n] f32 split-K partials (K split into ks ranges)
 void gemm_nt_f32(const Tensor& a, const Tensor& b, const Tensor& c) {
   auto mat = [](const Tensor& t, const char* name, at::ScalarType dt) {
     if (!t.defined() || !t.is_cuda() || t.scalar_type() != dt || t.dim() != 2 || t.stride(1) != 1)
@@ -613,30 +614,36 @@ void gemm_nt_f32(const Tensor& a, const Tensor& b, const Tensor& c) {
   };
   mat(a, "a", BF);
   mat(b, "b", BF);
-  mat(c, "c", F32);
   const int64_t M = a.size(0), K = a.size(1), N = b.size(0);
-  if (b.size(1) != K || c.size(0) != M || c.size(1) != N) bad("gemm_nt_f32: shapes disagree");
-  raise_status(tfa_gemm_nt_f32(a.data_ptr(), b.data_ptr(), c.data_ptr<float>(), M, N, K, a.stride(0), b.stride(0),
-                               c.stride(0), stream_of(c)));
+  if (b.size(1) != K) bad("gemm_nt_f32: shapes disagree");
+  if (!c.defined() || !c.is_cuda() || c.scalar_type() != F32 || !c.is_contiguous() || (c.dim() != 2 && c.dim() != 3))
+    bad("c: expected a contiguous f32 GPU tensor (m, n) or (ks, m, n)");
+  const int64_t ks = c.dim() == 3 ? c.size(0) : 1;
+  if (c.size(-2) != M || c.size(-1) != N) bad("gemm_nt_f32: shapes disagree");
+  raise_status(tfa_gemm_nt_f32_split(a.data_ptr(), b.data_ptr(), c.data_ptr<float>(), M, N, K, a.stride(0),
+                                     b.stride(0), N, ks, stream_of(c)));
 }
 
-// gu f32 (rows, 2 * inter) with interleaved gate / up columns; act bf16 (rows, inter)
+// gu f32 (rows, 2 * inter) or split-K partials (ks, rows, 2 * inter) with
+// interleaved gate / up columns; act bf16 (rows, inter)
 void swiglu_pairs(const Tensor& gu, const Tensor& act) {
-  if (!gu.defined() || !gu.is_cuda() || gu.scalar_type() != F32 || gu.dim() != 2 || gu.stride(1) != 1)
-    bad("gu: expected an f32 (rows, 2 * inter) GPU matrix with unit inner stride");
-  const int64_t R = gu.size(0), I = gu.size(1) / 2;
+  if (!gu.defined() || !gu.is_cuda() || gu.scalar_type() != F32 || !gu.is_contiguous() || (gu.dim() != 2 && gu.dim() != 3))
+    bad("gu: expected a contiguous f32 (rows, 2 * inter) or (ks, rows, 2 * inter) GPU tensor");
+  const int64_t ks = gu.dim() == 3 ? gu.size(0) : 1;
+  const int64_t R = gu.size(-2), I = gu.size(-1) / 2;
   need(act, "act", BF, R * I);
-  if (gu.size(1) != 2 * I) bad("gu: odd column count");
-  raise_status(tfa_swiglu_pairs(gu.data_ptr<float>(), gu.stride(0), R, I, act.data_ptr(), stream_of(gu)));
+  if (gu.size(-1) != 2 * I) bad("gu: odd column count");
+  raise_status(tfa_swiglu_pairs(gu.data_ptr<float>(), ks, 2 * I, R, I, act.data_ptr(), stream_of(gu)));
 }
 
-// qkv f32 (batch * n, ldq); caches (batch, cap, hkv * 128) or (cap, hkv * 128);
-// q_out bf16 (batch * n, hq * 128).
+// qkv f32 (batch * n, ldq) or split-K partials (ks, batch * n, ldq); caches
+// (batch, cap, hkv * 128) or (cap, hkv * 128); q_out bf16 (batch * n, hq * 128).
 void prefill_qk_rope(const Tensor& qkv, const Tensor& gamma_q, const Tensor& gamma_k, double eps, const Tensor& cos,
                      const Tensor& sin, int64_t batch, int64_t n, int64_t pos0, const Tensor& k_cache,
                      const Tensor& v_cache, const Tensor& q_out, int64_t hq, int64_t hkv) {
   need(qkv, "qkv", F32);
-  if (qkv.dim() != 2 || qkv.size(0) != batch * n) bad("qkv: expected (batch * n, columns)");
+  if ((qkv.dim() != 2 && qkv.dim() != 3) || qkv.size(-2) != batch * n) bad("qkv: expected ([ks,] batch * n, columns)");
+  const int64_t ks = qkv.dim() == 3 ? qkv.size(0) : 1;
   need(gamma_q, "gamma_q", BF, 128);
   need(gamma_k, "gamma_k", BF, 128);
   need(cos, "cos", BF);
@@ -648,7 +655,7 @@ void prefill_qk_rope(const Tensor& qkv, const Tensor& gamma_q, const Tensor& gam
   if (batch < 1 || KN < 1 || k_cache.size(-1) != KN || k_cache.numel() % (batch * KN) != 0)
     bad("k_cache / v_cache: expected (batch, cap, kv_heads * 128)");
   need(q_out, "q_out", BF, batch * n * hq * 128);
-  raise_status(tfa_prefill_qk_rope(qkv.data_ptr<float>(), qkv.size(1), gamma_q.data_ptr(), gamma_k.data_ptr(),
+  raise_status(tfa_prefill_qk_rope(qkv.data_ptr<float>(), ks, qkv.size(-1), gamma_q.data_ptr(), gamma_k.data_ptr(),
                                    (float)eps, cos.data_ptr(), sin.data_ptr(), cos.size(0), batch, n, pos0,
                                    k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() / (batch * KN),
                                    q_out.data_ptr(), hq, hkv, 128, stream_of(qkv)));
@@ -838,6 +845,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gemm_nt", &gemm_nt);
   m.def("qkv_norm_rope", &qkv_norm_rope);
   m.def("gemm_nt_f32", &gemm_nt_f32);
+  m.def("gemm_f32_splits", [](int64_t m, int64_t n, int64_t k) { return tfa_gemm_f32_splits(m, n, k); });
   m.def("swiglu_pairs", &swiglu_pairs);
   m.def("prefill_qk_rope", &prefill_qk_rope);
   m.def("causal_attention", &causal_attention);

@@ -167,7 +167,8 @@ def prefill_caches(cfg: Qwen3Config, embed, layers, kc, vc, cos, sin, ids: torch
     ``[cap, .]`` for B = 1). Afterwards cache rows 0..n-1 hold what n decode
     steps over the same tokens would have written, computed with the same
     rounding points: every projection is an f32 GEMM over all B*n rows
-    (``gemm_nt_f32``) whose consumer lands it in bf16 as the decode step lands
+    (``gemm_nt_f32``, its K split into partial slices when few rows would leave
+    most CUs idle) whose consumer lands it in bf16 as the decode step lands
     its split-K partials -- ``prefill_qk_rope`` (per-head norm + RoPE + cache
     write), ``rows_norm`` (residual add + norm), ``swiglu_pairs`` -- and the
     attention of every row is one causal launch over the cache
@@ -189,13 +190,18 @@ def prefill_caches(cfg: Qwen3Config, embed, layers, kc, vc, cos, sin, ids: torch
         return torch.empty(*shape, device=dev, dtype=dtype)
 
     h, h1, xn = e(R, H), e(R, H), e(R, H)
-    qkv = e(R, cfg.qkv_rows, dtype=f32)
+    # each projection's f32 result as split-K partials [ks, R, out] when few
+    # rows leave the GEMM's grid too small to fill the CUs; the consumers sum
+    # the partials in split order, as the decode step sums its own
+    ks = {name: C.gemm_f32_splits(R, nout, nin) for name, nout, nin in (
+        ("qkv", cfg.qkv_rows, H), ("o", H, HQ * D), ("gu", 2 * I, H), ("down", H, I))}
+    qkv = e(ks["qkv"], R, cfg.qkv_rows, dtype=f32)
     q = e(R, HQ * D)
     attn = e(R, HQ * D)
-    o = e(R, H, dtype=f32)
-    gu = e(R, 2 * I, dtype=f32)
+    o = e(ks["o"], R, H, dtype=f32)
+    gu = e(ks["gu"], R, 2 * I, dtype=f32)
     act = e(R, I)
-    d = e(R, H, dtype=f32)
+    d = e(ks["down"], R, H, dtype=f32)
     C.rows_norm(embed, ids.reshape(-1), None, None, h, layers[0]["gamma_in"], xn, cfg.eps, err)
     for i, w in enumerate(layers):
         k4 = kc[i].view(B, -1, HKV, D)
