@@ -683,10 +683,34 @@ def main() -> int:
                     help="skip the bs=32, MLA and prefill measurements")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only launch the dominant kernel loop (for rocprofv3 counter runs)")
-    ap.add_argument("--only", choices=("bs32", "mla", "prefill", "prompt", "minicpm3", "cpu"),
+    ap.add_argument("--only", choices=("bs32", "mla", "prefill", "prompt", "minicpm3", "cpu", "kernels"),
                     help="run one of the secondary configurations alone and print its line "
                          "(for rocprofv3 kernel traces of that workload)")
     return run(ap.parse_args())
+
+
+def kernels_only(args) -> int:
+    """The per-kernel workloads alone (for rocprofv3 counter passes): fused
+    add+RMSNorm, the decode GEMVs and head, one decode layer's attention over
+    rotating 4096-slot caches, the MLA core over rotating caches, then a plain
+    copy of 64 MiB (the calibration dispatch for FETCH_SIZE / WRITE_SIZE)."""
+    from tilefoundry_amd._lib import C
+    from tilefoundry_amd.qwen3 import Engine, QWEN3_1_7B
+
+    dev = torch.device("cuda:0")
+    eng = Engine(QWEN3_1_7B, device=dev, max_new=16, prompt_room=16, seed=args.seed, capture=False)
+    out = {"kernels": kernel_lines(eng), "decode_layer_bs1_ctx4096": decode_layer_ctx4096(eng)}
+    del eng
+    torch.cuda.empty_cache()
+    out["mla_decode_b8_ctx8192"] = mla_decode()
+    src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        C.copy_stream(src, dst)
+    torch.cuda.synchronize()
+    out["copy_bytes"] = src.numel()
+    print(json.dumps(out))
+    return 0
 
 
 def parse(argv: list[str]):
@@ -714,6 +738,8 @@ def run(args) -> int:
         return 2
 
     cfg_prompt = torch.randint(0, 151936, (PROMPT,), generator=torch.Generator().manual_seed(args.seed)).tolist()
+    if args.only == "kernels":
+        return kernels_only(args)
     if args.only:
         fn = {"bs32": lambda: batch32(args.seed, NEW_TOKENS, args), "mla": mla_decode,
               "prefill": prefill_layer, "prompt": lambda: prompt_only(args.seed, args),

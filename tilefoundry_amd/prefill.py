@@ -6,18 +6,18 @@ signatures, on the gfx950 prefill kernels.
 kernels/attention.py:313-438):
 
 * ``qkv`` -- one MFMA GEMM of the normed hidden state against ``[W_q; W_k; W_v]``
-  (the q projection holds ``[q | gate]`` per head) into one packed buffer, then
-  an in-place pass: per-head RMSNorm with ``(1 + gamma)`` in f32 landing once,
-  rotate-half RoPE on the leading ``rot`` dims with each product and the sum in
-  bf16. ``q``, ``gate``, ``k``, ``v`` come back as strided views of that buffer
-  (nothing is copied out).
+  (the q projection holds ``[q | gate]`` per head) into one packed buffer, with
+  the head norm and RoPE in its epilogue: per-head RMSNorm with ``(1 + gamma)``
+  in f32 landing once, rotate-half RoPE on the leading ``rot`` dims with each
+  product and the sum in bf16. ``q``, ``gate``, ``k``, ``v`` come back as
+  strided views of that buffer (nothing is copied out).
 * ``attention`` -- causal GQA flash attention (f32 scores scaled after the dot,
   online f32 softmax, bf16 weights into P.V) with the output gate
   ``bf16(o) * bf16(sigmoid(gate))``.
 * ``o_proj`` -- ``bf16(hidden + bf16(gated @ W_o^T))`` as the GEMM's epilogue.
 
 Weights are ``(out, in)`` (``b_layout="NK"`` in the reference). Token counts are
-multiples of 256 (the GEMM tile); activations are ``[1, N, .]`` bf16.
+multiples of 128 (the attention's row block); activations are ``[1, N, .]`` bf16.
 """
 from __future__ import annotations
 
@@ -78,8 +78,8 @@ class Attention:
         HQ, HKV, D = cfg.heads, cfg.kv_heads, cfg.head_dim
         x = hn.reshape(-1, cfg.hidden)
         N = x.shape[0]
-        if N % 256:
-            raise ValueError(f"N={N} tokens: the prefill GEMM takes multiples of 256")
+        if N % 128:
+            raise ValueError(f"N={N} tokens: the prefill attention takes multiples of 128")
         if cos.shape != (N, cfg.rot) or sin.shape != (N, cfg.rot):
             raise ValueError(f"cos / sin: expected ({N}, {cfg.rot})")
         width = HQ * 2 * D + 2 * HKV * D
