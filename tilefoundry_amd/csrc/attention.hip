@@ -98,8 +98,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
   const int wid = threadIdx.x / kWave;
   const int slot = lane >> 4;
   const int dc = lane & 15;
-  const int s = blockIdx.x;
-  const int kvh = blockIdx.y;
+  // kv head fastest: the blocks of one split are dispatched together and read
+  // the same cache rows (each position's row holds every kv head) close in time
+  const int kvh = blockIdx.x;
+  const int s = blockIdx.y;
   const int b = blockIdx.z;
   const int t = threadIdx.x;
   const int KN = a.hkv * D;
@@ -110,6 +112,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
   float* lp = a.lp + static_cast<size_t>(b) * a.ns * a.hq;
 
   int last = a.wr[b];
+  const int p_raw = a.gq != nullptr ? a.pos[b] : 0;   // issued beside wr: one round trip for both
   if (last < 0 || last >= a.cap) {
     if (s == 0 && kvh == 0 && t == 0) set_err(a.err, 4);
     last = last < 0 ? -1 : a.cap - 1;
@@ -134,7 +137,45 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
   const bool has_new = fused && last < start + SS;  // this split holds the newest slot
   const bool new_v = has_new && a.part != nullptr;  // ... and also brings the new value row
 
-  // 1. every K / V load of the split, first
+  // 1. the query's raw head values and its rope row (and, in the one block that
+  //    holds the newest slot, the new key / value) first: a few hundred bytes from
+  //    L2 that would otherwise complete only after the split's K / V (vector
+  //    loads complete in issue order), holding the prologue back by a whole
+  //    K / V round trip
+  const int nwork = fused ? G + (has_new ? 1 : 0) + (new_v ? 1 : 0) : 0;
+  constexpr int kItems = (G + 2 + kWaves - 1) / kWaves;   // prologue items per wave: hh = wid + kWaves j
+  float x0[kItems], x1[kItems];
+  float c0 = 0.f, s0 = 0.f, c1 = 0.f, s1 = 0.f;
+  if (fused) {
+    int p = p_raw;
+    if (p < 0 || p >= a.mp_rows) {
+      if (s == 0 && kvh == 0 && t == 0) set_err(a.err, 5);
+      p = 0;
+    }
+    const int rows = (a.hq + 2 * a.hkv) * D;   // q | k | v row width of the partials
+    const uint16_t* qsrc = a.q ? a.q + b * a.q_bstride : nullptr;
+    const float* psrc = a.part ? a.part + static_cast<size_t>(b) * rows : nullptr;
+    const size_t kstride = static_cast<size_t>(rows) * gridDim.z;  // partials are [ks, B, rows]
+#pragma unroll
+    for (int j = 0; j < kItems; ++j) {
+      const int hh = wid + kWaves * j;
+      x0[j] = x1[j] = 0.f;
+      if (hh < nwork) {
+        const int off = hh < G ? (kvh * G + hh) * D : hh == G ? (a.hq + kvh) * D : (a.hq + a.hkv + kvh) * D;
+        head_raw(hh <= G && qsrc ? qsrc + off : nullptr, psrc ? psrc + off : nullptr, a.part_ks, kstride, lane,
+                 x0[j], x1[j]);
+      }
+    }
+    c0 = bf2f(a.cos_t[static_cast<size_t>(p) * D + lane]);
+    s0 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane]);
+    c1 = bf2f(a.cos_t[static_cast<size_t>(p) * D + lane + 64]);
+    s1 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane + 64]);
+  } else {
+    for (int e = t; e < G * D; e += kThreads)
+      qs[e / D][e % D] = bf2f(a.q[b * a.q_bstride + (kvh * G) * D + e]);
+  }
+
+  // 2. every K / V load of the split
   uint4 kv[NIT], vv[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
@@ -145,52 +186,30 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
     vv[it] = valid ? ld16_stream(vc + off) : make_uint4(0, 0, 0, 0);
   }
 
-  // 2. the query (and, in one block, the new key) while they are in flight
-  if (fused) {
-    int p = a.pos[b];
-    if (p < 0 || p >= a.mp_rows) {
-      if (s == 0 && kvh == 0 && t == 0) set_err(a.err, 5);
-      p = 0;
+  // the prologue's arithmetic while the K / V loads are in flight
+#pragma unroll
+  for (int j = 0; j < kItems; ++j) {
+    const int hh = wid + kWaves * j;
+    if (!fused || hh >= nwork) continue;
+    float o0, o1;
+    if (hh < G) {
+      norm_rope_head(x0[j], x1[j], a.gq, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
+      qs[hh][lane] = o0;
+      qs[hh][lane + 64] = o1;
+    } else if (hh == G) {
+      norm_rope_head(x0[j], x1[j], a.gk, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
+      knew[lane] = o0;
+      knew[lane + 64] = o1;
+      uint16_t* dst = kc + static_cast<size_t>(last) * KN + kvh * D;
+      dst[lane] = static_cast<uint16_t>(f2bf(o0));
+      dst[lane + 64] = static_cast<uint16_t>(f2bf(o1));
+    } else {
+      vnew[lane] = x0[j];
+      vnew[lane + 64] = x1[j];
+      uint16_t* dst = vc + static_cast<size_t>(last) * KN + kvh * D;
+      dst[lane] = static_cast<uint16_t>(f2bf(x0[j]));
+      dst[lane + 64] = static_cast<uint16_t>(f2bf(x1[j]));
     }
-    const float c0 = bf2f(a.cos_t[static_cast<size_t>(p) * D + lane]);
-    const float s0 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane]);
-    const float c1 = bf2f(a.cos_t[static_cast<size_t>(p) * D + lane + 64]);
-    const float s1 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane + 64]);
-    const int rows = (a.hq + 2 * a.hkv) * D;   // q | k | v row width of the partials
-    const uint16_t* qsrc = a.q ? a.q + b * a.q_bstride : nullptr;
-    const float* psrc = a.part ? a.part + static_cast<size_t>(b) * rows : nullptr;
-    const size_t kstride = static_cast<size_t>(rows) * gridDim.z;  // partials are [ks, B, rows]
-    const int nwork = G + (has_new ? 1 : 0) + (new_v ? 1 : 0);
-    for (int hh = wid; hh < nwork; hh += kWaves) {
-      float x0, x1, o0, o1;
-      if (hh < G) {
-        const int off = (kvh * G + hh) * D;
-        head_raw(qsrc ? qsrc + off : nullptr, psrc ? psrc + off : nullptr, a.part_ks, kstride, lane, x0, x1);
-        norm_rope_head(x0, x1, a.gq, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
-        qs[hh][lane] = o0;
-        qs[hh][lane + 64] = o1;
-      } else if (hh == G) {
-        const int off = (a.hq + kvh) * D;
-        head_raw(qsrc ? qsrc + off : nullptr, psrc ? psrc + off : nullptr, a.part_ks, kstride, lane, x0, x1);
-        norm_rope_head(x0, x1, a.gk, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
-        knew[lane] = o0;
-        knew[lane + 64] = o1;
-        uint16_t* dst = kc + static_cast<size_t>(last) * KN + kvh * D;
-        dst[lane] = static_cast<uint16_t>(f2bf(o0));
-        dst[lane + 64] = static_cast<uint16_t>(f2bf(o1));
-      } else {
-        const int off = (a.hq + a.hkv + kvh) * D;
-        head_raw(nullptr, psrc + off, a.part_ks, kstride, lane, x0, x1);
-        vnew[lane] = x0;
-        vnew[lane + 64] = x1;
-        uint16_t* dst = vc + static_cast<size_t>(last) * KN + kvh * D;
-        dst[lane] = static_cast<uint16_t>(f2bf(x0));
-        dst[lane + 64] = static_cast<uint16_t>(f2bf(x1));
-      }
-    }
-  } else {
-    for (int e = t; e < G * D; e += kThreads)
-      qs[e / D][e % D] = bf2f(a.q[b * a.q_bstride + (kvh * G) * D + e]);
   }
   lds_barrier();
 
@@ -304,7 +323,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
 
 template <int G>
 int launch_attn_g(const AttnArgs& a, int ss, int batch, hipStream_t st) {
-  const dim3 grid(a.ns, a.hkv, batch);
+  const dim3 grid(a.hkv, a.ns, batch);
   switch (ss) {
     case 32: attn_decode_kernel<G, 2><<<grid, kThreads, 0, st>>>(a); break;
     case 64: attn_decode_kernel<G, 4><<<grid, kThreads, 0, st>>>(a); break;
@@ -409,6 +428,77 @@ __global__ __launch_bounds__(kCombThreads) void attn_combine_kernel(
 #pragma unroll
     for (int g = 0; g < kCombGroups; ++g) num += s_red[g][t];
     out[h * Dh + t] = static_cast<uint16_t>(f2bf(num / den));
+  }
+}
+
+// The merge for head_dim 128 and up to 128 splits, spread wider: block (head,
+// 32-dim slice), 256 threads = 8 groups of 32 lanes, group g owning splits g,
+// g + 8, ... and lane d one output dim. Every load a thread needs -- its splits'
+// statistics and partial outputs, active or not (rows past wr are allocated,
+// possibly stale, and never used) -- is issued at once, next to wr, so the whole
+// merge is one memory round trip; the block max and the group sums meet in LDS
+// in group order.
+constexpr int kFastSlices = 4;                     // 32-dim slices of a 128-dim head
+constexpr int kFastGroups = 8;
+constexpr int kFastPer = 16;                       // splits per group
+constexpr int kFastMaxSplits = kFastGroups * kFastPer;
+
+__global__ __launch_bounds__(256) void attn_combine_d128_kernel(const float* op, const float* mp, const float* lp,
+                                                                uint16_t* out, int ns, int hq, const int* wr,
+                                                                int split) {
+  const int h = blockIdx.x / kFastSlices, c = blockIdx.x % kFastSlices;
+  const int bb = blockIdx.y;
+  const int t = threadIdx.x, g = t / 32, d = 32 * c + (t & 31);
+  op += static_cast<size_t>(bb) * ns * hq * D;
+  mp += static_cast<size_t>(bb) * ns * hq;
+  lp += static_cast<size_t>(bb) * ns * hq;
+  __shared__ float s_m[kFastGroups];
+  __shared__ float s_den[kFastGroups];
+  __shared__ float s_num[kFastGroups][32];
+  const int w = wr ? wr[bb] : 0;
+  float m[kFastPer], l[kFastPer], o[kFastPer];
+#pragma unroll
+  for (int u = 0; u < kFastPer; ++u) {
+    const int j = g + kFastGroups * u;
+    const bool in = j < ns;
+    m[u] = in ? mp[j * hq + h] : -INFINITY;
+    l[u] = in ? lp[j * hq + h] : 0.f;
+    o[u] = in ? op[(static_cast<size_t>(j) * hq + h) * D + d] : 0.f;
+  }
+  int nact = ns;
+  if (wr) {
+    nact = w < 0 ? 0 : w / split + 1;
+    if (nact > ns) nact = ns;
+  }
+  float gm = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < kFastPer; ++u)
+    if (g + kFastGroups * u < nact) gm = fmaxf(gm, m[u]);
+  if ((t & 31) == 0) s_m[g] = gm;
+  lds_barrier();
+  float M = s_m[0];
+#pragma unroll
+  for (int k = 1; k < kFastGroups; ++k) M = fmaxf(M, s_m[k]);
+  float num = 0.f, den = 0.f;
+#pragma unroll
+  for (int u = 0; u < kFastPer; ++u) {
+    if (g + kFastGroups * u < nact) {
+      const float e = expf(m[u] - M);
+      num = fmaf(o[u], e, num);
+      den = fmaf(l[u], e, den);
+    }
+  }
+  s_num[g][t & 31] = num;
+  if ((t & 31) == 0) s_den[g] = den;
+  lds_barrier();
+  if (g == 0) {
+    float tn = 0.f, td = 0.f;
+#pragma unroll
+    for (int k = 0; k < kFastGroups; ++k) {
+      tn += s_num[k][t & 31];
+      td += s_den[k];
+    }
+    out[static_cast<size_t>(bb) * hq * D + h * D + d] = static_cast<uint16_t>(f2bf(tn / td));
   }
 }
 
@@ -563,6 +653,8 @@ int tfa_decode_attention(const void* q, const float* qkv_part, int64_t part_ks,
   a.hq = (int)hq;
   a.hkv = (int)hkv;
   a.cap = (int)cap;
+  if (cap / split > 65535)
+    return fail(TFA_ERR_SHAPE, "tfa_decode_attention: %lld splits exceed 65535", (long long)(cap / split));
   a.ns = (int)(cap / split);
   a.scale = scale;
   const int B = (int)batch;
@@ -583,6 +675,11 @@ int tfa_attn_combine(const float* op, const float* mp, const float* lp, void* ou
   if (wr && split <= 0) return fail(TFA_ERR_SHAPE, "tfa_attn_combine: split must be positive with wr");
   if (head_dim > kCombMaxD) return fail(TFA_ERR_SHAPE, "tfa_attn_combine: head_dim %lld exceeds %d", (long long)head_dim, kCombMaxD);
   if (splits > kCombMaxSplits) return fail(TFA_ERR_SHAPE, "tfa_attn_combine: %lld splits exceed %d", (long long)splits, kCombMaxSplits);
+  if (head_dim == D && splits <= kFastMaxSplits) {
+    attn_combine_d128_kernel<<<dim3((unsigned)(hq * kFastSlices), (unsigned)batch), 256, 0, stream>>>(
+        op, mp, lp, static_cast<uint16_t*>(out), (int)splits, (int)hq, wr, (int)split);
+    return launched("attn_combine");
+  }
   const dim3 grid((unsigned)hq, (unsigned)batch);
   attn_combine_kernel<<<grid, kCombThreads, 0, stream>>>(op, mp, lp, static_cast<uint16_t*>(out),
                                                          (int)splits, (int)hq, (int)head_dim, wr,
