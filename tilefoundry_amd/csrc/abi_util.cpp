@@ -3,6 +3,8 @@
 
 #include <string.h>
 
+#include <mutex>
+
 namespace {
 thread_local char g_msg[512] = "";
 }
@@ -21,6 +23,19 @@ int launched(const char* kernel) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TFA_ERR_LAUNCH, "%s: %s", kernel, hipGetErrorString(e));
   return TFA_OK;
+}
+
+int device_cus() {
+  static std::mutex mu;
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[dev] == 0) {
+    int n = 0;
+    cache[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cache[dev];
 }
 
 }  // namespace tfa

@@ -18,6 +18,9 @@ int fail(int code, const char* fmt, ...);
 // "<kernel>: <hip error string>" and returns TFA_ERR_LAUNCH.
 int launched(const char* kernel);
 
+// Compute units of the current device, read once per device (256 if the query fails).
+int device_cus();
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 

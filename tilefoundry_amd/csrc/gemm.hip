@@ -43,8 +43,6 @@
 //
 // Reference (jingchangshi/TileFoundry): examples/qwen3_8_27b_prefill-tilelang/kernels/gemm.py:104-356
 // (gemm_kernel, "qk_norm_rope" epilogue :226-300, "residual" :193-198), model.py:271-303,326-333.
-#include <mutex>
-
 #include "abi_util.h"
 #include "common.h"
 
@@ -349,21 +347,6 @@ int launch_cfg(const GemmArgs& g, hipStream_t st, const char* name) {
   return launched(name);
 }
 
-// Compute units of the current device (the launch picks a tile that gives
-// each of them a block), read once per device.
-int num_cus() {
-  static std::mutex mu;
-  static int cache[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  std::lock_guard<std::mutex> lock(mu);
-  if (cache[dev] == 0) {
-    int n = 0;
-    cache[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
-  }
-  return cache[dev];
-}
-
 // Tile choice. A 256 x 256 tile moves the fewest LDS bytes per FLOP and, at a
 // full round of blocks, runs fastest (measured 1.10-1.15 PFLOP/s on the prefill
 // shapes); but blocks run in rounds of one per CU, so a grid whose last round is
@@ -381,7 +364,7 @@ bool full_rounds_256(int64_t m, int64_t n, int cus) {
 // is split along K -- doubling while the blocks still fit twice per CU, each
 // range keeps at least 4 k-tiles, and the count divides the k-tiles -- up to 8.
 int64_t splits_f32(int64_t m, int64_t n, int64_t k) {
-  const int cus = num_cus();
+  const int cus = device_cus();
   if (full_rounds_256(m, n, cus) || n % 128 || k % kBK) return 1;
   const int64_t blocks = (m + 127) / 128 * (n / 128), nk = k / kBK;
   int64_t ks = 1;
@@ -391,7 +374,7 @@ int64_t splits_f32(int64_t m, int64_t n, int64_t k) {
 
 template <int EPI>
 int launch(const GemmArgs& g, hipStream_t st, const char* name) {
-  const int cus = num_cus();
+  const int cus = device_cus();
   if (full_rounds_256(g.M, g.N, cus) && !(EPI == EPI_F32 && g.ksplit > 1)) return launch_cfg<C256, EPI>(g, st, name);
   if (EPI == EPI_QKNR) {
     if (g.N % 256) return fail(TFA_ERR_SHAPE, "%s: the qkv width must be a multiple of 256", name);
