@@ -29,6 +29,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int D = 128;
+constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
   const uint16_t* q;      // prepared q [hq*D]; fused mode: raw [q | k] [(hq+hkv)*D]
@@ -214,7 +215,9 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
   lds_barrier();
 
   // 3. scores (scale applied to the finished f32 dot), kept in registers: after
-  //    the 16-lane butterfly every lane of a position's group holds its score
+  //    the 16-lane DPP row sum every lane of a position's group holds its score.
+  //    Reductions across the wave's four position slots use the gfx950 row
+  //    swaps (no LDS round trip); the weights are exp2 of the scaled difference
   float qf[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -236,7 +239,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
       float d = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) d = fmaf(qf[g][i], kf[i], d);
-      d = group_sum<16>(d);
+      d = row16_sum(d);
       sv[g][it] = pi < n ? d * a.scale : -INFINITY;
     }
   }
@@ -249,8 +252,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
     float mx = sv[g][0];
 #pragma unroll
     for (int it = 1; it < NIT; ++it) mx = fmaxf(mx, sv[g][it]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    mx = rows4_max(mx);
     if (lane == 0) red[0][wid][g] = mx;
   }
   lds_barrier();
@@ -260,12 +262,11 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
     float ls = 0.f;
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
-      const float e = sv[g][it] == -INFINITY ? 0.f : expf(sv[g][it] - m[g]);
+      const float e = sv[g][it] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((sv[g][it] - m[g]) * kLog2e);
       ls += e;
       sv[g][it] = round_bf(e);  // bf16 weights into the value product
     }
-    ls += __shfl_xor(ls, 16, kWave);
-    ls += __shfl_xor(ls, 32, kWave);
+    ls = rows4_sum(ls);
     if (lane == 0) red[1][wid][g] = ls;
   }
 
@@ -294,10 +295,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float v = o[g][i];
-      v += __shfl_xor(v, 16, kWave);
-      v += __shfl_xor(v, 32, kWave);
-      o[g][i] = v;
+      o[g][i] = rows4_sum(o[g][i]);
     }
   if (slot == 0) {
 #pragma unroll

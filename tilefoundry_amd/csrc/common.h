@@ -96,6 +96,31 @@ TFA_DEV float row16_max(float v) {
   v = fmaxf(v, dpp_f32<0x140>(v));   // row_mirror
   return v;
 }
+// Sum over each 16-lane row the same way: quads first, then the half-row and
+// row mirrors; every lane of the row ends with the identical value.
+TFA_DEV float row16_sum(float v) {
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  v += dpp_f32<0x141>(v);
+  v += dpp_f32<0x140>(v);
+  return v;
+}
+
+// Max / sum over the four 16-lane rows (lanes l, l ^ 16, l ^ 32, l ^ 48) with
+// gfx950's row swaps: permlane32_swap pairs lane l with l ^ 32, then
+// permlane16_swap pairs l with l ^ 16 -- no LDS round trip.
+TFA_DEV float rows4_max(float v) {
+  auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
+  auto y = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(y[0]), __uint_as_float(y[1]));
+}
+TFA_DEV float rows4_sum(float v) {
+  auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+  auto y = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(y[0]) + __uint_as_float(y[1]);
+}
 
 // Multi-row wave reduction: v[0..R) are one lane's partial sums of R rows.
 // Instead of R full butterflies (6R shuffles) the rows are halved at each step

@@ -253,20 +253,6 @@ TFA_DEV uint2 ld_tr(const char* lds_byte) {
   return __builtin_bit_cast(uint2, v);
 }
 
-// max / sum over the four 16-lane rows (lanes l, l ^ 16, l ^ 32, l ^ 48)
-TFA_DEV float rows4_max(float v) {
-  auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
-  auto y = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(y[0]), __uint_as_float(y[1]));
-}
-TFA_DEV float rows4_sum(float v) {
-  auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(x[0]) + __uint_as_float(x[1]);
-  auto y = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(y[0]) + __uint_as_float(y[1]);
-}
-
 // Scores are computed transposed, S^T = [c | k_rope] . q^T (positions as MFMA
 // rows, heads as columns): the accumulator of lane (head n16, row group g)
 // then holds positions 4g + r of 16, which is exactly the K-slice lane
