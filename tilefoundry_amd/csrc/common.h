@@ -10,6 +10,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #define TFA_DEV __device__ __forceinline__
 
 namespace tfa {
@@ -70,17 +72,6 @@ TFA_DEV void st16_stream(void* p, uint4 v) {
 }
 
 // ---------------------------------------------------------------- reductions
-TFA_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
-}
-
-TFA_DEV float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
-  return v;
-}
 
 // Max over each 16-lane row of the wave (every lane gets its row's max) by DPP
 // lane permutations -- quad swaps, then the half-row and row mirrors -- with
@@ -122,12 +113,55 @@ TFA_DEV float rows4_sum(float v) {
   return __uint_as_float(y[0]) + __uint_as_float(y[1]);
 }
 
+// Sum / max over the lanes that differ from this one only in the low K bits of
+// the lane id (K <= 6), bottom up: quad swaps (bits 0, 1), the half-row and row
+// mirrors (bits 2, 3 -- once the smaller groups are uniform, a mirror partner
+// holds the other group's value), then the row swaps (bits 4, 5). No step goes
+// through LDS, and every lane of a group ends with the identical value.
+template <int K>
+TFA_DEV float lanes_sum(float v) {
+  if (K >= 1) v += dpp_f32<0xB1>(v);
+  if (K >= 2) v += dpp_f32<0x4E>(v);
+  if (K >= 3) v += dpp_f32<0x141>(v);
+  if (K >= 4) v += dpp_f32<0x140>(v);
+  if (K >= 5) {
+    auto y = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(y[0]) + __uint_as_float(y[1]);
+  }
+  if (K >= 6) {
+    auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+  }
+  return v;
+}
+template <int K>
+TFA_DEV float lanes_max(float v) {
+  if (K >= 1) v = fmaxf(v, dpp_f32<0xB1>(v));
+  if (K >= 2) v = fmaxf(v, dpp_f32<0x4E>(v));
+  if (K >= 3) v = fmaxf(v, dpp_f32<0x141>(v));
+  if (K >= 4) v = fmaxf(v, dpp_f32<0x140>(v));
+  if (K >= 5) {
+    auto y = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(y[0]), __uint_as_float(y[1]));
+  }
+  if (K >= 6) {
+    auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
+  }
+  return v;
+}
+TFA_DEV float wave_sum(float v) { return lanes_sum<6>(v); }
+TFA_DEV float wave_max(float v) { return lanes_max<6>(v); }
+
+constexpr int log2_const(int n) { return n <= 1 ? 0 : 1 + log2_const(n / 2); }
+
 // Multi-row wave reduction: v[0..R) are one lane's partial sums of R rows.
-// Instead of R full butterflies (6R shuffles) the rows are halved at each step
+// Instead of R full butterflies (6R exchanges) the rows are halved at each step
 // -- a lane keeps the half of the rows its mask bit selects and adds the
-// partner's partials for that half -- so R = 8 costs 4+2+1+3 = 10 shuffles and
-// R = 16 costs 17. On return every lane holds the wave total of one row,
-// `row = wave_rows_owner<R>(lane)`; each row's total is replicated on 64/R lanes.
+// partner's partials for that half -- so R = 8 costs 4+2+1+3 = 10 exchanges and
+// R = 16 costs 17, each a row swap or a DPP move (no LDS). On return every
+// lane holds the wave total of one row, `row = wave_rows_owner<R>(lane)`; each
+// row's total is replicated on 64/R lanes.
 template <int R>
 TFA_DEV int wave_rows_owner(int lane) {
   int row = 0;
@@ -138,25 +172,64 @@ TFA_DEV int wave_rows_owner(int lane) {
   return row;
 }
 
+// Partner value of lane ^ M (M a power of two): row swaps for 32 and 16 are
+// handled in RowHalver itself; within a 16-lane row it takes DPP moves (a row
+// rotate by 8 is lane ^ 8 in either direction; lane ^ 4 is the half-row
+// mirror, lane ^ 7, followed by the quad reversal, lane ^ 3).
+template <int M>
+TFA_DEV float xor_partner(float v, int) {
+  if constexpr (M == 8) return dpp_f32<0x128>(v);   // row_ror:8
+  if constexpr (M == 4) return dpp_f32<0x1B>(dpp_f32<0x141>(v));   // quad_perm [3, 2, 1, 0] of row_half_mirror
+  if constexpr (M == 2) return dpp_f32<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+  if constexpr (M == 1) return dpp_f32<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+  return v;
+}
+
+// Value of lane ^ M for any M (float or int bits): the row swaps for 32 and 16
+// (each lane keeps the half of the swapped pair that came from its partner),
+// DPP within a row.
+template <int M>
+TFA_DEV uint32_t xor_lane_bits(uint32_t v, int lane) {
+  if constexpr (M == 32) {
+    auto x = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane & 32) ? x[0] : x[1];
+  } else if constexpr (M == 16) {
+    auto x = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16) ? x[0] : x[1];
+  } else {
+    return __builtin_bit_cast(uint32_t, xor_partner<M>(__builtin_bit_cast(float, v), lane));
+  }
+}
+template <int M>
+TFA_DEV float xor_lane(float v, int lane) { return __uint_as_float(xor_lane_bits<M>(__float_as_uint(v), lane)); }
+template <int M>
+TFA_DEV int xor_lane(int v, int lane) { return static_cast<int>(xor_lane_bits<M>(static_cast<uint32_t>(v), lane)); }
+
 template <int N, int M>
 struct RowHalver {
   TFA_DEV static void run(float* v, int lane) {
-    const bool upper = (lane & M) != 0;
 #pragma unroll
     for (int j = 0; j < N / 2; ++j) {
-      const float keep = upper ? v[j + N / 2] : v[j];
-      const float send = upper ? v[j] : v[j + N / 2];
-      v[j] = keep + __shfl_xor(send, M, kWave);
+      if constexpr (M == 32 || M == 16) {
+        // lane l keeps row j (bit clear) or j + N/2 (bit set) and adds its
+        // partner's other half: a row swap returns exactly those two values
+        auto x = M == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j + N / 2]), false, false)
+                         : __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]), __float_as_uint(v[j + N / 2]), false, false);
+        v[j] = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+      } else {
+        const bool upper = (lane & M) != 0;
+        const float keep = upper ? v[j + N / 2] : v[j];
+        const float send = upper ? v[j] : v[j + N / 2];
+        v[j] = keep + xor_partner<M>(send, lane);
+      }
     }
     RowHalver<N / 2, M / 2>::run(v, lane);
   }
 };
+// one row left: the full sum over lane bits M .. 0
 template <int M>
 struct RowHalver<1, M> {
-  TFA_DEV static void run(float* v, int lane) {
-#pragma unroll
-    for (int m = M; m >= 1; m >>= 1) v[0] += __shfl_xor(v[0], m, kWave);
-  }
+  TFA_DEV static void run(float* v, int) { v[0] = lanes_sum<log2_const(M) + 1>(v[0]); }
 };
 template <>
 struct RowHalver<1, 0> {
@@ -172,9 +245,7 @@ TFA_DEV float wave_sum_rows(float* v, int lane) {
 // Sum over groups of `width` consecutive lanes (width a power of two <= 64).
 template <int WIDTH>
 TFA_DEV float group_sum(float v) {
-#pragma unroll
-  for (int m = WIDTH / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
+  return lanes_sum<log2_const(WIDTH)>(v);
 }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `scratch` holds one
@@ -318,15 +389,22 @@ TFA_DEV int block_best(const float* bv, const int* bi, int nb, float* s_v, int* 
         best_i = ix[u];
       }
   }
-#pragma unroll
-  for (int m = kWave / 2; m >= 1; m >>= 1) {
-    const float ov = __shfl_xor(best_v, m, kWave);
-    const int oi = __shfl_xor(best_i, m, kWave);
+  const int lane = t & (kWave - 1);
+  auto step = [&](auto mc) __attribute__((always_inline)) {
+    constexpr int M = decltype(mc)::value;
+    const float ov = xor_lane<M>(best_v, lane);
+    const int oi = xor_lane<M>(best_i, lane);
     if (better_pick(ov, oi, best_v, best_i)) {
       best_v = ov;
       best_i = oi;
     }
-  }
+  };
+  step(std::integral_constant<int, 32>{});
+  step(std::integral_constant<int, 16>{});
+  step(std::integral_constant<int, 8>{});
+  step(std::integral_constant<int, 4>{});
+  step(std::integral_constant<int, 2>{});
+  step(std::integral_constant<int, 1>{});
   if ((t & (kWave - 1)) == 0) {
     s_v[t / kWave] = best_v;
     s_i[t / kWave] = best_i;

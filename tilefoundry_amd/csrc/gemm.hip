@@ -323,7 +323,7 @@ __global__ __launch_bounds__(C::kThreads) void gemm_kernel(const GemmArgs a) {
       for (int i = 0; i < 4; ++i) y[i] = round_bf(x[i] * inv * (1.0f + g4[i]));
       float partner[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) partner[i] = __shfl_xor(y[i], 8, kWave);
+      for (int i = 0; i < 4; ++i) partner[i] = xor_lane<8>(y[i], lane);
       if (lane < 16) {
         const uint2 cv = *reinterpret_cast<const uint2*>(a.cos_t + static_cast<size_t>(grow) * 64 + 4 * lane);
         const uint2 sv = *reinterpret_cast<const uint2*>(a.sin_t + static_cast<size_t>(grow) * 64 + 4 * lane);

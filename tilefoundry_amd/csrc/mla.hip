@@ -523,8 +523,7 @@ __global__ __launch_bounds__(kThreads) void mla_combine_up_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) d = fmaf(w8[i], olat[64 * q + 8 * c8 + i], d);
   }
-  d += __shfl_xor(d, 1, kWave);
-  d += __shfl_xor(d, 2, kWave);
+  d = lanes_sum<2>(d);
   if (q == 0) attn[static_cast<size_t>(b) * H * kV + h * kV + v] = static_cast<uint16_t>(f2bf(d));
 }
 

@@ -309,7 +309,7 @@ void flash_prefill_kernel(const FlashArgs a) {
         float mx = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * a.scale_log2;
+        mx = fmaxf(mx, xor_lane<32>(mx, lane)) * a.scale_log2;
         if (__builtin_amdgcn_ballot_w64(mx > m_run[t] + kSlack) != 0) {
           const float m_new = fmaxf(m_run[t], mx);
           const float alpha = m_run[t] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[t] - m_new);
@@ -382,7 +382,7 @@ void flash_prefill_kernel(const FlashArgs a) {
   // of query q0 + 32 t + n32
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
-    const float l_tot = l_run[t] + __shfl_xor(l_run[t], 32, kWave);
+    const float l_tot = l_run[t] + xor_lane<32>(l_run[t], lane);
     const float inv = 1.0f / l_tot;
     const int qn = q0 + 32 * t + n32;
     if (qn >= N) continue;

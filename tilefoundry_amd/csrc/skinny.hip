@@ -199,7 +199,7 @@ __global__ __launch_bounds__(W * kWave) void skinny_gemm_kernel(const SkinnyArgs
       }
       if (EPI == SK_SWIGLU) {
         // rows (2i, 2i+1) = (gate_i, up_i) sit in lanes r16 and r16 ^ 1
-        const float other = __shfl_xor(val, 1, kWave);
+        const float other = xor_lane<1>(val, r16);
         if ((r16 & 1) == 0 && m < a.M && n + 1 < a.N) {
           const float g = round_bf(val), u = round_bf(other);
           const float act = round_bf(round_bf(g / (1.0f + expf(-g))) * u);
@@ -212,12 +212,16 @@ __global__ __launch_bounds__(W * kWave) void skinny_gemm_kernel(const SkinnyArgs
         // per token: best of the tile's 16 rows (lowest index on ties)
         float bvv = n < a.N ? val : -FLT_MAX;
         int bii = n < a.N ? n : 0x7fffffff;
-#pragma unroll
-        for (int msk = 1; msk < 16; msk <<= 1) {
-          const float ov = __shfl_xor(bvv, msk, kWave);
-          const int oi = __shfl_xor(bii, msk, kWave);
+        auto pick = [&](auto mc) __attribute__((always_inline)) {
+          constexpr int M = decltype(mc)::value;
+          const float ov = xor_lane<M>(bvv, r16);
+          const int oi = xor_lane<M>(bii, r16);
           if (better(ov, oi, bvv, bii)) { bvv = ov; bii = oi; }
-        }
+        };
+        pick(std::integral_constant<int, 1>{});
+        pick(std::integral_constant<int, 2>{});
+        pick(std::integral_constant<int, 4>{});
+        pick(std::integral_constant<int, 8>{});
         const int grp16 = n0 / kGroupRows + rh;   // this tile's 16-row group
         if (r16 == 0 && m < a.M && grp16 < a.ngroups) {
           a.bv[static_cast<size_t>(m) * a.ngroups + grp16] = bvv;
