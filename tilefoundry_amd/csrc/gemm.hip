@@ -295,18 +295,43 @@ __global__ __launch_bounds__(C::kThreads) void gemm_kernel(const GemmArgs a) {
     const uint2 gv = *reinterpret_cast<const uint2*>(gamma + cl);
     g4[0] = lo_bf(gv.x); g4[1] = hi_bf(gv.x); g4[2] = lo_bf(gv.y); g4[3] = hi_bf(gv.y);
   }
-  for (int r0 = wid * kRPP; r0 < BM; r0 += C::kWaves * kRPP) {
-    const int row = r0 + sub;
+  // Every global input of the row passes -- the residual rows, or the rope rows
+  // of a q / k slice -- is issued before the first pass, into the registers the
+  // accumulators held: one memory round trip for the epilogue instead of one per
+  // pass (a one-round grid otherwise ends on 16-32 serial trips per block).
+  constexpr int kPasses = BM / (C::kWaves * kRPP);
+  static_assert(kPasses * C::kWaves * kRPP == BM, "whole row passes per wave");
+  auto pass_row = [&](int p) __attribute__((always_inline)) { return wid * kRPP + p * C::kWaves * kRPP + sub; };
+  uint2 pre_a[EPI == EPI_RESID || EPI == EPI_QKNR ? kPasses : 1];
+  uint2 pre_b[EPI == EPI_QKNR ? kPasses : 1];
+  if (EPI == EPI_RESID) {
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int grow = min(m0 + pass_row(p), a.M - 1);
+      pre_a[p] = *reinterpret_cast<const uint2*>(a.res + static_cast<size_t>(grow) * a.ldr + n0 + cl);
+    }
+  }
+  if (EPI == EPI_QKNR && norm && lane < 16) {
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int grow = min(m0 + pass_row(p), a.M - 1);
+      pre_a[p] = *reinterpret_cast<const uint2*>(a.cos_t + static_cast<size_t>(grow) * 64 + 4 * lane);
+      pre_b[p] = *reinterpret_cast<const uint2*>(a.sin_t + static_cast<size_t>(grow) * 64 + 4 * lane);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < kPasses; ++p) {
+    const int row = pass_row(p);
     const int grow = m0 + row;
     if (EPI == EPI_QKNR) {
-      if (m0 + r0 >= a.M) break;           // wave-uniform: one row per pass at BN = 256
+      if (m0 + row - sub >= a.M) break;    // wave-uniform: one row per pass at BN = 256
     } else if (grow >= a.M) {
       continue;
     }
     uint2 v = *reinterpret_cast<const uint2*>(ep + row * C::kEpPitch + cl);
     uint16_t* dst = a.c + static_cast<size_t>(grow) * a.ldc + n0 + cl;
     if (EPI == EPI_RESID) {
-      const uint2 rv = *reinterpret_cast<const uint2*>(a.res + static_cast<size_t>(grow) * a.ldr + n0 + cl);
+      const uint2 rv = pre_a[p];
       v.x = pack_bf(round_bf(lo_bf(rv.x) + lo_bf(v.x)), round_bf(hi_bf(rv.x) + hi_bf(v.x)));
       v.y = pack_bf(round_bf(lo_bf(rv.y) + lo_bf(v.y)), round_bf(hi_bf(rv.y) + hi_bf(v.y)));
     }
@@ -325,8 +350,8 @@ __global__ __launch_bounds__(C::kThreads) void gemm_kernel(const GemmArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) partner[i] = xor_lane<8>(y[i], lane);
       if (lane < 16) {
-        const uint2 cv = *reinterpret_cast<const uint2*>(a.cos_t + static_cast<size_t>(grow) * 64 + 4 * lane);
-        const uint2 sv = *reinterpret_cast<const uint2*>(a.sin_t + static_cast<size_t>(grow) * 64 + 4 * lane);
+        const uint2 cv = pre_a[p];
+        const uint2 sv = pre_b[p];
         const float c[4] = {lo_bf(cv.x), hi_bf(cv.x), lo_bf(cv.y), hi_bf(cv.y)};
         const float s4[4] = {lo_bf(sv.x), hi_bf(sv.x), lo_bf(sv.y), hi_bf(sv.y)};
         const float sign = lane < 8 ? -1.0f : 1.0f;   // rotate_half: first half pairs with -x[d + 32]
