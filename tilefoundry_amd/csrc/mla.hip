@@ -30,6 +30,7 @@
 #include <float.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "abi_util.h"
 #include "common.h"
@@ -527,6 +528,69 @@ __global__ __launch_bounds__(kThreads) void mla_combine_up_kernel(
   if (q == 0) attn[static_cast<size_t>(b) * H * kV + h * kV + v] = static_cast<uint16_t>(f2bf(d));
 }
 
+// The same merge for at most 64 splits in one memory round trip: every load a
+// thread needs -- the write slot, split (lane)'s max and sum, its latent column
+// of every split's output, its row quarter of W_UV -- is issued at the start,
+// none behind a branch (splits past the write slot are allocated and read but
+// weighted zero). The max is a wave reduction over the lanes' splits; each
+// split's weight reaches the other lanes by readlane, and the denominator and
+// the weighted sum run in split order as in the loop form.
+constexpr int kFastMergeSplits = 64;
+template <int NSP>   // splits, rounded up to 16 / 32 / 64
+__global__ __launch_bounds__(kThreads) void mla_combine_up_fast_kernel(
+    const uint16_t* __restrict__ op, const float* __restrict__ mp, const float* __restrict__ lp,
+    const int* __restrict__ wr, int ns, int split, int H, int cap, const uint16_t* __restrict__ w_kv_b,
+    uint16_t* __restrict__ attn) {
+  __shared__ float olat[kLat];
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const size_t srow = static_cast<size_t>(b) * ns * H + h;   // (b, s=0, h)
+  // 1. every load, none behind a branch (a split past ns re-reads split ns - 1)
+  const int last_raw = wr[b];
+  const int sl = min(lane, ns - 1);
+  const float m_l = mp[srow + static_cast<size_t>(sl) * H];
+  const float l_l = lp[srow + static_cast<size_t>(sl) * H];
+  uint16_t ov[NSP];
+#pragma unroll
+  for (int s = 0; s < NSP; ++s) ov[s] = op[(srow + static_cast<size_t>(min(s, ns - 1)) * H) * kLat + t];
+  const int v = t >> 2, q = t & 3;   // value row v, latent quarter q
+  const uint16_t* wrow = w_kv_b + (static_cast<size_t>(h) * kKvB + kNope + v) * kLat + 64 * q;
+  uint4 wv[8];
+#pragma unroll
+  for (int c8 = 0; c8 < 8; ++c8) wv[c8] = ld16(wrow + 8 * c8);
+  // 2. weights of the live splits
+  const int last = last_raw < 0 ? 0 : (last_raw >= cap ? cap - 1 : last_raw);
+  const int nsa = min(ns, last / split + 1);
+  const bool live = lane < nsa;
+  const float M = lanes_max<6>(live ? m_l : -INFINITY);
+  const float w = live ? l_l * expf(m_l - M) : 0.f;
+  // 3. o_lat[t] = sum_s w_s op_s / sum_s w_s in split order (dead splits add
+  //    exact zeros: their weight and their value are selected away)
+  float L = 0.f, acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < NSP; ++s) {
+    const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
+    const float val = s < nsa ? bf2f(ov[s]) : 0.f;
+    L += ws;
+    acc = fmaf(ws, val, acc);
+  }
+  olat[t] = acc / L;
+  lds_barrier();
+  // 4. attn[b, h*64 + v] = bf16(W_UV[h][v] . o_lat)
+  float d = 0.f;
+#pragma unroll
+  for (int c8 = 0; c8 < 8; ++c8) {
+    float w8[8];
+    unpack8(wv[c8], w8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) d = fmaf(w8[i], olat[64 * q + 8 * c8 + i], d);
+  }
+  d = lanes_sum<2>(d);
+  if (q == 0) attn[static_cast<size_t>(b) * H * kV + h * kV + v] = static_cast<uint16_t>(f2bf(d));
+}
+
 // ------------------------------------------------------------- rows_residual
 // out[m, i] = bf16(res[m, i] + bf16(bf16(sum_s part[s, m, i]) * alpha)), 8 elements
 // per thread.
@@ -874,9 +938,22 @@ int tfa_mla_combine_up(const void* op, const float* mp, const float* lp, const i
   TFA_REQUIRE(batch >= 1 && batch <= 65535 && heads >= 1 && heads <= kHeadRows, TFA_ERR_SHAPE,
               "tfa_mla_combine_up: batch %lld / heads %lld out of range", (long long)batch, (long long)heads);
   TFA_ALIGN16(w_kv_b);
-  mla_combine_up_kernel<<<dim3((unsigned)heads, (unsigned)batch), kThreads, 0, stream>>>(
-      static_cast<const uint16_t*>(op), mp, lp, wr, (int)splits, (int)split, (int)heads, (int)cap,
-      static_cast<const uint16_t*>(w_kv_b), static_cast<uint16_t*>(attn));
+  const dim3 grid((unsigned)heads, (unsigned)batch);
+  auto fast = [&](auto nsp) {
+    mla_combine_up_fast_kernel<decltype(nsp)::value><<<grid, kThreads, 0, stream>>>(
+        static_cast<const uint16_t*>(op), mp, lp, wr, (int)splits, (int)split, (int)heads, (int)cap,
+        static_cast<const uint16_t*>(w_kv_b), static_cast<uint16_t*>(attn));
+  };
+  if (splits <= 16)
+    fast(std::integral_constant<int, 16>{});
+  else if (splits <= 32)
+    fast(std::integral_constant<int, 32>{});
+  else if (splits <= kFastMergeSplits)
+    fast(std::integral_constant<int, kFastMergeSplits>{});
+  else
+    mla_combine_up_kernel<<<dim3((unsigned)heads, (unsigned)batch), kThreads, 0, stream>>>(
+        static_cast<const uint16_t*>(op), mp, lp, wr, (int)splits, (int)split, (int)heads, (int)cap,
+        static_cast<const uint16_t*>(w_kv_b), static_cast<uint16_t*>(attn));
   return launched("mla_combine_up");
 }
 
