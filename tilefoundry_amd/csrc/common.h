@@ -328,6 +328,11 @@ static_assert(waitcnt_vm(0) == 0xF70 && waitcnt_vm(16) == 0x4F70 && waitcnt_vm(6
 TFA_DEV void lds_dma16(const void* g, uint32_t lds_off) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_off) : "memory");
 }
+// The same for data read exactly once (a decode cache): non-temporal, as the
+// streaming register loads.
+TFA_DEV void lds_dma16_stream(const void* g, uint32_t lds_off) {
+  asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(lds_off) : "memory");
+}
 
 // The 32-bit LDS byte offset of a __shared__ object.
 template <typename T>

@@ -302,12 +302,12 @@ void mla_attn_kernel(const MlaAttnArgs a) {
       if (j < kStep / 2) {
         const int row = 2 * j + (lane >> 5);
         const int p = min(p0 + row, n - 1);
-        lds_dma16(lat + static_cast<size_t>(p) * kLat + 8 * lat_slot(row, lane & 31),
+        lds_dma16_stream(lat + static_cast<size_t>(p) * kLat + 8 * lat_slot(row, lane & 31),
                   lds0 + st * kStageBytes + j * 16 * kWave);
       } else {
         const int row = 16 * (j - kStep / 2) + (lane >> 2);
         const int p = min(p0 + row, n - 1);
-        lds_dma16(rk + static_cast<size_t>(p) * kRope + 8 * rope_slot(row, lane & 3),
+        lds_dma16_stream(rk + static_cast<size_t>(p) * kRope + 8 * rope_slot(row, lane & 3),
                   lds0 + st * kStageBytes + kLatStage + (j - kStep / 2) * 16 * kWave);
       }
     }
