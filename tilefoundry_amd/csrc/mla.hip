@@ -62,6 +62,20 @@ TFA_DEV void set_err(int* err, int code) {
   if (err) atomicExch(err, code);
 }
 
+// Sum of the first ks (1..kMaxSplitsK) split-K partials p[0], p[stride], ... in
+// split order, every load unconditional (a split past ks re-reads split ks - 1,
+// and is left out of the sum by a select): behind per-split branches the loads
+// were issued, and waited for, one at a time.
+TFA_DEV float sum_splits_flat(const float* p, size_t stride, int ks) {
+  float v[kMaxSplitsK];
+#pragma unroll
+  for (int s = 0; s < kMaxSplitsK; ++s) v[s] = p[static_cast<size_t>(min(s, ks - 1)) * stride];
+  float acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < kMaxSplitsK; ++s) acc += s < ks ? v[s] : 0.f;
+  return acc;
+}
+
 // Rotate-half over 32 dims in bf16, each product and the sum landing: the
 // torch spelling of reference_ops.py:99-109.
 TFA_DEV float rope_bf(float x, float partner, float c, float s) {
@@ -85,7 +99,7 @@ __global__ __launch_bounds__(kThreads) void mla_prep_kernel(
   const size_t kstride = static_cast<size_t>(B) * row;
   const float* pb = part + static_cast<size_t>(b) * row;
   auto reduced = [&](int i) {
-    return round_bf(sum_splits(pb + i, kstride, ks));   // the projection lands in bf16
+    return round_bf(sum_splits_flat(pb + i, kstride, ks));   // the projection lands in bf16
   };
 
   // Every load this thread needs goes out before any arithmetic (one memory
@@ -155,28 +169,68 @@ __global__ __launch_bounds__(kThreads) void mla_prep_kernel(
 
 // -------------------------------------------------------------- mla_q_absorb
 // One block per head; thread t owns latent column t. qpart: [ks, B, H*96] f32
-// split-K partials of q_n . W_q_b^T. w_kv_b: [H*128, 256] (out, in).
+// split-K partials of q_n . W_q_b^T. w_kv_b: [H*128, 256] (out, in). Every load
+// goes out first -- the head's W_UK column t, all of the thread's partials (the
+// B x 96 projection values of the head, dealt over the block, unrolled for
+// B <= MAXB), the positions -- so the block makes one memory round trip, and a
+// second only for the rope rows of the positions.
+template <int MAXB>
 __global__ __launch_bounds__(kThreads) void mla_q_absorb_kernel(
     const float* __restrict__ qpart, int ks, int B, int H, const uint16_t* __restrict__ w_kv_b,
     const uint16_t* __restrict__ cos_t, const uint16_t* __restrict__ sin_t, int rope_rows,
     const int* __restrict__ pos, uint16_t* __restrict__ q_abs, int* err) {
-  __shared__ float qn[kMaxBatch][kNope];
-  __shared__ float qr[kMaxBatch][kRope];
+  constexpr int kQH = kNope + kRope;                       // projection values per head
+  constexpr int kPer = (MAXB * kQH + kThreads - 1) / kThreads;   // values per thread
+  constexpr int kRopePer = (MAXB * kRope + kThreads - 1) / kThreads;
+  __shared__ float qn[MAXB][kNope];
+  __shared__ float qr[MAXB][kRope];
   const int h = blockIdx.x;
   const int t = threadIdx.x;
-  const int qrow = H * (kNope + kRope);
+  const int qrow = H * kQH;
   const size_t kstride = static_cast<size_t>(B) * qrow;
-  // this head's W_UK column t, loaded while the partials are reduced
+  const int nval = B * kQH;
   float wc[kNope];
   const uint16_t* wuk = w_kv_b + static_cast<size_t>(h) * kKvB * kLat + t;
 #pragma unroll
   for (int i = 0; i < kNope; ++i) wc[i] = bf2f(wuk[static_cast<size_t>(i) * kLat]);
-  for (int e = t; e < B * (kNope + kRope); e += kThreads) {
-    const int b = e / (kNope + kRope), i = e % (kNope + kRope);
-    const float* src = qpart + static_cast<size_t>(b) * qrow + h * (kNope + kRope) + i;
-    const float acc = sum_splits(src, kstride, ks);
+  float part[kPer][kMaxSplitsK];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = min(t + kThreads * j, nval - 1);
+    const int b = e / kQH, i = e % kQH;
+    const float* src = qpart + static_cast<size_t>(b) * qrow + h * kQH + i;
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplitsK; ++sp) part[j][sp] = src[static_cast<size_t>(min(sp, ks - 1)) * kstride];
+  }
+  int pr[kRopePer];
+#pragma unroll
+  for (int j = 0; j < kRopePer; ++j) pr[j] = pos[min((t + kThreads * j) / kRope, B - 1)];
+  // the projection values land in bf16 (split order)
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = t + kThreads * j;
+    if (e >= nval) continue;
+    float acc = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplitsK; ++sp) acc += sp < ks ? part[j][sp] : 0.f;
+    const int b = e / kQH, i = e % kQH;
     if (i < kNope) qn[b][i] = round_bf(acc);
     else qr[b][i - kNope] = round_bf(acc);
+  }
+  // the rope rows of the positions (the second round trip)
+  float cs[kRopePer], sn[kRopePer];
+#pragma unroll
+  for (int j = 0; j < kRopePer; ++j) {
+    const int e = t + kThreads * j;
+    int p = pr[j];
+    if (e < B * kRope && (p < 0 || p >= rope_rows)) {
+      if (h == 0) set_err(err, 6);
+      p = 0;
+    }
+    p = p < 0 || p >= rope_rows ? 0 : p;
+    const int d = e % kRope;
+    cs[j] = bf2f(cos_t[static_cast<size_t>(p) * kRope + d]);
+    sn[j] = bf2f(sin_t[static_cast<size_t>(p) * kRope + d]);
   }
   lds_barrier();
   for (int b = 0; b < B; ++b) {
@@ -185,18 +239,14 @@ __global__ __launch_bounds__(kThreads) void mla_q_absorb_kernel(
     for (int i = 0; i < kNope; ++i) acc = fmaf(qn[b][i], wc[i], acc);
     q_abs[(static_cast<size_t>(b) * H + h) * kQK + t] = static_cast<uint16_t>(f2bf(acc));
   }
-  for (int e = t; e < B * kRope; e += kThreads) {
+#pragma unroll
+  for (int j = 0; j < kRopePer; ++j) {
+    const int e = t + kThreads * j;
+    if (e >= B * kRope) continue;
     const int b = e / kRope, d = e % kRope;
-    int p = pos[b];
-    if (p < 0 || p >= rope_rows) {
-      if (h == 0) set_err(err, 6);
-      p = 0;
-    }
     const float partner = d < kRope / 2 ? -qr[b][d + kRope / 2] : qr[b][d - kRope / 2];
-    const float c = bf2f(cos_t[static_cast<size_t>(p) * kRope + d]);
-    const float s = bf2f(sin_t[static_cast<size_t>(p) * kRope + d]);
     q_abs[(static_cast<size_t>(b) * H + h) * kQK + kLat + d] =
-        static_cast<uint16_t>(f2bf(rope_bf(qr[b][d], partner, c, s)));
+        static_cast<uint16_t>(f2bf(rope_bf(qr[b][d], partner, cs[j], sn[j])));
   }
 }
 
@@ -875,10 +925,16 @@ int tfa_mla_q_absorb(const float* q_part, int64_t ks, int64_t batch, int64_t hea
   TFA_REQUIRE(ks >= 1 && ks <= kMaxSplitsK && rope_rows >= 1, TFA_ERR_SHAPE,
               "tfa_mla_q_absorb: ks %lld not in [1, %d] or empty rope table", (long long)ks, kMaxSplitsK);
   TFA_ALIGN16(w_kv_b);
-  mla_q_absorb_kernel<<<(int)heads, kThreads, 0, stream>>>(
-      q_part, (int)ks, (int)batch, (int)heads, static_cast<const uint16_t*>(w_kv_b),
-      static_cast<const uint16_t*>(cos_t), static_cast<const uint16_t*>(sin_t), (int)rope_rows, pos,
-      static_cast<uint16_t*>(q_abs), err);
+  if (batch <= 8)
+    mla_q_absorb_kernel<8><<<(int)heads, kThreads, 0, stream>>>(
+        q_part, (int)ks, (int)batch, (int)heads, static_cast<const uint16_t*>(w_kv_b),
+        static_cast<const uint16_t*>(cos_t), static_cast<const uint16_t*>(sin_t), (int)rope_rows, pos,
+        static_cast<uint16_t*>(q_abs), err);
+  else
+    mla_q_absorb_kernel<kMaxBatch><<<(int)heads, kThreads, 0, stream>>>(
+        q_part, (int)ks, (int)batch, (int)heads, static_cast<const uint16_t*>(w_kv_b),
+        static_cast<const uint16_t*>(cos_t), static_cast<const uint16_t*>(sin_t), (int)rope_rows, pos,
+        static_cast<uint16_t*>(q_abs), err);
   return launched("mla_q_absorb");
 }
 
