@@ -265,19 +265,20 @@ TFA_DEV float block_sum(float v, float* scratch) {
 }
 
 // ------------------------------------------------------------ split-K sums
-// Sum of the first `ks` (<= MAXKS) of p[0], p[stride], p[2 stride], ... in split
-// order, with every load issued before the first add: one memory round trip,
-// not one per split (a runtime-bounded loop waits for each load in turn).
+// Sum of the first `ks` (1 <= ks <= MAXKS) of p[0], p[stride], p[2 stride], ...
+// in split order, with every load issued before the first add and none behind
+// a branch (a split past ks re-reads split ks - 1 and a select leaves it out of
+// the sum): one memory round trip, not one per split (a runtime-bounded loop,
+// or a load per branch, is waited for in turn).
 constexpr int kMaxSplitsK = 8;
 template <int MAXKS = kMaxSplitsK>
 TFA_DEV float sum_splits(const float* p, size_t stride, int ks) {
   float v[MAXKS];
 #pragma unroll
-  for (int s = 0; s < MAXKS; ++s) v[s] = s < ks ? p[s * stride] : 0.f;
+  for (int s = 0; s < MAXKS; ++s) v[s] = p[static_cast<size_t>(min(s, ks - 1)) * stride];
   float acc = 0.f;
 #pragma unroll
-  for (int s = 0; s < MAXKS; ++s)
-    if (s < ks) acc += v[s];
+  for (int s = 0; s < MAXKS; ++s) acc += s < ks ? v[s] : 0.f;
   return acc;
 }
 
@@ -288,20 +289,19 @@ TFA_DEV void sum_splits8(const float* p, size_t stride, int ks, float* acc) {
   float4 v[MAXKS][2];
 #pragma unroll
   for (int s = 0; s < MAXKS; ++s) {
-    if (s < ks) {
-      const float4* q = reinterpret_cast<const float4*>(p + s * stride);
-      v[s][0] = q[0];
-      v[s][1] = q[1];
-    }
+    const float4* q = reinterpret_cast<const float4*>(p + static_cast<size_t>(min(s, ks - 1)) * stride);
+    v[s][0] = q[0];
+    v[s][1] = q[1];
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
 #pragma unroll
   for (int s = 0; s < MAXKS; ++s) {
-    if (s < ks) {
-      acc[0] += v[s][0].x; acc[1] += v[s][0].y; acc[2] += v[s][0].z; acc[3] += v[s][0].w;
-      acc[4] += v[s][1].x; acc[5] += v[s][1].y; acc[6] += v[s][1].z; acc[7] += v[s][1].w;
-    }
+    const bool in = s < ks;
+    acc[0] += in ? v[s][0].x : 0.f; acc[1] += in ? v[s][0].y : 0.f;
+    acc[2] += in ? v[s][0].z : 0.f; acc[3] += in ? v[s][0].w : 0.f;
+    acc[4] += in ? v[s][1].x : 0.f; acc[5] += in ? v[s][1].y : 0.f;
+    acc[6] += in ? v[s][1].z : 0.f; acc[7] += in ? v[s][1].w : 0.f;
   }
 }
 

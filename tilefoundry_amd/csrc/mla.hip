@@ -62,20 +62,6 @@ TFA_DEV void set_err(int* err, int code) {
   if (err) atomicExch(err, code);
 }
 
-// Sum of the first ks (1..kMaxSplitsK) split-K partials p[0], p[stride], ... in
-// split order, every load unconditional (a split past ks re-reads split ks - 1,
-// and is left out of the sum by a select): behind per-split branches the loads
-// were issued, and waited for, one at a time.
-TFA_DEV float sum_splits_flat(const float* p, size_t stride, int ks) {
-  float v[kMaxSplitsK];
-#pragma unroll
-  for (int s = 0; s < kMaxSplitsK; ++s) v[s] = p[static_cast<size_t>(min(s, ks - 1)) * stride];
-  float acc = 0.f;
-#pragma unroll
-  for (int s = 0; s < kMaxSplitsK; ++s) acc += s < ks ? v[s] : 0.f;
-  return acc;
-}
-
 // Rotate-half over 32 dims in bf16, each product and the sum landing: the
 // torch spelling of reference_ops.py:99-109.
 TFA_DEV float rope_bf(float x, float partner, float c, float s) {
@@ -99,7 +85,7 @@ __global__ __launch_bounds__(kThreads) void mla_prep_kernel(
   const size_t kstride = static_cast<size_t>(B) * row;
   const float* pb = part + static_cast<size_t>(b) * row;
   auto reduced = [&](int i) {
-    return round_bf(sum_splits_flat(pb + i, kstride, ks));   // the projection lands in bf16
+    return round_bf(sum_splits(pb + i, kstride, ks));   // the projection lands in bf16
   };
 
   // Every load this thread needs goes out before any arithmetic (one memory
