@@ -309,7 +309,7 @@ def batch32(seed: int, steps: int = NEW_TOKENS, args=None) -> dict:
     kv_bytes = 32 * cfg.layers * mean_ctx * 2 * cfg.kv_heads * cfg.head_dim * 2
     ms = gen.seconds * 1e3 / steps
     out = {"value": round(gen.tokens_per_second, 1), "unit": "tok/s", "batch": 32, "new_tokens": steps,
-           "prompt_tokens": PROMPT, "ms_per_step": round(ms, 4),
+           "prompt_tokens": PROMPT, "ms_per_step": round(ms, 4), "attention": eng.attention,
            "step_hbm": {"bytes_per_step": int(weight_bytes + kv_bytes),
                         "GB/s": round((weight_bytes + kv_bytes) / (ms * 1e-3) / 1e9, 1)},
            "prompt": {"walk": walk, "prefill": pre,

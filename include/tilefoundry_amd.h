@@ -221,6 +221,27 @@ int tfa_decode_attention(const void* q, const float* qkv_part, int64_t part_ks,
                          float* op, float* mp, float* lp, int neutral, int* err,
                          hipStream_t stream);
 
+/* One step of GQA decode attention with the query prep fused and no split:
+ * one block per (sequence, kv head) over the whole context 0..wr[b]. From the
+ * q|k|v split-K partials qkv_part [part_ks (<= 8), batch, (hq + 2 hkv) * 128]
+ * f32 (each value landing in bf16): the query heads get Qwen3RMSNorm (gamma_q,
+ * eps_head) + rotate-half RoPE at pos[b] (cos / sin [rope_rows, 128]), the key
+ * the same with gamma_k and is written to k_cache row wr[b], the value row to
+ * v_cache row wr[b] (caches [batch, cap, hkv * 128]). Then per query head
+ * s = scale q.k, e = exp(s - max s) in f32, out[b, h*128 + d] =
+ * bf16(sum bf16(e) v / sum e) -> out [batch, hq * 128] bf16. hq / hkv in
+ * {1, 2, 4}; (cap + 64) * (hq / hkv) <= 32768. For batches whose sequences x kv
+ * heads fill the device (the grid is hkv x batch blocks).
+ * err: 4 = wr out of [0, cap) (the heads' output is zero), 5 = pos out of
+ * [0, rope_rows).
+ * Replaces, for one step: examples/qwen3_1_7b-tilelang/fast/kernels.py:328-411
+ * (qk_rope_cache), :418-501 (attn_partial) and :504-540 (attn_combine). */
+int tfa_decode_attention_seq(const float* qkv_part, int64_t part_ks, const void* gamma_q,
+                             const void* gamma_k, float eps_head, const void* cos_t, const void* sin_t,
+                             int64_t rope_rows, void* k_cache, void* v_cache, const int* pos, const int* wr,
+                             int64_t batch, int64_t hq, int64_t hkv, int64_t head_dim, int64_t cap, float scale,
+                             void* out, int* err, hipStream_t stream);
+
 /* out[b, h*D + d] = bf16(sum_s op[b,s,h,d] e^(mp-M) / sum_s lp[b,s,h] e^(mp-M))
  * over all `splits`, or (wr != NULL) over the splits holding slots 0..wr[b].
  * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:504-540 (attn_combine). */

@@ -180,6 +180,87 @@ def test_batched_attention_from_partials(dev):
         assert_close(f"attention b={b}", out[b], OQ.attend(q, kk, vv, D ** -0.5))
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("hq,hkv,pos", [(16, 8, [0, 1, 31, 32, 100, 511, 1000, 2111, 4095]),
+                                        (8, 8, [0, 77, 300]), (16, 4, [5, 64, 1023])])
+def test_batched_attention_seq(dev, hq, hkv, pos):
+    """The whole-context form: one block per (sequence, kv head), the prep fused,
+    no split merge. Per sequence: the new K and V rows at its own slot, and its
+    output against the oracle's unsplit order (exp against the row max, bf16
+    weights, o / l landed once) -- contexts from one position to the full
+    4096-slot cache, and around the 32-position step."""
+    from tilefoundry_amd._lib import C
+
+    g = gen(12)
+    B, cap, ks = len(pos), 4096, 2
+    rows = (hq + 2 * hkv) * D
+    part = torch.randn(ks, B, rows, generator=g) * 0.5
+    gq = randn(D, g=g, std=0.1, mean=1.0)
+    gk = randn(D, g=g, std=0.1, mean=1.0)
+    cos, sin = OQ.rope_tables(cap, D, 1.0e6)
+    kc = torch.zeros(B, cap, hkv, D).to(BF)
+    vc = torch.zeros(B, cap, hkv, D).to(BF)
+    for b, p in enumerate(pos):
+        kc[b, :p] = randn(p, hkv, D, g=g)
+        vc[b, :p] = randn(p, hkv, D, g=g)
+    # slots past each context hold NaN: they must never be read into the result
+    for b, p in enumerate(pos):
+        kc[b, p + 1:] = float("nan")
+        vc[b, p + 1:] = float("nan")
+    kd, vd = kc.view(B, cap, -1).to(dev), vc.view(B, cap, -1).to(dev)
+    posd = torch.tensor(pos, dtype=torch.int32, device=dev)
+    out = torch.empty(B, hq * D, dtype=BF, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    C.decode_attention_seq(part.to(dev), gq.to(dev), gk.to(dev), 1e-6, cos.to(dev), sin.to(dev), posd, posd,
+                           kd, vd, hq, hkv, D ** -0.5, out, err)
+    assert int(err) == 0
+    raw = part.sum(0).to(BF)
+    for b, p in enumerate(pos):
+        q = OQ.rope(OQ.head_norm(raw[b, : hq * D].view(hq, D), gq, 1e-6), cos[p], sin[p])
+        k = OQ.rope(OQ.head_norm(raw[b, hq * D: (hq + hkv) * D].view(hkv, D), gk, 1e-6), cos[p], sin[p])
+        v = raw[b, (hq + hkv) * D:].view(hkv, D)
+        assert_close(f"k row b={b}", kd[b, p].view(hkv, D), k)
+        assert_equal(f"v row b={b}", vd[b, p].view(hkv, D), v)
+        kk = torch.cat([kc[b, :p], k.unsqueeze(0)])
+        vv = torch.cat([vc[b, :p], v.unsqueeze(0)])
+        assert_close(f"attention b={b} ctx {p + 1}", out[b], OQ.attend(q, kk, vv, D ** -0.5, p_bf16=True))
+
+
+@pytest.mark.gpu
+def test_batched_attention_seq_errors(dev):
+    """A newest slot outside the cache is flagged (err 4) and that sequence's
+    output is zero; a rope position past the table is flagged (err 5); a cache
+    too long for the score store and an unsupported group are refused."""
+    from tilefoundry_amd._lib import C
+
+    B, cap, hq, hkv = 2, 256, 16, 8
+    rows = (hq + 2 * hkv) * D
+    part = torch.ones(1, B, rows, device=dev)
+    gam = torch.ones(D, dtype=BF, device=dev)
+    cos, sin = (t.to(dev) for t in OQ.rope_tables(cap, D, 1.0e6))
+    kc = torch.zeros(B, cap, hkv * D, dtype=BF, device=dev)
+    vc = torch.zeros_like(kc)
+    out = torch.full((B, hq * D), 7.0, dtype=BF, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    wr = torch.tensor([3, cap], dtype=torch.int32, device=dev)
+    C.decode_attention_seq(part, gam, gam, 1e-6, cos, sin, wr.clamp(max=cap - 1), wr, kc, vc, hq, hkv, 0.1, out,
+                           err)
+    assert int(err) == 4
+    assert float(out[1].float().abs().max()) == 0.0
+    err.zero_()
+    pos = torch.tensor([3, cap + 5], dtype=torch.int32, device=dev)
+    C.decode_attention_seq(part, gam, gam, 1e-6, cos, sin, pos, torch.tensor([3, 4], dtype=torch.int32, device=dev),
+                           kc, vc, hq, hkv, 0.1, out, err)
+    assert int(err) == 5
+    big = torch.zeros(B, 16384, hkv * D, dtype=BF, device=dev)
+    with pytest.raises(ValueError, match="exceeds"):
+        C.decode_attention_seq(part, gam, gam, 1e-6, cos, sin, wr, wr, big, big, hq, hkv, 0.1, out, None)
+    part8 = torch.ones(1, B, (16 + 4) * D, device=dev)
+    kc2 = torch.zeros(B, cap, 2 * D, dtype=BF, device=dev)
+    with pytest.raises(ValueError, match="group"):
+        C.decode_attention_seq(part8, gam, gam, 1e-6, cos, sin, wr, wr, kc2, kc2, 16, 2, 0.1, out, None)
+
+
 def _small(layers=2, vocab=8192, seed=5):
     from tilefoundry_amd.qwen3 import Qwen3Config, synthetic_weights
 
@@ -194,12 +275,14 @@ def _oracle(wts, cfg):
 
 
 @pytest.mark.gpu
-def test_batch_engine_logits(dev):
+@pytest.mark.parametrize("attention", ["split", "seq"])
+def test_batch_engine_logits(dev, attention):
     from tilefoundry_amd.qwen3 import BatchEngine
 
     cfg, wts = _small()
     B = 4
-    eng = BatchEngine(cfg, batch=B, device=dev, max_new=32, prompt_room=32, weights=wts)
+    eng = BatchEngine(cfg, batch=B, device=dev, max_new=32, prompt_room=32, weights=wts, attention=attention)
+    assert eng.attention == attention
     prompts = OQ.prompt_ids(cfg.vocab, 9, seed=21, batch=B)
     got = eng.logits_for(prompts)
     om, oc = _oracle(wts, cfg)
@@ -226,6 +309,7 @@ def test_batch_engine_greedy(dev):
     cfg, wts = _small()
     B, n = 32, 16
     eng = BatchEngine(cfg, batch=B, device=dev, max_new=32, prompt_room=32, weights=wts)
+    assert eng.attention == "seq"   # 32 sequences x 8 kv heads fill the device
     prompts = OQ.prompt_ids(cfg.vocab, 8, seed=22, batch=B)
     om, oc = _oracle(wts, cfg)
     checked = (0, 7, 31)
@@ -247,13 +331,14 @@ def test_batch_engine_greedy(dev):
 
 
 @pytest.mark.gpu
-def test_batch_engine_matches_single_engine(dev):
+@pytest.mark.parametrize("attention", ["split", "seq"])
+def test_batch_engine_matches_single_engine(dev, attention):
     """The batch engine and the bs=1 engine agree on a sequence's logits."""
     from tilefoundry_amd.qwen3 import BatchEngine, Engine
 
     cfg, wts = _small()
     prompts = OQ.prompt_ids(cfg.vocab, 6, seed=23, batch=2)
-    be = BatchEngine(cfg, batch=2, device=dev, max_new=16, prompt_room=16, weights=wts)
+    be = BatchEngine(cfg, batch=2, device=dev, max_new=16, prompt_room=16, weights=wts, attention=attention)
     se = Engine(cfg, device=dev, max_new=16, prompt_room=16, weights=wts)
     got = be.logits_for(prompts)
     for b in range(2):

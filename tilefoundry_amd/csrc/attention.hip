@@ -51,6 +51,7 @@ struct AttnArgs {
   float* mp;              // [B, ns, hq]
   float* lp;              // [B, ns, hq]
   int neutral;            // write neutral partials for splits past the context
+  uint16_t* out;          // attn_seq: bf16 output [B, hq*D]
   int* err;
   int hq, hkv, cap, ns;
   float scale;
@@ -317,6 +318,264 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
       lp[s * a.hq + h] = l[g];
     }
   }
+}
+
+// attn_seq: the whole context of one (sequence, kv head) per block, with the
+// query prep fused and no split merge -- for batches whose sequences x kv heads
+// already fill the device (32 x 8 = 256 blocks, one per CU). The block sums its
+// G query heads, its key head and its value head from the q|k|v split-K
+// partials, applies the per-head norm and RoPE at pos[b], writes the new key
+// and value rows to cache slot wr[b], and then streams its kv head's cache in
+// two passes: keys -> every score of the context into LDS and the block max;
+// values -> exp(s - max) in f32 summed for the denominator and landed in bf16
+// into the f32 P.V. That is the order of the reference's unsplit softmax
+// (exp against the row max, bf16 weights, one landing of o / l), with no
+// per-split statistics. A position is one 256-byte cache row segment; lane
+// (slot = l / 16, dc = l % 16) of wave w takes position 32 s + 4 w + slot of
+// step s and the 8 dims 8 dc ..; the K steps then the V steps run through a
+// ring of R 16-byte loads per lane, so the value loads are in flight while the
+// last scores, the max and the weights are computed. Scores are v_dot2 bf16
+// products of the raw key rows; the weights are computed lane-parallel over
+// positions once the max is known and replace the scores in LDS. Replaces
+// examples/qwen3_1_7b-tilelang/fast/kernels.py:328-411 (qk_rope_cache),
+// :418-501 (attn_partial) and :504-540 (attn_combine) for one step.
+// Score store: 128 KB of LDS, so a context of up to kSeqScores / G positions;
+// it also keeps one block per CU (the blocks are as many as the CUs, and two on
+// one CU would leave another idle for the whole launch).
+constexpr int kSeqScores = 32768;
+// Waves per block and 16-byte loads in flight per lane, measured at 32 x 8
+// heads over 1000 / 2000 positions: 16 waves x 8 (four per SIMD, so one wave's
+// dependent score / weight arithmetic hides under the others') 26.1 / 46.0 us,
+// 8 x 16: 27.1 / 46.5, 8 x 32: 31.4 / 50.4, 12 x 16: 30.3 / 51.0. Four query
+// heads per kv head need 8 waves to keep the per-wave output rows in LDS.
+template <int G>
+struct SeqShape {
+  static constexpr int W = G <= 2 ? 16 : 8;
+  static constexpr int R = G <= 2 ? 8 : 16;
+  static constexpr int step = W * 4;   // positions per step (the score store's padding)
+};
+
+template <int G, int W = SeqShape<G>::W, int R = SeqShape<G>::R>
+__global__ __launch_bounds__(W * kWave) void attn_seq_kernel(const AttnArgs a, uint16_t* __restrict__ out) {
+  constexpr int kSeqThreads = W * kWave;
+  constexpr int kSeqStep = W * 4;
+  constexpr int kSeqRing = R;
+  constexpr int kSeqWaves = W;
+  __shared__ float sc[kSeqScores];   // [G][npos] scores of the context
+  __shared__ float qs[G][D];
+  __shared__ float knew[D];
+  __shared__ float vnew[D];
+  __shared__ float obuf[W][G][D];
+  __shared__ float red[2][W][G];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  const int slot = lane >> 4;
+  const int dc = lane & 15;
+  const int kvh = blockIdx.x;
+  const int b = blockIdx.y;
+  const int t = threadIdx.x;
+  const int KN = a.hkv * D;
+  uint16_t* kc = a.kc + b * a.cache_bstride;
+  uint16_t* vc = a.vc + b * a.cache_bstride;
+  uint16_t* ob = out + static_cast<size_t>(b) * a.hq * D + static_cast<size_t>(kvh) * G * D;
+
+  int last = a.wr[b];
+  int p = a.pos[b];
+  if (last < 0 || last >= a.cap) {
+    if (kvh == 0 && t == 0) set_err(a.err, 4);
+    for (int e = t; e < G * D; e += kSeqThreads) ob[e] = 0;
+    return;   // block-uniform: no barrier has been reached
+  }
+  if (p < 0 || p >= a.mp_rows) {
+    if (kvh == 0 && t == 0) set_err(a.err, 5);
+    p = 0;
+  }
+  const int n = last + 1;
+  const int nst = (n + kSeqStep - 1) / kSeqStep;   // steps per pass
+  const int npos = nst * kSeqStep;
+  const int nch = 2 * nst;                         // K steps, then V steps
+  const int pw = wid * 4 + slot;                   // this lane's position within a step
+
+  // 1. the prologue's raw heads (wave hh < G: query head kvh*G + hh; G: key; G+1: value)
+  //    and the rope row, ahead of the cache stream (loads complete in issue order)
+  const int rows = (a.hq + 2 * a.hkv) * D;
+  const size_t kstride = static_cast<size_t>(rows) * gridDim.y;   // partials are [ks, B, rows]
+  const float* psrc = a.part + static_cast<size_t>(b) * rows;
+  float x0 = 0.f, x1 = 0.f;
+  if (wid < G + 2) {
+    const int off = wid < G ? (kvh * G + wid) * D : wid == G ? (a.hq + kvh) * D : (a.hq + a.hkv + kvh) * D;
+    head_raw(nullptr, psrc + off, a.part_ks, kstride, lane, x0, x1);
+  }
+  const float c0 = bf2f(a.cos_t[static_cast<size_t>(p) * D + lane]);
+  const float s0 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane]);
+  const float c1 = bf2f(a.cos_t[static_cast<size_t>(p) * D + lane + 64]);
+  const float s1 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane + 64]);
+
+  // chunk c < nst: key step c; else value step c - nst. Positions past the
+  // context read row n - 1 (in bounds) and are never used.
+  auto chunk_ptr = [&](int c) -> const uint16_t* {
+    const bool isv = c >= nst;
+    const int pi = min((isv ? c - nst : c) * kSeqStep + pw, n - 1);
+    return (isv ? vc : kc) + static_cast<size_t>(pi) * KN + kvh * D + 8 * dc;
+  };
+  uint4 ring[kSeqRing];
+#pragma unroll
+  for (int r = 0; r < kSeqRing; ++r) ring[r] = ld16_stream(chunk_ptr(min(r, nch - 1)));
+
+  // 2. the prep's arithmetic while the first cache loads are in flight
+  if (wid < G + 2) {
+    if (wid <= G) {
+      float o0, o1;
+      norm_rope_head(x0, x1, wid < G ? a.gq : a.gk, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
+      if (wid < G) {
+        qs[wid][lane] = o0;
+        qs[wid][lane + 64] = o1;
+      } else {
+        knew[lane] = o0;
+        knew[lane + 64] = o1;
+        uint16_t* dst = kc + static_cast<size_t>(last) * KN + kvh * D;
+        dst[lane] = static_cast<uint16_t>(f2bf(o0));
+        dst[lane + 64] = static_cast<uint16_t>(f2bf(o1));
+      }
+    } else {
+      vnew[lane] = x0;
+      vnew[lane + 64] = x1;
+      uint16_t* dst = vc + static_cast<size_t>(last) * KN + kvh * D;
+      dst[lane] = static_cast<uint16_t>(f2bf(x0));
+      dst[lane + 64] = static_cast<uint16_t>(f2bf(x1));
+    }
+  }
+  lds_barrier();
+  // the query as packed bf16 pairs (its values are bf16 already): scores are
+  // v_dot2 products of the raw key rows, no unpacking
+  uint32_t qp[G][4];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const uint4 q4 = pack8(&qs[g][8 * dc]);
+    qp[g][0] = q4.x;
+    qp[g][1] = q4.y;
+    qp[g][2] = q4.z;
+    qp[g][3] = q4.w;
+  }
+  const uint4 knp = pack8(&knew[8 * dc]);
+  const uint4 vnp = pack8(&vnew[8 * dc]);
+  const int clast = last / kSeqStep;   // the step holding the new slot
+
+  float mloc[G], M[G], ls[G], o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    mloc[g] = -INFINITY;
+    M[g] = 0.f;
+    ls[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[g][i] = 0.f;
+  }
+
+  // 3. the stream: scores (keys); then the block max and every weight of the
+  //    wave's positions at once (lane-parallel over positions, not per row);
+  //    then P.V (values). The chunk count is padded to whole ring rounds and
+  //    every refill is issued (past the last chunk it re-reads that chunk;
+  //    padding chunks are value steps past the context, weight 0), so the loop
+  //    body is straight-line and each use waits only for its own load.
+  const int nrounds = (nch + kSeqRing - 1) / kSeqRing;
+  for (int rd = 0; rd < nrounds; ++rd) {
+#pragma unroll
+    for (int r = 0; r < kSeqRing; ++r) {
+      const int c = rd * kSeqRing + r;
+      uint4 v = ring[r];
+      ring[r] = ld16_stream(chunk_ptr(min(c + kSeqRing, nch - 1)));
+      if (c < nst) {
+        const int pi = c * kSeqStep + pw;
+        if (c == clast && pi == last) v = knp;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float d = dot2_bf16(qp[g][0], v.x, 0.f);
+          d = dot2_bf16(qp[g][1], v.y, d);
+          d = dot2_bf16(qp[g][2], v.z, d);
+          d = dot2_bf16(qp[g][3], v.w, d);
+          d = row16_sum(d) * a.scale;
+          if (pi < n) {
+            mloc[g] = fmaxf(mloc[g], d);
+            if (dc == 0) sc[g * npos + pi] = d;
+          }
+        }
+        if (c == nst - 1) {   // every score is in: the block max, then the weights
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float mx = rows4_max(mloc[g]);
+            if (lane == 0) red[0][wid][g] = mx;
+          }
+          lds_barrier();
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            float mx = red[0][0][g];
+#pragma unroll
+            for (int w = 1; w < kSeqWaves; ++w) mx = fmaxf(mx, red[0][w][g]);
+            M[g] = mx;
+          }
+          // this wave's positions 32 s + 4 wid + q, lane-parallel: e in f32 into
+          // the denominator, the bf16 weight back over the score (0 past the context)
+          for (int j = lane; j < 4 * nst; j += kWave) {
+            const int pj = (j >> 2) * kSeqStep + 4 * wid + (j & 3);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              const float e = pj < n ? __builtin_amdgcn_exp2f((sc[g * npos + pj] - M[g]) * kLog2e) : 0.f;
+              ls[g] += e;
+              sc[g * npos + pj] = round_bf(e);
+            }
+          }
+        }
+      } else {
+        const int pi = (c - nst) * kSeqStep + pw;
+        if (c == nst + clast && pi == last) v = vnp;
+        float vf[8];
+        unpack8(v, vf);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float wgt = pi < n ? sc[g * npos + min(pi, n - 1)] : 0.f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[g][i] = fmaf(wgt, vf[i], o[g][i]);
+        }
+      }
+    }
+  }
+
+  // 4. the four position slots of a wave (row swaps), then the waves in order
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float lw = wave_sum(ls[g]);   // the wave's positions sit one per lane
+    if (lane == 0) red[1][wid][g] = lw;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[g][i] = rows4_sum(o[g][i]);
+  }
+  if (slot == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) obuf[wid][g][8 * dc + i] = o[g][i];
+  }
+  lds_barrier();
+  for (int e = t; e < G * D; e += kSeqThreads) {
+    const int g = e / D, d = e % D;
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSeqWaves; w += 2) {
+      num += obuf[w][g][d] + obuf[w + 1][g][d];
+      den += red[1][w][g] + red[1][w + 1][g];
+    }
+    ob[e] = static_cast<uint16_t>(f2bf(num / den));
+  }
+}
+
+template <int G>
+int launch_attn_seq_g(const AttnArgs& a, int batch, hipStream_t st) {
+  using S = SeqShape<G>;
+  if (static_cast<int64_t>(a.cap + S::step) * G > kSeqScores)
+    return fail(TFA_ERR_SHAPE, "tfa_decode_attention_seq: cache of %d slots exceeds %d positions for group %d",
+                a.cap, kSeqScores / G - S::step, G);
+  attn_seq_kernel<G><<<dim3(a.hkv, batch), S::W * kWave, 0, st>>>(a, a.out);
+  return launched("attn_seq");
 }
 
 template <int G>
@@ -662,6 +921,52 @@ int tfa_decode_attention(const void* q, const float* qkv_part, int64_t part_ks,
     case 4: return launch_attn_g<4>(a, (int)split, B, stream);
     case 8: return launch_attn_g<8>(a, (int)split, B, stream);
     default: return fail(TFA_ERR_SHAPE, "tfa_decode_attention: group %lld not in {1,2,4,8}", (long long)(hq / hkv));
+  }
+}
+
+int tfa_decode_attention_seq(const float* qkv_part, int64_t part_ks, const void* gamma_q,
+                             const void* gamma_k, float eps_head, const void* cos_t, const void* sin_t,
+                             int64_t rope_rows, void* k_cache, void* v_cache, const int* pos, const int* wr,
+                             int64_t batch, int64_t hq, int64_t hkv, int64_t head_dim, int64_t cap, float scale,
+                             void* out, int* err, hipStream_t stream) {
+  if (!qkv_part || !gamma_q || !gamma_k || !cos_t || !sin_t || !k_cache || !v_cache || !pos || !wr || !out)
+    return fail(TFA_ERR_NULL, "tfa_decode_attention_seq: null pointer argument");
+  if (head_dim != D) return fail(TFA_ERR_SHAPE, "tfa_decode_attention_seq: head_dim %lld, only 128 supported", (long long)head_dim);
+  if (hkv <= 0 || hq % hkv != 0)
+    return fail(TFA_ERR_SHAPE, "tfa_decode_attention_seq: hq %lld not a multiple of hkv %lld", (long long)hq, (long long)hkv);
+  if (cap <= 0 || rope_rows <= 0) return fail(TFA_ERR_SHAPE, "tfa_decode_attention_seq: empty cache or rope table");
+  if (batch < 1 || batch > 65535) return fail(TFA_ERR_SHAPE, "tfa_decode_attention_seq: batch %lld out of range", (long long)batch);
+  if (part_ks < 1 || part_ks > kMaxSplitsK)
+    return fail(TFA_ERR_SHAPE, "tfa_decode_attention_seq: part_ks %lld not in [1, %d]", (long long)part_ks, kMaxSplitsK);
+  if (!aligned16(k_cache) || !aligned16(v_cache))
+    return fail(TFA_ERR_ALIGN, "tfa_decode_attention_seq: caches not 16-byte aligned");
+  AttnArgs a{};
+  a.part = qkv_part;
+  a.part_ks = (int)part_ks;
+  a.cache_bstride = static_cast<size_t>(cap) * hkv * D;
+  a.gq = static_cast<const uint16_t*>(gamma_q);
+  a.gk = static_cast<const uint16_t*>(gamma_k);
+  a.eps_head = eps_head;
+  a.cos_t = static_cast<const uint16_t*>(cos_t);
+  a.sin_t = static_cast<const uint16_t*>(sin_t);
+  a.mp_rows = (int)rope_rows;
+  a.kc = static_cast<uint16_t*>(k_cache);
+  a.vc = static_cast<uint16_t*>(v_cache);
+  a.pos = pos;
+  a.wr = wr;
+  a.out = static_cast<uint16_t*>(out);
+  a.err = err;
+  a.hq = (int)hq;
+  a.hkv = (int)hkv;
+  a.cap = (int)cap;
+  a.scale = scale;
+  const int B = (int)batch;
+  switch (hq / hkv) {
+    case 1: return launch_attn_seq_g<1>(a, B, stream);
+    case 2: return launch_attn_seq_g<2>(a, B, stream);
+    case 4: return launch_attn_seq_g<4>(a, B, stream);
+    default:
+      return fail(TFA_ERR_SHAPE, "tfa_decode_attention_seq: group %lld not in {1,2,4}", (long long)(hq / hkv));
   }
 }
 

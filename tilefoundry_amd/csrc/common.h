@@ -55,6 +55,14 @@ TFA_DEV uint4 pack8(const float* f) {
   return v;
 }
 
+// a.lo * b.lo + a.hi * b.hi + c over packed bf16 pairs (v_dot2_f32_bf16; a
+// bf16 x bf16 product is exact in f32)
+TFA_DEV float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                         false);
+}
+
 TFA_DEV uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 // Streaming load for data read exactly once (weights, KV cache): non-temporal
 // hint so it does not evict reusable lines from L2 / MALL.

@@ -765,6 +765,35 @@ void qk_rope_cache(const Tensor& part, const Tensor& gamma_q, const Tensor& gamm
                                  hkv, D, opt_ptr_t<int>(err), stream_of(part)));
 }
 
+void decode_attention_seq(const Tensor& part, const Tensor& gamma_q, const Tensor& gamma_k, double eps,
+                          const Tensor& cos_t, const Tensor& sin_t, const Tensor& pos, const Tensor& wr,
+                          const Tensor& k_cache, const Tensor& v_cache, int64_t hq, int64_t hkv, double scale,
+                          const Tensor& out, const OptT& err) {
+  const int64_t D = 128;
+  need(pos, "Pos", I32);
+  const int64_t B = pos.numel();
+  need(wr, "Wr", I32, B);
+  need(part, "P", F32);
+  const int64_t per = B * (hq + 2 * hkv) * D;
+  if (part.numel() % per != 0) bad("P: expected (SK, [batch,] (HQ + 2 HKV) * 128)");
+  need(gamma_q, "Gq", BF, D);
+  need(gamma_k, "Gk", BF, D);
+  need(cos_t, "Cos", BF);
+  need(sin_t, "Sin", BF, cos_t.numel());
+  if (cos_t.dim() != 2 || cos_t.size(1) != D) bad("Cos: expected (MP, 128)");
+  need(k_cache, "Kc", BF);
+  need(v_cache, "Vc", BF, k_cache.numel());
+  if (k_cache.numel() % (B * hkv * D) != 0) bad("Kc: size is not a multiple of batch*HKV*128");
+  const int64_t cap = k_cache.numel() / (B * hkv * D);
+  need(out, "O", BF, B * hq * D);
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_decode_attention_seq(part.data_ptr<float>(), part.numel() / per, gamma_q.data_ptr(),
+                                        gamma_k.data_ptr(), (float)eps, cos_t.data_ptr(), sin_t.data_ptr(),
+                                        cos_t.size(0), k_cache.data_ptr(), v_cache.data_ptr(),
+                                        pos.data_ptr<int>(), wr.data_ptr<int>(), B, hq, hkv, D, cap,
+                                        (float)scale, out.data_ptr(), opt_ptr_t<int>(err), stream_of(part)));
+}
+
 void rope_attend(const Tensor& q_up, const Tensor& kv_up, const Tensor& k_rope, const Tensor& cos_t,
                  const Tensor& sin_t, const Tensor& pos, const Tensor& k_cache, const Tensor& v_cache,
                  const Tensor& ctx, const Tensor& scale, int64_t heads, int64_t nope, int64_t rope,
@@ -854,6 +883,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("silu_mul", &silu_mul);
   m.def("embed", &embed);
   m.def("qk_rope_cache", &qk_rope_cache);
+  m.def("decode_attention_seq", &decode_attention_seq);
   m.def("rope_attend_splits", [](int64_t cap) { return tfa_rope_attend_splits(cap); });
   m.def("rope_attend", &rope_attend);
 }

@@ -461,14 +461,15 @@ class BatchEngine:
 
     Every projection is a skinny bf16-MFMA GEMM over the batch (the weights are
     streamed once per step for all sequences); each sequence has its own KV
-    cache, position and prompt. One step is 9 launches per layer plus 3:
+    cache, position and prompt. One step is 7 launches per layer plus 3 when
+    the sequences x kv heads fill the device (``attention="seq"``):
 
         rows_norm        embedding gather + input norm (once)
         skinny_gemm      q|k|v projection -> f32 split-K partials
-        qk_rope_cache    sums the partials, q/k head norm + RoPE, writes the new
-                         K and V rows and the prepared query
-        decode_attention split-KV attention per sequence over the cache
-        attn_combine     merge of the splits
+        decode_attention_seq
+                         per (sequence, kv head) one block over the whole
+                         context: sums the partials, q/k head norm + RoPE,
+                         writes the new K and V rows, attends, lands o / l
         skinny_gemm      o_proj -> split-K partials
         rows_norm        residual add + post-attention norm
         skinny_gemm      gate|up + SwiGLU
@@ -476,16 +477,25 @@ class BatchEngine:
         rows_norm        residual add + next input norm (final norm after the last layer)
         skinny_gemm      head -> per 16-row group winners per sequence
         batch_sample     greedy step per sequence
+
+    With fewer blocks than that (``attention="split"``) the attention is three
+    launches: ``qk_rope_cache`` (the prepared query, once per sequence),
+    split-KV ``decode_attention`` and ``attn_combine``. ``"auto"`` picks the
+    whole-context form from 256 (sequence, kv head) pairs up.
     """
 
     MAX_BATCH = 32
+    SEQ_GROUPS = (1, 2, 4)   # query heads per kv head the whole-context attention takes
+    SEQ_SCORES = 32768       # its per-block score store: group x (cache + 64) at most
 
     def __init__(self, cfg: Qwen3Config = QWEN3_1_7B, *, batch: int = 32, device="cuda:0",
                  max_new: int = 2048, prompt_room: int = 512, weights: dict | None = None,
                  seed: int = 0, split: int = 128, ks_qkv: int = 2, ks_o: int = 4, ks_down: int = 4,
-                 capture: bool = True, prompt_prefill: bool = False):
+                 capture: bool = True, prompt_prefill: bool = False, attention: str = "auto"):
         if not 1 <= batch <= self.MAX_BATCH:
             raise ValueError(f"batch {batch} not in [1, {self.MAX_BATCH}]")
+        if attention not in ("auto", "seq", "split"):
+            raise ValueError(f"attention {attention!r} not in ('auto', 'seq', 'split')")
         self.cfg = cfg
         self.batch = batch
         self.device = torch.device(device)
@@ -495,6 +505,14 @@ class BatchEngine:
         self.nsteps = max_new + prompt_room
         self.cap = ((self.nsteps + split - 1) // split) * split
         self.ns = self.cap // split
+        group = cfg.heads // cfg.kv_heads
+        seq_ok = group in self.SEQ_GROUPS and (self.cap + 64) * group <= self.SEQ_SCORES
+        if attention == "seq" and not seq_ok:
+            raise ValueError(f"attention='seq' needs a group in {self.SEQ_GROUPS} and a cache of at most "
+                             f"{self.SEQ_SCORES // max(group, 1) - 64} slots (group {group}, cache {self.cap})")
+        if attention == "auto":
+            attention = "seq" if seq_ok and batch * cfg.kv_heads >= 256 else "split"
+        self.attention = attention
         if weights is None:
             weights = synthetic_weights(cfg, seed, self.device)
         self.embed, self.gamma_final, self.layers, self.head = pack_weights(cfg, weights, self.device)
@@ -547,13 +565,18 @@ class BatchEngine:
         for i, w in enumerate(self.layers):
             C.skinny_gemm(self.xn, w["w_qkv"], self.ks["qkv"], 0, self.qkv_part, None, None, None,
                           None)
-            # the query prepared once per sequence, not once per split block
-            C.qk_rope_cache(self.qkv_part, w["gamma_q"], w["gamma_k"], cfg.eps, self.cos, self.sin,
-                            self.pos, self.pos, self.kc[i], self.vc[i], self.q, HQ, HKV, self.err)
-            C.decode_attention(self.q, None, None, None, 0.0, None, None, self.kc[i], self.vc[i], None,
-                               self.pos, HQ, HKV, self.split, cfg.scale, self.op, self.mp, self.lp,
-                               False, self.err)
-            C.attn_combine(self.op, self.mp, self.lp, self.attn, self.pos, self.split)
+            if self.attention == "seq":
+                C.decode_attention_seq(self.qkv_part, w["gamma_q"], w["gamma_k"], cfg.eps, self.cos, self.sin,
+                                       self.pos, self.pos, self.kc[i], self.vc[i], HQ, HKV, cfg.scale, self.attn,
+                                       self.err)
+            else:
+                # the query prepared once per sequence, not once per split block
+                C.qk_rope_cache(self.qkv_part, w["gamma_q"], w["gamma_k"], cfg.eps, self.cos, self.sin,
+                                self.pos, self.pos, self.kc[i], self.vc[i], self.q, HQ, HKV, self.err)
+                C.decode_attention(self.q, None, None, None, 0.0, None, None, self.kc[i], self.vc[i], None,
+                                   self.pos, HQ, HKV, self.split, cfg.scale, self.op, self.mp, self.lp,
+                                   False, self.err)
+                C.attn_combine(self.op, self.mp, self.lp, self.attn, self.pos, self.split)
             C.skinny_gemm(self.attn, w["w_o"], self.ks["o"], 0, self.o_part, None, None, None, None)
             C.rows_norm(None, None, self.h, self.o_part, self.h1, w["gamma_post"], self.xn, cfg.eps,
                         self.err)
