@@ -249,6 +249,19 @@ int tfa_attn_combine(const float* op, const float* mp, const float* lp, void* ou
                      int64_t batch, int64_t hq, int64_t head_dim, const int* wr, int64_t split,
                      hipStream_t stream);
 
+/* One sequence's split merge folded into the o_proj GEMV with its residual:
+ * a = merge of op [splits, hq, 128] / mp / lp [splits, hq] exactly as
+ * tfa_attn_combine (over the splits holding slots 0..wr[0] when wr != NULL),
+ * y[r] = bf16(residual[r] + bf16(a . w_o[r])) for w_o [n, hq * 128] -- bit-identical
+ * to tfa_attn_combine followed by tfa_gemv_residual, in one launch. attn_out
+ * (nullable, bf16 [hq * 128]) receives a. hq a multiple of 4 in [4, 16];
+ * splits <= 64; n <= 2560.
+ * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:154-207 (gemv_attn_combine)
+ * with the residual add of examples/qwen3_1_7b-tilelang/ref_src/model.py:263. */
+int tfa_attn_combine_gemv_residual(const float* op, const float* mp, const float* lp, int64_t splits, int64_t hq,
+                                   int64_t head_dim, const int* wr, int64_t split, const void* w_o,
+                                   const void* residual, void* y, int64_t n, void* attn_out, hipStream_t stream);
+
 /* Reduce the q|k|v split-K partials qkv_part [part_ks (<= 8), batch,
  * (hq + 2 hkv) * 128] f32 (each value landing in bf16); per query head
  * Qwen3RMSNorm (gamma_q, eps_head) + rotate-half RoPE at pos[b] -> q_out

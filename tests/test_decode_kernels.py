@@ -336,3 +336,48 @@ def test_attention_neutral_partials_and_full_combine(dev):
     full = ops.attn_combine(op, mp, lp)
     active = ops.attn_combine(op, mp, lp, wr=n - 1, split=256)
     assert_equal("combine over all == over active", full, active)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hq,n,ns,wr", [(16, 2048, 1, 0), (16, 2048, 17, 1050), (16, 2048, 33, 2100),
+                                        (16, 2048, 64, 4095), (16, 2048, 64, 1000), (8, 1000, 40, 2000),
+                                        (4, 96, 5, None)])
+def test_attn_combine_gemv_residual_bit_equal(dev, hq, n, ns, wr):
+    """The split merge folded into o_proj equals attn_combine followed by
+    gemv_residual bit for bit: the merged vector and y, with stale splits past
+    the write slot (never read into the result), ragged rows and small heads."""
+    from tilefoundry_amd._lib import C
+
+    g = gen(51 + ns + hq)
+    split = 64
+    op = torch.randn(ns, hq, D, generator=g).to(dev)
+    mp = (3.0 * torch.randn(ns, hq, generator=g)).to(dev)
+    lp = (1.0 + torch.rand(ns, hq, generator=g) * 60).to(dev)
+    w_o = randn(n, hq * D, g=g, std=0.02).to(dev)
+    res = randn(n, g=g).to(dev)
+    wrd = None if wr is None else torch.tensor([wr], dtype=torch.int32, device=dev)
+    attn = torch.empty(hq * D, dtype=BF, device=dev)
+    C.attn_combine(op, mp, lp, attn, wrd, split)
+    want = torch.empty(n, dtype=BF, device=dev)
+    C.gemv_residual(attn, w_o, res, None, want)
+    got = torch.empty(n, dtype=BF, device=dev)
+    a2 = torch.empty(hq * D, dtype=BF, device=dev)
+    C.attn_combine_gemv_residual(op, mp, lp, wrd, split, w_o, res, got, a2)
+    assert_equal("merged attention", a2, attn)
+    assert_equal("o_proj + residual", got, want)
+
+
+@pytest.mark.gpu
+def test_attn_combine_gemv_residual_refuses(dev):
+    from tilefoundry_amd._lib import C
+
+    op = torch.zeros(65, 16, D, device=dev)
+    mp = torch.zeros(65, 16, device=dev)
+    w_o = torch.zeros(2048, 16 * D, dtype=BF, device=dev)
+    h = torch.zeros(2048, dtype=BF, device=dev)
+    with pytest.raises(ValueError, match="splits"):
+        C.attn_combine_gemv_residual(op, mp, mp, None, 64, w_o, h, h.clone(), None)
+    w_big = torch.zeros(4096, 16 * D, dtype=BF, device=dev)
+    h4 = torch.zeros(4096, dtype=BF, device=dev)
+    with pytest.raises(ValueError, match="2560"):
+        C.attn_combine_gemv_residual(op[:8], mp[:8], mp[:8], None, 64, w_big, h4, h4.clone(), None)

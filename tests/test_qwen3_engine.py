@@ -96,6 +96,20 @@ def test_engine_logits_small(dev):
 
 
 @pytest.mark.gpu
+def test_engine_fused_o_proj_is_bit_identical(dev):
+    """The step with the split merge folded into o_proj gives the same logits,
+    bit for bit, as the step with attn_combine and gemv_residual apart."""
+    from tilefoundry_amd.qwen3 import Engine
+
+    cfg, wts = _small()
+    prompt = OQ.prompt_ids(cfg.vocab, 70, seed=3)[0]   # 70 positions: two splits of 64
+    fused = Engine(cfg, device=dev, max_new=16, prompt_room=80, weights=wts, fuse_o=True)
+    apart = Engine(cfg, device=dev, max_new=16, prompt_room=80, weights=wts)
+    assert fused.fuse_o and not apart.fuse_o
+    assert torch.equal(fused.logits_for(prompt), apart.logits_for(prompt))
+
+
+@pytest.mark.gpu
 def test_engine_greedy_small(dev):
     """Teacher-forced along the oracle's own greedy ids, every pick equals the
     oracle's except at near ties under the measured logit error; the free run

@@ -759,6 +759,160 @@ __global__ __launch_bounds__(256) void attn_combine_d128_kernel(const float* op,
   }
 }
 
+// combine_gemv: the split merge folded into the o_proj GEMV with its residual,
+// for one sequence, hq <= 16 heads of 128 (K = hq * 128 <= 2048). A block of 16
+// waves owns 8 RPW output rows. Every load is issued first: each wave's chunk
+// of its rows' weights (wave (quarter q, pair group pg): 16-byte chunk `lane` of
+// quarter q of RPW row pairs), then for wave h < hq its head's split statistics
+// (lane s: split s) and its lane's two dims of the first kCgRound splits'
+// partial rows. The merge is attn_combine_d128's arithmetic exactly -- the max
+// over the active splits, e = expf(m - max), splits summed by fmaf in groups
+// s % 8 (in s order within a group, the groups in order), one landing of
+// num / den -- with each split's e and l broadcast by readlane; the merged
+// vector goes to LDS (and, from block 0, to attn_out). The product is
+// gemv_rows_kernel's for 2-row blocks exactly: per row pair one quarter per
+// wave, one 16-byte chunk per lane, the wave's two-row transposed reduction,
+// quarters summed (0 + 1) + (2 + 3), y = bf16(res + bf16(sum)). So the result
+// is bit-identical to attn_combine followed by gemv_residual, one launch fewer.
+// Every block re-reads the partials, 16 x (128 + 2) floats per split; more than
+// kCgMaxSplits splits are refused (two launches). Measured in the Qwen3-1.7B
+// bs=1 step (contexts 64..2112): 905 tok/s against 961 for the two launches with
+// 8-row blocks, 897 / 846 with 16 / 32 rows -- the per-CU re-read costs more
+// than the launch it saves, so the engine keeps two launches by default.
+// Replaces examples/qwen3_1_7b-tilelang/fast/kernels.py:154-207 (gemv_attn_combine)
+// with the residual add of ref_src/model.py:263.
+constexpr int kCgWaves = 16;
+constexpr int kCgThreads = kCgWaves * kWave;
+constexpr int kCgMaxSplits = 64;   // one split's statistics per lane
+constexpr int kCgRound = 32;       // splits whose partial rows are in flight at once
+
+template <int RPW>
+__global__ __launch_bounds__(kCgThreads) void combine_gemv_kernel(
+    const float* op, const float* mp, const float* lp, int ns, int hq, const int* wr, int split,
+    const uint16_t* __restrict__ w, const uint16_t* __restrict__ res, uint16_t* __restrict__ y, int N,
+    uint16_t* attn_out) {
+  constexpr int RB = 8 * RPW;
+  __shared__ float xs[16 * D];
+  __shared__ float red[4][4][RPW][2];   // [pair group][quarter][pair][row of the pair]
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wid = t / kWave;
+  const int K = hq * D;
+  const int kq = K / 4;
+  const int q = wid & 3, pg = wid >> 2;
+  const int row0 = blockIdx.x * RB;
+  const bool cvalid = 8 * lane < kq;
+
+  // 1. the weights, the residual, the write slot, then the merge operands --
+  //    every load unconditional at an in-bounds address (rows, chunks, heads
+  //    and splits clamped; what they bring past the shape is never used), so
+  //    they all go out before the first wait
+  const int cl = min(lane, kq / 8 - 1);
+  uint4 wv[RPW][2];
+#pragma unroll
+  for (int p = 0; p < RPW; ++p)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int row = min(row0 + (pg * RPW + p) * 2 + r, N - 1);
+      wv[p][r] = ld16_stream(w + static_cast<size_t>(row) * K + q * kq + 8 * cl);
+    }
+  const float rv = bf2f(res[min(row0 + min(t, RB - 1), N - 1)]);
+  const int wslot = wr ? wr[0] : 0;
+  const int h = min(wid, hq - 1);
+  const bool merger = wid < hq;
+  const int sl = min(lane, ns - 1);
+  const float m_l = mp[sl * hq + h];
+  const float l_l = lp[sl * hq + h];
+  float2 o[kCgRound];
+#pragma unroll
+  for (int s = 0; s < kCgRound; ++s)
+    o[s] = *reinterpret_cast<const float2*>(op + (static_cast<size_t>(min(s, ns - 1)) * hq + h) * D + 2 * lane);
+
+  // 2. the merge (wave h: dims 2 lane, 2 lane + 1 of head h)
+  if (merger) {
+    int nact = ns;
+    if (wr) {
+      nact = wslot < 0 ? 0 : wslot / split + 1;
+      if (nact > ns) nact = ns;
+    }
+    const bool act = lane < nact;
+    const float M = wave_max(act ? m_l : -INFINITY);
+    const float e_l = act ? expf(m_l - M) : 0.f;
+    float n0[8], n1[8], dg[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) n0[g] = n1[g] = dg[g] = 0.f;
+    auto take = [&](int s, float2 v) __attribute__((always_inline)) {
+      const float es = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e_l), s));
+      const float ls = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_l), s));
+      n0[s & 7] = fmaf(v.x, es, n0[s & 7]);
+      n1[s & 7] = fmaf(v.y, es, n1[s & 7]);
+      dg[s & 7] = fmaf(ls, es, dg[s & 7]);
+    };
+#pragma unroll
+    for (int s = 0; s < kCgRound; ++s)
+      if (s < nact) take(s, o[s]);
+    if (nact > kCgRound) {   // wave-uniform: a second round of partial rows
+#pragma unroll
+      for (int s = 0; s < kCgRound; ++s)
+        o[s] = *reinterpret_cast<const float2*>(
+            op + (static_cast<size_t>(min(kCgRound + s, ns - 1)) * hq + h) * D + 2 * lane);
+#pragma unroll
+      for (int s = 0; s < kCgRound; ++s)
+        if (kCgRound + s < nact) take(kCgRound + s, o[s]);
+    }
+    float tn0 = 0.f, tn1 = 0.f, td = 0.f;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      tn0 += n0[g];
+      tn1 += n1[g];
+      td += dg[g];
+    }
+    const uint32_t a0 = f2bf(tn0 / td), a1 = f2bf(tn1 / td);
+    xs[h * D + 2 * lane] = bf2f(a0);
+    xs[h * D + 2 * lane + 1] = bf2f(a1);
+    if (attn_out && blockIdx.x == 0)
+      *reinterpret_cast<uint32_t*>(attn_out + h * D + 2 * lane) = a0 | (a1 << 16);
+  }
+  lds_barrier();
+
+  // 3. the product: wave (q, pg), row pairs pg * RPW + p
+  float xf[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) xf[i] = cvalid ? xs[q * kq + 8 * cl + i] : 0.f;
+#pragma unroll
+  for (int p = 0; p < RPW; ++p) {
+    float acc[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      float f[8];
+      unpack8(cvalid ? wv[p][r] : make_uint4(0, 0, 0, 0), f);
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s = fmaf(xf[i], f[i], s);
+      acc[r] = s;
+    }
+    const float tot = wave_sum_rows<2>(acc, lane);
+    if ((lane & (kWave / 2 - 1)) == 0) red[pg][q][p][wave_rows_owner<2>(lane)] = tot;
+  }
+  lds_barrier();
+  if (t < RB && row0 + t < N) {
+    const int pr = t >> 1, rr = t & 1;
+    const int g = pr / RPW, p = pr % RPW;
+    const float v = (red[g][0][p][rr] + red[g][1][p][rr]) + (red[g][2][p][rr] + red[g][3][p][rr]);
+    y[row0 + t] = static_cast<uint16_t>(f2bf(rv + round_bf(v)));
+  }
+}
+
+template <int RPW>
+int launch_combine_gemv(const float* op, const float* mp, const float* lp, int ns, int hq, const int* wr, int split,
+                        const void* w_o, const void* residual, void* y, int n, void* attn_out, hipStream_t stream) {
+  const unsigned blocks = static_cast<unsigned>((n + 8 * RPW - 1) / (8 * RPW));
+  combine_gemv_kernel<RPW><<<blocks, kCgThreads, 0, stream>>>(
+      op, mp, lp, ns, hq, wr, split, static_cast<const uint16_t*>(w_o), static_cast<const uint16_t*>(residual),
+      static_cast<uint16_t*>(y), n, static_cast<uint16_t*>(attn_out));
+  return launched("attn_combine_gemv_residual");
+}
+
 // qk_rope_cache: one wave per head of the [q | k | v] projection, summed from
 // its split-K partials [ks, B, (hq + 2 hkv) * 128] and landed in bf16. Query
 // heads get the per-head norm and RoPE at pos[b] and go to q_out; the key head
@@ -988,6 +1142,25 @@ int tfa_attn_combine(const float* op, const float* mp, const float* lp, void* ou
                                                          (int)splits, (int)hq, (int)head_dim, wr,
                                                          (int)split);
   return launched("attn_combine");
+}
+
+int tfa_attn_combine_gemv_residual(const float* op, const float* mp, const float* lp, int64_t splits, int64_t hq,
+                                   int64_t head_dim, const int* wr, int64_t split, const void* w_o,
+                                   const void* residual, void* y, int64_t n, void* attn_out, hipStream_t stream) {
+  if (!op || !mp || !lp || !w_o || !residual || !y)
+    return fail(TFA_ERR_NULL, "tfa_attn_combine_gemv_residual: null pointer argument");
+  if (head_dim != D) return fail(TFA_ERR_SHAPE, "tfa_attn_combine_gemv_residual: head_dim %lld, only 128 supported", (long long)head_dim);
+  if (hq < 4 || hq > kCgWaves || hq % 4 != 0)
+    return fail(TFA_ERR_SHAPE, "tfa_attn_combine_gemv_residual: hq %lld not a multiple of 4 in [4, %d]", (long long)hq, kCgWaves);
+  if (splits < 1 || splits > kCgMaxSplits)
+    return fail(TFA_ERR_SHAPE, "tfa_attn_combine_gemv_residual: %lld splits not in [1, %d]", (long long)splits, kCgMaxSplits);
+  if (wr && split <= 0) return fail(TFA_ERR_SHAPE, "tfa_attn_combine_gemv_residual: split must be positive with wr");
+  // up to 2560 rows the decode GEMV works in 2-row blocks, whose reduction this kernel repeats
+  if (n < 1 || n > 2560) return fail(TFA_ERR_SHAPE, "tfa_attn_combine_gemv_residual: n %lld not in [1, 2560]", (long long)n);
+  if (!aligned16(w_o) || !aligned16(op) || (attn_out && reinterpret_cast<uintptr_t>(attn_out) % 4 != 0))
+    return fail(TFA_ERR_ALIGN, "tfa_attn_combine_gemv_residual: w_o / op not 16-byte aligned");
+  return launch_combine_gemv<1>(op, mp, lp, (int)splits, (int)hq, wr, (int)split, w_o, residual, y, (int)n,
+                                attn_out, stream);
 }
 
 int tfa_qk_rope_cache(const float* qkv_part, int64_t part_ks, const void* gamma_q,

@@ -765,6 +765,27 @@ void qk_rope_cache(const Tensor& part, const Tensor& gamma_q, const Tensor& gamm
                                  hkv, D, opt_ptr_t<int>(err), stream_of(part)));
 }
 
+void attn_combine_gemv_residual(const Tensor& op, const Tensor& mp, const Tensor& lp, const OptT& wr, int64_t split,
+                                const Tensor& w_o, const Tensor& residual, const Tensor& y, const OptT& attn_out) {
+  const int64_t D = 128;
+  need(mp, "Mp", F32);
+  if (mp.dim() != 2) bad("Mp: expected (NS, HQ)");
+  const int64_t ns = mp.size(0), hq = mp.size(1);
+  need(op, "Op", F32, ns * hq * D);
+  need(lp, "Lp", F32, ns * hq);
+  if (wr) need(*wr, "wr", I32, 1);
+  if (w_o.dim() != 2) bad("w_o: expected a 2-D (N, HQ*128) weight");
+  const int64_t N = w_o.size(0);
+  need_mat(w_o, "w_o", N, hq * D);
+  need(residual, "residual", BF, N);
+  need(y, "y", BF, N);
+  if (attn_out) need(*attn_out, "attn_out", BF, hq * D);
+  raise_status(tfa_attn_combine_gemv_residual(op.data_ptr<float>(), mp.data_ptr<float>(), lp.data_ptr<float>(), ns,
+                                              hq, D, opt_ptr_t<const int>(wr), split, w_o.data_ptr(),
+                                              residual.data_ptr(), y.data_ptr(), N, opt_ptr_t<void>(attn_out),
+                                              stream_of(op)));
+}
+
 void decode_attention_seq(const Tensor& part, const Tensor& gamma_q, const Tensor& gamma_k, double eps,
                           const Tensor& cos_t, const Tensor& sin_t, const Tensor& pos, const Tensor& wr,
                           const Tensor& k_cache, const Tensor& v_cache, int64_t hq, int64_t hkv, double scale,
@@ -884,6 +905,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("embed", &embed);
   m.def("qk_rope_cache", &qk_rope_cache);
   m.def("decode_attention_seq", &decode_attention_seq);
+  m.def("attn_combine_gemv_residual", &attn_combine_gemv_residual);
   m.def("rope_attend_splits", [](int64_t cap) { return tfa_rope_attend_splits(cap); });
   m.def("rope_attend", &rope_attend);
 }

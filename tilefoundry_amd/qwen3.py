@@ -19,6 +19,10 @@ layers; the reference's TileLang step is 228):
                         attention partials
     attn_combine        log-sum-exp merge of the splits
     gemv_residual       o_proj + residual add
+
+(``fuse_o=True`` runs the merge and o_proj as one launch,
+``attn_combine_gemv_residual``, bit-identical; every one of its blocks re-reads
+the split partials, and the step measured 905 tok/s against 961 apart.)
     rmsnorm_gemv_swiglu post-attention norm + gate|up GEMV + SwiGLU
     gemv_residual       down_proj + residual add
     lm_head_argmax      final norm + head GEMV + per-block winners
@@ -247,7 +251,8 @@ class Engine:
 
     def __init__(self, cfg: Qwen3Config = QWEN3_1_7B, *, device="cuda:0", max_new: int = 2048,
                  prompt_room: int = 512, weights: dict | None = None, seed: int = 0,
-                 split: int = 64, capture: bool = True, prompt_prefill: bool = False):
+                 split: int = 64, capture: bool = True, prompt_prefill: bool = False,
+                 fuse_o: bool = False):
         self.cfg = cfg
         self.device = torch.device(device)
         self.split = split
@@ -255,6 +260,13 @@ class Engine:
         self.nsteps = max_new + prompt_room
         self.cap = ((self.nsteps + split - 1) // split) * split
         self.ns = self.cap // split
+        # the split merge folded into o_proj: up to 64 splits, 4..16 heads of 128, <= 2560 rows
+        fusable = (self.ns <= 64 and cfg.head_dim == 128 and cfg.heads % 4 == 0 and 4 <= cfg.heads <= 16
+                   and cfg.hidden <= 2560)
+        if fuse_o and not fusable:
+            raise ValueError(f"fuse_o needs <= 64 splits (cache {self.cap} / split {split}), 4..16 heads of 128 "
+                             f"and hidden <= 2560")
+        self.fuse_o = bool(fuse_o)
         if weights is None:
             weights = synthetic_weights(cfg, seed, self.device)
         self._pack(weights)
@@ -327,8 +339,12 @@ class Engine:
             C.decode_attention(self.qk, None, w["gamma_q"], w["gamma_k"], cfg.eps, self.cos,
                                self.sin, kc, vc, self.pos, self.pos, HQ, HKV, self.split,
                                cfg.scale, self.op, self.mp, self.lp, False, self.err)
-            C.attn_combine(self.op, self.mp, self.lp, self.attn, self.pos, self.split)
-            C.gemv_residual(self.attn, w["w_o"], self.hid, None, self.h1)
+            if self.fuse_o:
+                C.attn_combine_gemv_residual(self.op, self.mp, self.lp, self.pos, self.split, w["w_o"],
+                                             self.hid, self.h1, None)
+            else:
+                C.attn_combine(self.op, self.mp, self.lp, self.attn, self.pos, self.split)
+                C.gemv_residual(self.attn, w["w_o"], self.hid, None, self.h1)
             C.rmsnorm_gemv_swiglu(self.h1, w["gamma_post"], cfg.eps, w["w_gu"], self.act)
             C.gemv_residual(self.act, w["w_down"], self.h1, None, self.hid)
         C.lm_head_argmax(self.hid, self.gamma_final, cfg.eps, self.head, self.logits, self.bv,
