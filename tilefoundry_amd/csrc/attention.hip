@@ -219,27 +219,22 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
   //    the 16-lane DPP row sum every lane of a position's group holds its score.
   //    Reductions across the wave's four position slots use the gfx950 row
   //    swaps (no LDS round trip); the weights are exp2 of the scaled difference
-  float qf[G][8];
+  //    The query's values are bf16 (landed by the prep, or given so): packed in
+  //    pairs, each score is four v_dot2 products of the raw key row.
+  uint4 qp[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) qf[g][i] = qs[g][8 * dc + i];
+  for (int g = 0; g < G; ++g) qp[g] = pack8(&qs[g][8 * dc]);
   float sv[G][NIT];
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
     const int pi = start + it * 16 + wid * 4 + slot;
-    float kf[8];
-    if (has_new && pi == last) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) kf[i] = knew[8 * dc + i];
-    } else {
-      unpack8(kv[it], kf);
-    }
+    const uint4 kr = (has_new && pi == last) ? pack8(&knew[8 * dc]) : kv[it];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float d = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) d = fmaf(qf[g][i], kf[i], d);
+      float d = dot2_bf16(qp[g].x, kr.x, 0.f);
+      d = dot2_bf16(qp[g].y, kr.y, d);
+      d = dot2_bf16(qp[g].z, kr.z, d);
+      d = dot2_bf16(qp[g].w, kr.w, d);
       d = row16_sum(d);
       sv[g][it] = pi < n ? d * a.scale : -INFINITY;
     }
