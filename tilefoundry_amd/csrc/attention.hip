@@ -74,20 +74,78 @@ TFA_DEV void head_raw(const uint16_t* raw, const float* part, int ks, size_t kst
   }
 }
 
+// The same values, loaded now and landed later: a kernel issues these loads,
+// then its bulk loads, and only then lands them, so that its first wait covers
+// every small load at once (vector loads complete in issue order). Nothing
+// reads a loaded value before land(): a bf16 value stays in its 32-bit
+// register as loaded, split-K partials are summed as sum_splits does.
+template <bool PART>
+struct HeadRaw {
+  float v0[PART ? kMaxSplitsK : 1], v1[PART ? kMaxSplitsK : 1];
+  uint32_t r0 = 0, r1 = 0;
+  TFA_DEV void load(const uint16_t* raw, const float* part, int ks, size_t kstride, int lane) {
+    if constexpr (PART) {
+#pragma unroll
+      for (int s = 0; s < kMaxSplitsK; ++s) {
+        const size_t o = static_cast<size_t>(min(s, ks - 1)) * kstride;
+        v0[s] = part[o + lane];
+        v1[s] = part[o + lane + 64];
+      }
+    } else {
+      r0 = raw[lane];
+      r1 = raw[lane + 64];
+    }
+  }
+  // The partials count as read here (an empty asm that takes and returns each),
+  // so no part of their sum is moved up to the loads. (A bf16 value needs no
+  // pin: nothing but its widening reads it.)
+  TFA_DEV void pin() {
+    if constexpr (PART) {
+#pragma unroll
+      for (int s = 0; s < kMaxSplitsK; ++s) asm volatile("" : "+v"(v0[s]), "+v"(v1[s]));
+    }
+  }
+  TFA_DEV void land(int ks, float& x0, float& x1) {
+    pin();
+    if constexpr (PART) {
+      float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+      for (int s = 0; s < kMaxSplitsK; ++s) {
+        a0 += s < ks ? v0[s] : 0.f;
+        a1 += s < ks ? v1[s] : 0.f;
+      }
+      x0 = round_bf(a0);
+      x1 = round_bf(a1);
+    } else {
+      x0 = __uint_as_float(r0 << 16);
+      x1 = __uint_as_float(r1 << 16);
+    }
+  }
+};
+
+// How the split attention gets its query: prepared (normed, rotated) bf16;
+// fused from the raw [q | k] bf16 projection; fused from q|k|v split-K partials.
+enum { QM_PREPARED = 0, QM_RAW = 1, QM_PART = 2 };
+
 // Per-head Qwen3RMSNorm + rotate-half RoPE of one 128-wide head by one wave:
 // lane l owns d = l and its rotation partner d = l + 64.
-TFA_DEV void norm_rope_head(float x0, float x1, const uint16_t* gam, float eps, float c0, float s0,
-                            float c1, float s1, int lane, float& o0, float& o1) {
+TFA_DEV void norm_rope_head_g(float x0, float x1, float g0, float g1, float eps, float c0, float s0,
+                              float c1, float s1, float& o0, float& o1) {
   const float ss = wave_sum(x0 * x0 + x1 * x1);
   const float rs = rsqrt_rn(ss / static_cast<float>(D) + eps);
-  const float n0 = round_bf(round_bf(x0 * rs) * bf2f(gam[lane]));
-  const float n1 = round_bf(round_bf(x1 * rs) * bf2f(gam[lane + 64]));
+  const float n0 = round_bf(round_bf(x0 * rs) * g0);
+  const float n1 = round_bf(round_bf(x1 * rs) * g1);
   // rotate_half: first half pairs with -x[d + 64], second half with +x[d - 64]
   o0 = round_bf(__fadd_rn(__fmul_rn(n0, c0), __fmul_rn(-n1, s0)));
   o1 = round_bf(__fadd_rn(__fmul_rn(n1, c1), __fmul_rn(n0, s1)));
 }
 
-template <int G, int NIT>
+TFA_DEV void norm_rope_head(float x0, float x1, const uint16_t* gam, float eps, float c0, float s0,
+                            float c1, float s1, int lane, float& o0, float& o1) {
+  norm_rope_head_g(x0, x1, bf2f(gam[lane]), bf2f(gam[lane + 64]), eps, c0, s0, c1, s1, o0, o1);
+}
+
+template <int G, int NIT, int QM>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a) {
   constexpr int SS = 16 * NIT;
   __shared__ float qs[G][D];
@@ -113,8 +171,41 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
   float* mp = a.mp + static_cast<size_t>(b) * a.ns * a.hq;
   float* lp = a.lp + static_cast<size_t>(b) * a.ns * a.hq;
 
+  // 0. the loads that need nothing else, issued together: the write slot, the
+  //    rope position and (fused mode) the raw head values of this wave's prologue
+  //    items -- its query heads, the new key and (from partials) the new value,
+  //    loaded whether or not this split turns out to hold the new slot -- or
+  //    (prepared mode) the query. They complete in issue order, ahead of every
+  //    K / V load, and are landed only after those are issued: the first wait
+  //    covers them all, and the K / V loads go out one round trip after wr.
+  constexpr bool fused = QM != QM_PREPARED;
   int last = a.wr[b];
-  const int p_raw = a.gq != nullptr ? a.pos[b] : 0;   // issued beside wr: one round trip for both
+  const int p_raw = fused ? a.pos[b] : 0;
+  constexpr int kItems = (G + 2 + kWaves - 1) / kWaves;   // prologue items per wave: hh = wid + kWaves j
+  constexpr int kQPer = (G * D + kThreads - 1) / kThreads; // prepared query values per thread
+  const int rows = (a.hq + 2 * a.hkv) * D;   // q | k | v row width of the partials
+  const uint16_t* qsrc = a.q ? a.q + b * a.q_bstride : nullptr;
+  const float* psrc = a.part ? a.part + static_cast<size_t>(b) * rows : nullptr;
+  const size_t kstride = static_cast<size_t>(rows) * gridDim.z;  // partials are [ks, B, rows]
+  HeadRaw<QM == QM_PART> hr[kItems];
+  uint32_t gr0[kItems], gr1[kItems];   // the item's norm scale (query: gamma_q, key: gamma_k)
+  uint32_t qraw[kQPer];
+  if constexpr (fused) {
+#pragma unroll
+    for (int j = 0; j < kItems; ++j) {
+      // items past the value (and, without partials, the value itself: its row is
+      // already in the cache) load the key's values, never used
+      const int hh = min(wid + kWaves * j, QM == QM_PART ? G + 1 : G);
+      const int off = hh < G ? (kvh * G + hh) * D : hh == G ? (a.hq + kvh) * D : (a.hq + a.hkv + kvh) * D;
+      hr[j].load(QM == QM_RAW ? qsrc + off : nullptr, QM == QM_PART ? psrc + off : nullptr, a.part_ks, kstride, lane);
+      const uint16_t* gam = hh < G ? a.gq : a.gk;
+      gr0[j] = gam[lane];
+      gr1[j] = gam[lane + 64];
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < kQPer; ++u) qraw[u] = a.q[b * a.q_bstride + (kvh * G) * D + min(t + u * kThreads, G * D - 1)];
+  }
   if (last < 0 || last >= a.cap) {
     if (s == 0 && kvh == 0 && t == 0) set_err(a.err, 4);
     last = last < 0 ? -1 : a.cap - 1;
@@ -135,57 +226,49 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
     }
     return;
   }
-  const bool fused = a.gq != nullptr;
   const bool has_new = fused && last < start + SS;  // this split holds the newest slot
-  const bool new_v = has_new && a.part != nullptr;  // ... and also brings the new value row
-
-  // 1. the query's raw head values and its rope row (and, in the one block that
-  //    holds the newest slot, the new key / value) first: a few hundred bytes from
-  //    L2 that would otherwise complete only after the split's K / V (vector
-  //    loads complete in issue order), holding the prologue back by a whole
-  //    K / V round trip
+  const bool new_v = has_new && QM == QM_PART;      // ... and also brings the new value row
   const int nwork = fused ? G + (has_new ? 1 : 0) + (new_v ? 1 : 0) : 0;
-  constexpr int kItems = (G + 2 + kWaves - 1) / kWaves;   // prologue items per wave: hh = wid + kWaves j
-  float x0[kItems], x1[kItems];
-  float c0 = 0.f, s0 = 0.f, c1 = 0.f, s1 = 0.f;
-  if (fused) {
-    int p = p_raw;
-    if (p < 0 || p >= a.mp_rows) {
-      if (s == 0 && kvh == 0 && t == 0) set_err(a.err, 5);
-      p = 0;
-    }
-    const int rows = (a.hq + 2 * a.hkv) * D;   // q | k | v row width of the partials
-    const uint16_t* qsrc = a.q ? a.q + b * a.q_bstride : nullptr;
-    const float* psrc = a.part ? a.part + static_cast<size_t>(b) * rows : nullptr;
-    const size_t kstride = static_cast<size_t>(rows) * gridDim.z;  // partials are [ks, B, rows]
-#pragma unroll
-    for (int j = 0; j < kItems; ++j) {
-      const int hh = wid + kWaves * j;
-      x0[j] = x1[j] = 0.f;
-      if (hh < nwork) {
-        const int off = hh < G ? (kvh * G + hh) * D : hh == G ? (a.hq + kvh) * D : (a.hq + a.hkv + kvh) * D;
-        head_raw(hh <= G && qsrc ? qsrc + off : nullptr, psrc ? psrc + off : nullptr, a.part_ks, kstride, lane,
-                 x0[j], x1[j]);
-      }
-    }
-    c0 = bf2f(a.cos_t[static_cast<size_t>(p) * D + lane]);
-    s0 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane]);
-    c1 = bf2f(a.cos_t[static_cast<size_t>(p) * D + lane + 64]);
-    s1 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane + 64]);
-  } else {
-    for (int e = t; e < G * D; e += kThreads)
-      qs[e / D][e % D] = bf2f(a.q[b * a.q_bstride + (kvh * G) * D + e]);
+
+  // 1. the rope row (it needs the position), still ahead of the K / V
+  int p = p_raw;
+  if (fused && (p < 0 || p >= a.mp_rows)) {
+    if (s == 0 && kvh == 0 && t == 0) set_err(a.err, 5);
+    p = 0;
+  }
+  uint32_t cr0 = 0, sr0 = 0, cr1 = 0, sr1 = 0;
+  if constexpr (fused) {
+    cr0 = a.cos_t[static_cast<size_t>(p) * D + lane];
+    sr0 = a.sin_t[static_cast<size_t>(p) * D + lane];
+    cr1 = a.cos_t[static_cast<size_t>(p) * D + lane + 64];
+    sr1 = a.sin_t[static_cast<size_t>(p) * D + lane + 64];
   }
 
-  // 2. every K / V load of the split
+  // 2. every K / V load of the split, unconditional: positions past the context
+  //    read row n - 1 (in bounds) and are zeroed once landed, so no lane's load
+  //    sits behind a branch and the first wait can count them all
   uint4 kv[NIT], vv[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
-    const int pi = start + it * 16 + wid * 4 + slot;
-    const bool valid = pi < n;
+    const int pi = min(start + it * 16 + wid * 4 + slot, n - 1);
     const size_t off = static_cast<size_t>(pi) * KN + kvh * D + 8 * dc;
-    kv[it] = valid ? ld16_stream(kc + off) : make_uint4(0, 0, 0, 0);
-    vv[it] = valid ? ld16_stream(vc + off) : make_uint4(0, 0, 0, 0);
+    kv[it] = ld16_stream(kc + off);
+    vv[it] = ld16_stream(vc + off);
+  }
+
+  // 3. land the small loads (nothing above this line waits for a load but wr)
+  __builtin_amdgcn_sched_barrier(0);
+  float x0[kItems], x1[kItems];
+#pragma unroll
+  for (int j = 0; j < kItems; ++j) hr[j].land(a.part_ks, x0[j], x1[j]);
+  const float c0 = __uint_as_float(cr0 << 16), s0 = __uint_as_float(sr0 << 16);
+  const float c1 = __uint_as_float(cr1 << 16), s1 = __uint_as_float(sr1 << 16);
+  if constexpr (!fused) {
+#pragma unroll
+    for (int u = 0; u < kQPer; ++u) {
+      const int e = t + u * kThreads;
+      if (e < G * D) qs[e / D][e % D] = __uint_as_float(qraw[u] << 16);
+    }
   }
 
   // the prologue's arithmetic while the K / V loads are in flight
@@ -195,11 +278,13 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
     if (!fused || hh >= nwork) continue;
     float o0, o1;
     if (hh < G) {
-      norm_rope_head(x0[j], x1[j], a.gq, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
+      norm_rope_head_g(x0[j], x1[j], __uint_as_float(gr0[j] << 16), __uint_as_float(gr1[j] << 16), a.eps_head, c0,
+                       s0, c1, s1, o0, o1);
       qs[hh][lane] = o0;
       qs[hh][lane + 64] = o1;
     } else if (hh == G) {
-      norm_rope_head(x0[j], x1[j], a.gk, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
+      norm_rope_head_g(x0[j], x1[j], __uint_as_float(gr0[j] << 16), __uint_as_float(gr1[j] << 16), a.eps_head, c0,
+                       s0, c1, s1, o0, o1);
       knew[lane] = o0;
       knew[lane + 64] = o1;
       uint16_t* dst = kc + static_cast<size_t>(last) * KN + kvh * D;
@@ -280,7 +365,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
 #pragma unroll
       for (int i = 0; i < 8; ++i) vf[i] = vnew[8 * dc + i];
     } else {
-      unpack8(vv[it], vf);
+      // a position past the context brought row n - 1: weight 0, value 0
+      unpack8(pi < n ? vv[it] : make_uint4(0, 0, 0, 0), vf);
     }
 #pragma unroll
     for (int g = 0; g < G; ++g)
@@ -375,8 +461,25 @@ __global__ __launch_bounds__(W * kWave) void attn_seq_kernel(const AttnArgs a, u
   uint16_t* vc = a.vc + b * a.cache_bstride;
   uint16_t* ob = out + static_cast<size_t>(b) * a.hq * D + static_cast<size_t>(kvh) * G * D;
 
+  // 1. the loads that need nothing else: the write slot, the rope position and
+  //    the raw heads of the prologue (wave hh < G: query head kvh*G + hh; G: key;
+  //    G+1: value); then, once the position is known, the rope row; then the
+  //    first round of the cache stream. The raw heads and the rope row are landed
+  //    only after that round is issued (loads complete in issue order).
   int last = a.wr[b];
   int p = a.pos[b];
+  const int rows = (a.hq + 2 * a.hkv) * D;
+  const size_t kstride = static_cast<size_t>(rows) * gridDim.y;   // partials are [ks, B, rows]
+  const float* psrc = a.part + static_cast<size_t>(b) * rows;
+  HeadRaw<true> hr;
+  uint32_t gr0 = 0, gr1 = 0;   // the head's norm scale (query: gamma_q, key: gamma_k)
+  if (wid < G + 2) {
+    const int off = wid < G ? (kvh * G + wid) * D : wid == G ? (a.hq + kvh) * D : (a.hq + a.hkv + kvh) * D;
+    hr.load(nullptr, psrc + off, a.part_ks, kstride, lane);
+    const uint16_t* gam = wid < G ? a.gq : a.gk;
+    gr0 = gam[lane];
+    gr1 = gam[lane + 64];
+  }
   if (last < 0 || last >= a.cap) {
     if (kvh == 0 && t == 0) set_err(a.err, 4);
     for (int e = t; e < G * D; e += kSeqThreads) ob[e] = 0;
@@ -391,21 +494,10 @@ __global__ __launch_bounds__(W * kWave) void attn_seq_kernel(const AttnArgs a, u
   const int npos = nst * kSeqStep;
   const int nch = 2 * nst;                         // K steps, then V steps
   const int pw = wid * 4 + slot;                   // this lane's position within a step
-
-  // 1. the prologue's raw heads (wave hh < G: query head kvh*G + hh; G: key; G+1: value)
-  //    and the rope row, ahead of the cache stream (loads complete in issue order)
-  const int rows = (a.hq + 2 * a.hkv) * D;
-  const size_t kstride = static_cast<size_t>(rows) * gridDim.y;   // partials are [ks, B, rows]
-  const float* psrc = a.part + static_cast<size_t>(b) * rows;
-  float x0 = 0.f, x1 = 0.f;
-  if (wid < G + 2) {
-    const int off = wid < G ? (kvh * G + wid) * D : wid == G ? (a.hq + kvh) * D : (a.hq + a.hkv + kvh) * D;
-    head_raw(nullptr, psrc + off, a.part_ks, kstride, lane, x0, x1);
-  }
-  const float c0 = bf2f(a.cos_t[static_cast<size_t>(p) * D + lane]);
-  const float s0 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane]);
-  const float c1 = bf2f(a.cos_t[static_cast<size_t>(p) * D + lane + 64]);
-  const float s1 = bf2f(a.sin_t[static_cast<size_t>(p) * D + lane + 64]);
+  const uint32_t cr0 = a.cos_t[static_cast<size_t>(p) * D + lane];
+  const uint32_t sr0 = a.sin_t[static_cast<size_t>(p) * D + lane];
+  const uint32_t cr1 = a.cos_t[static_cast<size_t>(p) * D + lane + 64];
+  const uint32_t sr1 = a.sin_t[static_cast<size_t>(p) * D + lane + 64];
 
   // chunk c < nst: key step c; else value step c - nst. Positions past the
   // context read row n - 1 (in bounds) and are never used.
@@ -417,12 +509,21 @@ __global__ __launch_bounds__(W * kWave) void attn_seq_kernel(const AttnArgs a, u
   uint4 ring[kSeqRing];
 #pragma unroll
   for (int r = 0; r < kSeqRing; ++r) ring[r] = ld16_stream(chunk_ptr(min(r, nch - 1)));
+  const float c0 = __uint_as_float(cr0 << 16), s0 = __uint_as_float(sr0 << 16);
+  const float c1 = __uint_as_float(cr1 << 16), s1 = __uint_as_float(sr1 << 16);
 
-  // 2. the prep's arithmetic while the first cache loads are in flight
-  if (wid < G + 2) {
+  // 2. the prep's arithmetic while the first cache loads are in flight (the
+  //    wave index is re-read through readfirstlane so that this branch and the
+  //    loading one stay apart and the sums are not moved up to the loads)
+  __builtin_amdgcn_sched_barrier(0);
+  if (__builtin_amdgcn_readfirstlane(wid) < G + 2) {
+    float x0, x1;
+    hr.land(a.part_ks, x0, x1);
+    asm volatile("" : "+v"(gr0), "+v"(gr1));
     if (wid <= G) {
       float o0, o1;
-      norm_rope_head(x0, x1, wid < G ? a.gq : a.gk, a.eps_head, c0, s0, c1, s1, lane, o0, o1);
+      norm_rope_head_g(x0, x1, __uint_as_float(gr0 << 16), __uint_as_float(gr1 << 16), a.eps_head, c0, s0, c1, s1,
+                       o0, o1);
       if (wid < G) {
         qs[wid][lane] = o0;
         qs[wid][lane + 64] = o1;
@@ -474,67 +575,75 @@ __global__ __launch_bounds__(W * kWave) void attn_seq_kernel(const AttnArgs a, u
   //    padding chunks are value steps past the context, weight 0), so the loop
   //    body is straight-line and each use waits only for its own load.
   const int nrounds = (nch + kSeqRing - 1) / kSeqRing;
-  for (int rd = 0; rd < nrounds; ++rd) {
+  auto step = [&](const int c, uint4 v) __attribute__((always_inline)) {
+    if (c < nst) {
+      const int pi = c * kSeqStep + pw;
+      if (c == clast && pi == last) v = knp;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = dot2_bf16(qp[g][0], v.x, 0.f);
+        d = dot2_bf16(qp[g][1], v.y, d);
+        d = dot2_bf16(qp[g][2], v.z, d);
+        d = dot2_bf16(qp[g][3], v.w, d);
+        d = row16_sum(d) * a.scale;
+        if (pi < n) {
+          mloc[g] = fmaxf(mloc[g], d);
+          if (dc == 0) sc[g * npos + pi] = d;
+        }
+      }
+      if (c == nst - 1) {   // every score is in: the block max, then the weights
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float mx = rows4_max(mloc[g]);
+          if (lane == 0) red[0][wid][g] = mx;
+        }
+        lds_barrier();
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float mx = red[0][0][g];
+#pragma unroll
+          for (int w = 1; w < kSeqWaves; ++w) mx = fmaxf(mx, red[0][w][g]);
+          M[g] = mx;
+        }
+        // this wave's positions 32 s + 4 wid + q, lane-parallel: e in f32 into
+        // the denominator, the bf16 weight back over the score (0 past the context)
+        for (int j = lane; j < 4 * nst; j += kWave) {
+          const int pj = (j >> 2) * kSeqStep + 4 * wid + (j & 3);
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float e = pj < n ? __builtin_amdgcn_exp2f((sc[g * npos + pj] - M[g]) * kLog2e) : 0.f;
+            ls[g] += e;
+            sc[g * npos + pj] = round_bf(e);
+          }
+        }
+      }
+    } else {
+      const int pi = (c - nst) * kSeqStep + pw;
+      if (c == nst + clast && pi == last) v = vnp;
+      float vf[8];
+      unpack8(v, vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float wgt = pi < n ? sc[g * npos + min(pi, n - 1)] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[g][i] = fmaf(wgt, vf[i], o[g][i]);
+      }
+    }
+  };
+  for (int rd = 0; rd + 1 < nrounds; ++rd) {
 #pragma unroll
     for (int r = 0; r < kSeqRing; ++r) {
       const int c = rd * kSeqRing + r;
-      uint4 v = ring[r];
+      const uint4 v = ring[r];
       ring[r] = ld16_stream(chunk_ptr(min(c + kSeqRing, nch - 1)));
-      if (c < nst) {
-        const int pi = c * kSeqStep + pw;
-        if (c == clast && pi == last) v = knp;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float d = dot2_bf16(qp[g][0], v.x, 0.f);
-          d = dot2_bf16(qp[g][1], v.y, d);
-          d = dot2_bf16(qp[g][2], v.z, d);
-          d = dot2_bf16(qp[g][3], v.w, d);
-          d = row16_sum(d) * a.scale;
-          if (pi < n) {
-            mloc[g] = fmaxf(mloc[g], d);
-            if (dc == 0) sc[g * npos + pi] = d;
-          }
-        }
-        if (c == nst - 1) {   // every score is in: the block max, then the weights
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const float mx = rows4_max(mloc[g]);
-            if (lane == 0) red[0][wid][g] = mx;
-          }
-          lds_barrier();
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            float mx = red[0][0][g];
-#pragma unroll
-            for (int w = 1; w < kSeqWaves; ++w) mx = fmaxf(mx, red[0][w][g]);
-            M[g] = mx;
-          }
-          // this wave's positions 32 s + 4 wid + q, lane-parallel: e in f32 into
-          // the denominator, the bf16 weight back over the score (0 past the context)
-          for (int j = lane; j < 4 * nst; j += kWave) {
-            const int pj = (j >> 2) * kSeqStep + 4 * wid + (j & 3);
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-              const float e = pj < n ? __builtin_amdgcn_exp2f((sc[g * npos + pj] - M[g]) * kLog2e) : 0.f;
-              ls[g] += e;
-              sc[g * npos + pj] = round_bf(e);
-            }
-          }
-        }
-      } else {
-        const int pi = (c - nst) * kSeqStep + pw;
-        if (c == nst + clast && pi == last) v = vnp;
-        float vf[8];
-        unpack8(v, vf);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float wgt = pi < n ? sc[g * npos + min(pi, n - 1)] : 0.f;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[g][i] = fmaf(wgt, vf[i], o[g][i]);
-        }
-      }
+      step(c, v);
     }
   }
+  // the last round issues no refills: none would be consumed, and the ring's
+  // registers are reused after the loop (a load still in flight into them
+  // would be waited for there)
+#pragma unroll
+  for (int r = 0; r < kSeqRing; ++r) step((nrounds - 1) * kSeqRing + r, ring[r]);
 
   // 4. the four position slots of a wave (row swaps), then the waves in order
 #pragma unroll
@@ -573,14 +682,21 @@ int launch_attn_seq_g(const AttnArgs& a, int batch, hipStream_t st) {
   return launched("attn_seq");
 }
 
+template <int G, int NIT>
+void launch_attn_mode(const AttnArgs& a, dim3 grid, hipStream_t st) {
+  if (a.gq == nullptr) attn_decode_kernel<G, NIT, QM_PREPARED><<<grid, kThreads, 0, st>>>(a);
+  else if (a.part == nullptr) attn_decode_kernel<G, NIT, QM_RAW><<<grid, kThreads, 0, st>>>(a);
+  else attn_decode_kernel<G, NIT, QM_PART><<<grid, kThreads, 0, st>>>(a);
+}
+
 template <int G>
 int launch_attn_g(const AttnArgs& a, int ss, int batch, hipStream_t st) {
   const dim3 grid(a.hkv, a.ns, batch);
   switch (ss) {
-    case 32: attn_decode_kernel<G, 2><<<grid, kThreads, 0, st>>>(a); break;
-    case 64: attn_decode_kernel<G, 4><<<grid, kThreads, 0, st>>>(a); break;
-    case 128: attn_decode_kernel<G, 8><<<grid, kThreads, 0, st>>>(a); break;
-    case 256: attn_decode_kernel<G, 16><<<grid, kThreads, 0, st>>>(a); break;
+    case 32: launch_attn_mode<G, 2>(a, grid, st); break;
+    case 64: launch_attn_mode<G, 4>(a, grid, st); break;
+    case 128: launch_attn_mode<G, 8>(a, grid, st); break;
+    case 256: launch_attn_mode<G, 16>(a, grid, st); break;
     default: return fail(TFA_ERR_SHAPE, "attn_decode: split %d not in {32, 64, 128, 256}", ss);
   }
   return launched("attn_decode");
