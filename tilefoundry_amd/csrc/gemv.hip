@@ -144,13 +144,25 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
       if (t < kLoraRope) krv = a.xf[K + kLoraLat + t];
     }
   } else {
+    // unconditional (a chunk past the quarter reads its last chunk, zeroed once
+    // landed): no load behind a branch, so the norm below waits for these alone
+    // and not for the weights issued after them
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
-      const int c = lane + j * kWave;
-      xv[j] = c < nch ? ld16(src + kbase + 8 * c) : make_uint4(0, 0, 0, 0);
-      if (PRO != PRO_PLAIN) gv[j] = c < nch ? ld16(a.gamma + kbase + 8 * c) : make_uint4(0, 0, 0, 0);
+      const int c = min(lane + j * kWave, nch - 1);
+      xv[j] = ld16(src + kbase + 8 * c);
+      if (PRO != PRO_PLAIN) gv[j] = ld16(a.gamma + kbase + 8 * c);
     }
   }
+
+  // the epilogue's own inputs (the residual row, the residual scale, the value
+  // cache slot) go out with the first loads, so the epilogue adds no round trip
+  uint32_t res_raw = 0, al_raw = 0;
+  int slot_raw = 0;
+  if constexpr (EPI == EPI_RESID || EPI == EPI_RESID_SCALED)
+    res_raw = a.res[min(row0 + min(t, R - 1), a.N - 1)];
+  if constexpr (EPI == EPI_RESID_SCALED) al_raw = a.alpha[0];
+  if constexpr (EPI == EPI_QKV) slot_raw = a.wr[0];
 
   // 2. weights: streamed once, non-temporal
   uint4 w[R][NCH];
@@ -161,13 +173,13 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
     for (int j = 0; j < NCH; ++j) {
       const int c = lane + j * kWave;
       // R is even, so (row & 1) == (r & 1) and the matrix pick is static
+      // rows past N and chunks past the quarter read the last ones (real, finite
+      // weights): the chunk's input is zero and the row is never stored
+      const int rc = min(row, a.N - 1);
       const uint16_t* wrow = (EPI == EPI_SWIGLU && a.w_odd)
-                                 ? ((r & 1) ? a.w_odd : a.w) + static_cast<size_t>(row >> 1) * K
-                                 : a.w + static_cast<size_t>(row) * K;
-      if (row < a.N && c < nch)
-        w[r][j] = ld16_stream(wrow + kbase + 8 * c);
-      else
-        w[r][j] = make_uint4(0, 0, 0, 0);
+                                 ? ((r & 1) ? a.w_odd : a.w) + static_cast<size_t>(rc >> 1) * K
+                                 : a.w + static_cast<size_t>(rc) * K;
+      w[r][j] = ld16_stream(wrow + kbase + 8 * min(c, nch - 1));
     }
   }
 
@@ -182,7 +194,7 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
   float xf[NCH][8];
   if (PRO != PRO_LORA) {
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) unpack8(xv[j], xf[j]);
+    for (int j = 0; j < NCH; ++j) unpack8(lane + j * kWave < nch ? xv[j] : make_uint4(0, 0, 0, 0), xf[j]);
   }
   if (PRO == PRO_PLAIN && a.in_div != 0.f) {
 #pragma unroll
@@ -297,10 +309,10 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
       const float v = total(t);
       if (EPI == EPI_F32) a.yf[row] = v;
       if (EPI == EPI_BF16) a.yb[row] = static_cast<uint16_t>(f2bf(v));
-      if (EPI == EPI_RESID) a.yb[row] = static_cast<uint16_t>(f2bf(bf2f(a.res[row]) + round_bf(v)));
+      if (EPI == EPI_RESID) a.yb[row] = static_cast<uint16_t>(f2bf(__uint_as_float(res_raw << 16) + round_bf(v)));
       if (EPI == EPI_RESID_SCALED) {
-        const float al = bf2f(a.alpha[0]);
-        a.yb[row] = static_cast<uint16_t>(f2bf(bf2f(a.res[row]) + round_bf(round_bf(v) * al)));
+        const float al = __uint_as_float(al_raw << 16);
+        a.yb[row] = static_cast<uint16_t>(f2bf(__uint_as_float(res_raw << 16) + round_bf(round_bf(v) * al)));
       }
     }
   }
@@ -320,7 +332,7 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
       if (row < a.n_qk) {
         a.yb[row] = v;
       } else {
-        const int slot = a.wr[0];
+        const int slot = slot_raw;
         const int nv = a.N - a.n_qk;  // value row width (hkv * head_dim)
         if (slot < 0 || slot >= a.cap) set_err(a.err, 3);
         else a.vc[static_cast<size_t>(slot) * nv + (row - a.n_qk)] = v;
