@@ -377,31 +377,11 @@ TFA_DEV bool better_pick(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
-// The best (value, lowest index) pair of nb candidates, reduced by a whole block
-// (blockDim.x a multiple of 64, at most 1024; s_v / s_i hold one entry per
-// wave). Each thread issues eight loads before its first compare. The returned
-// index is valid in thread 0.
-TFA_DEV int block_best(const float* bv, const int* bi, int nb, float* s_v, int* s_i) {
+// The rest of a block-wide pick: each thread's (best_v, best_i) across the wave
+// (row swaps / DPP, no LDS), then the waves in order through s_v / s_i (one
+// entry per wave). The result is valid in thread 0.
+TFA_DEV int block_best_reduce(float best_v, int best_i, float* s_v, int* s_i) {
   const int t = threadIdx.x, nt = blockDim.x;
-  float best_v = -3.402823466e38f;
-  int best_i = 0x7fffffff;
-  for (int b0 = t; b0 < nb; b0 += 8 * nt) {
-    float v[8];
-    int ix[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int b = b0 + u * nt;
-      const bool ok = b < nb;
-      v[u] = ok ? bv[b] : -3.402823466e38f;
-      ix[u] = ok ? bi[b] : 0x7fffffff;
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (better_pick(v[u], ix[u], best_v, best_i)) {
-        best_v = v[u];
-        best_i = ix[u];
-      }
-  }
   const int lane = t & (kWave - 1);
   auto step = [&](auto mc) __attribute__((always_inline)) {
     constexpr int M = decltype(mc)::value;
@@ -431,6 +411,63 @@ TFA_DEV int block_best(const float* bv, const int* bi, int nb, float* s_v, int* 
       }
   }
   return best_i;
+}
+
+// The best (value, lowest index) pair of nb candidates, reduced by a whole block
+// (blockDim.x a multiple of 64, at most 1024; s_v / s_i hold one entry per
+// wave). Each thread issues eight loads before its first compare. The returned
+// index is valid in thread 0.
+TFA_DEV int block_best(const float* bv, const int* bi, int nb, float* s_v, int* s_i) {
+  const int t = threadIdx.x, nt = blockDim.x;
+  float best_v = -3.402823466e38f;
+  int best_i = 0x7fffffff;
+  for (int b0 = t; b0 < nb; b0 += 8 * nt) {
+    float v[8];
+    int ix[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int b = b0 + u * nt;
+      const bool ok = b < nb;
+      v[u] = ok ? bv[b] : -3.402823466e38f;
+      ix[u] = ok ? bi[b] : 0x7fffffff;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (better_pick(v[u], ix[u], best_v, best_i)) {
+        best_v = v[u];
+        best_i = ix[u];
+      }
+  }
+  return block_best_reduce(best_v, best_i, s_v, s_i);
+}
+
+// The same pick in one memory round trip for nb <= U * blockDim.x: every
+// candidate load is issued at once (past nb at a clamped index, left out of the
+// compare), then `between()` -- the caller's loads that must not wait behind
+// these -- and only then the compares.
+template <int U, typename F>
+TFA_DEV int block_best_once(const float* bv, const int* bi, int nb, float* s_v, int* s_i, F&& between) {
+  const int t = threadIdx.x, nt = blockDim.x;
+  float v[U];
+  int ix[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int b = min(t + u * nt, nb - 1);
+    v[u] = bv[b];
+    ix[u] = bi[b];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  between();
+  __builtin_amdgcn_sched_barrier(0);
+  float best_v = -3.402823466e38f;
+  int best_i = 0x7fffffff;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (t + u * nt < nb && better_pick(v[u], ix[u], best_v, best_i)) {
+      best_v = v[u];
+      best_i = ix[u];
+    }
+  return block_best_reduce(best_v, best_i, s_v, s_i);
 }
 
 }  // namespace tfa

@@ -416,15 +416,26 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(
   __shared__ float rv[kSampleThreads / kWave];
   __shared__ int ri[kSampleThreads / kWave];
   const int t = threadIdx.x;
-  const int best = block_best(bv, bi, nb, rv, ri);
+  // the position and prompt length first, the next prompt id as soon as the
+  // position is known: none of them waits behind the candidates' round trip
+  const int p = pos[0];
+  const int pl = plen[0];
+  int nxt = 0;
+  auto next_id = [&]() { nxt = inp[min(max(p + 1, 0), nsteps - 1)]; };
+  int best;
+  if (nb <= 16 * kSampleThreads) {
+    best = block_best_once<16>(bv, bi, nb, rv, ri, next_id);
+  } else {
+    next_id();
+    best = block_best(bv, bi, nb, rv, ri);
+  }
   if (t == 0) {
-    const int p = pos[0];
     if (p < 0 || p >= nsteps) {
       set_err(err, 2);
     } else {
       sam[p] = best;
-      const bool prompt = (p + 1 < plen[0]) && (p + 1 < nsteps);
-      ids[0] = prompt ? static_cast<int64_t>(inp[p + 1]) : static_cast<int64_t>(best);
+      const bool prompt = (p + 1 < pl) && (p + 1 < nsteps);
+      ids[0] = prompt ? static_cast<int64_t>(nxt) : static_cast<int64_t>(best);
       pos[0] = p + 1;
     }
   }

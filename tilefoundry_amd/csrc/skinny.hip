@@ -289,9 +289,13 @@ int launch_skinny(const SkinnyArgs& a, hipStream_t st, const char* name) {
 // (residual mode), or with SCALED h = bf16(h_in[m] + bf16(bf16(sum_s part) * alpha))
 // (MiniCPM3's scale_depth residual); h_out[m] = h;
 // xn[m] = bf16(bf16(h * rsqrt(mean h^2 + eps)) * gamma).
-// Every load of the row is issued before any arithmetic (one memory round trip).
+// Every load of the row -- the residual or embedding row, the norm scale and
+// MAXKS partial rows per chunk (clamped to the last of the ks) -- is issued,
+// unconditionally at clamped addresses, before any of them is read: one memory
+// round trip (two in embed mode, whose row address needs the id).
 constexpr int kRowChunks = 2;   // 8-element chunks per thread: hidden <= 256 * 8 * 2
-template <bool SCALED>
+enum { RN_EMBED = 0, RN_RESID = 1, RN_RESID_SCALED = 2 };
+template <int MODE, int MAXKS, int CH>
 __global__ __launch_bounds__(kThreads) void rows_norm_kernel(
     const uint16_t* __restrict__ table, const int64_t* __restrict__ ids, int64_t vocab,
     const uint16_t* h_in, const float* __restrict__ part, int ks, uint16_t* h_out,
@@ -301,8 +305,8 @@ __global__ __launch_bounds__(kThreads) void rows_norm_kernel(
   const int m = blockIdx.x;
   const int t = threadIdx.x;
   const int nch = H / 8;
-  const uint16_t* src = nullptr;
-  if (table) {
+  const uint16_t* src;
+  if constexpr (MODE == RN_EMBED) {
     int64_t id = ids[m];
     if (id < 0 || id >= vocab) {
       if (t == 0 && err) atomicExch(err, 1);
@@ -312,36 +316,54 @@ __global__ __launch_bounds__(kThreads) void rows_norm_kernel(
   } else {
     src = h_in + static_cast<size_t>(m) * H;
   }
-  // gamma goes out with the row's own loads: it is not needed until after the
-  // reduction, and loading it there would add a second memory round trip
-  uint4 gq[kRowChunks];
+  constexpr int KS = MODE == RN_EMBED ? 1 : MAXKS;
+  uint4 hv[CH], gq[CH];
+  float4 pv[CH][KS][2];
 #pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    const int ch = t + c * kThreads;
-    if (ch < nch) gq[c] = ld16(gamma + 8 * ch);
+  for (int c = 0; c < CH; ++c) {
+    const int ch = min(t + c * kThreads, nch - 1);
+    hv[c] = ld16(src + 8 * ch);
+    gq[c] = ld16(gamma + 8 * ch);
+    if constexpr (MODE != RN_EMBED) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const float4* q = reinterpret_cast<const float4*>(
+            part + (static_cast<size_t>(min(s, ks - 1)) * M + m) * H + 8 * ch);
+        pv[c][s][0] = q[0];
+        pv[c][s][1] = q[1];
+      }
+    }
   }
-  float v[kRowChunks][8];
+  float v[CH][8];
   float ss = 0.f;
 #pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    const int ch = t + c * kThreads;
-    if (ch >= nch) continue;
-    unpack8(ld16(src + 8 * ch), v[c]);
-    if (!table) {
+  for (int c = 0; c < CH; ++c) {
+    const bool in = t + c * kThreads < nch;
+    unpack8(hv[c], v[c]);
+    if constexpr (MODE != RN_EMBED) {
       float acc[8];
-      sum_splits8(part + static_cast<size_t>(m) * H + 8 * ch, static_cast<size_t>(M) * H, ks, acc);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {   // split order, as sum_splits8
+        const bool sin = s < ks;
+        acc[0] += sin ? pv[c][s][0].x : 0.f; acc[1] += sin ? pv[c][s][0].y : 0.f;
+        acc[2] += sin ? pv[c][s][0].z : 0.f; acc[3] += sin ? pv[c][s][0].w : 0.f;
+        acc[4] += sin ? pv[c][s][1].x : 0.f; acc[5] += sin ? pv[c][s][1].y : 0.f;
+        acc[6] += sin ? pv[c][s][1].z : 0.f; acc[7] += sin ? pv[c][s][1].w : 0.f;
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        v[c][i] = SCALED ? round_bf(v[c][i] + round_bf(round_bf(acc[i]) * alpha))
-                         : round_bf(v[c][i] + round_bf(acc[i]));
+        v[c][i] = MODE == RN_RESID_SCALED ? round_bf(v[c][i] + round_bf(round_bf(acc[i]) * alpha))
+                                          : round_bf(v[c][i] + round_bf(acc[i]));
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss += v[c][i] * v[c][i];
+    for (int i = 0; i < 8; ++i) ss += in ? v[c][i] * v[c][i] : 0.f;
   }
   ss = block_sum(ss, red);
   const float rs = rsqrt_rn(ss / static_cast<float>(H) + eps);
 #pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
+  for (int c = 0; c < CH; ++c) {
     const int ch = t + c * kThreads;
     if (ch >= nch) continue;
     st16(h_out + static_cast<size_t>(m) * H + 8 * ch, pack8(v[c]));
@@ -350,6 +372,27 @@ __global__ __launch_bounds__(kThreads) void rows_norm_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = round_bf(round_bf(v[c][i] * rs) * g[i]);
     st16(xn + static_cast<size_t>(m) * H + 8 * ch, pack8(y));
+  }
+}
+
+template <int MODE>
+void launch_rows_norm(int m, hipStream_t stream, int ks, const uint16_t* table, const int64_t* ids, int64_t vocab,
+                      const uint16_t* h_in, const float* part, uint16_t* h_out, const uint16_t* gamma, uint16_t* xn,
+                      int M, int H, float eps, int* err, float alpha) {
+  // one 8-element chunk per thread up to 2048 wide rows, two beyond
+  auto go = [&](auto ksc, auto chc) {
+    rows_norm_kernel<MODE, decltype(ksc)::value, decltype(chc)::value><<<m, kThreads, 0, stream>>>(
+        table, ids, vocab, h_in, part, ks, h_out, gamma, xn, M, H, eps, err, alpha);
+  };
+  using K4 = std::integral_constant<int, 4>;
+  using K8 = std::integral_constant<int, kMaxSplitsK>;
+  using C1 = std::integral_constant<int, 1>;
+  using C2 = std::integral_constant<int, kRowChunks>;
+  const bool one = H <= kThreads * 8;
+  if (MODE == RN_EMBED || ks <= 4) {
+    if (one) go(K4{}, C1{}); else go(K4{}, C2{});
+  } else {
+    if (one) go(K8{}, C1{}); else go(K8{}, C2{});
   }
 }
 
@@ -363,16 +406,28 @@ __global__ __launch_bounds__(kSampleThreads) void batch_sample_kernel(
   __shared__ int ri[kSampleThreads / kWave];
   const int b = blockIdx.x;
   const int t = threadIdx.x;
-  const int best = block_best(bv + static_cast<size_t>(b) * nb, bi + static_cast<size_t>(b) * nb, nb, rv, ri);
+  // the position and prompt length first, the next prompt id as soon as the
+  // position is known: none of them waits behind the candidates' round trip
+  const int p = pos[b];
+  const int pl = plen[b];
+  int nxt = 0;
+  auto next_id = [&]() { nxt = inp[static_cast<size_t>(b) * nsteps + min(max(p + 1, 0), nsteps - 1)]; };
+  const float* bvb = bv + static_cast<size_t>(b) * nb;
+  const int* bib = bi + static_cast<size_t>(b) * nb;
+  int best;
+  if (nb <= 16 * kSampleThreads) {
+    best = block_best_once<16>(bvb, bib, nb, rv, ri, next_id);
+  } else {
+    next_id();
+    best = block_best(bvb, bib, nb, rv, ri);
+  }
   if (t == 0) {
-    const int p = pos[b];
     if (p < 0 || p >= nsteps) {
       if (err) atomicExch(err, 2);
     } else {
       sam[static_cast<size_t>(b) * nsteps + p] = best;
-      const bool prompt = (p + 1 < plen[b]) && (p + 1 < nsteps);
-      ids[b] = prompt ? static_cast<int64_t>(inp[static_cast<size_t>(b) * nsteps + p + 1])
-                      : static_cast<int64_t>(best);
+      const bool prompt = (p + 1 < pl) && (p + 1 < nsteps);
+      ids[b] = prompt ? static_cast<int64_t>(nxt) : static_cast<int64_t>(best);
       pos[b] = p + 1;
     }
   }
@@ -450,10 +505,14 @@ int tfa_rows_norm(const void* table, const int64_t* ids, int64_t vocab, const vo
                 (long long)ks, kMaxSplitsK);
   }
   if (m == 0) return TFA_OK;
-  rows_norm_kernel<false><<<(int)m, kThreads, 0, stream>>>(
-      static_cast<const uint16_t*>(table), ids, vocab, static_cast<const uint16_t*>(h_in), part,
-      (int)ks, static_cast<uint16_t*>(h_out), static_cast<const uint16_t*>(gamma),
-      static_cast<uint16_t*>(xn), (int)m, (int)hidden, eps, err, 0.f);
+  if (table)
+    launch_rows_norm<RN_EMBED>((int)m, stream, 1, static_cast<const uint16_t*>(table), ids, vocab, nullptr, nullptr,
+                               static_cast<uint16_t*>(h_out), static_cast<const uint16_t*>(gamma),
+                               static_cast<uint16_t*>(xn), (int)m, (int)hidden, eps, err, 0.f);
+  else
+    launch_rows_norm<RN_RESID>((int)m, stream, (int)ks, nullptr, nullptr, 0, static_cast<const uint16_t*>(h_in), part,
+                               static_cast<uint16_t*>(h_out), static_cast<const uint16_t*>(gamma),
+                               static_cast<uint16_t*>(xn), (int)m, (int)hidden, eps, err, 0.f);
   return launched("rows_norm");
 }
 
@@ -474,9 +533,9 @@ int tfa_rows_norm_scaled(const float* part, int64_t ks, const void* h_in, float 
   TFA_ALIGN16(xn);
   TFA_ALIGN16(gamma);
   if (m == 0) return TFA_OK;
-  rows_norm_kernel<true><<<(int)m, kThreads, 0, stream>>>(
-      nullptr, nullptr, 0, static_cast<const uint16_t*>(h_in), part, (int)ks, static_cast<uint16_t*>(h_out),
-      static_cast<const uint16_t*>(gamma), static_cast<uint16_t*>(xn), (int)m, (int)hidden, eps, nullptr, alpha);
+  launch_rows_norm<RN_RESID_SCALED>((int)m, stream, (int)ks, nullptr, nullptr, 0, static_cast<const uint16_t*>(h_in),
+                                    part, static_cast<uint16_t*>(h_out), static_cast<const uint16_t*>(gamma),
+                                    static_cast<uint16_t*>(xn), (int)m, (int)hidden, eps, nullptr, alpha);
   return launched("rows_norm_scaled");
 }
 
