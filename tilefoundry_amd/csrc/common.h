@@ -301,6 +301,7 @@ TFA_DEV void sum_splits8(const float* p, size_t stride, int ks, float* acc) {
     v[s][0] = q[0];
     v[s][1] = q[1];
   }
+  __builtin_amdgcn_sched_barrier(0);   // every load out before the first add
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
 #pragma unroll

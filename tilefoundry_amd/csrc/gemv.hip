@@ -118,31 +118,34 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
   // LoRA prologue: q_a[t + 256 j] (the order its norm sums in), this lane's f32
   // chunks, and for block 0 the latent column t, the rope slice and the position
   float qs[4], xl[NCH][8];
-  float cv = 0.f, gk = 0.f, krv = 0.f;
+  float cv = 0.f, krv = 0.f;
   int p_raw = 0;
   const bool side = PRO == PRO_LORA && blockIdx.x == 0;
+  uint32_t gkr = 0, cr = 0, sr = 0;
   if (PRO == PRO_LORA) {
+    // unconditional loads at clamped indices (values past the shape are zeroed
+    // once landed); every block also loads block 0's latent / rope operands
+    // (a few hundred bytes from L2) so that no load sits behind a branch; the
+    // position first, so the rope row can follow without waiting for the rest
+    p_raw = a.pos[0];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = t + kThreads * j;
-      qs[j] = i < K ? a.xf[i] : 0.f;
-    }
+    for (int j = 0; j < 4; ++j) qs[j] = a.xf[min(t + kThreads * j, K - 1)];
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
-      const int c = lane + j * kWave;
-      const uint4 zero = make_uint4(0, 0, 0, 0);
-      const float4 lo = __builtin_bit_cast(float4, c < nch ? ld16(a.xf + kbase + 8 * c) : zero);
-      const float4 hi = __builtin_bit_cast(float4, c < nch ? ld16(a.xf + kbase + 8 * c + 4) : zero);
+      const int c = min(lane + j * kWave, nch - 1);
+      const float4 lo = __builtin_bit_cast(float4, ld16(a.xf + kbase + 8 * c));
+      const float4 hi = __builtin_bit_cast(float4, ld16(a.xf + kbase + 8 * c + 4));
       xl[j][0] = lo.x; xl[j][1] = lo.y; xl[j][2] = lo.z; xl[j][3] = lo.w;
       xl[j][4] = hi.x; xl[j][5] = hi.y; xl[j][6] = hi.z; xl[j][7] = hi.w;
-      gv[j] = c < nch ? ld16(a.gamma + kbase + 8 * c) : make_uint4(0, 0, 0, 0);
+      gv[j] = ld16(a.gamma + kbase + 8 * c);
     }
-    if (side) {
-      p_raw = a.pos[0];
-      gk = bf2f(a.gkv[t]);
-      cv = a.xf[K + t];
-      if (t < kLoraRope) krv = a.xf[K + kLoraLat + t];
-    }
+    gkr = a.gkv[t];
+    cv = a.xf[K + t];
+    krv = a.xf[K + kLoraLat + min(t, kLoraRope - 1)];
+    const bool pv = p_raw >= 0 && p_raw < a.cap && p_raw < a.rope_rows;
+    const size_t ro = static_cast<size_t>(pv ? p_raw : 0) * kLoraRope + min(t, kLoraRope - 1);
+    cr = a.cos_t[ro];
+    sr = a.sin_t[ro];
   } else {
     // unconditional (a chunk past the quarter reads its last chunk, zeroed once
     // landed): no load behind a branch, so the norm below waits for these alone
@@ -211,7 +214,7 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float q = round_bf(0.f + qs[j]);
+      const float q = round_bf(0.f + (t + kThreads * j < K ? qs[j] : 0.f));
       ss += q * q;
     }
     ss = wave_sum(ss);
@@ -223,8 +226,8 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
       if (t < kLoraRope) kr[t] = round_bf(0.f + krv);
       p_ok = p_raw >= 0 && p_raw < a.cap && p_raw < a.rope_rows;
       if (t < kLoraRope && p_ok) {
-        c = bf2f(a.cos_t[static_cast<size_t>(p_raw) * kLoraRope + t]);
-        s = bf2f(a.sin_t[static_cast<size_t>(p_raw) * kLoraRope + t]);
+        c = bf2f(cr);
+        s = bf2f(sr);
       }
     }
     if (lane == 0) {
@@ -241,7 +244,8 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
       float g[8];
       unpack8(gv[j], g);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xf[j][i] = round_bf(round_bf(round_bf(0.f + xl[j][i]) * rq) * g[i]);
+      for (int i = 0; i < 8; ++i)
+        xf[j][i] = lane + j * kWave < nch ? round_bf(round_bf(round_bf(0.f + xl[j][i]) * rq) * g[i]) : 0.f;
     }
     if (side) {
       float tk = 0.f;
@@ -251,7 +255,8 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const GemvArgs a) {
       if (!p_ok) {
         if (t == 0) set_err(a.err, 6);
       } else {
-        a.lat_cache[static_cast<size_t>(p_raw) * kLoraLat + t] = static_cast<uint16_t>(f2bf(round_bf(cv * rk) * gk));
+        a.lat_cache[static_cast<size_t>(p_raw) * kLoraLat + t] =
+            static_cast<uint16_t>(f2bf(round_bf(cv * rk) * bf2f(gkr)));
         if (t < kLoraRope) {
           const float x = kr[t];
           const float partner = t < kLoraRope / 2 ? -kr[t + kLoraRope / 2] : kr[t - kLoraRope / 2];

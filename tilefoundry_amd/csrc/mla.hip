@@ -84,36 +84,51 @@ __global__ __launch_bounds__(kThreads) void mla_prep_kernel(
   const int row = qa + kLat + kRope;
   const size_t kstride = static_cast<size_t>(B) * row;
   const float* pb = part + static_cast<size_t>(b) * row;
-  auto reduced = [&](int i) {
-    return round_bf(sum_splits(pb + i, kstride, ks));   // the projection lands in bf16
-  };
-
   // Every load this thread needs goes out before any arithmetic (one memory
-  // round trip): the position, both norm scales, the split-K partials, and
-  // the rope table row (behind the position's scalar load only).
+  // round trip), unconditionally at clamped indices: the position, both norm
+  // scales, the split-K partials of its q_a, latent and rope values, and the
+  // rope table row (behind the position's load only).
   const int p_raw = pos[b];
-  float gqv[4];
+  uint32_t gqr[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = t + kThreads * j;
-    gqv[j] = i < qa ? bf2f(gq[i]) : 0.f;
-  }
-  const float gk = bf2f(gkv[t]);
-  // q_a -> LoRA norm; kv_c -> LoRA norm (the latent); the rope slice
-  float qv[4];
+  for (int j = 0; j < 4; ++j) gqr[j] = gq[min(t + kThreads * j, qa - 1)];
+  const uint32_t gkr = gkv[t];
+  float qp[4][kMaxSplitsK], cp[kMaxSplitsK], rp[kMaxSplitsK];
+  auto load_splits = [&](int i, float* v) __attribute__((always_inline)) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = t + kThreads * j;
-    qv[j] = i < qa ? reduced(i) : 0.f;
-  }
-  const float cv = reduced(qa + t);
-  if (t < kRope) kr[t] = reduced(qa + kLat + t);
+    for (int sp = 0; sp < kMaxSplitsK; ++sp) v[sp] = pb[static_cast<size_t>(min(sp, ks - 1)) * kstride + i];
+  };
+#pragma unroll
+  for (int j = 0; j < 4; ++j) load_splits(min(t + kThreads * j, qa - 1), qp[j]);
+  load_splits(qa + t, cp);
+  load_splits(qa + kLat + min(t, kRope - 1), rp);
   const bool p_ok = p_raw >= 0 && p_raw < cap && p_raw < rope_rows;
-  float c = 0.f, s = 0.f;
-  if (t < kRope && p_ok) {
-    c = bf2f(cos_t[static_cast<size_t>(p_raw) * kRope + t]);
-    s = bf2f(sin_t[static_cast<size_t>(p_raw) * kRope + t]);
+  const int pc = p_ok ? p_raw : 0;
+  const uint32_t cr = cos_t[static_cast<size_t>(pc) * kRope + min(t, kRope - 1)];
+  const uint32_t sr = sin_t[static_cast<size_t>(pc) * kRope + min(t, kRope - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  // the projection values land in bf16 (sum_splits' order)
+  auto landed = [&](const float* v) __attribute__((always_inline)) {
+    float acc = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplitsK; ++sp) acc += sp < ks ? v[sp] : 0.f;
+    return round_bf(acc);
+  };
+  float gqv[4], qv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bool in = t + kThreads * j < qa;
+    gqv[j] = in ? bf2f(gqr[j]) : 0.f;
+    qv[j] = in ? landed(qp[j]) : 0.f;
   }
+  const float gk = bf2f(gkr);
+  // q_a -> LoRA norm; kv_c -> LoRA norm (the latent); the rope slice
+  const float cv = landed(cp);
+  // every thread lands its (clamped) rope slice, so its loads are not sunk into
+  // a branch; threads past the slice write the last value again, unchanged
+  kr[min(t, kRope - 1)] = landed(rp);
+  const float c = t < kRope && p_ok ? bf2f(cr) : 0.f;
+  const float s = t < kRope && p_ok ? bf2f(sr) : 0.f;
   // both sums of squares in one block reduction (waves summed in order)
   float ss = 0.f;
 #pragma unroll
@@ -175,10 +190,17 @@ __global__ __launch_bounds__(kThreads) void mla_q_absorb_kernel(
   const int qrow = H * kQH;
   const size_t kstride = static_cast<size_t>(B) * qrow;
   const int nval = B * kQH;
-  float wc[kNope];
+  // 1. the positions first, then the W_UK column and every split-K partial; the
+  //    rope rows go out as soon as the positions are in, while the rest is
+  //    still in flight (loads complete in issue order), so the kernel is about
+  //    one memory round trip
+  int pr[kRopePer];
+#pragma unroll
+  for (int j = 0; j < kRopePer; ++j) pr[j] = pos[min((t + kThreads * j) / kRope, B - 1)];
+  uint32_t wraw[kNope];
   const uint16_t* wuk = w_kv_b + static_cast<size_t>(h) * kKvB * kLat + t;
 #pragma unroll
-  for (int i = 0; i < kNope; ++i) wc[i] = bf2f(wuk[static_cast<size_t>(i) * kLat]);
+  for (int i = 0; i < kNope; ++i) wraw[i] = wuk[static_cast<size_t>(i) * kLat];
   float part[kPer][kMaxSplitsK];
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
@@ -188,10 +210,22 @@ __global__ __launch_bounds__(kThreads) void mla_q_absorb_kernel(
 #pragma unroll
     for (int sp = 0; sp < kMaxSplitsK; ++sp) part[j][sp] = src[static_cast<size_t>(min(sp, ks - 1)) * kstride];
   }
-  int pr[kRopePer];
+  uint32_t csr[kRopePer], snr[kRopePer];
 #pragma unroll
-  for (int j = 0; j < kRopePer; ++j) pr[j] = pos[min((t + kThreads * j) / kRope, B - 1)];
-  // the projection values land in bf16 (split order)
+  for (int j = 0; j < kRopePer; ++j) {
+    const int e = t + kThreads * j;
+    int p = pr[j];
+    if (e < B * kRope && (p < 0 || p >= rope_rows)) {
+      if (h == 0) set_err(err, 6);
+      p = 0;
+    }
+    p = p < 0 || p >= rope_rows ? 0 : p;
+    const int d = e % kRope;
+    csr[j] = cos_t[static_cast<size_t>(p) * kRope + d];
+    snr[j] = sin_t[static_cast<size_t>(p) * kRope + d];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 2. the projection values land in bf16 (split order)
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int e = t + kThreads * j;
@@ -203,20 +237,13 @@ __global__ __launch_bounds__(kThreads) void mla_q_absorb_kernel(
     if (i < kNope) qn[b][i] = round_bf(acc);
     else qr[b][i - kNope] = round_bf(acc);
   }
-  // the rope rows of the positions (the second round trip)
-  float cs[kRopePer], sn[kRopePer];
+  float wc[kNope], cs[kRopePer], sn[kRopePer];
+#pragma unroll
+  for (int i = 0; i < kNope; ++i) wc[i] = bf2f(wraw[i]);
 #pragma unroll
   for (int j = 0; j < kRopePer; ++j) {
-    const int e = t + kThreads * j;
-    int p = pr[j];
-    if (e < B * kRope && (p < 0 || p >= rope_rows)) {
-      if (h == 0) set_err(err, 6);
-      p = 0;
-    }
-    p = p < 0 || p >= rope_rows ? 0 : p;
-    const int d = e % kRope;
-    cs[j] = bf2f(cos_t[static_cast<size_t>(p) * kRope + d]);
-    sn[j] = bf2f(sin_t[static_cast<size_t>(p) * kRope + d]);
+    cs[j] = bf2f(csr[j]);
+    sn[j] = bf2f(snr[j]);
   }
   lds_barrier();
   for (int b = 0; b < B; ++b) {
@@ -596,6 +623,7 @@ __global__ __launch_bounds__(kThreads) void mla_combine_up_fast_kernel(
   uint4 wv[8];
 #pragma unroll
   for (int c8 = 0; c8 < 8; ++c8) wv[c8] = ld16(wrow + 8 * c8);
+  __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the first is read
   // 2. weights of the live splits
   const int last = last_raw < 0 ? 0 : (last_raw >= cap ? cap - 1 : last_raw);
   const int nsa = min(ns, last / split + 1);
@@ -636,10 +664,11 @@ __global__ __launch_bounds__(kThreads) void rows_residual_kernel(
   const size_t e0 = (static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x) * 8;
   const size_t total = static_cast<size_t>(M) * N;
   if (e0 >= total) return;
+  const uint4 rv = ld16(res + e0);   // issued with the partials: one round trip
   float acc[8];
   sum_splits8(part + e0, total, ks, acc);
   float r[8];
-  unpack8(ld16(res + e0), r);
+  unpack8(rv, r);
   float o[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) o[i] = round_bf(r[i] + round_bf(round_bf(acc[i]) * alpha));
