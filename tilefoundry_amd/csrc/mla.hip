@@ -387,7 +387,12 @@ void mla_attn_kernel(const MlaAttnArgs a) {
     for (int ks = 0; ks < 9; ++ks) qop[ks] = ld16(qrow + 32 * ks);
   }
   issue(0, 0);
-  issue(1, 1);   // clamped rows when there is no step 1
+  // The DMAs are invisible to the compiler, so its own wait for the q loads
+  // (issued before them) also waits for every DMA behind them. With a second
+  // step that wait covers both stages; a one-step split issues nothing more,
+  // so step 0 waits for its own rows only (one sequence at 300 positions:
+  // 8.3 -> 7.8 us).
+  if (nsteps > 1) issue(1, 1);
 
   // Lane byte offsets into a stage (the lat_slot swizzle worked out so that
   // the rest of each address is an immediate). Score operand (ks, pt): row
@@ -479,7 +484,10 @@ void mla_attn_kernel(const MlaAttnArgs a) {
   // step 0 (step 1 is in flight behind it); from step 1 on, the next step's
   // DMA goes out once every wave is past the barrier, i.e. done with the
   // stage it refills
-  __builtin_amdgcn_s_waitcnt(kWaitVmStep);
+  if (nsteps > 1)
+    __builtin_amdgcn_s_waitcnt(kWaitVmStep);
+  else
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
   block_barrier();
   step(0, lds);
   for (int t = 1; t < nsteps; ++t) {
@@ -491,7 +499,6 @@ void mla_attn_kernel(const MlaAttnArgs a) {
 
   // merge the four quarters of each head tile: per-head max and sum, then
   // each quarter's share of the latent columns (64) summed in f32
-  __builtin_amdgcn_s_waitcnt(kWaitVm0);   // an unused step-1 DMA may still be out
   lds_barrier();   // every wave is done with the stages
   {
     const float lw = rows4_sum(l_run);
