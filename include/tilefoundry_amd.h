@@ -358,7 +358,7 @@ int tfa_mla_q_absorb(const float* q_part, int64_t ks, int64_t batch, int64_t hea
 
 /* Split attention of q_abs [batch, heads, 288] bf16 over slots 0..wr[b] of the
  * compressed cache on bf16 MFMA: s = scale * (q_abs . [latent | rope]) in f32,
- * per split (split positions, a multiple of 128, at most 1024) the softmax in
+ * per split (split positions: 32, 64, 96 or a multiple of 128 up to 1024) the softmax in
  * f32 with bf16 weights into the latent sum; op [batch, cap/split, heads, 256]
  * bf16 = the split's latent sum / its own weight sum, mp / lp [batch,
  * cap/split, heads] its max and sum. Only splits holding slots <= wr[b] are

@@ -134,8 +134,10 @@ def test_attention_argument_checks(lib):
 def test_mla_attention_argument_checks(lib):
     args = lambda heads, cap, split: (A, A, A, A, I64(8), I64(heads), I64(cap), I64(split), F(0.1), A, A, A,
                                       P(None), P(None))
-    st, msg = call(lib, "tfa_mla_attention", *args(40, 8192, 64))
+    st, msg = call(lib, "tfa_mla_attention", *args(40, 8192, 48))   # not a multiple of 32
     assert st == SHAPE and "multiple of 128" in msg
+    st, _ = call(lib, "tfa_mla_attention", *args(40, 8192, 160))   # past 128, not whole 128-position steps
+    assert st == SHAPE
     st, _ = call(lib, "tfa_mla_attention", *args(40, 8192, 2048))
     assert st == SHAPE
     st, _ = call(lib, "tfa_mla_attention", *args(49, 8192, 256))

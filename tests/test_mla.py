@@ -164,10 +164,11 @@ def _attend(dev, q_abs, lat, rk, pos, split, w_kv_b, cap):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("split,pos", [(256, [0, 63, 700]), (128, [128, 1, 1023]), (1024, [500, 1023, 2])])
+@pytest.mark.parametrize("split,pos", [(256, [0, 63, 700]), (128, [128, 1, 1023]), (1024, [500, 1023, 2]),
+                                       (32, [0, 31, 700]), (64, [64, 1, 1023]), (96, [95, 96, 500])])
 def test_mla_attention_vs_oracle(dev, split, pos):
     g = gen(sum(pos) + split)
-    B, cap = 3, 1024
+    B, cap = 3, 1024 // split * split
     w = oracle_weights()
     lat, rk = OM.random_cache(B, cap, CFG, seed=split)
     q_abs = torch.randn(B, H, KV + R, generator=g).to(BF)
@@ -179,8 +180,8 @@ def test_mla_attention_vs_oracle(dev, split, pos):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("heads", [1, 8, 17, 48])
-def test_mla_attention_split_outputs_other_head_counts(dev, heads):
+@pytest.mark.parametrize("heads,split", [(1, 128), (8, 128), (17, 128), (48, 128), (17, 32), (48, 64)])
+def test_mla_attention_split_outputs_other_head_counts(dev, heads, split):
     """The split outputs (op normalised by the split's own sum, natural-log max,
     sum) merged over the live splits equal the oracle's latent sum, for head
     counts that leave whole or partial 16-head tiles empty and contexts that end
@@ -190,7 +191,7 @@ def test_mla_attention_split_outputs_other_head_counts(dev, heads):
     from tilefoundry_amd._lib import C
 
     cfg = replace(CFG, heads=heads)
-    B, cap, split = 2, 512, 128
+    B, cap = 2, 512
     pos = [129, 511]
     lat, rk = OM.random_cache(B, cap, cfg, seed=heads)
     g = gen(heads)

@@ -278,25 +278,25 @@ struct MlaAttnArgs {
   float scale_log2;   // scale * log2(e)
 };
 
-// Work split: a step is 128 positions in two LDS stages, filled by DMA. Wave
-// (quarter u, head tile mt) -- 12 waves, three per SIMD -- owns positions
+// Work split: a step is Q x 32 positions in two LDS stages, filled by DMA.
+// Wave (quarter u, head tile mt) -- 3Q waves, three per SIMD -- owns positions
 // 32u .. 32u + 31 of every step and heads 16mt .. 16mt + 15, with its own
-// online-softmax state; the four quarters of a head tile are merged at the
-// end. One barrier per step publishes the step's rows and frees the other
-// stage for the next step's DMA.
-constexpr int kAttnWaves = 12;
-constexpr int kAttnThreads = kAttnWaves * kWave;
-constexpr int kQuarters = 4;
+// online-softmax state; with Q = 4 the four quarters of a head tile are
+// merged at the end. One barrier per step publishes the step's rows and frees
+// the other stage for the next step's DMA. Q = 4 (128-position steps) for
+// splits of whole steps; Q = 1 (32-position steps, no quarter merge) for
+// splits of 32 / 64 / 96 positions, the short-latency form for one sequence.
 constexpr int kWaveRows = 32;
-constexpr int kStep = kQuarters * kWaveRows;
-constexpr int kLatChunks = kLat / 8;     // 16-byte chunks per latent row
-constexpr int kLatStage = kStep * kLat * 2;     // bytes
-constexpr int kRopeStage = kStep * kRope * 2;
-constexpr int kStageBytes = kLatStage + kRopeStage;
-constexpr int kStepDma = kStageBytes / (16 * kWave);   // 64 latent (2 rows) + 8 rope (16 rows)
-constexpr int kStepVm = kStepDma / kAttnWaves;          // per wave
-static_assert(kStepDma == 72 && kStepVm * kAttnWaves == kStepDma, "step DMA split evenly over the waves");
+constexpr int kStepVm = 6;   // DMAs per wave per step: 2Q rows' latent and rope per wave
 constexpr int kWaitVmStep = waitcnt_vm(kStepVm);
+template <int Q>
+struct AttnShape {
+  static constexpr int waves = 3 * Q;
+  static constexpr int step = Q * kWaveRows;
+  static constexpr int lat_stage = step * kLat * 2;     // bytes
+  static constexpr int stage_bytes = lat_stage + step * kRope * 2;
+  static_assert(stage_bytes / (16 * kWave) == kStepVm * waves, "step DMA split evenly over the waves");
+};
 constexpr int kWaitVm0 = waitcnt_vm(0);
 
 // Latent rows are 512 bytes of 32 16-byte chunks, stored XOR-swizzled by the
@@ -323,8 +323,14 @@ TFA_DEV uint2 ld_tr(const char* lds_byte) {
 // (n16, g) supplies as the B operand of the value product O^T += C^T . P^T,
 // so the weights never leave registers. K index 8g + i of that product is
 // position 4g + i (i < 4) or 16 + 4g + i - 4 of the wave's 32.
-__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3, 3)))
+template <int Q>
+__global__ __launch_bounds__(3 * Q * kWave) __attribute__((amdgpu_waves_per_eu(3, 3)))
 void mla_attn_kernel(const MlaAttnArgs a) {
+  constexpr int kQuarters = Q;
+  constexpr int kAttnWaves = AttnShape<Q>::waves;
+  constexpr int kStep = AttnShape<Q>::step;
+  constexpr int kLatStage = AttnShape<Q>::lat_stage;
+  constexpr int kStageBytes = AttnShape<Q>::stage_bytes;
   __shared__ uint4 smem[2 * kStageBytes / 16];   // two stages; the split merge reuses them
   __shared__ float st_m[kAttnWaves][16];
   __shared__ float st_l[kAttnWaves][16];
@@ -499,6 +505,25 @@ void mla_attn_kernel(const MlaAttnArgs a) {
 
   // merge the four quarters of each head tile: per-head max and sum, then
   // each quarter's share of the latent columns (64) summed in f32
+  if constexpr (Q == 1) {   // the wave holds its head tile's whole split
+    const float lsum = rows4_sum(l_run);
+    const float fself = 1.0f / lsum;
+    const size_t orow = (static_cast<size_t>(b) * a.ns + s) * a.H;
+    const int h = 16 * mt + n16;
+    if (h < a.H) {
+#pragma unroll
+      for (int ct = 0; ct < 16; ++ct) {
+        const f32x4 acc = o[ct] * fself;
+        *reinterpret_cast<uint2*>(a.op + (orow + h) * kLat + 16 * ct + 4 * g) =
+            make_uint2(pack_bf(acc[0], acc[1]), pack_bf(acc[2], acc[3]));
+      }
+      if (g == 0) {
+        a.mp[orow + h] = m_run * 0.6931471805599453f;   // natural-log units
+        a.lp[orow + h] = lsum;
+      }
+    }
+    return;
+  }
   lds_barrier();   // every wave is done with the stages
   {
     const float lw = rows4_sum(l_run);
@@ -973,8 +998,11 @@ int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* r
   TFA_REQUIRE(batch >= 1 && batch <= 65535, TFA_ERR_SHAPE, "tfa_mla_attention: batch %lld out of range", (long long)batch);
   TFA_REQUIRE(heads >= 1 && heads <= kHeadRows, TFA_ERR_SHAPE, "tfa_mla_attention: heads %lld not in [1, %d]",
               (long long)heads, kHeadRows);
-  TFA_REQUIRE(split >= kStep && split % kStep == 0 && split <= 8 * kStep, TFA_ERR_SHAPE,
-              "tfa_mla_attention: split %lld must be a multiple of %d, at most %d", (long long)split, kStep, 8 * kStep);
+  const bool quarters = split % AttnShape<4>::step == 0;   // whole 128-position steps
+  TFA_REQUIRE(split >= 1 && split <= 8 * AttnShape<4>::step &&
+                  (quarters || (split % kWaveRows == 0 && split < AttnShape<4>::step)),
+              TFA_ERR_SHAPE, "tfa_mla_attention: split %lld must be 32, 64, 96 or a multiple of 128 up to 1024",
+              (long long)split);
   TFA_REQUIRE(cap >= 1 && cap % split == 0 && cap / split <= kMaxSplits, TFA_ERR_SHAPE,
               "tfa_mla_attention: cap %lld must be a multiple of split %lld with at most %d splits",
               (long long)cap, (long long)split, kMaxSplits);
@@ -993,11 +1021,14 @@ int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* r
   a.H = (int)heads;
   a.cap = (int)cap;
   a.ns = (int)(cap / split);
-  a.tiles = (int)(split / kStep);
+  a.tiles = (int)(split / (quarters ? AttnShape<4>::step : AttnShape<1>::step));
   a.scale = scale;
   a.scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid(a.ns, (unsigned)batch);
-  mla_attn_kernel<<<grid, kAttnThreads, 0, stream>>>(a);
+  if (quarters)
+    mla_attn_kernel<4><<<grid, 3 * 4 * kWave, 0, stream>>>(a);
+  else
+    mla_attn_kernel<1><<<grid, 3 * 1 * kWave, 0, stream>>>(a);
   return launched("mla_attn");
 }
 
