@@ -211,6 +211,8 @@ int tfa_decode_qkv(const void* h, const void* table, const int64_t* ids, int64_t
  * Qwen3RMSNorm (gamma_q, eps_head) and rotate-half RoPE at pos[b] (cos / sin
  * [rope_rows, 128]); the new key gets the same with gamma_k and is written to
  * k_cache row wr[b] (and, from partials, the new value row to v_cache row wr[b]).
+ * err (optional int32[1]): 4 = wr out of [0, cap) -- the reads are clamped to
+ * slots 0..cap-1 and no cache row is written; 5 = pos out of [0, rope_rows).
  * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:418-501 (attn_partial)
  * and :328-411 (qk_rope_cache). */
 int tfa_decode_attention(const void* q, const float* qkv_part, int64_t part_ks,
@@ -487,29 +489,36 @@ int tfa_gemm_nt_f32(const void* a, const void* b, float* c, int64_t m, int64_t n
 
 /* The same product with K split into ks equal ranges (ks in [1, 8], dividing k / 64):
  * range z lands, unrounded, in c + z * m * ldc, so c holds ks partials [ks, m, ldc]
- * whose consumers sum them in split order (tfa_rows_norm, tfa_swiglu_pairs and
- * tfa_prefill_qk_rope take ks). For few token rows, where the unsplit grid leaves
+ * whose consumers sum them in split order (tfa_rows_norm, tfa_swiglu_pairs_split
+ * and tfa_prefill_qk_rope_split take ks). For few token rows, where the unsplit grid leaves
  * most CUs idle. Replaces the same products as tfa_gemm_nt_f32. */
 int tfa_gemm_nt_f32_split(const void* a, const void* b, float* c, int64_t m, int64_t n, int64_t k, int64_t lda,
                           int64_t ldb, int64_t ldc, int64_t ks, hipStream_t stream);
 
-/* The split count tfa_gemm_nt_f32_split is fastest with for this shape on the
- * current device (1 when the unsplit grid fills the CUs). */
+/* The split count tfa_gemm_nt_f32_split is fastest with for this shape (1 when
+ * the unsplit grid fills the CUs). It is planned for MI355X's 256 CUs from the
+ * shape alone, not from the device's reported CU count: the count fixes the
+ * order the partials are summed in, so the same prompt prefills to the same
+ * bits on any device. */
 int64_t tfa_gemm_f32_splits(int64_t m, int64_t n, int64_t k);
 
-/* SwiGLU of the prompt rows' fused gate|up product: gu f32 [ks, rows, ld] split-K
- * partials (ks in [1, 8], summed in split order) with column 2i = gate_i, 2i+1 =
- * up_i (the interleaved decode weight layout);
+/* SwiGLU of the prompt rows' fused gate|up product: gu f32 [rows, ld] with
+ * column 2i = gate_i, 2i+1 = up_i (the interleaved decode weight layout);
  * act[r, i] = bf16(bf16(silu(bf16 g)) * bf16 u) -- the decode step's epilogue.
  * inter a multiple of 4; ld >= 2*inter, a multiple of 4; gu 16-byte aligned.
  * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:547-572 (silu_mul) and the
  * SwiGLU prologue of :210-257 (gemv_silu), for every prompt row at once. */
-int tfa_swiglu_pairs(const float* gu, int64_t ks, int64_t ld, int64_t rows, int64_t inter, void* act,
-                     hipStream_t stream);
+int tfa_swiglu_pairs(const float* gu, int64_t ld, int64_t rows, int64_t inter, void* act, hipStream_t stream);
+
+/* tfa_swiglu_pairs over ks f32 split-K partials gu [ks, rows, ld] (ks in [1, 8],
+ * summed in split order before the landing), the output of
+ * tfa_gemm_nt_f32_split. tfa_swiglu_pairs is this entry with ks = 1.
+ * Replaces the same reference interfaces as tfa_swiglu_pairs. */
+int tfa_swiglu_pairs_split(const float* gu, int64_t ks, int64_t ld, int64_t rows, int64_t inter, void* act,
+                           hipStream_t stream);
 
 /* Per-head norm + RoPE + cache write for the prompt rows of a batch: qkv f32
- * [ks, batch * n, ldq] split-K partials (ks in [1, 8], summed in split order)
- * hold sequence b's row r at b * n + r (position pos0 + r),
+ * [batch * n, ldq] holds sequence b's row r at b * n + r (position pos0 + r),
  * columns [q (hq*128) | k (hkv*128) | v (hkv*128)]. Each head lands in bf16;
  * query heads get Qwen3RMSNorm(gamma_q) + rotate-half RoPE at the position and
  * go to q_out[(b*n + r), hq*128]; key heads the same with gamma_k into
@@ -519,10 +528,19 @@ int tfa_swiglu_pairs(const float* gu, int64_t ks, int64_t ld, int64_t rows, int6
  * projection values. head_dim 128; pos0 + n <= cap and <= rope_rows.
  * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:328-411 (qk_rope_cache) run
  * once per prompt token by the walk (fast/engine.py:261-263). */
-int tfa_prefill_qk_rope(const float* qkv, int64_t ks, int64_t ldq, const void* gamma_q, const void* gamma_k,
-                        float eps_head, const void* cos_t, const void* sin_t, int64_t rope_rows, int64_t batch,
-                        int64_t n, int64_t pos0, void* k_cache, void* v_cache, int64_t cap, void* q_out, int64_t hq,
+int tfa_prefill_qk_rope(const float* qkv, int64_t ldq, const void* gamma_q, const void* gamma_k, float eps_head,
+                        const void* cos_t, const void* sin_t, int64_t rope_rows, int64_t batch, int64_t n,
+                        int64_t pos0, void* k_cache, void* v_cache, int64_t cap, void* q_out, int64_t hq,
                         int64_t hkv, int64_t head_dim, hipStream_t stream);
+
+/* tfa_prefill_qk_rope over ks f32 split-K partials qkv [ks, batch * n, ldq]
+ * (ks in [1, 8], summed in split order before each head lands), the output of
+ * tfa_gemm_nt_f32_split. tfa_prefill_qk_rope is this entry with ks = 1.
+ * Replaces the same reference interface as tfa_prefill_qk_rope. */
+int tfa_prefill_qk_rope_split(const float* qkv, int64_t ks, int64_t ldq, const void* gamma_q, const void* gamma_k,
+                              float eps_head, const void* cos_t, const void* sin_t, int64_t rope_rows,
+                              int64_t batch, int64_t n, int64_t pos0, void* k_cache, void* v_cache, int64_t cap,
+                              void* q_out, int64_t hq, int64_t hkv, int64_t head_dim, hipStream_t stream);
 
 /* Causal GQA attention of every row of a batch of prompts, no gate:
  * out[b, r, h*D + d] = bf16(o / l), o = sum_{j <= r} bf16(exp(s - m)) v[b, j, g],

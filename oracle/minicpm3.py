@@ -392,8 +392,10 @@ def greedy(logits: torch.Tensor) -> int:
 
 
 def decode(model: ModelWeights, cfg: ModelConfig, prompt: list, max_new: int, record=None,
-           p_bf16: bool = True) -> list:
-    """Greedy continuation; ``record`` receives ``(logits, pick, top-2 gap)`` per generated step."""
+           p_bf16: bool = True, teacher: list | None = None) -> list:
+    """Greedy continuation; ``record`` receives ``(logits, pick, top-2 gap)`` per generated step.
+    With ``teacher``, step i feeds ``teacher[i]`` instead of its own pick (the
+    picks are still returned)."""
     cos, sin = rope_tables(len(prompt) + max_new, cfg)
     caches = empty_caches(cfg, len(model.layers))
     for p, t in enumerate(prompt):
@@ -406,5 +408,6 @@ def decode(model: ModelWeights, cfg: ModelConfig, prompt: list, max_new: int, re
             top = torch.topk(logits, 2).values
             record.append((logits.clone(), pick, float(top[0] - top[1])))
         if i + 1 < max_new:
-            logits = decode_step(model, cfg, pick, len(prompt) + i, caches, cos, sin, p_bf16)
+            nxt = teacher[i] if teacher is not None else pick
+            logits = decode_step(model, cfg, nxt, len(prompt) + i, caches, cos, sin, p_bf16)
     return out

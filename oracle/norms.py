@@ -20,6 +20,11 @@ Pinned by (tests/test_oracle.py): the constant-row closed form (a row of one
 value c normalises to sign(c), so y == sign(c) * gamma exactly); agreement with
 an f64 evaluation to within one bf16 rounding; and a planted-mistake check
 (dropping the bf16 landing before gamma changes the result on random rows).
+``resid_rms_norm`` is pinned on its own: against its f64 statement (1-8
+partials, one ulp), exactly on integer partials (the integer sum; a row summing
+to a constant normalises to sign(c) * gamma), and by two hand-worked
+known answers that separate its two landings, which fail when the partials are
+landed before the sum or when the residual add and the sum land once.
 """
 from __future__ import annotations
 

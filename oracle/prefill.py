@@ -125,6 +125,10 @@ def attention_rows(q, k, v, gate, rows, heads, cfg: PrefillConfig = PrefillConfi
 
 
 def o_proj(gated, hidden, w_o):
+    """``bf16(hidden + bf16(gated . W_o^T))``: the product lands, then the
+    residual add lands (examples/qwen3_8_27b_prefill-tilelang/model.py:326-333).
+    Pinned with a non-zero hidden state against its f64 statement and a
+    hand-worked known answer that one landing fails (tests/test_oracle.py)."""
     return hidden.to(BF16) + proj(gated, w_o)
 
 

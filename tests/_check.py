@@ -74,7 +74,8 @@ def assert_equal(name: str, got, ref):
     assert not bool(bad.any()), f"{name}: {int(bad.sum())} of {g.numel()} elements differ"
 
 
-def forced_agreement(name: str, picks, gold, gpu_logits, top_ids, top_vals, gaps, floor: int):
+def forced_agreement(name: str, picks, gold, gpu_logits, top_ids, top_vals, gaps, floor: int,
+                     max_delta=None):
     """Teacher-forced greedy agreement with the oracle, position by position.
 
     ``picks[i]`` is the GPU's pick at position i when fed the oracle's ids;
@@ -84,14 +85,21 @@ def forced_agreement(name: str, picks, gold, gpu_logits, top_ids, top_vals, gaps
     largest |GPU - oracle| over those candidates: a pick can only flip where
     the gap is at most ``2 * delta``. Every differing pick must be such a near
     tie and one of the oracle's candidates; the count of equal picks is printed
-    and must reach ``floor``. Returns ``(agree, deltas)``."""
+    and must reach ``floor``. ``max_delta`` (a number, or one per position) is
+    an absolute bound every ``delta`` must stay within, so that a regression
+    raising the logit error fails instead of widening the set of allowed
+    near ties. Returns ``(agree, deltas)``."""
     n = len(gold)
     agree, ties, bad, deltas = 0, 0, [], []
+    caps = [max_delta] * n if max_delta is None or isinstance(max_delta, (int, float)) else list(max_delta)
+    over = []
     for i in range(n):
         ids = torch.as_tensor(top_ids[i], dtype=torch.int64)
         got = gpu_logits[i].reshape(-1)[ids.to(gpu_logits[i].device)].double().cpu()
         delta = float((got - torch.as_tensor(top_vals[i], dtype=torch.float64)).abs().max())
         deltas.append(delta)
+        if caps[i] is not None and delta > caps[i]:
+            over.append((i, delta, caps[i]))
         tie = gaps[i] <= 2.0 * delta
         ties += int(tie)
         if picks[i] == gold[i]:
@@ -101,9 +109,16 @@ def forced_agreement(name: str, picks, gold, gpu_logits, top_ids, top_vals, gaps
     print(f"\n[agreement] {name}: {agree}/{n} picks equal the oracle's; {ties} positions are near ties "
           f"under the measured logit error (max |delta| {max(deltas):.4g}, median "
           f"{sorted(deltas)[n // 2]:.4g})", flush=True)
+    assert not over, f"{name}: logit error above its absolute bound (pos, delta, bound): {over[:5]}"
     assert not bad, f"{name}: picks differ at clear margins (pos, got, want, gap, delta): {bad[:5]}"
     assert agree >= floor, f"{name}: {agree}/{n} picks agree, below the floor {floor}"
     return agree, deltas
+
+
+def logit_bounds(logits_list, frac: float = 1e-2):
+    """Per-position absolute logit-error bounds: ``frac`` of the oracle's
+    largest |logit| at each position (the reference's bf16 bar on logits)."""
+    return [frac * float(lg.float().abs().max()) for lg in logits_list]
 
 
 def oracle_candidates(logits_list, k: int = 16):

@@ -29,3 +29,27 @@ def _name_the_case(request):
     if request.node.get_closest_marker("gpu") is not None:
         print(f"\n[case] {request.node.nodeid}", flush=True)
     yield
+
+
+#: Prefixes of the lines a parity test prints about its agreement with the
+#: oracle (teacher-forced pick counts, logit-error spreads, free-run
+#: divergence); the run's summary repeats them so the counts appear in the tail
+#: of the output even when pytest captures each test's own output.
+_RECORD_PREFIXES = ("[agreement]", "[spread]", "[free run]", "[exact]")
+_records: list[str] = []
+
+
+def pytest_runtest_logreport(report):
+    if report.when != "call":
+        return
+    for _, text in report.sections:
+        for line in text.splitlines():
+            if line.startswith(_RECORD_PREFIXES):
+                _records.append(f"{report.nodeid.split('::')[-1]}: {line}")
+
+
+def pytest_terminal_summary(terminalreporter):
+    if _records:
+        terminalreporter.section("oracle agreement records")
+        for line in _records:
+            terminalreporter.write_line(line)

@@ -184,28 +184,38 @@ def test_prompt_prefill_argument_checks(lib):
     st, _ = call(lib, "tfa_gemm_nt_f32_split", A, A, A, I64(37), I64(512), I64(2048), I64(2048), I64(2048),
                  I64(512), I64(16), P(None))
     assert st == SHAPE
-    # SwiGLU pairs: odd inter, ld too small, misaligned gu, bad split count
-    st, _ = call(lib, "tfa_swiglu_pairs", A, I64(1), I64(12288), I64(4), I64(6146), A, P(None))
+    # SwiGLU pairs: odd inter, ld too small, misaligned gu, bad split count; the
+    # unsplit entry keeps its own argument list and checks the same shapes
+    st, _ = call(lib, "tfa_swiglu_pairs_split", A, I64(1), I64(12288), I64(4), I64(6146), A, P(None))
     assert st == SHAPE
-    st, _ = call(lib, "tfa_swiglu_pairs", A, I64(1), I64(100), I64(4), I64(6144), A, P(None))
+    st, _ = call(lib, "tfa_swiglu_pairs_split", A, I64(1), I64(100), I64(4), I64(6144), A, P(None))
     assert st == SHAPE
-    st, _ = call(lib, "tfa_swiglu_pairs", MIS, I64(1), I64(12288), I64(4), I64(6144), A, P(None))
+    st, _ = call(lib, "tfa_swiglu_pairs_split", MIS, I64(1), I64(12288), I64(4), I64(6144), A, P(None))
     assert st == ALIGN
-    st, _ = call(lib, "tfa_swiglu_pairs", A, I64(9), I64(12288), I64(4), I64(6144), A, P(None))
+    st, _ = call(lib, "tfa_swiglu_pairs_split", A, I64(9), I64(12288), I64(4), I64(6144), A, P(None))
     assert st == SHAPE
+    st, _ = call(lib, "tfa_swiglu_pairs", A, I64(12288), I64(4), I64(6146), A, P(None))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_swiglu_pairs", MIS, I64(12288), I64(4), I64(6144), A, P(None))
+    assert st == ALIGN
     # q/k norm + RoPE rows: positions past the cache or the rope table, head_dim, split count
     qk = lambda n, pos0, cap, rope, hd=128, ks=1: (A, I64(ks), I64(4096), A, A, F(1e-6), A, A, I64(rope), I64(2),
                                                    I64(n), I64(pos0), A, A, I64(cap), A, I64(16), I64(8), I64(hd),
                                                    P(None))
-    st, msg = call(lib, "tfa_prefill_qk_rope", *qk(100, 0, 512, 512, ks=0))
+    st, msg = call(lib, "tfa_prefill_qk_rope_split", *qk(100, 0, 512, 512, ks=0))
     assert st == SHAPE and "ks" in msg
-    st, msg = call(lib, "tfa_prefill_qk_rope", *qk(100, 10, 100, 512))
+    st, msg = call(lib, "tfa_prefill_qk_rope_split", *qk(100, 10, 100, 512))
     assert st == CAPACITY and "capacity" in msg
-    st, msg = call(lib, "tfa_prefill_qk_rope", *qk(100, 0, 512, 64))
+    st, msg = call(lib, "tfa_prefill_qk_rope_split", *qk(100, 0, 512, 64))
     assert st == CAPACITY and "rope" in msg
-    st, _ = call(lib, "tfa_prefill_qk_rope", *qk(100, 0, 512, 512, hd=64))
+    st, _ = call(lib, "tfa_prefill_qk_rope_split", *qk(100, 0, 512, 512, hd=64))
     assert st == SHAPE
-    st, _ = call(lib, "tfa_prefill_qk_rope", *qk(0, 0, 512, 512))
+    st, _ = call(lib, "tfa_prefill_qk_rope_split", *qk(0, 0, 512, 512))
+    assert st == SHAPE
+    unsplit = lambda *a: (a[0],) + a[2:]   # the same arguments without ks
+    st, msg = call(lib, "tfa_prefill_qk_rope", *unsplit(*qk(100, 10, 100, 512)))
+    assert st == CAPACITY and "capacity" in msg
+    st, _ = call(lib, "tfa_prefill_qk_rope", *unsplit(*qk(100, 0, 512, 512, hd=64)))
     assert st == SHAPE
     # causal attention: head_dim, empty n, heads not a multiple, misaligned stride
     ca = lambda n, hd=128, hq=16, hkv=8, q_rs=2048: (A, I64(q_rs), I64(128), I64(0), A, I64(1024), I64(128), I64(0),

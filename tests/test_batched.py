@@ -6,7 +6,7 @@ import torch
 
 from oracle import norms as ON
 from oracle import qwen3 as OQ
-from tests._check import forced_agreement, oracle_candidates, assert_close, assert_equal, assert_l2, max_rel
+from tests._check import forced_agreement, logit_bounds, oracle_candidates, assert_close, assert_equal, assert_l2, max_rel
 
 BF = torch.bfloat16
 H, HQ, HKV, D, I = 2048, 16, 8, 128, 6144
@@ -324,7 +324,8 @@ def test_batch_engine_greedy(dev):
     for b in checked:
         ids, vals, gaps = oracle_candidates([r[0] for r in recs[b]])
         _, deltas = forced_agreement(f"2-layer bs=32, sequence {b}", picks[b], wants[b], [lg[b] for lg in logits],
-                                     ids, vals, gaps, floor=n - 2)
+                                     ids, vals, gaps, floor=n - 2,
+                                     max_delta=logit_bounds([r[0] for r in recs[b]]))
         diff = next((i for i, (x, y) in enumerate(zip(gen.tokens[b], wants[b])) if x != y), None)
         if diff is not None:
             assert gaps[diff] <= 2 * deltas[diff], f"seq {b}: free run leaves the oracle at a clear margin"
@@ -357,6 +358,7 @@ def test_full_model_batch32_golden(dev):
     import json
     from pathlib import Path
 
+    from tests.test_qwen3_engine import FULL_MODEL_MAX_DELTA
     from tilefoundry_amd.qwen3 import BatchEngine, QWEN3_1_7B
 
     gold = json.loads((Path(__file__).parent / "golden" / "qwen3_batch_golden.json").read_text())
@@ -372,7 +374,8 @@ def test_full_model_batch32_golden(dev):
     for b in range(keep):
         agree, _ = forced_agreement(f"28-layer bs=32, sequence {b}, 32 teacher-forced positions", picks[b],
                                     gold["tokens"][b], [lg[b] for lg in logits], gold["top_ids"][b],
-                                    gold["top_vals"][b], gold["gaps"][b], floor=n - 8)
+                                    gold["top_vals"][b], gold["gaps"][b], floor=n - 8,
+                                    max_delta=FULL_MODEL_MAX_DELTA)
         total += agree
     print(f"[agreement] 28-layer bs=32: {total}/{keep * n} over the {keep} checked sequences", flush=True)
     # the bs=1 model's own two valid orders agree on 91 % of picks (233 / 256);

@@ -269,6 +269,35 @@ def test_fused_attention_prologue(dev, pos, wr):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("wr", [512, -1])
+def test_fused_attention_bad_write_slot(dev, wr):
+    """A write slot outside the cache is flagged (err 4) and no cache row is
+    written -- the split path's rule is the whole-context kernel's; a rope
+    position past the table is flagged (err 5)."""
+    from tilefoundry_amd import ops
+
+    cap = 512
+    h, gamma_in, wq, wk, wv, gq, gk, cos, sin = _qkv_case(gen(71), cap)
+    xn = ON.rms_norm_q(h, gamma_in, EPS)
+    qk_raw = torch.cat([OQ.proj(xn, wq), OQ.proj(xn, wk)]).to(dev)
+    kd = randn(cap, HKV * D, g=gen(72)).to(dev)
+    vd = randn(cap, HKV * D, g=gen(73)).to(dev)
+    k0, v0 = kd.clone(), vd.clone()
+    rope = (gq.to(dev), gk.to(dev), EPS, cos.to(dev), sin.to(dev), 7)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.attn_partial(qk_raw, kd, vd, wr, HQ, HKV, split=64, rope=rope, neutral=True, err=err)
+    torch.cuda.synchronize()
+    assert int(err) == 4
+    assert_equal("k cache untouched", kd, k0)
+    assert_equal("v cache untouched", vd, v0)
+    err.zero_()
+    rope_bad = rope[:5] + (cap + 3,)
+    ops.attn_partial(qk_raw, kd, vd, 9, HQ, HKV, split=64, rope=rope_bad, neutral=True, err=err)
+    torch.cuda.synchronize()
+    assert int(err) == 5
+
+
+@pytest.mark.gpu
 def test_rope_position_zero_is_identity(dev):
     """At position 0 (cos = 1, sin = 0) the key written is exactly the head-normed
     projection: RoPE contributes nothing."""

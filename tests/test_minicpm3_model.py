@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import minicpm3 as OM
-from tests._check import assert_close, forced_agreement, oracle_candidates
+from tests._check import assert_close, forced_agreement, logit_bounds, oracle_candidates
 
 BF16 = torch.bfloat16
 
@@ -79,7 +79,7 @@ def test_minicpm3_engine_greedy_against_oracle(dev):
     picks, logits = eng.forced([prompt], [want[:-1]], record_logits=True)
     ids, vals, gaps = oracle_candidates([r[0] for r in rec])
     _, deltas = forced_agreement("MiniCPM3 2-layer bs=1, 20 positions", picks[0], want, [lg[0] for lg in logits],
-                                 ids, vals, gaps, floor=n - 2)
+                                 ids, vals, gaps, floor=n - 2, max_delta=logit_bounds([r[0] for r in rec]))
     got = eng.generate([prompt], n).tokens[0]
     diff = next((i for i, (a, b) in enumerate(zip(got, want)) if a != b), None)
     if diff is not None:

@@ -66,6 +66,81 @@ def test_add_rms_norm_residual_is_the_landed_sum():
     assert torch.equal(y, ON.rms_norm_q(ro, gamma, 1e-6))
 
 
+def _resid_rms_norm_f64(a, partials, gamma, eps):
+    """The residual norm stated in f64: the split-K partials' sum lands once in
+    bf16, the residual add lands again, and the Qwen3 norm of the landed sum."""
+    h = (a.double() + partials.double().sum(0).to(BF).double()).to(BF)
+    h64 = h.double()
+    n = (h64 * torch.rsqrt(h64.pow(2).mean(-1, keepdim=True) + eps)).to(BF)
+    return h, (n.double() * gamma.double()).to(BF)
+
+
+def test_resid_rms_norm_matches_f64_within_one_rounding():
+    """``resid_rms_norm`` against its f64 statement on random rows and 1-8
+    split-K partials: the residual and the normed row within one bf16 ulp."""
+    gen = g(60)
+    for ks in (1, 4, 8):
+        a = torch.randn(16, 2048, generator=gen).to(BF)
+        p = torch.randn(ks, 16, 2048, generator=gen)
+        gamma = (1 + 0.1 * torch.randn(2048, generator=gen)).to(BF)
+        h, xn = ON.resid_rms_norm(a, p, gamma, 1e-6)
+        h64, xn64 = _resid_rms_norm_f64(a, p, gamma, 1e-6)
+        assert int(bf16_ulps(h, h64).max()) <= 1, ks
+        assert int(bf16_ulps(xn, xn64).max()) <= 1, ks
+
+
+def test_resid_rms_norm_exact_on_integer_partials():
+    """Integer partials and residuals small enough that every sum is exact in
+    f32 and bf16: the residual is the integer sum, and a row built to sum to
+    one constant c normalises to sign(c) * gamma exactly."""
+    gen = g(61)
+    a = torch.randint(-64, 65, (8, 512), generator=gen).to(BF)
+    p = torch.randint(-16, 17, (4, 8, 512), generator=gen).float()
+    gamma = (1 + 0.1 * torch.randn(512, generator=gen)).to(BF)
+    h, _ = ON.resid_rms_norm(a, p, gamma, 1e-6)
+    want = a.to(torch.int64) + p.to(torch.int64).sum(0)
+    assert torch.equal(h.to(torch.int64), want)
+    for c in (3.0, -20.0, 0.5):
+        a_c = (c - p.sum(0)).to(BF)          # exact: |c - sum| <= 84
+        h, xn = ON.resid_rms_norm(a_c, p, gamma, 1e-6)
+        assert torch.equal(h, torch.full_like(h, c))
+        assert torch.equal(xn, (math.copysign(1.0, c) * gamma.float()).to(BF).expand_as(xn))
+
+
+def _landing_kat(resid):
+    """Two hand-worked cases that separate the two bf16 landings of
+    ``bf16(a + bf16(sum_s P[s]))`` (bf16 keeps 8 significant bits: the spacing
+    at 1.0 is 2^-7, and a tie rounds to even):
+
+    * a = 0, P = [1 + 2^-8, 2^-8]: the f32 sum is 1 + 2^-7 exactly, so h = 1 + 2^-7.
+      Landing each partial first gives bf16(1 + 2^-8) + 2^-8 = 1 + 2^-8, a tie -> 1.0.
+    * a = 1, P = [2^-8 + 2^-20]: the sum lands as 2^-8; 1 + 2^-8 is a tie -> h = 1.0.
+      One landing of a + sum (1 + 2^-8 + 2^-20, above the tie) gives 1 + 2^-7.
+
+    Returns True when ``resid(a, partials)`` gives both expected residuals."""
+    H = 64
+    one = torch.ones(1, H)
+    case1 = resid(torch.zeros(1, H).to(BF), torch.stack([(1 + 2 ** -8) * one, 2 ** -8 * one]))
+    case2 = resid(one.to(BF), ((2 ** -8 + 2 ** -20) * one)[None])
+    return (torch.equal(case1, torch.full((1, H), 1 + 2 ** -7).to(BF))
+            and torch.equal(case2, torch.ones(1, H).to(BF)))
+
+
+def test_resid_rms_norm_landings_known_answers():
+    gamma = torch.ones(64).to(BF)
+    assert _landing_kat(lambda a, p: ON.resid_rms_norm(a, p, gamma, 1e-6)[0])
+
+
+@pytest.mark.parametrize("plant", ["partials_landed_first", "single_landing"])
+def test_resid_rms_norm_planted_landing_mistakes_fail(plant):
+    """Planted mistakes in the residual's rounding points fail the known answers."""
+    if plant == "partials_landed_first":     # bf16(P[s]) summed, instead of bf16(sum P[s])
+        wrong = lambda a, p: a + p.to(BF).float().sum(0).to(BF)  # noqa: E731
+    else:                                    # bf16(a + sum P[s]) in one landing
+        wrong = lambda a, p: (a.float() + p.float().sum(0)).to(BF)  # noqa: E731
+    assert not _landing_kat(wrong)
+
+
 # ---------------------------------------------------------------- rope
 def test_rope_position_zero_is_identity():
     cos, sin = OQ.rope_tables(8, 128, 1.0e6)
@@ -818,3 +893,29 @@ def test_prefill_attention_rows_equals_full_attention():
     assert int(bf16_ulps(got, full[rows][:, heads]).max()) <= 1
     # row 0 sees only key 0: its output is v0 * sigmoid(gate)
     assert torch.equal(got[0, 0], v[0, 0] * torch.sigmoid(gate[0, 0]))
+
+
+def test_prefill_o_proj_double_landing_f64_and_known_answer():
+    """``o_proj`` is ``bf16(hidden + bf16(gated . W_o^T))`` with a non-zero
+    hidden state: within one bf16 ulp of its f64 statement on random rows, and
+    on a hand-worked row the product's own landing decides the answer -- the
+    product 2^-8 + 2^-20 lands as 2^-8, and 1 + 2^-8 is a tie that rounds to
+    1.0 (even); one landing of hidden + product gives 1 + 2^-7."""
+    from oracle import prefill as OP
+
+    gen = g(62)
+    gated = torch.randn(32, 384, generator=gen).to(BF)
+    w_o = (0.05 * torch.randn(256, 384, generator=gen)).to(BF)
+    hidden = torch.randn(32, 256, generator=gen).to(BF)
+    got = OP.o_proj(gated, hidden, w_o)
+    prod = (gated.double() @ w_o.double().t()).to(BF)
+    want = (hidden.double() + prod.double()).to(BF)
+    assert int(bf16_ulps(got, want).max()) <= 1
+    single = (hidden.float() + gated.float() @ w_o.float().t()).to(BF)
+    assert not torch.equal(got, single), "the double landing is exercised on random rows"
+    # known answer
+    g2 = torch.tensor([[2 ** -8, 2 ** -20]]).to(BF)
+    w2 = torch.ones(4, 2).to(BF)
+    h2 = torch.ones(1, 4).to(BF)
+    assert torch.equal(OP.o_proj(g2, h2, w2), torch.ones(1, 4).to(BF))
+    assert torch.equal((h2.float() + g2.float() @ w2.float().t()).to(BF), torch.full((1, 4), 1 + 2 ** -7).to(BF))

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import qwen3 as OQ
-from tests._check import assert_close, assert_l2, assert_ulps, forced_agreement, oracle_candidates
+from tests._check import assert_close, assert_l2, assert_ulps, forced_agreement, logit_bounds, oracle_candidates
 from tests.test_qwen3_engine import _small, oracle_cfg, oracle_model
 
 BF16 = torch.bfloat16
@@ -244,7 +244,7 @@ def test_engine_prefill_greedy_small(dev):
     picks, logits = eng.forced(prompt, want[:-1], record_logits=True)
     ids, vals, gaps = oracle_candidates([r[0] for r in rec])
     _, deltas = forced_agreement("2-layer bs=1 prefilled, 24 positions", picks, want, logits, ids, vals, gaps,
-                                 floor=n - 2)
+                                 floor=n - 2, max_delta=logit_bounds([r[0] for r in rec]))
     gen = eng.generate(prompt, n)
     assert gen.prompt_steps == len(prompt)
     diff = next((i for i, (a, b) in enumerate(zip(gen.tokens, want)) if a != b), None)
@@ -294,7 +294,7 @@ def test_batch_engine_prefill_small(dev):
     for b, prompt in enumerate(prompts):
         ids, vals, gaps = oracle_candidates([r[0] for r in recs[b]])
         forced_agreement(f"2-layer batch prefilled, sequence {b}", picks[b], wants[b], [lg[b] for lg in logits],
-                         ids, vals, gaps, floor=n - 2)
+                         ids, vals, gaps, floor=n - 2, max_delta=logit_bounds([r[0] for r in recs[b]]))
         _, caches = _oracle_walk(wts, cfg, prompt[:-1])
         m = len(prompt) - 1
         assert_close(f"seq {b} k cache layer 0", eng.kc[0, b, :m].view(m, cfg.kv_heads, cfg.head_dim), caches[0][0])
@@ -310,7 +310,7 @@ def test_full_model_prefill_greedy_golden(dev):
     import json
     from pathlib import Path
 
-    from tests.test_qwen3_engine import FULL_MODEL_FLOOR, check_spread
+    from tests.test_qwen3_engine import FULL_MODEL_FLOOR, FULL_MODEL_MAX_DELTA, check_spread
     from tilefoundry_amd.qwen3 import Engine
 
     gold = json.loads((Path(__file__).parent / "golden" / "qwen3_greedy_256.json").read_text())
@@ -319,5 +319,5 @@ def test_full_model_prefill_greedy_golden(dev):
     picks, logits = eng.forced(gold["prompt"], gold["tokens"][:-1], record_logits=True)
     _, deltas = forced_agreement("28-layer bs=1 after prompt prefill, 256 teacher-forced positions", picks,
                                  gold["tokens"], logits, gold["top_ids"], gold["top_vals"], gold["gaps"],
-                                 floor=FULL_MODEL_FLOOR)
+                                 floor=FULL_MODEL_FLOOR, max_delta=FULL_MODEL_MAX_DELTA)
     check_spread("28-layer bs=1 after prompt prefill", deltas, gold["order_spread"])

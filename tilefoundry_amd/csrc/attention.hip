@@ -206,7 +206,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
 #pragma unroll
     for (int u = 0; u < kQPer; ++u) qraw[u] = a.q[b * a.q_bstride + (kvh * G) * D + min(t + u * kThreads, G * D - 1)];
   }
-  if (last < 0 || last >= a.cap) {
+  // a write slot outside the cache is flagged and clamped for the reads only:
+  // no block then holds the new slot, so no cache row is written (attn_seq's rule)
+  const bool wr_ok = last >= 0 && last < a.cap;
+  if (!wr_ok) {
     if (s == 0 && kvh == 0 && t == 0) set_err(a.err, 4);
     last = last < 0 ? -1 : a.cap - 1;
   }
@@ -226,7 +229,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(const AttnArgs a)
     }
     return;
   }
-  const bool has_new = fused && last < start + SS;  // this split holds the newest slot
+  const bool has_new = fused && wr_ok && last < start + SS;  // this split holds the newest slot
   const bool new_v = has_new && QM == QM_PART;      // ... and also brings the new value row
   const int nwork = fused ? G + (has_new ? 1 : 0) + (new_v ? 1 : 0) : 0;
 
@@ -1297,10 +1300,18 @@ int tfa_qk_rope_cache(const float* qkv_part, int64_t part_ks, const void* gamma_
   return launched("qk_rope_cache");
 }
 
-int tfa_prefill_qk_rope(const float* qkv, int64_t ks, int64_t ldq, const void* gamma_q, const void* gamma_k,
-                        float eps_head, const void* cos_t, const void* sin_t, int64_t rope_rows, int64_t batch,
-                        int64_t n, int64_t pos0, void* k_cache, void* v_cache, int64_t cap, void* q_out, int64_t hq,
+int tfa_prefill_qk_rope(const float* qkv, int64_t ldq, const void* gamma_q, const void* gamma_k, float eps_head,
+                        const void* cos_t, const void* sin_t, int64_t rope_rows, int64_t batch, int64_t n,
+                        int64_t pos0, void* k_cache, void* v_cache, int64_t cap, void* q_out, int64_t hq,
                         int64_t hkv, int64_t head_dim, hipStream_t stream) {
+  return tfa_prefill_qk_rope_split(qkv, 1, ldq, gamma_q, gamma_k, eps_head, cos_t, sin_t, rope_rows, batch, n, pos0,
+                                   k_cache, v_cache, cap, q_out, hq, hkv, head_dim, stream);
+}
+
+int tfa_prefill_qk_rope_split(const float* qkv, int64_t ks, int64_t ldq, const void* gamma_q, const void* gamma_k,
+                              float eps_head, const void* cos_t, const void* sin_t, int64_t rope_rows,
+                              int64_t batch, int64_t n, int64_t pos0, void* k_cache, void* v_cache, int64_t cap,
+                              void* q_out, int64_t hq, int64_t hkv, int64_t head_dim, hipStream_t stream) {
   if (!qkv || !gamma_q || !gamma_k || !cos_t || !sin_t || !k_cache || !v_cache || !q_out)
     return fail(TFA_ERR_NULL, "tfa_prefill_qk_rope: null pointer argument");
   if (ks < 1 || ks > kMaxSplitsK)

@@ -388,8 +388,14 @@ bool full_rounds_256(int64_t m, int64_t n, int cus) {
 // K splits for the f32 store: a small grid (few token rows) of 128 x 128 tiles
 // is split along K -- doubling while the blocks still fit twice per CU, each
 // range keeps at least 4 k-tiles, and the count divides the k-tiles -- up to 8.
+// The split count sets the order the consumers sum the partials in, and so the
+// rounding of everything after the prompt prefill; it is therefore derived from
+// the shape and MI355X's fixed 256 CUs, never from the device's reported count,
+// so that a given prompt prefills to the same bits on any gfx950 part.
+constexpr int kSplitPlanCus = 256;
+
 int64_t splits_f32(int64_t m, int64_t n, int64_t k) {
-  const int cus = device_cus();
+  const int cus = kSplitPlanCus;
   if (full_rounds_256(m, n, cus) || n % 128 || k % kBK) return 1;
   const int64_t blocks = (m + 127) / 128 * (n / 128), nk = k / kBK;
   int64_t ks = 1;

@@ -762,8 +762,12 @@ int tfa_silu_mul(const float* part, int64_t ks, int64_t inter, int64_t rows, voi
   return launched("silu_mul");
 }
 
-int tfa_swiglu_pairs(const float* gu, int64_t ks, int64_t ld, int64_t rows, int64_t inter, void* act,
-                     hipStream_t stream) {
+int tfa_swiglu_pairs(const float* gu, int64_t ld, int64_t rows, int64_t inter, void* act, hipStream_t stream) {
+  return tfa_swiglu_pairs_split(gu, 1, ld, rows, inter, act, stream);
+}
+
+int tfa_swiglu_pairs_split(const float* gu, int64_t ks, int64_t ld, int64_t rows, int64_t inter, void* act,
+                           hipStream_t stream) {
   if (!gu || !act) return fail(TFA_ERR_NULL, "tfa_swiglu_pairs: null pointer argument");
   if (ks < 1 || ks > kMaxSplitsK) return fail(TFA_ERR_SHAPE, "tfa_swiglu_pairs: ks %lld not in [1, %d]", (long long)ks, kMaxSplitsK);
   if (inter < 4 || inter % 4 || rows < 1 || ld < 2 * inter || ld % 4)

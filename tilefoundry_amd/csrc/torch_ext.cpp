@@ -633,7 +633,7 @@ void swiglu_pairs(const Tensor& gu, const Tensor& act) {
   const int64_t R = gu.size(-2), I = gu.size(-1) / 2;
   need(act, "act", BF, R * I);
   if (gu.size(-1) != 2 * I) bad("gu: odd column count");
-  raise_status(tfa_swiglu_pairs(gu.data_ptr<float>(), ks, 2 * I, R, I, act.data_ptr(), stream_of(gu)));
+  raise_status(tfa_swiglu_pairs_split(gu.data_ptr<float>(), ks, 2 * I, R, I, act.data_ptr(), stream_of(gu)));
 }
 
 // qkv f32 (batch * n, ldq) or split-K partials (ks, batch * n, ldq); caches
@@ -655,7 +655,7 @@ void prefill_qk_rope(const Tensor& qkv, const Tensor& gamma_q, const Tensor& gam
   if (batch < 1 || KN < 1 || k_cache.size(-1) != KN || k_cache.numel() % (batch * KN) != 0)
     bad("k_cache / v_cache: expected (batch, cap, kv_heads * 128)");
   need(q_out, "q_out", BF, batch * n * hq * 128);
-  raise_status(tfa_prefill_qk_rope(qkv.data_ptr<float>(), ks, qkv.size(-1), gamma_q.data_ptr(), gamma_k.data_ptr(),
+  raise_status(tfa_prefill_qk_rope_split(qkv.data_ptr<float>(), ks, qkv.size(-1), gamma_q.data_ptr(), gamma_k.data_ptr(),
                                    (float)eps, cos.data_ptr(), sin.data_ptr(), cos.size(0), batch, n, pos0,
                                    k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() / (batch * KN),
                                    q_out.data_ptr(), hq, hkv, 128, stream_of(qkv)));
