@@ -311,7 +311,8 @@ def batch32(seed: int, steps: int = NEW_TOKENS, args=None) -> dict:
     out = {"value": round(gen.tokens_per_second, 1), "unit": "tok/s", "batch": 32, "new_tokens": steps,
            "prompt_tokens": PROMPT, "ms_per_step": round(ms, 4), "attention": eng.attention,
            "step_hbm": {"bytes_per_step": int(weight_bytes + kv_bytes),
-                        "GB/s": round((weight_bytes + kv_bytes) / (ms * 1e-3) / 1e9, 1)},
+                        "GB/s": round((weight_bytes + kv_bytes) / (ms * 1e-3) / 1e9, 1),
+                        "frac": round((weight_bytes + kv_bytes) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
            "prompt": {"walk": walk, "prefill": pre,
                       "speedup": round(walk["prompt_ms"] / pre["prompt_ms"], 1)}}
     del eng
@@ -423,6 +424,7 @@ def mla_decode(nblocks: int = 8) -> dict:
            "block_us": round(ms_blk * 1e3, 2),
            "block_bytes": int(cache + weights),
            "block_GB/s": round((cache + weights) / (ms_blk * 1e-3) / 1e9, 1),
+           "block_frac": round((cache + weights) / (ms_blk * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
            "attention_core_us": round(ms_core * 1e3, 2),
            "attention_core_bytes": int(cache),
            "attention_core_GB/s": round(cache / (ms_core * 1e-3) / 1e9, 1),
@@ -589,13 +591,22 @@ def cpu_baseline(seed: int, prompt: list[int]) -> dict:
                                       "sample": "one layer step over a 4096-position cache"}
     del kc, vc
 
-    # config 5 at bs=1: one greedy step of the 28-layer model per run, after a 4-token walk
-    caches = OQ.empty_caches(ocfg, ocfg.layers)
-    cos, sin = OQ.rope_tables(64, ocfg.head_dim, ocfg.rope_theta)
-    walk = prompt[:4]
-    for i, t in enumerate(walk):                  # untimed: also converts weights to f32
-        logits = OQ.step(model, ocfg, t, i, caches, cos, sin, p_bf16=True)
-    state = {"tok": OQ.greedy(logits), "pos": len(walk)}
+    # config 5: the greedy steps are timed at the GPU workload's mean context --
+    # a 64-token prompt then 2048 new tokens attend 1088 positions on average --
+    # over a synthetic cache of MEAN_CTX - 1 seeded rows per layer (the cost of a
+    # step depends on the context only through the attention's length)
+    mean_ctx = PROMPT + NEW_TOKENS // 2
+    cos, sin = OQ.rope_tables(mean_ctx + 16, ocfg.head_dim, ocfg.rope_theta)
+
+    def synthetic_caches(gen):
+        return [[torch.randn(mean_ctx - 1, ocfg.kv_heads, ocfg.head_dim, generator=gen).to(bf),
+                 torch.randn(mean_ctx - 1, ocfg.kv_heads, ocfg.head_dim, generator=gen).to(bf)]
+                for _ in range(ocfg.layers)]
+
+    # bs=1: one greedy step of the 28-layer model per run
+    caches = synthetic_caches(g)
+    logits = OQ.step(model, ocfg, prompt[0], mean_ctx - 1, caches, cos, sin, p_bf16=True)  # untimed
+    state = {"tok": OQ.greedy(logits), "pos": mean_ctx}
 
     def one_step():
         lg = OQ.step(model, ocfg, state["tok"], state["pos"], caches, cos, sin, p_bf16=True)
@@ -603,17 +614,19 @@ def cpu_baseline(seed: int, prompt: list[int]) -> dict:
 
     p = _protocol(one_step)
     head = {**_rate(p, 1.0, "tok/s"),
-            "sample": ("oracle (torch CPU, f32 matmuls) of the same 28-layer model: 9 greedy decode "
-                       "steps at bs=1 (2 untimed + 7 timed, one step per run) after a 4-token prompt "
-                       "walk, contexts 5..13")}
+            "sample": (f"oracle (torch CPU, f32 matmuls) of the same 28-layer model: 9 greedy decode "
+                       f"steps at bs=1 (2 untimed + 7 timed, one step per run) at contexts "
+                       f"{mean_ctx + 1}..{mean_ctx + 9} over a synthetic {mean_ctx - 1}-position cache "
+                       f"(the GPU workload's mean context is {mean_ctx})")}
+    del caches
 
-    # config 5 at bs=32: one batched greedy step of 32 sequences per run
+    # bs=32: one batched greedy step of 32 sequences per run
     B = 32
-    pr = OQ.prompt_ids(cfg.vocab, 4, seed=seed + 1, batch=B)
-    caches_b = [OQ.empty_caches(ocfg, ocfg.layers) for _ in range(B)]
-    for i in range(4):
-        logits = OQ.step_batch(model, ocfg, [row[i] for row in pr], [i] * B, caches_b, cos, sin, p_bf16=True)
-    st = {"tok": logits.argmax(-1).tolist(), "pos": 4}
+    pr = OQ.prompt_ids(cfg.vocab, 1, seed=seed + 1, batch=B)
+    caches_b = [synthetic_caches(g) for _ in range(B)]
+    logits = OQ.step_batch(model, ocfg, [row[0] for row in pr], [mean_ctx - 1] * B, caches_b, cos, sin,
+                           p_bf16=True)
+    st = {"tok": logits.argmax(-1).tolist(), "pos": mean_ctx}
 
     def batch_step():
         lg = OQ.step_batch(model, ocfg, st["tok"], [st["pos"]] * B, caches_b, cos, sin, p_bf16=True)
@@ -621,9 +634,9 @@ def cpu_baseline(seed: int, prompt: list[int]) -> dict:
 
     p = _protocol(batch_step)
     by["decode_bs32"] = {**_rate(p, float(B), "tok/s"),
-                         "sample": "9 batched greedy steps of 32 sequences (one step per run) after a "
-                                   "4-token prompt walk"}
-    del model, layers, caches, caches_b
+                         "sample": f"9 batched greedy steps of 32 sequences (one step per run) at contexts "
+                                   f"{mean_ctx + 1}..{mean_ctx + 9} over synthetic caches"}
+    del model, layers, caches_b
 
     # config 3: MLA attention block, batch 8, 8192 positions (absorbed form)
     mcfg = OM.MLAConfig()

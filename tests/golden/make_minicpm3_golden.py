@@ -4,13 +4,21 @@ full-model GPU test compares against: ``minicpm3_greedy_256.json``.
 
 The prompt is the MiniCPM3 decode benchmark's: 8 ids drawn by
 ``torch.randint(0, 73448, (8,), generator=torch.Generator().manual_seed(seed + 3))``.
-Then 256 greedy ids over the bf16 logits the model returns, and with them how
-far the oracle's other valid order (f32 softmax weights into the latent sum
-instead of bf16) lies from these logits along the same ids (``order_spread``).
-Stored per generated step: the id, the oracle's top-1 / top-2 gap and its 16
-largest logits with their ids, so that a test can measure the GPU logits' error
-at the candidates that decide the pick. The whole run is the oracle alone --
-nothing from the reference is imported or run. About 25 minutes on 8 cores.
+
+* ``free``: the oracle's free greedy run of 256 ids over the bf16 logits the
+  model returns. With random weights this model settles on one id at once
+  (the same id at every step), so it is kept as a check of the free run only;
+* ``forced``: 256 positions teacher-forced along seeded uniform-random ids
+  (``torch.randint(0, 73448, (255,), generator=torch.Generator().manual_seed(seed + 11))``),
+  so that the pick differs from position to position: per position the
+  oracle's pick, its top-1 / top-2 gap and its 16 largest logits with their
+  ids, and how far the oracle's other valid order (f32 softmax weights into
+  the latent sum instead of bf16) lies from these logits along the same ids
+  (``order_spread``).
+
+A test can then measure the GPU logits' error at the candidates that decide
+each pick. The whole run is the oracle alone -- nothing from the reference is
+imported or run. About 45 minutes on 8 cores.
 
     python tests/golden/make_minicpm3_golden.py [--steps 256] [--seed 0]
 """
@@ -60,11 +68,15 @@ def main():
     model = _model(cfg, args.seed)
     print(f"weights {time.time() - t0:.0f}s", flush=True)
     prompt = torch.randint(0, cfg.vocab, (PROMPT,), generator=torch.Generator().manual_seed(args.seed + 3)).tolist()
+    free = OM.decode(model, ocfg, prompt, args.steps, p_bf16=True)
+    print(f"free run {time.time() - t0:.0f}s", flush=True)
+    teacher = torch.randint(0, cfg.vocab, (args.steps - 1,),
+                            generator=torch.Generator().manual_seed(args.seed + 11)).tolist()
     rec = []
-    ids = OM.decode(model, ocfg, prompt, args.steps, record=rec, p_bf16=True)
-    print(f"decode {time.time() - t0:.0f}s", flush=True)
+    picks = OM.decode(model, ocfg, prompt, args.steps, record=rec, p_bf16=True, teacher=teacher)
+    print(f"forced {time.time() - t0:.0f}s", flush=True)
     alt = []
-    OM.decode(model, ocfg, prompt, args.steps, record=alt, p_bf16=False, teacher=ids)
+    OM.decode(model, ocfg, prompt, args.steps, record=alt, p_bf16=False, teacher=teacher)
     print(f"other order {time.time() - t0:.0f}s", flush=True)
     top_ids, top_vals, gaps, spread = [], [], [], []
     for (lg, _, _), (la, _, _) in zip(rec, alt):
@@ -73,19 +85,21 @@ def main():
         top_vals.append([float(v) for v in top.values])
         gaps.append(float(top.values[0] - top.values[1]))
         spread.append(float((la[top.indices].double() - top.values.double()).abs().max()))
-    alt_agree = sum(int(r[1] == t) for r, t in zip(alt, ids))
-    data = {"seed": args.seed, "prompt": prompt, "tokens": ids,
-            "order_spread": {"what": "oracle p_bf16=False teacher-forced along these ids: per-position max "
-                                     "|logit - golden logit| over the 16 candidates, and its picks' agreement",
-                             "deltas": spread, "agree": alt_agree},
-            "gaps": gaps, "top_ids": top_ids, "top_vals": top_vals,
-            "oracle": "oracle.minicpm3.decode(p_bf16=True)",
+    alt_agree = sum(int(r[1] == t) for r, t in zip(alt, picks))
+    data = {"seed": args.seed, "prompt": prompt,
+            "free": {"tokens": free, "oracle": "oracle.minicpm3.decode(p_bf16=True)"},
+            "forced": {"teacher_seed": args.seed + 11, "teacher": teacher, "tokens": picks,
+                       "order_spread": {"what": "oracle p_bf16=False along the same teacher: per-position max "
+                                                "|logit - golden logit| over the 16 candidates, and its picks' "
+                                                "agreement", "deltas": spread, "agree": alt_agree},
+                       "gaps": gaps, "top_ids": top_ids, "top_vals": top_vals,
+                       "oracle": "oracle.minicpm3.decode(p_bf16=True, teacher=teacher)"},
             "weights": "tilefoundry_amd.minicpm3.synthetic_model_weights",
             "first_logits_head": [round(float(v), 5) for v in rec[0][0][:8]]}
     out = Path(__file__).parent / "minicpm3_greedy_256.json"
     out.write_text(json.dumps(data) + "\n")
-    print(f"wrote {out}: {len(ids)} ids, orders agree {alt_agree}/{len(ids)}, min gap {min(gaps):.4g}, "
-          f"{time.time() - t0:.0f}s", flush=True)
+    print(f"wrote {out}: free run {len(set(free))} distinct ids; forced {len(set(picks))} distinct picks, "
+          f"orders agree {alt_agree}/{len(picks)}, min gap {min(gaps):.4g}, {time.time() - t0:.0f}s", flush=True)
 
 
 if __name__ == "__main__":

@@ -97,6 +97,13 @@ def test_gemv_attn_combine(K, dev):
     attn = ((op.double() * e[..., None]).sum(0) / (lp.double() * e).sum(0)[:, None]).to(BF)
     ref = attn.reshape(-1).double() @ w.double().t()
     assert_close("gemv_attn_combine", p.sum(0), ref, rtol=5e-3)
+    # a caller-owned workspace gives the same bits; a wrong one is refused
+    fn = K.gemv_attn_combine(HQ, D, H, 128, 128, SK, NS, 128)
+    p2 = torch.empty_like(p)
+    fn(op.to(dev), mp.to(dev), lp.to(dev), w.to(dev), p2, workspace=torch.empty(HQ * D, device=dev, dtype=BF))
+    assert torch.equal(p2, p)
+    with pytest.raises(ValueError, match="workspace"):
+        fn(op.to(dev), mp.to(dev), lp.to(dev), w.to(dev), p2, workspace=torch.empty(HQ * D, device=dev))
 
 
 @pytest.mark.gpu
@@ -110,6 +117,11 @@ def test_gemv_silu(K, dev):
     gb, ub = s[:I].to(BF), s[I:].to(BF)
     act = torch.nn.functional.silu(gb.float()).to(BF) * ub
     assert_close("gemv_silu", p.sum(0), act.double() @ w.double().t(), rtol=5e-3)
+    fn = K.gemv_silu(I, H, 128, 128, SK, SKG, 128)
+    p2 = torch.empty_like(p)
+    fn(gu.to(dev), w.to(dev), p2, workspace=torch.empty(I, device=dev, dtype=BF))
+    assert torch.equal(p2, p)
+    assert fn.reserve(torch.device(dev)).numel() == I
 
 
 @pytest.mark.gpu

@@ -11,7 +11,9 @@
 //
 // One block per (query head, 128 or 256 query rows, sequence): each wave (two
 // per SIMD) owns 32 query rows over the whole head dimension and walks the
-// 32-key tiles up to its diagonal. Per tile:
+// 32-key tiles up to its diagonal -- or, in 128-row blocks at head_dim 256 on
+// small grids, every other one of them, the two wave groups of the block
+// merging their softmax states at the end. Per tile:
 //
 //   S^T = K . Q^T     v_mfma_f32_32x32x16_bf16, M = 32 keys, N = 32 queries,
 //                     D/16 k-steps; Q^T is resident as the B operand, the
@@ -98,18 +100,28 @@ constexpr int kWaitVm0 = waitcnt_vm(0);
 template <int N>
 using IC = std::integral_constant<int, N>;
 
-// W waves of 32 query rows per block. W = 8 (256 rows, 3 stages, one block per
-// CU) halves the K/V bytes moved into LDS per FLOP against W = 4 (128 rows, 2
-// stages, two blocks per CU); both keep two waves per SIMD. D is the head
-// dimension (128 or 256); GATE applies the sigmoid output gate.
-template <int W, int D, bool GATE>
-__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// W waves of 32 query rows per block, times KG key groups. W = 8 (256 rows, 3
+// stages, one block per CU) halves the K/V bytes moved into LDS per FLOP
+// against W = 4 (128 rows, 2 stages, two blocks per CU); both keep two waves
+// per SIMD. KG = 2 (with W = 4) splits the keys of one 128-row tile between two
+// wave groups over the same rows: group g takes key tiles g, g + 2, ..., each
+// step brings one tile per group, and the groups' (max, sum, output) merge
+// through LDS at the end. That halves the longest walk of a block, keeps two
+// waves per SIMD with one block per CU, and makes the causal work finer
+// grained, so the grid balances where the longest 256-row tile would outlast
+// the average load of a CU. D is the head dimension (128 or 256); GATE
+// applies the sigmoid output gate.
+template <int W, int D, bool GATE, int KG = 1>
+__global__ __launch_bounds__(W * KG * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_prefill_kernel(const FlashArgs a) {
+  static_assert(KG == 1 || (KG == 2 && W == 4), "key groups: one, or two with 128-row blocks");
   constexpr int QT = 1;       // 32-row query tiles per wave
   constexpr int kWM = 32 * QT;
   constexpr int kBM = kWM * W;                 // query rows per block
-  constexpr int kStages = W == 8 ? 3 : 2;      // loads run kStages - 1 tiles ahead
-  constexpr int kRowsPerWave = kBN / W;        // K and V rows each wave moves per tile
+  constexpr int NW = W * KG;                   // waves per block
+  constexpr int kStages = W == 8 ? 3 : 2;      // loads run kStages - 1 steps ahead
+  constexpr int kTK = kBN * KG;                // keys per step (one tile per key group)
+  constexpr int kRowsPerWave = kTK / NW;       // K and V rows each wave moves per step
   constexpr int kKPitch = D;                   // elements: rows are unpadded, chunks swizzled
   constexpr int kVPitch = D;
   constexpr int kRowBytes = 2 * D;
@@ -128,12 +140,14 @@ void flash_prefill_kernel(const FlashArgs a) {
   constexpr int kKPF = kTight ? 3 : 4;
   constexpr int kVPF = kTight ? 2 : 3;
   // one LDS object per ring stage, indexed only by compile-time stage numbers
-  __shared__ __attribute__((aligned(1024))) uint16_t ks0[kBN][kKPitch];
-  __shared__ __attribute__((aligned(1024))) uint16_t ks1[kBN][kKPitch];
-  __shared__ __attribute__((aligned(1024))) uint16_t ks2[kStages == 3 ? kBN : 1][kKPitch];
-  __shared__ __attribute__((aligned(1024))) uint16_t vs0[kBN][kVPitch];
-  __shared__ __attribute__((aligned(1024))) uint16_t vs1[kBN][kVPitch];
-  __shared__ __attribute__((aligned(1024))) uint16_t vs2[kStages == 3 ? kBN : 1][kVPitch];
+  __shared__ __attribute__((aligned(1024))) uint16_t ks0[kTK][kKPitch];
+  __shared__ __attribute__((aligned(1024))) uint16_t ks1[kTK][kKPitch];
+  __shared__ __attribute__((aligned(1024))) uint16_t ks2[kStages == 3 ? kTK : 1][kKPitch];
+  __shared__ __attribute__((aligned(1024))) uint16_t vs0[kTK][kVPitch];
+  __shared__ __attribute__((aligned(1024))) uint16_t vs1[kTK][kVPitch];
+  __shared__ __attribute__((aligned(1024))) uint16_t vs2[kStages == 3 ? kTK : 1][kVPitch];
+  // the second key group's running max and sum per lane, for the final merge
+  __shared__ float ml_part[KG == 2 ? 2 : 1][KG == 2 ? W : 1][kWave];
   auto kbuf = [&](auto b) __attribute__((always_inline)) -> uint16_t(*)[kKPitch] {
     if constexpr (decltype(b)::value == 0) return ks0;
     else if constexpr (decltype(b)::value == 1) return ks1;
@@ -147,6 +161,8 @@ void flash_prefill_kernel(const FlashArgs a) {
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int rw = wid % W;        // the wave's 32 query rows within the block
+  const int kgi = wid / W;       // its key group: key tiles kgi, kgi + KG, ...
   const int n32 = lane & 31;
   const int kg = lane >> 5;
   const int N = a.N;
@@ -169,10 +185,12 @@ void flash_prefill_kernel(const FlashArgs a) {
   const int g = h / (a.HQ / a.HKV);
   const uint16_t* kseq = a.k + b * a.k_bs + g * a.k_hs;
   const uint16_t* vseq = a.v + b * a.v_bs + g * a.v_hs;
-  const int q0 = qt * kBM + wid * kWM;          // the wave's first query row
-  // key tiles the block walks: up to its last row, and no tile wholly past N
+  const int q0 = qt * kBM + rw * kWM;           // the wave's first query row
+  // key tiles the block walks: up to its last row, and no tile wholly past N;
+  // a step brings KG consecutive tiles
   const int kend = min((qt + 1) * kBM, N);
   const int ntiles = (kend + kBN - 1) / kBN;
+  const int nsteps = (ntiles + KG - 1) / KG;
   const int my_last = min((q0 + kWM - 1) / kBN, ntiles - 1);   // the wave's last tile with a visible key
 
   // Direct global -> LDS tile loads, 1 KB per instruction: the 64 lanes fill
@@ -183,19 +201,21 @@ void flash_prefill_kernel(const FlashArgs a) {
   // fetches the logical chunk its physical slot holds. Wave w moves rows
   // R w .. R w + R - 1 of K and of V (R = 32 / W). Rows past N repeat row
   // N - 1 (only rows past N see them, and those rows are not stored). Every
-  // step issues exactly one tile's loads (past the last tile it reloads the
-  // last tile into a free stage, where nothing reads it), so the number of
-  // loads in flight behind tile kt is constant and so is every wait count.
+  // step issues exactly one step's loads (past the last step it reloads the
+  // last step into a free stage, where nothing reads it), so the number of
+  // loads in flight behind step ks is constant and so is every wait count.
+  // Stage row j holds key kTK ks + j: tile KG ks + j / 32, whose rows keep the
+  // same swizzle as a one-tile stage (32 is a multiple of 16).
   const int dma_row = lane / kCPR, dma_chunk = lane % kCPR;
-  auto load_tile = [&](int kt, auto bs) __attribute__((always_inline)) {
-    kt = kt < ntiles ? kt : ntiles - 1;
+  auto load_tile = [&](int ks, auto bs) __attribute__((always_inline)) {
+    ks = ks < nsteps ? ks : nsteps - 1;
     uint16_t(*kb)[kKPitch] = kbuf(bs);
     uint16_t(*vb)[kVPitch] = vbuf(bs);
 #pragma unroll
     for (int i = 0; i < kInstr; ++i) {
-      const int t0 = kRowsPerWave * wid + kRPI * i;     // first tile row of this instruction
+      const int t0 = kRowsPerWave * wid + kRPI * i;     // first stage row of this instruction
       const int trow = t0 + dma_row;
-      const size_t r = static_cast<size_t>(min(kt * kBN + trow, N - 1));
+      const size_t r = static_cast<size_t>(min(ks * kTK + trow, N - 1));
       lds_dma16(kseq + r * a.k_rs + 8 * (dma_chunk ^ (trow & 15)), lds_offset(&kb[t0][0]));
       lds_dma16(vseq + r * a.v_rs + 8 * (dma_chunk ^ (4 * (trow & 3))), lds_offset(&vb[t0][0]));
     }
@@ -244,19 +264,21 @@ void flash_prefill_kernel(const FlashArgs a) {
   // 2 half16 + (L & 3) / 2 + 4 dt, physical ... + 4 (dt ^ q) with q = (L / 4) & 3
   // -- the swizzle bits (5-7 for K, 6-7 for V) are zero in the rest of the
   // lane's base, so each address is that base XOR a compile-time constant.
-  const int k_base = n32 * kRowBytes + 16 * (kg ^ (n32 & 1)) + 32 * ((n32 & 15) >> 1);
-  const int v_base = (4 * kg + (L >> 2)) * kRowBytes + 16 * (2 * half16 + ((L & 3) >> 1)) + 8 * (L & 1) +
+  // (plus the wave's key group's 32-row half of the stage)
+  const int k_base = (32 * kgi + n32) * kRowBytes + 16 * (kg ^ (n32 & 1)) + 32 * ((n32 & 15) >> 1);
+  const int v_base = (32 * kgi + 4 * kg + (L >> 2)) * kRowBytes + 16 * (2 * half16 + ((L & 3) >> 1)) + 8 * (L & 1) +
                      64 * ((L >> 2) & 3);
   // One key tile in ring stage `bs`. The block barrier is a bare s_barrier
   // between compiler fences: each wave first waits for its own loads of tile
   // kt (the only ones in flight), and its reads of the stage being refilled --
   // tile kt - 1's -- were consumed by MFMAs of the previous step before it
   // arrives.
-  auto step = [&](int kt, auto bs) __attribute__((always_inline)) {
+  auto step = [&](int ks, auto bs) __attribute__((always_inline)) {
     constexpr int B = decltype(bs)::value;
-    __builtin_amdgcn_s_waitcnt(kWaitStep);   // tile kt landed; with three stages tile kt + 1 may fly
+    __builtin_amdgcn_s_waitcnt(kWaitStep);   // step ks landed; with three stages step ks + 1 may fly
     block_barrier();
-    load_tile(kt + kStages - 1, IC<(B + kStages - 1) % kStages>{});   // into the stage of tile kt - 1
+    load_tile(ks + kStages - 1, IC<(B + kStages - 1) % kStages>{});   // into the stage of step ks - 1
+    const int kt = KG * ks + kgi;            // this wave's key tile
     uint16_t(*kb)[kKPitch] = kbuf(bs);
     uint16_t(*vb)[kVPitch] = vbuf(bs);
 
@@ -369,14 +391,52 @@ void flash_prefill_kernel(const FlashArgs a) {
       }
     }
   };
-  for (int kt = 0; kt < ntiles; kt += kStages) {
-    step(kt, IC<0>{});
-    if (kt + 1 < ntiles) step(kt + 1, IC<1>{});
+  for (int ks = 0; ks < nsteps; ks += kStages) {
+    step(ks, IC<0>{});
+    if (ks + 1 < nsteps) step(ks + 1, IC<1>{});
     if constexpr (kStages == 3)
-      if (kt + 2 < ntiles) step(kt + 2, IC<2>{});
+      if (ks + 2 < nsteps) step(ks + 2, IC<2>{});
   }
   // no load may still be writing this block's LDS when the block ends
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
+
+  if constexpr (KG == 2) {
+    // Merge the key groups: the second group leaves its (max, sum, output)
+    // in the stage buffers (every wave is past its last operand read), the
+    // first rescales both to the joint max and adds. A group that saw no key
+    // has max -inf and contributes nothing. The output is 128 f32 per lane,
+    // stored lane-fastest in 16-byte pieces (each instruction 1 KB contiguous).
+    lds_barrier();
+    float4* part = reinterpret_cast<float4*>(rw == 0 ? &ks0[0][0] : rw == 1 ? &ks1[0][0] : rw == 2 ? &vs0[0][0]
+                                                                                                   : &vs1[0][0]);
+    if (kgi == 1) {
+#pragma unroll
+      for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          part[(4 * dt + j) * kWave + lane] = make_float4(o[dt][0][4 * j], o[dt][0][4 * j + 1], o[dt][0][4 * j + 2],
+                                                          o[dt][0][4 * j + 3]);
+      ml_part[0][rw][lane] = m_run[0];
+      ml_part[1][rw][lane] = l_run[0];
+    }
+    lds_barrier();
+    if (kgi == 1) return;
+    const float m1 = ml_part[0][rw][lane], l1 = ml_part[1][rw][lane];
+    const float mj = fmaxf(m_run[0], m1);
+    const float a0 = m_run[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[0] - mj);
+    const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mj);
+    l_run[0] = l_run[0] * a0 + l1 * a1;
+#pragma unroll
+    for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 p1 = part[(4 * dt + j) * kWave + lane];
+        o[dt][0][4 * j] = o[dt][0][4 * j] * a0 + p1.x * a1;
+        o[dt][0][4 * j + 1] = o[dt][0][4 * j + 1] * a0 + p1.y * a1;
+        o[dt][0][4 * j + 2] = o[dt][0][4 * j + 2] * a0 + p1.z * a1;
+        o[dt][0][4 * j + 3] = o[dt][0][4 * j + 3] * a0 + p1.w * a1;
+      }
+  }
 
   // epilogue: element e = 4j + r of o[dt][t] is value dim 32 dt + 8j + 4kg + r
   // of query q0 + 32 t + n32
@@ -422,11 +482,20 @@ int xcd_heads(int64_t heads, int64_t kv_heads) {
 // (64- and 32-row blocks were measured slower on short prompts: a block walks
 // its key tiles one after another with one tile of look-ahead, so thinner
 // blocks only add more serial walks of the same latency.)
+//
+// Below that, head_dim 256 takes the 128-row blocks with the keys split over two
+// wave groups: 8 waves and 133 KB of LDS, one block per CU (24 heads x 1024
+// tokens: 43.5 -> 41 us; x 2048: 86.5 -> 80.5 us against 4 waves per block).
+// At 4096 and 8192 tokens the 256-row blocks stay faster (211 against 236 us,
+// 751 against 822 us), and head_dim 128 (the decode model's prompt prefill)
+// measured the same either way, so it keeps its one key group.
 template <int D, bool GATE>
 int launch_flash(const FlashArgs& a, int64_t batch, hipStream_t stream, const char* name) {
   const int64_t t256 = (a.N + 255) / 256, t128 = (a.N + 127) / 128;
   if (a.HQ * t256 * batch >= 256)
     flash_prefill_kernel<8, D, GATE><<<dim3((unsigned)(a.HQ * t256), (unsigned)batch), 8 * kWave, 0, stream>>>(a);
+  else if constexpr (D == 256)
+    flash_prefill_kernel<4, D, GATE, 2><<<dim3((unsigned)(a.HQ * t128), (unsigned)batch), 8 * kWave, 0, stream>>>(a);
   else
     flash_prefill_kernel<4, D, GATE><<<dim3((unsigned)(a.HQ * t128), (unsigned)batch), 4 * kWave, 0, stream>>>(a);
   return launched(name);

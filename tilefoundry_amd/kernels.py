@@ -21,9 +21,12 @@ Departures, each forced by the hardware or stated for the caller:
   meaning: a partial buffer ``P[SK, N]`` holds split ``s``'s dot over the
   ``s``-th contiguous ``K / SK`` slice, and consumers sum the splits in order.
 * **Workspaces.** ``gemv_attn_combine`` and ``gemv_silu`` are two launches here
-  (merge / activation, then the GEMV) with the intermediate vector in a
-  per-device buffer the callable allocates on its first call and keeps; later
-  calls allocate nothing.
+  (merge / activation, then the GEMV) through an intermediate bf16 vector
+  (``HQ * D`` or ``I`` elements). The caller may own it -- ``workspace=`` on the
+  call, then nothing allocates -- or leave it to the callable, which allocates
+  one buffer per device on that device's first call and keeps it (so the first
+  call must not be the one under graph capture; ``callable.reserve(device)``
+  allocates it ahead).
 * **Block winners.** ``lm_head`` returns ``(kernel, NB)`` like the reference,
   with ``NB`` the gfx950 head's own count of 16-row blocks.
 
@@ -68,12 +71,19 @@ def _partials(P: torch.Tensor, sk: int, n: int, name: str = "P") -> None:
 
 
 class _Workspace:
-    """One buffer per device, allocated on first use and kept."""
+    """One buffer per device, allocated on first use and kept -- or the
+    caller's own (``given``), checked and used as is."""
 
     def __init__(self, n: int, dtype: torch.dtype):
         self.n, self.dtype, self.bufs = n, dtype, {}
 
-    def get(self, device: torch.device) -> torch.Tensor:
+    def get(self, device: torch.device, given: torch.Tensor | None = None) -> torch.Tensor:
+        if given is not None:
+            if given.dtype != self.dtype or given.numel() != self.n or not given.is_contiguous() \
+                    or given.device != torch.device(device):
+                raise ValueError(f"workspace: expected a contiguous {self.dtype} tensor of {self.n} elements "
+                                 f"on {device}, got {given.dtype} {tuple(given.shape)} on {given.device}")
+            return given
         buf = self.bufs.get(device)
         if buf is None:
             buf = torch.empty(self.n, device=device, dtype=self.dtype)
@@ -137,15 +147,16 @@ def gemv_attn_combine(HQ: int, D: int, N: int, BN: int, BK: int, SK: int, NS: in
     K = HQ * D
     ws = _Workspace(K, torch.bfloat16)
 
-    def main(Op, Mp, Lp, W, P):
+    def main(Op, Mp, Lp, W, P, workspace=None):
         if Op.numel() != NS * HQ * D or Mp.numel() != NS * HQ or Lp.numel() != NS * HQ:
             raise ValueError(f"Op / Mp / Lp: expected ({NS}, {HQ}, {D}) / ({NS}, {HQ})")
         _partials(P, SK, N)
         w = _weight(W, N, K)
-        attn = ws.get(Op.device)
+        attn = ws.get(Op.device, workspace)
         C.attn_combine(Op.view(NS, HQ, D), Mp.view(NS, HQ), Lp.view(NS, HQ), attn, None, 0)
         _split_gemv(attn, w, P, SK)
 
+    main.reserve = ws.get
     return main
 
 
@@ -159,14 +170,15 @@ def gemv_silu(I: int, N: int, BN: int, BK: int, SK: int, SKG: int, threads: int,
     _positive(I=I, N=N, BN=BN, BK=BK, SK=SK, SKG=SKG, threads=threads, stages=stages)
     ws = _Workspace(I, torch.bfloat16)
 
-    def main(GU, W, P):
+    def main(GU, W, P, workspace=None):
         _partials(GU, SKG, 2 * I, "GU")
         _partials(P, SK, N)
         w = _weight(W, N, I)
-        act = ws.get(GU.device)
+        act = ws.get(GU.device, workspace)
         C.silu_mul(GU.view(SKG, 2 * I), act)
         _split_gemv(act, w, P, SK)
 
+    main.reserve = ws.get
     return main
 
 
