@@ -384,6 +384,15 @@ def minicpm3_decode(seed: int, lengths=MINICPM3_LENGTHS, args=None) -> dict:
         out["by_new_tokens"][str(n)] = {"tok/s": round(tps, 1), "ms_per_step": round(gen.seconds * 1e3 / n, 4),
                                         "vs_reference_h200": round(tps / ref[n], 3)}
     out["first_tokens"] = gen.tokens[0][:8]
+    # the reference's default sampling (T = 0.8, top-p 0.8), drawn on the device in the step
+    from tilefoundry_amd.minicpm3 import sample_top_p
+
+    n = MINICPM3_LENGTHS[1]
+    eng.generate([prompt], 8, sampler=sample_top_p(0.8, 0.8, seed=seed))   # captures the sampling step
+    gen = eng.generate([prompt], n, sampler=sample_top_p(0.8, 0.8, seed=seed))
+    out["top_p_sampled"] = {"new_tokens": n, "tok/s": round(gen.tokens_per_second, 1),
+                            "ms_per_step": round(gen.seconds * 1e3 / n, 4), "temperature": 0.8, "top_p": 0.8,
+                            "first_tokens": gen.tokens[0][:8]}
     del eng
     torch.cuda.empty_cache()
     return out

@@ -329,6 +329,22 @@ int tfa_batch_sample_step(const float* block_val, const int* block_idx, int64_t 
                           int64_t batch, const int* inp, const int* prompt_len, int64_t* ids,
                           int* pos, int* sam, int64_t nsteps, int* err, hipStream_t stream);
 
+/* The sampling step for `batch` sequences (vocab <= 81920): per sequence b,
+ * probabilities softmax(logits[b] / T) (logits [batch, vocab] f32); ranked in
+ * descending order (ties in index order), a token is kept while the mass ranked
+ * before it is below top_p; one draw from the kept mass with a counter-based
+ * generator of (seed[0], b, pos[b]) -- reproducible, and a different stream per
+ * sequence and position. params = {T, top_p} (device f32[2], T > 0, top_p > 0).
+ * Then sam[b, pos[b]] = the draw; ids[b] = pos[b]+1 < prompt_len[b] ?
+ * inp[b, pos[b]+1] : the draw; pos[b] += 1 (inp / sam [batch, nsteps]).
+ * err (optional): 2 = pos out of [0, nsteps).
+ * Replaces: examples/minicpm3_4b-cutedsl/run.py:29-47 (_sampler: T = 0.8,
+ * top-p 0.8), drawn on the device inside the captured step instead of on the
+ * host after it. */
+int tfa_top_p_sample_step(const float* logits, int64_t vocab, int64_t batch, const float* params,
+                          const int64_t* seed, const int* inp, const int* prompt_len, int64_t* ids, int* pos,
+                          int* sam, int64_t nsteps, int* err, hipStream_t stream);
+
 /* ------------------------------------------ MLA decode, absorbed (MiniCPM3) */
 
 /* Per sequence b (batch <= 65535): reduce the split-K partials part

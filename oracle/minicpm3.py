@@ -36,6 +36,15 @@ What each function follows (jingchangshi/TileFoundry):
 * ``o_proj_residual`` -- ``gemv_residual``, reference_ops.py:63-65:
   ``residual + bf16(x @ W_o^T) * alpha``, each step landing in bf16.
 
+* ``top_p_kept`` -- the token set and probabilities the sampler of
+  examples/minicpm3_4b-cutedsl/run.py:29-47 (``_sampler``) draws from:
+  softmax of ``logits / T`` in f32, ranked in descending order (a stable sort:
+  ties in index order), a token kept while the mass ranked before it is below
+  ``top_p``; the draw is proportional to the kept probabilities. Pinned
+  (tests/test_oracle.py) by closed forms: one dominant logit keeps that token
+  alone, a uniform row keeps the first ceil(top_p V) tokens, and top_p >= 1 keeps
+  every token of nonzero probability.
+
 Weights are ``(out, in)``: ``w_kv_b`` rows ``h*128 .. h*128+63`` are head h's
 ``W_UK`` and rows ``h*128+64 .. h*128+127`` its ``W_UV`` (the ``[k_nope | v]``
 split of model.py:247-250).
@@ -411,3 +420,17 @@ def decode(model: ModelWeights, cfg: ModelConfig, prompt: list, max_new: int, re
             nxt = teacher[i] if teacher is not None else pick
             logits = decode_step(model, cfg, nxt, len(prompt) + i, caches, cos, sin, p_bf16)
     return out
+
+
+def top_p_kept(logits: torch.Tensor, temperature: float, top_p: float):
+    """``(ids, probs)`` of the tokens the run.py sampler may draw for one row of
+    logits, and their probabilities renormalised over the kept set (the
+    distribution of its one multinomial draw). Ties are ranked in index order."""
+    probs = torch.softmax(logits.reshape(-1).float() / temperature, dim=-1)
+    order = torch.sort(probs, descending=True, stable=True).indices
+    ranked = probs[order]
+    before = torch.cumsum(ranked, dim=-1) - ranked
+    keep = before < top_p
+    ids = order[keep]
+    kept = ranked[keep].double()
+    return ids, kept / kept.sum()

@@ -130,6 +130,90 @@ def test_minicpm3_sampler(dev):
     assert a == b
     assert eng.generate(prompt, 16, sampler=sample_top_p(0.8, 1e-9, g)).tokens == greedy
     assert all(0 <= t < cfg.vocab for t in a[0])
+    c = eng.generate(prompt, 16, sampler=sample_top_p(0.8, 0.8, seed=2)).tokens
+    assert c != a, "another seed gives another continuation"
+    # the greedy step is untouched by the sampling graph beside it
+    assert eng.generate(prompt, 16).tokens == greedy
+
+
+def _draws(dev, logits, temperature, top_p, n, seed=0):
+    """``n`` top-p draws per row of ``logits`` [B, V]: the sampling step run n
+    times, each at the next position (the generator's counter)."""
+    from tilefoundry_amd._lib import C
+
+    B, V = logits.shape
+    lg = logits.to(dev).float().contiguous()
+    params = torch.tensor([temperature, top_p], dtype=torch.float32, device=dev)
+    sd = torch.tensor([seed], dtype=torch.int64, device=dev)
+    inp = torch.zeros(B, n + 1, dtype=torch.int32, device=dev)
+    plen = torch.zeros(B, dtype=torch.int32, device=dev)
+    ids = torch.zeros(B, dtype=torch.int64, device=dev)
+    pos = torch.zeros(B, dtype=torch.int32, device=dev)
+    sam = torch.full((B, n + 1), -1, dtype=torch.int32, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    for _ in range(n):
+        C.top_p_sample_step(lg, params, sd, inp, plen, ids, pos, sam, err)
+    torch.cuda.synchronize()
+    assert int(err) == 0 and pos.tolist() == [n] * B
+    assert torch.equal(ids, sam[:, n - 1].long()), "the draw is fed as the next input"
+    return sam[:, :n].cpu()
+
+
+@pytest.mark.gpu
+def test_top_p_step_draws_from_the_kept_set(dev):
+    """The device sampling step against the run.py sampler's kept set and
+    probabilities (oracle ``top_p_kept``) on bf16-valued logits over the full
+    73448-token vocabulary: every draw is a kept token, and the frequencies of
+    the likeliest kept tokens match their probabilities within 5 sigma over
+    32 x 400 draws."""
+    V, B, n = 73448, 32, 400
+    g = torch.Generator().manual_seed(31)
+    row = (2.5 * torch.randn(V, generator=g)).to(BF16).float()
+    ids, probs = OM.top_p_kept(row, 0.8, 0.8)
+    draws = _draws(dev, row.expand(B, V), 0.8, 0.8, n).flatten()
+    kept = torch.zeros(V, dtype=torch.bool)
+    kept[ids] = True
+    assert bool(kept[draws.long()].all()), "a draw outside the kept set"
+    counts = torch.bincount(draws.long(), minlength=V).double()
+    N = draws.numel()
+    for i, p in zip(ids[:20].tolist(), probs[:20].tolist()):
+        sigma = (N * p * (1 - p)) ** 0.5
+        assert abs(counts[i] - N * p) <= 5 * sigma + 1, (i, counts[i], N * p)
+    # each sequence (block row) draws its own stream
+    per_row = draws.view(B, n)
+    assert not torch.equal(per_row[0], per_row[1])
+
+
+@pytest.mark.gpu
+def test_top_p_step_ties_and_limits(dev):
+    """Ties at the kept boundary are kept in index order (a stable ranking); a
+    uniform row keeps its first ceil(top_p V) tokens; a vanishing top_p gives
+    the lowest-index greedy pick; a position past the buffers is flagged."""
+    V = 4096
+    tie = torch.full((V,), -1.0e4)        # probability zero past the first four tokens
+    tie[0], tie[1:4] = 10.0, 5.0          # e^-5 each: the mass before the third tie is past 0.99
+    ids, _ = OM.top_p_kept(tie, 1.0, 0.99)
+    assert ids.tolist() == [0, 1, 2]
+    d = _draws(dev, tie.expand(32, V), 1.0, 0.99, 100)
+    assert set(d.flatten().tolist()) <= {0, 1, 2}
+    uni = torch.zeros(V)
+    d = _draws(dev, uni.expand(32, V), 1.0, 0.25, 50)
+    assert int(d.max()) < V // 4 and len(set(d.flatten().tolist())) > 500
+    peaks = torch.zeros(V)
+    peaks[[7, 900, 3000]] = 3.0           # three equal maxima: greedy takes the lowest index
+    d = _draws(dev, peaks.expand(4, V), 0.8, 1e-9, 20)
+    assert set(d.flatten().tolist()) == {7}
+    from tilefoundry_amd._lib import C
+
+    lg = torch.zeros(1, V, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    pos = torch.tensor([5], dtype=torch.int32, device=dev)
+    C.top_p_sample_step(lg, torch.tensor([1.0, 0.5], device=dev), torch.zeros(1, dtype=torch.int64, device=dev),
+                        torch.zeros(1, 4, dtype=torch.int32, device=dev), torch.zeros(1, dtype=torch.int32, device=dev),
+                        torch.zeros(1, dtype=torch.int64, device=dev), pos,
+                        torch.zeros(1, 4, dtype=torch.int32, device=dev), err)
+    torch.cuda.synchronize()
+    assert int(err) == 2 and int(pos) == 5
 
 
 @pytest.mark.gpu

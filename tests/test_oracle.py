@@ -919,3 +919,28 @@ def test_prefill_o_proj_double_landing_f64_and_known_answer():
     h2 = torch.ones(1, 4).to(BF)
     assert torch.equal(OP.o_proj(g2, h2, w2), torch.ones(1, 4).to(BF))
     assert torch.equal((h2.float() + g2.float() @ w2.float().t()).to(BF), torch.full((1, 4), 1 + 2 ** -7).to(BF))
+
+
+def test_top_p_kept_closed_forms():
+    """The sampler's kept set: one dominant logit keeps it alone; a uniform row
+    keeps the first ceil(top_p V) tokens in index order with equal
+    probabilities; top_p >= 1 keeps every token of nonzero probability; a
+    planted mistake (keeping while the mass *including* the token is below
+    top_p) drops the boundary token of the uniform row."""
+    from oracle import minicpm3 as OM
+
+    lg = torch.zeros(1000)
+    lg[417] = 100.0
+    ids, p = OM.top_p_kept(lg, 0.8, 0.8)
+    assert ids.tolist() == [417] and float(p[0]) == 1.0
+    uni = torch.zeros(1000)
+    for top_p in (0.25, 0.5, 0.8, 0.999):
+        ids, p = OM.top_p_kept(uni, 1.0, top_p)
+        n = math.ceil(top_p * 1000 - 1e-9)
+        assert ids.tolist() == list(range(n)), (top_p, len(ids))
+        assert float((p - 1.0 / n).abs().max()) < 1e-12
+    ids, _ = OM.top_p_kept(torch.randn(500, generator=g(70)), 0.8, 1.0)
+    assert sorted(ids.tolist()) == list(range(500))
+    probs = torch.softmax(uni / 1.0, -1)
+    wrong = (torch.cumsum(probs, -1) < 0.25).sum()   # mass including the token
+    assert int(wrong) != len(OM.top_p_kept(uni, 1.0, 0.25)[0])

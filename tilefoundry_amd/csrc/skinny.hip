@@ -433,6 +433,218 @@ __global__ __launch_bounds__(kSampleThreads) void batch_sample_kernel(
   }
 }
 
+// ------------------------------------------------------------- top-p sampling
+// The sampling step of MiniCPM3's run.py (examples/minicpm3_4b-cutedsl/run.py:29-47,
+// `_sampler`): probabilities softmax(logits / T); ranked in descending order, a
+// token is kept while the mass ranked before it is below top_p; one draw from
+// the kept mass. One 512-thread block per sequence, thread t holding the
+// vocabulary slice [t * per, t * per + per) in registers:
+//   1. e = exp((logit - max logit) / T), Z = sum e;
+//   2. the smallest f32 bit pattern tau with f(tau) = sum_{e > tau} e < top_p Z,
+//      by binary search (positive floats order as their bit patterns): tau is
+//      then itself a value of e, every e > tau is kept, and of the tokens equal
+//      to tau those of tie rank r (in index order) with f(tau) + r tau < top_p Z
+//      -- the prefix a stable descending sort would keep;
+//   3. u in (0, 1) from a counter-based generator of (seed, sequence, position),
+//      and the kept token where the running kept mass, in index order, first
+//      exceeds u times the kept total (the distribution of a multinomial draw
+//      over the ranked kept mass).
+// Then the feed / advance of the greedy step: sam[b, pos] = the draw; the next
+// input is the next prompt id while the prompt lasts, else the draw; pos + 1.
+// Sums and scans run in a fixed order, so a draw is reproducible.
+constexpr int kTopPThreads = 512;                      // two waves per SIMD: 256 registers a thread
+constexpr int kTopPWaves = kTopPThreads / kWave;
+constexpr int kTopPPer = 144;                          // vocabulary <= 73728
+
+TFA_DEV uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// Block-wide sum (every thread gets it), the waves' sums added in wave order.
+// `slot` alternates between calls so that one barrier per call suffices.
+TFA_DEV float topp_block_sum(float v, float (*red)[kTopPWaves], int& slot) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  if (lane == 0) red[slot][wid] = v;
+  lds_barrier();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kTopPWaves; ++w) tot += red[slot][w];
+  slot ^= 1;
+  return tot;
+}
+
+TFA_DEV float topp_block_max(float v, float (*red)[kTopPWaves], int& slot) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  if (lane == 0) red[slot][wid] = v;
+  lds_barrier();
+  float m = red[slot][0];
+#pragma unroll
+  for (int w = 1; w < kTopPWaves; ++w) m = fmaxf(m, red[slot][w]);
+  slot ^= 1;
+  return m;
+}
+
+// Exclusive prefix sum over the threads in thread order (and the total).
+TFA_DEV float topp_block_exscan(float v, float (*red)[kTopPWaves], int& slot, float& total) {
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  float inc = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const float o = __shfl_up(inc, d, kWave);
+    if (lane >= d) inc += o;
+  }
+  if (lane == kWave - 1) red[slot][wid] = inc;
+  lds_barrier();
+  float base = 0.f;
+  total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kTopPWaves; ++w) {
+    if (w < wid) base += red[slot][w];
+    total += red[slot][w];
+  }
+  slot ^= 1;
+  return base + inc - v;
+}
+
+__global__ __launch_bounds__(kTopPThreads) void top_p_sample_kernel(
+    const float* __restrict__ logits, int vocab, const float* __restrict__ params, const int64_t* __restrict__ seed,
+    const int* inp, const int* plen, int64_t* ids, int* pos, int* sam, int nsteps, int* err) {
+  __shared__ float red[2][kTopPWaves];
+  __shared__ int s_pick, s_last;
+  const int b = blockIdx.x;
+  const int t = threadIdx.x;
+  int slot = 0;
+  const int p = pos[b];
+  const int pl = plen[b];
+  const int nxt = inp[static_cast<size_t>(b) * nsteps + min(max(p + 1, 0), nsteps - 1)];
+  const float temp = params[0], top_p = params[1];
+  const uint64_t sd = static_cast<uint64_t>(seed[0]);
+  const int per = (vocab + kTopPThreads - 1) / kTopPThreads;
+  const int i0 = t * per;
+  const float* row = logits + static_cast<size_t>(b) * vocab;
+  if (t == 0) {
+    s_pick = -1;
+    s_last = -1;
+  }
+  // 1. softmax numerators
+  // every load from one per-lane base (immediate offsets, one memory round
+  // trip): a slice that would run past the vocabulary is shifted back inside
+  // it, and the slots that do not belong to this thread are masked once the
+  // values are in
+  float e[kTopPPer];
+  const int nin = min(per, vocab - i0);         // this thread's tokens (<= 0 past the vocabulary)
+  const int base = max(0, min(i0, vocab - kTopPPer));
+  const int shift = i0 - base;                  // slot j holds token base + j
+  const float* rb = row + base;
+#pragma unroll
+  for (int j = 0; j < kTopPPer; ++j) e[j] = rb[j];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kTopPPer; ++j) {
+    const int k = j - shift;                    // the slot's position in this thread's slice
+    e[j] = k >= 0 && k < nin ? e[j] : -INFINITY;
+    mx = fmaxf(mx, e[j]);
+  }
+  // exp((x - max x) / T) as exp2 of one product per token (the weights are
+  // drawn from, not compared bit for bit)
+  const float M = topp_block_max(mx, red, slot);
+  const float c = 1.4426950408889634f / temp;
+  float zs = 0.f;
+#pragma unroll
+  for (int j = 0; j < kTopPPer; ++j) {
+    e[j] = e[j] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((e[j] - M) * c);
+    zs += e[j];
+  }
+  const float Z = topp_block_sum(zs, red, slot);
+  const float target = top_p * Z;
+  // 2. the kept threshold: smallest tau with f(tau) < target (f(1.0) = 0)
+  // e >= 0, so e > tau is an integer compare of the bit patterns; the select
+  // is a mask of the sign of their difference (VALU bit operations only: no
+  // per-element condition registers)
+  auto mass_above = [&](float tau) __attribute__((always_inline)) {
+    const int tb = __float_as_int(tau);
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < kTopPPer; ++j) {
+      const int eb = __float_as_int(e[j]);
+      sum += __int_as_float(eb & ((tb - eb) >> 31));   // e if eb > tb, else +0
+    }
+    return topp_block_sum(sum, red, slot);
+  };
+  uint32_t lo = 0u, hi = 0x3F800000u;
+  while (lo < hi) {   // uniform: every thread sees the same sums
+    const uint32_t mid = lo + (hi - lo) / 2;
+    if (mass_above(__uint_as_float(mid)) < target) hi = mid;
+    else lo = mid + 1;
+  }
+  const float tau = __uint_as_float(lo);
+  const float above = mass_above(tau);
+  // tie rank of this thread's first token equal to tau, in index order
+  float nt = 0.f;
+#pragma unroll
+  for (int j = 0; j < kTopPPer; ++j) {
+    nt += (e[j] == tau && e[j] > 0.f) ? 1.f : 0.f;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  float nties;
+  float rank = topp_block_exscan(nt, red, slot, nties);
+  // the kept weights, in place
+  // (one element at a time: the scheduler may not hoist the compares, whose
+  // masks would otherwise pile up and spill)
+  float ks = 0.f;
+  int last = -1;
+#pragma unroll
+  for (int j = 0; j < kTopPPer; ++j) {
+    const float v = e[j];
+    const bool tie = v == tau && v > 0.f;
+    const bool keep = v > tau || (tie && above + rank * tau < target);
+    rank += tie ? 1.f : 0.f;
+    e[j] = keep ? v : 0.f;
+    ks += e[j];
+    last = keep && v > 0.f ? base + j : last;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  float kept;
+  const float before = topp_block_exscan(ks, red, slot, kept);
+  if (last >= 0) atomicMax(&s_last, last);
+  // 3. the draw
+  const uint64_t r = mix64(sd ^ mix64(0x9E3779B97F4A7C15ull * static_cast<uint64_t>(b + 1) +
+                                      static_cast<uint64_t>(static_cast<uint32_t>(p))));
+  const float u = (static_cast<float>(r >> 40) + 0.5f) * (1.0f / 16777216.0f);
+  const float goal = u * kept;
+  if (ks > 0.f && goal >= before && goal < before + ks) {
+    // the first kept token whose running mass passes the goal (branch-free)
+    float acc = before;
+    int pick = last;
+    bool found = false;
+#pragma unroll
+    for (int j = 0; j < kTopPPer; ++j) {
+      acc += e[j];
+      const bool hit = !found && e[j] > 0.f && goal < acc;
+      pick = hit ? base + j : pick;
+      found = found || hit;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    s_pick = pick;
+  }
+  lds_barrier();
+  if (t == 0) {
+    const int draw = s_pick >= 0 ? s_pick : s_last;   // u * kept rounded onto the total: the last kept token
+    if (p < 0 || p >= nsteps || draw < 0) {
+      if (err) atomicExch(err, 2);
+    } else {
+      sam[static_cast<size_t>(b) * nsteps + p] = draw;
+      const bool prompt = (p + 1 < pl) && (p + 1 < nsteps);
+      ids[b] = prompt ? static_cast<int64_t>(nxt) : static_cast<int64_t>(draw);
+      pos[b] = p + 1;
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -537,6 +749,19 @@ int tfa_rows_norm_scaled(const float* part, int64_t ks, const void* h_in, float 
                                     part, static_cast<uint16_t*>(h_out), static_cast<const uint16_t*>(gamma),
                                     static_cast<uint16_t*>(xn), (int)m, (int)hidden, eps, nullptr, alpha);
   return launched("rows_norm_scaled");
+}
+
+int tfa_top_p_sample_step(const float* logits, int64_t vocab, int64_t batch, const float* params,
+                          const int64_t* seed, const int* inp, const int* prompt_len, int64_t* ids, int* pos,
+                          int* sam, int64_t nsteps, int* err, hipStream_t stream) {
+  if (!logits || !params || !seed || !inp || !prompt_len || !ids || !pos || !sam)
+    return fail(TFA_ERR_NULL, "tfa_top_p_sample_step: null pointer argument");
+  TFA_REQUIRE(vocab > 0 && vocab <= (int64_t)kTopPThreads * kTopPPer, TFA_ERR_SHAPE,
+              "tfa_top_p_sample_step: vocab %lld not in [1, %d]", (long long)vocab, kTopPThreads * kTopPPer);
+  TFA_REQUIRE(batch > 0 && batch <= 65535 && nsteps > 0, TFA_ERR_SHAPE, "tfa_top_p_sample_step: empty shape");
+  top_p_sample_kernel<<<(int)batch, kTopPThreads, 0, stream>>>(logits, (int)vocab, params, seed, inp, prompt_len,
+                                                               ids, pos, sam, (int)nsteps, err);
+  return launched("top_p_sample_step");
 }
 
 int tfa_batch_sample_step(const float* block_val, const int* block_idx, int64_t nblocks,

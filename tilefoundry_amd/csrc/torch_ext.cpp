@@ -423,6 +423,29 @@ void batch_sample_step(const Tensor& block_val, const Tensor& block_idx, const T
                                      nsteps, opt_ptr_t<int>(err), stream_of(pos)));
 }
 
+void top_p_sample_step(const Tensor& logits, const Tensor& params, const Tensor& seed, const Tensor& inp,
+                       const Tensor& prompt_len, const Tensor& ids, const Tensor& pos, const Tensor& sam,
+                       const OptT& err) {
+  need(pos, "pos", I32);
+  const int64_t B = pos.numel();
+  need(logits, "logits", F32);
+  if (logits.numel() % B != 0) bad("logits: expected (batch, vocab)");
+  const int64_t V = logits.numel() / B;
+  need(params, "params", F32, 2);
+  need(seed, "seed", I64, 1);
+  need(inp, "inp", I32);
+  if (inp.numel() % B != 0) bad("inp: expected (batch, nsteps)");
+  const int64_t nsteps = inp.numel() / B;
+  need(sam, "sam", I32, B * nsteps);
+  need(prompt_len, "prompt_len", I32, B);
+  need(ids, "ids", I64, B);
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_top_p_sample_step(logits.data_ptr<float>(), V, B, params.data_ptr<float>(),
+                                     seed.data_ptr<int64_t>(), inp.data_ptr<int>(), prompt_len.data_ptr<int>(),
+                                     ids.data_ptr<int64_t>(), pos.data_ptr<int>(), sam.data_ptr<int>(), nsteps,
+                                     opt_ptr_t<int>(err), stream_of(pos)));
+}
+
 // ------------------------------------------------------------------ MLA
 // part [ks, B, q_lora + 288] f32; latent [B, cap, 256], rope [B, cap, 32] bf16.
 void mla_prep(const Tensor& part, const Tensor& gamma_q_a, const Tensor& gamma_kv_a, double eps,
@@ -884,6 +907,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("skinny_gemm", &skinny_gemm);
   m.def("rows_norm", &rows_norm);
   m.def("batch_sample_step", &batch_sample_step);
+  m.def("top_p_sample_step", &top_p_sample_step);
   m.def("mla_prep", &mla_prep);
   m.def("mla_prep_q_gemv", &mla_prep_q_gemv);
   m.def("mla_q_absorb", &mla_q_absorb);

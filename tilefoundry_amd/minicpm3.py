@@ -263,23 +263,30 @@ def synthetic_model_weights(cfg: MiniCPM3Config = MINICPM3_4B, seed: int = 0, de
     return out
 
 
-def sample_top_p(temperature: float = 0.8, top_p: float = 0.8, generator: torch.Generator | None = None):
-    """The sampler of examples/minicpm3_4b-cutedsl/run.py:29-47 (``_sampler``, the
-    published ``generation_config.json``: T = 0.8, top-p 0.8): softmax of
-    ``logits / T``, probabilities ranked, a token kept while the mass before it is
-    below ``top_p``, one multinomial draw over the kept mass. Runs on the device
-    the logits are on; ``generator`` makes the draws reproducible."""
+class TopP:
+    """Top-p sampling as the decode step's last kernel (``tfa_top_p_sample_step``):
+    the sampler of examples/minicpm3_4b-cutedsl/run.py:29-47 (``_sampler``, the
+    published ``generation_config.json``: T = 0.8, top-p 0.8) -- probabilities
+    softmax(logits / T), ranked, a token kept while the mass ranked before it is
+    below ``top_p``, one draw from the kept mass -- drawn on the device inside the
+    captured step, so no host round trip per token. The draws come from a
+    counter-based generator of (``seed``, sequence, position): a seed gives the
+    same continuation on every run, on any device."""
 
-    def sample(logits: torch.Tensor) -> int:
-        row = logits.reshape(-1).float() / temperature
-        probs = torch.softmax(row, dim=-1)
-        order = torch.argsort(probs, descending=True)
-        ranked = probs[order]
-        keep = torch.cumsum(ranked, dim=-1) - ranked < top_p
-        ranked = torch.where(keep, ranked, torch.zeros_like(ranked))
-        return int(order[torch.multinomial(ranked, 1, generator=generator)].item())
+    def __init__(self, temperature: float = 0.8, top_p: float = 0.8, seed: int = 0):
+        if not temperature > 0.0 or not top_p > 0.0:
+            raise ValueError(f"temperature {temperature} and top_p {top_p} must be positive")
+        self.temperature, self.top_p, self.seed = float(temperature), float(top_p), int(seed)
 
-    return sample
+
+def sample_top_p(temperature: float = 0.8, top_p: float = 0.8, generator: torch.Generator | None = None,
+                 seed: int | None = None) -> TopP:
+    """The run.py sampler for ``MiniCPM3Engine.generate(sampler=...)``: a
+    :class:`TopP` whose seed is ``seed``, else the generator's seed (run.py's
+    ``--seed``), else 0."""
+    if seed is None:
+        seed = generator.initial_seed() if generator is not None else 0
+    return TopP(temperature, top_p, seed)
 
 
 class MiniCPM3Engine:
@@ -307,10 +314,12 @@ class MiniCPM3Engine:
         batch_sample     greedy pick, next input id, position + 1
 
     The compressed cache holds 576 bytes per position per layer (latent 256 +
-    rotated rope key 32, bf16). ``generate`` takes ``sampler=`` (for example
-    ``sample_top_p()``) to sample instead of taking the greedy pick: the step then
-    also keeps the bf16 logits, and the sampled id replaces the greedy one after
-    each replay (one host round trip per step, as the reference's sampler has).
+    rotated rope key 32, bf16). ``generate`` takes ``sampler=`` to sample instead
+    of taking the greedy pick: a :class:`TopP` (``sample_top_p()``) runs a second
+    captured step whose last kernel draws on the device
+    (``top_p_sample_step``, no host round trip); any other callable
+    ``sampler(logits) -> id`` is called on each sequence's bf16 logits after each
+    replay, and its id fed back (one host round trip per step).
     """
 
     MAX_BATCH = 32
@@ -348,8 +357,9 @@ class MiniCPM3Engine:
         self.alpha = cfg.residual_scale
         self.alpha_t = torch.tensor([self.alpha], dtype=BF16, device=self.device)
         self._buffers()
-        self.sampler = None
         self.graph = None
+        self.graph_sample = None   # the step ending in the device top-p draw, captured on first use
+        self.capture = capture
         if capture:
             self._capture()
 
@@ -425,10 +435,23 @@ class MiniCPM3Engine:
         self.sam = z(B, self.nsteps, dtype=torch.int32)
         self.plen = z(B, dtype=torch.int32)
         self.err = z(1, dtype=torch.int32)
+        self.topp = z(2, dtype=f32)                 # temperature, top_p of the sampling step
+        self.topp_seed = z(1, dtype=torch.int64)
 
-    def _step(self, keep_logits: bool = True):
+    def _finish(self, sample: bool):
+        """The step's last launch: the greedy pick over the head's block winners,
+        or the top-p draw over the bf16 logits."""
+        if sample:
+            C.top_p_sample_step(self.logits, self.topp, self.topp_seed, self.inp, self.plen, self.ids, self.pos,
+                                self.sam, self.err)
+        else:
+            C.batch_sample_step(self.bv, self.bi, self.inp, self.plen, self.ids, self.pos, self.sam,
+                                self.err)
+
+    def _step(self, keep_logits: bool = True, sample: bool = False):
+        keep_logits = keep_logits or sample
         if self.batch == 1:
-            self._step_one(keep_logits)
+            self._step_one(keep_logits, sample)
             return
         cfg, ks = self.cfg, self.ks
         L = len(self.layers)
@@ -456,10 +479,9 @@ class MiniCPM3Engine:
         C.rms_norm_div(self.h, self.gamma_final, self.xn, cfg.eps, cfg.logits_scaling)
         C.skinny_gemm(self.xn, self.head, 1, 3, None, None, self.logits if keep_logits else None,
                       self.bv, self.bi)
-        C.batch_sample_step(self.bv, self.bi, self.inp, self.plen, self.ids, self.pos, self.sam,
-                            self.err)
+        self._finish(sample)
 
-    def _step_one(self, keep_logits: bool = True):
+    def _step_one(self, keep_logits: bool = True, sample: bool = False):
         """One sequence: the projections on the bs=1 GEMVs, each with its norm or
         scaled residual fused (8 launches per layer):
         rmsnorm_gemv_f32 [q_a | kv_a] (one f32 split-K partial), mla_prep_q_gemv
@@ -486,24 +508,34 @@ class MiniCPM3Engine:
         C.rms_norm_div(self.h, self.gamma_final, self.xn, cfg.eps, cfg.logits_scaling)
         C.skinny_gemm(self.xn, self.head, 1, 3, None, None, self.logits if keep_logits else None,
                       self.bv, self.bi)
-        C.batch_sample_step(self.bv, self.bi, self.inp, self.plen, self.ids, self.pos, self.sam,
-                            self.err)
+        self._finish(sample)
 
-    def _capture(self):
+    def _capture(self, sample: bool = False):
         side = torch.cuda.Stream(device=self.device)
         side.wait_stream(torch.cuda.current_stream(self.device))
         self._load([[0]] * self.batch, 1)
         with torch.cuda.stream(side):
-            self._step()  # every kernel has run once before capture
+            self._step(sample=sample)  # every kernel has run once before capture
         torch.cuda.current_stream(self.device).wait_stream(side)
         torch.cuda.synchronize(self.device)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self._step()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self._step(sample=sample)
         self._load([[0]] * self.batch, 1)
+        if sample:
+            self.graph_sample = graph
+        else:
+            self.graph = graph
 
-    def _run_step(self):
-        if self.graph is not None:
+    def _run_step(self, sample: bool = False):
+        if sample:
+            if self.capture and self.graph_sample is None:
+                self._capture(sample=True)
+            if self.graph_sample is not None:
+                self.graph_sample.replay()
+            else:
+                self._step(sample=True)
+        elif self.graph is not None:
             self.graph.replay()
         else:
             self._step()
@@ -562,16 +594,22 @@ class MiniCPM3Engine:
         pl = len(prompts[0])
         if pl + max_new > self.nsteps:
             raise ValueError(f"prompt {pl} + {max_new} new exceeds this engine's {self.nsteps} steps")
+        device_draw = isinstance(sampler, TopP)
+        if device_draw and self.capture and self.graph_sample is None:
+            self._capture(sample=True)   # before the load: capturing reloads the buffers
         self._load([list(p) for p in prompts], pl)
+        if device_draw:
+            self.topp.copy_(torch.tensor([sampler.temperature, sampler.top_p], dtype=torch.float32))
+            self.topp_seed.fill_(sampler.seed)
         torch.cuda.synchronize(self.device)
         t0 = perf_counter()
         for _ in range(pl - 1):
-            self._run_step()
+            self._run_step(device_draw)
         torch.cuda.synchronize(self.device)
         t1 = perf_counter()
         for s in range(max_new):
-            self._run_step()
-            if sampler is not None:
+            self._run_step(device_draw)
+            if sampler is not None and not device_draw:
                 p = pl - 1 + s
                 picks = [sampler(self.logits[b]) for b in range(self.batch)]
                 t = torch.tensor(picks, dtype=torch.int64, device=self.device)
