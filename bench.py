@@ -218,6 +218,18 @@ def kernel_lines(eng) -> dict:
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    # the floor of the gate|up GEMV's access pattern: the same weight stream (28
+    # layers' 12288 x 2048 matrices, one-shot blocks of 4 or 6 rows) with no arithmetic
+    fold = torch.empty(2 * I, device=dev)
+    nbytes = 2 * I * H * 2
+    floor = {}
+    for rpb in (4, 6):
+        ms = per_layer(lambda w, r=rpb: C.read_rows(w["w_gu"], r, fold))
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        floor[f"rows_per_block_{rpb}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                                          "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    out["gate_up_access_pattern_floor"] = {**floor, "bytes": nbytes,
+                                           "what": "tfa_read_rows: the gate|up GEMV's weight loads alone"}
     ms = _graph_time(lambda: C.lm_head_argmax(eng.hid, eng.gamma_final, cfg.eps, eng.embed,
                                               eng.logits, eng.bv, eng.bi), 20)
     nbytes = cfg.vocab * H * 2

@@ -320,6 +320,29 @@ int tfa_rows_norm(const void* table, const int64_t* ids, int64_t vocab, const vo
 int tfa_rows_norm_scaled(const float* part, int64_t ks, const void* h_in, float alpha, void* h_out,
                          const void* gamma, void* xn, int64_t m, int64_t hidden, float eps, hipStream_t stream);
 
+/* The batched o_proj with the residual add and the post-attention norm's sums
+ * folded in: h_out[i, :] = bf16(res[i, :] + bf16(x[i, :] . w^T)) for m <= 32
+ * token rows, x [m, k], w [n, k] (out, in), k a multiple of 256; and per
+ * 32-row block b of w, ssq[b, i] = sum over the block's rows j of h_out[i, j]^2
+ * (f32; tfa_skinny_residual_blocks(n) blocks). With
+ * tfa_skinny_gemm_norm_swiglu it takes the place of tfa_skinny_gemm
+ * (partials) + tfa_rows_norm: one launch fewer.
+ * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:82-116 (resid_rms_norm: its
+ * residual add and the sum of squares) with the o_proj GEMV :123-145 before it. */
+int64_t tfa_skinny_residual_blocks(int64_t n);
+int tfa_skinny_gemm_residual(const void* x, const void* w, int64_t m, int64_t n, int64_t k, const void* res,
+                             void* h_out, float* ssq, hipStream_t stream);
+
+/* The batched gate|up GEMM + SwiGLU over the residual stream h [m, k] itself:
+ * each token row is staged as xn = bf16(bf16(h * r) * gamma), r = 1 / sqrt(
+ * sum_b ssq[b, i] / k + eps) (ssq [nssq <= 64, m] from tfa_skinny_gemm_residual,
+ * summed in b order), then act = the SwiGLU epilogue of tfa_skinny_gemm
+ * (epilogue 1) over interleaved gate|up rows, w [n, k], n even.
+ * Replaces: examples/qwen3_1_7b-tilelang/fast/kernels.py:82-116 (resid_rms_norm: the
+ * norm) and :210-257 (gemv_silu's SwiGLU) around the gate|up GEMV. */
+int tfa_skinny_gemm_norm_swiglu(const void* h, const void* w, int64_t m, int64_t n, int64_t k, const float* ssq,
+                                int64_t nssq, const void* gamma, float eps, void* act, hipStream_t stream);
+
 /* The greedy step for `batch` sequences: per sequence b, best = argmax over
  * block_val[b, :] (lowest index on ties); sam[b, pos[b]] = best;
  * ids[b] = pos[b]+1 < prompt_len[b] ? inp[b, pos[b]+1] : best; pos[b] += 1.
@@ -582,6 +605,15 @@ int tfa_causal_attention(const void* q, int64_t q_rs, int64_t q_hs, int64_t q_bs
  * hardware byte counters. No counterpart in the reference (its READMEs quote
  * H200 nominal bandwidth). bytes % 16 == 0. */
 int tfa_copy_stream(const void* src, void* dst, int64_t bytes, hipStream_t stream);
+
+/* Measurement utility: the decode GEMV's weight stream alone over w [rows, k]
+ * bf16 -- one-shot 256-thread blocks of rows_per_block (2, 4, 6 or 8) rows,
+ * each wave a contiguous quarter of every row in 16-byte non-temporal loads --
+ * folded to one value per block in out [ceil(rows / rows_per_block)] f32 (its
+ * value means nothing). Its time per launch is the floor of the GEMV's access
+ * pattern on a matrix of that shape. No counterpart in the reference (a
+ * measurement of this device). */
+int tfa_read_rows(const void* w, int64_t rows, int64_t k, int64_t rows_per_block, float* out, hipStream_t stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -50,6 +50,87 @@ def test_skinny_exact_on_integers(dev):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("M", [32, 5])
+def test_skinny_residual_then_norm_swiglu(dev, M):
+    """The folded post-attention path: o_proj with the residual add and the
+    per-32-row sums of squares in its epilogue, then the gate|up GEMM staging
+    its tokens as the Qwen3 norm of the residual stream. h1 is the oracle's
+    bf16(h + bf16(o)) (within one ulp: the f32 dot's order), the sums of
+    squares its f64 sums, and the SwiGLU output the oracle's over the
+    normalised h1; against the unfolded launches (split-K partials, rows_norm,
+    SwiGLU GEMM) nearly every element is identical."""
+    from tilefoundry_amd import ops
+    from tilefoundry_amd._lib import C
+
+    g = gen(40 + M)
+    attn = randn(M, HQ * D, g=g)
+    w_o = randn(H, HQ * D, g=g, std=0.02)
+    h = randn(M, H, g=g)
+    gamma = randn(H, g=g, std=0.1, mean=1.0)
+    wg, wu = randn(I, H, g=g, std=0.02), randn(I, H, g=g, std=0.02)
+    w_gu = torch.stack([wg, wu], 1).reshape(2 * I, H)
+    d = {k: v.to(dev) for k, v in dict(attn=attn, w_o=w_o, h=h, gamma=gamma, w_gu=w_gu).items()}
+    nb = C.skinny_residual_blocks(H)
+    h1 = torch.empty(M, H, device=dev, dtype=BF)
+    ssq = torch.full((nb, M), float("nan"), device=dev)
+    C.skinny_gemm_residual(d["attn"], d["w_o"], d["h"], h1, ssq)
+    act = torch.empty(M, I, device=dev, dtype=BF)
+    C.skinny_gemm_norm_swiglu(h1, d["w_gu"], ssq, d["gamma"], 1e-6, act)
+    torch.cuda.synchronize()
+    o_ref = OQ.proj(attn, w_o)
+    h1_ref = h + o_ref
+    from tests._check import assert_ulps
+    # the f32 dot's order may move the landed o by one of its own ulps, which is
+    # more than one ulp of h1 where h and o nearly cancel
+    spacing = torch.ldexp(torch.ones(()), torch.frexp(o_ref.float())[1] - 8)
+    assert bool(((h1.cpu().float() - h1_ref.float()).abs() <= spacing).all()), "h1 beyond one ulp of o"
+    assert_ulps("h1", h1, h1_ref, max_ulps=8, max_frac=0.01)
+    sq_ref = (h1.cpu().double() ** 2).view(M, nb, 32).sum(-1).t()
+    assert float(((ssq.cpu().double() - sq_ref).abs() / sq_ref).max()) < 1e-5
+    xn = ON.rms_norm_q(h1.cpu(), gamma, 1e-6)
+    act_ref = torch.nn.functional.silu(OQ.proj(xn, wg).float()).to(BF) * OQ.proj(xn, wu)
+    assert_close("norm + swiglu", act, act_ref)
+    # the unfolded launches over the same h1
+    part = ops.skinny_gemm(d["attn"], d["w_o"], "partial", ks=4)
+    h1b, xnb = torch.empty_like(h1), torch.empty_like(h1)
+    C.rows_norm(None, None, d["h"], part, h1b, d["gamma"], xnb, 1e-6, None)
+    actb = ops.skinny_gemm(xnb, d["w_gu"], "swiglu")
+    assert bool(((h1.float() - h1b.float()).abs().cpu() <= 2 * spacing).all()), "h1 folded vs unfolded"
+    assert_ulps("act folded vs unfolded", act, actb, max_ulps=2, max_frac=0.02)
+
+
+@pytest.mark.gpu
+def test_batch_engine_fold_o_norm_matches(dev):
+    """The batch engine with the post-attention norm folded (opt-in) picks the
+    same greedy ids as the default launches on a 2-layer model, and its logits
+    agree within bf16 relative L2."""
+    from tilefoundry_amd.qwen3 import BatchEngine
+
+    cfg, wts = _small()
+    prompts = OQ.prompt_ids(cfg.vocab, 6, seed=12, batch=8)
+    a = BatchEngine(cfg, batch=8, device=dev, max_new=12, prompt_room=8, weights=wts)
+    b = BatchEngine(cfg, batch=8, device=dev, max_new=12, prompt_room=8, weights=wts, fold_o_norm=True)
+    assert b.fold_o_norm and not a.fold_o_norm
+    assert_l2("logits", b.logits_for(prompts), a.logits_for(prompts))
+    assert a.generate(prompts, 10).tokens == b.generate(prompts, 10).tokens
+
+
+@pytest.mark.gpu
+def test_skinny_residual_refuses(dev):
+    from tilefoundry_amd._lib import C
+
+    x = torch.zeros(33, 256, device=dev, dtype=BF)
+    w = torch.zeros(64, 256, device=dev, dtype=BF)
+    with pytest.raises(ValueError):
+        C.skinny_gemm_residual(x, w, torch.zeros(33 * 64, device=dev, dtype=BF),
+                               torch.zeros(33, 64, device=dev, dtype=BF), torch.zeros(2, 33, device=dev))
+    h = torch.zeros(4, 256, device=dev, dtype=BF)
+    with pytest.raises(ValueError):   # 65 partial rows
+        C.skinny_gemm_norm_swiglu(h, w, torch.zeros(65, 4, device=dev), torch.zeros(256, device=dev, dtype=BF),
+                                  1e-6, torch.zeros(4, 32, device=dev, dtype=BF))
+
+
+@pytest.mark.gpu
 def test_skinny_swiglu(dev):
     from tilefoundry_amd import ops
 

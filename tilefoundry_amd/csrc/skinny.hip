@@ -48,7 +48,7 @@ constexpr int kGroupRows = 16;   // argmax winners are kept per 16 weight rows
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-enum { SK_PARTIAL = 0, SK_SWIGLU = 1, SK_ARGMAX = 2, SK_ARGMAX_BF16 = 3 };
+enum { SK_PARTIAL = 0, SK_SWIGLU = 1, SK_ARGMAX = 2, SK_ARGMAX_BF16 = 3, SK_RESID_SSQ = 4 };
 
 struct SkinnyArgs {
   const uint16_t* x;  // [M, K]
@@ -60,6 +60,17 @@ struct SkinnyArgs {
   float* bv;          // [M, ngroups]
   int* bi;            // [M, ngroups]
   int ngroups;        // 16-row groups of N
+  // residual epilogue: h_out[m, n] = bf16(res[m, n] + bf16(y)), and per block b
+  // the token's sum of squares of its rows of h_out in ssq[b, m]
+  const uint16_t* res;
+  uint16_t* h_out;
+  float* ssq;
+  // norm prologue: x is the residual stream h; the token rows are staged as
+  // bf16(bf16(h * r_m) * gamma), r_m = 1 / sqrt(sum_b ssq_in[b, m] / K + eps)
+  const float* ssq_in;
+  int nssq;
+  const uint16_t* gamma;
+  float eps;
 };
 
 TFA_DEV bf16x8 as_bf8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -86,13 +97,16 @@ struct SkinnyStage {
 
 // TR weight rows per block (32 or 48: TR / 16 MFMA column tiles) against the
 // 32 token rows (two row tiles).
-template <int EPI, int P, int TR, int W>
+template <int EPI, int P, int TR, int W, bool NORM = false>
 __global__ __launch_bounds__(W * kWave) void skinny_gemm_kernel(const SkinnyArgs a) {
   constexpr int RT = TR / 16;       // weight-row tiles
   constexpr int NT = 2 * RT;        // output tiles (token half, row tile)
   constexpr int WL = TR / 8;        // weight-row loads per lane per chunk
   static_assert(sizeof(SkinnyStage<TR>) >= NT * kWave * sizeof(float) * 4, "partials reuse the staging tile");
+  static_assert(EPI != SK_RESID_SSQ || NT <= W, "the residual epilogue finishes one tile per wave");
   __shared__ SkinnyStage<TR> stage[W];   // reused for the block's partial sums
+  __shared__ float rn[NORM ? kMaxTokens : 1];                       // the tokens' norm scales
+  __shared__ float sq[NORM ? 8 : RT][kMaxTokens];                   // norm / ssq partials
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = threadIdx.x / kWave;
@@ -114,6 +128,34 @@ __global__ __launch_bounds__(W * kWave) void skinny_gemm_kernel(const SkinnyArgs
   // unconditional so the compiler can count them and wait only for the oldest.
   const int srow = lane >> 3;               // 0..7
   const int scol = (lane & 7) * 8;          // element offset in the chunk
+  // Norm prologue, first of all (its loads complete first): thread t sums
+  // ssq_in[b, t % 32] over b = 8 (t / 32) .. + 7 in order, the eight groups meet
+  // in LDS in order, and r_m lands in rn[m] before the first chunk is staged.
+  // (the first 256 threads: 8 groups of 8 of the at most 64 partial rows)
+  float nsum = 0.f;
+  const bool nthread = threadIdx.x < 8 * kMaxTokens;
+  if constexpr (NORM) {
+    const int m = threadIdx.x % kMaxTokens, g8 = min(static_cast<int>(threadIdx.x) / kMaxTokens, 7);
+    float v8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int b = 8 * g8 + j;
+      v8[j] = (nthread && b < a.nssq && m < a.M)
+                  ? a.ssq_in[static_cast<size_t>(min(b, a.nssq - 1)) * a.M + min(m, a.M - 1)] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) nsum += v8[j];
+  }
+  // residual epilogue: this lane's residual values, loaded with the first loads
+  uint32_t res_pre[4] = {0u, 0u, 0u, 0u};
+  if constexpr (EPI == SK_RESID_SSQ) {
+    if (wid < NT) {
+      const int th = wid / RT, rh = wid % RT;
+      const int n = min(n0 + 16 * rh + r16, a.N - 1);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) res_pre[r] = a.res[static_cast<size_t>(min(16 * th + 4 * grp + r, a.M - 1)) * a.N + n];
+    }
+  }
   const uint16_t* wp[WL];
   const uint16_t* xp[4];
 #pragma unroll
@@ -127,15 +169,41 @@ __global__ __launch_bounds__(W * kWave) void skinny_gemm_kernel(const SkinnyArgs
     xp[i] = a.x + static_cast<size_t>(tok) * K + kw0 + scol;
   }
   // ring of P chunks in registers: chunk g*P + p lives in slot p (nchunks % P == 0)
-  uint4 rw[P][WL], rx[P][4];
+  const uint16_t* gp = NORM ? a.gamma + kw0 + scol : nullptr;
+  uint4 rw[P][WL], rx[P][4], rg[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
 #pragma unroll
     for (int i = 0; i < WL; ++i) rw[p][i] = ld16_stream(wp[i] + p * kStride);
 #pragma unroll
     for (int i = 0; i < 4; ++i) rx[p][i] = ld16(xp[i] + p * kStride);
+    if constexpr (NORM) rg[p] = ld16(gp + p * kStride);
     __builtin_amdgcn_sched_barrier(0);   // issue the slots in order: slot p is waited for alone
   }
+  float rtok[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (NORM) {
+    if (nthread) sq[threadIdx.x / kMaxTokens][threadIdx.x % kMaxTokens] = nsum;
+    __syncthreads();
+    if (threadIdx.x < kMaxTokens) {
+      float ss = 0.f;
+#pragma unroll
+      for (int g8 = 0; g8 < 8; ++g8) ss += sq[g8][threadIdx.x];
+      rn[threadIdx.x] = rsqrt_rn(ss / static_cast<float>(K) + a.eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rtok[i] = rn[8 * i + srow];
+  }
+  // a token chunk as staged: the residual stream normalised (norm prologue)
+  auto token_chunk = [&](uint4 v, int i, uint4 g) __attribute__((always_inline)) {
+    if constexpr (!NORM) return v;
+    float f[8], gg[8];
+    unpack8(v, f);
+    unpack8(g, gg);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = round_bf(round_bf(f[e] * rtok[i]) * gg[e]);
+    return pack8(f);
+  };
 
   f32x4 c[NT];
 #pragma unroll
@@ -150,13 +218,14 @@ __global__ __launch_bounds__(W * kWave) void skinny_gemm_kernel(const SkinnyArgs
 #pragma unroll
       for (int i = 0; i < WL; ++i) *reinterpret_cast<uint4*>(&st.w[8 * i + srow][scol]) = rw[p][i];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&st.x[8 * i + srow][scol]) = rx[p][i];
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&st.x[8 * i + srow][scol]) = token_chunk(rx[p][i], i, rg[p]);
       if (refill) {   // P chunks stay in flight during the MFMAs
         const int off = ((g + 1) * P + p) * kStride;
 #pragma unroll
         for (int i = 0; i < WL; ++i) rw[p][i] = ld16_stream(wp[i] + off);
 #pragma unroll
         for (int i = 0; i < 4; ++i) rx[p][i] = ld16(xp[i] + off);
+        if constexpr (NORM) rg[p] = ld16(gp + off);
       }
       wave_lds_sync();
 #pragma unroll
@@ -197,6 +266,14 @@ __global__ __launch_bounds__(W * kWave) void skinny_gemm_kernel(const SkinnyArgs
       if (EPI == SK_PARTIAL) {
         if (m < a.M && n < a.N) a.part[(static_cast<size_t>(blockIdx.y) * a.M + m) * a.N + n] = val;
       }
+      if (EPI == SK_RESID_SSQ) {
+        // h1 = bf16(h + bf16(y)); the tile's 16 rows of h1^2 summed per token
+        const float h1 = round_bf(__uint_as_float(res_pre[r] << 16) + round_bf(val));
+        const bool in = m < a.M && n < a.N;
+        if (in) a.h_out[static_cast<size_t>(m) * a.N + n] = static_cast<uint16_t>(f2bf(h1));
+        const float rs = row16_sum(in ? h1 * h1 : 0.f);
+        if (r16 == 0) sq[rh][m] = rs;
+      }
       if (EPI == SK_SWIGLU) {
         // rows (2i, 2i+1) = (gate_i, up_i) sit in lanes r16 and r16 ^ 1
         const float other = xor_lane<1>(val, r16);
@@ -230,6 +307,15 @@ __global__ __launch_bounds__(W * kWave) void skinny_gemm_kernel(const SkinnyArgs
       }
     }
   }
+  if constexpr (EPI == SK_RESID_SSQ) {   // the block's rows summed per token, row tiles in order
+    __syncthreads();
+    if (threadIdx.x < a.M) {
+      float tot = 0.f;
+#pragma unroll
+      for (int rh = 0; rh < RT; ++rh) tot += sq[rh][threadIdx.x];
+      a.ssq[static_cast<size_t>(blockIdx.x) * a.M + threadIdx.x] = tot;
+    }
+  }
 }
 
 // Register ring depth: two chunks in flight per wave when the wave's chunk count
@@ -250,36 +336,38 @@ int skinny_cus() {
   return cus;
 }
 
-template <int EPI, int TR, int W>
+template <int EPI, int TR, int W, bool NORM = false>
 void launch_trw(const SkinnyArgs& a, hipStream_t st) {
   const dim3 grid((a.N + TR - 1) / TR, a.ks);
   if (skinny_depth(a.K / a.ks / W / kChunk) == 2)
-    skinny_gemm_kernel<EPI, 2, TR, W><<<grid, W * kWave, 0, st>>>(a);
+    skinny_gemm_kernel<EPI, 2, TR, W, NORM><<<grid, W * kWave, 0, st>>>(a);
   else
-    skinny_gemm_kernel<EPI, 1, TR, W><<<grid, W * kWave, 0, st>>>(a);
+    skinny_gemm_kernel<EPI, 1, TR, W, NORM><<<grid, W * kWave, 0, st>>>(a);
 }
 
 // Eight waves per block (two per SIMD) when the block's K range splits into
 // 512-element steps: twice the loads in flight per CU of the four-wave form.
-template <int EPI, int TR>
+template <int EPI, int TR, bool NORM = false>
 void launch_tr(const SkinnyArgs& a, hipStream_t st) {
   if ((a.K / a.ks) % (8 * kChunk) == 0)
-    launch_trw<EPI, TR, 8>(a, st);
+    launch_trw<EPI, TR, 8, NORM>(a, st);
   else
-    launch_trw<EPI, TR, 4>(a, st);
+    launch_trw<EPI, TR, 4, NORM>(a, st);
 }
 
-template <int EPI>
+template <int EPI, bool NORM = false>
 int launch_skinny(const SkinnyArgs& a, hipStream_t st, const char* name) {
   const int64_t cus = skinny_cus();
   auto cost = [&](int64_t tr) {   // rounds of resident blocks x rows per block
     const int64_t blocks = (a.N + tr - 1) / tr * a.ks;
     return (blocks + cus - 1) / cus * tr;
   };
-  if (cost(48) < cost(32))
-    launch_tr<EPI, 48>(a, st);
+  if constexpr (EPI == SK_RESID_SSQ)
+    launch_tr<EPI, 32>(a, st);   // the residual epilogue's sums are per 32 rows
+  else if (cost(48) < cost(32))
+    launch_tr<EPI, 48, NORM>(a, st);
   else
-    launch_tr<EPI, 32>(a, st);
+    launch_tr<EPI, 32, NORM>(a, st);
   return launched(name);
 }
 
@@ -693,6 +781,64 @@ int tfa_skinny_gemm(const void* x, const void* w, int64_t m, int64_t n, int64_t 
     default:
       return fail(TFA_ERR_ARG, "tfa_skinny_gemm: epilogue %d not in {0, 1, 2, 3}", epilogue);
   }
+}
+
+int64_t tfa_skinny_residual_blocks(int64_t n) { return (n + 31) / 32; }
+
+int tfa_skinny_gemm_residual(const void* x, const void* w, int64_t m, int64_t n, int64_t k, const void* res,
+                             void* h_out, float* ssq, hipStream_t stream) {
+  TFA_NONNULL(x);
+  TFA_NONNULL(w);
+  TFA_NONNULL(res);
+  TFA_NONNULL(h_out);
+  TFA_NONNULL(ssq);
+  TFA_REQUIRE(m >= 1 && m <= kMaxTokens, TFA_ERR_SHAPE, "tfa_skinny_gemm_residual: m=%lld not in [1, 32]", (long long)m);
+  TFA_REQUIRE(n >= 1 && k % (kWaves * kChunk) == 0 && k > 0, TFA_ERR_SHAPE,
+              "tfa_skinny_gemm_residual: n=%lld, k=%lld must be a positive multiple of 256", (long long)n, (long long)k);
+  TFA_ALIGN16(x);
+  TFA_ALIGN16(w);
+  SkinnyArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = static_cast<const uint16_t*>(w);
+  a.M = (int)m;
+  a.N = (int)n;
+  a.K = (int)k;
+  a.ks = 1;
+  a.res = static_cast<const uint16_t*>(res);
+  a.h_out = static_cast<uint16_t*>(h_out);
+  a.ssq = ssq;
+  return launch_skinny<SK_RESID_SSQ>(a, stream, "skinny_gemm_residual");
+}
+
+int tfa_skinny_gemm_norm_swiglu(const void* h, const void* w, int64_t m, int64_t n, int64_t k, const float* ssq,
+                                int64_t nssq, const void* gamma, float eps, void* act, hipStream_t stream) {
+  TFA_NONNULL(h);
+  TFA_NONNULL(w);
+  TFA_NONNULL(ssq);
+  TFA_NONNULL(gamma);
+  TFA_NONNULL(act);
+  TFA_REQUIRE(m >= 1 && m <= kMaxTokens, TFA_ERR_SHAPE, "tfa_skinny_gemm_norm_swiglu: m=%lld not in [1, 32]", (long long)m);
+  TFA_REQUIRE(n >= 2 && n % 2 == 0 && k % (kWaves * kChunk) == 0 && k > 0, TFA_ERR_SHAPE,
+              "tfa_skinny_gemm_norm_swiglu: n=%lld must be even, k=%lld a positive multiple of 256", (long long)n,
+              (long long)k);
+  TFA_REQUIRE(nssq >= 1 && nssq <= 64, TFA_ERR_SHAPE, "tfa_skinny_gemm_norm_swiglu: %lld ssq rows not in [1, 64]",
+              (long long)nssq);
+  TFA_ALIGN16(h);
+  TFA_ALIGN16(w);
+  TFA_ALIGN16(gamma);
+  SkinnyArgs a{};
+  a.x = static_cast<const uint16_t*>(h);
+  a.w = static_cast<const uint16_t*>(w);
+  a.M = (int)m;
+  a.N = (int)n;
+  a.K = (int)k;
+  a.ks = 1;
+  a.act = static_cast<uint16_t*>(act);
+  a.ssq_in = ssq;
+  a.nssq = (int)nssq;
+  a.gamma = static_cast<const uint16_t*>(gamma);
+  a.eps = eps;
+  return launch_skinny<SK_SWIGLU, true>(a, stream, "skinny_gemm_norm_swiglu");
 }
 
 int tfa_rows_norm(const void* table, const int64_t* ids, int64_t vocab, const void* h_in,

@@ -423,6 +423,34 @@ void batch_sample_step(const Tensor& block_val, const Tensor& block_idx, const T
                                      nsteps, opt_ptr_t<int>(err), stream_of(pos)));
 }
 
+void skinny_gemm_residual(const Tensor& x, const Tensor& w, const Tensor& res, const Tensor& h_out,
+                          const Tensor& ssq) {
+  need(x, "x", BF);
+  need(w, "w", BF);
+  if (x.dim() != 2 || w.dim() != 2 || x.size(1) != w.size(1)) bad("skinny_gemm_residual: x [m, k], w [n, k]");
+  const int64_t m = x.size(0), n = w.size(0), k = w.size(1);
+  need(res, "res", BF, m * n);
+  need(h_out, "h_out", BF, m * n);
+  need(ssq, "ssq", F32, tfa_skinny_residual_blocks(n) * m);
+  raise_status(tfa_skinny_gemm_residual(x.data_ptr(), w.data_ptr(), m, n, k, res.data_ptr(), h_out.data_ptr(),
+                                        ssq.data_ptr<float>(), stream_of(x)));
+}
+
+void skinny_gemm_norm_swiglu(const Tensor& h, const Tensor& w, const Tensor& ssq, const Tensor& gamma, double eps,
+                             const Tensor& act) {
+  need(h, "h", BF);
+  need(w, "w", BF);
+  if (h.dim() != 2 || w.dim() != 2 || h.size(1) != w.size(1)) bad("skinny_gemm_norm_swiglu: h [m, k], w [n, k]");
+  const int64_t m = h.size(0), n = w.size(0), k = w.size(1);
+  need(ssq, "ssq", F32);
+  if (ssq.numel() % m != 0) bad("ssq: expected (blocks, m)");
+  need(gamma, "gamma", BF, k);
+  need(act, "act", BF, m * (n / 2));
+  raise_status(tfa_skinny_gemm_norm_swiglu(h.data_ptr(), w.data_ptr(), m, n, k, ssq.data_ptr<float>(),
+                                           ssq.numel() / m, gamma.data_ptr(), (float)eps, act.data_ptr(),
+                                           stream_of(h)));
+}
+
 void top_p_sample_step(const Tensor& logits, const Tensor& params, const Tensor& seed, const Tensor& inp,
                        const Tensor& prompt_len, const Tensor& ids, const Tensor& pos, const Tensor& sam,
                        const OptT& err) {
@@ -903,11 +931,21 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode_attention", &decode_attention);
   m.def("attn_combine", &attn_combine);
   m.def("copy_stream", &copy_stream);
+  m.def("read_rows", [](const Tensor& w, int64_t rows_per_block, const Tensor& out) {
+    if (!w.is_cuda() || !w.is_contiguous() || w.scalar_type() != at::kBFloat16 || w.dim() != 2)
+      bad("read_rows: contiguous bf16 GPU matrix required");
+    need(out, "out", F32, (w.size(0) + rows_per_block - 1) / std::max<int64_t>(rows_per_block, 1));
+    raise_status(tfa_read_rows(w.data_ptr(), w.size(0), w.size(1), rows_per_block, out.data_ptr<float>(),
+                               stream_of(w)));
+  });
   m.def("skinny_blocks", [](int64_t n) { return tfa_skinny_blocks(n); });
   m.def("skinny_gemm", &skinny_gemm);
   m.def("rows_norm", &rows_norm);
   m.def("batch_sample_step", &batch_sample_step);
   m.def("top_p_sample_step", &top_p_sample_step);
+  m.def("skinny_gemm_residual", &skinny_gemm_residual);
+  m.def("skinny_gemm_norm_swiglu", &skinny_gemm_norm_swiglu);
+  m.def("skinny_residual_blocks", [](int64_t n) { return tfa_skinny_residual_blocks(n); });
   m.def("mla_prep", &mla_prep);
   m.def("mla_prep_q_gemv", &mla_prep_q_gemv);
   m.def("mla_q_absorb", &mla_q_absorb);

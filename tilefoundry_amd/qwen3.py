@@ -507,7 +507,8 @@ class BatchEngine:
     def __init__(self, cfg: Qwen3Config = QWEN3_1_7B, *, batch: int = 32, device="cuda:0",
                  max_new: int = 2048, prompt_room: int = 512, weights: dict | None = None,
                  seed: int = 0, split: int = 128, ks_qkv: int = 2, ks_o: int = 4, ks_down: int = 4,
-                 capture: bool = True, prompt_prefill: bool = False, attention: str = "auto"):
+                 capture: bool = True, prompt_prefill: bool = False, attention: str = "auto",
+                 fold_o_norm: bool = False):
         if not 1 <= batch <= self.MAX_BATCH:
             raise ValueError(f"batch {batch} not in [1, {self.MAX_BATCH}]")
         if attention not in ("auto", "seq", "split"):
@@ -518,6 +519,12 @@ class BatchEngine:
         self.split = split
         self.prompt_prefill = prompt_prefill
         self.ks = {"qkv": ks_qkv, "o": ks_o, "down": ks_down}
+        # fold_o_norm: o_proj unsplit with the residual add and the post-attention
+        # norm's sums in its epilogue, the norm itself in the gate|up GEMM's
+        # staging -- one launch fewer per layer, but measured slower (15.6-15.7k
+        # against 16.26k tok/s at 32 x 2048: the unsplit o_proj has 64 blocks for
+        # its 8.4 MB, and the norm lengthens the gate|up staging loop), so off
+        self.fold_o_norm = bool(fold_o_norm)
         self.nsteps = max_new + prompt_room
         self.cap = ((self.nsteps + split - 1) // split) * split
         self.ns = self.cap // split
@@ -549,6 +556,7 @@ class BatchEngine:
         f32 = torch.float32
         self.h = z(B, H)
         self.h1 = z(B, H)
+        self.ssq = z(C.skinny_residual_blocks(H), B, dtype=torch.float32)
         self.xn = z(B, H)
         self.act = z(B, I)
         self.attn = z(B, HQ * D)
@@ -593,10 +601,14 @@ class BatchEngine:
                                    self.pos, HQ, HKV, self.split, cfg.scale, self.op, self.mp, self.lp,
                                    False, self.err)
                 C.attn_combine(self.op, self.mp, self.lp, self.attn, self.pos, self.split)
-            C.skinny_gemm(self.attn, w["w_o"], self.ks["o"], 0, self.o_part, None, None, None, None)
-            C.rows_norm(None, None, self.h, self.o_part, self.h1, w["gamma_post"], self.xn, cfg.eps,
-                        self.err)
-            C.skinny_gemm(self.xn, w["w_gu"], 1, 1, None, self.act, None, None, None)
+            if self.fold_o_norm:
+                C.skinny_gemm_residual(self.attn, w["w_o"], self.h, self.h1, self.ssq)
+                C.skinny_gemm_norm_swiglu(self.h1, w["w_gu"], self.ssq, w["gamma_post"], cfg.eps, self.act)
+            else:
+                C.skinny_gemm(self.attn, w["w_o"], self.ks["o"], 0, self.o_part, None, None, None, None)
+                C.rows_norm(None, None, self.h, self.o_part, self.h1, w["gamma_post"], self.xn, cfg.eps,
+                            self.err)
+                C.skinny_gemm(self.xn, w["w_gu"], 1, 1, None, self.act, None, None, None)
             C.skinny_gemm(self.act, w["w_down"], self.ks["down"], 0, self.d_part, None, None, None,
                           None)
             nxt = self.layers[i + 1]["gamma_in"] if i + 1 < L else self.gamma_final
