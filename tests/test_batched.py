@@ -101,18 +101,38 @@ def test_skinny_residual_then_norm_swiglu(dev, M):
 
 @pytest.mark.gpu
 def test_batch_engine_fold_o_norm_matches(dev):
-    """The batch engine with the post-attention norm folded (opt-in) picks the
-    same greedy ids as the default launches on a 2-layer model, and its logits
-    agree within bf16 relative L2."""
+    """The batch engine with the post-attention norm folded (opt-in) against the
+    default launches on a 2-layer model. The two round differently (o_proj as
+    one f32 dot instead of four split-K partials, the norm's sum of squares in
+    another order), so a near tie may flip: teacher-forced along the default
+    engine's free run, every folded pick equals the default one except where
+    the default's top-1 / top-2 gap is within twice the measured logit
+    difference, which itself stays within 1 % of the largest logit; the folded
+    free run leaves the default one only at such a tie; logits agree within
+    bf16 relative L2."""
     from tilefoundry_amd.qwen3 import BatchEngine
 
     cfg, wts = _small()
-    prompts = OQ.prompt_ids(cfg.vocab, 6, seed=12, batch=8)
-    a = BatchEngine(cfg, batch=8, device=dev, max_new=12, prompt_room=8, weights=wts)
-    b = BatchEngine(cfg, batch=8, device=dev, max_new=12, prompt_room=8, weights=wts, fold_o_norm=True)
+    B, n = 8, 10
+    prompts = OQ.prompt_ids(cfg.vocab, 6, seed=12, batch=B)
+    a = BatchEngine(cfg, batch=B, device=dev, max_new=12, prompt_room=8, weights=wts)
+    b = BatchEngine(cfg, batch=B, device=dev, max_new=12, prompt_room=8, weights=wts, fold_o_norm=True)
     assert b.fold_o_norm and not a.fold_o_norm
     assert_l2("logits", b.logits_for(prompts), a.logits_for(prompts))
-    assert a.generate(prompts, 10).tokens == b.generate(prompts, 10).tokens
+    free_a, free_b = a.generate(prompts, n).tokens, b.generate(prompts, n).tokens
+    teachers = [t[:-1] for t in free_a]
+    picks_a, logits_a = a.forced(prompts, teachers, record_logits=True)
+    picks_b, logits_b = b.forced(prompts, teachers, record_logits=True)
+    assert picks_a == free_a, "the default engine's forced picks repeat its free run"
+    for s in range(B):
+        ref = [lg[s] for lg in logits_a]
+        ids, vals, gaps = oracle_candidates(ref)
+        _, deltas = forced_agreement(f"2-layer bs=8 folded vs default, sequence {s}", picks_b[s], picks_a[s],
+                                     [lg[s] for lg in logits_b], ids, vals, gaps, floor=n - 2,
+                                     max_delta=logit_bounds(ref))
+        diff = next((i for i, (x, y) in enumerate(zip(free_b[s], free_a[s])) if x != y), None)
+        if diff is not None:
+            assert gaps[diff] <= 2 * deltas[diff], f"seq {s}: folded free run leaves the default at a clear margin"
 
 
 @pytest.mark.gpu

@@ -4,8 +4,9 @@ pinned to Hugging Face's MiniCPM3ForCausalLM in test_oracle.py).
 
 Small stacks keep the published layer shapes (hidden 2560, 40 heads, q_lora 768,
 kv_lora 256, SwiGLU 6400) with fewer layers and a smaller vocabulary, so the
-CPU oracle finishes in seconds; the full 62-layer model runs as a smoke test
-(finite, reproducible, the sampler's contract).
+CPU oracle finishes in seconds; the full 62-layer model is checked against the
+oracle's golden ids (tests/golden/minicpm3_greedy_256.json) and as a smoke test
+(finite, reproducible).
 """
 from dataclasses import replace
 
@@ -214,6 +215,46 @@ def test_top_p_step_ties_and_limits(dev):
                         torch.zeros(1, 4, dtype=torch.int32, device=dev), err)
     torch.cuda.synchronize()
     assert int(err) == 2 and int(pos) == 5
+
+
+@pytest.mark.gpu
+def test_minicpm3_full_model_golden(dev):
+    """The full MiniCPM3-4B-shaped model (62 layers, vocab 73448, seed-0
+    weights) after the decode benchmark's 8-token prompt, against the oracle's
+    ids in tests/golden/minicpm3_greedy_256.json (make_minicpm3_golden.py):
+
+    * teacher-forced along 255 seeded random ids, every pick at a clear
+      position (top-2 gap above twice the oracle's own two-order spread there)
+      equals the oracle's, every other pick is a near tie under the measured
+      logit error, and the logit error stays within twice the oracle's largest
+      order spread;
+    * the free greedy run equals the oracle's 256 ids exactly."""
+    import json
+    from pathlib import Path
+
+    from tests.test_qwen3_engine import check_spread
+    from tilefoundry_amd.minicpm3 import MiniCPM3Engine
+
+    gold = json.loads((Path(__file__).parent / "golden" / "minicpm3_greedy_256.json").read_text())
+    f = gold["forced"]
+    n = len(f["tokens"])
+    spread = f["order_spread"]["deltas"]
+    clear = [gap > 2.0 * sp for gap, sp in zip(f["gaps"], spread)]
+    eng = MiniCPM3Engine(device=dev, max_new=n, prompt_room=len(gold["prompt"]), seed=gold["seed"])
+    picks, logits = eng.forced([gold["prompt"]], [f["teacher"]], record_logits=True)
+    picks = picks[0]
+    _, deltas = forced_agreement("MiniCPM3 62-layer bs=1, 256 teacher-forced positions", picks, f["tokens"],
+                                 [lg[0] for lg in logits], f["top_ids"], f["top_vals"], f["gaps"],
+                                 floor=sum(clear), max_delta=2.0 * max(spread))
+    del logits
+    check_spread("MiniCPM3 62-layer bs=1", deltas, f["order_spread"])
+    off = [i for i in range(n) if clear[i] and picks[i] != f["tokens"][i]]
+    assert not off, f"picks differ at clear positions: {off[:8]}"
+    gen = eng.generate([gold["prompt"]], n).tokens[0]
+    diff = next((i for i, (a, b) in enumerate(zip(gen, gold["free"]["tokens"])) if a != b), None)
+    print(f"[exact] MiniCPM3 62-layer bs=1: {sum(clear)}/{n} clear teacher-forced positions, all equal; "
+          f"free run identical for {n if diff is None else diff}/{n} steps", flush=True)
+    assert diff is None, f"free run leaves the oracle at step {diff}"
 
 
 @pytest.mark.gpu
