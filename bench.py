@@ -220,11 +220,11 @@ def kernel_lines(eng) -> dict:
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes}
     # the floor of the gate|up GEMV's access pattern: the same weight stream (28
     # layers' 12288 x 2048 matrices, one-shot blocks of 4 or 6 rows) with no arithmetic
-    fold = torch.empty(2 * I, device=dev)
     nbytes = 2 * I * H * 2
     floor = {}
     for rpb in (4, 6):
-        ms = per_layer(lambda w, r=rpb: C.read_rows(w["w_gu"], r, fold))
+        fold = torch.empty((2 * I + rpb - 1) // rpb, device=dev)   # one value per block
+        ms = per_layer(lambda w, r=rpb, f=fold: C.read_rows(w["w_gu"], r, f))
         gbs = nbytes / (ms * 1e-3) / 1e9
         floor[f"rows_per_block_{rpb}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                                           "frac": round(gbs / HBM_PEAK_GBS, 4)}

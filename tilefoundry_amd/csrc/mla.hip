@@ -278,14 +278,12 @@ struct MlaAttnArgs {
   float scale_log2;   // scale * log2(e)
 };
 
-// Work split: a step is Q x 32 positions in two LDS stages, filled by DMA.
-// Wave (quarter u, head tile mt) -- 3Q waves, three per SIMD -- owns positions
-// 32u .. 32u + 31 of every step and heads 16mt .. 16mt + 15, with its own
-// online-softmax state; with Q = 4 the four quarters of a head tile are
-// merged at the end. One barrier per step publishes the step's rows and frees
-// the other stage for the next step's DMA. Q = 4 (128-position steps) for
-// splits of whole steps; Q = 1 (32-position steps, no quarter merge) for
-// splits of 32 / 64 / 96 positions, the short-latency form for one sequence.
+// Splits of 32 / 64 / 96 positions (the short-latency form for one sequence;
+// splits of whole 128-position steps take mla_attn_heads_kernel below): a step
+// is 32 positions in two LDS stages, filled by DMA. Wave mt -- three waves,
+// one per head tile -- owns heads 16mt .. 16mt + 15 over the whole split with
+// its own online-softmax state. One barrier per step publishes the step's
+// rows and frees the other stage for the next step's DMA.
 constexpr int kWaveRows = 32;
 constexpr int kStepVm = 6;   // DMAs per wave per step: 2Q rows' latent and rope per wave
 constexpr int kWaitVmStep = waitcnt_vm(kStepVm);
@@ -326,18 +324,16 @@ TFA_DEV uint2 ld_tr(const char* lds_byte) {
 template <int Q>
 __global__ __launch_bounds__(3 * Q * kWave) __attribute__((amdgpu_waves_per_eu(3, 3)))
 void mla_attn_kernel(const MlaAttnArgs a) {
-  constexpr int kQuarters = Q;
+  static_assert(Q == 1, "one 32-position quarter per step");
   constexpr int kAttnWaves = AttnShape<Q>::waves;
   constexpr int kStep = AttnShape<Q>::step;
   constexpr int kLatStage = AttnShape<Q>::lat_stage;
   constexpr int kStageBytes = AttnShape<Q>::stage_bytes;
-  __shared__ uint4 smem[2 * kStageBytes / 16];   // two stages; the split merge reuses them
-  __shared__ float st_m[kAttnWaves][16];
-  __shared__ float st_l[kAttnWaves][16];
+  __shared__ uint4 smem[2 * kStageBytes / 16];   // two stages
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int u = wid / 3;    // position quarter
+  const int u = wid / 3;    // position quarter (0: one quarter per step)
   const int mt = wid % 3;   // head tile
   const int n16 = lane & 15;
   const int g = lane >> 4;
@@ -503,72 +499,280 @@ void mla_attn_kernel(const MlaAttnArgs a) {
     step(t, lds + (t & 1) * kStageBytes);
   }
 
-  // merge the four quarters of each head tile: per-head max and sum, then
-  // each quarter's share of the latent columns (64) summed in f32
-  if constexpr (Q == 1) {   // the wave holds its head tile's whole split
-    const float lsum = rows4_sum(l_run);
-    const float fself = 1.0f / lsum;
-    const size_t orow = (static_cast<size_t>(b) * a.ns + s) * a.H;
-    const int h = 16 * mt + n16;
-    if (h < a.H) {
+  // the wave holds its head tile's whole split
+  const float lsum = rows4_sum(l_run);
+  const float fself = 1.0f / lsum;
+  const size_t orow = (static_cast<size_t>(b) * a.ns + s) * a.H;
+  const int h = 16 * mt + n16;
+  if (h < a.H) {
 #pragma unroll
-      for (int ct = 0; ct < 16; ++ct) {
-        const f32x4 acc = o[ct] * fself;
-        *reinterpret_cast<uint2*>(a.op + (orow + h) * kLat + 16 * ct + 4 * g) =
-            make_uint2(pack_bf(acc[0], acc[1]), pack_bf(acc[2], acc[3]));
-      }
-      if (g == 0) {
-        a.mp[orow + h] = m_run * 0.6931471805599453f;   // natural-log units
-        a.lp[orow + h] = lsum;
-      }
+    for (int ct = 0; ct < 16; ++ct) {
+      const f32x4 acc = o[ct] * fself;
+      *reinterpret_cast<uint2*>(a.op + (orow + h) * kLat + 16 * ct + 4 * g) =
+          make_uint2(pack_bf(acc[0], acc[1]), pack_bf(acc[2], acc[3]));
     }
-    return;
-  }
-  lds_barrier();   // every wave is done with the stages
-  {
-    const float lw = rows4_sum(l_run);
     if (g == 0) {
-      st_m[wid][n16] = m_run;
-      st_l[wid][n16] = lw;
+      a.mp[orow + h] = m_run * 0.6931471805599453f;   // natural-log units
+      a.lp[orow + h] = lsum;
     }
   }
-  lds_barrier();
-  float mmax = -INFINITY;
+}
+
+// Splits of whole 128-position steps: eight waves, two per SIMD, each holding
+// the query of all 48 (padded) heads. Wave w scores positions 16w .. 16w + 15
+// of the step against every head, so each cache row is read from LDS once for
+// the scores (three times when waves own head tiles). The per-head maxima of
+// the eight position groups meet in LDS, so every wave raises the same running
+// max; the bf16 weights go to LDS in the value product's operand layout; and
+// wave w accumulates latent columns 32w .. 32w + 31 of every head over all 128
+// positions. Its O is then final for those columns: only the per-head sums are
+// combined at the end, with no merge of partial O.
+constexpr int kHW = 8;
+constexpr int kHRows = 16;                       // positions scored per wave per step
+constexpr int kHStep = kHW * kHRows;             // 128
+constexpr int kHLatStage = kHStep * kLat * 2;
+constexpr int kHStageBytes = kHLatStage + kHStep * kRope * 2;
+constexpr int kHLatDma = kHStep / 2 / kHW;       // latent DMAs per wave per step (two rows each)
+constexpr int kHRopeDma = kHStep / 16 / kHW;     // rope DMAs per wave per step (16 rows each)
+constexpr int kHStepVm = kHLatDma + kHRopeDma;
+static_assert(kHStepVm * kHW * 16 * kWave == kHStageBytes, "step DMA split evenly over the waves");
+constexpr int kHQDma = 4;                        // query DMAs per wave: 32 KB >= 48 heads x 576 B
+static_assert(kHQDma * kHW * 16 * kWave >= kHeadRows * kQK * 2 && kHQDma * kHW * 16 * kWave <= kHStageBytes,
+              "the query fits the second stage");
+static_assert(kHQDma + 2 * kHStepVm <= 63, "the DMAs in flight fit the vmcnt counter");
+constexpr int kHWaitVmStep = waitcnt_vm(kHStepVm);
+
+__global__ __launch_bounds__(kHW * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void mla_attn_heads_kernel(const MlaAttnArgs a) {
+  __shared__ uint4 smem[2 * kHStageBytes / 16];   // two stages of cache rows
+  __shared__ uint2 pw[kHStep / 32][3][kWave][2];  // P^T operands [32-position group][head tile][lane][half]
+  __shared__ float sx[kHW][kHeadRows];            // per-wave head maxima, at the end the sums
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int n16 = lane & 15;
+  const int g = lane >> 4;
+  const int s = blockIdx.x;
+  const int b = blockIdx.y;
+
+  int last = __builtin_amdgcn_readfirstlane(a.wr[b]);
+  if (last < 0 || last >= a.cap) {
+    if (s == 0 && threadIdx.x == 0) set_err(a.err, 4);
+    last = last < 0 ? -1 : a.cap - 1;
+  }
+  const int n = last + 1;
+  const int pos0 = s * kHStep * a.tiles;
+  if (pos0 >= n) return;
+  const int nsteps = min(a.tiles, (n - pos0 + kHStep - 1) / kHStep);
+  const uint16_t* lat = a.lat + static_cast<size_t>(b) * a.cap * kLat;
+  const uint16_t* rk = a.rk + static_cast<size_t>(b) * a.cap * kRope;
+  const char* lds = reinterpret_cast<const char*>(smem);
+  const uint32_t lds0 = lds_offset(smem);
+
+  // step t's rows into stage st: latent DMA j lands rows 2j, 2j + 1 (wave w
+  // issues j = 8w .. 8w + 7), rope DMA j rows 16j .. 16j + 15 (wave w: j = w).
+  // Rows past the context load the last live row (finite; their weight is 0).
+  auto issue = [&](int t, int st) __attribute__((always_inline)) {
+    const int p0 = pos0 + kHStep * t;
 #pragma unroll
-  for (int v = 0; v < kQuarters; ++v) mmax = fmaxf(mmax, st_m[3 * v + mt][n16]);   // quarter 0 saw pos0
-  float lsum = 0.f;
-#pragma unroll
-  for (int v = 0; v < kQuarters; ++v)
-    lsum += st_l[3 * v + mt][n16] * __builtin_amdgcn_exp2f(st_m[3 * v + mt][n16] - mmax);
-  const float fself = __builtin_amdgcn_exp2f(m_run - mmax) / lsum;
-  // columns 64v .. 64v + 63 of head tile mt belong to quarter v; the other
-  // quarters' parts go through LDS: xb[mt][owner][sender slot][ct % 4][lane]
-  f32x4* xb = reinterpret_cast<f32x4*>(smem);
-  static_assert(3 * kQuarters * 3 * 4 * kWave * 16 <= 2 * kStageBytes, "merge fits the stages");
-#pragma unroll
-  for (int ct = 0; ct < 16; ++ct) {
-    const int owner = ct >> 2;
-    if (owner != u) {
-      const int slot = u < owner ? u : u - 1;
-      xb[(((mt * kQuarters + owner) * 3 + slot) * 4 + (ct & 3)) * kWave + lane] = o[ct] * fself;
+    for (int i = 0; i < kHLatDma; ++i) {
+      const int j = kHLatDma * w + i;
+      const int row = 2 * j + (lane >> 5);
+      const int p = min(p0 + row, n - 1);
+      lds_dma16_stream(lat + static_cast<size_t>(p) * kLat + 8 * lat_slot(row, lane & 31),
+                       lds0 + st * kHStageBytes + j * 16 * kWave);
     }
+#pragma unroll
+    for (int i = 0; i < kHRopeDma; ++i) {
+      const int j = kHRopeDma * w + i;
+      const int row = 16 * j + (lane >> 2);
+      const int p = min(p0 + row, n - 1);
+      lds_dma16_stream(rk + static_cast<size_t>(p) * kRope + 8 * rope_slot(row, lane & 3),
+                       lds0 + st * kHStageBytes + kHLatStage + j * 16 * kWave);
+    }
+  };
+
+  // The query rows of the sequence (H x 576 bytes) go by DMA into the second
+  // stage, then to registers, before that stage is filled. Every load of the
+  // kernel is then a DMA the waits below count exactly: step 0 starts once its
+  // own rows have landed, with step 1's still in flight behind them (a query
+  // held by register loads would be waited for by the compiler with a wait
+  // for every load in flight, step 1's rows included).
+  {
+    const int qbytes = a.H * kQK * 2;
+    const char* qseq = reinterpret_cast<const char*>(a.q + static_cast<size_t>(b) * a.H * kQK);
+#pragma unroll
+    for (int i = 0; i < kHQDma; ++i) {
+      const int j = kHW * i + w;   // 1 KB piece j of the query rows (pieces past the end re-read the last 16 bytes)
+      lds_dma16(qseq + min(1024 * j + 16 * lane, qbytes - 16), lds0 + kHStageBytes + j * 16 * kWave);
+    }
+  }
+  issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(kHStepVm));   // this wave's query pieces landed
+  lds_barrier();
+  // q^T operands of the three head tiles, resident: lane (n16, g) holds
+  // q[head 16mt + n16][32ks + 8g .. +7] (padding heads repeat the last head)
+  uint4 qop[3][9];
+#pragma unroll
+  for (int mt = 0; mt < 3; ++mt) {
+    const char* qrow = lds + kHStageBytes + min(16 * mt + n16, a.H - 1) * kQK * 2 + 16 * g;
+#pragma unroll
+    for (int ks = 0; ks < 9; ++ks) qop[mt][ks] = *reinterpret_cast<const uint4*>(qrow + 64 * ks);
+  }
+  lds_barrier();   // every wave has its query: the second stage is free
+  if (nsteps > 1) issue(1, 1);
+
+  // score operand ks of wave w: row 16w + n16, chunk 4ks + g
+  const int fs = ((n16 & 7) << 1) | (n16 >> 3);
+  uint32_t so[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) so[j] = (kHRows * w + n16) * 2 * kLat + 16 * (g ^ (fs & 3)) + 64 * (j ^ (fs >> 2));
+  const uint32_t ro = kHLatStage + (kHRows * w + n16) * 2 * kRope + 16 * (g ^ ((n16 >> 2) & 3));
+  // value operand of column tile 2w + c over 32-position group kk: rows 32kk +
+  // r1 and 32kk + r1 + 16 (r1 = 4g + n16 / 4), columns 16 (2w + c) + 4 (n16 %
+  // 4), at tw[c] + 16384 kk (+ 8192 for the second row)
+  const int r1 = 4 * g + (n16 >> 2);
+  const int f1 = ((r1 & 7) << 1) | ((r1 >> 3) & 1);
+  uint32_t tw[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int ct = 2 * w + c;
+    tw[c] = r1 * 2 * kLat + 16 * (((n16 & 3) >> 1) ^ (f1 & 1)) + 8 * (n16 & 1) + 32 * ((ct & 7) ^ (f1 >> 1)) +
+            256 * (ct >> 3);
+  }
+
+  // running state of head 16mt + n16 (the same in every wave; l_run sums only
+  // this lane's own positions)
+  float m_run[3] = {-INFINITY, -INFINITY, -INFINITY};
+  float l_run[3] = {0.f, 0.f, 0.f};
+  bool started[3] = {false, false, false};
+  f32x4 o[3][2];   // O^T[latent column 16 (2w + c) + 4g + r][head 16mt + n16]
+#pragma unroll
+  for (int mt = 0; mt < 3; ++mt) o[mt][0] = o[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto step = [&](int t, const char* stage) __attribute__((always_inline)) {
+    const int pb = pos0 + kHStep * t + kHRows * w;
+    const bool live = pb < n;   // some position of this wave's 16 is in the context
+    f32x4 sacc[3];
+#pragma unroll
+    for (int mt = 0; mt < 3; ++mt) sacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (live) {
+#pragma unroll
+      for (int ks = 0; ks < 9; ++ks) {
+        const uint4 aop = ks < 8 ? *reinterpret_cast<const uint4*>(stage + so[ks & 3] + 256 * (ks >> 2))
+                                 : *reinterpret_cast<const uint4*>(stage + ro);
+#pragma unroll
+        for (int mt = 0; mt < 3; ++mt)
+          sacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(aop), as_bf8(qop[mt][ks]), sacc[mt], 0, 0, 0);
+      }
+    }
+    // scores in log2 units; masked positions (and a whole dead wave) -inf
+    float sv[3][4];
+#pragma unroll
+    for (int mt = 0; mt < 3; ++mt) {
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sv[mt][r] = live && pb + 4 * g + r < n ? sacc[mt][r] * a.scale_log2 : -INFINITY;
+        tmax = fmaxf(tmax, sv[mt][r]);
+      }
+      tmax = rows4_max(tmax);
+      if (g == 0) sx[w][16 * mt + n16] = tmax;
+    }
+    lds_barrier();
+    // the step max of each head over the eight groups; the running max is
+    // raised (and O rescaled) only when some head of the tile passes it by
+    // kSlack -- the same decision in every wave, which read the same maxima
+#pragma unroll
+    for (int mt = 0; mt < 3; ++mt) {
+      const int h = 16 * mt + n16;
+      float smax = sx[0][h];
+#pragma unroll
+      for (int v = 1; v < kHW; ++v) smax = fmaxf(smax, sx[v][h]);
+      if (__builtin_amdgcn_ballot_w64(smax > m_run[mt] + kSlack) != 0) {
+        const float m_new = fmaxf(m_run[mt], smax);
+        const float alpha = __builtin_amdgcn_exp2f(m_run[mt] - m_new);   // 0 while m_run is -inf
+        l_run[mt] *= alpha;
+        m_run[mt] = m_new;
+        if (started[mt]) {
+          o[mt][0] *= alpha;
+          o[mt][1] *= alpha;
+        }
+        started[mt] = true;
+      }
+      float e[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        e[r] = __builtin_amdgcn_exp2f(sv[mt][r] - m_run[mt]);   // masked: exp2(-inf) = 0
+        l_run[mt] += e[r];
+      }
+      // half (w % 2) of the P^T operand of group w / 2: bf16 weights of
+      // positions 4g .. 4g + 3 of this wave's 16 (all zero past the context)
+      pw[w >> 1][mt][lane][w & 1] = make_uint2(pack_bf(e[0], e[1]), pack_bf(e[2], e[3]));
+    }
+    lds_barrier();
+    // O^T += C^T . P^T over the step's four 32-position groups, this wave's 32 columns
+#pragma unroll
+    for (int kk = 0; kk < kHStep / 32; ++kk) {
+      uint4 aop[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const uint2 v1 = ld_tr(stage + tw[c] + 16384 * kk);
+        const uint2 v2 = ld_tr(stage + tw[c] + 16384 * kk + 8192);
+        aop[c] = make_uint4(v1.x, v1.y, v2.x, v2.y);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 3; ++mt) {
+        const uint4 pop = *reinterpret_cast<const uint4*>(&pw[kk][mt][lane][0]);
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          o[mt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(aop[c]), as_bf8(pop), o[mt][c], 0, 0, 0);
+      }
+    }
+  };
+
+  // the next step's DMA goes out once every wave is past the step barrier,
+  // i.e. done with the stage it refills
+  if (nsteps > 1)
+    __builtin_amdgcn_s_waitcnt(kHWaitVmStep);
+  else
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  block_barrier();
+  step(0, lds);
+  for (int t = 1; t < nsteps; ++t) {
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    block_barrier();
+    if (t + 1 < nsteps) issue(t + 1, (t + 1) & 1);
+    step(t, lds + (t & 1) * kHStageBytes);
+  }
+
+  // the per-head sums of the eight groups (every wave is past the last maxima
+  // read, so sx is free), in group order; each wave stores its own columns
+#pragma unroll
+  for (int mt = 0; mt < 3; ++mt) {
+    const float lw = rows4_sum(l_run[mt]);
+    if (g == 0) sx[w][16 * mt + n16] = lw;
   }
   lds_barrier();
   const size_t orow = (static_cast<size_t>(b) * a.ns + s) * a.H;
-  const int h = 16 * mt + n16;
 #pragma unroll
-  for (int ct = 0; ct < 16; ++ct) {
-    if ((ct >> 2) != u) continue;
-    f32x4 acc = o[ct] * fself;
+  for (int mt = 0; mt < 3; ++mt) {
+    const int h = 16 * mt + n16;
+    if (h >= a.H) continue;
+    float lsum = sx[0][h];
 #pragma unroll
-    for (int slot = 0; slot < 3; ++slot) acc += xb[(((mt * kQuarters + u) * 3 + slot) * 4 + (ct & 3)) * kWave + lane];
-    if (h < a.H)
-      *reinterpret_cast<uint2*>(a.op + (orow + h) * kLat + 16 * ct + 4 * g) =
+    for (int v = 1; v < kHW; ++v) lsum += sx[v][h];
+    const float inv = 1.0f / lsum;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const f32x4 acc = o[mt][c] * inv;
+      *reinterpret_cast<uint2*>(a.op + (orow + h) * kLat + 16 * (2 * w + c) + 4 * g) =
           make_uint2(pack_bf(acc[0], acc[1]), pack_bf(acc[2], acc[3]));
-  }
-  if (u == 0 && g == 0 && h < a.H) {
-    a.mp[orow + h] = mmax * 0.6931471805599453f;   // natural-log units
-    a.lp[orow + h] = lsum;
+    }
+    if (w == 0 && g == 0) {
+      a.mp[orow + h] = m_run[mt] * 0.6931471805599453f;   // natural-log units
+      a.lp[orow + h] = lsum;
+    }
   }
 }
 
@@ -998,9 +1202,8 @@ int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* r
   TFA_REQUIRE(batch >= 1 && batch <= 65535, TFA_ERR_SHAPE, "tfa_mla_attention: batch %lld out of range", (long long)batch);
   TFA_REQUIRE(heads >= 1 && heads <= kHeadRows, TFA_ERR_SHAPE, "tfa_mla_attention: heads %lld not in [1, %d]",
               (long long)heads, kHeadRows);
-  const bool quarters = split % AttnShape<4>::step == 0;   // whole 128-position steps
-  TFA_REQUIRE(split >= 1 && split <= 8 * AttnShape<4>::step &&
-                  (quarters || (split % kWaveRows == 0 && split < AttnShape<4>::step)),
+  const bool whole = split % kHStep == 0;   // whole 128-position steps
+  TFA_REQUIRE(split >= 1 && split <= 8 * kHStep && (whole || (split % kWaveRows == 0 && split < kHStep)),
               TFA_ERR_SHAPE, "tfa_mla_attention: split %lld must be 32, 64, 96 or a multiple of 128 up to 1024",
               (long long)split);
   TFA_REQUIRE(cap >= 1 && cap % split == 0 && cap / split <= kMaxSplits, TFA_ERR_SHAPE,
@@ -1021,12 +1224,12 @@ int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* r
   a.H = (int)heads;
   a.cap = (int)cap;
   a.ns = (int)(cap / split);
-  a.tiles = (int)(split / (quarters ? AttnShape<4>::step : AttnShape<1>::step));
+  a.tiles = (int)(split / (whole ? kHStep : AttnShape<1>::step));
   a.scale = scale;
   a.scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid(a.ns, (unsigned)batch);
-  if (quarters)
-    mla_attn_kernel<4><<<grid, 3 * 4 * kWave, 0, stream>>>(a);
+  if (whole)
+    mla_attn_heads_kernel<<<grid, kHW * kWave, 0, stream>>>(a);
   else
     mla_attn_kernel<1><<<grid, 3 * 1 * kWave, 0, stream>>>(a);
   return launched("mla_attn");
