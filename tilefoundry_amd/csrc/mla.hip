@@ -541,12 +541,13 @@ static_assert(kHQDma * kHW * 16 * kWave >= kHeadRows * kQK * 2 && kHQDma * kHW *
               "the query fits the second stage");
 static_assert(kHQDma + 2 * kHStepVm <= 63, "the DMAs in flight fit the vmcnt counter");
 constexpr int kHWaitVmStep = waitcnt_vm(kHStepVm);
+static_assert(kHW == 8, "a head's eight wave maxima / sums are two float4 in LDS");
 
 __global__ __launch_bounds__(kHW * kWave) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mla_attn_heads_kernel(const MlaAttnArgs a) {
   __shared__ uint4 smem[2 * kHStageBytes / 16];   // two stages of cache rows
   __shared__ uint2 pw[kHStep / 32][3][kWave][2];  // P^T operands [32-position group][head tile][lane][half]
-  __shared__ float sx[kHW][kHeadRows];            // per-wave head maxima, at the end the sums
+  __shared__ float4 sx[kHeadRows][kHW / 4];       // per-head maxima of the waves, at the end their sums
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -677,7 +678,7 @@ void mla_attn_heads_kernel(const MlaAttnArgs a) {
         tmax = fmaxf(tmax, sv[mt][r]);
       }
       tmax = rows4_max(tmax);
-      if (g == 0) sx[w][16 * mt + n16] = tmax;
+      if (g == 0) reinterpret_cast<float*>(sx[16 * mt + n16])[w] = tmax;
     }
     lds_barrier();
     // the step max of each head over the eight groups; the running max is
@@ -686,9 +687,8 @@ void mla_attn_heads_kernel(const MlaAttnArgs a) {
 #pragma unroll
     for (int mt = 0; mt < 3; ++mt) {
       const int h = 16 * mt + n16;
-      float smax = sx[0][h];
-#pragma unroll
-      for (int v = 1; v < kHW; ++v) smax = fmaxf(smax, sx[v][h]);
+      const float4 x0 = sx[h][0], x1 = sx[h][1];
+      const float smax = fmaxf(fmaxf(fmaxf(x0.x, x0.y), fmaxf(x0.z, x0.w)), fmaxf(fmaxf(x1.x, x1.y), fmaxf(x1.z, x1.w)));
       if (__builtin_amdgcn_ballot_w64(smax > m_run[mt] + kSlack) != 0) {
         const float m_new = fmaxf(m_run[mt], smax);
         const float alpha = __builtin_amdgcn_exp2f(m_run[mt] - m_new);   // 0 while m_run is -inf
@@ -751,7 +751,7 @@ void mla_attn_heads_kernel(const MlaAttnArgs a) {
 #pragma unroll
   for (int mt = 0; mt < 3; ++mt) {
     const float lw = rows4_sum(l_run[mt]);
-    if (g == 0) sx[w][16 * mt + n16] = lw;
+    if (g == 0) reinterpret_cast<float*>(sx[16 * mt + n16])[w] = lw;
   }
   lds_barrier();
   const size_t orow = (static_cast<size_t>(b) * a.ns + s) * a.H;
@@ -759,9 +759,8 @@ void mla_attn_heads_kernel(const MlaAttnArgs a) {
   for (int mt = 0; mt < 3; ++mt) {
     const int h = 16 * mt + n16;
     if (h >= a.H) continue;
-    float lsum = sx[0][h];
-#pragma unroll
-    for (int v = 1; v < kHW; ++v) lsum += sx[v][h];
+    const float4 x0 = sx[h][0], x1 = sx[h][1];
+    const float lsum = ((((((x0.x + x0.y) + x0.z) + x0.w) + x1.x) + x1.y) + x1.z) + x1.w;   // wave order
     const float inv = 1.0f / lsum;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -835,55 +834,85 @@ __global__ __launch_bounds__(kThreads) void mla_combine_up_kernel(
 // split's weight reaches the other lanes by readlane, and the denominator and
 // the weighted sum run in split order as in the loop form.
 constexpr int kFastMergeSplits = 64;
+// One block per (head, sequence), every load issued first and 16 bytes wide:
+// thread t takes latent columns 8 (t % 32) .. + 7 of splits t / 32, t / 32 + 8,
+// ... (NSP / 8 loads), weights them with w_s = l_s e^(m_s - M), and the eight
+// split groups meet -- lane pairs (l, l ^ 32) in registers, then the four
+// waves in order through LDS -- in o_lat = sum_s w_s op_s / sum_s w_s (f32).
+// Then attn[b, h*64 + v] = bf16(W_UV[h][v] . o_lat).
 template <int NSP>   // splits, rounded up to 16 / 32 / 64
 __global__ __launch_bounds__(kThreads) void mla_combine_up_fast_kernel(
     const uint16_t* __restrict__ op, const float* __restrict__ mp, const float* __restrict__ lp,
     const int* __restrict__ wr, int ns, int split, int H, int cap, const uint16_t* __restrict__ w_kv_b,
     uint16_t* __restrict__ attn) {
+  static_assert(NSP % 8 == 0 && NSP <= kWave, "splits in eight groups, one lane each for the weights");
+  constexpr int kPer = NSP / 8;   // splits per thread
+  __shared__ float red[kWaves][kLat];
   __shared__ float olat[kLat];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(t / kWave);
   const size_t srow = static_cast<size_t>(b) * ns * H + h;   // (b, s=0, h)
   // 1. every load, none behind a branch (a split past ns re-reads split ns - 1)
   const int last_raw = wr[b];
   const int sl = min(lane, ns - 1);
   const float m_l = mp[srow + static_cast<size_t>(sl) * H];
   const float l_l = lp[srow + static_cast<size_t>(sl) * H];
-  uint16_t ov[NSP];
+  const int cc = lane & 31;               // columns 8cc .. 8cc + 7
+  const int hi = lane >> 5;
+  const int sg = 2 * wv + hi;             // splits sg + 8i
+  uint4 ov[kPer];
 #pragma unroll
-  for (int s = 0; s < NSP; ++s) ov[s] = op[(srow + static_cast<size_t>(min(s, ns - 1)) * H) * kLat + t];
+  for (int i = 0; i < kPer; ++i)
+    ov[i] = ld16(op + (srow + static_cast<size_t>(min(sg + 8 * i, ns - 1)) * H) * kLat + 8 * cc);
   const int v = t >> 2, q = t & 3;   // value row v, latent quarter q
   const uint16_t* wrow = w_kv_b + (static_cast<size_t>(h) * kKvB + kNope + v) * kLat + 64 * q;
-  uint4 wv[8];
+  uint4 wv8[8];
 #pragma unroll
-  for (int c8 = 0; c8 < 8; ++c8) wv[c8] = ld16(wrow + 8 * c8);
+  for (int c8 = 0; c8 < 8; ++c8) wv8[c8] = ld16(wrow + 8 * c8);
   __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the first is read
-  // 2. weights of the live splits
+  // 2. weights of the live splits (lane s holds split s)
   const int last = last_raw < 0 ? 0 : (last_raw >= cap ? cap - 1 : last_raw);
   const int nsa = min(ns, last / split + 1);
   const bool live = lane < nsa;
   const float M = lanes_max<6>(live ? m_l : -INFINITY);
   const float w = live ? l_l * expf(m_l - M) : 0.f;
-  // 3. o_lat[t] = sum_s w_s op_s / sum_s w_s in split order (dead splits add
-  //    exact zeros: their weight and their value are selected away)
-  float L = 0.f, acc = 0.f;
+  const float L = lanes_sum<6>(w);
+  // 3. this thread's splits in order (dead splits add exact zeros: their weight
+  //    and their value are selected away), then the lane pair, then the waves
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int s = 0; s < NSP; ++s) {
-    const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
-    const float val = s < nsa ? bf2f(ov[s]) : 0.f;
-    L += ws;
-    acc = fmaf(ws, val, acc);
+  for (int i = 0; i < kPer; ++i) {
+    const float w_lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), 2 * wv + 8 * i));
+    const float w_hi =
+        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), 2 * wv + 1 + 8 * i));
+    const float ws = hi ? w_hi : w_lo;
+    const bool in = sg + 8 * i < nsa;
+    float x[8];
+    unpack8(ov[i], x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = fmaf(ws, in ? x[j] : 0.f, acc[j]);
   }
-  olat[t] = acc / L;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[j]), __float_as_uint(acc[j]), false, false);
+    acc[j] = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+  }
+  if (hi == 0) {
+    *reinterpret_cast<float4*>(&red[wv][8 * cc]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    *reinterpret_cast<float4*>(&red[wv][8 * cc + 4]) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
+  lds_barrier();
+  olat[t] = (((red[0][t] + red[1][t]) + red[2][t]) + red[3][t]) / L;
   lds_barrier();
   // 4. attn[b, h*64 + v] = bf16(W_UV[h][v] . o_lat)
   float d = 0.f;
 #pragma unroll
   for (int c8 = 0; c8 < 8; ++c8) {
     float w8[8];
-    unpack8(wv[c8], w8);
+    unpack8(wv8[c8], w8);
 #pragma unroll
     for (int i = 0; i < 8; ++i) d = fmaf(w8[i], olat[64 * q + 8 * c8 + i], d);
   }
