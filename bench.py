@@ -490,13 +490,22 @@ def prefill_layer(ns=(1024, 4096, 8192)) -> dict:
         f_qkv = lambda: C.qkv_norm_rope(hn, w_qkv, qkv, HQ, HKV, gq, gk, 1e-6, cos, sin)
         f_att = lambda: C.prefill_attention(qv[:, :, :D], kv, vv, qv[:, :, D:], attn, D ** -0.5)
         f_o = lambda: C.gemm_nt(attn, w_o, res, hidden)
-        for _ in range(3):          # clocks up and caches warm before any timing
+        # clocks up before any timing: the layer repeated for 0.2 s (a few
+        # calls of the 1024-token layer, ~0.3 ms, leave the first timing on
+        # ramping clocks), then each part timed over ~5 ms of calls
+        t_end = time.perf_counter() + 0.2
+        while time.perf_counter() < t_end:
             f_qkv(), f_att(), f_o()
-        reps = 20 if n <= 4096 else 8
-        t_qkv = _events_time(f_qkv, reps)
-        t_att = _events_time(f_att, reps)
-        t_o = _events_time(f_o, reps)
-        t_layer = _events_time(lambda: (f_qkv(), f_att(), f_o()), max(4, reps // 2))
+            torch.cuda.synchronize()
+
+        def timed(fn):
+            reps = max(8, min(400, int(5.0 / max(_events_time(fn, 3), 1e-3))))
+            return _events_time(fn, reps)
+
+        t_qkv = timed(f_qkv)
+        t_att = timed(f_att)
+        t_o = timed(f_o)
+        t_layer = timed(lambda: (f_qkv(), f_att(), f_o()))
         fl_att = 12288.0 * n * n
         fl_qkv = 2.0 * n * W * HID
         fl_o = 2.0 * n * HID * HQ * D
