@@ -403,7 +403,8 @@ int tfa_mla_q_absorb(const float* q_part, int64_t ks, int64_t batch, int64_t hea
  * f32 with bf16 weights into the latent sum; op [batch, cap/split, heads, 256]
  * bf16 = the split's latent sum / its own weight sum, mp / lp [batch,
  * cap/split, heads] its max and sum. Only splits holding slots <= wr[b] are
- * written. A wr outside [0, cap) sets *err = 4 (clamped).
+ * written. A wr outside [0, cap) sets *err = 4 (clamped). q_abs, both caches and
+ * op 16-byte aligned.
  * Replaces (absorbed form): kernels/cute_attention.py:56-200 (ROPE_ATTEND),
  * kernels/reference_ops.py:87-130 (rope_attend). */
 int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* rope_cache, const int* wr,
@@ -413,6 +414,7 @@ int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* r
 /* Merge of tfa_mla_attention's splits per (head, sequence): weights
  * w_s = lp e^(mp - max), o_lat = sum_s w_s op_s / sum_s w_s (f32), then
  * attn[b, h*64 + v] = bf16(W_UV_h o_lat) over the splits holding slots <= wr[b].
+ * op and w_kv_b 16-byte aligned.
  * Replaces (absorbed form): the 8-warp LSE merge of kernels/cute_attention.py:56-200
  * and the value half of W_kv_b applied per position in reference_ops.py:111-128. */
 int tfa_mla_combine_up(const void* op, const float* mp, const float* lp, const int* wr, int64_t splits,

@@ -753,25 +753,38 @@ void mla_attn_heads_kernel(const MlaAttnArgs a) {
     const float lw = rows4_sum(l_run[mt]);
     if (g == 0) reinterpret_cast<float*>(sx[16 * mt + n16])[w] = lw;
   }
-  lds_barrier();
+  lds_barrier();   // every wave is past its last stage read: the stages are free
+  // the normalised split output, through LDS so that each store instruction
+  // writes 1 KB of whole head rows (rows padded to 528 bytes: the 16 heads of a
+  // lane group land on distinct banks)
+  constexpr int kOPitch = kLat + 8;
+  static_assert(kHeadRows * kOPitch * 2 <= kHStageBytes, "the split output fits a stage");
+  uint16_t* obuf = reinterpret_cast<uint16_t*>(smem);
   const size_t orow = (static_cast<size_t>(b) * a.ns + s) * a.H;
 #pragma unroll
   for (int mt = 0; mt < 3; ++mt) {
     const int h = 16 * mt + n16;
-    if (h >= a.H) continue;
     const float4 x0 = sx[h][0], x1 = sx[h][1];
     const float lsum = ((((((x0.x + x0.y) + x0.z) + x0.w) + x1.x) + x1.y) + x1.z) + x1.w;   // wave order
     const float inv = 1.0f / lsum;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const f32x4 acc = o[mt][c] * inv;
-      *reinterpret_cast<uint2*>(a.op + (orow + h) * kLat + 16 * (2 * w + c) + 4 * g) =
+      *reinterpret_cast<uint2*>(obuf + h * kOPitch + 16 * (2 * w + c) + 4 * g) =
           make_uint2(pack_bf(acc[0], acc[1]), pack_bf(acc[2], acc[3]));
     }
-    if (w == 0 && g == 0) {
+    if (w == 0 && g == 0 && h < a.H) {
       a.mp[orow + h] = m_run[mt] * 0.6931471805599453f;   // natural-log units
       a.lp[orow + h] = lsum;
     }
+  }
+  lds_barrier();
+  // 16-byte piece i of the H x 512-byte split output (consecutive heads are
+  // consecutive rows of op)
+  for (int i = threadIdx.x; i < a.H * (kLat / 8); i += kHW * kWave) {
+    const int h = i / (kLat / 8), ch = i % (kLat / 8);
+    *reinterpret_cast<uint4*>(a.op + (orow + h) * kLat + 8 * ch) =
+        *reinterpret_cast<const uint4*>(obuf + h * kOPitch + 8 * ch);
   }
 }
 
@@ -1241,6 +1254,7 @@ int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* r
   TFA_ALIGN16(q_abs);
   TFA_ALIGN16(latent_cache);
   TFA_ALIGN16(rope_cache);
+  TFA_ALIGN16(op);
   MlaAttnArgs a{};
   a.q = static_cast<const uint16_t*>(q_abs);
   a.lat = static_cast<const uint16_t*>(latent_cache);
@@ -1278,6 +1292,7 @@ int tfa_mla_combine_up(const void* op, const float* mp, const float* lp, const i
               (long long)splits, (long long)split, (long long)cap, kMaxSplits);
   TFA_REQUIRE(batch >= 1 && batch <= 65535 && heads >= 1 && heads <= kHeadRows, TFA_ERR_SHAPE,
               "tfa_mla_combine_up: batch %lld / heads %lld out of range", (long long)batch, (long long)heads);
+  TFA_ALIGN16(op);
   TFA_ALIGN16(w_kv_b);
   const dim3 grid((unsigned)heads, (unsigned)batch);
   auto fast = [&](auto nsp) {
