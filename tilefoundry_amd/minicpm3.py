@@ -333,10 +333,11 @@ class MiniCPM3Engine:
         if not 1 <= batch <= self.MAX_BATCH:
             raise ValueError(f"batch {batch} not in [1, {self.MAX_BATCH}]")
         self.nsteps = max_new + prompt_room
-        # positions per attention split: at small batch the shortest split (32,
-        # a three-wave block with no quarter merge) whose split count the merge
-        # still takes in one memory round trip (64); 256 once the batch alone
-        # fills the device. bs=1, 8 + 512 positions: 128 -> 32 took the step
+        # positions per attention split: at small batch the shortest split (32:
+        # a three-wave block over one 32-position step) whose split count the
+        # merge still takes in one memory round trip (64); 256 (eight-wave
+        # blocks over two 128-position steps) once the batch alone fills the
+        # device. bs=1, 8 + 512 positions: 128 -> 32 took the step
         # from 322 to 343 tok/s.
         if split is None:
             split = 256
