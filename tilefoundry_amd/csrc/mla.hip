@@ -70,7 +70,8 @@ TFA_DEV float rope_bf(float x, float partner, float c, float s) {
 
 // ------------------------------------------------------------------ mla_prep
 // One block per sequence. part: [ks, B, qa + 256 + 32] f32 split-K partials of
-// x_n . [W_q_a; W_kv_a]^T.
+// x_n . [W_q_a; W_kv_a]^T; KS = ks, so that exactly the live partials are loaded.
+template <int KS>
 __global__ __launch_bounds__(kThreads) void mla_prep_kernel(
     const float* __restrict__ part, int ks, int B, int qa, const uint16_t* __restrict__ gq,
     const uint16_t* __restrict__ gkv, float eps, const uint16_t* __restrict__ cos_t,
@@ -93,10 +94,10 @@ __global__ __launch_bounds__(kThreads) void mla_prep_kernel(
 #pragma unroll
   for (int j = 0; j < 4; ++j) gqr[j] = gq[min(t + kThreads * j, qa - 1)];
   const uint32_t gkr = gkv[t];
-  float qp[4][kMaxSplitsK], cp[kMaxSplitsK], rp[kMaxSplitsK];
+  float qp[4][KS], cp[KS], rp[KS];
   auto load_splits = [&](int i, float* v) __attribute__((always_inline)) {
 #pragma unroll
-    for (int sp = 0; sp < kMaxSplitsK; ++sp) v[sp] = pb[static_cast<size_t>(min(sp, ks - 1)) * kstride + i];
+    for (int sp = 0; sp < KS; ++sp) v[sp] = pb[static_cast<size_t>(sp) * kstride + i];
   };
 #pragma unroll
   for (int j = 0; j < 4; ++j) load_splits(min(t + kThreads * j, qa - 1), qp[j]);
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(kThreads) void mla_prep_kernel(
   auto landed = [&](const float* v) __attribute__((always_inline)) {
     float acc = 0.f;
 #pragma unroll
-    for (int sp = 0; sp < kMaxSplitsK; ++sp) acc += sp < ks ? v[sp] : 0.f;
+    for (int sp = 0; sp < KS; ++sp) acc += v[sp];
     return round_bf(acc);
   };
   float gqv[4], qv[4];
@@ -169,47 +170,63 @@ __global__ __launch_bounds__(kThreads) void mla_prep_kernel(
 }
 
 // -------------------------------------------------------------- mla_q_absorb
-// One block per head; thread t owns latent column t. qpart: [ks, B, H*96] f32
-// split-K partials of q_n . W_q_b^T. w_kv_b: [H*128, 256] (out, in). Every load
-// goes out first -- the head's W_UK column t, all of the thread's partials (the
-// B x 96 projection values of the head, dealt over the block, unrolled for
-// B <= MAXB), the positions -- so the block makes one memory round trip, and a
-// second only for the rope rows of the positions.
+// One block per head. qpart: [ks, B, H*96] f32 split-K partials of
+// q_n . W_q_b^T. w_kv_b: [H*128, 256] (out, in). Every load goes out first, 16
+// bytes wide -- the positions, the head's W_UK (thread t: latent columns
+// 8 (t % 32) .. + 7 of rows t / 32, t / 32 + 8, ...), the head's partials
+// (16-byte pieces dealt over the block) -- so the block makes one memory round
+// trip, and a second only for the rope rows of the positions. The partials
+// land through LDS: each projection value is the sum of its splits in split
+// order, landed in bf16. The absorbed query of eight sequences at a time: each
+// thread's eight rows in order, then the row-group pairs (lanes l, l ^ 32) in
+// registers, then the four waves in order through LDS. MAXB (1, 8 or 32) sizes
+// the unrolled loads and passes.
 template <int MAXB>
 __global__ __launch_bounds__(kThreads) void mla_q_absorb_kernel(
     const float* __restrict__ qpart, int ks, int B, int H, const uint16_t* __restrict__ w_kv_b,
     const uint16_t* __restrict__ cos_t, const uint16_t* __restrict__ sin_t, int rope_rows,
     const int* __restrict__ pos, uint16_t* __restrict__ q_abs, int* err) {
-  constexpr int kQH = kNope + kRope;                       // projection values per head
+  constexpr int kQH = kNope + kRope;                             // projection values per head
+  constexpr int kQV = kQH / 4;                                   // their 16-byte pieces per (split, sequence)
+  constexpr int kQLoads = (kMaxSplitsK * MAXB * kQV + kThreads - 1) / kThreads;
   constexpr int kPer = (MAXB * kQH + kThreads - 1) / kThreads;   // values per thread
   constexpr int kRopePer = (MAXB * kRope + kThreads - 1) / kThreads;
+  constexpr int kGroup = MAXB < 8 ? MAXB : 8;                    // sequences per absorption pass
+  constexpr int kRows = kNope / 8;                               // W_UK rows per thread
+  __shared__ float4 qraw[kMaxSplitsK * MAXB * kQV];              // [split][sequence][piece]
   __shared__ float qn[MAXB][kNope];
   __shared__ float qr[MAXB][kRope];
+  __shared__ float red[kWaves][kGroup][kLat];
   const int h = blockIdx.x;
   const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int cc = lane & 31;          // latent columns 8cc .. 8cc + 7
+  const int hi = lane >> 5;
+  const int rg = 2 * wv + hi;        // W_UK rows rg + 8k
   const int qrow = H * kQH;
   const size_t kstride = static_cast<size_t>(B) * qrow;
-  const int nval = B * kQH;
-  // 1. the positions first, then the W_UK column and every split-K partial; the
-  //    rope rows go out as soon as the positions are in, while the rest is
-  //    still in flight (loads complete in issue order), so the kernel is about
-  //    one memory round trip
+  const int nq = ks * B * kQV;
+  // 1. every load, none behind a branch (indices past the live range re-read
+  //    the last piece, in bounds; their values are not used)
   int pr[kRopePer];
 #pragma unroll
   for (int j = 0; j < kRopePer; ++j) pr[j] = pos[min((t + kThreads * j) / kRope, B - 1)];
-  uint32_t wraw[kNope];
-  const uint16_t* wuk = w_kv_b + static_cast<size_t>(h) * kKvB * kLat + t;
+  uint4 wk[kRows];
+  const uint16_t* wuk = w_kv_b + (static_cast<size_t>(h) * kKvB + rg) * kLat + 8 * cc;
 #pragma unroll
-  for (int i = 0; i < kNope; ++i) wraw[i] = wuk[static_cast<size_t>(i) * kLat];
-  float part[kPer][kMaxSplitsK];
+  for (int k = 0; k < kRows; ++k) wk[k] = ld16(wuk + static_cast<size_t>(8 * k) * kLat);
+  // the partials in passes of kQPass pieces a thread (one pass up to batch 8)
+  constexpr int kQPass = kQLoads < 6 ? kQLoads : 6;
+  auto piece = [&](int j) __attribute__((always_inline)) {
+    const int e = min(t + kThreads * j, nq - 1);
+    const int sp = e / (B * kQV), r = e % (B * kQV);
+    return *reinterpret_cast<const float4*>(qpart + sp * kstride + static_cast<size_t>(r / kQV) * qrow + h * kQH +
+                                            4 * (r % kQV));
+  };
+  float4 qv[kQPass];
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int e = min(t + kThreads * j, nval - 1);
-    const int b = e / kQH, i = e % kQH;
-    const float* src = qpart + static_cast<size_t>(b) * qrow + h * kQH + i;
-#pragma unroll
-    for (int sp = 0; sp < kMaxSplitsK; ++sp) part[j][sp] = src[static_cast<size_t>(min(sp, ks - 1)) * kstride];
-  }
+  for (int j = 0; j < kQPass; ++j) qv[j] = piece(j);
   uint32_t csr[kRopePer], snr[kRopePer];
 #pragma unroll
   for (int j = 0; j < kRopePer; ++j) {
@@ -227,30 +244,75 @@ __global__ __launch_bounds__(kThreads) void mla_q_absorb_kernel(
   __builtin_amdgcn_sched_barrier(0);
   // 2. the projection values land in bf16 (split order)
 #pragma unroll
+  for (int j = 0; j < kQPass; ++j)
+    if (t + kThreads * j < nq) qraw[t + kThreads * j] = qv[j];
+  for (int j0 = kQPass; j0 < kQLoads; j0 += kQPass) {
+    float4 qw[kQPass];
+#pragma unroll
+    for (int j = 0; j < kQPass; ++j) qw[j] = piece(j0 + j);
+#pragma unroll
+    for (int j = 0; j < kQPass; ++j)
+      if (t + kThreads * (j0 + j) < nq) qraw[t + kThreads * (j0 + j)] = qw[j];
+  }
+  lds_barrier();
+  const float* qf = reinterpret_cast<const float*>(qraw);
+#pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int e = t + kThreads * j;
-    if (e >= nval) continue;
+    if (e >= B * kQH) continue;
+    const int b = e / kQH, i = e % kQH;
     float acc = 0.f;
 #pragma unroll
-    for (int sp = 0; sp < kMaxSplitsK; ++sp) acc += sp < ks ? part[j][sp] : 0.f;
-    const int b = e / kQH, i = e % kQH;
+    for (int sp = 0; sp < kMaxSplitsK; ++sp) acc += sp < ks ? qf[(sp * B + b) * kQH + i] : 0.f;
     if (i < kNope) qn[b][i] = round_bf(acc);
     else qr[b][i - kNope] = round_bf(acc);
   }
-  float wc[kNope], cs[kRopePer], sn[kRopePer];
-#pragma unroll
-  for (int i = 0; i < kNope; ++i) wc[i] = bf2f(wraw[i]);
+  float cs[kRopePer], sn[kRopePer];
 #pragma unroll
   for (int j = 0; j < kRopePer; ++j) {
     cs[j] = bf2f(csr[j]);
     sn[j] = bf2f(snr[j]);
   }
   lds_barrier();
-  for (int b = 0; b < B; ++b) {
-    float acc = 0.f;
+  // 3. q_abs[b, h, c] = bf16(sum_i qn[b][i] W_UK[i][c]), eight sequences a pass
+  for (int b0 = 0; b0 < B; b0 += kGroup) {
+    float acc[kGroup][8];
 #pragma unroll
-    for (int i = 0; i < kNope; ++i) acc = fmaf(qn[b][i], wc[i], acc);
-    q_abs[(static_cast<size_t>(b) * H + h) * kQK + t] = static_cast<uint16_t>(f2bf(acc));
+    for (int j = 0; j < kGroup; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
+#pragma unroll
+    for (int k = 0; k < kRows; ++k) {
+      float w[8];
+      unpack8(wk[k], w);
+#pragma unroll
+      for (int j = 0; j < kGroup; ++j) {
+        const float q = qn[min(b0 + j, B - 1)][rg + 8 * k];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(q, w[e], acc[j][e]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[j][e]), __float_as_uint(acc[j][e]), false, false);
+        acc[j][e] = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+      }
+      if (hi == 0) {
+        *reinterpret_cast<float4*>(&red[wv][j][8 * cc]) = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+        *reinterpret_cast<float4*>(&red[wv][j][8 * cc + 4]) = make_float4(acc[j][4], acc[j][5], acc[j][6], acc[j][7]);
+      }
+    }
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) {
+      const int b = b0 + j;
+      if (b < B)
+        q_abs[(static_cast<size_t>(b) * H + h) * kQK + t] =
+            static_cast<uint16_t>(f2bf(((red[0][j][t] + red[1][j][t]) + red[2][j][t]) + red[3][j][t]));
+    }
+    lds_barrier();
   }
 #pragma unroll
   for (int j = 0; j < kRopePer; ++j) {
@@ -936,15 +998,16 @@ __global__ __launch_bounds__(kThreads) void mla_combine_up_fast_kernel(
 // ------------------------------------------------------------- rows_residual
 // out[m, i] = bf16(res[m, i] + bf16(bf16(sum_s part[s, m, i]) * alpha)), 8 elements
 // per thread.
+template <int KS>   // the split count: exactly the live partials are loaded
 __global__ __launch_bounds__(kThreads) void rows_residual_kernel(
-    const float* __restrict__ part, int ks, const uint16_t* __restrict__ res, float alpha,
+    const float* __restrict__ part, const uint16_t* __restrict__ res, float alpha,
     uint16_t* __restrict__ out, int M, int N) {
   const size_t e0 = (static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x) * 8;
   const size_t total = static_cast<size_t>(M) * N;
   if (e0 >= total) return;
   const uint4 rv = ld16(res + e0);   // issued with the partials: one round trip
   float acc[8];
-  sum_splits8(part + e0, total, ks, acc);
+  sum_splits8<KS>(part + e0, total, KS, acc);
   float r[8];
   unpack8(rv, r);
   float o[8];
@@ -1194,11 +1257,24 @@ int tfa_mla_prep(const float* part, int64_t ks, int64_t batch, int64_t q_lora, c
   TFA_REQUIRE(q_lora >= 1 && q_lora <= 4 * kThreads, TFA_ERR_SHAPE,
               "tfa_mla_prep: q_lora %lld not in [1, %d]", (long long)q_lora, 4 * kThreads);
   TFA_REQUIRE(cap >= 1 && rope_rows >= 1, TFA_ERR_SHAPE, "tfa_mla_prep: empty cache or rope table");
-  mla_prep_kernel<<<(int)batch, kThreads, 0, stream>>>(
-      part, (int)ks, (int)batch, (int)q_lora, static_cast<const uint16_t*>(gamma_q_a),
-      static_cast<const uint16_t*>(gamma_kv_a), eps, static_cast<const uint16_t*>(cos_t),
-      static_cast<const uint16_t*>(sin_t), (int)rope_rows, pos, static_cast<uint16_t*>(latent_cache),
-      static_cast<uint16_t*>(rope_cache), (int)cap, static_cast<uint16_t*>(q_n), err);
+  auto prep = [&](auto kc) {
+    mla_prep_kernel<decltype(kc)::value><<<(int)batch, kThreads, 0, stream>>>(
+        part, (int)ks, (int)batch, (int)q_lora, static_cast<const uint16_t*>(gamma_q_a),
+        static_cast<const uint16_t*>(gamma_kv_a), eps, static_cast<const uint16_t*>(cos_t),
+        static_cast<const uint16_t*>(sin_t), (int)rope_rows, pos, static_cast<uint16_t*>(latent_cache),
+        static_cast<uint16_t*>(rope_cache), (int)cap, static_cast<uint16_t*>(q_n), err);
+  };
+  static_assert(kMaxSplitsK == 8, "one instance per split count");
+  switch (ks) {
+    case 1: prep(std::integral_constant<int, 1>{}); break;
+    case 2: prep(std::integral_constant<int, 2>{}); break;
+    case 3: prep(std::integral_constant<int, 3>{}); break;
+    case 4: prep(std::integral_constant<int, 4>{}); break;
+    case 5: prep(std::integral_constant<int, 5>{}); break;
+    case 6: prep(std::integral_constant<int, 6>{}); break;
+    case 7: prep(std::integral_constant<int, 7>{}); break;
+    default: prep(std::integral_constant<int, 8>{}); break;
+  }
   return launched("mla_prep");
 }
 
@@ -1217,8 +1293,14 @@ int tfa_mla_q_absorb(const float* q_part, int64_t ks, int64_t batch, int64_t hea
               (long long)heads, kHeadRows);
   TFA_REQUIRE(ks >= 1 && ks <= kMaxSplitsK && rope_rows >= 1, TFA_ERR_SHAPE,
               "tfa_mla_q_absorb: ks %lld not in [1, %d] or empty rope table", (long long)ks, kMaxSplitsK);
+  TFA_ALIGN16(q_part);
   TFA_ALIGN16(w_kv_b);
-  if (batch <= 8)
+  if (batch == 1)
+    mla_q_absorb_kernel<1><<<(int)heads, kThreads, 0, stream>>>(
+        q_part, (int)ks, (int)batch, (int)heads, static_cast<const uint16_t*>(w_kv_b),
+        static_cast<const uint16_t*>(cos_t), static_cast<const uint16_t*>(sin_t), (int)rope_rows, pos,
+        static_cast<uint16_t*>(q_abs), err);
+  else if (batch <= 8)
     mla_q_absorb_kernel<8><<<(int)heads, kThreads, 0, stream>>>(
         q_part, (int)ks, (int)batch, (int)heads, static_cast<const uint16_t*>(w_kv_b),
         static_cast<const uint16_t*>(cos_t), static_cast<const uint16_t*>(sin_t), (int)rope_rows, pos,
@@ -1324,8 +1406,20 @@ int tfa_rows_residual(const float* part, int64_t ks, const void* residual, float
   TFA_ALIGN16(residual);
   TFA_ALIGN16(out);
   const int64_t blocks = (m * n / 8 + kThreads - 1) / kThreads;
-  rows_residual_kernel<<<(unsigned)blocks, kThreads, 0, stream>>>(
-      part, (int)ks, static_cast<const uint16_t*>(residual), alpha, static_cast<uint16_t*>(out), (int)m, (int)n);
+  auto run = [&](auto kc) {
+    rows_residual_kernel<decltype(kc)::value><<<(unsigned)blocks, kThreads, 0, stream>>>(
+        part, static_cast<const uint16_t*>(residual), alpha, static_cast<uint16_t*>(out), (int)m, (int)n);
+  };
+  switch (ks) {
+    case 1: run(std::integral_constant<int, 1>{}); break;
+    case 2: run(std::integral_constant<int, 2>{}); break;
+    case 3: run(std::integral_constant<int, 3>{}); break;
+    case 4: run(std::integral_constant<int, 4>{}); break;
+    case 5: run(std::integral_constant<int, 5>{}); break;
+    case 6: run(std::integral_constant<int, 6>{}); break;
+    case 7: run(std::integral_constant<int, 7>{}); break;
+    default: run(std::integral_constant<int, 8>{}); break;
+  }
   return launched("rows_residual");
 }
 
