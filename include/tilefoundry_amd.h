@@ -483,8 +483,8 @@ int tfa_rows_residual(const float* part, int64_t ks, const void* residual, float
  * scores s = scale * q[n, h] . k[j, g] (bf16 MFMA, f32 accumulate). Element
  * (n, h, d) of q / gate sits at q + n*q_rs + h*q_hs + d (k, v likewise per kv
  * head), so q, gate, k and v can be read in place from the qkv projection's
- * output. head_dim 256; n a multiple of 128; q/k/v strides multiples of 8,
- * gate/out strides multiples of 4 (elements).
+ * output. head_dim 256; n a multiple of 128; q/k/v/gate/out strides multiples
+ * of 8 (elements), every pointer 16-byte aligned.
  * Replaces: examples/qwen3_8_27b_prefill-tilelang/kernels/attention.py:313-438
  * (attention_ws / attention_tir), model.py:305-324 (Attention.attention). */
 int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void* k, int64_t k_rs, int64_t k_hs,
@@ -589,8 +589,8 @@ int tfa_prefill_qk_rope_split(const float* qkv, int64_t ks, int64_t ldq, const v
  * Element (b, r, h, d) of q sits at q + b*q_bs + r*q_rs + h*q_hs + d; k and v
  * likewise per kv head (the decode cache [batch, cap, kv_heads*D] is read in
  * place: k_rs = kv_heads*D, k_hs = D, k_bs = cap*kv_heads*D); out rows at
- * out + b*o_bs + r*o_rs. head_dim 128 or 256; any n >= 1; q/k/v strides
- * multiples of 8, out strides multiples of 4 (elements).
+ * out + b*o_bs + r*o_rs. head_dim 128 or 256; any n >= 1; q/k/v/out strides
+ * multiples of 8 (elements), every pointer 16-byte aligned.
  * Replaces: the per-token attention of the prompt walk,
  * examples/qwen3_1_7b-tilelang/fast/kernels.py:418-540 (attn_partial + merge) at each
  * position 0..n-1 (fast/engine.py:261-263); ref_src/model.py:171-215 (self_attention). */

@@ -97,6 +97,21 @@ TFA_DEV uint2 ld_tr(const uint16_t* lds_elem) {
 
 constexpr int kWaitVm0 = waitcnt_vm(0);
 
+// This wave's LDS writes are visible to its other lanes (LDS operations of one
+// wave complete in order; the fences keep the compiler from moving them).
+TFA_DEV void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Epilogue staging: each output wave's 32 rows x 64 dims of bf16(o / l) at a
+// time, rows padded by 8 elements (the 32 rows' 8-byte writes spread over the
+// banks), so that the gate is read and the output written as 16-byte pieces of
+// whole rows (128 contiguous bytes per row, eight rows per instruction).
+constexpr int kEpiDims = 64;
+constexpr int kEpiPitch = kEpiDims + 8;
+
 template <int N>
 using IC = std::integral_constant<int, N>;
 
@@ -146,8 +161,10 @@ void flash_prefill_kernel(const FlashArgs a) {
   __shared__ __attribute__((aligned(1024))) uint16_t vs0[kTK][kVPitch];
   __shared__ __attribute__((aligned(1024))) uint16_t vs1[kTK][kVPitch];
   __shared__ __attribute__((aligned(1024))) uint16_t vs2[kStages == 3 ? kTK : 1][kVPitch];
-  // the second key group's running max and sum per lane, for the final merge
-  __shared__ float ml_part[KG == 2 ? 2 : 1][KG == 2 ? W : 1][kWave];
+  // each key group's running max and sum per lane, for the final merge
+  __shared__ float ml_part[KG == 2 ? 2 : 1][KG == 2 ? NW : 1][kWave];
+  // (with two key groups the staging rows live in the stage buffers instead)
+  __shared__ __attribute__((aligned(16))) uint16_t ebuf[KG == 2 ? 1 : W][kWM][kEpiPitch];
   auto kbuf = [&](auto b) __attribute__((always_inline)) -> uint16_t(*)[kKPitch] {
     if constexpr (decltype(b)::value == 0) return ks0;
     else if constexpr (decltype(b)::value == 1) return ks1;
@@ -400,75 +417,132 @@ void flash_prefill_kernel(const FlashArgs a) {
   // no load may still be writing this block's LDS when the block ends
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
-  if constexpr (KG == 2) {
-    // Merge the key groups: the second group leaves its (max, sum, output)
-    // in the stage buffers (every wave is past its last operand read), the
-    // first rescales both to the joint max and adds. A group that saw no key
-    // has max -inf and contributes nothing. The output is 128 f32 per lane,
-    // stored lane-fastest in 16-byte pieces (each instruction 1 KB contiguous).
-    lds_barrier();
-    float4* part = reinterpret_cast<float4*>(rw == 0 ? &ks0[0][0] : rw == 1 ? &ks1[0][0] : rw == 2 ? &vs0[0][0]
-                                                                                                   : &vs1[0][0]);
-    if (kgi == 1) {
+  // epilogue: element e = 4j + r of o[dt][0] is value dim 32 dt + 8j + 4kg + r
+  // of query q0 + n32. out = bf16(bf16(o / l) * bf16(sigmoid(gate))) with the
+  // gate, bf16(o / l) without, in passes of kEpiDims dims through this wave's
+  // staging rows: bf16(o / l) into LDS, then 16-byte pieces of whole rows --
+  // piece p of a pass is row p / 8, dims 8 (p % 8) .. + 7 of the pass -- for
+  // the gate (its loads issued first: it does not depend on O) and the output.
+  // Rows past N are not stored. With two key groups the wave pair (rw, 0),
+  // (rw, 1) first merges symmetrically: wave (rw, g) keeps value dims
+  // D/2 g .. D/2 g + D/2 - 1 and hands its partner the other half of its
+  // output with its (max, sum), through the stage buffers (every wave is past
+  // its last operand read); each rescales both to the joint max and adds them,
+  // group 0's term first, so both waves hold the same sums; then each wave
+  // stores its half. A group that saw no key has max -inf and contributes
+  // nothing. A half is D/2 f32 per lane, written lane-fastest in 16-byte
+  // pieces (each instruction 1 KB contiguous).
+  static_assert(QT == 1 && D % (2 * kEpiDims) == 0, "one 32-row query tile per wave, whole passes per half");
+  constexpr int kPieces = kWM * kEpiDims / 8 / kWave;   // 16-byte pieces per lane per pass
+  constexpr int kDTP = kEpiDims / 32;                   // 32-dim output tiles per pass
+  uint16_t(*eb)[kEpiPitch] = ebuf[KG == 2 ? 0 : rw];
+  // G: the half of the value dims this wave stores (-1: all of them)
+  auto finish = [&](auto gc) __attribute__((always_inline)) {
+    constexpr int G = decltype(gc)::value;
+    constexpr int kP0 = G < 0 ? 0 : G * (D / kEpiDims / 2);
+    constexpr int kP1 = G < 0 ? D / kEpiDims : kP0 + D / kEpiDims / 2;
+    uint4 gp[GATE ? kP1 - kP0 : 1][kPieces];
+    if constexpr (GATE) {
 #pragma unroll
-      for (int dt = 0; dt < kDT; ++dt)
+      for (int c = kP0; c < kP1; ++c)
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i) {
+          const int pc = i * kWave + lane, row = pc / (kEpiDims / 8);
+          const size_t qn = static_cast<size_t>(min(q0 + row, N - 1));
+          gp[c - kP0][i] = *reinterpret_cast<const uint4*>(a.gate + b * a.g_bs + qn * a.g_rs + h * a.g_hs +
+                                                           kEpiDims * c + 8 * (pc % (kEpiDims / 8)));
+        }
+    }
+    if constexpr (G >= 0) {
+      constexpr int kHalf = kDT / 2;
+      constexpr int kT0 = G * kHalf, kO0 = (1 - G) * kHalf;   // own and partner's first output tile
+      lds_barrier();
+      float4* part = reinterpret_cast<float4*>(rw == 0 ? &ks0[0][0] : rw == 1 ? &ks1[0][0] : rw == 2 ? &vs0[0][0]
+                                                                                                   : &vs1[0][0]);
+      // slot g of the pair's buffer: the half that wave (rw, g) hands over
+#pragma unroll
+      for (int u = 0; u < kHalf; ++u)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          part[(4 * dt + j) * kWave + lane] = make_float4(o[dt][0][4 * j], o[dt][0][4 * j + 1], o[dt][0][4 * j + 2],
-                                                          o[dt][0][4 * j + 3]);
-      ml_part[0][rw][lane] = m_run[0];
-      ml_part[1][rw][lane] = l_run[0];
-    }
-    lds_barrier();
-    if (kgi == 1) return;
-    const float m1 = ml_part[0][rw][lane], l1 = ml_part[1][rw][lane];
-    const float mj = fmaxf(m_run[0], m1);
-    const float a0 = m_run[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[0] - mj);
-    const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mj);
-    l_run[0] = l_run[0] * a0 + l1 * a1;
+          part[((G * kHalf + u) * 4 + j) * kWave + lane] =
+              make_float4(o[kO0 + u][0][4 * j], o[kO0 + u][0][4 * j + 1], o[kO0 + u][0][4 * j + 2],
+                          o[kO0 + u][0][4 * j + 3]);
+      ml_part[0][rw + W * G][lane] = m_run[0];
+      ml_part[1][rw + W * G][lane] = l_run[0];
+      lds_barrier();
+      const float mo = ml_part[0][rw + W * (1 - G)][lane], lo = ml_part[1][rw + W * (1 - G)][lane];
+      const float mj = fmaxf(m_run[0], mo);
+      const float as = m_run[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[0] - mj);
+      const float ao = mo == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo - mj);
+      // group 0's term first
+      const float a0 = G == 0 ? as : ao, a1 = G == 0 ? ao : as;
+      const float l0 = G == 0 ? l_run[0] : lo, l1 = G == 0 ? lo : l_run[0];
+      l_run[0] = l0 * a0 + l1 * a1;
 #pragma unroll
-    for (int dt = 0; dt < kDT; ++dt)
+      for (int u = 0; u < kHalf; ++u)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float4 p1 = part[(4 * dt + j) * kWave + lane];
-        o[dt][0][4 * j] = o[dt][0][4 * j] * a0 + p1.x * a1;
-        o[dt][0][4 * j + 1] = o[dt][0][4 * j + 1] * a0 + p1.y * a1;
-        o[dt][0][4 * j + 2] = o[dt][0][4 * j + 2] * a0 + p1.z * a1;
-        o[dt][0][4 * j + 3] = o[dt][0][4 * j + 3] * a0 + p1.w * a1;
-      }
-  }
-
-  // epilogue: element e = 4j + r of o[dt][t] is value dim 32 dt + 8j + 4kg + r
-  // of query q0 + 32 t + n32
-#pragma unroll
-  for (int t = 0; t < QT; ++t) {
-    const float l_tot = l_run[t] + xor_lane<32>(l_run[t], lane);
-    const float inv = 1.0f / l_tot;
-    const int qn = q0 + 32 * t + n32;
-    if (qn >= N) continue;
-    uint16_t* orow = a.out + b * a.o_bs + static_cast<size_t>(qn) * a.o_rs + h * D;
-    const uint16_t* grow = GATE ? a.gate + b * a.g_bs + static_cast<size_t>(qn) * a.g_rs + h * a.g_hs : nullptr;
-#pragma unroll
-    for (int dt = 0; dt < kDT; ++dt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d0 = 32 * dt + 8 * j + 4 * kg;
-        float y[4];
-        if constexpr (GATE) {
-          // out = bf16(bf16(o / l) * bf16(sigmoid(gate)))
-          const uint2 gv = *reinterpret_cast<const uint2*>(grow + d0);
-          const float gx[4] = {lo_bf(gv.x), hi_bf(gv.x), lo_bf(gv.y), hi_bf(gv.y)};
+        for (int j = 0; j < 4; ++j) {
+          const float4 p = part[(((1 - G) * kHalf + u) * 4 + j) * kWave + lane];
+          const float pv[4] = {p.x, p.y, p.z, p.w};
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float sg = round_bf(__builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gx[r] * 1.4426950408889634f)));
-            y[r] = round_bf(round_bf(o[dt][t][4 * j + r] * inv) * sg);
+            const float own = o[kT0 + u][0][4 * j + r];
+            const float v0 = G == 0 ? own : pv[r], v1 = G == 0 ? pv[r] : own;
+            o[kT0 + u][0][4 * j + r] = v0 * a0 + v1 * a1;
           }
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) y[r] = round_bf(o[dt][t][4 * j + r] * inv);
         }
-        *reinterpret_cast<uint2*>(orow + d0) = make_uint2(pack_bf(y[0], y[1]), pack_bf(y[2], y[3]));
+      // every wave has read its partner's half: the pair's stage buffer holds
+      // the two waves' staging rows from here on
+      lds_barrier();
+      static_assert(2 * kWM * kEpiPitch * 2 <= kTK * kKPitch * 2, "two waves' staging rows fit a stage buffer");
+      eb = reinterpret_cast<uint16_t(*)[kEpiPitch]>(reinterpret_cast<char*>(part) + G * kWM * kEpiPitch * 2);
+    }
+    const float inv = 1.0f / (l_run[0] + xor_lane<32>(l_run[0], lane));
+#pragma unroll
+    for (int c = kP0; c < kP1; ++c) {
+#pragma unroll
+      for (int u = 0; u < kDTP; ++u) {
+        const int dt = kDTP * c + u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float y[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[r] = o[dt][0][4 * j + r] * inv;
+          *reinterpret_cast<uint2*>(&eb[n32][32 * u + 8 * j + 4 * kg]) =
+              make_uint2(pack_bf(y[0], y[1]), pack_bf(y[2], y[3]));
+        }
       }
+      wave_lds_sync();
+#pragma unroll
+      for (int i = 0; i < kPieces; ++i) {
+        const int pc = i * kWave + lane, row = pc / (kEpiDims / 8), ch = pc % (kEpiDims / 8);
+        const uint4 yv = *reinterpret_cast<const uint4*>(&eb[row][8 * ch]);
+        uint4 ov = yv;
+        if constexpr (GATE) {
+          float yf[8], gf[8];
+          unpack8(yv, yf);
+          unpack8(gp[c - kP0][i], gf);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float sg =
+                round_bf(__builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gf[e] * 1.4426950408889634f)));
+            yf[e] = round_bf(yf[e] * sg);
+          }
+          ov = pack8(yf);
+        }
+        const int qn = q0 + row;
+        if (qn < N)
+          *reinterpret_cast<uint4*>(a.out + b * a.o_bs + static_cast<size_t>(qn) * a.o_rs + h * D + kEpiDims * c +
+                                    8 * ch) = ov;
+      }
+      wave_lds_sync();   // this pass's reads are done before the next pass's writes
+    }
+  };
+  if constexpr (KG == 2) {
+    if (kgi == 0) finish(IC<0>{});
+    else finish(IC<1>{});
+  } else {
+    finish(IC<-1>{});
   }
 }
 
@@ -520,13 +594,13 @@ int tfa_prefill_attention(const void* q, int64_t q_rs, int64_t q_hs, const void*
   TFA_REQUIRE(kv_heads >= 1 && heads >= kv_heads && heads % kv_heads == 0 && heads <= 65535, TFA_ERR_SHAPE,
               "tfa_prefill_attention: heads %lld not a multiple of kv_heads %lld", (long long)heads, (long long)kv_heads);
   TFA_REQUIRE(q_rs % 8 == 0 && q_hs % 8 == 0 && k_rs % 8 == 0 && k_hs % 8 == 0 && v_rs % 8 == 0 &&
-                  v_hs % 8 == 0 && g_rs % 4 == 0 && g_hs % 4 == 0 && o_rs % 4 == 0,
-              TFA_ERR_ALIGN, "tfa_prefill_attention: row / head strides must keep 16-byte (q, k, v) and 8-byte (gate, out) alignment");
+                  v_hs % 8 == 0 && g_rs % 8 == 0 && g_hs % 8 == 0 && o_rs % 8 == 0,
+              TFA_ERR_ALIGN, "tfa_prefill_attention: row / head strides must keep 16-byte alignment");
   TFA_ALIGN16(q);
   TFA_ALIGN16(k);
   TFA_ALIGN16(v);
-  TFA_REQUIRE(aligned4(gate) && (reinterpret_cast<uintptr_t>(gate) & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0,
-              TFA_ERR_ALIGN, "tfa_prefill_attention: gate / out must be 8-byte aligned");
+  TFA_ALIGN16(gate);
+  TFA_ALIGN16(out);
   FlashArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
@@ -567,12 +641,12 @@ int tfa_causal_attention(const void* q, int64_t q_rs, int64_t q_hs, int64_t q_bs
                   q_bs >= 0 && k_bs >= 0 && v_bs >= 0 && o_bs >= 0,
               TFA_ERR_SHAPE, "tfa_causal_attention: strides must be non-negative, row / head strides below 2^31");
   TFA_REQUIRE(q_rs % 8 == 0 && q_hs % 8 == 0 && q_bs % 8 == 0 && k_rs % 8 == 0 && k_hs % 8 == 0 && k_bs % 8 == 0 &&
-                  v_rs % 8 == 0 && v_hs % 8 == 0 && v_bs % 8 == 0 && o_rs % 4 == 0 && o_bs % 4 == 0,
-              TFA_ERR_ALIGN, "tfa_causal_attention: strides must keep 16-byte (q, k, v) and 8-byte (out) alignment");
+                  v_rs % 8 == 0 && v_hs % 8 == 0 && v_bs % 8 == 0 && o_rs % 8 == 0 && o_bs % 8 == 0,
+              TFA_ERR_ALIGN, "tfa_causal_attention: strides must keep 16-byte alignment");
   TFA_ALIGN16(q);
   TFA_ALIGN16(k);
   TFA_ALIGN16(v);
-  TFA_REQUIRE((reinterpret_cast<uintptr_t>(out) & 7) == 0, TFA_ERR_ALIGN, "tfa_causal_attention: out must be 8-byte aligned");
+  TFA_ALIGN16(out);
   FlashArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
