@@ -397,6 +397,18 @@ int tfa_mla_q_absorb(const float* q_part, int64_t ks, int64_t batch, int64_t hea
                      const void* cos_t, const void* sin_t, int64_t rope_rows, const int* pos, void* q_abs,
                      int* err, hipStream_t stream);
 
+/* The q_b projection and the absorbed query in one launch: q_up[b] =
+ * bf16(q_n[b] . W_q_b^T) (f32 accumulate) for q_n [batch, q_lora] bf16 and
+ * w_q_b [heads*96, q_lora] (out, in), then q_abs as tfa_mla_q_absorb writes it
+ * from q_up. q_lora = 768, batch <= 32, heads <= 48; q_n, w_q_b and w_kv_b
+ * 16-byte aligned. A position outside the rope table sets *err = 6 (row 0 used).
+ * Replaces (absorbed form): examples/minicpm3_4b-cutedsl/model.py:232-236 (q_up =
+ * q_n . w_q_b, split into nope | rope) with the q half of kernels/cute_gemv.py:291-347
+ * and the q rotation of kernels/reference_ops.py:99-107. */
+int tfa_mla_qb_absorb(const void* q_n, int64_t batch, int64_t heads, int64_t q_lora, const void* w_q_b,
+                      const void* w_kv_b, const void* cos_t, const void* sin_t, int64_t rope_rows, const int* pos,
+                      void* q_abs, int* err, hipStream_t stream);
+
 /* Split attention of q_abs [batch, heads, 288] bf16 over slots 0..wr[b] of the
  * compressed cache on bf16 MFMA: s = scale * (q_abs . [latent | rope]) in f32,
  * per split (split positions: 32, 64, 96 or a multiple of 128 up to 1024) the softmax in

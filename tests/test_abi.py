@@ -247,6 +247,22 @@ def test_mla_prep_q_gemv_argument_checks(lib):
     assert st == ALIGN
 
 
+def test_mla_qb_absorb_argument_checks(lib):
+    # q_lora other than 768, a batch past 32, heads past 48, a null weight, a misaligned q_n
+    args = lambda qa=768, b=8, h=40, wq=A, qn=A: (qn, I64(b), I64(h), I64(qa), wq, A, A, A, I64(64), A, A,
+                                                  P(None), P(None))
+    st, msg = call(lib, "tfa_mla_qb_absorb", *args(qa=512))
+    assert st == SHAPE and "768" in msg
+    st, _ = call(lib, "tfa_mla_qb_absorb", *args(b=33))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_mla_qb_absorb", *args(h=49))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_mla_qb_absorb", *args(wq=P(None)))
+    assert st == NULL
+    st, _ = call(lib, "tfa_mla_qb_absorb", *args(qn=MIS))
+    assert st == ALIGN
+
+
 def test_torch_extension_rejects_host_tensors():
     from tilefoundry_amd import ops
 

@@ -146,6 +146,80 @@ def test_mla_q_absorb(dev):
         assert_equal(f"q_rope b={b}", q_abs[b, :, KV:], ref[:, KV:])
 
 
+def _qb_absorb(dev, q_n, w, pos, cos, sin, err=None):
+    from tilefoundry_amd._lib import C
+
+    q_abs = torch.full((q_n.shape[0], H, KV + R), float("nan"), dtype=BF, device=dev)
+    C.mla_qb_absorb(q_n.to(dev), w.w_q_b.to(dev), w.w_kv_b.to(dev), cos.to(dev), sin.to(dev),
+                    torch.tensor(pos, dtype=torch.int32, device=dev), q_abs, err)
+    return q_abs.cpu()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B", [1, 8, 13, 32])
+def test_mla_qb_absorb_vs_oracle(dev, B):
+    """The q_b projection and absorption in one launch against the oracle's
+    q_up = bf16(q_n . W_q_b^T) and absorb_query, at batch 1 / 8 / 13 (a partial
+    16-sequence tile) / 32 (two tiles). The projection's f32 sum runs in another
+    order than torch's, so a q_up value whose exact sum lies within the f32
+    error (8 u sum|p|, u = 2^-24) of a bf16 rounding boundary may land one ulp
+    apart. Those values are found from the f64 sum; each output may differ from
+    the oracle's by what they carry (one ulp of each times |W_UK| for q_lat,
+    two ulps of a rotated pair for q_rope) plus two ulps of its own landing,
+    and a rotated value whose inputs carry nothing must be equal."""
+    g = gen(40 + B)
+    w = oracle_weights()
+    q_n = torch.randn(B, QA, generator=g).to(BF)
+    cos, sin = OM.rope_tables(512, CFG)
+    pos = [(37 * b + 5 * B) % 512 for b in range(B)]
+    pos[-1] = 511
+    got = _qb_absorb(dev, q_n, w, pos, cos, sin)
+    q_up = OM.proj(q_n, w.w_q_b).view(B, H, -1)
+    ref = torch.stack([OM.absorb_query(q_up[b], w, CFG, p, cos, sin) for b, p in enumerate(pos)])
+    # q_up values whose landing the summation order can change
+    exact = (q_n.double() @ w.w_q_b.double().t()).view(B, H, -1)
+    slack = 8 * 2.0 ** -24 * (q_n.double().abs() @ w.w_q_b.double().abs().t()).view(B, H, -1)   # f32 sums: <= 1.3x
+    amb = ((exact - slack).to(BF) != (exact + slack).to(BF)).double()
+    ulp = lambda x: torch.exp2(torch.floor(torch.log2(x.double().abs().clamp_min(1e-30))) - 7)
+    q_ulp = amb * ulp(q_up)
+    carry = torch.einsum("bhi,hic->bhc", q_ulp[..., :CFG.nope], w.w_uk(CFG).double().abs())
+    err = (got[..., :KV].double() - ref[..., :KV].double()).abs()
+    allowed = 2 * ulp(ref[..., :KV]) + 1.01 * carry
+    assert bool((err <= allowed).all()), f"q_lat: {int((err > allowed).sum())} elements past the bound"
+    assert float((err > 0).double().mean()) <= 0.03
+    half = CFG.rope // 2
+    r_amb = q_ulp[..., CFG.nope:] > 0
+    r_amb = r_amb | torch.cat((r_amb[..., half:], r_amb[..., :half]), -1)
+    d = bf16_ulps(got[..., KV:], ref[..., KV:])
+    assert not bool((d[~r_amb] > 0).any()), "q_rope differs where its inputs land unambiguously"
+    assert int(d.max()) <= 2
+
+
+@pytest.mark.gpu
+def test_mla_qb_absorb_exact(dev):
+    """Inputs on a grid where every sum is exact in f32 (q_n in {-2..2}, weights
+    in {-2..2} / 16): any summation order gives the same f32 values, so the
+    projection, its landing, the absorption and the rotation must match the
+    oracle bit for bit; and a position past the rope table sets err = 6."""
+    g = gen(77)
+    B = 11
+    w = oracle_weights()
+    grid = lambda *s: (torch.randint(-2, 3, s, generator=g).float() / 16).to(BF)
+    w.w_q_b, w.w_kv_b = grid(*w.w_q_b.shape), grid(*w.w_kv_b.shape)
+    q_n = torch.randint(-2, 3, (B, QA), generator=g).float().to(BF)
+    cos, sin = OM.rope_tables(256, CFG)
+    pos = list(range(0, 23 * B, 23))
+    got = _qb_absorb(dev, q_n, w, pos, cos, sin)
+    q_up = OM.proj(q_n, w.w_q_b).view(B, H, -1)
+    for b, p in enumerate(pos):
+        assert_equal(f"q_abs b={b}", got[b], OM.absorb_query(q_up[b], w, CFG, p, cos, sin))
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    got = _qb_absorb(dev, q_n[:2], w, [3, 256], cos, sin, err)
+    assert int(err.item()) == 6
+    assert_equal("q_abs, good position", got[0], OM.absorb_query(q_up[0], w, CFG, 3, cos, sin))
+    assert bool(torch.isfinite(got[1].float()).all())
+
+
 def _attend(dev, q_abs, lat, rk, pos, split, w_kv_b, cap):
     from tilefoundry_amd._lib import C
 

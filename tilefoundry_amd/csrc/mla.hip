@@ -68,6 +68,17 @@ TFA_DEV float rope_bf(float x, float partner, float c, float s) {
   return round_bf(round_bf(x * c) + round_bf(partner * s));
 }
 
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4
+// of the 8-byte reads of lanes 4j + i / 4 (j = 0..3). Lane L reading row
+// base + L / 4 at column col0 + 4 (L % 4) therefore receives
+// C[base + j][col0 + i], j = 0..3 -- four consecutive rows of one column, the
+// MFMA's K-major operand.
+TFA_DEV uint2 ld_tr(const char* lds_byte) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(lds_byte));
+  return __builtin_bit_cast(uint2, v);
+}
+
 // ------------------------------------------------------------------ mla_prep
 // One block per sequence. part: [ks, B, qa + 256 + 32] f32 split-K partials of
 // x_n . [W_q_a; W_kv_a]^T; KS = ks, so that exactly the live partials are loaded.
@@ -325,6 +336,198 @@ __global__ __launch_bounds__(kThreads) void mla_q_absorb_kernel(
   }
 }
 
+// ------------------------------------------------------------- mla_qb_absorb
+// The q_b projection and the query absorption in one launch, two blocks per
+// head (grid [H, 2]), both products on bf16 MFMA with f32 accumulation. Block
+// (h, 0) projects the head's 64 nope rows of W_q_b, q_nope[b][i] =
+// bf16(q_n[b] . W_q_b[96h + i]), and absorbs them, q_abs[b, h, c] =
+// bf16(sum_i q_nope[b][i] W_UK_h[i][c]); block (h, 1) projects the 32 rope
+// rows, lands them and rotates them at pos[b]. Every operand goes to LDS by
+// DMA, all issued before any is read: the q_n rows, the block's weight rows
+// (contiguous in W_q_b: 64 or 32 rows of 1536 bytes), then W_UK (64 rows of 512
+// bytes). 16-byte piece s of a q_n or W_q_b row r sits at piece s ^ (r % 16) of
+// its row, so an operand read (16 rows at one piece) is free of bank
+// conflicts; the 32-byte chunks of W_UK row r are XOR-swizzled by
+// (r % 4) + 4 ((r / 8) % 2), so the transpose reads of its operand (4 rows x
+// 32 bytes per 16 lanes, row groups 8 apart) are too. Projection: wave w owns
+// weight rows 16w .. 16w + 15 against every sequence, k-steps dealt over four
+// accumulators; absorption: wave w owns latent columns 64w .. 64w + 63. NT:
+// 16-sequence tiles (batch <= 16 NT); at NT = 2 the q_n rows take the LDS that
+// W_UK has at NT = 1, so W_UK is loaded over the weight rows once the
+// projection has read them.
+constexpr int kQLora = 768;             // q_lora_rank: the K of the q_b projection
+constexpr int kQbPieces = kQLora / 8;   // 16-byte pieces of a row
+constexpr int kQnPitch = kNope + 8;     // landed q_nope row pitch, bf16 (144 bytes)
+TFA_DEV int uk_slot(int row, int piece) { return piece ^ (2 * ((row & 3) | (((row >> 3) & 1) << 2))); }
+template <int NT>
+__global__ __launch_bounds__(kThreads) void mla_qb_absorb_kernel(
+    const uint16_t* __restrict__ q_n, int B, int H, const uint16_t* __restrict__ w_q_b,
+    const uint16_t* __restrict__ w_kv_b, const uint16_t* __restrict__ cos_t, const uint16_t* __restrict__ sin_t,
+    int rope_rows, const int* __restrict__ pos, uint16_t* __restrict__ q_abs, int* err) {
+  constexpr int kQH = kNope + kRope;
+  constexpr int kXDma = 16 * NT * kQbPieces / kThreads;   // q_n DMAs per thread
+  constexpr int kUkDma = kNope * kLat / 8 / kThreads;     // W_UK DMAs per thread
+  constexpr bool kUkEarly = NT == 1;                      // W_UK has LDS of its own
+  constexpr int kRopePer = 16 * NT * kRope / kThreads;
+  constexpr int kSteps = kQLora / 32;                     // projection k-steps
+  constexpr int kBatch = 12;                              // k-steps whose operands are read at once
+  static_assert(16 * NT * kQbPieces % kThreads == 0 && kRope * kQbPieces % kThreads == 0 &&
+                    kNope * kLat / 8 % kThreads == 0 && kSteps % kBatch == 0, "loads split evenly");
+  static_assert(kWaves * 16 == kNope && kWaves * 64 == kLat, "one wave per 16 nope rows and 64 latent columns");
+  __shared__ uint4 wl[kNope * kQbPieces];                 // W_q_b rows (at NT = 2 then W_UK)
+  __shared__ uint4 xl[16 * NT * kQbPieces];               // q_n rows; after the projection the landed values
+  __shared__ uint4 ukl[kUkEarly ? kNope * kLat / 8 : 1];  // W_UK rows (NT = 1)
+  static_assert(sizeof(xl) >= 16 * NT * kQnPitch * 2 && sizeof(xl) >= 16 * NT * kRope * 4, "the LDS reuse fits");
+  uint16_t(*qnb)[kQnPitch] = reinterpret_cast<uint16_t(*)[kQnPitch]>(xl);   // landed q_nope
+  float(*qv)[kRope] = reinterpret_cast<float(*)[kRope]>(xl);                // landed q_rope
+  const int h = blockIdx.x;
+  const int part = blockIdx.y;   // 0: nope rows + absorption, 1: rope rows + rotation
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int n16 = lane & 15;
+  const int g = lane >> 4;
+
+  // 1. every load: the rope table rows (part 1, in registers), then by DMA the
+  //    q_n rows (rows past the batch re-read the last row), the weight rows and
+  //    (part 0, NT = 1) W_UK
+  uint32_t csr[kRopePer], snr[kRopePer];
+  if (part == 1) {
+#pragma unroll
+    for (int j = 0; j < kRopePer; ++j) {
+      const int e = t + kThreads * j;
+      int p = pos[min(e / kRope, B - 1)];
+      if (e < B * kRope && (p < 0 || p >= rope_rows) && h == 0) set_err(err, 6);
+      p = p < 0 || p >= rope_rows ? 0 : p;
+      csr[j] = cos_t[static_cast<size_t>(p) * kRope + e % kRope];
+      snr[j] = sin_t[static_cast<size_t>(p) * kRope + e % kRope];
+    }
+  }
+  const uint32_t xl0 = lds_offset(xl), wl0 = lds_offset(wl);
+#pragma unroll
+  for (int i = 0; i < kXDma; ++i) {
+    const int q = kThreads * i + t, r = q / kQbPieces, s = q % kQbPieces;
+    lds_dma16(q_n + static_cast<size_t>(min(r, B - 1)) * kQLora + 8 * (s ^ (r & 15)),
+              xl0 + (kThreads * i + kWave * w) * 16);
+  }
+  const int ntile = part == 0 ? kNope / 16 : kRope / 16;
+  const uint16_t* wsrc = w_q_b + (static_cast<size_t>(h) * kQH + part * kNope) * kQLora;
+  for (int i = 0; i < ntile * 16 * kQbPieces / kThreads; ++i) {
+    const int q = kThreads * i + t, r = q / kQbPieces, s = q % kQbPieces;
+    lds_dma16_stream(wsrc + static_cast<size_t>(r) * kQLora + 8 * (s ^ (r & 15)), wl0 + (kThreads * i + kWave * w) * 16);
+  }
+  const uint16_t* uk_src = w_kv_b + static_cast<size_t>(h) * kKvB * kLat;
+  auto issue_uk = [&](uint32_t dst0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kUkDma; ++i) {
+      const int q = kThreads * i + t, r = q / (kLat / 8);
+      lds_dma16_stream(uk_src + static_cast<size_t>(r) * kLat + 8 * uk_slot(r, q % (kLat / 8)),
+                       dst0 + (kThreads * i + kWave * w) * 16);
+    }
+  };
+  if (kUkEarly && part == 0) {
+    issue_uk(lds_offset(ukl));
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kUkDma));   // q_n and the weight rows landed
+  } else {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  }
+  lds_barrier();
+
+  // 2. the projection: C[sequence 16nt + 4g + r][row 16w + n16]; k-step ks
+  //    reads piece 4ks + g of both operands
+  f32x4 c[NT];
+  if (w < ntile) {
+    f32x4 acc[4][NT];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[a][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint4* wrow = wl + (16 * w + n16) * kQbPieces;
+#pragma unroll
+    for (int k0 = 0; k0 < kSteps; k0 += kBatch) {
+      uint4 bw[kBatch], ax[kBatch][NT];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int p = (4 * (k0 + j) + g) ^ n16;
+        bw[j] = wrow[p];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) ax[j][nt] = xl[(16 * nt + n16) * kQbPieces + p];
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          acc[j & 3][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(ax[j][nt]), as_bf8(bw[j]), acc[j & 3][nt],
+                                                                   0, 0, 0);
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) c[nt] = (acc[0][nt] + acc[1][nt]) + (acc[2][nt] + acc[3][nt]);
+  }
+  lds_barrier();   // both operands consumed: their LDS is reused below
+  if (w < ntile) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * nt + 4 * g + r, col = 16 * w + n16;
+        if (part == 0) qnb[row][col] = static_cast<uint16_t>(f2bf(c[nt][r]));
+        else qv[row][col] = round_bf(c[nt][r]);
+      }
+  }
+  if (!kUkEarly && part == 0) {
+    issue_uk(wl0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  } else if (part == 0) {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  }
+  lds_barrier();
+
+  if (part == 1) {
+    // 3b. q_rope rotated at the sequence's position
+#pragma unroll
+    for (int j = 0; j < kRopePer; ++j) {
+      const int e = t + kThreads * j;
+      if (e >= B * kRope) continue;
+      const int b = e / kRope, d = e % kRope;
+      const float partner = d < kRope / 2 ? -qv[b][d + kRope / 2] : qv[b][d - kRope / 2];
+      q_abs[(static_cast<size_t>(b) * H + h) * kQK + kLat + d] =
+          static_cast<uint16_t>(f2bf(rope_bf(qv[b][d], partner, bf2f(csr[j]), bf2f(snr[j]))));
+    }
+    return;
+  }
+  // 3a. q_abs[b, h, c] = bf16(sum_i q_nope[b][i] W_UK[i][c]): A = q_nope rows
+  //     16bt + n16 (k = 32ks + 8g ..), B = W_UK by transpose reads of rows
+  //     32ks + 8g + n16 / 4 (+ 4) at column col + 4 (n16 % 4)
+  const char* uk = kUkEarly ? reinterpret_cast<const char*>(ukl) : reinterpret_cast<const char*>(wl);
+  const char* qb = reinterpret_cast<const char*>(qnb);
+#pragma unroll
+  for (int bt = 0; bt < NT; ++bt) {
+    uint4 aq[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      aq[ks] = *reinterpret_cast<const uint4*>(qb + (16 * bt + n16) * kQnPitch * 2 + (32 * ks + 8 * g) * 2);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int col = 64 * w + 16 * nt;
+      const int cb = col + 4 * (n16 & 3);
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int r1 = 32 * ks + 8 * g + (n16 >> 2), r2 = r1 + 4;
+        const uint2 v1 = ld_tr(uk + r1 * kLat * 2 + uk_slot(r1, cb / 8) * 16 + (cb % 8) * 2);
+        const uint2 v2 = ld_tr(uk + r2 * kLat * 2 + uk_slot(r2, cb / 8) * 16 + (cb % 8) * 2);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(aq[ks]), as_bf8(make_uint4(v1.x, v1.y, v2.x, v2.y)),
+                                                      acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int b = 16 * bt + 4 * g + r;
+        if (b < B) q_abs[(static_cast<size_t>(b) * H + h) * kQK + col + n16] = static_cast<uint16_t>(f2bf(acc[r]));
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ mla_attn
 struct MlaAttnArgs {
   const uint16_t* q;     // [B, H, 288]: q_lat | rotated q_rope
@@ -365,17 +568,6 @@ constexpr int kWaitVm0 = waitcnt_vm(0);
 // distinct bank groups. The maps are involutions: slot <-> chunk.
 TFA_DEV int lat_slot(int row, int chunk) { return chunk ^ (((row & 7) << 1) | ((row >> 3) & 1)); }
 TFA_DEV int rope_slot(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
-
-// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4
-// of the 8-byte reads of lanes 4j + i / 4 (j = 0..3). Lane L reading row
-// base + L / 4 at column col0 + 4 (L % 4) therefore receives
-// C[base + j][col0 + i], j = 0..3 -- four consecutive positions of one latent
-// column, the MFMA's K-major operand.
-TFA_DEV uint2 ld_tr(const char* lds_byte) {
-  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4*)(lds_byte));
-  return __builtin_bit_cast(uint2, v);
-}
 
 // Scores are computed transposed, S^T = [c | k_rope] . q^T (positions as MFMA
 // rows, heads as columns): the accumulator of lane (head n16, row group g)
@@ -1311,6 +1503,39 @@ int tfa_mla_q_absorb(const float* q_part, int64_t ks, int64_t batch, int64_t hea
         static_cast<const uint16_t*>(cos_t), static_cast<const uint16_t*>(sin_t), (int)rope_rows, pos,
         static_cast<uint16_t*>(q_abs), err);
   return launched("mla_q_absorb");
+}
+
+int tfa_mla_qb_absorb(const void* q_n, int64_t batch, int64_t heads, int64_t q_lora, const void* w_q_b,
+                      const void* w_kv_b, const void* cos_t, const void* sin_t, int64_t rope_rows, const int* pos,
+                      void* q_abs, int* err, hipStream_t stream) {
+  TFA_NONNULL(q_n);
+  TFA_NONNULL(w_q_b);
+  TFA_NONNULL(w_kv_b);
+  TFA_NONNULL(cos_t);
+  TFA_NONNULL(sin_t);
+  TFA_NONNULL(pos);
+  TFA_NONNULL(q_abs);
+  TFA_REQUIRE(batch >= 1 && batch <= kMaxBatch, TFA_ERR_SHAPE, "tfa_mla_qb_absorb: batch %lld not in [1, %d]",
+              (long long)batch, kMaxBatch);
+  TFA_REQUIRE(heads >= 1 && heads <= kHeadRows, TFA_ERR_SHAPE, "tfa_mla_qb_absorb: heads %lld not in [1, %d]",
+              (long long)heads, kHeadRows);
+  TFA_REQUIRE(q_lora == kQLora && rope_rows >= 1, TFA_ERR_SHAPE,
+              "tfa_mla_qb_absorb: q_lora %lld (built for %d) or empty rope table", (long long)q_lora, kQLora);
+  TFA_ALIGN16(q_n);
+  TFA_ALIGN16(w_q_b);
+  TFA_ALIGN16(w_kv_b);
+  const dim3 grid((unsigned)heads, 2);
+  if (batch <= 16)
+    mla_qb_absorb_kernel<1><<<grid, kThreads, 0, stream>>>(
+        static_cast<const uint16_t*>(q_n), (int)batch, (int)heads, static_cast<const uint16_t*>(w_q_b),
+        static_cast<const uint16_t*>(w_kv_b), static_cast<const uint16_t*>(cos_t),
+        static_cast<const uint16_t*>(sin_t), (int)rope_rows, pos, static_cast<uint16_t*>(q_abs), err);
+  else
+    mla_qb_absorb_kernel<2><<<grid, kThreads, 0, stream>>>(
+        static_cast<const uint16_t*>(q_n), (int)batch, (int)heads, static_cast<const uint16_t*>(w_q_b),
+        static_cast<const uint16_t*>(w_kv_b), static_cast<const uint16_t*>(cos_t),
+        static_cast<const uint16_t*>(sin_t), (int)rope_rows, pos, static_cast<uint16_t*>(q_abs), err);
+  return launched("mla_qb_absorb");
 }
 
 int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* rope_cache, const int* wr,

@@ -522,6 +522,28 @@ void mla_q_absorb(const Tensor& q_part, const Tensor& w_kv_b, const Tensor& cos,
                                 pos.data_ptr<int>(), q_abs.data_ptr(), opt_ptr_t<int>(err), stream_of(pos)));
 }
 
+// q_n [B, 768] bf16, w_q_b [H*96, 768], w_kv_b [H*128, 256], q_abs [B, H, 288] bf16.
+void mla_qb_absorb(const Tensor& q_n, const Tensor& w_q_b, const Tensor& w_kv_b, const Tensor& cos,
+                   const Tensor& sin, const Tensor& pos, const Tensor& q_abs, const OptT& err) {
+  need(pos, "pos", I32);
+  const int64_t B = pos.numel();
+  need(q_abs, "q_abs", BF);
+  if (q_abs.dim() != 3 || q_abs.size(0) != B || q_abs.size(2) != 288) bad("q_abs: expected (batch, heads, 288)");
+  const int64_t H = q_abs.size(1);
+  need(q_n, "q_n", BF);
+  if (q_n.dim() != 2 || q_n.size(0) != B) bad("q_n: expected (batch, q_lora)");
+  const int64_t QL = q_n.size(1);
+  need_mat(w_q_b, "w_q_b", H * 96, QL);
+  need_mat(w_kv_b, "w_kv_b", H * 128, 256);
+  need(cos, "cos", BF);
+  need(sin, "sin", BF, cos.numel());
+  if (cos.numel() % 32 != 0) bad("cos: expected (rows, 32)");
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_mla_qb_absorb(q_n.data_ptr(), B, H, QL, w_q_b.data_ptr(), w_kv_b.data_ptr(), cos.data_ptr(),
+                                 sin.data_ptr(), cos.numel() / 32, pos.data_ptr<int>(), q_abs.data_ptr(),
+                                 opt_ptr_t<int>(err), stream_of(pos)));
+}
+
 // op [B, ns, H, 256] bf16, mp / lp [B, ns, H] f32.
 void mla_attention(const Tensor& q_abs, const Tensor& latent, const Tensor& rope, const Tensor& wr,
                    int64_t split, double scale, const Tensor& op, const Tensor& mp, const Tensor& lp,
@@ -949,6 +971,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("mla_prep", &mla_prep);
   m.def("mla_prep_q_gemv", &mla_prep_q_gemv);
   m.def("mla_q_absorb", &mla_q_absorb);
+  m.def("mla_qb_absorb", &mla_qb_absorb);
   m.def("mla_attention", &mla_attention);
   m.def("mla_combine_up", &mla_combine_up);
   m.def("rows_residual", &rows_residual);

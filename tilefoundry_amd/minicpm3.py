@@ -9,13 +9,13 @@ the value up-projection, o_proj and MiniCPM3's ``scale_depth`` residual --
 cache holding the 288-wide compressed entry per position (latent c | rotated
 rope key) instead of 40 assembled keys and values.
 
-Launch sequence of one step (9 kernels, capturable as one graph):
+Launch sequence of one step (8 kernels, capturable as one graph):
 
     rms_norm         input norm (eps 1e-5)                       [B, 2560]
     skinny_gemm      x_n . [W_q_a; W_kv_a]^T -> split-K partials   [ks, B, 1056]
     mla_prep         q_a / kv_c LoRA norms, latent + rope cache append at pos
-    skinny_gemm      q_n . W_q_b^T -> split-K partials             [ks, B, 3840]
-    mla_q_absorb     q_lat = bf16(W_UK^T q_nope), rotated q_rope   [B, 40, 288]
+    mla_qb_absorb    q_up = bf16(q_n . W_q_b^T) per head on MFMA, then
+                     q_lat = bf16(W_UK^T q_nope), rotated q_rope   [B, 40, 288]
     mla_attention    split attention over the compressed cache (bf16 MFMA)
     mla_combine_up   split merge, bf16(W_UV o_lat)                  [B, 2560]
     skinny_gemm      attn . W_o^T -> split-K partials              [ks, B, 2560]
@@ -139,7 +139,7 @@ class MLABlock:
 
     def __init__(self, cfg: MiniCPM3Config = MINICPM3_4B, *, batch: int = 8, cap: int = 8192,
                  device="cuda:0", weights: dict | None = None, seed: int = 0, split: int = 256,
-                 ks_a: int = 5, ks_qb: int = 3, ks_o: int = 5):
+                 ks_a: int = 5, ks_qb: int = 3, ks_o: int = 5, fuse_qb: bool = True):
         if cfg.kv_lora != 256 or cfg.rope != 32 or cfg.nope != 64 or cfg.v_dim != 64:
             raise ValueError("the MLA kernels are built for kv_lora 256, rope 32, nope 64, value 64")
         if cap % split:
@@ -147,6 +147,7 @@ class MLABlock:
         self.cfg, self.batch, self.cap, self.split = cfg, batch, cap, split
         self.device = torch.device(device)
         self.ks = {"a": ks_a, "qb": ks_qb, "o": ks_o}
+        self.fuse_qb = fuse_qb   # q_b projection + absorption in one launch (else split-K q_b, then absorb)
         w = synthetic_weights(cfg, seed, self.device) if weights is None else {
             k: v.to(self.device) for k, v in weights.items()}
         self.w = w
@@ -185,8 +186,11 @@ class MLABlock:
         C.skinny_gemm(self.xn, self.w_a, self.ks["a"], 0, self.part_a, None, None, None, None)
         C.mla_prep(self.part_a, w["gamma_q_a"], w["gamma_kv_a"], cfg.lora_eps, self.cos, self.sin,
                    self.pos, self.latent, self.rope_k, self.q_n, self.err)
-        C.skinny_gemm(self.q_n, w["w_q_b"], self.ks["qb"], 0, self.part_qb, None, None, None, None)
-        C.mla_q_absorb(self.part_qb, w["w_kv_b"], self.cos, self.sin, self.pos, self.q_abs, self.err)
+        if self.fuse_qb:
+            C.mla_qb_absorb(self.q_n, w["w_q_b"], w["w_kv_b"], self.cos, self.sin, self.pos, self.q_abs, self.err)
+        else:
+            C.skinny_gemm(self.q_n, w["w_q_b"], self.ks["qb"], 0, self.part_qb, None, None, None, None)
+            C.mla_q_absorb(self.part_qb, w["w_kv_b"], self.cos, self.sin, self.pos, self.q_abs, self.err)
         C.mla_attention(self.q_abs, self.latent, self.rope_k, self.pos, self.split, cfg.scale,
                         self.op, self.mp, self.lp, self.err)
         C.mla_combine_up(self.op, self.mp, self.lp, self.pos, self.split, w["w_kv_b"], self.attn)
@@ -294,12 +298,12 @@ class MiniCPM3Engine:
     captured step over all of them (examples/minicpm3_4b-cutedsl/model.py:320-420,
     runtime twin runtime_model.py; run.py drives it token by token).
 
-    One step (batch > 1), 11 launches per layer plus 5 -- at one sequence the
+    One step (batch > 1), 10 launches per layer plus 5 -- at one sequence the
     projections run on the bs=1 GEMVs instead, 8 launches per layer (``_step_one``):
 
         embed            bf16(table[id] * scale_emb), then the first input norm
         -- per layer: the MLA attention block of ``MLABlock`` ----------------
-        skinny_gemm [q_a | kv_a], mla_prep, skinny_gemm q_b, mla_q_absorb,
+        skinny_gemm [q_a | kv_a], mla_prep, mla_qb_absorb (q_b + absorption),
         mla_attention, mla_combine_up, skinny_gemm o_proj,
         rows_norm_scaled h1 = h + bf16(bf16(o) * a), a = scale_depth / sqrt(layers),
                          and the post-attention norm of h1
@@ -463,8 +467,7 @@ class MiniCPM3Engine:
             C.skinny_gemm(self.xn, w["w_a"], ks["a"], 0, self.part_a, None, None, None, None)
             C.mla_prep(self.part_a, w["gamma_q_a"], w["gamma_kv_a"], cfg.lora_eps, self.cos, self.sin,
                        self.pos, lat, rk, self.q_n, self.err)
-            C.skinny_gemm(self.q_n, w["w_q_b"], ks["qb"], 0, self.part_qb, None, None, None, None)
-            C.mla_q_absorb(self.part_qb, w["w_kv_b"], self.cos, self.sin, self.pos, self.q_abs, self.err)
+            C.mla_qb_absorb(self.q_n, w["w_q_b"], w["w_kv_b"], self.cos, self.sin, self.pos, self.q_abs, self.err)
             C.mla_attention(self.q_abs, lat, rk, self.pos, self.split, cfg.scale, self.op, self.mp,
                             self.lp, self.err)
             C.mla_combine_up(self.op, self.mp, self.lp, self.pos, self.split, w["w_kv_b"], self.attn)
