@@ -409,6 +409,22 @@ int tfa_mla_qb_absorb(const void* q_n, int64_t batch, int64_t heads, int64_t q_l
                       const void* w_kv_b, const void* cos_t, const void* sin_t, int64_t rope_rows, const int* pos,
                       void* q_abs, int* err, hipStream_t stream);
 
+/* One sequence's MLA prep, q_b projection and absorbed query in one launch:
+ * from part = [q_a (768) | kv_c (256) | k_rope (32)] f32 (the single split-K
+ * partial tfa_rmsnorm_gemv_f32 leaves), q_n = LoRA norm of q_a with gamma_q_a
+ * (bit-equal to tfa_mla_prep's), latent_cache[pos[0]] and rope_cache[pos[0]]
+ * written as tfa_mla_prep writes them (a pos outside [0, cap) or the rope table
+ * sets *err = 6 and skips them), and q_abs [1, heads, 288] as tfa_mla_qb_absorb
+ * computes it from q_n. q_lora = 768, heads <= 48; part, gamma_q_a, w_q_b and
+ * w_kv_b 16-byte aligned.
+ * Replaces: examples/minicpm3_4b-cutedsl/model.py:220-251 (steps 1-4 of
+ * mla_attention at one sequence) with kernels/cute_gemv.py:246-347 (NORM_GEMV,
+ * NORM_GEMV_PAIR) and the q rotation of kernels/reference_ops.py:99-107. */
+int tfa_mla_prep_qb_absorb(const float* part, int64_t q_lora, const void* gamma_q_a, const void* gamma_kv_a,
+                           float eps, const void* cos_t, const void* sin_t, int64_t rope_rows, const int* pos,
+                           void* latent_cache, void* rope_cache, int64_t cap, const void* w_q_b, const void* w_kv_b,
+                           int64_t heads, void* q_abs, int* err, hipStream_t stream);
+
 /* Split attention of q_abs [batch, heads, 288] bf16 over slots 0..wr[b] of the
  * compressed cache on bf16 MFMA: s = scale * (q_abs . [latent | rope]) in f32,
  * per split (split positions: 32, 64, 96 or a multiple of 128 up to 1024) the softmax in

@@ -263,6 +263,22 @@ def test_mla_qb_absorb_argument_checks(lib):
     assert st == ALIGN
 
 
+def test_mla_prep_qb_absorb_argument_checks(lib):
+    # q_lora other than 768, heads past 48, an empty cache, a null cache, a misaligned partial
+    args = lambda qa=768, h=40, cap=64, part=A, lat=A: (part, I64(qa), A, A, F(1e-6), A, A, I64(64), A, lat, A,
+                                                        I64(cap), A, A, I64(h), A, P(None), P(None))
+    st, msg = call(lib, "tfa_mla_prep_qb_absorb", *args(qa=1024))
+    assert st == SHAPE and "768" in msg
+    st, _ = call(lib, "tfa_mla_prep_qb_absorb", *args(h=49))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_mla_prep_qb_absorb", *args(cap=0))
+    assert st == SHAPE
+    st, _ = call(lib, "tfa_mla_prep_qb_absorb", *args(lat=P(None)))
+    assert st == NULL
+    st, _ = call(lib, "tfa_mla_prep_qb_absorb", *args(part=MIS))
+    assert st == ALIGN
+
+
 def test_torch_extension_rejects_host_tensors():
     from tilefoundry_amd import ops
 

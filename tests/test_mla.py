@@ -173,7 +173,11 @@ def test_mla_qb_absorb_vs_oracle(dev, B):
     cos, sin = OM.rope_tables(512, CFG)
     pos = [(37 * b + 5 * B) % 512 for b in range(B)]
     pos[-1] = 511
-    got = _qb_absorb(dev, q_n, w, pos, cos, sin)
+    _check_q_abs(_qb_absorb(dev, q_n, w, pos, cos, sin), q_n, w, pos, cos, sin)
+
+
+def _check_q_abs(got, q_n, w, pos, cos, sin):
+    B = q_n.shape[0]
     q_up = OM.proj(q_n, w.w_q_b).view(B, H, -1)
     ref = torch.stack([OM.absorb_query(q_up[b], w, CFG, p, cos, sin) for b, p in enumerate(pos)])
     # q_up values whose landing the summation order can change
@@ -193,6 +197,67 @@ def test_mla_qb_absorb_vs_oracle(dev, B):
     d = bf16_ulps(got[..., KV:], ref[..., KV:])
     assert not bool((d[~r_amb] > 0).any()), "q_rope differs where its inputs land unambiguously"
     assert int(d.max()) <= 2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("p", [0, 77, 511])
+def test_mla_prep_qb_absorb(dev, p):
+    """One sequence's prep + q_b + absorption in one launch: the cache slots
+    bit-equal to mla_prep_q_gemv's (the same norm order), no other slot
+    written, and q_abs against the oracle from the oracle's LoRA-normed q_n."""
+    from tilefoundry_amd._lib import C
+
+    g = gen(300 + p)
+    cap = 512
+    w = oracle_weights()
+    part = (torch.randn(QA + KV + R, generator=g) * 0.5).to(dev)
+    gq = (1 + 0.1 * torch.randn(QA, generator=g)).to(BF).to(dev)
+    gkv = (1 + 0.1 * torch.randn(KV, generator=g)).to(BF).to(dev)
+    cos, sin = OM.rope_tables(cap, CFG)
+    posd = torch.tensor([p], dtype=torch.int32, device=dev)
+    caches = []
+    for fused in (True, False):
+        lat = torch.zeros(1, cap, KV, dtype=BF, device=dev)
+        rk = torch.zeros(1, cap, R, dtype=BF, device=dev)
+        err = torch.zeros(1, dtype=torch.int32, device=dev)
+        if fused:
+            q_abs = torch.full((1, H, KV + R), float("nan"), dtype=BF, device=dev)
+            C.mla_prep_qb_absorb(part, gq, gkv, 1e-6, cos.to(dev), sin.to(dev), posd, lat, rk,
+                                 w.w_q_b.to(dev), w.w_kv_b.to(dev), q_abs, err)
+        else:
+            C.mla_prep_q_gemv(part, gq, gkv, 1e-6, cos.to(dev), sin.to(dev), posd, lat, rk, w.w_q_b.to(dev),
+                              torch.empty(H * 96, device=dev), err)
+        assert int(err.item()) == 0
+        caches.append((lat, rk))
+    assert_equal("latent cache", caches[0][0], caches[1][0])
+    assert_equal("rope cache", caches[0][1], caches[1][1])
+    mask = torch.ones(cap, dtype=torch.bool)
+    mask[p] = False
+    assert float(caches[0][0][0].cpu()[mask].float().abs().sum()) == 0.0
+    q_n = rms_norm_q(part[:QA].cpu().to(BF)[None], gq.cpu(), 1e-6)
+    _check_q_abs(q_abs.cpu(), q_n, w, [p], cos, sin)
+
+
+@pytest.mark.gpu
+def test_mla_prep_qb_absorb_position_error(dev):
+    """A position outside the cache sets err = 6 and writes no cache slot; the
+    query is still written (finite)."""
+    from tilefoundry_amd._lib import C
+
+    cap = 64
+    w = oracle_weights()
+    lat = torch.zeros(1, cap, KV, dtype=BF, device=dev)
+    rk = torch.zeros(1, cap, R, dtype=BF, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    q_abs = torch.full((1, H, KV + R), float("nan"), dtype=BF, device=dev)
+    cos, sin = OM.rope_tables(cap, CFG)
+    C.mla_prep_qb_absorb(torch.ones(QA + KV + R, device=dev), torch.ones(QA, dtype=BF, device=dev),
+                         torch.ones(KV, dtype=BF, device=dev), 1e-6, cos.to(dev), sin.to(dev),
+                         torch.tensor([cap], dtype=torch.int32, device=dev), lat, rk, w.w_q_b.to(dev),
+                         w.w_kv_b.to(dev), q_abs, err)
+    assert int(err.item()) == 6
+    assert float(lat.float().abs().sum()) == 0.0 and float(rk.float().abs().sum()) == 0.0
+    assert bool(torch.isfinite(q_abs.float()).all())
 
 
 @pytest.mark.gpu

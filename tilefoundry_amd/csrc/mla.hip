@@ -355,17 +355,45 @@ __global__ __launch_bounds__(kThreads) void mla_q_absorb_kernel(
 // 16-sequence tiles (batch <= 16 NT); at NT = 2 the q_n rows take the LDS that
 // W_UK has at NT = 1, so W_UK is loaded over the weight rows once the
 // projection has read them.
+// PREP (one sequence): the input is the f32 [q_a | kv_c | k_rope] partial of
+// the LoRA-A projection instead of q_n. Every block brings q_a and gamma_q_a
+// into LDS by DMA ahead of its weight rows and takes the LoRA norm while they
+// stream (in mla_prep's order, so q_n is bit-equal to it); block (0, 1) also
+// appends the normalised latent and the rotated rope key to the caches at
+// pos[0] as mla_prep does.
 constexpr int kQLora = 768;             // q_lora_rank: the K of the q_b projection
 constexpr int kQbPieces = kQLora / 8;   // 16-byte pieces of a row
 constexpr int kQnPitch = kNope + 8;     // landed q_nope row pitch, bf16 (144 bytes)
+constexpr int kQaPieces = kQLora / 4;   // PREP: f32 q_a pieces, then gamma_q_a's kQbPieces
 TFA_DEV int uk_slot(int row, int piece) { return piece ^ (2 * ((row & 3) | (((row >> 3) & 1) << 2))); }
-template <int NT>
-__global__ __launch_bounds__(kThreads) void mla_qb_absorb_kernel(
-    const uint16_t* __restrict__ q_n, int B, int H, const uint16_t* __restrict__ w_q_b,
-    const uint16_t* __restrict__ w_kv_b, const uint16_t* __restrict__ cos_t, const uint16_t* __restrict__ sin_t,
-    int rope_rows, const int* __restrict__ pos, uint16_t* __restrict__ q_abs, int* err) {
+
+struct QbArgs {
+  const uint16_t* q_n;        // [B, 768] bf16 (not PREP)
+  const float* part;          // PREP: [768 + 256 + 32] f32
+  const uint16_t* gamma_q_a;  // PREP
+  const uint16_t* gamma_kv_a; // PREP
+  float eps;                  // PREP: the LoRA norms' eps
+  uint16_t* lat_cache;        // PREP: [cap, 256]
+  uint16_t* rope_cache;       // PREP: [cap, 32]
+  int cap;
+  const uint16_t* w_q_b;      // [H*96, 768]
+  const uint16_t* w_kv_b;     // [H*128, 256]
+  const uint16_t* cos_t;
+  const uint16_t* sin_t;
+  int rope_rows;
+  const int* pos;             // [B]
+  uint16_t* q_abs;            // [B, H, 288]
+  int* err;
+  int B, H;
+};
+
+template <int NT, bool PREP>
+__global__ __launch_bounds__(kThreads) void mla_qb_absorb_kernel(const QbArgs a) {
+  static_assert(!PREP || NT == 1, "the prep form takes one sequence");
   constexpr int kQH = kNope + kRope;
+  constexpr int kXRows = PREP ? 1 : 16 * NT;              // q_n rows in LDS
   constexpr int kXDma = 16 * NT * kQbPieces / kThreads;   // q_n DMAs per thread
+  constexpr int kPreDma = 2;                              // PREP: q_a + gamma_q_a DMAs per thread
   constexpr int kUkDma = kNope * kLat / 8 / kThreads;     // W_UK DMAs per thread
   constexpr bool kUkEarly = NT == 1;                      // W_UK has LDS of its own
   constexpr int kRopePer = 16 * NT * kRope / kThreads;
@@ -373,13 +401,20 @@ __global__ __launch_bounds__(kThreads) void mla_qb_absorb_kernel(
   constexpr int kBatch = 12;                              // k-steps whose operands are read at once
   static_assert(16 * NT * kQbPieces % kThreads == 0 && kRope * kQbPieces % kThreads == 0 &&
                     kNope * kLat / 8 % kThreads == 0 && kSteps % kBatch == 0, "loads split evenly");
+  static_assert(kPreDma * kThreads >= kQaPieces + kQbPieces && kQLora == 3 * kThreads, "the prep's slots");
   static_assert(kWaves * 16 == kNope && kWaves * 64 == kLat, "one wave per 16 nope rows and 64 latent columns");
   __shared__ uint4 wl[kNope * kQbPieces];                 // W_q_b rows (at NT = 2 then W_UK)
-  __shared__ uint4 xl[16 * NT * kQbPieces];               // q_n rows; after the projection the landed values
+  __shared__ uint4 xl[kXRows * kQbPieces];                // q_n rows
   __shared__ uint4 ukl[kUkEarly ? kNope * kLat / 8 : 1];  // W_UK rows (NT = 1)
-  static_assert(sizeof(xl) >= 16 * NT * kQnPitch * 2 && sizeof(xl) >= 16 * NT * kRope * 4, "the LDS reuse fits");
-  uint16_t(*qnb)[kQnPitch] = reinterpret_cast<uint16_t(*)[kQnPitch]>(xl);   // landed q_nope
-  float(*qv)[kRope] = reinterpret_cast<float(*)[kRope]>(xl);                // landed q_rope
+  __shared__ uint4 pre[PREP ? kPreDma * kThreads : 1];    // PREP: q_a (f32) | gamma_q_a
+  __shared__ float land[16 * NT * kQnPitch / 2];          // landed q_nope (bf16) or q_rope (f32)
+  __shared__ float ssq[2][kWaves];                        // PREP: the q_a and latent norms' wave sums
+  __shared__ float kr[kRope];                             // PREP: the landed rope key
+  static_assert(sizeof(land) >= 16 * NT * kRope * 4, "q_rope fits the landing tile");
+  uint16_t(*qnb)[kQnPitch] = reinterpret_cast<uint16_t(*)[kQnPitch]>(land);
+  float(*qv)[kRope] = reinterpret_cast<float(*)[kRope]>(land);
+  const int B = PREP ? 1 : a.B;
+  const int H = a.H;
   const int h = blockIdx.x;
   const int part = blockIdx.y;   // 0: nope rows + absorption, 1: rope rows + rotation
   const int t = threadIdx.x;
@@ -387,36 +422,58 @@ __global__ __launch_bounds__(kThreads) void mla_qb_absorb_kernel(
   const int w = __builtin_amdgcn_readfirstlane(t / kWave);
   const int n16 = lane & 15;
   const int g = lane >> 4;
+  const bool side = PREP && part == 1 && h == 0;   // the cache append
 
-  // 1. every load: the rope table rows (part 1, in registers), then by DMA the
-  //    q_n rows (rows past the batch re-read the last row), the weight rows and
-  //    (part 0, NT = 1) W_UK
+  // 1. every load: the rope table rows (part 1, in registers; the cache
+  //    append's latent, rope-key and gamma values with them), then by DMA the
+  //    q_n rows (rows past the batch re-read the last row) or q_a and
+  //    gamma_q_a, the weight rows and (part 0, NT = 1) W_UK
   uint32_t csr[kRopePer], snr[kRopePer];
+  int p_raw = 0;
+  float cv = 0.f, krv = 0.f;
+  uint32_t gkr = 0;
   if (part == 1) {
 #pragma unroll
     for (int j = 0; j < kRopePer; ++j) {
       const int e = t + kThreads * j;
-      int p = pos[min(e / kRope, B - 1)];
-      if (e < B * kRope && (p < 0 || p >= rope_rows) && h == 0) set_err(err, 6);
-      p = p < 0 || p >= rope_rows ? 0 : p;
-      csr[j] = cos_t[static_cast<size_t>(p) * kRope + e % kRope];
-      snr[j] = sin_t[static_cast<size_t>(p) * kRope + e % kRope];
+      int p = a.pos[min(e / kRope, B - 1)];
+      if (j == 0) p_raw = p;
+      if (e < B * kRope && (p < 0 || p >= a.rope_rows) && h == 0) set_err(a.err, 6);
+      p = p < 0 || p >= a.rope_rows ? 0 : p;
+      csr[j] = a.cos_t[static_cast<size_t>(p) * kRope + e % kRope];
+      snr[j] = a.sin_t[static_cast<size_t>(p) * kRope + e % kRope];
+    }
+    if (side) {
+      cv = a.part[kQLora + t];
+      krv = a.part[kQLora + kLat + min(t, kRope - 1)];
+      gkr = a.gamma_kv_a[t];
     }
   }
   const uint32_t xl0 = lds_offset(xl), wl0 = lds_offset(wl);
+  if constexpr (PREP) {
+    const uint32_t pre0 = lds_offset(pre);
 #pragma unroll
-  for (int i = 0; i < kXDma; ++i) {
-    const int q = kThreads * i + t, r = q / kQbPieces, s = q % kQbPieces;
-    lds_dma16(q_n + static_cast<size_t>(min(r, B - 1)) * kQLora + 8 * (s ^ (r & 15)),
-              xl0 + (kThreads * i + kWave * w) * 16);
+    for (int i = 0; i < kPreDma; ++i) {
+      const int q = kThreads * i + t;
+      const void* src = q < kQaPieces ? static_cast<const void*>(a.part + 4 * q)
+                                      : static_cast<const void*>(a.gamma_q_a + 8 * min(q - kQaPieces, kQbPieces - 1));
+      lds_dma16(src, pre0 + (kThreads * i + kWave * w) * 16);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kXDma; ++i) {
+      const int q = kThreads * i + t, r = q / kQbPieces, s = q % kQbPieces;
+      lds_dma16(a.q_n + static_cast<size_t>(min(r, B - 1)) * kQLora + 8 * (s ^ (r & 15)),
+                xl0 + (kThreads * i + kWave * w) * 16);
+    }
   }
   const int ntile = part == 0 ? kNope / 16 : kRope / 16;
-  const uint16_t* wsrc = w_q_b + (static_cast<size_t>(h) * kQH + part * kNope) * kQLora;
+  const uint16_t* wsrc = a.w_q_b + (static_cast<size_t>(h) * kQH + part * kNope) * kQLora;
   for (int i = 0; i < ntile * 16 * kQbPieces / kThreads; ++i) {
     const int q = kThreads * i + t, r = q / kQbPieces, s = q % kQbPieces;
     lds_dma16_stream(wsrc + static_cast<size_t>(r) * kQLora + 8 * (s ^ (r & 15)), wl0 + (kThreads * i + kWave * w) * 16);
   }
-  const uint16_t* uk_src = w_kv_b + static_cast<size_t>(h) * kKvB * kLat;
+  const uint16_t* uk_src = a.w_kv_b + static_cast<size_t>(h) * kKvB * kLat;
   auto issue_uk = [&](uint32_t dst0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kUkDma; ++i) {
@@ -425,33 +482,87 @@ __global__ __launch_bounds__(kThreads) void mla_qb_absorb_kernel(
                        dst0 + (kThreads * i + kWave * w) * 16);
     }
   };
-  if (kUkEarly && part == 0) {
-    issue_uk(lds_offset(ukl));
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kUkDma));   // q_n and the weight rows landed
-  } else {
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  if (kUkEarly && part == 0) issue_uk(lds_offset(ukl));
+
+  if constexpr (PREP) {
+    // q_n = bf16(bf16(q_a * r) * gamma_q_a), q_a landed in bf16 (a one-split
+    // sum, 0 + v); thread t sums its values t + 256j in order, then the wave,
+    // then the four waves in order. The weight rows stay in flight.
+    if (part == 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm(kNope * kQbPieces / kThreads + kUkDma));
+    else __builtin_amdgcn_s_waitcnt(waitcnt_vm(kRope * kQbPieces / kThreads));
+    lds_barrier();
+    const float* qa = reinterpret_cast<const float*>(pre);
+    const uint16_t* gq = reinterpret_cast<const uint16_t*>(pre + kQaPieces);
+    float qa3[3];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float q = round_bf(0.f + (j < 3 ? qa[t + kThreads * j] : 0.f));
+      if (j < 3) qa3[j] = q;
+      ss += q * q;
+    }
+    ss = wave_sum(ss);
+    float sk = 0.f;
+    if (side) {
+      cv = round_bf(0.f + cv);
+      sk = wave_sum(cv * cv);
+      if (t < kRope) kr[t] = round_bf(0.f + krv);
+    }
+    if (lane == 0) {
+      ssq[0][w] = ss;
+      ssq[1][w] = sk;
+    }
+    lds_barrier();
+    float tq = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < kWaves; ++w2) tq += ssq[0][w2];
+    const float rq = rsqrt_rn(tq / static_cast<float>(kQLora) + a.eps);
+    uint16_t* xq = reinterpret_cast<uint16_t*>(xl);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int i = t + kThreads * j;
+      xq[i] = static_cast<uint16_t>(f2bf(round_bf(round_bf(qa3[j] * rq) * bf2f(gq[i]))));
+    }
+    if (side) {
+      float tk = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < kWaves; ++w2) tk += ssq[1][w2];
+      const float rk = rsqrt_rn(tk / static_cast<float>(kLat) + a.eps);
+      if (p_raw < 0 || p_raw >= a.cap || p_raw >= a.rope_rows) {
+        if (t == 0) set_err(a.err, 6);
+      } else {
+        a.lat_cache[static_cast<size_t>(p_raw) * kLat + t] = static_cast<uint16_t>(f2bf(round_bf(cv * rk) * bf2f(gkr)));
+        if (t < kRope) {
+          const float x = kr[t], partner = t < kRope / 2 ? -kr[t + kRope / 2] : kr[t - kRope / 2];
+          a.rope_cache[static_cast<size_t>(p_raw) * kRope + t] =
+              static_cast<uint16_t>(f2bf(rope_bf(x, partner, bf2f(csr[0]), bf2f(snr[0]))));
+        }
+      }
+    }
   }
+  if (kUkEarly && part == 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm(kUkDma));   // q_n and the weight rows landed
+  else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   lds_barrier();
 
   // 2. the projection: C[sequence 16nt + 4g + r][row 16w + n16]; k-step ks
-  //    reads piece 4ks + g of both operands
+  //    reads piece 4ks + g of both operands (at PREP every lane reads row 0)
   f32x4 c[NT];
   if (w < ntile) {
     f32x4 acc[4][NT];
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) acc[a][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     const uint4* wrow = wl + (16 * w + n16) * kQbPieces;
 #pragma unroll
     for (int k0 = 0; k0 < kSteps; k0 += kBatch) {
       uint4 bw[kBatch], ax[kBatch][NT];
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
-        const int p = (4 * (k0 + j) + g) ^ n16;
-        bw[j] = wrow[p];
+        const int p = 4 * (k0 + j) + g;
+        bw[j] = wrow[p ^ n16];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) ax[j][nt] = xl[(16 * nt + n16) * kQbPieces + p];
+        for (int nt = 0; nt < NT; ++nt) ax[j][nt] = PREP ? xl[p] : xl[(16 * nt + n16) * kQbPieces + (p ^ n16)];
       }
 #pragma unroll
       for (int j = 0; j < kBatch; ++j)
@@ -462,9 +573,7 @@ __global__ __launch_bounds__(kThreads) void mla_qb_absorb_kernel(
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) c[nt] = (acc[0][nt] + acc[1][nt]) + (acc[2][nt] + acc[3][nt]);
-  }
-  lds_barrier();   // both operands consumed: their LDS is reused below
-  if (w < ntile) {
+    // landed: q_nope in bf16 (the absorption's operand), q_rope in f32
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -475,9 +584,8 @@ __global__ __launch_bounds__(kThreads) void mla_qb_absorb_kernel(
       }
   }
   if (!kUkEarly && part == 0) {
+    lds_barrier();   // every wave has read its weight rows: W_UK goes over them
     issue_uk(wl0);
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-  } else if (part == 0) {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   }
   lds_barrier();
@@ -490,7 +598,7 @@ __global__ __launch_bounds__(kThreads) void mla_qb_absorb_kernel(
       if (e >= B * kRope) continue;
       const int b = e / kRope, d = e % kRope;
       const float partner = d < kRope / 2 ? -qv[b][d + kRope / 2] : qv[b][d - kRope / 2];
-      q_abs[(static_cast<size_t>(b) * H + h) * kQK + kLat + d] =
+      a.q_abs[(static_cast<size_t>(b) * H + h) * kQK + kLat + d] =
           static_cast<uint16_t>(f2bf(rope_bf(qv[b][d], partner, bf2f(csr[j]), bf2f(snr[j]))));
     }
     return;
@@ -522,7 +630,7 @@ __global__ __launch_bounds__(kThreads) void mla_qb_absorb_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int b = 16 * bt + 4 * g + r;
-        if (b < B) q_abs[(static_cast<size_t>(b) * H + h) * kQK + col + n16] = static_cast<uint16_t>(f2bf(acc[r]));
+        if (b < B) a.q_abs[(static_cast<size_t>(b) * H + h) * kQK + col + n16] = static_cast<uint16_t>(f2bf(acc[r]));
       }
     }
   }
@@ -1524,18 +1632,70 @@ int tfa_mla_qb_absorb(const void* q_n, int64_t batch, int64_t heads, int64_t q_l
   TFA_ALIGN16(q_n);
   TFA_ALIGN16(w_q_b);
   TFA_ALIGN16(w_kv_b);
+  QbArgs a{};
+  a.q_n = static_cast<const uint16_t*>(q_n);
+  a.w_q_b = static_cast<const uint16_t*>(w_q_b);
+  a.w_kv_b = static_cast<const uint16_t*>(w_kv_b);
+  a.cos_t = static_cast<const uint16_t*>(cos_t);
+  a.sin_t = static_cast<const uint16_t*>(sin_t);
+  a.rope_rows = (int)rope_rows;
+  a.pos = pos;
+  a.q_abs = static_cast<uint16_t*>(q_abs);
+  a.err = err;
+  a.B = (int)batch;
+  a.H = (int)heads;
   const dim3 grid((unsigned)heads, 2);
   if (batch <= 16)
-    mla_qb_absorb_kernel<1><<<grid, kThreads, 0, stream>>>(
-        static_cast<const uint16_t*>(q_n), (int)batch, (int)heads, static_cast<const uint16_t*>(w_q_b),
-        static_cast<const uint16_t*>(w_kv_b), static_cast<const uint16_t*>(cos_t),
-        static_cast<const uint16_t*>(sin_t), (int)rope_rows, pos, static_cast<uint16_t*>(q_abs), err);
+    mla_qb_absorb_kernel<1, false><<<grid, kThreads, 0, stream>>>(a);
   else
-    mla_qb_absorb_kernel<2><<<grid, kThreads, 0, stream>>>(
-        static_cast<const uint16_t*>(q_n), (int)batch, (int)heads, static_cast<const uint16_t*>(w_q_b),
-        static_cast<const uint16_t*>(w_kv_b), static_cast<const uint16_t*>(cos_t),
-        static_cast<const uint16_t*>(sin_t), (int)rope_rows, pos, static_cast<uint16_t*>(q_abs), err);
+    mla_qb_absorb_kernel<2, false><<<grid, kThreads, 0, stream>>>(a);
   return launched("mla_qb_absorb");
+}
+
+int tfa_mla_prep_qb_absorb(const float* part, int64_t q_lora, const void* gamma_q_a, const void* gamma_kv_a,
+                           float eps, const void* cos_t, const void* sin_t, int64_t rope_rows, const int* pos,
+                           void* latent_cache, void* rope_cache, int64_t cap, const void* w_q_b, const void* w_kv_b,
+                           int64_t heads, void* q_abs, int* err, hipStream_t stream) {
+  TFA_NONNULL(part);
+  TFA_NONNULL(gamma_q_a);
+  TFA_NONNULL(gamma_kv_a);
+  TFA_NONNULL(cos_t);
+  TFA_NONNULL(sin_t);
+  TFA_NONNULL(pos);
+  TFA_NONNULL(latent_cache);
+  TFA_NONNULL(rope_cache);
+  TFA_NONNULL(w_q_b);
+  TFA_NONNULL(w_kv_b);
+  TFA_NONNULL(q_abs);
+  TFA_REQUIRE(heads >= 1 && heads <= kHeadRows, TFA_ERR_SHAPE, "tfa_mla_prep_qb_absorb: heads %lld not in [1, %d]",
+              (long long)heads, kHeadRows);
+  TFA_REQUIRE(q_lora == kQLora && rope_rows >= 1 && cap >= 1, TFA_ERR_SHAPE,
+              "tfa_mla_prep_qb_absorb: q_lora %lld (built for %d), empty rope table or cache", (long long)q_lora,
+              kQLora);
+  TFA_ALIGN16(part);
+  TFA_ALIGN16(gamma_q_a);
+  TFA_ALIGN16(w_q_b);
+  TFA_ALIGN16(w_kv_b);
+  QbArgs a{};
+  a.part = part;
+  a.gamma_q_a = static_cast<const uint16_t*>(gamma_q_a);
+  a.gamma_kv_a = static_cast<const uint16_t*>(gamma_kv_a);
+  a.eps = eps;
+  a.lat_cache = static_cast<uint16_t*>(latent_cache);
+  a.rope_cache = static_cast<uint16_t*>(rope_cache);
+  a.cap = (int)cap;
+  a.w_q_b = static_cast<const uint16_t*>(w_q_b);
+  a.w_kv_b = static_cast<const uint16_t*>(w_kv_b);
+  a.cos_t = static_cast<const uint16_t*>(cos_t);
+  a.sin_t = static_cast<const uint16_t*>(sin_t);
+  a.rope_rows = (int)rope_rows;
+  a.pos = pos;
+  a.q_abs = static_cast<uint16_t*>(q_abs);
+  a.err = err;
+  a.B = 1;
+  a.H = (int)heads;
+  mla_qb_absorb_kernel<1, true><<<dim3((unsigned)heads, 2), kThreads, 0, stream>>>(a);
+  return launched("mla_prep_qb_absorb");
 }
 
 int tfa_mla_attention(const void* q_abs, const void* latent_cache, const void* rope_cache, const int* wr,

@@ -544,6 +544,36 @@ void mla_qb_absorb(const Tensor& q_n, const Tensor& w_q_b, const Tensor& w_kv_b,
                                  opt_ptr_t<int>(err), stream_of(pos)));
 }
 
+// part [768 + 288] f32 (one sequence), latent [cap, 256] / rope [cap, 32] bf16, q_abs [1, H, 288] bf16.
+void mla_prep_qb_absorb(const Tensor& part, const Tensor& gamma_q_a, const Tensor& gamma_kv_a, double eps,
+                        const Tensor& cos, const Tensor& sin, const Tensor& pos, const Tensor& latent,
+                        const Tensor& rope, const Tensor& w_q_b, const Tensor& w_kv_b, const Tensor& q_abs,
+                        const OptT& err) {
+  need(part, "part", F32);
+  const int64_t QL = part.numel() - 288;
+  need(gamma_q_a, "gamma_q_a", BF, QL);
+  need(gamma_kv_a, "gamma_kv_a", BF, 256);
+  need(pos, "pos", I32, 1);
+  need(latent, "latent", BF);
+  if (latent.dim() < 1 || latent.size(-1) != 256) bad("latent: expected (cap, 256)");
+  const int64_t cap = latent.numel() / 256;
+  need(rope, "rope", BF, cap * 32);
+  need(q_abs, "q_abs", BF);
+  if (q_abs.dim() != 3 || q_abs.size(0) != 1 || q_abs.size(2) != 288) bad("q_abs: expected (1, heads, 288)");
+  const int64_t H = q_abs.size(1);
+  need_mat(w_q_b, "w_q_b", H * 96, QL);
+  need_mat(w_kv_b, "w_kv_b", H * 128, 256);
+  need(cos, "cos", BF);
+  need(sin, "sin", BF, cos.numel());
+  if (cos.numel() % 32 != 0) bad("cos: expected (rows, 32)");
+  if (err) need(*err, "err", I32, 1);
+  raise_status(tfa_mla_prep_qb_absorb(part.data_ptr<float>(), QL, gamma_q_a.data_ptr(), gamma_kv_a.data_ptr(),
+                                      (float)eps, cos.data_ptr(), sin.data_ptr(), cos.numel() / 32,
+                                      pos.data_ptr<int>(), latent.data_ptr(), rope.data_ptr(), cap,
+                                      w_q_b.data_ptr(), w_kv_b.data_ptr(), H, q_abs.data_ptr(), opt_ptr_t<int>(err),
+                                      stream_of(pos)));
+}
+
 // op [B, ns, H, 256] bf16, mp / lp [B, ns, H] f32.
 void mla_attention(const Tensor& q_abs, const Tensor& latent, const Tensor& rope, const Tensor& wr,
                    int64_t split, double scale, const Tensor& op, const Tensor& mp, const Tensor& lp,
@@ -972,6 +1002,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("mla_prep_q_gemv", &mla_prep_q_gemv);
   m.def("mla_q_absorb", &mla_q_absorb);
   m.def("mla_qb_absorb", &mla_qb_absorb);
+  m.def("mla_prep_qb_absorb", &mla_prep_qb_absorb);
   m.def("mla_attention", &mla_attention);
   m.def("mla_combine_up", &mla_combine_up);
   m.def("rows_residual", &rows_residual);

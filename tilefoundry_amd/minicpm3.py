@@ -299,7 +299,7 @@ class MiniCPM3Engine:
     runtime twin runtime_model.py; run.py drives it token by token).
 
     One step (batch > 1), 10 launches per layer plus 5 -- at one sequence the
-    projections run on the bs=1 GEMVs instead, 8 launches per layer (``_step_one``):
+    projections run on the bs=1 GEMVs instead, 7 launches per layer (``_step_one``):
 
         embed            bf16(table[id] * scale_emb), then the first input norm
         -- per layer: the MLA attention block of ``MLABlock`` ----------------
@@ -331,7 +331,7 @@ class MiniCPM3Engine:
     def __init__(self, cfg: MiniCPM3Config = MINICPM3_4B, *, batch: int = 1, device="cuda:0",
                  max_new: int = 512, prompt_room: int = 512, weights: dict | None = None, seed: int = 0,
                  split: int | None = None, ks_a: int = 5, ks_qb: int = 3, ks_o: int = 5, ks_down: int = 5,
-                 capture: bool = True):
+                 capture: bool = True, fuse_qb: bool = True):
         if cfg.kv_lora != 256 or cfg.rope != 32 or cfg.nope != 64 or cfg.v_dim != 64:
             raise ValueError("the MLA kernels are built for kv_lora 256, rope 32, nope 64, value 64")
         if not 1 <= batch <= self.MAX_BATCH:
@@ -350,6 +350,7 @@ class MiniCPM3Engine:
         self.cfg, self.batch, self.split = cfg, batch, split
         self.device = torch.device(device)
         self.ks = {"a": ks_a, "qb": ks_qb, "o": ks_o, "down": ks_down}
+        self.fuse_qb = fuse_qb   # one sequence: prep + q_b + absorption in one launch (else prep-q GEMV, absorb)
         self.cap = ((self.nsteps + split - 1) // split) * split
         if self.cap > cfg.original_max_pos:
             raise ValueError(f"cache of {self.cap} positions: past original_max_position_embeddings "
@@ -487,12 +488,14 @@ class MiniCPM3Engine:
 
     def _step_one(self, keep_logits: bool = True, sample: bool = False):
         """One sequence: the projections on the bs=1 GEMVs, each with its norm or
-        scaled residual fused (8 launches per layer):
-        rmsnorm_gemv_f32 [q_a | kv_a] (one f32 split-K partial), mla_prep_q_gemv
-        (q_a lands, LoRA norm, q_b GEMV in f32; block 0 lands the latent and the
-        rope key in the caches), mla_q_absorb, mla_attention, mla_combine_up,
-        gemv_residual o_proj + scaled residual, rmsnorm_gemv_swiglu (post norm +
-        gate|up + SwiGLU), gemv_residual down + scaled residual."""
+        scaled residual fused (7 launches per layer):
+        rmsnorm_gemv_f32 [q_a | kv_a] (one f32 split-K partial), mla_prep_qb_absorb
+        (q_a lands, LoRA norm, q_b and the absorption per head on MFMA; one block
+        lands the latent and the rope key in the caches), mla_attention,
+        mla_combine_up, gemv_residual o_proj + scaled residual,
+        rmsnorm_gemv_swiglu (post norm + gate|up + SwiGLU), gemv_residual down +
+        scaled residual. With ``fuse_qb=False`` the prep and q_b run as
+        mla_prep_q_gemv (f32 out) and the absorption as mla_q_absorb (8 launches)."""
         cfg = self.cfg
         h, h1 = self.h[0], self.h1[0]
         part_a, part_qb = self.part_a[:1], self.part_qb[:1]
@@ -500,9 +503,13 @@ class MiniCPM3Engine:
         for i, w in enumerate(self.layers):
             lat, rk = self.latent[i], self.rope_k[i]
             C.rmsnorm_gemv_f32(h, w["gamma_in"], cfg.eps, w["w_a"], part_a.view(-1))
-            C.mla_prep_q_gemv(part_a.view(-1), w["gamma_q_a"], w["gamma_kv_a"], cfg.lora_eps, self.cos,
-                              self.sin, self.pos, lat, rk, w["w_q_b"], part_qb.view(-1), self.err)
-            C.mla_q_absorb(part_qb, w["w_kv_b"], self.cos, self.sin, self.pos, self.q_abs, self.err)
+            if self.fuse_qb:
+                C.mla_prep_qb_absorb(part_a.view(-1), w["gamma_q_a"], w["gamma_kv_a"], cfg.lora_eps, self.cos,
+                                     self.sin, self.pos, lat, rk, w["w_q_b"], w["w_kv_b"], self.q_abs, self.err)
+            else:
+                C.mla_prep_q_gemv(part_a.view(-1), w["gamma_q_a"], w["gamma_kv_a"], cfg.lora_eps, self.cos,
+                                  self.sin, self.pos, lat, rk, w["w_q_b"], part_qb.view(-1), self.err)
+                C.mla_q_absorb(part_qb, w["w_kv_b"], self.cos, self.sin, self.pos, self.q_abs, self.err)
             C.mla_attention(self.q_abs, lat, rk, self.pos, self.split, cfg.scale, self.op, self.mp,
                             self.lp, self.err)
             C.mla_combine_up(self.op, self.mp, self.lp, self.pos, self.split, w["w_kv_b"], self.attn)
