@@ -423,22 +423,27 @@ def test_rows_residual(dev):
 
 
 @pytest.mark.gpu
-def test_mla_block_vs_reference(dev):
+@pytest.mark.parametrize("B,cap,pos,fuse_qb", [
+    (2, 512, [100, 511], True),
+    (2, 512, [100, 511], False),
+    (8, 8192, [8191, 0, 4095, 8191, 17, 6000, 8190, 1234], True),   # the benchmark's shape
+])
+def test_mla_block_vs_reference(dev, B, cap, pos, fuse_qb):
     """The whole attention block (norm, projections, cache append, absorbed
     attention, o_proj, scaled residual) against the non-absorbed reference
-    order, with each sequence at its own position."""
+    order, with each sequence at its own position: at batch 2 over 512 slots
+    with the q_b projection and the absorption in one launch or as two, and at
+    the benchmark's batch 8 over 8192 slots (first, middle and last slots)."""
     from tilefoundry_amd.minicpm3 import MLABlock, MiniCPM3Config, synthetic_weights
 
     cfg = MiniCPM3Config()
-    B, cap = 2, 512
     wts = synthetic_weights(cfg, seed=7)
-    blk = MLABlock(cfg, batch=B, cap=cap, device=dev, weights=wts)
+    blk = MLABlock(cfg, batch=B, cap=cap, device=dev, weights=wts, fuse_qb=fuse_qb)
     ow = OM.MLAWeights(**wts)
     lat, rk = OM.random_cache(B, cap, CFG, seed=13)
     blk.latent.copy_(lat.to(dev))
     blk.rope_k.copy_(rk.to(dev))
     hidden = torch.randn(B, cfg.hidden, generator=gen(14)).to(BF)
-    pos = [100, 511]
     out = blk.step(hidden.to(dev), pos).cpu()
     attn = blk.attn.cpu()
     cos, sin = OM.rope_tables(cap, CFG)
