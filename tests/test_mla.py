@@ -200,6 +200,35 @@ def _check_q_abs(got, q_n, w, pos, cos, sin):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("B", [8, 20])
+def test_mla_qb_absorb_repeatable(dev, B):
+    """Thirty calls in a row, each after an MLA attention launch that leaves its
+    own data in LDS, give bit-identical queries: every operand the kernel
+    reads from LDS (W_UK included) has landed before it is read."""
+    from tilefoundry_amd._lib import C
+
+    g = gen(90 + B)
+    w = oracle_weights()
+    q_n = torch.randn(B, QA, generator=g).to(BF).to(dev)
+    cos, sin = (t.to(dev) for t in OM.rope_tables(8192, CFG))
+    posd = torch.full((B,), 8191, dtype=torch.int32, device=dev)
+    wq, wk = w.w_q_b.to(dev), w.w_kv_b.to(dev)
+    lat, rk = (t.to(dev) for t in OM.random_cache(B, 8192, CFG, seed=5))
+    ns = 8192 // 256
+    op = torch.empty(B, ns, H, KV, dtype=BF, device=dev)
+    mp = torch.empty(B, ns, H, device=dev)
+    lp = torch.empty(B, ns, H, device=dev)
+    outs = []
+    for _ in range(30):
+        q_abs = torch.empty(B, H, KV + R, dtype=BF, device=dev)
+        C.mla_qb_absorb(q_n, wq, wk, cos, sin, posd, q_abs, None)
+        C.mla_attention(q_abs, lat, rk, posd, 256, CFG.scale, op, mp, lp, None)
+        outs.append(q_abs)
+    for i, o in enumerate(outs[1:], 1):
+        assert_equal(f"call {i}", o, outs[0])
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("p", [0, 77, 511])
 def test_mla_prep_qb_absorb(dev, p):
     """One sequence's prep + q_b + absorption in one launch: the cache slots

@@ -583,9 +583,13 @@ __global__ __launch_bounds__(kThreads) void mla_qb_absorb_kernel(const QbArgs a)
         else qv[row][col] = round_bf(c[nt][r]);
       }
   }
-  if (!kUkEarly && part == 0) {
-    lds_barrier();   // every wave has read its weight rows: W_UK goes over them
-    issue_uk(wl0);
+  if (part == 0) {
+    if (!kUkEarly) {
+      lds_barrier();   // every wave has read its weight rows: W_UK goes over them
+      issue_uk(wl0);
+    }
+    // W_UK landed: the absorption reads it, and no DMA of the block may still be
+    // writing LDS when it ends
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   }
   lds_barrier();
