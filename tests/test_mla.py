@@ -149,7 +149,8 @@ def test_mla_q_absorb(dev):
 def _qb_absorb(dev, q_n, w, pos, cos, sin, err=None):
     from tilefoundry_amd._lib import C
 
-    q_abs = torch.full((q_n.shape[0], H, KV + R), float("nan"), dtype=BF, device=dev)
+    heads = w.w_kv_b.shape[0] // (CFG.nope + CFG.v_dim)
+    q_abs = torch.full((q_n.shape[0], heads, KV + R), float("nan"), dtype=BF, device=dev)
     C.mla_qb_absorb(q_n.to(dev), w.w_q_b.to(dev), w.w_kv_b.to(dev), cos.to(dev), sin.to(dev),
                     torch.tensor(pos, dtype=torch.int32, device=dev), q_abs, err)
     return q_abs.cpu()
@@ -176,27 +177,44 @@ def test_mla_qb_absorb_vs_oracle(dev, B):
     _check_q_abs(_qb_absorb(dev, q_n, w, pos, cos, sin), q_n, w, pos, cos, sin)
 
 
-def _check_q_abs(got, q_n, w, pos, cos, sin):
+def _check_q_abs(got, q_n, w, pos, cos, sin, cfg=CFG):
     B = q_n.shape[0]
-    q_up = OM.proj(q_n, w.w_q_b).view(B, H, -1)
-    ref = torch.stack([OM.absorb_query(q_up[b], w, CFG, p, cos, sin) for b, p in enumerate(pos)])
+    q_up = OM.proj(q_n, w.w_q_b).view(B, cfg.heads, -1)
+    ref = torch.stack([OM.absorb_query(q_up[b], w, cfg, p, cos, sin) for b, p in enumerate(pos)])
     # q_up values whose landing the summation order can change
-    exact = (q_n.double() @ w.w_q_b.double().t()).view(B, H, -1)
-    slack = 8 * 2.0 ** -24 * (q_n.double().abs() @ w.w_q_b.double().abs().t()).view(B, H, -1)   # f32 sums: <= 1.3x
+    exact = (q_n.double() @ w.w_q_b.double().t()).view(B, cfg.heads, -1)
+    slack = 8 * 2.0 ** -24 * (q_n.double().abs() @ w.w_q_b.double().abs().t()).view(B, cfg.heads, -1)   # f32: <= 1.3x
     amb = ((exact - slack).to(BF) != (exact + slack).to(BF)).double()
     ulp = lambda x: torch.exp2(torch.floor(torch.log2(x.double().abs().clamp_min(1e-30))) - 7)
     q_ulp = amb * ulp(q_up)
-    carry = torch.einsum("bhi,hic->bhc", q_ulp[..., :CFG.nope], w.w_uk(CFG).double().abs())
+    carry = torch.einsum("bhi,hic->bhc", q_ulp[..., :cfg.nope], w.w_uk(cfg).double().abs())
     err = (got[..., :KV].double() - ref[..., :KV].double()).abs()
     allowed = 2 * ulp(ref[..., :KV]) + 1.01 * carry
     assert bool((err <= allowed).all()), f"q_lat: {int((err > allowed).sum())} elements past the bound"
     assert float((err > 0).double().mean()) <= 0.03
-    half = CFG.rope // 2
-    r_amb = q_ulp[..., CFG.nope:] > 0
+    half = cfg.rope // 2
+    r_amb = q_ulp[..., cfg.nope:] > 0
     r_amb = r_amb | torch.cat((r_amb[..., half:], r_amb[..., :half]), -1)
     d = bf16_ulps(got[..., KV:], ref[..., KV:])
     assert not bool((d[~r_amb] > 0).any()), "q_rope differs where its inputs land unambiguously"
     assert int(d.max()) <= 2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,B", [(17, 5), (48, 3), (1, 2)])
+def test_mla_qb_absorb_other_head_counts(dev, heads, B):
+    """The one-launch q_b + absorption for head counts other than MiniCPM3's 40
+    (a partial last 16-head attention tile, the 48-head maximum, one head),
+    against the oracle with the same rounding-boundary bound."""
+    from dataclasses import replace
+
+    cfg = replace(CFG, heads=heads)
+    w = OM.random_weights(cfg, seed=heads, std=0.05)
+    g = gen(60 + heads)
+    q_n = torch.randn(B, QA, generator=g).to(BF)
+    cos, sin = OM.rope_tables(256, cfg)
+    pos = [(91 * b + heads) % 256 for b in range(B)]
+    _check_q_abs(_qb_absorb(dev, q_n, w, pos, cos, sin), q_n, w, pos, cos, sin, cfg)
 
 
 @pytest.mark.gpu
