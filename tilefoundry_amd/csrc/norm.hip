@@ -27,6 +27,19 @@ TFA_DEV float norm_scale(float x, float r, float g, float d) {
   return (x * r) * (g + 1.0f);
 }
 
+// norm_scale for the two bf16 values of a packed word, landed as a packed
+// word: every landing converts both values in one v_cvt_pk_bf16_f32 (the same
+// round-to-nearest-even), and the final landing is the stored word itself.
+template <int MODE>
+TFA_DEV uint32_t norm_pair(uint32_t hw, float r, uint32_t gw, float d) {
+  const float h0 = lo_bf(hw), h1 = hi_bf(hw), g0 = lo_bf(gw), g1 = hi_bf(gw);
+  if (MODE == 1) return pack_bf((h0 * r) * (g0 + 1.0f), (h1 * r) * (g1 + 1.0f));
+  const uint32_t t = pack_bf(h0 * r, h1 * r);   // bf16(x * r)
+  const uint32_t u = pack_bf(lo_bf(t) * g0, hi_bf(t) * g1);
+  if (MODE == 0) return u;
+  return pack_bf(__fdiv_rn(lo_bf(u), d), __fdiv_rn(hi_bf(u), d));
+}
+
 // One wave per row; each lane owns NC 16-byte vectors of the row, so the whole
 // row sits in registers between the sum of squares and the write. NT: the
 // outputs go out with non-temporal stores (many-row calls, where nothing reads
@@ -54,22 +67,26 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(
       if (ADD) rv[c] = ld16_stream(res + base + 8 * v);
     }
   }
+  // the add lands each pair of sums in bf16 with one convert (that packed word
+  // is also the residual output); squares summed in element order
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int v = lane + c * kWave;
     if (v < nvec) {
-      float f[8];
-      unpack8(xv[c], f);
+      uint32_t w[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
       if (ADD) {
-        float g[8];
-        unpack8(rv[c], g);
+        const uint32_t q[4] = {rv[c].x, rv[c].y, rv[c].z, rv[c].w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) f[i] = round_bf(f[i] + g[i]);
-        xv[c] = pack8(f);
+        for (int k = 0; k < 4; ++k) w[k] = pack_bf(lo_bf(w[k]) + lo_bf(q[k]), hi_bf(w[k]) + hi_bf(q[k]));
+        xv[c] = make_uint4(w[0], w[1], w[2], w[3]);
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
+      for (int k = 0; k < 4; ++k) {
+        const float h0 = lo_bf(w[k]), h1 = hi_bf(w[k]);
+        ss += h0 * h0;
+        ss += h1 * h1;
+      }
     }
   }
   ss = wave_sum(ss);
@@ -78,16 +95,14 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(
   for (int c = 0; c < NC; ++c) {
     const int v = lane + c * kWave;
     if (v < nvec) {
-      float f[8], g[8];
-      unpack8(xv[c], f);
-      unpack8(ld16(gamma + 8 * v), g);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) f[i] = norm_scale<MODE>(f[i], r, g[i], div);
+      const uint4 gv = ld16(gamma + 8 * v);
+      const uint4 yv = make_uint4(norm_pair<MODE>(xv[c].x, r, gv.x, div), norm_pair<MODE>(xv[c].y, r, gv.y, div),
+                                  norm_pair<MODE>(xv[c].z, r, gv.z, div), norm_pair<MODE>(xv[c].w, r, gv.w, div));
       if (NT) {
-        st16_stream(y + base + 8 * v, pack8(f));
+        st16_stream(y + base + 8 * v, yv);
         if (ADD) st16_stream(res_out + base + 8 * v, xv[c]);
       } else {
-        st16(y + base + 8 * v, pack8(f));
+        st16(y + base + 8 * v, yv);
         if (ADD) st16(res_out + base + 8 * v, xv[c]);
       }
     }
