@@ -1219,16 +1219,26 @@ constexpr int kFastMergeSplits = 64;
 // split groups meet -- lane pairs (l, l ^ 32) in registers, then the four
 // waves in order through LDS -- in o_lat = sum_s w_s op_s / sum_s w_s (f32).
 // Then attn[b, h*64 + v] = bf16(W_UV[h][v] . o_lat).
-template <int NSP>   // splits, rounded up to 16 / 32 / 64
+// Each (head, sequence) takes VP blocks, each merging the splits (the cheap part,
+// done by all VP) and applying W_UV for its 64 / VP value rows: smaller blocks,
+// two of which share a CU and overlap their round trips (VP = 2: MLA core at
+// 8 x 8192 17.8-18.1 -> 17.4-17.9 us, MiniCPM3 bs=1 369 -> 373 tok/s; VP = 4 was
+// slower at batch 8).
+constexpr int kMergeParts = 2;
+template <int NSP, int VP>   // splits, rounded up to 16 / 32 / 64; blocks per head's value rows
 __global__ __launch_bounds__(kThreads) void mla_combine_up_fast_kernel(
     const uint16_t* __restrict__ op, const float* __restrict__ mp, const float* __restrict__ lp,
     const int* __restrict__ wr, int ns, int split, int H, int cap, const uint16_t* __restrict__ w_kv_b,
     uint16_t* __restrict__ attn) {
   static_assert(NSP % 8 == 0 && NSP <= kWave, "splits in eight groups, one lane each for the weights");
   constexpr int kPer = NSP / 8;   // splits per thread
+  constexpr int kVR = kV / VP;    // value rows of this block
+  constexpr int kTPR = kThreads / kVR;   // threads per value row
+  constexpr int kCPT = kLat / kTPR;      // latent columns per thread
   __shared__ float red[kWaves][kLat];
   __shared__ float olat[kLat];
-  const int h = blockIdx.x;
+  const int h = blockIdx.x / VP;
+  const int vpart = blockIdx.x % VP;
   const int b = blockIdx.y;
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1);
@@ -1246,11 +1256,11 @@ __global__ __launch_bounds__(kThreads) void mla_combine_up_fast_kernel(
 #pragma unroll
   for (int i = 0; i < kPer; ++i)
     ov[i] = ld16(op + (srow + static_cast<size_t>(min(sg + 8 * i, ns - 1)) * H) * kLat + 8 * cc);
-  const int v = t >> 2, q = t & 3;   // value row v, latent quarter q
-  const uint16_t* wrow = w_kv_b + (static_cast<size_t>(h) * kKvB + kNope + v) * kLat + 64 * q;
-  uint4 wv8[8];
+  const int v = vpart * kVR + t / kTPR, q = t % kTPR;   // value row v, latent slice q
+  const uint16_t* wrow = w_kv_b + (static_cast<size_t>(h) * kKvB + kNope + v) * kLat + kCPT * q;
+  uint4 wv8[kCPT / 8];
 #pragma unroll
-  for (int c8 = 0; c8 < 8; ++c8) wv8[c8] = ld16(wrow + 8 * c8);
+  for (int c8 = 0; c8 < kCPT / 8; ++c8) wv8[c8] = ld16(wrow + 8 * c8);
   __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the first is read
   // 2. weights of the live splits (lane s holds split s)
   const int last = last_raw < 0 ? 0 : (last_raw >= cap ? cap - 1 : last_raw);
@@ -1289,13 +1299,13 @@ __global__ __launch_bounds__(kThreads) void mla_combine_up_fast_kernel(
   // 4. attn[b, h*64 + v] = bf16(W_UV[h][v] . o_lat)
   float d = 0.f;
 #pragma unroll
-  for (int c8 = 0; c8 < 8; ++c8) {
+  for (int c8 = 0; c8 < kCPT / 8; ++c8) {
     float w8[8];
     unpack8(wv8[c8], w8);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) d = fmaf(w8[i], olat[64 * q + 8 * c8 + i], d);
+    for (int i = 0; i < 8; ++i) d = fmaf(w8[i], olat[kCPT * q + 8 * c8 + i], d);
   }
-  d = lanes_sum<2>(d);
+  d = lanes_sum<log2_const(kTPR)>(d);
   if (q == 0) attn[static_cast<size_t>(b) * H * kV + h * kV + v] = static_cast<uint16_t>(f2bf(d));
 }
 
@@ -1765,11 +1775,11 @@ int tfa_mla_combine_up(const void* op, const float* mp, const float* lp, const i
               "tfa_mla_combine_up: batch %lld / heads %lld out of range", (long long)batch, (long long)heads);
   TFA_ALIGN16(op);
   TFA_ALIGN16(w_kv_b);
-  const dim3 grid((unsigned)heads, (unsigned)batch);
   auto fast = [&](auto nsp) {
-    mla_combine_up_fast_kernel<decltype(nsp)::value><<<grid, kThreads, 0, stream>>>(
-        static_cast<const uint16_t*>(op), mp, lp, wr, (int)splits, (int)split, (int)heads, (int)cap,
-        static_cast<const uint16_t*>(w_kv_b), static_cast<uint16_t*>(attn));
+    mla_combine_up_fast_kernel<decltype(nsp)::value, kMergeParts>
+        <<<dim3((unsigned)(heads * kMergeParts), (unsigned)batch), kThreads, 0, stream>>>(
+            static_cast<const uint16_t*>(op), mp, lp, wr, (int)splits, (int)split, (int)heads, (int)cap,
+            static_cast<const uint16_t*>(w_kv_b), static_cast<uint16_t*>(attn));
   };
   if (splits <= 16)
     fast(std::integral_constant<int, 16>{});
