@@ -241,16 +241,47 @@ void flash_prefill_kernel(const FlashArgs a) {
   // Q^T operands, resident: q-tile t, lane (query q0 + 32t + n32, k-group kg)
   // holds Q[.][16 st + 8 kg .. +7]; rows past N read row N - 1
   uint4 qop[QT][kST];
+  if constexpr (KG == 2) {
+    // The two key groups hold the same 128 query rows: they come once, by DMA
+    // into the second stage (free until step 0's barrier refills it), rows
+    // 0..63 in ks1 and 64..127 in vs1, each row's chunks swizzled like a K row
+    // (logical chunk c at c ^ (r & 15)), with the first tile in flight behind
+    // them; every wave then reads its Q^T operands from there, conflict-free
+    // like the K operand reads.
+    constexpr int kQRowsPerWave = kBM / NW;               // 16
+    constexpr int kQInstr = kQRowsPerWave / kRPI;         // 8 DMA instructions per wave
+    static_assert(kBM == 2 * kTK && kQRowsPerWave % kRPI == 0, "the query rows fill the second stage");
 #pragma unroll
-  for (int t = 0; t < QT; ++t) {
-    const size_t qn = static_cast<size_t>(min(q0 + 32 * t + n32, N - 1));
-    const uint16_t* qrow = a.q + b * a.q_bs + qn * a.q_rs + h * a.q_hs + 8 * kg;
+    for (int i = 0; i < kQInstr; ++i) {
+      const int r0 = kQRowsPerWave * wid + kRPI * i;     // first block row of this instruction
+      const int qr = r0 + dma_row;
+      const size_t qn = static_cast<size_t>(min(qt * kBM + qr, N - 1));
+      uint16_t(*qb)[kKPitch] = r0 < kTK ? ks1 : vs1;
+      lds_dma16(a.q + b * a.q_bs + qn * a.q_rs + h * a.q_hs + 8 * (dma_chunk ^ (qr & 15)),
+                lds_offset(&qb[r0 % kTK][0]));
+    }
+    load_tile(0, IC<0>{});
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kTileVm));   // this wave's query rows landed (loads complete in order)
+    lds_barrier();                                     // and every other wave's
+    const int qr = rw * kWM + n32;                     // block row of this lane's query
+    const char* qbase = reinterpret_cast<const char*>(qr < kTK ? &ks1[qr][0] : &vs1[qr - kTK][0]);
 #pragma unroll
-    for (int st = 0; st < kST; ++st) qop[t][st] = ld16(qrow + 16 * st);
+    for (int st = 0; st < kST; ++st)
+      qop[0][st] = *reinterpret_cast<const uint4*>(qbase + 16 * ((2 * st + kg) ^ (qr & 15)));
+    // the reads are complete before any wave passes step 0's barrier and refills the stage
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  } else {
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      const size_t qn = static_cast<size_t>(min(q0 + 32 * t + n32, N - 1));
+      const uint16_t* qrow = a.q + b * a.q_bs + qn * a.q_rs + h * a.q_hs + 8 * kg;
+#pragma unroll
+      for (int st = 0; st < kST; ++st) qop[t][st] = ld16(qrow + 16 * st);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);   // Q is in; from here on only tile loads are in flight
+    load_tile(0, IC<0>{});
+    if constexpr (kStages == 3) load_tile(1, IC<1>{});
   }
-  __builtin_amdgcn_s_waitcnt(kWaitVm0);   // Q is in; from here on only tile loads are in flight
-  load_tile(0, IC<0>{});
-  if constexpr (kStages == 3) load_tile(1, IC<1>{});
 
   f32x16 o[kDT][QT];   // O^T: value dims 32 dt + ..., queries q0 + 32 t + n32
 #pragma unroll
