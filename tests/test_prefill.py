@@ -52,6 +52,24 @@ def test_prefill_attention_1024_subset(dev):
 
 
 @pytest.mark.gpu
+def test_prefill_attention_2048_sampled_rows(dev):
+    """2048 tokens, 24 / 4 heads: still the 128-row blocks with two key groups
+    (their shared query rows staged once through LDS), 16 query tiles per
+    head. Sampled rows -- both ends of every fourth tile and rows at the tile
+    and 32-row wave boundaries -- of four heads (both edges of two kv groups)
+    against the oracle."""
+    n = 2048
+    q, k, v, gate = inputs(n, 29)
+    got = run(dev, q, k, v, gate).cpu().view(n, HQ, D)
+    rows = sorted({r for t in range(0, n // 128, 4) for r in (128 * t, 128 * t + 127)}
+                  | {31, 32, 63, 64, 95, 96, 1023, 1024, 1055, 2047})
+    heads = [0, 5, 6, 23]
+    ref = OP.attention_rows(q, k, v, gate, rows, heads, CFG)
+    assert_close("sampled rows", got[rows][:, heads], ref)
+    assert rel_l2(got[rows][:, heads], ref) < 5e-3
+
+
+@pytest.mark.gpu
 def test_prefill_attention_reads_packed_qkv(dev):
     """q, gate, k, v as strided views of one [n, 24*512 + 2*4*256] projection
     output (per head [q | gate], then k heads, then v heads)."""
